@@ -1,0 +1,238 @@
+"""Benchmark of the GLA inference path on one MI355X.
+
+Headline (BASELINE.json metric): GLA prefill tokens/s at B=4, H=6, T=16384, Dk=Dv=64, bf16 I/O,
+fp32 state (config 1), with the batched decode step at B=256 (config 2) reported alongside.
+
+  step (prefill) = one fast_chunk_gla forward over the whole [4, 16384, 6, 64] batch, inputs
+                   resident in HBM, bf16 outputs and fp32 final states written to HBM.
+  step (decode)  = one decode step for 256 sequences (H=6, D=64) on one of 12 rotating fp32
+                   state buffers (302 MB in total, larger than the 256 MB MALL); the 512-step
+                   loop is captured in a HIP graph and replayed.
+
+Prints ONE JSON line.  Roofline: HBM-bound (algorithmic bytes per pass / measured pass time vs
+8 TB/s); MFMA fraction = algorithmic flops / time / 2.5 PFLOP/s (dense bf16).
+cpu_baseline: the CPU restatement of the reference's PyTorch scan (oracle/ref_port.py) on a
+bounded sample of the same workload, on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "GLA prefill tok/s @B4 H6 T16k D64 (MFMA %); decode tok/s @B256 (HBM GB/s %)"
+
+
+def _events_time_ms(fn, iters, stream):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def bench_prefill(steps, warmup, dev):
+    from triune_amd import fast_chunk_gla
+    from triune_amd.workloads import config1, gla_algorithmic_bytes, gla_algorithmic_flops
+
+    B, T, H, D = 4, 16384, 6, 64
+    q, k, v, g, s0 = config1(T=T, B=B, H=H, D=D)
+    q, k, v, g, s0 = (x.to(dev) for x in (q, k, v, g, s0))
+    out = torch.empty_like(v)
+    fn = lambda: fast_chunk_gla(q, k, v, g, initial_state=s0, out=out)  # noqa: E731
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    t0 = time.perf_counter()
+    ms = _events_time_ms(fn, steps, stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    n_th = B * T * H
+    alg_bytes = gla_algorithmic_bytes(n_th, D, D, 2, 2, 2) + 2 * B * H * D * D * 4  # + S0 read, S write
+    alg_flops = gla_algorithmic_flops(n_th, D, D)
+    gbs = alg_bytes / (ms * 1e-3) / 1e9
+    tflops = alg_flops / (ms * 1e-3) / 1e12
+    return {
+        "ms": ms,
+        "wall_s": wall,
+        "tok_s": B * T / (ms * 1e-3),
+        "alg_bytes": alg_bytes,
+        "alg_flops": alg_flops,
+        "gbs": gbs,
+        "tflops": tflops,
+    }
+
+
+def bench_decode(steps_total, dev, n_bufs=12):
+    from triune_amd import gla_decode_step
+    from triune_amd.workloads import config2
+
+    B, H, D = 256, 6, 64
+    q, k, v, g, s0 = config2(steps=steps_total, B=B, H=H, D=D)
+    q, k, v, g = (x.to(dev) for x in (q, k, v, g))
+    states = [s0.to(dev).clone() for _ in range(n_bufs)]
+    outs = torch.empty(steps_total, B, 1, H, D, device=dev, dtype=torch.bfloat16)
+
+    def loop():
+        for t in range(steps_total):
+            gla_decode_step(q[t], k[t], v[t], g[t], states[t % n_bufs], inplace=True, out=outs[t])
+
+    # warm up on a side stream, then capture the whole loop in one graph
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        loop()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loop()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    reps = 3
+    ms_loop = _events_time_ms(graph.replay, reps, stream)
+    eager_ms = _events_time_ms(loop, 1, stream)
+    step_us = ms_loop * 1e3 / steps_total
+    state_bytes = B * H * D * D * 4
+    step_bytes = 2 * state_bytes + B * H * D * 2 * 4 + B * H * D * 2  # state r+w; q,k,v,g read; o write
+    return {
+        "step_us": step_us,
+        "eager_step_us": eager_ms * 1e3 / steps_total,
+        "tok_s": B / (step_us * 1e-6),
+        "step_bytes": step_bytes,
+        "gbs": step_bytes / (step_us * 1e-6) / 1e9,
+        "state_buffers": n_bufs,
+    }
+
+
+def cpu_baseline(budget_s=20.0):
+    """The reference's PyTorch CPU scan, restated (oracle/ref_port.py), on one batch row of the
+    config-1 workload (B=1, H=6, T=16384, D=64, inputs widened to fp32), all host cores."""
+    from oracle.ref_port import fast_chunk_gla_cpu
+    from triune_amd.workloads import config1
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    q, k, v, g, s0 = config1(T=16384, B=1, H=6, D=64)
+    q, k, v, g = (x.float() for x in (q, k, v, g))
+    fast_chunk_gla_cpu(q[:, :1024], k[:, :1024], v[:, :1024], g[:, :1024], s0)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
+        t0 = time.perf_counter()
+        fast_chunk_gla_cpu(q, k, v, g, s0)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end and len(times) >= 1:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": 16384 / med,
+        "unit": "tok/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"config-1 batch row 0 (B=1, H=6, T=16384, D=64, fp32 math), median of {len(times)} runs, "
+        f"{med:.2f} s each; os.cpu_count()={os.cpu_count()}; cpu={cpu_model or platform.processor()}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--decode-steps", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one GPU: this build has no multi-GPU path (the (b, h) recurrences shard "
+            "with no exchange; see DESIGN.md). Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    pre = bench_prefill(args.steps, args.warmup, dev)
+    dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": METRIC,
+        "value": round(pre["tok_s"], 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded, BASELINE config 1 distributions)",
+        "config": {
+            "workload": "GLA chunked prefill, config 1",
+            "B": 4,
+            "T": 16384,
+            "H": 6,
+            "Dk": 64,
+            "Dv": 64,
+            "chunk": 64,
+            "io": "bf16",
+            "state": "fp32",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(pre["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(pre["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "prefill pass = gla_seg_state + recurrent_scan + gla_seg_output (event-timed together)",
+            "alg_bytes_per_pass": pre["alg_bytes"],
+            "mfma_alg_tflops": round(pre["tflops"], 2),
+            "mfma_alg_frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
+        },
+        "cpu_baseline": cpu,
+    }
+    if dec is not None:
+        line["decode"] = {
+            "workload": "batched decode step, config 2 (B=256, H=6, D=64, fp32 state, bf16 q/k/v/g/o), "
+            f"{args.decode_steps}-step graph, {dec['state_buffers']} rotating state buffers",
+            "tok_s": round(dec["tok_s"], 1),
+            "us_per_step": round(dec["step_us"], 3),
+            "eager_us_per_step": round(dec["eager_step_us"], 3),
+            "roofline": {
+                "bound": "hbm",
+                "achieved": round(dec["gbs"], 1),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
+                "alg_bytes_per_step": dec["step_bytes"],
+            },
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

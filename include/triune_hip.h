@@ -1,0 +1,146 @@
+/*
+ * triune_hip.h -- C ABI of libtriune_hip.so, the MI355X (gfx950) implementation of the
+ * reference's gated-linear-attention inference path.
+ *
+ * Conventions (shared by every entry point):
+ *   - Every pointer argument named q, k, v, g, beta, o, kv, decay, s_all, fin, state*, s0,
+ *     s_final, cu_seqlens, slots, workspace is a DEVICE pointer; `strides` arrays are HOST
+ *     arrays read during the call.  The library never allocates or frees device memory.
+ *   - Token tensors use the reference layout [B, T, H, D] (varlen: [N_tok, H, D]) with the
+ *     innermost (D) stride 1; the other strides are given in elements.  States are
+ *     contiguous fp32 [*, H, Dk, Dv] with S[i][j], i = key index, j = value index.
+ *   - dtype codes: TRIUNE_DT_F32, TRIUNE_DT_BF16, TRIUNE_DT_F16.
+ *   - Work is enqueued on `stream` (a hipStream_t, passed as void*) without host
+ *     synchronisation or device allocation, so calls can be captured in a hipGraph.
+ *   - Return 0 on success or a negative TRIUNE_ERR_* code; nothing is launched on error.
+ *
+ * Reference interfaces replaced (paths under the reference repository):
+ *   triune_hip_gla_decode_step     <- triune_gla_recurrent_step_f32, csrc/engine/api.h:94-103
+ *                                     (engine.cpp:419-475); launch_gla_decode_step,
+ *                                     csrc/kernels/gla.cu:97-114; the T == 1 branch of
+ *                                     fast_chunk_gla, triune/kernels/fast_gla.py:746-753
+ *   triune_hip_gla_prefill         <- _triton_chunk_gla_tc_fwd, triune/kernels/fast_gla.py:318-380,
+ *                                     and fast_chunk_gla's chunked path, fast_gla.py:692-778
+ *   triune_hip_gla_prefill_varlen  <- no reference counterpart (the reference has no
+ *                                     cu_seqlens path); one launch = a Python loop of
+ *                                     fast_chunk_gla calls over the packed sequences
+ *   triune_hip_recurrent_scan_fwd  <- FusedRecurrentScan.forward, triune/kernels/fast_gla.py:109-149
+ *                                     (_recurrent_scan_fwd, fast_gla.py:34-64)
+ *   triune_hip_gdn_prefill         <- fast_chunk_gated_deltanet, triune/kernels/fast_gla.py:839-904,
+ *                                     with _triton_gated_deltanet_fwd (fast_gla.py:479-550) and
+ *                                     fast_recurrent_gated_deltanet (fast_gla.py:781-836)
+ */
+#ifndef TRIUNE_HIP_H
+#define TRIUNE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRIUNE_HIP_ABI_VERSION 1
+
+enum {
+    TRIUNE_DT_F32 = 0,
+    TRIUNE_DT_BF16 = 1,
+    TRIUNE_DT_F16 = 2,
+};
+
+enum {
+    TRIUNE_OK = 0,
+    TRIUNE_ERR_NULL = -1,        /* a required pointer is NULL */
+    TRIUNE_ERR_SHAPE = -2,       /* unsupported or inconsistent sizes */
+    TRIUNE_ERR_DTYPE = -3,       /* unsupported dtype code */
+    TRIUNE_ERR_LAYOUT = -4,      /* stride / alignment requirement not met */
+    TRIUNE_ERR_WORKSPACE = -5,   /* workspace missing or smaller than required */
+    TRIUNE_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
+};
+
+/* Prefill flags. */
+#define TRIUNE_FLAG_TAIL_UNCLAMPED 0x1 /* last token of each sequence keeps g > 0 (see below) */
+#define TRIUNE_FLAG_SEG_SHIFT 8        /* bits 8..15: chunks per segment, 0 = automatic */
+
+/* Gated DeltaNet beta kinds. */
+enum {
+    TRIUNE_BETA_NONE = 0,  /* beta = 1 */
+    TRIUNE_BETA_HEAD = 1,  /* beta [B, T, H]: one scalar per token and head */
+    TRIUNE_BETA_KEY = 2,   /* beta [B, T, H, Dk]: scales rows of k u^T (reference PyTorch path) */
+    TRIUNE_BETA_VALUE = 3, /* beta [B, T, H, Dv]: scales columns of k u^T (reference Triton path) */
+};
+
+int triune_hip_abi_version(void);
+const char* triune_hip_error_string(int code);
+
+/* Batched recurrent decode step, for every row (b, h):
+ *     S <- diag(exp(g)) S + k v^T ;   o = S^T q          (g is NOT clamped, as in the reference)
+ * q, k, g: [B, 1, H, Dk] (g may be fp32 when q/k/v are 16-bit: g_dtype), v: [B, 1, H, Dv],
+ * o: [B, 1, H, Dv] in o_dtype.  strides[10] = (batch, head) element strides of q, k, v, g, o.
+ * state_in / state_out: fp32 [n_state_rows, H, Dk, Dv]; they may be the same buffer (in place).
+ * slots: NULL (state row b for batch b) or int32 [B] state-row indices (a state pool).
+ * Supported (Dk, Dv): (32,32), (64,64), (128,128), (64,128), (128,64).
+ * Replaces: triune_gla_recurrent_step_f32 (api.h:94-103), launch_gla_decode_step (gla.cu:97-114). */
+int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                               int g_dtype, const int64_t* strides, const float* state_in, float* state_out,
+                               const int32_t* slots, void* o, int o_dtype, int64_t B, int64_t H, int Dk, int Dv,
+                               void* stream);
+
+/* Chunked GLA prefill over dense [B, T, H, D] tensors:
+ *     S_t = diag(exp(min(g_t, 0))) S_{t-1} + k_t v_t^T ;   o_t = S_t^T q_t ,   S_{-1} = s0 (or 0)
+ * q, k, g: Dk wide; v, o: Dv wide.  strides[15] = (batch, token, head) element strides of
+ * q, k, v, g, o.  o may alias g when both have the same dtype and strides (the reference's
+ * VectorisedGLA passes out=g, attention.py:443-451).  s0 / s_final: fp32 [B, H, Dk, Dv] or NULL.
+ * flags: TRIUNE_FLAG_TAIL_UNCLAMPED reproduces fast_chunk_gla's unclamped single-token
+ * remainder (fast_gla.py:768-775) for the last token.  Dk in {32, 64, 128}; Dv a multiple of 32.
+ * workspace: device buffer of at least triune_hip_gla_prefill_workspace_size(...) bytes.
+ * Replaces: _triton_chunk_gla_tc_fwd (fast_gla.py:318-380), fast_chunk_gla (fast_gla.py:692-778). */
+size_t triune_hip_gla_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags);
+int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                           const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
+                           int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Packed ragged GLA prefill: sequence i covers rows [cu_seqlens[i], cu_seqlens[i+1]) of the
+ * [total_tokens, H, D] tensors, starts from s0[i] (or 0) and ends in s_final[i]; every token's
+ * g is clamped at 0.  cu_seqlens: device int32 [n_seqs + 1], non-decreasing, cu[0] = 0,
+ * cu[n_seqs] = total_tokens.  strides[10] = (token, head) element strides of q, k, v, g, o.
+ * No reference counterpart: the reference has no cu_seqlens path; this is one launch for what
+ * would be a loop of fast_chunk_gla calls (fast_gla.py:692-778), one per sequence. */
+size_t triune_hip_gla_prefill_varlen_workspace_size(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,
+                                                    int Dv, int flags);
+int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                  int g_dtype, const int64_t* strides, const int32_t* cu_seqlens, int64_t n_seqs,
+                                  int64_t total_tokens, const float* s0, void* o, int o_dtype, float* s_final,
+                                  int64_t H, int Dk, int Dv, int flags, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
+/* Exclusive affine scan (FusedRecurrentScan forward), all tensors contiguous:
+ *     s_all[b,h,n] = s ;  s = decay[b,h,n,:,None] * s + kv[b,h,n]      (s starts at init or 0)
+ *     fin[b,h] = s after the last step
+ * kv: [B, H, N, Dk, Dv] in kv_dtype; decay: [B, H, N, Dk] in decay_dtype; init: [B, H, Dk, Dv]
+ * in init_dtype (or NULL for zero); s_all [B, H, N, Dk, Dv] and fin [B, H, Dk, Dv] in out_dtype
+ * (the reference returns kv.dtype tensors, fast_gla.py:147-149).  Arithmetic in fp32.
+ * s_all may alias kv when out_dtype == kv_dtype.  Dv must be a multiple of 4.
+ * Replaces: FusedRecurrentScan.forward (fast_gla.py:109-149). */
+int triune_hip_recurrent_scan_fwd(const void* kv, int kv_dtype, const void* decay, int decay_dtype, const void* init,
+                                  int init_dtype, void* s_all, void* fin, int out_dtype, int64_t B, int64_t H,
+                                  int64_t N, int Dk, int Dv, void* stream);
+
+/* Gated DeltaNet forward, the reference's variant (fast_gla.py:781-836):
+ *     u_t = v_t - S_{t-1}^T k_t ;  S_t = diag(exp(min(g_t,0))) S_{t-1} + beta_t . (k_t u_t^T) ;
+ *     o_t = S_t^T q_t
+ * beta: NULL with TRIUNE_BETA_NONE, else see the TRIUNE_BETA_* kinds (beta_dtype any dtype code).
+ * strides[18] = (batch, token, head) element strides of q, k, v, g, beta, o.
+ * s0 / s_final: fp32 [B, H, Dk, Dv] or NULL.  (Dk, Dv) in {(32,32), (64,64), (128,128)}.
+ * Replaces: fast_chunk_gated_deltanet (fast_gla.py:839-904) for T > 1. */
+int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                           const void* beta, int beta_dtype, int beta_kind, const int64_t* strides, const float* s0,
+                           void* o, int o_dtype, float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
+                           void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRIUNE_HIP_H */

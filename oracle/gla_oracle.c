@@ -1,0 +1,274 @@
+/*
+ * gla_oracle.c -- fp64 CPU restatement of the reference's GLA / Gated DeltaNet
+ * arithmetic.  TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, as the checker.  Nothing in
+ * triune_amd/ links, imports or calls it; the product path is the HIP library.
+ *
+ * Every function computes in double precision from the caller's (already rounded)
+ * inputs, so the GPU kernels and the oracle consume identical values.
+ *
+ * Layouts (all contiguous, row-major):
+ *   token tensors  q,k,g : [B, T, H, Dk]     v,o : [B, T, H, Dv]
+ *   packed (varlen) tokens: [N_tok, H, D], sequence i owns rows [cu[i], cu[i+1])
+ *   states S             : [B, H, Dk, Dv]    S[b,h,i,j], i = key index, j = value index
+ *
+ * Reference anchors (paths under the reference repository):
+ *   GLA token recurrence     tests/test_attention_fallback.py:12-24, tests/test_kernels.py:270-277
+ *                            S_t = diag(exp g_t) S_{t-1} + k_t v_t^T ,  o_t = S_t^T q_t
+ *   g <= 0 clamp in prefill  triune/kernels/fast_gla.py:586 (_run_gla_chunks), :278 (Triton TC)
+ *   no clamp at T == 1 and   triune/kernels/fast_gla.py:746-753 (T == 1 decode branch),
+ *   for a 1-token remainder  triune/kernels/fast_gla.py:768-775 (T_rem == 1 branch)
+ *   decode step              triune/kernels/fast_gla.py:746-753, csrc/engine/engine.cpp:419-475,
+ *                            csrc/kernels/gla.cu:23-75
+ *   exclusive affine scan    triune/kernels/fast_gla.py:34-64 (_recurrent_scan_fwd),
+ *                            tests/test_kernels.py:236-243
+ *   Gated DeltaNet variant   triune/kernels/fast_gla.py:781-836 (fast_recurrent_gated_deltanet),
+ *                            :453-471 (Triton per-token loop, beta over value dim)
+ *   varlen                   absent from the reference; defined as one independent GLA
+ *                            recurrence per packed sequence with its own initial state.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORACLE_API __attribute__((visibility("default")))
+
+/* Whether token t of a length-T call of fast_chunk_gla clamps g at 0.
+ * fast_gla.py:746-753: T == 1 takes the decode branch (no clamp).
+ * fast_gla.py:768-775: a remainder of exactly one token after >= 1 full chunk
+ * takes the same unclamped decode expression.  Every other token goes through
+ * _run_gla_chunks (clamp at :586) or the Triton TC kernel (clamp at :278). */
+static int clamp_token(long t, long T, long chunk) {
+    if (T == 1) return 0;
+    if (chunk > 0 && T > chunk && (T % chunk) == 1 && t == T - 1) return 0;
+    return 1;
+}
+
+/* One (sequence, head) GLA recurrence over n tokens.
+ * q,k,g advance by tok_stride_k per token, v,o by tok_stride_v. */
+static void gla_one_head(const double* q, const double* k, const double* v, const double* g,
+                         long n, long tok_stride_k, long tok_stride_v, int Dk, int Dv,
+                         const double* s0, double* o, double* s_out, long clamp_T, long chunk,
+                         int clamp_mode) {
+    double* S = (double*)malloc(sizeof(double) * (size_t)Dk * Dv);
+    if (s0) memcpy(S, s0, sizeof(double) * (size_t)Dk * Dv);
+    else memset(S, 0, sizeof(double) * (size_t)Dk * Dv);
+    for (long t = 0; t < n; ++t) {
+        const double* qt = q + t * tok_stride_k;
+        const double* kt = k + t * tok_stride_k;
+        const double* gt = g + t * tok_stride_k;
+        const double* vt = v + t * tok_stride_v;
+        int do_clamp = clamp_mode == 1 ? 1 : (clamp_mode == 0 ? 0 : clamp_token(t, clamp_T, chunk));
+        for (int i = 0; i < Dk; ++i) {
+            double gi = gt[i];
+            if (do_clamp && gi > 0.0) gi = 0.0;
+            double d = exp(gi);
+            double ki = kt[i];
+            double* row = S + (size_t)i * Dv;
+            for (int j = 0; j < Dv; ++j) row[j] = d * row[j] + ki * vt[j];
+        }
+        double* ot = o + t * tok_stride_v;
+        for (int j = 0; j < Dv; ++j) ot[j] = 0.0;
+        for (int i = 0; i < Dk; ++i) {
+            double qi = qt[i];
+            const double* row = S + (size_t)i * Dv;
+            for (int j = 0; j < Dv; ++j) ot[j] += qi * row[j];
+        }
+    }
+    if (s_out) memcpy(s_out, S, sizeof(double) * (size_t)Dk * Dv);
+    free(S);
+}
+
+/* GLA forward with the reference's fast_chunk_gla clamp semantics.
+ * clamp_mode: 2 = follow fast_chunk_gla dispatch for (T, chunk); 1 = always clamp g<=0;
+ * 0 = never clamp.  s0 may be NULL (zero initial state); s_out may be NULL. */
+ORACLE_API void oracle_gla_fwd(const double* q, const double* k, const double* v, const double* g,
+                               const double* s0, double* o, double* s_out, long B, long T, long H,
+                               int Dk, int Dv, long chunk, int clamp_mode) {
+    long bh_total = B * H;
+#pragma omp parallel for schedule(dynamic)
+    for (long bh = 0; bh < bh_total; ++bh) {
+        long b = bh / H, h = bh % H;
+        long sk = H * Dk, sv = H * Dv;
+        const double* qb = q + (b * T) * sk + h * Dk;
+        const double* kb = k + (b * T) * sk + h * Dk;
+        const double* gb = g + (b * T) * sk + h * Dk;
+        const double* vb = v + (b * T) * sv + h * Dv;
+        double* ob = o + (b * T) * sv + h * Dv;
+        const double* s0b = s0 ? s0 + bh * (long)Dk * Dv : NULL;
+        double* sob = s_out ? s_out + bh * (long)Dk * Dv : NULL;
+        gla_one_head(qb, kb, vb, gb, T, sk, sv, Dk, Dv, s0b, ob, sob, T, chunk, clamp_mode);
+    }
+}
+
+/* Packed ragged GLA: sequence i covers rows [cu[i], cu[i+1]) of [N_tok, H, D] tensors,
+ * starts from s0[i] (or zero) and writes its final state to s_out[i].  g is clamped at 0
+ * for every token (varlen rows are prefill rows). */
+ORACLE_API void oracle_gla_varlen_fwd(const double* q, const double* k, const double* v,
+                                      const double* g, const int32_t* cu, long n_seqs,
+                                      const double* s0, double* o, double* s_out, long H, int Dk,
+                                      int Dv) {
+    long total = n_seqs * H;
+#pragma omp parallel for schedule(dynamic)
+    for (long ih = 0; ih < total; ++ih) {
+        long i = ih / H, h = ih % H;
+        long r0 = cu[i], n = (long)cu[i + 1] - (long)cu[i];
+        long sk = H * Dk, sv = H * Dv;
+        const double* s0i = s0 ? s0 + ih * (long)Dk * Dv : NULL;
+        double* soi = s_out ? s_out + ih * (long)Dk * Dv : NULL;
+        gla_one_head(q + r0 * sk + h * Dk, k + r0 * sk + h * Dk, v + r0 * sv + h * Dv,
+                     g + r0 * sk + h * Dk, n, sk, sv, Dk, Dv, s0i, o + r0 * sv + h * Dv, soi, n, 0,
+                     1);
+    }
+}
+
+/* Closed form of the same map, with no recurrence:
+ *   o_t[j] = sum_i q_t[i] ( e^{G_t[i]} S0[i][j] + sum_{s<=t} e^{G_t[i]-G_s[i]} k_s[i] v_s[j] )
+ *   S_T[i][j] = e^{G_T[i]} S0[i][j] + sum_s e^{G_T[i]-G_s[i]} k_s[i] v_s[j]
+ * with G_t = sum_{tau<=t} g_tau (g clamped at 0).  O(T^2 Dk Dv): tiny inputs only.
+ * Used to pin oracle_gla_fwd, not as a product reference. */
+ORACLE_API void oracle_gla_closed_form(const double* q, const double* k, const double* v,
+                                       const double* g, const double* s0, double* o,
+                                       double* s_out, long B, long T, long H, int Dk, int Dv) {
+    double* G = (double*)malloc(sizeof(double) * (size_t)(T + 1) * Dk);
+    for (long b = 0; b < B; ++b)
+        for (long h = 0; h < H; ++h) {
+            long sk = H * Dk, sv = H * Dv;
+            const double* s0b = s0 ? s0 + (b * H + h) * (long)Dk * Dv : NULL;
+            for (int i = 0; i < Dk; ++i) G[i] = 0.0;
+            for (long t = 0; t < T; ++t)
+                for (int i = 0; i < Dk; ++i) {
+                    double gi = g[(b * T + t) * sk + h * Dk + i];
+                    if (gi > 0.0) gi = 0.0;
+                    G[(t + 1) * Dk + i] = G[t * Dk + i] + gi;
+                }
+            for (long t = 0; t <= T; ++t) {
+                /* t < T: output row t (cumulative index t+1); t == T: final state */
+                long ct = (t < T) ? t + 1 : T;
+                for (int j = 0; j < Dv; ++j) {
+                    double acc_o = 0.0;
+                    for (int i = 0; i < Dk; ++i) {
+                        double sij = s0b ? exp(G[ct * Dk + i]) * s0b[(long)i * Dv + j] : 0.0;
+                        for (long s = 0; s < ct; ++s)
+                            sij += exp(G[ct * Dk + i] - G[(s + 1) * Dk + i]) *
+                                   k[(b * T + s) * sk + h * Dk + i] * v[(b * T + s) * sv + h * Dv + j];
+                        if (t < T) acc_o += q[(b * T + t) * sk + h * Dk + i] * sij;
+                        else if (s_out) s_out[((b * H + h) * (long)Dk + i) * Dv + j] = sij;
+                    }
+                    if (t < T) o[(b * T + t) * sv + h * Dv + j] = acc_o;
+                }
+            }
+        }
+    free(G);
+}
+
+/* One recurrent decode step over rows bh (no clamp; fast_gla.py:746-753):
+ *   S[bh] <- diag(exp g[bh]) S[bh] + k[bh] v[bh]^T ;  o[bh] = S[bh]^T q[bh]
+ * q,k,g: [BH, Dk]; v,o: [BH, Dv]; S: [BH, Dk, Dv] updated in place. */
+ORACLE_API void oracle_gla_decode_step(const double* q, const double* k, const double* v,
+                                       const double* g, double* S, double* o, long BH, int Dk,
+                                       int Dv) {
+#pragma omp parallel for schedule(static)
+    for (long bh = 0; bh < BH; ++bh) {
+        double* Sb = S + bh * (long)Dk * Dv;
+        double* ob = o + bh * Dv;
+        for (int j = 0; j < Dv; ++j) ob[j] = 0.0;
+        for (int i = 0; i < Dk; ++i) {
+            double d = exp(g[bh * Dk + i]);
+            double ki = k[bh * Dk + i], qi = q[bh * Dk + i];
+            double* row = Sb + (long)i * Dv;
+            for (int j = 0; j < Dv; ++j) {
+                row[j] = d * row[j] + ki * v[bh * Dv + j];
+                ob[j] += qi * row[j];
+            }
+        }
+    }
+}
+
+/* Exclusive affine scan (FusedRecurrentScan forward, fast_gla.py:34-64, :109-149):
+ * for each lane m of M = B*H*Dk*Dv and n = 0..N-1:
+ *   s_all[m][n] = s ;  s = s * decay[m][n] + kv[m][n]      (s starts at init[m])
+ * kv, s_all: [B,H,N,Dk,Dv]; decay: [B,H,N,Dk] (broadcast over Dv); init, fin: [B,H,Dk,Dv]. */
+ORACLE_API void oracle_recurrent_scan_fwd(const double* kv, const double* decay, const double* init,
+                                          double* s_all, double* fin, long B, long H, long N, int Dk,
+                                          int Dv) {
+    long DD = (long)Dk * Dv;
+#pragma omp parallel for schedule(static)
+    for (long bh = 0; bh < B * H; ++bh)
+        for (long e = 0; e < DD; ++e) {
+            long i = e / Dv;
+            double s = init ? init[bh * DD + e] : 0.0;
+            for (long n = 0; n < N; ++n) {
+                long idx = (bh * N + n) * DD + e;
+                s_all[idx] = s;
+                s = s * decay[(bh * N + n) * Dk + i] + kv[idx];
+            }
+            fin[bh * DD + e] = s;
+        }
+}
+
+/* Gated DeltaNet, the reference variant (fast_gla.py:781-836 and :453-471):
+ *   u_t   = v_t - S_{t-1}^T k_t              (prediction from the un-decayed state)
+ *   S_t   = diag(exp(min(g_t,0))) S_{t-1} + W_t
+ *   W_t   = k_t u_t^T scaled by beta
+ *   o_t   = S_t^T q_t
+ * beta_kind: 0 none (beta = 1); 1 per (token, head) scalar, beta [B,T,H];
+ *            2 per key dim (rows of W, the PyTorch path fast_gla.py:823-827), beta [B,T,H,Dk];
+ *            3 per value dim (columns of W, the Triton path fast_gla.py:464-465), beta [B,T,H,Dv]. */
+ORACLE_API void oracle_gdn_fwd(const double* q, const double* k, const double* v, const double* g,
+                               const double* beta, int beta_kind, const double* s0, double* o,
+                               double* s_out, long B, long T, long H, int Dk, int Dv) {
+#pragma omp parallel for schedule(dynamic)
+    for (long bh = 0; bh < B * H; ++bh) {
+        long b = bh / H, h = bh % H;
+        long sk = H * Dk, sv = H * Dv;
+        double* S = (double*)malloc(sizeof(double) * (size_t)Dk * Dv);
+        double* u = (double*)malloc(sizeof(double) * (size_t)Dv);
+        if (s0) memcpy(S, s0 + bh * (long)Dk * Dv, sizeof(double) * (size_t)Dk * Dv);
+        else memset(S, 0, sizeof(double) * (size_t)Dk * Dv);
+        for (long t = 0; t < T; ++t) {
+            const double* qt = q + (b * T + t) * sk + h * Dk;
+            const double* kt = k + (b * T + t) * sk + h * Dk;
+            const double* gt = g + (b * T + t) * sk + h * Dk;
+            const double* vt = v + (b * T + t) * sv + h * Dv;
+            for (int j = 0; j < Dv; ++j) {
+                double pred = 0.0;
+                for (int i = 0; i < Dk; ++i) pred += kt[i] * S[(long)i * Dv + j];
+                u[j] = vt[j] - pred;
+            }
+            for (int i = 0; i < Dk; ++i) {
+                double gi = gt[i] > 0.0 ? 0.0 : gt[i];
+                double d = exp(gi);
+                double rs = 1.0;
+                if (beta_kind == 1) rs = beta[(b * T + t) * H + h];
+                else if (beta_kind == 2) rs = beta[(b * T + t) * sk + h * Dk + i];
+                for (int j = 0; j < Dv; ++j) {
+                    double cs = (beta_kind == 3) ? beta[(b * T + t) * sv + h * Dv + j] : 1.0;
+                    S[(long)i * Dv + j] = d * S[(long)i * Dv + j] + rs * cs * kt[i] * u[j];
+                }
+            }
+            double* ot = o + (b * T + t) * sv + h * Dv;
+            for (int j = 0; j < Dv; ++j) {
+                double acc = 0.0;
+                for (int i = 0; i < Dk; ++i) acc += qt[i] * S[(long)i * Dv + j];
+                ot[j] = acc;
+            }
+        }
+        if (s_out) memcpy(s_out + bh * (long)Dk * Dv, S, sizeof(double) * (size_t)Dk * Dv);
+        free(S);
+        free(u);
+    }
+}
+
+ORACLE_API int oracle_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

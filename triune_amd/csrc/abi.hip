@@ -1,0 +1,324 @@
+// abi.hip -- extern "C" entry points of libtriune_hip.so (declared in include/triune_hip.h).
+// Argument validation, workspace layout and the launch sequence of each operator.
+#include "../../include/triune_hip.h"
+#include "kernels.h"
+
+using namespace triune;
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool dtype_ok(int dt) { return dt == TRIUNE_DT_F32 || dt == TRIUNE_DT_BF16 || dt == TRIUNE_DT_F16; }
+
+// 16-byte vector access of 8 elements (16-bit) or 2x4 elements (fp32) needs every row start
+// 16-byte aligned: base pointer aligned and strides a multiple of 16 bytes.
+bool vec_ok(const void* p, int dt, const int64_t* st, int n) {
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) return false;
+    const int64_t m = dt == TRIUNE_DT_F32 ? 4 : 8;
+    for (int i = 0; i < n; ++i)
+        if (st[i] % m != 0) return false;
+    return true;
+}
+
+// 8-byte access of 4 elements (16-bit) or 16-byte (fp32).
+bool vec4_ok(const void* p, int dt, const int64_t* st, int n) {
+    if (reinterpret_cast<uintptr_t>(p) % (dt == TRIUNE_DT_F32 ? 16 : 8) != 0) return false;
+    for (int i = 0; i < n; ++i)
+        if (st[i] % 4 != 0) return false;
+    return true;
+}
+
+int seg_chunks(int64_t jobs, int flags) {
+    int forced = (flags >> TRIUNE_FLAG_SEG_SHIFT) & 0xff;
+    if (forced > 0) return forced;
+    int64_t p = jobs / 1024;  // one wave per work item; ~1 resident wave per SIMD
+    if (p < 1) p = 1;
+    if (p > 255) p = 255;
+    return (int)p;
+}
+
+bool prefill_shape_ok(int Dk, int Dv) {
+    if (!(Dk == 32 || Dk == 64 || Dk == 128)) return false;
+    if (Dv <= 0 || Dv % 32 != 0 || Dv > 512) return false;
+    return true;
+}
+
+struct PrefillPlan {
+    int P, dvs;
+    int64_t nseg, n_work;
+    size_t off_segoff, off_state, off_gamma, total;
+};
+
+PrefillPlan plan_dense(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {
+    PrefillPlan p{};
+    p.dvs = prefill_dv_slice(Dk, Dv);
+    const int64_t nchunks = (T + 63) / 64;
+    p.P = seg_chunks(B * H * nchunks * (Dv / p.dvs), flags);
+    p.nseg = (nchunks + p.P - 1) / p.P;
+    p.n_work = B * p.nseg;
+    p.off_segoff = 0;
+    p.off_state = 0;
+    p.off_gamma = align_up((size_t)p.n_work * H * Dk * Dv * sizeof(float));
+    p.total = p.off_gamma + align_up((size_t)p.n_work * H * Dk * sizeof(float));
+    return p;
+}
+
+PrefillPlan plan_varlen(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk, int Dv, int flags) {
+    PrefillPlan p{};
+    p.dvs = prefill_dv_slice(Dk, Dv);
+    const int64_t nchunks = (total_tokens + 63) / 64 + n_seqs;
+    p.P = seg_chunks(H * nchunks * (Dv / p.dvs), flags);
+    p.n_work = (total_tokens + 64 * (int64_t)p.P - 1) / (64 * (int64_t)p.P) + n_seqs;
+    p.nseg = 0;
+    p.off_segoff = 0;
+    p.off_state = align_up((size_t)(n_seqs + 1) * sizeof(int32_t));
+    p.off_gamma = p.off_state + align_up((size_t)p.n_work * H * Dk * Dv * sizeof(float));
+    p.total = p.off_gamma + align_up((size_t)p.n_work * H * Dk * sizeof(float));
+    return p;
+}
+
+int launch_status(hipError_t e) { return e == hipSuccess ? TRIUNE_OK : TRIUNE_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+int triune_hip_abi_version(void) { return TRIUNE_HIP_ABI_VERSION; }
+
+const char* triune_hip_error_string(int code) {
+    switch (code) {
+        case TRIUNE_OK: return "ok";
+        case TRIUNE_ERR_NULL: return "a required pointer is NULL";
+        case TRIUNE_ERR_SHAPE: return "unsupported or inconsistent sizes";
+        case TRIUNE_ERR_DTYPE: return "unsupported dtype code";
+        case TRIUNE_ERR_LAYOUT: return "stride or alignment requirement not met";
+        case TRIUNE_ERR_WORKSPACE: return "workspace missing or too small";
+        case TRIUNE_ERR_LAUNCH: return "HIP kernel launch failed";
+        default: return "unknown error";
+    }
+}
+
+int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                               int g_dtype, const int64_t* strides, const float* state_in, float* state_out,
+                               const int32_t* slots, void* o, int o_dtype, int64_t B, int64_t H, int Dk, int Dv,
+                               void* stream) {
+    if (!q || !k || !v || !g || !strides || !state_in || !state_out || !o) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
+    if (B < 0 || H <= 0) return TRIUNE_ERR_SHAPE;
+    if (!((Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128) ||
+          (Dk == 64 && Dv == 128) || (Dk == 128 && Dv == 64)))
+        return TRIUNE_ERR_SHAPE;
+    if (B == 0) return TRIUNE_OK;
+    if (!vec_ok(q, io_dtype, strides + 0, 2) || !vec_ok(k, io_dtype, strides + 2, 2) ||
+        !vec4_ok(v, io_dtype, strides + 4, 2) || !vec_ok(g, g_dtype, strides + 6, 2) ||
+        !vec4_ok(o, o_dtype, strides + 8, 2) || reinterpret_cast<uintptr_t>(state_in) % 16 ||
+        reinterpret_cast<uintptr_t>(state_out) % 16)
+        return TRIUNE_ERR_LAYOUT;
+    DecodeParams a{};
+    a.q = q; a.k = k; a.v = v; a.g = g;
+    a.io_dt = io_dtype; a.g_dt = g_dtype; a.o_dt = o_dtype;
+    a.q_sb = strides[0]; a.q_sh = strides[1];
+    a.k_sb = strides[2]; a.k_sh = strides[3];
+    a.v_sb = strides[4]; a.v_sh = strides[5];
+    a.g_sb = strides[6]; a.g_sh = strides[7];
+    a.o_sb = strides[8]; a.o_sh = strides[9];
+    a.state_in = state_in; a.state_out = state_out; a.slots = slots;
+    a.o = o; a.B = B; a.H = H;
+    return launch_status(launch_gla_decode(a, Dk, Dv, (hipStream_t)stream));
+}
+
+size_t triune_hip_gla_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {
+    if (B <= 0 || T <= 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return 0;
+    return plan_dense(B, T, H, Dk, Dv, flags).total;
+}
+
+static void fill_tok(TokTensor& t, const void* p, const int64_t* st3) {
+    t.p = p; t.sb = st3[0]; t.st = st3[1]; t.sh = st3[2];
+}
+
+int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                           const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
+                           int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
+    if (B < 0 || T < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return TRIUNE_ERR_SHAPE;
+    if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
+        !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
+        !vec_ok(o, o_dtype, strides + 12, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
+        reinterpret_cast<uintptr_t>(s_final) % 16)
+        return TRIUNE_ERR_LAYOUT;
+    hipStream_t st = (hipStream_t)stream;
+    if (B == 0) return TRIUNE_OK;
+    if (T == 0) {
+        if (!s_final) return TRIUNE_OK;
+        ScanParams sc{};  // N = 0: fin = init (or zero)
+        sc.kv = s_final; sc.kv_dt = DT_F32; sc.dec = s_final; sc.dec_dt = DT_F32;
+        sc.init = s0; sc.i_so = H * (int64_t)Dk * Dv; sc.i_sh = (int64_t)Dk * Dv;
+        sc.fin = s_final; sc.fin_dt = DT_F32; sc.f_so = sc.i_so; sc.f_sh = sc.i_sh;
+        sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = 0;
+        return launch_status(launch_recurrent_scan(sc, st));
+    }
+    const PrefillPlan pl = plan_dense(B, T, H, Dk, Dv, flags);
+    if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
+    char* ws = reinterpret_cast<char*>(workspace);
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
+
+    PrefillParams a{};
+    fill_tok(a.q, q, strides + 0);
+    fill_tok(a.k, k, strides + 3);
+    fill_tok(a.v, v, strides + 6);
+    fill_tok(a.g, g, strides + 9);
+    a.o = o; a.o_sb = strides[12]; a.o_st = strides[13]; a.o_sh = strides[14];
+    a.g_dt = g_dtype; a.o_dt = o_dtype;
+    a.s0 = s0;
+    a.ws_state = reinterpret_cast<float*>(ws + pl.off_state);
+    a.ws_gamma = reinterpret_cast<float*>(ws + pl.off_gamma);
+    a.n_seqs = B; a.H = H; a.T = T; a.Dk = Dk; a.Dv = Dv;
+    a.P = pl.P; a.nseg_dense = (int)pl.nseg; a.varlen = 0; a.flags = flags & 0xff;
+
+    hipError_t e = launch_gla_seg_state(a, pl.n_work, pl.dvs, io_dtype, st);
+    if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
+
+    const int64_t DD = (int64_t)Dk * Dv;
+    ScanParams sc{};
+    sc.kv = a.ws_state; sc.kv_dt = DT_F32;
+    sc.kv_so = pl.nseg * H * DD; sc.kv_sh = DD; sc.kv_sn = H * DD;
+    sc.dec = a.ws_gamma; sc.dec_dt = DT_F32; sc.dec_is_log = 1;
+    sc.d_so = pl.nseg * H * Dk; sc.d_sh = Dk; sc.d_sn = H * Dk;
+    sc.init = s0; sc.i_so = H * DD; sc.i_sh = DD;
+    sc.s_all = a.ws_state; sc.sa_dt = DT_F32;
+    sc.sa_so = sc.kv_so; sc.sa_sh = sc.kv_sh; sc.sa_sn = sc.kv_sn;
+    sc.fin = s_final; sc.fin_dt = DT_F32; sc.f_so = H * DD; sc.f_sh = DD;
+    sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = pl.nseg;
+    e = launch_recurrent_scan(sc, st);
+    if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
+
+    return launch_status(launch_gla_seg_output(a, pl.n_work, pl.dvs, io_dtype, st));
+}
+
+size_t triune_hip_gla_prefill_varlen_workspace_size(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,
+                                                    int Dv, int flags) {
+    if (n_seqs <= 0 || total_tokens < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return 0;
+    return plan_varlen(n_seqs, total_tokens, H, Dk, Dv, flags).total;
+}
+
+int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                  int g_dtype, const int64_t* strides, const int32_t* cu_seqlens, int64_t n_seqs,
+                                  int64_t total_tokens, const float* s0, void* o, int o_dtype, float* s_final,
+                                  int64_t H, int Dk, int Dv, int flags, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    if (!q || !k || !v || !g || !o || !strides || !cu_seqlens) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
+    if (n_seqs <= 0 || total_tokens < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return TRIUNE_ERR_SHAPE;
+    // (token, head) strides; the batch stride is unused (single packed batch)
+    const int64_t st3[15] = {0, strides[0], strides[1], 0, strides[2], strides[3], 0, strides[4], strides[5],
+                             0, strides[6], strides[7], 0, strides[8], strides[9]};
+    if (!vec_ok(q, io_dtype, st3 + 1, 2) || !vec_ok(k, io_dtype, st3 + 4, 2) || !vec_ok(v, io_dtype, st3 + 7, 2) ||
+        !vec_ok(g, g_dtype, st3 + 10, 2) || !vec_ok(o, o_dtype, st3 + 13, 2) ||
+        reinterpret_cast<uintptr_t>(s0) % 16 || reinterpret_cast<uintptr_t>(s_final) % 16)
+        return TRIUNE_ERR_LAYOUT;
+    const PrefillPlan pl = plan_varlen(n_seqs, total_tokens, H, Dk, Dv, flags);
+    if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
+    char* ws = reinterpret_cast<char*>(workspace);
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
+    hipStream_t st = (hipStream_t)stream;
+
+    PrefillParams a{};
+    fill_tok(a.q, q, st3 + 0);
+    fill_tok(a.k, k, st3 + 3);
+    fill_tok(a.v, v, st3 + 6);
+    fill_tok(a.g, g, st3 + 9);
+    a.o = o; a.o_sb = 0; a.o_st = st3[13]; a.o_sh = st3[14];
+    a.g_dt = g_dtype; a.o_dt = o_dtype;
+    a.s0 = s0;
+    int32_t* seg_off = reinterpret_cast<int32_t*>(ws + pl.off_segoff);
+    a.ws_state = reinterpret_cast<float*>(ws + pl.off_state);
+    a.ws_gamma = reinterpret_cast<float*>(ws + pl.off_gamma);
+    a.n_seqs = n_seqs; a.H = H; a.T = 0; a.Dk = Dk; a.Dv = Dv;
+    a.P = pl.P; a.nseg_dense = 1; a.varlen = 1; a.cu = cu_seqlens; a.seg_off = seg_off;
+    a.flags = flags & 0xff & ~TRIUNE_FLAG_TAIL_UNCLAMPED;
+
+    hipError_t e = launch_gla_varlen_plan(cu_seqlens, n_seqs, pl.P, seg_off, st);
+    if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    if (pl.n_work > 0) {
+        e = launch_gla_seg_state(a, pl.n_work, pl.dvs, io_dtype, st);
+        if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    }
+    const int64_t DD = (int64_t)Dk * Dv;
+    ScanParams sc{};
+    sc.kv = a.ws_state; sc.kv_dt = DT_F32;
+    sc.kv_so = 0; sc.kv_sh = DD; sc.kv_sn = H * DD;
+    sc.dec = a.ws_gamma; sc.dec_dt = DT_F32; sc.dec_is_log = 1;
+    sc.d_so = 0; sc.d_sh = Dk; sc.d_sn = H * Dk;
+    sc.init = s0; sc.i_so = H * DD; sc.i_sh = DD;
+    sc.s_all = a.ws_state; sc.sa_dt = DT_F32;
+    sc.sa_so = 0; sc.sa_sh = DD; sc.sa_sn = H * DD;
+    sc.fin = s_final; sc.fin_dt = DT_F32; sc.f_so = H * DD; sc.f_sh = DD;
+    sc.n_outer = n_seqs; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.seg_off = seg_off;
+    e = launch_recurrent_scan(sc, st);
+    if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    if (pl.n_work > 0) return launch_status(launch_gla_seg_output(a, pl.n_work, pl.dvs, io_dtype, st));
+    return TRIUNE_OK;
+}
+
+int triune_hip_recurrent_scan_fwd(const void* kv, int kv_dtype, const void* decay, int decay_dtype, const void* init,
+                                  int init_dtype, void* s_all, void* fin, int out_dtype, int64_t B, int64_t H,
+                                  int64_t N, int Dk, int Dv, void* stream) {
+    if (!kv || !decay || !s_all || !fin) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(kv_dtype) || !dtype_ok(decay_dtype) || !dtype_ok(out_dtype) || (init && !dtype_ok(init_dtype)))
+        return TRIUNE_ERR_DTYPE;
+    if (B < 0 || H < 0 || N < 0 || Dk <= 0 || Dv <= 0 || Dv % 4 != 0) return TRIUNE_ERR_SHAPE;
+    auto al = [](int dt) -> uintptr_t { return dt == TRIUNE_DT_F32 ? 16 : 8; };
+    if (reinterpret_cast<uintptr_t>(kv) % al(kv_dtype) || reinterpret_cast<uintptr_t>(s_all) % al(out_dtype) ||
+        reinterpret_cast<uintptr_t>(fin) % al(out_dtype) || (init && reinterpret_cast<uintptr_t>(init) % al(init_dtype)))
+        return TRIUNE_ERR_LAYOUT;
+    if (B == 0 || H == 0) return TRIUNE_OK;
+    const int64_t DD = (int64_t)Dk * Dv;
+    ScanParams sc{};
+    sc.kv = kv; sc.kv_dt = kv_dtype;
+    sc.kv_so = H * N * DD; sc.kv_sh = N * DD; sc.kv_sn = DD;
+    sc.dec = decay; sc.dec_dt = decay_dtype; sc.dec_is_log = 0;
+    sc.d_so = H * N * Dk; sc.d_sh = N * Dk; sc.d_sn = Dk;
+    sc.init = nullptr; sc.init_any = init; sc.init_dt = init_dtype; sc.i_so = H * DD; sc.i_sh = DD;
+    sc.s_all = s_all; sc.sa_dt = out_dtype; sc.sa_so = sc.kv_so; sc.sa_sh = sc.kv_sh; sc.sa_sn = sc.kv_sn;
+    sc.fin = fin; sc.fin_dt = out_dtype; sc.f_so = H * DD; sc.f_sh = DD;
+    sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = N;
+    return launch_status(launch_recurrent_scan(sc, (hipStream_t)stream));
+}
+
+int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                           const void* beta, int beta_dtype, int beta_kind, const int64_t* strides, const float* s0,
+                           void* o, int o_dtype, float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
+                           void* stream) {
+    if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
+    if (beta_kind < TRIUNE_BETA_NONE || beta_kind > TRIUNE_BETA_VALUE) return TRIUNE_ERR_SHAPE;
+    if (beta_kind != TRIUNE_BETA_NONE && !beta) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype) ||
+        (beta_kind != TRIUNE_BETA_NONE && !dtype_ok(beta_dtype)))
+        return TRIUNE_ERR_DTYPE;
+    if (B < 0 || T < 0 || H <= 0) return TRIUNE_ERR_SHAPE;
+    if (!((Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128))) return TRIUNE_ERR_SHAPE;
+    if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
+        !vec_ok(g, g_dtype, strides + 9, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
+        reinterpret_cast<uintptr_t>(s_final) % 16)
+        return TRIUNE_ERR_LAYOUT;
+    if (B == 0) return TRIUNE_OK;
+    GdnParams a{};
+    a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
+    a.io_dt = io_dtype; a.g_dt = g_dtype; a.beta_dt = beta_dtype; a.o_dt = o_dtype; a.beta_kind = beta_kind;
+    a.q_sb = strides[0]; a.q_st = strides[1]; a.q_sh = strides[2];
+    a.k_sb = strides[3]; a.k_st = strides[4]; a.k_sh = strides[5];
+    a.v_sb = strides[6]; a.v_st = strides[7]; a.v_sh = strides[8];
+    a.g_sb = strides[9]; a.g_st = strides[10]; a.g_sh = strides[11];
+    a.b_sb = strides[12]; a.b_st = strides[13]; a.b_sh = strides[14];
+    a.o_sb = strides[15]; a.o_st = strides[16]; a.o_sh = strides[17];
+    a.o = o; a.s0 = s0; a.s_final = s_final;
+    a.B = B; a.T = T; a.H = H;
+    return launch_status(launch_gdn_tokenwise(a, Dk, Dv, (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,192 @@
+// common.h -- device helpers shared by the GLA / Gated DeltaNet kernels (gfx950, wave64).
+//
+// MFMA fragment conventions used throughout (v_mfma_f32_16x16x32_bf16):
+//   lane l = 16*g4 + r16  (g4 = l >> 4 in 0..3, r16 = l & 15)
+//   A operand (16 x 32, M x K):  lane holds row m = r16, eight K slots (g4, j), j = 0..7
+//   B operand (32 x 16, K x N):  lane holds column n = r16, the same eight K slots (g4, j)
+//   C/D (16 x 16):               lane holds rows 4*g4 + i (i = 0..3) of column r16
+// Any bijection between K slots and the contracted index is valid as long as the A and B
+// operands use the same one; the kernels pick the one that lets accumulator tiles feed the
+// next product without moving data between lanes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace triune {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+
+__device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+__device__ __forceinline__ float bf2f(__bf16 x) { return (float)x; }
+
+// ---------------------------------------------------------------------------------------
+// Splitting fp32 values into sums of bf16 parts: x ~= p0 + p1 (+ p2).  Each part is the
+// round-to-nearest bf16 of the remaining residual, so N parts carry ~8N mantissa bits.
+// ---------------------------------------------------------------------------------------
+template <int N>
+struct Split8 {
+    bf16x8 p[N];
+};
+
+template <int N>
+__device__ __forceinline__ Split8<N> split8(const float (&x)[8]) {
+    Split8<N> s;
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = x[j];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            __bf16 h = (__bf16)r[j];
+            s.p[n][j] = h;
+            if (n + 1 < N) r[j] = r[j] - (float)h;
+        }
+    }
+    return s;
+}
+
+// Products of split operands: sum over part pairs (ia, ib) with ia + ib < NS.
+// NA / NB are the number of parts each operand carries (an operand exactly representable
+// in bf16 has one part).
+template <int NA, int NB, int NS>
+__device__ __forceinline__ f32x4 mfma_split(const Split8<NA>& a, const Split8<NB>& b, f32x4 c) {
+#pragma unroll
+    for (int ia = 0; ia < NA; ++ia)
+#pragma unroll
+        for (int ib = 0; ib < NB; ++ib)
+            if (ia + ib < NS) c = mfma(a.p[ia], b.p[ib], c);
+    return c;
+}
+
+// ---------------------------------------------------------------------------------------
+// Element loads: eight consecutive elements starting at p (16-byte aligned for 16-bit types,
+// 32-byte for fp32), returned as float, or zeros when !valid.
+// ---------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, bool valid, float (&x)[8]);
+
+template <>
+__device__ __forceinline__ void load8<__bf16>(const __bf16* p, bool valid, float (&x)[8]) {
+    if (valid) {
+        uint4 u = *reinterpret_cast<const uint4*>(p);
+        uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x[2 * j] = __uint_as_float(w[j] << 16);
+            x[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = 0.f;
+    }
+}
+
+template <>
+__device__ __forceinline__ void load8<_Float16>(const _Float16* p, bool valid, float (&x)[8]) {
+    if (valid) {
+        f16x8 h = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = (float)h[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = 0.f;
+    }
+}
+
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, bool valid, float (&x)[8]) {
+    if (valid) {
+        float4 a = reinterpret_cast<const float4*>(p)[0];
+        float4 b = reinterpret_cast<const float4*>(p)[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = 0.f;
+    }
+}
+
+// Runtime-typed variant (gates may be fp32 while q/k/v are 16-bit).
+__device__ __forceinline__ void load8_dt(const void* p, int dt, bool valid, float (&x)[8]) {
+    if (dt == DT_F32) load8<float>(reinterpret_cast<const float*>(p), valid, x);
+    else if (dt == DT_BF16) load8<__bf16>(reinterpret_cast<const __bf16*>(p), valid, x);
+    else load8<_Float16>(reinterpret_cast<const _Float16*>(p), valid, x);
+}
+
+__device__ __forceinline__ int dt_size(int dt) { return dt == DT_F32 ? 4 : 2; }
+
+// Store eight consecutive floats as dtype dt.
+__device__ __forceinline__ void store8_dt(void* p, int dt, const float (&x)[8]) {
+    if (dt == DT_F32) {
+        float4* q = reinterpret_cast<float4*>(p);
+        q[0] = make_float4(x[0], x[1], x[2], x[3]);
+        q[1] = make_float4(x[4], x[5], x[6], x[7]);
+    } else if (dt == DT_BF16) {
+        bf16x8 h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = (__bf16)x[j];
+        *reinterpret_cast<bf16x8*>(p) = h;
+    } else {
+        f16x8 h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = (_Float16)x[j];
+        *reinterpret_cast<f16x8*>(p) = h;
+    }
+}
+
+// Store four consecutive floats as dtype dt.
+__device__ __forceinline__ void store4_dt(void* p, int dt, float a, float b, float c, float d) {
+    if (dt == DT_F32) {
+        *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+    } else if (dt == DT_BF16) {
+        bf16x4 h = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+        *reinterpret_cast<bf16x4*>(p) = h;
+    } else {
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+        f16x4 h = {(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
+        *reinterpret_cast<f16x4*>(p) = h;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Lane helpers (wave64).
+// ---------------------------------------------------------------------------------------
+// Value of x in lane (lane - n) of the same 16-lane row, or 0 for the first n lanes of the
+// row (DPP row_shr with bound_ctrl).
+template <int N>
+__device__ __forceinline__ float row_shr(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
+}
+
+// Inclusive prefix sum across the 16 lanes of each row.
+__device__ __forceinline__ float row_inclusive_scan(float x) {
+    x += row_shr<1>(x);
+    x += row_shr<2>(x);
+    x += row_shr<4>(x);
+    x += row_shr<8>(x);
+    return x;
+}
+
+// Value held by lane src_lane.
+__device__ __forceinline__ float lane_bcast(float x, int src_lane) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
+}
+
+__device__ __forceinline__ float fast_exp(float x) {
+    // exp(x) = 2^(x log2 e); v_exp_f32 is accurate to ~1 ulp over the range used here.
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+}  // namespace triune

@@ -1,0 +1,89 @@
+// kernels.h -- parameter blocks and launchers of the gfx950 kernels (internal to libtriune_hip).
+#pragma once
+
+#include "common.h"
+
+namespace triune {
+
+struct TokTensor {
+    const void* p;
+    int64_t sb, st, sh;  // element strides: batch, token, head (innermost stride is 1)
+};
+
+struct PrefillParams {
+    TokTensor q, k, v, g;
+    void* o;
+    int64_t o_sb, o_st, o_sh;
+    int g_dt, o_dt;
+    const float* s0;       // [n_seqs, H, Dk, Dv] or null
+    float* ws_state;       // [n_work, H, Dk, Dv]
+    float* ws_gamma;       // [n_work, H, Dk]
+    int64_t n_seqs, H, T;  // T: dense sequence length
+    int Dk, Dv;
+    int P;                 // chunks per segment
+    int nseg_dense;        // segments per sequence (dense)
+    int varlen;
+    const int32_t* cu;     // varlen: [n_seqs + 1] token offsets (device)
+    const int32_t* seg_off;// varlen: [n_seqs + 1] segment offsets (device, from plan kernel)
+    int flags;             // bit 0: the last token of each sequence keeps g unclamped
+};
+
+struct ScanParams {
+    const void* kv;
+    int kv_dt;
+    int64_t kv_so, kv_sh, kv_sn;
+    const void* dec;  // decay factor or log-decay, per (n, dim)
+    int dec_dt;
+    int dec_is_log;
+    int64_t d_so, d_sh, d_sn;
+    const float* init;  // fp32 or null; [o][h] stride i_so, i_sh, contiguous Dk*Dv
+    int64_t i_so, i_sh;
+    const void* init_any;  // alternative init in init_dt (FusedRecurrentScan), or null
+    int init_dt;
+    void* s_all;
+    int sa_dt;
+    int64_t sa_so, sa_sh, sa_sn;
+    void* fin;
+    int fin_dt;
+    int64_t f_so, f_sh;
+    int64_t n_outer, H;
+    int Dk, Dv;
+    int64_t N;              // steps when seg_off is null
+    const int32_t* seg_off; // per outer o: steps N_o = seg_off[o+1]-seg_off[o], first step seg_off[o]
+};
+
+struct DecodeParams {
+    const void* q; const void* k; const void* v; const void* g;
+    int io_dt, g_dt, o_dt;
+    int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh, g_sb, g_sh, o_sb, o_sh;  // element strides
+    const float* state_in;  // [B, H, Dk, Dv]
+    float* state_out;       // may equal state_in
+    const int32_t* slots;   // optional: state row of batch b is slots[b] (state pool), or null
+    void* o;
+    int64_t B, H;
+};
+
+enum BetaKind : int { BETA_NONE = 0, BETA_HEAD = 1, BETA_KEY = 2, BETA_VALUE = 3 };
+
+struct GdnParams {
+    const void* q; const void* k; const void* v; const void* g; const void* beta;
+    int io_dt, g_dt, beta_dt, o_dt, beta_kind;
+    int64_t q_sb, q_st, q_sh, k_sb, k_st, k_sh, v_sb, v_st, v_sh, g_sb, g_st, g_sh;
+    int64_t b_sb, b_st, b_sh;  // beta strides (batch, token, head); innermost 1 for per-dim kinds
+    int64_t o_sb, o_st, o_sh;
+    void* o;
+    const float* s0;   // [B, H, Dk, Dv] or null
+    float* s_final;    // [B, H, Dk, Dv] or null
+    int64_t B, T, H;
+};
+
+hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);
+hipError_t launch_gla_decode(const DecodeParams& a, int Dk, int Dv, hipStream_t stream);
+hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t stream);
+// Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).  dvs = Dv slice.
+hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int dvs, int io_dt, hipStream_t stream);
+hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int dvs, int io_dt, hipStream_t stream);
+hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream);
+int prefill_dv_slice(int Dk, int Dv);
+
+}  // namespace triune

@@ -1,0 +1,98 @@
+// recurrent_scan.hip -- exclusive affine scan over a sequence of [Dk, Dv] states.
+//
+// For each (outer o, head h) and n = 0..N_o-1, with s starting at init (or zero):
+//   s_all[n] = s ;   s = decay[n] (row-broadcast over Dv) * s + kv[n]
+// and fin = s after the last step.  This is the forward of the reference's
+// FusedRecurrentScan (triune/kernels/fast_gla.py:34-64 kernel, :109-149 wrapper), and the
+// prefill's inter-segment carry (decay given as a log, kv = segment-local states, s_all
+// written in place of kv).  Arithmetic in fp32; kv / s_all / fin may be fp32, bf16 or fp16.
+#include "kernels.h"
+
+namespace triune {
+
+__device__ __forceinline__ float ld_dt(const void* p, int dt, int64_t i) {
+    if (dt == DT_F32) return reinterpret_cast<const float*>(p)[i];
+    if (dt == DT_BF16) return (float)reinterpret_cast<const __bf16*>(p)[i];
+    return (float)reinterpret_cast<const _Float16*>(p)[i];
+}
+
+__device__ __forceinline__ void ld4_dt(const void* p, int dt, int64_t i, float (&x)[4]) {
+    if (dt == DT_F32) {
+        float4 a = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    } else if (dt == DT_BF16) {
+        bf16x4 a = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const __bf16*>(p) + i);
+        x[0] = (float)a[0]; x[1] = (float)a[1]; x[2] = (float)a[2]; x[3] = (float)a[3];
+    } else {
+        typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+        f16x4 a = *reinterpret_cast<const f16x4*>(reinterpret_cast<const _Float16*>(p) + i);
+        x[0] = (float)a[0]; x[1] = (float)a[1]; x[2] = (float)a[2]; x[3] = (float)a[3];
+    }
+}
+
+__device__ __forceinline__ void st4_dt(void* p, int dt, int64_t i, const float (&x)[4]) {
+    if (dt == DT_F32) store4_dt(reinterpret_cast<float*>(p) + i, dt, x[0], x[1], x[2], x[3]);
+    else if (dt == DT_BF16) store4_dt(reinterpret_cast<__bf16*>(p) + i, dt, x[0], x[1], x[2], x[3]);
+    else store4_dt(reinterpret_cast<_Float16*>(p) + i, dt, x[0], x[1], x[2], x[3]);
+}
+
+// grid: (ceil(Dk*Dv/4 / 256), H, n_outer), block 256; each thread owns 4 consecutive elements.
+__global__ __launch_bounds__(256) void recurrent_scan_kernel(ScanParams a) {
+    const int64_t DD = (int64_t)a.Dk * a.Dv;
+    const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (e >= DD) return;
+    const int64_t h = blockIdx.y, o = blockIdx.z;
+    const int row = (int)(e / a.Dv);
+    int64_t n0 = 0, N = a.N;
+    if (a.seg_off) {
+        n0 = a.seg_off[o];
+        N = (int64_t)a.seg_off[o + 1] - n0;
+    }
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.init) {
+        const float* ip = a.init + o * a.i_so + h * a.i_sh + e;
+        float4 v = *reinterpret_cast<const float4*>(ip);
+        s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
+    } else if (a.init_any) {
+        ld4_dt(a.init_any, a.init_dt, o * a.i_so + h * a.i_sh + e, s);
+    }
+    const int64_t kv_base = o * a.kv_so + h * a.kv_sh + e;
+    const int64_t sa_base = o * a.sa_so + h * a.sa_sh + e;
+    const int64_t d_base = o * a.d_so + h * a.d_sh + row;
+    constexpr int U = 4;  // read U steps ahead of the dependent chain
+    int64_t n = 0;
+    for (; n + U <= N; n += U) {
+        float x[U][4], d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            ld4_dt(a.kv, a.kv_dt, kv_base + (n0 + n + u) * a.kv_sn, x[u]);
+            d[u] = ld_dt(a.dec, a.dec_dt, d_base + (n0 + n + u) * a.d_sn);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float dd = a.dec_is_log ? expf(d[u]) : d[u];
+            if (a.s_all) st4_dt(a.s_all, a.sa_dt, sa_base + (n0 + n + u) * a.sa_sn, s);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] = s[c] * dd + x[u][c];
+        }
+    }
+    for (; n < N; ++n) {
+        float x[4];
+        ld4_dt(a.kv, a.kv_dt, kv_base + (n0 + n) * a.kv_sn, x);
+        float dd = ld_dt(a.dec, a.dec_dt, d_base + (n0 + n) * a.d_sn);
+        if (a.dec_is_log) dd = expf(dd);
+        if (a.s_all) st4_dt(a.s_all, a.sa_dt, sa_base + (n0 + n) * a.sa_sn, s);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[c] = s[c] * dd + x[c];
+    }
+    if (a.fin) st4_dt(a.fin, a.fin_dt, o * a.f_so + h * a.f_sh + e, s);
+}
+
+hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream) {
+    const int64_t DD = (int64_t)a.Dk * a.Dv;
+    dim3 grid((unsigned)((DD / 4 + 255) / 256), (unsigned)a.H, (unsigned)a.n_outer);
+    hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(256), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace triune

@@ -1,0 +1,361 @@
+"""MI355X implementation of the reference's GLA / Gated DeltaNet kernel surface.
+
+Mirrors triune/kernels/fast_gla.py (names, argument meaning, return tuples and [B, T, H, D]
+layouts) on top of libtriune_hip.so.  Every function runs the HIP kernels on the tensors'
+device; there is no CPU or PyTorch fallback: unsupported inputs raise.
+
+Differences from the reference, by design:
+  * final states are returned in float32 (the reference returns q.dtype: fast_gla.py:332,
+    :739-743); the recurrent state never round-trips through bf16 between calls;
+  * beta of shape [B, T, H] at T == 1 is applied per (token, head); the reference's T == 1
+    branch broadcasts it against the wrong axes unless H == head_dim (fast_gla.py:880);
+  * backward passes are not provided (inference path only): FusedRecurrentScan.apply raises
+    if gradients are requested.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from ._lib import TriuneHipError, check, dtype_code, lib, ptr, stream_of, strides
+
+__all__ = [
+    "fast_chunk_gla",
+    "fast_chunk_gla_varlen",
+    "gla_decode_step",
+    "FusedRecurrentScan",
+    "fast_chunk_gated_deltanet",
+    "fast_recurrent_gated_deltanet",
+    "_triton_chunk_gla_tc_fwd",
+    "TriuneHipError",
+]
+
+_PREFILL_DK = (32, 64, 128)
+_DECODE_PAIRS = {(32, 32), (64, 64), (128, 128), (64, 128), (128, 64)}
+
+
+def _on_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("triune_amd kernels take HIP device tensors (device='cuda'); got a CPU tensor")
+
+
+def _round_dk(d: int) -> int:
+    for c in _PREFILL_DK:
+        if d <= c:
+            return c
+    raise ValueError(f"key head dim {d} > 128 is not supported")
+
+
+def _round32(d: int) -> int:
+    if d > 512:
+        raise ValueError(f"value head dim {d} > 512 is not supported")
+    return (d + 31) // 32 * 32
+
+
+def _vec_layout(x: torch.Tensor) -> torch.Tensor:
+    """x with unit innermost stride, 16-byte aligned rows (a contiguous copy otherwise)."""
+    m = 4 if x.dtype == torch.float32 else 8
+    ok = x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % m == 0 for s in x.stride()[:-1])
+    return x if ok else x.contiguous()
+
+
+def _pad_last(x: torch.Tensor, d: int) -> torch.Tensor:
+    return x if x.shape[-1] == d else F.pad(x, (0, d - x.shape[-1]))
+
+
+def _state_in(s: torch.Tensor | None, dk: int, dv: int) -> torch.Tensor | None:
+    if s is None:
+        return None
+    s = s.to(torch.float32)
+    if s.shape[-2] != dk or s.shape[-1] != dv:
+        s = F.pad(s, (0, dv - s.shape[-1], 0, dk - s.shape[-2]))
+    return s.contiguous()
+
+
+def _check_io(q, k, v, g):
+    _on_device(q, k, v, g)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k and v must share one dtype")
+    if g.dtype not in (q.dtype, torch.float32):
+        raise TypeError("g must have q's dtype or float32")
+
+
+def _tok3(x: torch.Tensor):
+    return (x.stride(0), x.stride(1), x.stride(2))
+
+
+# ---------------------------------------------------------------------------------------
+# GLA prefill / decode
+# ---------------------------------------------------------------------------------------
+
+
+def _prefill(q, k, v, g, initial_state, out, flags, save_final=True, out_dtype=None):
+    B, T, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    if T == 0 or B == 0:  # nothing to scan: the final state is the initial state
+        o = out if out is not None else torch.empty(B, T, H, Dv0, device=q.device, dtype=out_dtype or v.dtype)
+        if not save_final:
+            return o, None
+        if initial_state is None:
+            return o, torch.zeros(B, H, Dk0, Dv0, device=q.device, dtype=torch.float32)
+        return o, initial_state.to(torch.float32).clone()
+    Dk, Dv = _round_dk(Dk0), _round32(Dv0)
+    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
+    vp = _vec_layout(_pad_last(v, Dv))
+    odt = out.dtype if out is not None else (out_dtype or v.dtype)
+    if out is not None and out.shape[-1] == Dv and out.stride(-1) == 1 and _vec_layout(out) is out:
+        o = out
+    else:
+        o = torch.empty(B, T, H, Dv, device=q.device, dtype=odt)
+    s0 = _state_in(initial_state, Dk, Dv)
+    sf = torch.empty(B, H, Dk, Dv, device=q.device, dtype=torch.float32) if save_final else None
+    L = lib()
+    wsb = L.triune_hip_gla_prefill_workspace_size(B, T, H, Dk, Dv, flags)
+    ws = torch.empty(max(int(wsb), 256), device=q.device, dtype=torch.uint8)
+    st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), _tok3(o))
+    rc = L.triune_hip_gla_prefill(
+        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, ptr(s0), ptr(o), dtype_code(o),
+        ptr(sf), B, T, H, Dk, Dv, flags, ptr(ws), ws.numel(), stream_of(q),
+    )
+    check(rc, "triune_hip_gla_prefill")
+    if o is not out:
+        res = o[..., :Dv0]
+        if out is not None:
+            out.copy_(res)
+            res = out
+        o = res
+    if sf is not None and (Dk != Dk0 or Dv != Dv0):
+        sf = sf[..., :Dk0, :Dv0].contiguous()
+    return o, sf
+
+
+def gla_decode_step(q, k, v, g, state, out=None, *, inplace=False, slots=None, out_dtype=None):
+    """One recurrent decode step for a batch of sequences (reference: fast_gla.py:746-753,
+    csrc/engine/engine.cpp:419-475, csrc/kernels/gla.cu:23-75):
+        S <- diag(exp(g)) S + k v^T ;  o = S^T q          (g not clamped)
+    q, k, g: [B, 1, H, Dk] or [B, H, Dk]; v: [B, 1, H, Dv] or [B, H, Dv]; state fp32
+    [B, H, Dk, Dv] (or a pool [N, H, Dk, Dv] addressed by int32 `slots` [B]).
+    Returns (o shaped like v, state).  With inplace=True the state tensor is updated in place
+    (it must then be a contiguous float32 tensor); otherwise a new state is returned."""
+    _check_io(q, k, v, g)
+    squeeze = q.dim() == 4
+    if squeeze:
+        if q.shape[1] != 1:
+            raise ValueError("decode step takes one token per sequence (T == 1)")
+        q, k, v, g = q[:, 0], k[:, 0], v[:, 0], g[:, 0]
+    B, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    Dk, Dv = _round_dk(Dk0), _round32(Dv0)
+    if (Dk, Dv) not in _DECODE_PAIRS:
+        Dk = Dv = max(Dk, Dv) if max(Dk, Dv) <= 128 else None
+        if Dk is None:
+            raise ValueError(f"unsupported decode head dims ({Dk0}, {Dv0})")
+    padded = (Dk, Dv) != (Dk0, Dv0)
+    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
+    vp = _vec_layout(_pad_last(v, Dv))
+    if inplace:
+        if padded or state.dtype != torch.float32 or not state.is_contiguous():
+            raise ValueError("inplace decode needs a contiguous float32 state with supported head dims")
+        s_in = s_out = state
+    else:
+        s_in = _state_in(state, Dk, Dv)
+        s_out = torch.empty_like(s_in)
+    odt = out.dtype if out is not None else (out_dtype or v.dtype)
+    o = None
+    if out is not None and Dv == Dv0:
+        ov = out[:, 0] if out.dim() == 4 else out
+        if tuple(ov.shape) == (B, H, Dv) and ov.stride(-1) == 1 and _vec_layout(ov) is ov:
+            o = ov  # write straight into the caller's buffer
+    if o is None:
+        o = torch.empty(B, H, Dv, device=q.device, dtype=odt)
+    if slots is not None:
+        slots = slots.to(device=q.device, dtype=torch.int32).contiguous()
+    st = strides(qp.stride()[:2], kp.stride()[:2], vp.stride()[:2], gp.stride()[:2], o.stride()[:2])
+    rc = lib().triune_hip_gla_decode_step(
+        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, ptr(s_in), ptr(s_out), ptr(slots),
+        ptr(o), dtype_code(o), B, H, Dk, Dv, stream_of(q),
+    )
+    check(rc, "triune_hip_gla_decode_step")
+    if not inplace and padded:
+        s_out = s_out[..., :Dk0, :Dv0].contiguous()
+    if out is not None:
+        if o.data_ptr() != out.data_ptr():
+            out.copy_(o[..., :Dv0].reshape(out.shape))
+        return out, s_out
+    o = o[..., :Dv0]
+    if squeeze:
+        o = o.unsqueeze(1)
+    return o, s_out
+
+
+def fast_chunk_gla(q, k, v, g, initial_state=None, chunk_size=64, out=None):
+    """Chunked GLA forward (reference: fast_chunk_gla, triune/kernels/fast_gla.py:692-778).
+
+    q, k, g: [B, T, H, Dk]; v: [B, T, H, Dv]; initial_state: [B, H, Dk, Dv] or None;
+    out: optional [B, T, H, Dv] output buffer (may alias g).  Returns (out, final_state) with
+    final_state in float32.  g is clamped at 0 for prefill tokens; T == 1 runs the decode step
+    (no clamp), and a single-token remainder after whole chunks of `chunk_size` keeps its g
+    unclamped, exactly as the reference's dispatch does (fast_gla.py:746-775).  chunk_size only
+    affects that dispatch rule: the kernels always use 64-token chunks internally."""
+    _check_io(q, k, v, g)
+    B, T, H, _ = q.shape
+    if T == 1:
+        st = initial_state
+        if st is None:
+            st = torch.zeros(B, H, q.shape[-1], v.shape[-1], device=q.device, dtype=torch.float32)
+        return gla_decode_step(q, k, v, g, st, out=out)
+    C = int(chunk_size)
+    flags = _lib.FLAG_TAIL_UNCLAMPED if (C > 0 and T > C and T % C == 1) else 0
+    return _prefill(q, k, v, g, initial_state, out, flags)
+
+
+def _triton_chunk_gla_tc_fwd(q, k, v, g, initial_state=None, out=None, save_final=True):
+    """Drop-in for the reference's fused prefill entry (fast_gla.py:318-380), as called by
+    VectorisedGLA (attention.py:443-451, :486-494): returns (out, final_state); when
+    save_final is False the second item is a 1-element placeholder, as in the reference."""
+    _check_io(q, k, v, g)
+    o, sf = _prefill(q, k, v, g, initial_state, out, 0, save_final=save_final)
+    if sf is None:
+        sf = torch.empty((1,), device=q.device, dtype=torch.float32)
+    return o, sf
+
+
+def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None):
+    """Packed ragged GLA prefill (no reference counterpart; equals one fast_chunk_gla call per
+    sequence).  q, k, g: [1, N, H, Dk] or [N, H, Dk]; v likewise with Dv; cu_seqlens: int32
+    [n + 1] offsets (device or host); initial_state: [n, H, Dk, Dv] or None.
+    Returns (out shaped like v, final_states fp32 [n, H, Dk, Dv]).  g is clamped at 0."""
+    _check_io(q, k, v, g)
+    lead1 = q.dim() == 4
+    if lead1:
+        if q.shape[0] != 1:
+            raise ValueError("packed varlen tensors have batch size 1")
+        q, k, v, g = q[0], k[0], v[0], g[0]
+    N, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    Dk, Dv = _round_dk(Dk0), _round32(Dv0)
+    cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    n = cu.numel() - 1
+    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
+    vp = _vec_layout(_pad_last(v, Dv))
+    odt = out.dtype if out is not None else v.dtype
+    o = torch.empty(N, H, Dv, device=q.device, dtype=odt)
+    s0 = _state_in(initial_state, Dk, Dv)
+    sf = torch.empty(n, H, Dk, Dv, device=q.device, dtype=torch.float32)
+    L = lib()
+    wsb = L.triune_hip_gla_prefill_varlen_workspace_size(n, N, H, Dk, Dv, 0)
+    ws = torch.empty(max(int(wsb), 256), device=q.device, dtype=torch.uint8)
+    st = strides(qp.stride()[:2], kp.stride()[:2], vp.stride()[:2], gp.stride()[:2], o.stride()[:2])
+    rc = L.triune_hip_gla_prefill_varlen(
+        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, ptr(cu), n, N, ptr(s0), ptr(o),
+        dtype_code(o), ptr(sf), H, Dk, Dv, 0, ptr(ws), ws.numel(), stream_of(q),
+    )
+    check(rc, "triune_hip_gla_prefill_varlen")
+    o = o[..., :Dv0]
+    if Dk != Dk0 or Dv != Dv0:
+        sf = sf[..., :Dk0, :Dv0].contiguous()
+    if lead1:
+        o = o.unsqueeze(0)
+    if out is not None:
+        out.copy_(o)
+        o = out
+    return o, sf
+
+
+# ---------------------------------------------------------------------------------------
+# FusedRecurrentScan (forward)
+# ---------------------------------------------------------------------------------------
+
+
+class FusedRecurrentScan:
+    """Exclusive affine scan over chunk states (reference: FusedRecurrentScan, fast_gla.py:109-203).
+
+    apply(kv [B,H,N,Dk,Dv], decay_k [B,H,N,Dk,1], init_state [B,H,Dk,Dv]) ->
+        (S_all [B,H,N,Dk,Dv], final [B,H,Dk,Dv]), both in kv.dtype, where S_all[:, :, n] is the
+    state before step n and each step is s <- decay * s + kv.  Forward only."""
+
+    @staticmethod
+    def apply(kv: torch.Tensor, decay_k: torch.Tensor, init_state: torch.Tensor):
+        if torch.is_grad_enabled() and any(t.requires_grad for t in (kv, decay_k, init_state)):
+            raise NotImplementedError("FusedRecurrentScan backward is not implemented (inference path only)")
+        _on_device(kv, decay_k, init_state)
+        B, H, N, Dk, Dv = kv.shape
+        kvc = kv.contiguous()
+        dec = decay_k.expand(B, H, N, Dk, 1)[..., 0].contiguous()
+        init = init_state.expand(B, H, Dk, Dv).contiguous()
+        if Dv % 4 != 0:
+            raise ValueError("FusedRecurrentScan needs Dv % 4 == 0")
+        s_all = torch.empty_like(kvc)
+        fin = torch.empty(B, H, Dk, Dv, device=kv.device, dtype=kv.dtype)
+        rc = lib().triune_hip_recurrent_scan_fwd(
+            ptr(kvc), dtype_code(kvc), ptr(dec), dtype_code(dec), ptr(init), dtype_code(init), ptr(s_all), ptr(fin),
+            dtype_code(s_all), B, H, N, Dk, Dv, stream_of(kv),
+        )
+        check(rc, "triune_hip_recurrent_scan_fwd")
+        return s_all, fin
+
+
+# ---------------------------------------------------------------------------------------
+# Gated DeltaNet
+# ---------------------------------------------------------------------------------------
+
+
+def _gdn(q, k, v, g, beta, initial_state, beta_kind):
+    _check_io(q, k, v, g)
+    _on_device(beta, initial_state)
+    B, T, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    D = _round_dk(max(Dk0, Dv0))
+    qp, kp, gp, vp = (_vec_layout(_pad_last(x, D)) for x in (q, k, g, v))
+    bp = None
+    bst = (0, 0, 0)
+    if beta is not None:
+        bp = beta
+        if beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE):
+            bp = _pad_last(beta, D)
+        bp = bp.contiguous()
+        bst = (bp.stride(0), bp.stride(1), bp.stride(2))
+    o = torch.empty(B, T, H, D, device=q.device, dtype=v.dtype)
+    s0 = _state_in(initial_state, D, D)
+    sf = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), bst, _tok3(o))
+    rc = lib().triune_hip_gdn_prefill(
+        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(bp),
+        dtype_code(bp) if bp is not None else 0, beta_kind, st, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
+        B, T, H, D, D, stream_of(q),
+    )
+    check(rc, "triune_hip_gdn_prefill")
+    if D != Dv0:
+        o = o[..., :Dv0]
+    if D != Dk0 or D != Dv0:
+        sf = sf[..., :Dk0, :Dv0].contiguous()
+    return o, sf
+
+
+def _beta_kind(beta, orientation):
+    if beta is None:
+        return _lib.BETA_NONE
+    if beta.dim() == 3:
+        return _lib.BETA_HEAD
+    return _lib.BETA_KEY if orientation == "key" else _lib.BETA_VALUE
+
+
+def fast_recurrent_gated_deltanet(q, k, v, g, beta=None, initial_state=None):
+    """Gated DeltaNet, reference variant (fast_gla.py:781-836):
+        u_t = v_t - S_{t-1}^T k_t ; S_t = diag(exp(min(g_t,0))) S_{t-1} + beta_t (k_t u_t^T) ; o_t = S_t^T q_t
+    beta None, [B, T, H] or [B, T, H, D]; a 4-D beta scales rows (key dim), as this reference
+    function does.  Returns (out, final_state fp32)."""
+    return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, "key"))
+
+
+def fast_chunk_gated_deltanet(q, k, v, g, beta=None, initial_state=None, chunk_size=64):
+    """Gated DeltaNet operator entry (reference: fast_chunk_gated_deltanet, fast_gla.py:839-904).
+    A 4-D beta scales columns (value dim) as the reference's GPU kernel does for T > 1
+    (fast_gla.py:464-465), and rows at T == 1 (fast_gla.py:880).  chunk_size is accepted for
+    signature parity.  Returns (out, final_state fp32)."""
+    T = q.shape[1]
+    orientation = "key" if T == 1 else "value"
+    return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, orientation))
