@@ -92,7 +92,8 @@ int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, cons
  * q, k, v, g, o.  o may alias g when both have the same dtype and strides (the reference's
  * VectorisedGLA passes out=g, attention.py:443-451).  s0 / s_final: fp32 [B, H, Dk, Dv] or NULL.
  * flags: TRIUNE_FLAG_TAIL_UNCLAMPED reproduces fast_chunk_gla's unclamped single-token
- * remainder (fast_gla.py:768-775) for the last token.  Dk in {32, 64, 128}; Dv a multiple of 32.
+ * remainder (fast_gla.py:768-775) for the last token.  (Dk, Dv) in {(32,32), (64,64), (128,128),
+ * (64,128), (128,64)}; g_dtype is io_dtype or TRIUNE_DT_F32.
  * workspace: device buffer of at least triune_hip_gla_prefill_workspace_size(...) bytes.
  * Replaces: _triton_chunk_gla_tc_fwd (fast_gla.py:318-380), fast_chunk_gla (fast_gla.py:692-778). */
 size_t triune_hip_gla_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags);
@@ -105,6 +106,7 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
  * [total_tokens, H, D] tensors, starts from s0[i] (or 0) and ends in s_final[i]; every token's
  * g is clamped at 0.  cu_seqlens: device int32 [n_seqs + 1], non-decreasing, cu[0] = 0,
  * cu[n_seqs] = total_tokens.  strides[10] = (token, head) element strides of q, k, v, g, o.
+ * Head dims and dtypes as for triune_hip_gla_prefill.
  * No reference counterpart: the reference has no cu_seqlens path; this is one launch for what
  * would be a loop of fast_chunk_gla calls (fast_gla.py:692-778), one per sequence. */
 size_t triune_hip_gla_prefill_varlen_workspace_size(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,

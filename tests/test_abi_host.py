@@ -1,0 +1,128 @@
+"""CPU tests of the C-ABI boundary and the host-side logic (no GPU compute is launched).
+
+Every call here fails argument validation before any HIP API is touched, so these run in a
+container without a GPU."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import triune_amd
+import triune_amd._lib as L
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "triune_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(triune_hip_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_entry_point():
+    lib = L.lib()
+    declared = _declared()
+    assert len(declared) >= 9
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/triune_hip.h but not exported"
+    assert set(declared) == set(L.EXPORTS)
+
+
+def test_abi_version_matches_header():
+    m = re.search(r"#define TRIUNE_HIP_ABI_VERSION (\d+)", HEADER.read_text())
+    assert L.lib().triune_hip_abi_version() == int(m.group(1))
+
+
+def test_error_strings_and_codes_match_header():
+    text = HEADER.read_text()
+    codes = {k: int(v) for k, v in re.findall(r"(TRIUNE_ERR_\w+) = (-\d+)", text)}
+    assert codes == {
+        "TRIUNE_ERR_NULL": -1,
+        "TRIUNE_ERR_SHAPE": -2,
+        "TRIUNE_ERR_DTYPE": -3,
+        "TRIUNE_ERR_LAYOUT": -4,
+        "TRIUNE_ERR_WORKSPACE": -5,
+        "TRIUNE_ERR_LAUNCH": -6,
+    }
+    lib = L.lib()
+    for c in [0, *codes.values()]:
+        assert lib.triune_hip_error_string(c)
+    assert lib.triune_hip_error_string(-99) == b"unknown error"
+
+
+_FAKE = ctypes.c_void_p(0x1000)  # 16-byte aligned, never dereferenced: validation fails first
+
+
+def _st(n):
+    return (ctypes.c_int64 * n)(*([64] * n))
+
+
+def test_prefill_validation_errors():
+    lib = L.lib()
+    f = lib.triune_hip_gla_prefill
+    ok_args = dict(q=_FAKE, k=_FAKE, v=_FAKE, g=_FAKE, io=1, gdt=1, st=_st(15), s0=None, o=_FAKE, odt=1, sf=None,
+                   B=1, T=64, H=1, Dk=64, Dv=64, flags=0, ws=None, wsb=0, stream=None)
+
+    def call(**kw):
+        a = {**ok_args, **kw}
+        return f(a["q"], a["k"], a["v"], a["g"], a["io"], a["gdt"], a["st"], a["s0"], a["o"], a["odt"], a["sf"],
+                 a["B"], a["T"], a["H"], a["Dk"], a["Dv"], a["flags"], a["ws"], a["wsb"], a["stream"])
+
+    assert call(q=None) == -1
+    assert call(io=7) == -3
+    assert call(Dk=48) == -2
+    assert call(Dv=40) == -2
+    assert call(H=0) == -2
+    assert call(st=(ctypes.c_int64 * 15)(*([63] * 15))) == -4  # rows not 16-byte aligned
+    assert call(q=ctypes.c_void_p(0x1002)) == -4
+    assert call(ws=None, wsb=0) == -5  # workspace required once T > 0
+
+
+def test_decode_and_gdn_and_scan_validation_errors():
+    lib = L.lib()
+    d = lib.triune_hip_gla_decode_step
+    assert d(None, _FAKE, _FAKE, _FAKE, 1, 1, _st(10), _FAKE, _FAKE, None, _FAKE, 1, 1, 1, 64, 64, None) == -1
+    assert d(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _st(10), _FAKE, _FAKE, None, _FAKE, 1, 1, 1, 64, 32, None) == -2
+    assert d(_FAKE, _FAKE, _FAKE, _FAKE, 5, 1, _st(10), _FAKE, _FAKE, None, _FAKE, 1, 1, 1, 64, 64, None) == -3
+    gdn = lib.triune_hip_gdn_prefill
+    assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 1, _st(18), None, _FAKE, 1, None, 1, 8, 1, 64, 64, None) == -1
+    assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 9, _st(18), None, _FAKE, 1, None, 1, 8, 1, 64, 64, None) == -2
+    assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, _st(18), None, _FAKE, 1, None, 1, 8, 1, 48, 48, None) == -2
+    sc = lib.triune_hip_recurrent_scan_fwd
+    assert sc(None, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -1
+    assert sc(_FAKE, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 6, None) == -2
+    assert sc(_FAKE, 4, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -3
+
+
+def test_workspace_sizes():
+    lib = L.lib()
+    w1 = lib.triune_hip_gla_prefill_workspace_size(4, 16384, 6, 64, 64, 0)
+    w2 = lib.triune_hip_gla_prefill_workspace_size(4, 2 * 16384, 6, 64, 64, 0)
+    assert 0 < w1 < 64 << 20 and w1 <= w2
+    assert lib.triune_hip_gla_prefill_workspace_size(1, 64, 1, 48, 64, 0) == 0
+    forced = lib.triune_hip_gla_prefill_workspace_size(1, 64 * 100, 1, 64, 64, 10 << L.FLAG_SEG_SHIFT)
+    assert forced >= 10 * 64 * 64 * 4  # 10 segments of one 64x64 fp32 state
+    assert lib.triune_hip_gla_prefill_varlen_workspace_size(32, 133000, 12, 128, 128, 0) > 0
+
+
+def test_host_layer_rejects_cpu_tensors_and_bad_dtypes():
+    q = torch.zeros(1, 4, 1, 64)
+    with pytest.raises(ValueError):
+        triune_amd.fast_chunk_gla(q, q, q, q)
+    with pytest.raises(ValueError):
+        triune_amd.gla(q, q, q, q)
+    with pytest.raises(ValueError):
+        triune_amd.gated_deltanet(q, q, q, q)
+    with pytest.raises(ValueError):
+        triune_amd.FusedRecurrentScan.apply(torch.zeros(1, 1, 2, 4, 4), torch.ones(1, 1, 2, 4, 1), torch.zeros(1, 1, 4, 4))
+    with pytest.raises(TypeError):
+        L.dtype_code(torch.zeros(1, dtype=torch.int32))
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(L, "_LIB", None)
+    monkeypatch.setattr(L, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(L.TriuneHipError):
+        L.lib()

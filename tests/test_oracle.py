@@ -1,0 +1,259 @@
+"""CPU checks that pin the fp64 oracle (oracle/gla_oracle.c) before it is trusted.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped term, the decay
+applied after instead of before the write, a wrong clamp rule, a transposed state, a wrong beta
+orientation) fails at least one of them:
+  * hand-computed scalar cases of the reference's recurrences,
+  * the non-recursive closed form, and its special cases g = 0 (causal linear attention,
+    brute force) and k = 0 (pure decay),
+  * invariants: carried-state splitting, decode steps == prefill, linearity in v,
+  * the reference's own C decode step, compiled from its sources into oracle/_ref,
+  * input/output vectors of the reference's fast_recurrent_gated_deltanet (tests/golden/).
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle.ref_port import fast_chunk_gla_cpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "gdn_reference_cpu.npz"
+
+
+def _rand(seed, *shape):
+    return np.random.default_rng(seed).standard_normal(shape)
+
+
+def _gates(seed, *shape, scale=1.0):
+    x = np.random.default_rng(seed).standard_normal(shape)
+    return -np.log1p(np.exp(-x)) * scale  # logsigmoid
+
+
+# ---------------------------------------------------------------------------------------------
+# GLA
+# ---------------------------------------------------------------------------------------------
+def test_gla_scalar_hand_case():
+    """D = 1, T = 2: S1 = e^a s + k1 v1, o1 = q1 S1; S2 = e^b S1 + k2 v2, o2 = q2 S2
+    (test_attention_fallback.py:12-24: decay, then write, then read)."""
+    s, a, b = 0.7, -0.3, -1.1
+    q1, q2, k1, k2, v1, v2 = 1.5, -0.5, 2.0, 0.25, -1.0, 3.0
+    S1 = np.exp(a) * s + k1 * v1
+    S2 = np.exp(b) * S1 + k2 * v2
+    f = lambda *x: np.array(x, dtype=np.float64).reshape(1, 2, 1, 1)  # noqa: E731
+    o, S = O.gla_fwd(f(q1, q2), f(k1, k2), f(v1, v2), f(a, b), np.full((1, 1, 1, 1), s))
+    assert np.allclose(o.ravel(), [q1 * S1, q2 * S2], rtol=0, atol=1e-14)
+    assert np.allclose(S.ravel(), [S2], rtol=0, atol=1e-14)
+
+
+@pytest.mark.parametrize("T,D,Dv", [(1, 4, 4), (9, 4, 6), (40, 8, 8), (70, 5, 3)])
+def test_gla_recurrence_equals_closed_form(T, D, Dv):
+    q, k = _rand(1, 2, T, 3, D), _rand(2, 2, T, 3, D)
+    v, g = _rand(3, 2, T, 3, Dv), _gates(4, 2, T, 3, D)
+    s0 = _rand(5, 2, 3, D, Dv)
+    o1, s1 = O.gla_fwd(q, k, v, g, s0, clamp_mode=1)
+    o2, s2 = O.gla_closed_form(q, k, v, g, s0)
+    assert np.abs(o1 - o2).max() < 1e-11 and np.abs(s1 - s2).max() < 1e-11
+
+
+def test_gla_zero_gate_is_causal_linear_attention():
+    """g = 0: o_t = sum_{s<=t} (q_t . k_s) v_s + q_t S0, brute force."""
+    T, D = 23, 6
+    q, k, v, s0 = _rand(1, 1, T, 2, D), _rand(2, 1, T, 2, D), _rand(3, 1, T, 2, D), _rand(4, 1, 2, D, D)
+    o, S = O.gla_fwd(q, k, v, np.zeros_like(q), s0)
+    ref = np.zeros_like(o)
+    for h in range(2):
+        for t in range(T):
+            ref[0, t, h] = q[0, t, h] @ s0[0, h]
+            for s in range(t + 1):
+                ref[0, t, h] += (q[0, t, h] @ k[0, s, h]) * v[0, s, h]
+    assert np.abs(o - ref).max() < 1e-11
+    kv = np.einsum("thi,thj->hij", k[0], v[0])
+    assert np.abs(S[0] - (s0[0] + kv)).max() < 1e-11
+
+
+def test_gla_zero_keys_is_pure_decay():
+    T, D = 17, 5
+    q, g, s0 = _rand(1, 1, T, 1, D), _gates(2, 1, T, 1, D), _rand(3, 1, 1, D, D)
+    o, S = O.gla_fwd(q, np.zeros_like(q), _rand(4, 1, T, 1, D), g, s0)
+    G = np.cumsum(g[0, :, 0], axis=0)
+    ref = np.stack([q[0, t, 0] @ (np.exp(G[t])[:, None] * s0[0, 0]) for t in range(T)])
+    assert np.abs(o[0, :, 0] - ref).max() < 1e-12
+    assert np.abs(S[0, 0] - np.exp(G[-1])[:, None] * s0[0, 0]).max() < 1e-12
+
+
+def test_gla_clamp_rules_follow_reference_dispatch():
+    """clamp_mode 2: T == 1 and the lone remainder token after whole chunks keep g > 0
+    (fast_gla.py:746-753, :768-775); every other token is clamped (fast_gla.py:586)."""
+    T, C, D = 65, 64, 3
+    q, k, v, s0 = _rand(1, 1, T, 1, D), _rand(2, 1, T, 1, D), _rand(3, 1, T, 1, D), _rand(4, 1, 1, D, D)
+    g = np.abs(_rand(5, 1, T, 1, D)) * 0.1  # all positive
+    o, S = O.gla_fwd(q, k, v, g, s0, chunk=C, clamp_mode=2)
+    g_ref = np.zeros_like(g)
+    g_ref[:, -1] = g[:, -1]  # only the remainder token keeps its gate
+    o2, S2 = O.gla_fwd(q, k, v, g_ref, s0, clamp_mode=0)
+    assert np.abs(o - o2).max() < 1e-12 and np.abs(S - S2).max() < 1e-12
+    o1, S1 = O.gla_fwd(q[:, :1], k[:, :1], v[:, :1], g[:, :1], s0, clamp_mode=2)
+    o1b, S1b = O.gla_decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], s0)
+    assert np.abs(o1[:, 0] - o1b).max() < 1e-12 and np.abs(S1 - S1b).max() < 1e-12
+
+
+def test_gla_split_with_carried_state_and_linearity():
+    T, D = 90, 4
+    q, k, v, v2 = (_rand(i, 2, T, 2, D) for i in range(4))
+    g, s0 = _gates(9, 2, T, 2, D), _rand(10, 2, 2, D, D)
+    o, S = O.gla_fwd(q, k, v, g, s0, clamp_mode=1)
+    oa, Sa = O.gla_fwd(q[:, :37], k[:, :37], v[:, :37], g[:, :37], s0, clamp_mode=1)
+    ob, Sb = O.gla_fwd(q[:, 37:], k[:, 37:], v[:, 37:], g[:, 37:], Sa, clamp_mode=1)
+    assert np.abs(np.concatenate([oa, ob], 1) - o).max() < 1e-12 and np.abs(Sb - S).max() < 1e-12
+    z = np.zeros_like(s0)
+    l1, _ = O.gla_fwd(q, k, v, g, z, clamp_mode=1)
+    l2, _ = O.gla_fwd(q, k, v2, g, z, clamp_mode=1)
+    l3, _ = O.gla_fwd(q, k, v + 2 * v2, g, z, clamp_mode=1)
+    assert np.abs(l3 - (l1 + 2 * l2)).max() < 1e-11
+
+
+def test_gla_varlen_is_per_sequence_recurrence():
+    lens = [3, 0, 64, 65, 1]
+    N, D = sum(lens), 4
+    q, k, v, g = _rand(1, 1, N, 2, D), _rand(2, 1, N, 2, D), _rand(3, 1, N, 2, D), _gates(4, 1, N, 2, D)
+    s0 = _rand(5, len(lens), 2, D, D)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    o, S = O.gla_varlen_fwd(q, k, v, g, cu, s0)
+    for i, (a, b) in enumerate(zip(cu[:-1], cu[1:])):
+        oi, Si = O.gla_fwd(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], s0[i:i + 1], clamp_mode=1)
+        assert oi.size == 0 or np.abs(o[:, a:b] - oi).max() < 1e-12
+        assert np.abs(S[i] - Si[0]).max() < 1e-12
+
+
+def test_decode_step_matches_reference_c_engine():
+    """The reference's own triune_gla_recurrent_step_f32 (csrc/engine/engine.cpp:419-475),
+    compiled from its sources; it uses a polynomial exp (engine.cpp:57-69), so agreement is to
+    fp32 rounding plus that approximation."""
+    if not O.ref_available():
+        pytest.skip("oracle/_ref/libtriune_core_ref.so not built (reference tree absent)")
+    BH, D = 24, 64
+    q, k, v = _rand(1, BH, D), _rand(2, BH, D), _rand(3, BH, D)
+    g, S = _gates(4, BH, D, scale=1 / 16), 0.1 * _rand(5, BH, D, D)
+    o_ref, S_ref = O.ref_c_decode_step_f32(q, k, v, g, S)
+    f32 = lambda a: a.astype(np.float32).astype(np.float64)  # noqa: E731
+    o, Sn = O.gla_decode_step(f32(q), f32(k), f32(v), f32(g), f32(S))
+    assert np.abs(Sn - S_ref).max() <= 2e-6 * max(1, np.abs(S_ref).max())
+    assert np.abs(o - o_ref).max() <= 2e-6 * max(1, np.abs(o_ref).max())
+
+
+# ---------------------------------------------------------------------------------------------
+# FusedRecurrentScan
+# ---------------------------------------------------------------------------------------------
+def test_scan_scalar_hand_case():
+    kv = np.array([1.0, 2.0, 3.0]).reshape(1, 1, 3, 1, 1)
+    d = np.array([0.5, 0.25, 2.0]).reshape(1, 1, 3, 1, 1)
+    s_all, fin = O.recurrent_scan_fwd(kv, d, np.full((1, 1, 1, 1), 4.0))
+    # s: 4 -> 4*0.5+1 = 3 -> 3*0.25+2 = 2.75 -> 2.75*2+3 = 8.5 ; exclusive outputs 4, 3, 2.75
+    assert np.allclose(s_all.ravel(), [4.0, 3.0, 2.75]) and np.allclose(fin.ravel(), [8.5])
+
+
+def test_scan_closed_form():
+    """s_all[n] = (prod_{m<n} d_m) init + sum_{m<n} (prod_{m<j<n} d_j) kv_m."""
+    B, H, N, Dk, Dv = 2, 3, 7, 4, 5
+    kv, init = _rand(1, B, H, N, Dk, Dv), _rand(2, B, H, Dk, Dv)
+    d = np.random.default_rng(3).random((B, H, N, Dk, 1))
+    s_all, fin = O.recurrent_scan_fwd(kv, d, init)
+    for n in range(N + 1):
+        ref = np.prod(d[:, :, :n], axis=2) * init
+        for m in range(n):
+            ref = ref + np.prod(d[:, :, m + 1:n], axis=2) * kv[:, :, m]
+        got = s_all[:, :, n] if n < N else fin
+        assert np.abs(got - ref).max() < 1e-12
+
+
+# ---------------------------------------------------------------------------------------------
+# Gated DeltaNet
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("name,kind", [("none", O.BETA_NONE), ("head", O.BETA_HEAD), ("key", O.BETA_KEY)])
+def test_gdn_matches_reference_golden_vectors(name, kind):
+    z = np.load(GOLDEN)
+    beta = z[f"{name}_beta"] if f"{name}_beta" in z.files else None
+    o, s = O.gdn_fwd(z[f"{name}_q"], z[f"{name}_k"], z[f"{name}_v"], z[f"{name}_g"], beta, z[f"{name}_s0"],
+                     beta_kind=kind)
+    assert np.abs(o - z[f"{name}_o"]).max() < 1e-12
+    assert np.abs(s - z[f"{name}_s"]).max() < 1e-12
+
+
+def test_gdn_zero_gate_is_delta_rule_in_transition_form():
+    """g = 0: S_t = (I - beta k k^T) S_{t-1} + beta k v^T (the textbook delta rule, computed here
+    in that matrix form, not the residual form the oracle uses)."""
+    T, D = 12, 5
+    q, k, v = _rand(1, 1, T, 1, D), _rand(2, 1, T, 1, D) * 0.4, _rand(3, 1, T, 1, D)
+    beta = np.random.default_rng(4).random((1, T, 1))
+    S = _rand(5, 1, 1, D, D)
+    o, Sf = O.gdn_fwd(q, k, v, np.zeros_like(q), beta, S)
+    cur = S[0, 0].copy()
+    for t in range(T):
+        kt = k[0, t, 0]
+        cur = (np.eye(D) - beta[0, t, 0] * np.outer(kt, kt)) @ cur + beta[0, t, 0] * np.outer(kt, v[0, t, 0])
+        assert np.abs(o[0, t, 0] - q[0, t, 0] @ cur).max() < 1e-12
+    assert np.abs(Sf[0, 0] - cur).max() < 1e-12
+
+
+def test_gdn_orthonormal_write_then_read():
+    """g = 0, beta = 1, zero state: writing v under an orthonormal key and reading with the same
+    key returns v exactly (associative recall)."""
+    D = 6
+    keys = np.linalg.qr(_rand(1, D, D))[0]
+    T = D
+    k = keys.T.reshape(1, T, 1, D)
+    v = _rand(2, 1, T, 1, D)
+    o, S = O.gdn_fwd(k, k, v, np.zeros_like(k), np.ones((1, T, 1)), None)
+    for t in range(T):
+        assert np.abs(o[0, t, 0] - v[0, t, 0]).max() < 1e-12
+
+
+def test_gdn_zero_beta_is_pure_decay():
+    T, D = 9, 4
+    q, k, v, g = _rand(1, 1, T, 1, D), _rand(2, 1, T, 1, D), _rand(3, 1, T, 1, D), _gates(4, 1, T, 1, D)
+    s0 = _rand(5, 1, 1, D, D)
+    o, S = O.gdn_fwd(q, k, v, g, np.zeros((1, T, 1)), s0)
+    G = np.cumsum(g[0, :, 0], 0)
+    assert np.abs(S[0, 0] - np.exp(G[-1])[:, None] * s0[0, 0]).max() < 1e-12
+
+
+def test_gdn_beta_orientations_differ_only_for_per_dim_beta():
+    T, D = 8, 4
+    q, k, v, g = _rand(1, 1, T, 1, D), _rand(2, 1, T, 1, D), _rand(3, 1, T, 1, D), _gates(4, 1, T, 1, D)
+    b = np.random.default_rng(6).random((1, T, 1, D))
+    ok, _ = O.gdn_fwd(q, k, v, g, b, None, beta_kind=O.BETA_KEY)
+    ov, _ = O.gdn_fwd(q, k, v, g, b, None, beta_kind=O.BETA_VALUE)
+    assert np.abs(ok - ov).max() > 1e-3
+    bh = np.broadcast_to(b[..., :1], b.shape)
+    ok, _ = O.gdn_fwd(q, k, v, g, bh, None, beta_kind=O.BETA_KEY)
+    ov, _ = O.gdn_fwd(q, k, v, g, bh, None, beta_kind=O.BETA_VALUE)
+    oh, _ = O.gdn_fwd(q, k, v, g, b[..., 0], None)
+    assert np.abs(ok - ov).max() < 1e-12 and np.abs(ok - oh).max() < 1e-12
+
+
+# ---------------------------------------------------------------------------------------------
+# CPU baseline port (oracle/ref_port.py) against the oracle
+# ---------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("T", [1, 5, 64, 65, 200, 640])
+def test_port_fp64_matches_oracle(T):
+    gen = torch.Generator().manual_seed(T)
+    q, k, v = (torch.randn(1, T, 2, 8, generator=gen, dtype=torch.float64) for _ in range(3))
+    g = torch.nn.functional.logsigmoid(torch.randn(1, T, 2, 8, generator=gen, dtype=torch.float64))
+    s0 = torch.randn(1, 2, 8, 8, generator=gen, dtype=torch.float64)
+    o, s = fast_chunk_gla_cpu(q, k, v, g, s0)
+    ro, rs = O.gla_fwd(q, k, v, g, s0)
+    assert np.abs(o.numpy() - ro).max() < 1e-10 and np.abs(s.numpy() - rs).max() < 1e-10
+
+
+def test_port_fp32_factored_path_matches_oracle():
+    gen = torch.Generator().manual_seed(1)
+    T = 1024
+    q = torch.randn(1, T, 2, 64, generator=gen) * 0.125
+    k, v = torch.randn(1, T, 2, 64, generator=gen), torch.randn(1, T, 2, 64, generator=gen)
+    g = torch.nn.functional.logsigmoid(torch.randn(1, T, 2, 64, generator=gen)) / 16
+    o, s = fast_chunk_gla_cpu(q, k, v, g, None)
+    ro, rs = O.gla_fwd(q, k, v, g, None)
+    assert np.abs(o.double().numpy() - ro).max() < 1e-4 and np.abs(s.double().numpy() - rs).max() < 1e-4

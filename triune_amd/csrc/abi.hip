@@ -31,32 +31,32 @@ bool vec4_ok(const void* p, int dt, const int64_t* st, int n) {
     return true;
 }
 
-int seg_chunks(int64_t jobs, int flags) {
-    int forced = (flags >> TRIUNE_FLAG_SEG_SHIFT) & 0xff;
+// Chunks per segment: enough (segment, head) workgroups to keep every CU busy (two resident
+// 64-column workgroups per CU), as few as possible to keep the carried-state traffic small.
+int seg_chunks(int64_t chunk_jobs, int Dv, int flags) {
+    const int forced = (flags >> TRIUNE_FLAG_SEG_SHIFT) & 0xff;
     if (forced > 0) return forced;
-    int64_t p = jobs / 1024;  // one wave per work item; ~1 resident wave per SIMD
+    const int64_t target = Dv >= 128 ? 256 : 512;
+    int64_t p = (chunk_jobs + target - 1) / target;
     if (p < 1) p = 1;
     if (p > 255) p = 255;
     return (int)p;
 }
 
-bool prefill_shape_ok(int Dk, int Dv) {
-    if (!(Dk == 32 || Dk == 64 || Dk == 128)) return false;
-    if (Dv <= 0 || Dv % 32 != 0 || Dv > 512) return false;
-    return true;
-}
+bool prefill_shape_ok(int Dk, int Dv) { return prefill_shape_supported(Dk, Dv); }
+
+bool gate_dtype_ok(int io_dtype, int g_dtype) { return g_dtype == io_dtype || g_dtype == TRIUNE_DT_F32; }
 
 struct PrefillPlan {
-    int P, dvs;
+    int P;
     int64_t nseg, n_work;
     size_t off_segoff, off_state, off_gamma, total;
 };
 
 PrefillPlan plan_dense(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {
     PrefillPlan p{};
-    p.dvs = prefill_dv_slice(Dk, Dv);
     const int64_t nchunks = (T + 63) / 64;
-    p.P = seg_chunks(B * H * nchunks * (Dv / p.dvs), flags);
+    p.P = seg_chunks(B * H * nchunks, Dv, flags);
     p.nseg = (nchunks + p.P - 1) / p.P;
     p.n_work = B * p.nseg;
     p.off_segoff = 0;
@@ -68,9 +68,8 @@ PrefillPlan plan_dense(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flag
 
 PrefillPlan plan_varlen(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk, int Dv, int flags) {
     PrefillPlan p{};
-    p.dvs = prefill_dv_slice(Dk, Dv);
     const int64_t nchunks = (total_tokens + 63) / 64 + n_seqs;
-    p.P = seg_chunks(H * nchunks * (Dv / p.dvs), flags);
+    p.P = seg_chunks(H * nchunks, Dv, flags);
     p.n_work = (total_tokens + 64 * (int64_t)p.P - 1) / (64 * (int64_t)p.P) + n_seqs;
     p.nseg = 0;
     p.off_segoff = 0;
@@ -145,6 +144,7 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
                            size_t workspace_bytes, void* stream) {
     if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
+    if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
     if (B < 0 || T < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return TRIUNE_ERR_SHAPE;
     if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
         !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
@@ -180,7 +180,7 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     a.n_seqs = B; a.H = H; a.T = T; a.Dk = Dk; a.Dv = Dv;
     a.P = pl.P; a.nseg_dense = (int)pl.nseg; a.varlen = 0; a.flags = flags & 0xff;
 
-    hipError_t e = launch_gla_seg_state(a, pl.n_work, pl.dvs, io_dtype, st);
+    hipError_t e = launch_gla_seg_state(a, pl.n_work, io_dtype, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
 
     const int64_t DD = (int64_t)Dk * Dv;
@@ -197,7 +197,7 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     e = launch_recurrent_scan(sc, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
 
-    return launch_status(launch_gla_seg_output(a, pl.n_work, pl.dvs, io_dtype, st));
+    return launch_status(launch_gla_seg_output(a, pl.n_work, io_dtype, st));
 }
 
 size_t triune_hip_gla_prefill_varlen_workspace_size(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,
@@ -213,6 +213,7 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
                                   void* stream) {
     if (!q || !k || !v || !g || !o || !strides || !cu_seqlens) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
+    if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
     if (n_seqs <= 0 || total_tokens < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return TRIUNE_ERR_SHAPE;
     // (token, head) strides; the batch stride is unused (single packed batch)
     const int64_t st3[15] = {0, strides[0], strides[1], 0, strides[2], strides[3], 0, strides[4], strides[5],
@@ -245,7 +246,7 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
     hipError_t e = launch_gla_varlen_plan(cu_seqlens, n_seqs, pl.P, seg_off, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
     if (pl.n_work > 0) {
-        e = launch_gla_seg_state(a, pl.n_work, pl.dvs, io_dtype, st);
+        e = launch_gla_seg_state(a, pl.n_work, io_dtype, st);
         if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
     }
     const int64_t DD = (int64_t)Dk * Dv;
@@ -261,7 +262,7 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
     sc.n_outer = n_seqs; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.seg_off = seg_off;
     e = launch_recurrent_scan(sc, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
-    if (pl.n_work > 0) return launch_status(launch_gla_seg_output(a, pl.n_work, pl.dvs, io_dtype, st));
+    if (pl.n_work > 0) return launch_status(launch_gla_seg_output(a, pl.n_work, io_dtype, st));
     return TRIUNE_OK;
 }
 

@@ -6,27 +6,39 @@
 // for every (sequence, head), starting from S0 (or zero), returning every o_t and S_T.
 //
 // Work decomposition.  A sequence is cut into segments of P chunks of 64 tokens.
-//   K1 seg_state : per (segment, head, Dv slice) the segment's local end state from zero,
-//                  L = sum over its tokens, and the segment's summed log-decay.
+//   K1 seg_state : per (segment, head) the segment's local end state from zero and its summed
+//                  log-decay.
 //   K2 (recurrent_scan.hip): exclusive affine scan over the segments of each (sequence, head)
 //                  S_in[p+1] = exp(Gseg_p) * S_in[p] + L_p, written in place of L; final state.
-//   K3 seg_output: per (segment, head, Dv slice) walks its chunks from S_in[p], writes o.
+//   K3 seg_output: per (segment, head) walks its chunks from S_in[p] and writes o.
 // Within a chunk (C = 64 tokens, G = inclusive cumulative log-decay from the chunk start,
 // m = G_C / 2 per key dim):
-//   Qt = q * exp(G - m), Kt = k * exp(m - G)         (|exponents| <= span/2)
-//   A^T[s][t] = sum_d Kt[s][d] Qt[t][d]  for s <= t  (causal, diagonal included)
+//   Qt = q * exp(G - m), Kt = k * exp(m - G)          (|exponents| <= span / 2)
+//   A^T[s][t] = sum_d Kt[s][d] Qt[t][d]  for s <= t   (causal, diagonal included)
 //   O^T = (exp(m) * S)^T Qt^T + V^T A^T
 //   S  <- exp(G_C) * S + exp(m) * (Kt^T V)
 // Products run on v_mfma_f32_16x16x32_bf16.  Operands that are not exactly bf16 are split
-// into 2 (16-bit I/O) or 3 (fp32 I/O) bf16 parts and the part products with combined order
-// below the split depth are accumulated in fp32.  Chunks whose key-dim decay span exceeds
-// SPAN_MAX (or that hold the reference's unclamped 1-token tail) run token by token.
+// into 2 (16-bit I/O) or 3 (fp32 I/O) bf16 parts; part products whose combined order is
+// below the split depth are accumulated in fp32.
+//
+// One workgroup of NW = Dv/16 waves handles a (segment, head).  Per chunk:
+//   stage 1  wave w, lane = token: cumulative decay, factors and split Qt/Kt for key dims
+//            [w*DPW, (w+1)*DPW) -> LDS (row planes for Qt/Kt, a [dim][token] plane for Kt^T);
+//            its own 16 value columns of V -> LDS ([column][token] plane)
+//   stage 2  the ten 16x16 causal tiles of A^T, spread over the waves -> LDS
+//   stage 3  wave w: O^T and the state update for value columns [16w, 16w+16)
+// The next chunk's inputs are loaded into registers while the current chunk is processed.
+// Chunks whose key-dim decay span exceeds SPAN_MAX (or that hold the reference's unclamped
+// 1-token tail) run token by token on the same state registers.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace triune {
 
 constexpr int CHUNK = 64;
 constexpr float SPAN_MAX = 64.f;
+constexpr int PAD = 4;  // row padding (elements) of LDS planes: spreads rows over banks
 
 struct Work {
     int64_t seq, b, row0, t_begin, t_end, len;
@@ -35,7 +47,7 @@ struct Work {
 
 __device__ __forceinline__ bool find_work(const PrefillParams& a, int64_t w, Work& wk) {
     if (!a.varlen) {
-        int64_t seq = w / a.nseg_dense;
+        const int64_t seq = w / a.nseg_dense;
         if (seq >= a.n_seqs) return false;
         wk.seq = seq;
         wk.b = seq;
@@ -43,11 +55,11 @@ __device__ __forceinline__ bool find_work(const PrefillParams& a, int64_t w, Wor
         wk.p = (int)(w - seq * a.nseg_dense);
         wk.len = a.T;
     } else {
-        int64_t total = a.seg_off[a.n_seqs];
+        const int64_t total = a.seg_off[a.n_seqs];
         if (w >= total) return false;
         int64_t lo = 0, hi = a.n_seqs - 1;  // largest seq with seg_off[seq] <= w
         while (lo < hi) {
-            int64_t mid = (lo + hi + 1) >> 1;
+            const int64_t mid = (lo + hi + 1) >> 1;
             if (a.seg_off[mid] <= w) lo = mid;
             else hi = mid - 1;
         }
@@ -63,454 +75,517 @@ __device__ __forceinline__ bool find_work(const PrefillParams& a, int64_t w, Wor
     return wk.t_begin < wk.t_end;
 }
 
+// ---------------------------------------------------------------------------------------
+// Precision and LDS layout
+// ---------------------------------------------------------------------------------------
+template <typename TIn>
+struct Prec {
+    static constexpr bool F32 = std::is_same<TIn, float>::value;
+    static constexpr int NS = F32 ? 3 : 2;                                             // parts of derived operands
+    static constexpr int NX = F32 ? 3 : (std::is_same<TIn, _Float16>::value ? 2 : 1);  // parts of V
+    static constexpr int DPL = F32 ? 1 : NS;  // LDS planes of a derived matrix (fp32 I/O: one fp32 plane)
+    static constexpr int DES = F32 ? 4 : 2;   // bytes per element of such a plane
+    static constexpr int VPL = F32 ? 1 : NX;  // LDS planes of V
+};
+
+template <typename TIn, int DK, int DV, bool OUT>
+struct Lay {
+    using P = Prec<TIn>;
+    static constexpr int NW = DV / 16;            // waves per workgroup
+    static constexpr int DPW = DK / NW;           // key dims per wave in stage 1
+    static constexpr int RS = DK + PAD;           // row stride of [token][dim] planes
+    static constexpr int TS = CHUNK + PAD;        // row stride of [dim][token] / [column][token] planes
+    static constexpr int ROWP = CHUNK * RS * P::DES;
+    static constexpr int KTTP = DK * TS * P::DES;
+    static constexpr int VPP = 16 * TS * P::DES;  // one wave's V, per plane
+    static constexpr int ATP = 10 * 64 * 4 * P::DES;
+    static constexpr int OFF_QT = 0;
+    static constexpr int OFF_KT = OFF_QT + (OUT ? P::DPL * ROWP : 0);
+    static constexpr int OFF_KTT = OFF_KT + (OUT ? P::DPL * ROWP : 0);
+    static constexpr int OFF_AT = OFF_KTT + P::DPL * KTTP;
+    static constexpr int OFF_VP = OFF_AT + (OUT ? P::DPL * ATP : 0);
+    static constexpr int OFF_FAC = OFF_VP + NW * P::VPL * VPP;
+    static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
+    static constexpr int BYTES = OFF_FLAG + 16 * 4;
+    static_assert(DPW == 8 || DPW == 16 || DPW == 32, "stage-1 dims per wave");
+    static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+
+// Causal tiles of A^T (key block sb <= query block tb); index i = tb*(tb+1)/2 + sb.
+__device__ __forceinline__ void tile_sb_tb(int i, int& sb, int& tb) {
+    tb = i >= 6 ? 3 : (i >= 3 ? 2 : (i >= 1 ? 1 : 0));
+    sb = i - tb * (tb + 1) / 2;
+}
+__device__ __forceinline__ int tile_index(int sb, int tb) { return tb * (tb + 1) / 2 + sb; }
+
+// ---- LDS plane access ------------------------------------------------------------------
+// Fragment of a plane set with row stride rs: lane (g4, r16) reads row `row`, elements
+// col0 + 4*g4 + [0,4) into K slots 0..3 and col0 + 16 + 4*g4 + [0,4) into slots 4..7.
+// 16-bit I/O: NP bf16 planes, one part each.  fp32 I/O: one fp32 plane split into NP parts.
+template <typename TIn, int NP>
+__device__ __forceinline__ Split8<NP> lds_frag(const char* base, int plane_bytes, int rs, int row, int col0, int g4) {
+    Split8<NP> f;
+    if constexpr (Prec<TIn>::F32) {
+        const float* p = reinterpret_cast<const float*>(base) + row * rs + col0 + 4 * g4;
+        const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+        const f32x4 b = *reinterpret_cast<const f32x4*>(p + 16);
+        float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        f = split8<NP>(x);
+    } else {
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+            const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes) + row * rs + col0 + 4 * g4;
+            const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
+            const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+            f.p[pl] = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        }
+    }
+    return f;
+}
+
+// One value, split into NP bf16 planes (16-bit I/O) or stored as fp32 (fp32 I/O).
+template <typename TIn, int NP>
+__device__ __forceinline__ void lds_put(char* base, int plane_bytes, int idx, float x) {
+    if constexpr (Prec<TIn>::F32) {
+        reinterpret_cast<float*>(base)[idx] = x;
+    } else {
+        float r = x;
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+            const __bf16 hb = (__bf16)r;
+            reinterpret_cast<__bf16*>(base + pl * plane_bytes)[idx] = hb;
+            r -= (float)hb;
+        }
+    }
+}
+
+// N (multiple of 4) consecutive values at element index idx (a multiple of 4).
+template <typename TIn, int NP, int N>
+__device__ __forceinline__ void lds_put_row(char* base, int plane_bytes, int idx, const float* x) {
+    if constexpr (Prec<TIn>::F32) {
+#pragma unroll
+        for (int c = 0; c < N; c += 4)
+            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(base) + idx + c) =
+                f32x4{x[c], x[c + 1], x[c + 2], x[c + 3]};
+    } else {
+        float r[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) r[j] = x[j];
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) {
+#pragma unroll
+            for (int c = 0; c < N; c += 4) {
+                bf16x4 hb;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    hb[j] = (__bf16)r[c + j];
+                    r[c + j] -= (float)hb[j];
+                }
+                *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(base + pl * plane_bytes) + idx + c) = hb;
+            }
+        }
+    }
+}
+
+// ---- global input rows (lane = token) --------------------------------------------------
+template <typename T, int N>
+struct Row {
+    static constexpr int V = N * (int)sizeof(T) / 16;  // 16-byte vectors
+    uint4 u[V];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void row_load(Row<T, N>& r, const T* p) {
+#pragma unroll
+    for (int i = 0; i < Row<T, N>::V; ++i) r.u[i] = reinterpret_cast<const uint4*>(p)[i];
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void row_float(const Row<T, N>& r, float* x, bool valid) {
+    if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+        for (int i = 0; i < Row<T, N>::V; ++i) {
+            x[4 * i] = __uint_as_float(r.u[i].x);
+            x[4 * i + 1] = __uint_as_float(r.u[i].y);
+            x[4 * i + 2] = __uint_as_float(r.u[i].z);
+            x[4 * i + 3] = __uint_as_float(r.u[i].w);
+        }
+    } else if constexpr (std::is_same<T, __bf16>::value) {
+#pragma unroll
+        for (int i = 0; i < Row<T, N>::V; ++i) {
+            const uint32_t w[4] = {r.u[i].x, r.u[i].y, r.u[i].z, r.u[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
+                x[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < Row<T, N>::V; ++i) {
+            const f16x8 hv = *reinterpret_cast<const f16x8*>(&r.u[i]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)hv[j];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) x[j] = valid ? x[j] : 0.f;
+}
+
 template <typename T>
-__device__ __forceinline__ const T* tok_ptr(const TokTensor& x, const Work& wk, int64_t t, int64_t h,
-                                            int d) {
+__device__ __forceinline__ const T* tok_row(const TokTensor& x, const Work& wk, int64_t t, int64_t h, int d) {
     return reinterpret_cast<const T*>(x.p) + wk.b * x.sb + (wk.row0 + t) * x.st + h * x.sh + d;
 }
 
-__device__ __forceinline__ const void* tok_ptr_dt(const TokTensor& x, int dt, const Work& wk, int64_t t,
-                                                  int64_t h, int d) {
-    int64_t off = wk.b * x.sb + (wk.row0 + t) * x.st + h * x.sh + d;
-    return reinterpret_cast<const char*>(x.p) + off * dt_size(dt);
+// Inclusive prefix sum over the 64 lanes of a wave (rows of 16 lanes, then across rows).
+__device__ __forceinline__ float wave_inclusive_scan(float x) {
+    x = row_inclusive_scan(x);
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));  // row_bcast:15
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));  // row_bcast:31
+    return x;
 }
 
-// Number of bf16 parts that hold an input element exactly / that derived operands carry.
-template <typename T> struct Prec;
-template <> struct Prec<__bf16> { static constexpr int NX = 1, NS = 2; };
-template <> struct Prec<_Float16> { static constexpr int NX = 2, NS = 2; };
-template <> struct Prec<float> { static constexpr int NX = 3, NS = 3; };
-
-// Permutation matrix used as B operand to transpose an A-operand fragment: lane (g4, r16)
-// holds 1 in slot j iff column 8*g4 + j of the A fragment's 32-column group is the column
-// that label r16 of a 16-column block of parity par maps to:
-//   label(16*cb + n) -> column 32*(cb >> 1) + 8*(n >> 2) + 4*(cb & 1) + (n & 3).
-__device__ __forceinline__ bf16x8 perm_frag(int par, int g4, int r16) {
-    bf16x8 f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-        f[j] = (__bf16)((g4 == (r16 >> 2) && j == 4 * par + (r16 & 3)) ? 1.f : 0.f);
-    return f;
+__device__ __forceinline__ float lane_value(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
-__device__ __forceinline__ int label_col(int blk, int n) {  // see perm_frag
-    return 32 * (blk >> 1) + 8 * (n >> 2) + 4 * (blk & 1) + (n & 3);
+// ---- the chunk inputs a wave loads (lane = token) -------------------------------------
+template <typename TIn, typename TG, int DPW>
+struct ChunkIn {
+    Row<TIn, DPW> q;
+    Row<TIn, DPW> k;
+    Row<TG, DPW> g;
+    Row<TIn, 16> v;
+};
+
+template <bool OUT, typename TIn, typename TG, int DPW>
+__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DPW>& c, const PrefillParams& a, const Work& wk, int64_t h,
+                                           int64_t tc, int nv, int lane, int d0, int c0) {
+    const int64_t t = tc + (lane < nv ? lane : nv - 1);  // every lane reads a row inside the chunk
+    if (OUT) row_load(c.q, tok_row<TIn>(a.q, wk, t, h, d0));
+    row_load(c.k, tok_row<TIn>(a.k, wk, t, h, d0));
+    row_load(c.g, tok_row<TG>(a.g, wk, t, h, d0));
+    row_load(c.v, tok_row<TIn>(a.v, wk, t, h, c0));
 }
 
-// Two accumulator tiles (rows 4*g4+i of tiles lo, hi) as the eight K slots of a fragment.
-template <int N>
-__device__ __forceinline__ Split8<N> frag_from_tiles(const f32x4& lo, const f32x4& hi, float scale_lo[4],
-                                                     float scale_hi[4]) {
-    float x[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        x[i] = lo[i] * scale_lo[i];
-        x[4 + i] = hi[i] * scale_hi[i];
-    }
-    return split8<N>(x);
-}
-
-__device__ __forceinline__ bf16x8 frag_exact(const f32x4& lo, const f32x4& hi) {
-    bf16x8 f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f[i] = (__bf16)lo[i];
-        f[4 + i] = (__bf16)hi[i];
-    }
-    return f;
-}
-
-// Chunk totals of clamped g for the lane's dims (32*ks + 8*g4 + j); returns whether the chunk
-// can take the factored MFMA path (wave-uniform).
-template <int NKS>
-__device__ __forceinline__ bool chunk_totals(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc,
-                                             int nv, int g4, int r16, int lane, float (&GC)[NKS][8],
-                                             bool tail_unclamped) {
-    bool bad = tail_unclamped;
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-        float tot[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tot[j] = 0.f;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            int t = 16 * mb + r16;
-            float gx[8];
-            load8_dt(tok_ptr_dt(a.g, a.g_dt, wk, tc + t, h, 32 * ks + 8 * g4), a.g_dt, t < nv, gx);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) tot[j] += fminf(gx[j], 0.f);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float s = row_inclusive_scan(tot[j]);
-            GC[ks][j] = lane_bcast(s, (lane & 48) | 15);
-            bad |= !(GC[ks][j] >= -SPAN_MAX);
-        }
-    }
-    return !__any(bad);
-}
-
-// Inclusive cumulative clamped log-decay for the four 16-token blocks of one dim k-step.
-__device__ __forceinline__ void chunk_cumsum(float (&gx)[4][8], int lane) {
-    float carry[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) carry[j] = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float s = row_inclusive_scan(fminf(gx[mb][j], 0.f));
-            gx[mb][j] = s + carry[j];
-            if (mb < 3) carry[j] += lane_bcast(s, (lane & 48) | 15);
-        }
-    }
-}
-
-// Token-by-token chunk update (large decay spans, unclamped tail).  S tile (db, jb) element i
-// is S[dim 32*(db>>1) + 8*g4 + 4*(db&1) + i][col v0 + label_col(jb, r16)].
-template <typename TIn, int DK, int DVS, bool WITH_OUT>
-__device__ void chunk_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int v0, int64_t tc, int nv,
-                                int g4, int r16, f32x4 (&S)[DK / 16][DVS / 16]) {
-    constexpr int NKS = DK / 32, NDB = DK / 16, NJB = DVS / 16;
+// ---------------------------------------------------------------------------------------
+// Token-by-token update of one wave's state columns (large decay spans, unclamped tail).
+// S tile db holds S[16*db + 4*g4 + i][c0 + r16].
+// ---------------------------------------------------------------------------------------
+template <typename TIn, typename TG, int DK, bool OUT>
+__device__ void chunk_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int c0, int64_t tc, int nv,
+                                int g4, int r16, f32x4 (&S)[DK / 16]) {
+    constexpr int NDB = DK / 16;
     for (int t = 0; t < nv; ++t) {
-        int64_t tt = tc + t;
-        bool unclamped = (a.flags & 1) && (tt == wk.len - 1);
-        float gq[NKS][8], kq[NKS][8], qq[NKS][8];
+        const int64_t tt = tc + t;
+        const bool unclamped = (a.flags & 1) && (tt == wk.len - 1);
+        float dcy[NDB][4], kk[NDB][4], qq[NDB][4];
 #pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            load8_dt(tok_ptr_dt(a.g, a.g_dt, wk, tt, h, 32 * ks + 8 * g4), a.g_dt, true, gq[ks]);
-            load8<TIn>(tok_ptr<TIn>(a.k, wk, tt, h, 32 * ks + 8 * g4), true, kq[ks]);
-            if (WITH_OUT) load8<TIn>(tok_ptr<TIn>(a.q, wk, tt, h, 32 * ks + 8 * g4), true, qq[ks]);
+        for (int db = 0; db < NDB; ++db) {
+            const int d = 16 * db + 4 * g4;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float gg = unclamped ? gq[ks][j] : fminf(gq[ks][j], 0.f);
-                gq[ks][j] = expf(gg);
+            for (int i = 0; i < 4; ++i) {
+                const float gg = (float)tok_row<TG>(a.g, wk, tt, h, d)[i];
+                dcy[db][i] = expf(unclamped ? gg : fminf(gg, 0.f));
+                kk[db][i] = (float)tok_row<TIn>(a.k, wk, tt, h, d)[i];
+                qq[db][i] = OUT ? (float)tok_row<TIn>(a.q, wk, tt, h, d)[i] : 0.f;
             }
         }
-        float vv[NJB];
-        const TIn* vrow = tok_ptr<TIn>(a.v, wk, tt, h, v0);
-#pragma unroll
-        for (int jb = 0; jb < NJB; ++jb) vv[jb] = (float)vrow[label_col(jb, r16)];
-        float part[NJB];
-#pragma unroll
-        for (int jb = 0; jb < NJB; ++jb) part[jb] = 0.f;
+        const float vv = (float)tok_row<TIn>(a.v, wk, tt, h, c0)[r16];
+        float part = 0.f;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int jb = 0; jb < NJB; ++jb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    int ks = db >> 1, j = 4 * (db & 1) + i;
-                    float s = gq[ks][j] * S[db][jb][i] + kq[ks][j] * vv[jb];
-                    S[db][jb][i] = s;
-                    if (WITH_OUT) part[jb] += qq[ks][j] * s;
-                }
-        if (WITH_OUT) {
-#pragma unroll
-            for (int jb = 0; jb < NJB; ++jb) {
-                float x = part[jb];
-                x += __shfl_xor(x, 16);
-                x += __shfl_xor(x, 32);
-                part[jb] = x;
+            for (int i = 0; i < 4; ++i) {
+                const float s = dcy[db][i] * S[db][i] + kk[db][i] * vv;
+                S[db][i] = s;
+                part += qq[db][i] * s;
             }
+        if (OUT) {
+            part += __shfl_xor(part, 16);
+            part += __shfl_xor(part, 32);
             if (g4 == 0) {
-                char* orow = reinterpret_cast<char*>(a.o) +
-                             (wk.b * a.o_sb + (wk.row0 + tt) * a.o_st + h * a.o_sh + v0) * dt_size(a.o_dt);
-#pragma unroll
-                for (int jb = 0; jb < NJB; ++jb) {
-                    int col = label_col(jb, r16);
-                    if (a.o_dt == DT_F32) reinterpret_cast<float*>(orow)[col] = part[jb];
-                    else if (a.o_dt == DT_BF16) reinterpret_cast<__bf16*>(orow)[col] = (__bf16)part[jb];
-                    else reinterpret_cast<_Float16*>(orow)[col] = (_Float16)part[jb];
-                }
+                const int64_t off = wk.b * a.o_sb + (wk.row0 + tt) * a.o_st + h * a.o_sh + c0 + r16;
+                char* op = reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt);
+                if (a.o_dt == DT_F32) *reinterpret_cast<float*>(op) = part;
+                else if (a.o_dt == DT_BF16) *reinterpret_cast<__bf16*>(op) = (__bf16)part;
+                else *reinterpret_cast<_Float16*>(op) = (_Float16)part;
             }
         }
     }
 }
 
-// One segment: walk its chunks from S (in registers), optionally writing outputs.
-template <typename TIn, int DK, int DVS, bool WITH_OUT>
-__device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, int v0,
-                             f32x4 (&S)[DK / 16][DVS / 16], float (&Gseg)[DK / 32][8]) {
-    constexpr int NKS = DK / 32, NDB = DK / 16, NJB = DVS / 16, NVC = DVS / 32;
-    constexpr int NX = Prec<TIn>::NX, NS = Prec<TIn>::NS;
-    const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
-    const bf16x8 perm0 = perm_frag(0, g4, r16), perm1 = perm_frag(1, g4, r16);
+// ---------------------------------------------------------------------------------------
+// One segment.  OUT = false: state only (K1).  OUT = true: outputs (K3).
+// ---------------------------------------------------------------------------------------
+template <typename TIn, typename TG, int DK, int DV, bool OUT>
+__device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16],
+                             float (&Gseg)[DK / (DV / 16)], char* smem) {
+    using L = Lay<TIn, DK, DV, OUT>;
+    using PR = Prec<TIn>;
+    constexpr int NW = L::NW, DPW = L::DPW, NDB = DK / 16, NKS = DK / 32, NS = PR::NS, NX = PR::NX;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const int d0 = wave * DPW;  // stage-1 key dims
+    const int c0 = wave * 16;   // stage-3 value columns
+
+    char* sQT = smem + L::OFF_QT;
+    char* sKT = smem + L::OFF_KT;
+    char* sKTT = smem + L::OFF_KTT;
+    char* sAT = smem + L::OFF_AT;
+    char* sVP = smem + L::OFF_VP + wave * PR::VPL * L::VPP;
+    float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
+    float* sEG = sEM + DK;
+    int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
+
+    ChunkIn<TIn, TG, DPW> cur, nxt;
+    int nv = (int)((wk.t_end - wk.t_begin) < CHUNK ? (wk.t_end - wk.t_begin) : CHUNK);
+    chunk_load<OUT>(cur, a, wk, h, wk.t_begin, nv, lane, d0, c0);
 
     for (int64_t tc = wk.t_begin; tc < wk.t_end; tc += CHUNK) {
-        const int nv = (int)((wk.t_end - tc) < CHUNK ? (wk.t_end - tc) : CHUNK);
+        const int64_t tn = tc + CHUNK;
+        const int nvn = (int)((wk.t_end - tn) < CHUNK ? (wk.t_end - tn) : CHUNK);
+        if (tn < wk.t_end) chunk_load<OUT>(nxt, a, wk, h, tn, nvn, lane, d0, c0);
+        const bool valid = lane < nv;
         const bool tail_unclamped = (a.flags & 1) && (tc + nv == wk.len);
-        float GC[NKS][8];
-        const bool fast = chunk_totals<NKS>(a, wk, h, tc, nv, g4, r16, lane, GC, tail_unclamped);
-        if (!fast) {
-            chunk_tokenwise<TIn, DK, DVS, WITH_OUT>(a, wk, h, v0, tc, nv, g4, r16, S);
-            // GC holds clamped totals; an unclamped tail token adds its positive part back.
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) {
-                float gx[8];
-                load8_dt(tok_ptr_dt(a.g, a.g_dt, wk, wk.len - 1, h, 32 * ks + 8 * g4), a.g_dt, tail_unclamped, gx);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) Gseg[ks][j] += GC[ks][j] + fmaxf(gx[j], 0.f);
-            }
-            continue;
-        }
 
-        // ---- V: row fragments -> transposed fragments (tokens along K) -------------------
-        // vf[p][jb][ks2]: lane holds V[token 32*ks2 + pi(g4, j)][col v0 + label_col(jb, r16)]
-        Split8<NX> vf[NJB][2];
+        // ---------------- stage 1: decay, factors, split operands -> LDS -----------------
+        float gx[DPW], kx[DPW], eq[DPW], GC[DPW];
+        row_float(cur.g, gx, valid);
+        row_float(cur.k, kx, valid);
+        bool bad = tail_unclamped;
+#pragma unroll
+        for (int d = 0; d < DPW; ++d) {
+            const float G = wave_inclusive_scan(fminf(gx[d], 0.f));
+            GC[d] = lane_value(G, 63);
+            bad |= !(GC[d] >= -SPAN_MAX);
+            eq[d] = fast_exp(G - 0.5f * GC[d]);  // exp(G - m)
+        }
+        if (tail_unclamped) {  // the unclamped tail token adds its positive part to the decay
+#pragma unroll
+            for (int d = 0; d < DPW; ++d) GC[d] += fmaxf(lane_value(gx[d], nv - 1), 0.f);
+        }
+#pragma unroll
+        for (int d = 0; d < DPW; ++d) Gseg[d] += GC[d];
+        if (lane == 0) {
+#pragma unroll
+            for (int d = 0; d < DPW; ++d) {
+                const float em = fast_exp(0.5f * GC[d]);
+                sEM[d0 + d] = em;
+                sEG[d0 + d] = em * em;
+            }
+            sFLAG[wave] = bad ? 1 : 0;
+        }
         {
-            f32x4 vt[NX][NJB][4];
+            float kt[DPW];
 #pragma unroll
-            for (int c = 0; c < NVC; ++c)
+            for (int d = 0; d < DPW; ++d) kt[d] = kx[d] * __builtin_amdgcn_rcpf(eq[d]);
+            if (OUT) lds_put_row<TIn, PR::DPL, DPW>(sKT, L::ROWP, lane * L::RS + d0, kt);
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb) {
-                    int t = 16 * mb + r16;
-                    float x[8];
-                    load8<TIn>(tok_ptr<TIn>(a.v, wk, tc + t, h, v0 + 32 * c + 8 * g4), t < nv, x);
-                    Split8<NX> xs = split8<NX>(x);
+            for (int d = 0; d < DPW; ++d) lds_put<TIn, PR::DPL>(sKTT, L::KTTP, (d0 + d) * L::TS + lane, kt[d]);
+        }
+        if (OUT) {
+            float qx[DPW];
+            row_float(cur.q, qx, valid);
 #pragma unroll
-                    for (int pp = 0; pp < NX; ++pp) {
-                        vt[pp][2 * c][mb] = mfma(xs.p[pp], perm0, zero4());
-                        vt[pp][2 * c + 1][mb] = mfma(xs.p[pp], perm1, zero4());
+            for (int d = 0; d < DPW; ++d) qx[d] *= eq[d];
+            lds_put_row<TIn, PR::DPL, DPW>(sQT, L::ROWP, lane * L::RS + d0, qx);
+        }
+        {
+            float vx[16];
+            row_float(cur.v, vx, valid);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) lds_put<TIn, PR::VPL>(sVP, L::VPP, c * L::TS + lane, vx[c]);
+        }
+        __syncthreads();
+        bool fast = true;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
+
+        if (!fast) {
+            chunk_tokenwise<TIn, TG, DK, OUT>(a, wk, h, c0, tc, nv, g4, r16, S);
+        } else {
+            // ---------------- stage 2: causal tiles of A^T -> LDS ------------------------
+            if (OUT) {
+                for (int i = wave; i < 10; i += NW) {
+                    int sb, tb;
+                    tile_sb_tb(i, sb, tb);
+                    f32x4 acc = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        const Split8<NS> kf = lds_frag<TIn, NS>(sKT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
+                        const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                        acc = mfma_split<NS, NS, NS>(kf, qf, acc);
                     }
+                    if (sb == tb) {  // row = key 4*g4 + j, column = query r16
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[j] = (4 * g4 + j > r16) ? 0.f : acc[j];
+                    }
+                    const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+                    lds_put_row<TIn, PR::DPL, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
                 }
-#pragma unroll
-            for (int jb = 0; jb < NJB; ++jb)
-#pragma unroll
-                for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-                    for (int pp = 0; pp < NX; ++pp) vf[jb][k2].p[pp] = frag_exact(vt[pp][jb][2 * k2], vt[pp][jb][2 * k2 + 1]);
-        }
-
-        f32x4 At[4][4];  // At[sb][tb], used for sb <= tb
-        f32x4 Ot[NJB][4];
-        if (WITH_OUT) {
-#pragma unroll
-            for (int sb = 0; sb < 4; ++sb)
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) At[sb][tb] = zero4();
-#pragma unroll
-            for (int jb = 0; jb < NJB; ++jb)
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) Ot[jb][tb] = zero4();
-        }
-
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            float G[4][8], kx[4][8];
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                int t = 16 * mb + r16;
-                load8_dt(tok_ptr_dt(a.g, a.g_dt, wk, tc + t, h, 32 * ks + 8 * g4), a.g_dt, t < nv, G[mb]);
-                load8<TIn>(tok_ptr<TIn>(a.k, wk, tc + t, h, 32 * ks + 8 * g4), t < nv, kx[mb]);
-            }
-            chunk_cumsum(G, lane);
-            float m[8], em[8], eG[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                m[j] = 0.5f * GC[ks][j];
-                em[j] = fast_exp(m[j]);
-                eG[j] = em[j] * em[j];
-                Gseg[ks][j] += GC[ks][j];
-            }
-            // key side Kt = k * exp(m - G)
-            Split8<NS> kt[4];
-#pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-                float x[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = kx[mb][j] * fast_exp(m[j] - G[mb][j]);
-                kt[mb] = split8<NS>(x);
+                __syncthreads();
             }
 
-            if (WITH_OUT) {
-                Split8<NS> qt[4];
+            // ---------------- stage 3: outputs and state for columns [c0, c0+16) --------
+            Split8<NX> vf[2];
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb) {
-                    int t = 16 * mb + r16;
+            for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag<TIn, NX>(sVP, L::VPP, L::TS, r16, 32 * k2, g4);
+            if (OUT) {
+                f32x4 Ot[4];
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) Ot[tb] = zero4();
+                // (exp(m) S)^T Qt^T
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    const f32x4 e0 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 4 * g4);
+                    const f32x4 e1 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 16 + 4 * g4);
                     float x[8];
-                    load8<TIn>(tok_ptr<TIn>(a.q, wk, tc + t, h, 32 * ks + 8 * g4), t < nv, x);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) x[j] *= fast_exp(G[mb][j] - m[j]);
-                    qt[mb] = split8<NS>(x);
-                }
-                // A^T[sb][tb] += Kt[sb] Qt[tb]^T
-#pragma unroll
-                for (int sb = 0; sb < 4; ++sb)
-#pragma unroll
-                    for (int tb = sb; tb < 4; ++tb) At[sb][tb] = mfma_split<NS, NS, NS>(kt[sb], qt[tb], At[sb][tb]);
-                // O^T[jb][tb] += (exp(m) S)^T[jb] Qt[tb]^T over this k-step's dims
-#pragma unroll
-                for (int jb = 0; jb < NJB; ++jb) {
-                    float slo[4], shi[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        slo[i] = em[i];
-                        shi[i] = em[4 + i];
+                        x[i] = S[2 * ks][i] * e0[i];
+                        x[4 + i] = S[2 * ks + 1][i] * e1[i];
                     }
-                    Split8<NS> sf = frag_from_tiles<NS>(S[2 * ks][jb], S[2 * ks + 1][jb], slo, shi);
+                    const Split8<NS> sf = split8<NS>(x);
 #pragma unroll
-                    for (int tb = 0; tb < 4; ++tb) Ot[jb][tb] = mfma_split<NS, NS, NS>(sf, qt[tb], Ot[jb][tb]);
-                }
-            }
-
-            // Kt^T fragments for dim blocks 2ks, 2ks+1 (tokens along K), then the state rows.
-#pragma unroll
-            for (int dl = 0; dl < 2; ++dl) {
-                const bf16x8& pm = dl ? perm1 : perm0;
-                Split8<NS> ktT[2];
-#pragma unroll
-                for (int pp = 0; pp < NS; ++pp) {
-                    f32x4 tt[4];
-#pragma unroll
-                    for (int mb = 0; mb < 4; ++mb) tt[mb] = mfma(kt[mb].p[pp], pm, zero4());
-                    ktT[0].p[pp] = frag_exact(tt[0], tt[1]);
-                    ktT[1].p[pp] = frag_exact(tt[2], tt[3]);
-                }
-                const int db = 2 * ks + dl;
-#pragma unroll
-                for (int jb = 0; jb < NJB; ++jb) {
-                    f32x4 P = zero4();
-#pragma unroll
-                    for (int k2 = 0; k2 < 2; ++k2) P = mfma_split<NS, NX, NS>(ktT[k2], vf[jb][k2], P);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        int j = 4 * dl + i;
-                        S[db][jb][i] = eG[j] * S[db][jb][i] + em[j] * P[i];
+                    for (int tb = 0; tb < 4; ++tb) {
+                        const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                        Ot[tb] = mfma_split<NS, NS, NS>(sf, qf, Ot[tb]);
                     }
                 }
+                // V^T A^T: tiles (2*k2, tb) and (2*k2+1, tb) with key block <= query block
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+                    for (int k2 = 0; k2 < 2; ++k2) {
+                        if (2 * k2 > tb) continue;
+                        const int i0 = tile_index(2 * k2, tb);
+                        const bool has_hi = 2 * k2 + 1 <= tb;
+                        const int i1 = has_hi ? tile_index(2 * k2 + 1, tb) : i0;
+                        Split8<NS> af;
+                        if constexpr (PR::F32) {
+                            const float* p = reinterpret_cast<const float*>(sAT);
+                            const f32x4 lo = *reinterpret_cast<const f32x4*>(p + (i0 * 64 + lane) * 4);
+                            f32x4 hi = *reinterpret_cast<const f32x4*>(p + (i1 * 64 + lane) * 4);
+                            if (!has_hi) hi = zero4();
+                            float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                            af = split8<NS>(x);
+                        } else {
+#pragma unroll
+                            for (int pl = 0; pl < NS; ++pl) {
+                                const __bf16* p = reinterpret_cast<const __bf16*>(sAT + pl * L::ATP);
+                                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
+                                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
+                                const __bf16 z = (__bf16)0.f;
+                                af.p[pl] = has_hi ? bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}
+                                                  : bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
+                            }
+                        }
+                        Ot[tb] = mfma_split<NX, NS, NS>(vf[k2], af, Ot[tb]);
+                    }
+                }
+                // store: lane holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3]
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    const int t = 16 * tb + r16;
+                    if (t < nv) {
+                        const int64_t off = wk.b * a.o_sb + (wk.row0 + tc + t) * a.o_st + h * a.o_sh + c0 + 4 * g4;
+                        store4_dt(reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt), a.o_dt, Ot[tb][0], Ot[tb][1],
+                                  Ot[tb][2], Ot[tb][3]);
+                    }
+                }
             }
-        }
-
-        if (WITH_OUT) {
-            // causal mask on diagonal tiles: row s = 4*g4 + i (key), column t = r16 (query)
+            // S <- exp(G_C) S + exp(m) Kt^T V
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (4 * g4 + i > r16) At[tb][tb][i] = 0.f;
-            // O^T += V^T A^T
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
+            for (int db = 0; db < NDB; ++db) {
+                f32x4 P = zero4();
 #pragma unroll
                 for (int k2 = 0; k2 < 2; ++k2) {
-                    if (2 * k2 > tb) continue;
-                    float one[4] = {1.f, 1.f, 1.f, 1.f};
-                    f32x4 hiTile = (2 * k2 + 1 <= tb) ? At[2 * k2 + 1][tb] : zero4();
-                    Split8<NS> af = frag_from_tiles<NS>(At[2 * k2][tb], hiTile, one, one);
-#pragma unroll
-                    for (int jb = 0; jb < NJB; ++jb) Ot[jb][tb] = mfma_split<NX, NS, NS>(vf[jb][k2], af, Ot[jb][tb]);
+                    const Split8<NS> kf = lds_frag<TIn, NS>(sKTT, L::KTTP, L::TS, 16 * db + r16, 32 * k2, g4);
+                    P = mfma_split<NS, NX, NS>(kf, vf[k2], P);
                 }
-            }
-            // store: lane holds O[token 16*tb + r16][cols v0 + 32*c + 8*g4 + 0..7]
-            char* obase = reinterpret_cast<char*>(a.o);
+                const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
+                const f32x4 eg = *reinterpret_cast<const f32x4*>(sEG + 16 * db + 4 * g4);
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                int t = 16 * tb + r16;
-                if (t >= nv) continue;
-#pragma unroll
-                for (int c = 0; c < NVC; ++c) {
-                    float x[8];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        x[i] = Ot[2 * c][tb][i];
-                        x[4 + i] = Ot[2 * c + 1][tb][i];
-                    }
-                    int64_t off = wk.b * a.o_sb + (wk.row0 + tc + t) * a.o_st + h * a.o_sh + v0 + 32 * c + 8 * g4;
-                    store8_dt(obase + off * dt_size(a.o_dt), a.o_dt, x);
-                }
+                for (int i = 0; i < 4; ++i) S[db][i] = eg[i] * S[db][i] + em[i] * P[i];
             }
         }
+        __syncthreads();  // the next chunk rewrites LDS
+        cur = nxt;
+        nv = nvn;
     }
 }
 
-template <int DK, int DVS>
-__device__ __forceinline__ int64_t state_index(int db, int jb, int i, int g4, int r16, int v0, int Dv) {
-    int dim = 32 * (db >> 1) + 8 * g4 + 4 * (db & 1) + i;
-    int col = v0 + label_col(jb, r16);
-    return (int64_t)dim * Dv + col;
+// S tile db of wave w: element i is S[16*db + 4*g4 + i][16*w + r16].
+__device__ __forceinline__ int64_t state_off(int db, int i, int g4, int r16, int wave, int Dv) {
+    return (int64_t)(16 * db + 4 * g4 + i) * Dv + 16 * wave + r16;
 }
 
-// K1: local end state of each segment (from zero) and its summed log-decay.
-template <typename TIn, int DK, int DVS>
-__global__ __launch_bounds__(64) void gla_seg_state_kernel(PrefillParams a) {
-    const int64_t w = blockIdx.x;
-    const int64_t h = blockIdx.y;
-    const int v0 = blockIdx.z * DVS;
+template <typename TIn, typename TG, int DK, int DV>
+__global__ __launch_bounds__(DV * 4) void gla_seg_state_kernel(PrefillParams a) {
+    using L = Lay<TIn, DK, DV, false>;
+    __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
+    const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
-    f32x4 S[DK / 16][DVS / 16];
-    float Gseg[DK / 32][8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    f32x4 S[DK / 16];
+    float Gseg[L::DPW];
+#pragma unroll
+    for (int db = 0; db < DK / 16; ++db) S[db] = zero4();
+#pragma unroll
+    for (int d = 0; d < L::DPW; ++d) Gseg[d] = 0.f;
+    segment_walk<TIn, TG, DK, DV, false>(a, wk, h, S, Gseg, smem);
+    float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
 #pragma unroll
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
-        for (int jb = 0; jb < DVS / 16; ++jb) S[db][jb] = zero4();
+        for (int i = 0; i < 4; ++i) st[state_off(db, i, g4, r16, wave, DV)] = S[db][i];
+    if (lane == 0) {
+        float* gs = a.ws_gamma + (w * a.H + h) * (int64_t)DK + wave * L::DPW;
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) Gseg[ks][j] = 0.f;
-    segment_walk<TIn, DK, DVS, false>(a, wk, h, v0, S, Gseg);
-    float* st = a.ws_state + (w * a.H + h) * (int64_t)a.Dk * a.Dv;
-#pragma unroll
-    for (int db = 0; db < DK / 16; ++db)
-#pragma unroll
-        for (int jb = 0; jb < DVS / 16; ++jb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) st[state_index<DK, DVS>(db, jb, i, g4, r16, v0, a.Dv)] = S[db][jb][i];
-    if (blockIdx.z == 0 && r16 == 0) {
-        float* gs = a.ws_gamma + (w * a.H + h) * (int64_t)a.Dk;
-#pragma unroll
-        for (int ks = 0; ks < DK / 32; ++ks)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) gs[32 * ks + 8 * g4 + j] = Gseg[ks][j];
+        for (int d = 0; d < L::DPW; ++d) gs[d] = Gseg[d];
     }
 }
 
-// K3: outputs of each segment from its carried-in state (ws_state after the scan).
-template <typename TIn, int DK, int DVS>
-__global__ __launch_bounds__(64) void gla_seg_output_kernel(PrefillParams a) {
-    const int64_t w = blockIdx.x;
-    const int64_t h = blockIdx.y;
-    const int v0 = blockIdx.z * DVS;
+template <typename TIn, typename TG, int DK, int DV>
+__global__ __launch_bounds__(DV * 4) void gla_seg_output_kernel(PrefillParams a) {
+    using L = Lay<TIn, DK, DV, true>;
+    __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
+    const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
-    f32x4 S[DK / 16][DVS / 16];
-    float Gseg[DK / 32][8];
-    const float* st = a.ws_state + (w * a.H + h) * (int64_t)a.Dk * a.Dv;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    f32x4 S[DK / 16];
+    float Gseg[L::DPW];
+    const float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
 #pragma unroll
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
-        for (int jb = 0; jb < DVS / 16; ++jb)
+        for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, DV)];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) S[db][jb][i] = st[state_index<DK, DVS>(db, jb, i, g4, r16, v0, a.Dv)];
-#pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) Gseg[ks][j] = 0.f;
-    segment_walk<TIn, DK, DVS, true>(a, wk, h, v0, S, Gseg);
+    for (int d = 0; d < L::DPW; ++d) Gseg[d] = 0.f;
+    segment_walk<TIn, TG, DK, DV, true>(a, wk, h, S, Gseg, smem);
 }
 
 // K0 (varlen): segment offsets from cu_seqlens, one thread block.
 __global__ __launch_bounds__(256) void gla_varlen_plan_kernel(const int32_t* cu, int64_t n_seqs, int P,
                                                                int32_t* seg_off) {
-    // serial prefix over sequences in chunks of 256 (n_seqs is small: a batch of requests)
     __shared__ int32_t part[256];
     int32_t base = 0;
     if (threadIdx.x == 0) seg_off[0] = 0;
     for (int64_t s0 = 0; s0 < n_seqs; s0 += 256) {
-        int64_t s = s0 + threadIdx.x;
+        const int64_t s = s0 + threadIdx.x;
         int32_t n = 0;
         if (s < n_seqs) {
             int64_t len = (int64_t)cu[s + 1] - (int64_t)cu[s];
-            int64_t chunks = (len + CHUNK - 1) / CHUNK;
+            if (len < 0) len = 0;
+            const int64_t chunks = (len + CHUNK - 1) / CHUNK;
             n = (int32_t)((chunks + P - 1) / P);
         }
         part[threadIdx.x] = n;
         __syncthreads();
         for (int off = 1; off < 256; off <<= 1) {
-            int32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+            const int32_t add = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
             __syncthreads();
             part[threadIdx.x] += add;
             __syncthreads();
@@ -524,43 +599,50 @@ __global__ __launch_bounds__(256) void gla_varlen_plan_kernel(const int32_t* cu,
 // ---------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------
-int prefill_dv_slice(int Dk, int Dv) {
-    if (Dk == 64 && Dv % 64 == 0) return 64;
-    return 32;
+bool prefill_shape_supported(int Dk, int Dv) {
+    return (Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128) ||
+           (Dk == 64 && Dv == 128) || (Dk == 128 && Dv == 64);
 }
 
-template <typename TIn>
-static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, int dvs, bool with_out, hipStream_t stream) {
-    dim3 grid((unsigned)n_work, (unsigned)a.H, (unsigned)(a.Dv / dvs));
-    dim3 block(64);
-#define TRIUNE_SEG_CASE(DK_, DVS_)                                                                      \
-    if (a.Dk == DK_ && dvs == DVS_) {                                                                   \
-        if (with_out) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, DK_, DVS_>), grid, block, 0, stream, a); \
-        else hipLaunchKernelGGL((gla_seg_state_kernel<TIn, DK_, DVS_>), grid, block, 0, stream, a);          \
+template <typename TIn, typename TG>
+static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
+    const dim3 grid((unsigned)n_work, (unsigned)a.H);
+    const dim3 block((unsigned)(a.Dv * 4));
+#define TRIUNE_SEG_CASE(DK_, DV_)                                                                       \
+    if (a.Dk == DK_ && a.Dv == DV_) {                                                                   \
+        if (with_out) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_>), grid, block, 0, stream, a); \
+        else hipLaunchKernelGGL((gla_seg_state_kernel<TIn, TG, DK_, DV_>), grid, block, 0, stream, a);          \
         return hipGetLastError();                                                                       \
     }
     TRIUNE_SEG_CASE(64, 64)
-    TRIUNE_SEG_CASE(64, 32)
-    TRIUNE_SEG_CASE(128, 32)
+    TRIUNE_SEG_CASE(128, 128)
     TRIUNE_SEG_CASE(32, 32)
+    TRIUNE_SEG_CASE(64, 128)
+    TRIUNE_SEG_CASE(128, 64)
 #undef TRIUNE_SEG_CASE
     return hipErrorInvalidValue;
 }
 
-static hipError_t launch_seg(const PrefillParams& a, int64_t n_work, int dvs, int io_dt, bool with_out,
-                             hipStream_t stream) {
-    if (io_dt == DT_BF16) return launch_seg_t<__bf16>(a, n_work, dvs, with_out, stream);
-    if (io_dt == DT_F16) return launch_seg_t<_Float16>(a, n_work, dvs, with_out, stream);
-    if (io_dt == DT_F32) return launch_seg_t<float>(a, n_work, dvs, with_out, stream);
+static hipError_t launch_seg(const PrefillParams& a, int64_t n_work, int io_dt, bool with_out, hipStream_t stream) {
+    const bool g32 = a.g_dt == DT_F32;
+    if (io_dt == DT_BF16) {
+        if (g32) return launch_seg_t<__bf16, float>(a, n_work, with_out, stream);
+        if (a.g_dt == DT_BF16) return launch_seg_t<__bf16, __bf16>(a, n_work, with_out, stream);
+    } else if (io_dt == DT_F16) {
+        if (g32) return launch_seg_t<_Float16, float>(a, n_work, with_out, stream);
+        if (a.g_dt == DT_F16) return launch_seg_t<_Float16, _Float16>(a, n_work, with_out, stream);
+    } else if (io_dt == DT_F32 && g32) {
+        return launch_seg_t<float, float>(a, n_work, with_out, stream);
+    }
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int dvs, int io_dt, hipStream_t stream) {
-    return launch_seg(a, n_work, dvs, io_dt, false, stream);
+hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream) {
+    return launch_seg(a, n_work, io_dt, false, stream);
 }
 
-hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int dvs, int io_dt, hipStream_t stream) {
-    return launch_seg(a, n_work, dvs, io_dt, true, stream);
+hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream) {
+    return launch_seg(a, n_work, io_dt, true, stream);
 }
 
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream) {

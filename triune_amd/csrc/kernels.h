@@ -80,10 +80,10 @@ struct GdnParams {
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);
 hipError_t launch_gla_decode(const DecodeParams& a, int Dk, int Dv, hipStream_t stream);
 hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t stream);
-// Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).  dvs = Dv slice.
-hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int dvs, int io_dt, hipStream_t stream);
-hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int dvs, int io_dt, hipStream_t stream);
+// Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).
+hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
+hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream);
-int prefill_dv_slice(int Dk, int Dv);
+bool prefill_shape_supported(int Dk, int Dv);
 
 }  // namespace triune

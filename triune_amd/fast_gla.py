@@ -32,8 +32,8 @@ __all__ = [
     "TriuneHipError",
 ]
 
-_PREFILL_DK = (32, 64, 128)
-_DECODE_PAIRS = {(32, 32), (64, 64), (128, 128), (64, 128), (128, 64)}
+_DIMS = (32, 64, 128)
+_PAIRS = ((32, 32), (64, 64), (64, 128), (128, 64), (128, 128))  # (Dk, Dv) the kernels support
 
 
 def _on_device(*ts):
@@ -43,16 +43,21 @@ def _on_device(*ts):
 
 
 def _round_dk(d: int) -> int:
-    for c in _PREFILL_DK:
+    for c in _DIMS:
         if d <= c:
             return c
     raise ValueError(f"key head dim {d} > 128 is not supported")
 
 
-def _round32(d: int) -> int:
-    if d > 512:
-        raise ValueError(f"value head dim {d} > 512 is not supported")
-    return (d + 31) // 32 * 32
+def _pair(dk: int, dv: int) -> tuple[int, int]:
+    """Smallest supported (Dk, Dv) >= (dk, dv); inputs are zero-padded up to it."""
+    best = None
+    for a, b in _PAIRS:
+        if a >= dk and b >= dv and (best is None or a * b < best[0] * best[1]):
+            best = (a, b)
+    if best is None:
+        raise ValueError(f"head dims ({dk}, {dv}) exceed the supported (128, 128)")
+    return best
 
 
 def _vec_layout(x: torch.Tensor) -> torch.Tensor:
@@ -92,9 +97,26 @@ def _tok3(x: torch.Tensor):
 # ---------------------------------------------------------------------------------------
 
 
+def _gate(g, q):
+    return g if g.dtype in (q.dtype, torch.float32) else g.float()
+
+
 def _prefill(q, k, v, g, initial_state, out, flags, save_final=True, out_dtype=None):
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
+    if Dv0 > 128:  # value columns evolve independently: run 128-wide column slices
+        outs, states = [], []
+        for c in range(0, Dv0, 128):
+            s0 = None if initial_state is None else initial_state[..., c:c + 128]
+            o_c, s_c = _prefill(q, k, v[..., c:c + 128], g, s0, None, flags, save_final,
+                                out.dtype if out is not None else (out_dtype or v.dtype))
+            outs.append(o_c)
+            states.append(s_c)
+        o = torch.cat(outs, dim=-1)
+        if out is not None:
+            out.copy_(o)
+            o = out
+        return o, (torch.cat(states, dim=-1) if save_final else None)
     if T == 0 or B == 0:  # nothing to scan: the final state is the initial state
         o = out if out is not None else torch.empty(B, T, H, Dv0, device=q.device, dtype=out_dtype or v.dtype)
         if not save_final:
@@ -102,8 +124,8 @@ def _prefill(q, k, v, g, initial_state, out, flags, save_final=True, out_dtype=N
         if initial_state is None:
             return o, torch.zeros(B, H, Dk0, Dv0, device=q.device, dtype=torch.float32)
         return o, initial_state.to(torch.float32).clone()
-    Dk, Dv = _round_dk(Dk0), _round32(Dv0)
-    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
+    Dk, Dv = _pair(Dk0, Dv0)
+    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, _gate(g, q)))
     vp = _vec_layout(_pad_last(v, Dv))
     odt = out.dtype if out is not None else (out_dtype or v.dtype)
     if out is not None and out.shape[-1] == Dv and out.stride(-1) == 1 and _vec_layout(out) is out:
@@ -148,11 +170,7 @@ def gla_decode_step(q, k, v, g, state, out=None, *, inplace=False, slots=None, o
         q, k, v, g = q[:, 0], k[:, 0], v[:, 0], g[:, 0]
     B, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
-    Dk, Dv = _round_dk(Dk0), _round32(Dv0)
-    if (Dk, Dv) not in _DECODE_PAIRS:
-        Dk = Dv = max(Dk, Dv) if max(Dk, Dv) <= 128 else None
-        if Dk is None:
-            raise ValueError(f"unsupported decode head dims ({Dk0}, {Dv0})")
+    Dk, Dv = _pair(Dk0, Dv0)
     padded = (Dk, Dv) != (Dk0, Dv0)
     qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
     vp = _vec_layout(_pad_last(v, Dv))
@@ -236,10 +254,10 @@ def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None):
         q, k, v, g = q[0], k[0], v[0], g[0]
     N, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
-    Dk, Dv = _round_dk(Dk0), _round32(Dv0)
+    Dk, Dv = _pair(Dk0, Dv0)
     cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     n = cu.numel() - 1
-    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
+    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, _gate(g, q)))
     vp = _vec_layout(_pad_last(v, Dv))
     odt = out.dtype if out is not None else v.dtype
     o = torch.empty(N, H, Dv, device=q.device, dtype=odt)
