@@ -118,24 +118,23 @@ def bench_decode(steps_total, dev, n_bufs=12):
     }
 
 
-def cpu_baseline(budget_s=20.0):
-    """The reference's PyTorch CPU scan, restated (oracle/ref_port.py), on one batch row of the
-    config-1 workload (B=1, H=6, T=16384, D=64, inputs widened to fp32), all host cores."""
+def cpu_baseline(budget_s=12.0):
+    """The reference's PyTorch CPU scan, restated (oracle/ref_port.py), on the config-1 workload
+    itself (B=4, H=6, T=16384, D=64; bf16 inputs widened to fp32, as the CPU path computes in
+    the input dtype), repeated for about budget_s seconds on all host cores."""
     from oracle.ref_port import fast_chunk_gla_cpu
     from triune_amd.workloads import config1
 
     torch.set_num_threads(os.cpu_count() or 1)
-    q, k, v, g, s0 = config1(T=16384, B=1, H=6, D=64)
+    q, k, v, g, s0 = config1(T=16384, B=4, H=6, D=64)
     q, k, v, g = (x.float() for x in (q, k, v, g))
     fast_chunk_gla_cpu(q[:, :1024], k[:, :1024], v[:, :1024], g[:, :1024], s0)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
+    while len(times) < 3 or time.perf_counter() < t_end:
         t0 = time.perf_counter()
         fast_chunk_gla_cpu(q, k, v, g, s0)
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end and len(times) >= 1:
-            break
     times.sort()
     med = times[len(times) // 2]
     cpu_model = ""
@@ -148,13 +147,25 @@ def cpu_baseline(budget_s=20.0):
     except OSError:
         pass
     return {
-        "value": 16384 / med,
+        "value": 4 * 16384 / med,
         "unit": "tok/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"config-1 batch row 0 (B=1, H=6, T=16384, D=64, fp32 math), median of {len(times)} runs, "
-        f"{med:.2f} s each; os.cpu_count()={os.cpu_count()}; cpu={cpu_model or platform.processor()}",
+        "sample": f"full config-1 pass (B=4, H=6, T=16384, D=64, fp32 math), median of {len(times)} runs, "
+        f"{med:.3f} s each; os.cpu_count()={os.cpu_count()}; cpu={cpu_model or platform.processor()}",
     }
+
+
+def _traffic_from_profiles():
+    """HBM bytes per prefill pass measured with rocprofv3 FETCH_SIZE / WRITE_SIZE counters and
+    scaled by the same counters on a copy of known size (profiles/prefill_traffic.json, written
+    from those runs); None when no measurement has been recorded."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "prefill_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("bytes_per_pass")
+    except (OSError, ValueError):
+        return None
 
 
 def main():
@@ -165,15 +176,32 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument(
+        "--copy-probe",
+        type=int,
+        default=0,
+        metavar="MIB",
+        help="only run a plain device copy of MIB MiB (steps times): the known-size reference used to "
+        "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
-            "bench.py measures one GPU: this build has no multi-GPU path (the (b, h) recurrences shard "
-            "with no exchange; see DESIGN.md). Run with --gpus 1.",
+            "bench.py measures one GPU: this build has no multi-GPU path (the (b, h) recurrences "
+            "shard across GPUs with no exchange). Run with --gpus 1.",
             file=sys.stderr,
         )
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.copy_probe:
+        n = args.copy_probe << 18  # fp32 elements
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_mib": args.copy_probe, "launches": args.steps}), flush=True)
+        return
     pre = bench_prefill(args.steps, args.warmup, dev)
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     cpu = None if args.no_cpu else cpu_baseline()
@@ -207,7 +235,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(pre["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": _traffic_from_profiles(),
             "kernel": "prefill pass = gla_seg_state + recurrent_scan + gla_seg_output (event-timed together)",
             "alg_bytes_per_pass": pre["alg_bytes"],
             "mfma_alg_tflops": round(pre["tflops"], 2),

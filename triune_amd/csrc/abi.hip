@@ -3,6 +3,10 @@
 #include "../../include/triune_hip.h"
 #include "kernels.h"
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 using namespace triune;
 
 namespace {
@@ -31,13 +35,42 @@ bool vec4_ok(const void* p, int dt, const int64_t* st, int n) {
     return true;
 }
 
-// Chunks per segment: enough (segment, head) workgroups to keep every CU busy (two resident
-// 64-column workgroups per CU), as few as possible to keep the carried-state traffic small.
-int seg_chunks(int64_t chunk_jobs, int Dv, int flags) {
+// Resident (segment, head) workgroups the device holds at once: CUs x output-kernel occupancy.
+// Queried once per device and cached (host-side runtime queries only; nothing is enqueued).
+int64_t resident_slots(int Dk, int Dv) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, int, int>, int64_t> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    std::lock_guard<std::mutex> lock(mu);
+    auto key = std::make_tuple(dev, Dk, Dv);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int ncu = 0;
+    if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+        ncu = 256;  // MI355X
+    const int64_t slots = (int64_t)ncu * gla_seg_output_blocks_per_cu(Dk, Dv);
+    cache[key] = slots;
+    return slots;
+}
+
+// Segments per sequence (dense): fill the resident workgroup slots once with near-equal
+// segments; never more segments than chunks.  flags bits 8..15 force a chunk count instead.
+int64_t dense_segments(int64_t B, int64_t H, int64_t nchunks, int Dk, int Dv, int flags) {
+    const int forced = (flags >> TRIUNE_FLAG_SEG_SHIFT) & 0xff;
+    if (forced > 0) return (nchunks + forced - 1) / forced;
+    int64_t nseg = resident_slots(Dk, Dv) / (B * H);
+    if (nseg < 1) nseg = 1;
+    if (nseg > nchunks) nseg = nchunks;
+    return nseg;
+}
+
+// Chunks per segment (varlen): about one resident round of workgroups.
+int varlen_seg_chunks(int64_t chunk_jobs, int Dk, int Dv, int flags) {
     const int forced = (flags >> TRIUNE_FLAG_SEG_SHIFT) & 0xff;
     if (forced > 0) return forced;
-    const int64_t target = Dv >= 128 ? 256 : 512;
-    int64_t p = (chunk_jobs + target - 1) / target;
+    const int64_t slots = resident_slots(Dk, Dv);
+    int64_t p = (chunk_jobs + slots - 1) / slots;
     if (p < 1) p = 1;
     if (p > 255) p = 255;
     return (int)p;
@@ -56,8 +89,8 @@ struct PrefillPlan {
 PrefillPlan plan_dense(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {
     PrefillPlan p{};
     const int64_t nchunks = (T + 63) / 64;
-    p.P = seg_chunks(B * H * nchunks, Dv, flags);
-    p.nseg = (nchunks + p.P - 1) / p.P;
+    p.nseg = dense_segments(B, H, nchunks, Dk, Dv, flags);
+    p.P = (int)((nchunks + p.nseg - 1) / p.nseg);
     p.n_work = B * p.nseg;
     p.off_segoff = 0;
     p.off_state = 0;
@@ -69,7 +102,7 @@ PrefillPlan plan_dense(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flag
 PrefillPlan plan_varlen(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk, int Dv, int flags) {
     PrefillPlan p{};
     const int64_t nchunks = (total_tokens + 63) / 64 + n_seqs;
-    p.P = seg_chunks(H * nchunks, Dv, flags);
+    p.P = varlen_seg_chunks(H * nchunks, Dk, Dv, flags);
     p.n_work = (total_tokens + 64 * (int64_t)p.P - 1) / (64 * (int64_t)p.P) + n_seqs;
     p.nseg = 0;
     p.off_segoff = 0;

@@ -69,8 +69,14 @@ __device__ __forceinline__ bool find_work(const PrefillParams& a, int64_t w, Wor
         wk.p = (int)(w - a.seg_off[lo]);
         wk.len = (int64_t)a.cu[lo + 1] - (int64_t)a.cu[lo];
     }
-    wk.t_begin = (int64_t)wk.p * a.P * CHUNK;
-    wk.t_end = wk.t_begin + (int64_t)a.P * CHUNK;
+    if (!a.varlen) {  // dense: nseg near-equal segments (chunk counts differ by at most one)
+        const int64_t nch = (wk.len + CHUNK - 1) / CHUNK;
+        wk.t_begin = (int64_t)wk.p * nch / a.nseg_dense * CHUNK;
+        wk.t_end = (int64_t)(wk.p + 1) * nch / a.nseg_dense * CHUNK;
+    } else {
+        wk.t_begin = (int64_t)wk.p * a.P * CHUNK;
+        wk.t_end = wk.t_begin + (int64_t)a.P * CHUNK;
+    }
     if (wk.t_end > wk.len) wk.t_end = wk.len;
     return wk.t_begin < wk.t_end;
 }
@@ -228,8 +234,10 @@ __device__ __forceinline__ void row_float(const Row<T, N>& r, float* x, bool val
             for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)hv[j];
         }
     }
+    if (!valid) {  // lanes past the end of a partial chunk (wave-uniform branch skipped when full)
 #pragma unroll
-    for (int j = 0; j < N; ++j) x[j] = valid ? x[j] : 0.f;
+        for (int j = 0; j < N; ++j) x[j] = 0.f;
+    }
 }
 
 template <typename T>
@@ -243,6 +251,26 @@ __device__ __forceinline__ float wave_inclusive_scan(float x) {
     x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));  // row_bcast:15
     x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));  // row_bcast:31
     return x;
+}
+
+// N independent inclusive scans, step by step so consecutive DPP operations are independent
+// (no wait states between them).
+template <int N>
+__device__ __forceinline__ void wave_inclusive_scan_n(float (&x)[N]) {
+#pragma unroll
+    for (int d = 0; d < N; ++d) x[d] += row_shr<1>(x[d]);
+#pragma unroll
+    for (int d = 0; d < N; ++d) x[d] += row_shr<2>(x[d]);
+#pragma unroll
+    for (int d = 0; d < N; ++d) x[d] += row_shr<4>(x[d]);
+#pragma unroll
+    for (int d = 0; d < N; ++d) x[d] += row_shr<8>(x[d]);
+#pragma unroll
+    for (int d = 0; d < N; ++d)
+        x[d] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[d]), 0x142, 0xa, 0xf, false));
+#pragma unroll
+    for (int d = 0; d < N; ++d)
+        x[d] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[d]), 0x143, 0xc, 0xf, false));
 }
 
 __device__ __forceinline__ float lane_value(float x, int lane) {
@@ -353,12 +381,17 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
         row_float(cur.g, gx, valid);
         row_float(cur.k, kx, valid);
         bool bad = tail_unclamped;
+        {
+            float G[DPW];
 #pragma unroll
-        for (int d = 0; d < DPW; ++d) {
-            const float G = wave_inclusive_scan(fminf(gx[d], 0.f));
-            GC[d] = lane_value(G, 63);
-            bad |= !(GC[d] >= -SPAN_MAX);
-            eq[d] = fast_exp(G - 0.5f * GC[d]);  // exp(G - m)
+            for (int d = 0; d < DPW; ++d) G[d] = fminf(gx[d], 0.f);
+            wave_inclusive_scan_n<DPW>(G);
+#pragma unroll
+            for (int d = 0; d < DPW; ++d) {
+                GC[d] = lane_value(G[d], 63);
+                bad |= !(GC[d] >= -SPAN_MAX);
+                eq[d] = fast_exp(G[d] - 0.5f * GC[d]);  // exp(G - m)
+            }
         }
         if (tail_unclamped) {  // the unclamped tail token adds its positive part to the decay
 #pragma unroll
@@ -635,6 +668,24 @@ static hipError_t launch_seg(const PrefillParams& a, int64_t n_work, int io_dt, 
         return launch_seg_t<float, float>(a, n_work, with_out, stream);
     }
     return hipErrorInvalidValue;
+}
+
+// Resident workgroups per CU of the output kernel for (Dk, Dv) (bf16 I/O instance; the other
+// dtypes use at least as much LDS, so this is an upper bound that only costs balance).
+int gla_seg_output_blocks_per_cu(int Dk, int Dv) {
+    int nb = 0;
+    hipError_t e = hipErrorInvalidValue;
+#define TRIUNE_OCC_CASE(DK_, DV_)                                                                             \
+    if (Dk == DK_ && Dv == DV_)                                                                               \
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                                     \
+            &nb, reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_>), DV_ * 4, 0);
+    TRIUNE_OCC_CASE(64, 64)
+    TRIUNE_OCC_CASE(128, 128)
+    TRIUNE_OCC_CASE(32, 32)
+    TRIUNE_OCC_CASE(64, 128)
+    TRIUNE_OCC_CASE(128, 64)
+#undef TRIUNE_OCC_CASE
+    return (e == hipSuccess && nb > 0) ? nb : 1;
 }
 
 hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream) {

@@ -20,8 +20,8 @@ struct PrefillParams {
     float* ws_gamma;       // [n_work, H, Dk]
     int64_t n_seqs, H, T;  // T: dense sequence length
     int Dk, Dv;
-    int P;                 // chunks per segment
-    int nseg_dense;        // segments per sequence (dense)
+    int P;                 // varlen: chunks per segment
+    int nseg_dense;        // dense: segments per sequence (near-equal chunk counts)
     int varlen;
     const int32_t* cu;     // varlen: [n_seqs + 1] token offsets (device)
     const int32_t* seg_off;// varlen: [n_seqs + 1] segment offsets (device, from plan kernel)
@@ -85,5 +85,6 @@ hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_d
 hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream);
 bool prefill_shape_supported(int Dk, int Dv);
+int gla_seg_output_blocks_per_cu(int Dk, int Dv);
 
 }  // namespace triune
