@@ -113,7 +113,7 @@ struct Lay {
     static constexpr int OFF_FAC = OFF_VP + NW * P::VPL * VPP;
     static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
     static constexpr int BYTES = OFF_FLAG + 16 * 4;
-    static_assert(DPW == 8 || DPW == 16 || DPW == 32, "stage-1 dims per wave");
+    static_assert(DPW == 16 || DPW == 32, "stage-1 dims per wave");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -193,50 +193,49 @@ __device__ __forceinline__ void lds_put_row(char* base, int plane_bytes, int idx
     }
 }
 
-// ---- global input rows (lane = token) --------------------------------------------------
+// ---- global inputs -----------------------------------------------------------------------
+// N consecutive elements of T as 32-bit words (N * sizeof(T) is 4, 8, 16 or 32 bytes).
 template <typename T, int N>
-struct Row {
-    static constexpr int V = N * (int)sizeof(T) / 16;  // 16-byte vectors
-    uint4 u[V];
+struct Vec {
+    static constexpr int BYTES = N * (int)sizeof(T);
+    static constexpr int W = BYTES / 4;
+    uint32_t w[W];
 };
 
 template <typename T, int N>
-__device__ __forceinline__ void row_load(Row<T, N>& r, const T* p) {
+__device__ __forceinline__ void vec_load(Vec<T, N>& v, const T* p) {
+    if constexpr (Vec<T, N>::BYTES % 16 == 0) {
 #pragma unroll
-    for (int i = 0; i < Row<T, N>::V; ++i) r.u[i] = reinterpret_cast<const uint4*>(p)[i];
+        for (int i = 0; i < Vec<T, N>::BYTES / 16; ++i) {
+            const uint4 u = reinterpret_cast<const uint4*>(p)[i];
+            v.w[4 * i] = u.x; v.w[4 * i + 1] = u.y; v.w[4 * i + 2] = u.z; v.w[4 * i + 3] = u.w;
+        }
+    } else if constexpr (Vec<T, N>::BYTES == 8) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        v.w[0] = u.x; v.w[1] = u.y;
+    } else {
+        v.w[0] = *reinterpret_cast<const uint32_t*>(p);
+    }
 }
 
 template <typename T, int N>
-__device__ __forceinline__ void row_float(const Row<T, N>& r, float* x, bool valid) {
+__device__ __forceinline__ void vec_float(const Vec<T, N>& v, float* x) {
     if constexpr (std::is_same<T, float>::value) {
 #pragma unroll
-        for (int i = 0; i < Row<T, N>::V; ++i) {
-            x[4 * i] = __uint_as_float(r.u[i].x);
-            x[4 * i + 1] = __uint_as_float(r.u[i].y);
-            x[4 * i + 2] = __uint_as_float(r.u[i].z);
-            x[4 * i + 3] = __uint_as_float(r.u[i].w);
-        }
+        for (int i = 0; i < N; ++i) x[i] = __uint_as_float(v.w[i]);
     } else if constexpr (std::is_same<T, __bf16>::value) {
 #pragma unroll
-        for (int i = 0; i < Row<T, N>::V; ++i) {
-            const uint32_t w[4] = {r.u[i].x, r.u[i].y, r.u[i].z, r.u[i].w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                x[8 * i + 2 * j] = __uint_as_float(w[j] << 16);
-                x[8 * i + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-            }
+        for (int i = 0; i < N / 2; ++i) {
+            x[2 * i] = __uint_as_float(v.w[i] << 16);
+            x[2 * i + 1] = __uint_as_float(v.w[i] & 0xffff0000u);
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < Row<T, N>::V; ++i) {
-            const f16x8 hv = *reinterpret_cast<const f16x8*>(&r.u[i]);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[8 * i + j] = (float)hv[j];
+        for (int i = 0; i < N / 2; ++i) {
+            const uint32_t u = v.w[i];
+            x[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu));
+            x[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
         }
-    }
-    if (!valid) {  // lanes past the end of a partial chunk (wave-uniform branch skipped when full)
-#pragma unroll
-        for (int j = 0; j < N; ++j) x[j] = 0.f;
     }
 }
 
@@ -245,55 +244,83 @@ __device__ __forceinline__ const T* tok_row(const TokTensor& x, const Work& wk, 
     return reinterpret_cast<const T*>(x.p) + wk.b * x.sb + (wk.row0 + t) * x.st + h * x.sh + d;
 }
 
-// Inclusive prefix sum over the 64 lanes of a wave (rows of 16 lanes, then across rows).
-__device__ __forceinline__ float wave_inclusive_scan(float x) {
-    x = row_inclusive_scan(x);
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xa, 0xf, false));  // row_bcast:15
-    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xc, 0xf, false));  // row_bcast:31
-    return x;
-}
-
-// N independent inclusive scans, step by step so consecutive DPP operations are independent
-// (no wait states between them).
-template <int N>
-__device__ __forceinline__ void wave_inclusive_scan_n(float (&x)[N]) {
-#pragma unroll
-    for (int d = 0; d < N; ++d) x[d] += row_shr<1>(x[d]);
-#pragma unroll
-    for (int d = 0; d < N; ++d) x[d] += row_shr<2>(x[d]);
-#pragma unroll
-    for (int d = 0; d < N; ++d) x[d] += row_shr<4>(x[d]);
-#pragma unroll
-    for (int d = 0; d < N; ++d) x[d] += row_shr<8>(x[d]);
-#pragma unroll
-    for (int d = 0; d < N; ++d)
-        x[d] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[d]), 0x142, 0xa, 0xf, false));
-#pragma unroll
-    for (int d = 0; d < N; ++d)
-        x[d] += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x[d]), 0x143, 0xc, 0xf, false));
-}
-
 __device__ __forceinline__ float lane_value(float x, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
-// ---- the chunk inputs a wave loads (lane = token) -------------------------------------
-template <typename TIn, typename TG, int DPW>
+// Stage-1 lane mapping: lane = 16*row + tg holds tokens 4*tg + j (j < 4) of key dims
+// d0 + DL*row + i (i < DL, DL = DPW/4) and value columns c0 + 4*row + c (c < 4).  Rows are DPP
+// rows, so a scan over tokens is a 4-step serial sum plus a 16-lane DPP scan.
+template <typename TIn, typename TG, int DL>
 struct ChunkIn {
-    Row<TIn, DPW> q;
-    Row<TIn, DPW> k;
-    Row<TG, DPW> g;
-    Row<TIn, 16> v;
+    Vec<TIn, DL> q[4], k[4];
+    Vec<TG, DL> g[4];
+    Vec<TIn, 4> v[4];
 };
 
-template <bool OUT, typename TIn, typename TG, int DPW>
-__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DPW>& c, const PrefillParams& a, const Work& wk, int64_t h,
-                                           int64_t tc, int nv, int lane, int d0, int c0) {
-    const int64_t t = tc + (lane < nv ? lane : nv - 1);  // every lane reads a row inside the chunk
-    if (OUT) row_load(c.q, tok_row<TIn>(a.q, wk, t, h, d0));
-    row_load(c.k, tok_row<TIn>(a.k, wk, t, h, d0));
-    row_load(c.g, tok_row<TG>(a.g, wk, t, h, d0));
-    row_load(c.v, tok_row<TIn>(a.v, wk, t, h, c0));
+template <bool OUT, typename TIn, typename TG, int DL>
+__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const PrefillParams& a, const Work& wk, int64_t h,
+                                           int64_t tc, int nv, int tg, int dcol, int vcol) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int tl = 4 * tg + j;
+        const int64_t t = tc + (tl < nv ? tl : nv - 1);  // every lane reads a row inside the chunk
+        if (OUT) vec_load(c.q[j], tok_row<TIn>(a.q, wk, t, h, dcol));
+        vec_load(c.k[j], tok_row<TIn>(a.k, wk, t, h, dcol));
+        vec_load(c.g[j], tok_row<TG>(a.g, wk, t, h, dcol));
+        vec_load(c.v[j], tok_row<TIn>(a.v, wk, t, h, vcol));
+    }
+}
+
+// x[j][i] = element i of token j, zeroed for tokens at or past nv (partial chunks only).
+template <typename T, int N>
+__device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[4][N], int tg, int nv) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vec_float(v[j], x[j]);
+    if (nv < CHUNK) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = 4 * tg + j < nv;
+#pragma unroll
+            for (int i = 0; i < N; ++i) x[j][i] = ok ? x[j][i] : 0.f;
+        }
+    }
+}
+
+// In place: G[j][i] <- inclusive sum over tokens 0..4*tg+j of the chunk (per key dim i);
+// returns the chunk totals in GC[i] (identical across the 16 lanes of a row).
+template <int DL>
+__device__ __forceinline__ void chunk_cumsum(float (&G)[4][DL], float (&GC)[DL], int lane) {
+    float T[DL], I[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        G[1][i] += G[0][i];
+        G[2][i] += G[1][i];
+        G[3][i] += G[2][i];
+        T[i] = G[3][i];
+        I[i] = T[i];
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) I[i] += row_shr<1>(I[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) I[i] += row_shr<2>(I[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) I[i] += row_shr<4>(I[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) I[i] += row_shr<8>(I[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float E = I[i] - T[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) G[j][i] += E;
+        GC[i] = lane_bcast(I[i], (lane & 48) | 15);
+    }
+}
+
+// Store 4 consecutive tokens (one lane's) of one row of a [row][token] plane set.
+template <typename TIn, int NP>
+__device__ __forceinline__ void lds_put_tok4(char* base, int plane_bytes, int idx, const float (&x)[4]) {
+    lds_put_row<TIn, NP, 4>(base, plane_bytes, idx, x);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -343,91 +370,113 @@ __device__ void chunk_tokenwise(const PrefillParams& a, const Work& wk, int64_t 
     }
 }
 
-// ---------------------------------------------------------------------------------------
-// One segment.  OUT = false: state only (K1).  OUT = true: outputs (K3).
-// ---------------------------------------------------------------------------------------
-template <typename TIn, typename TG, int DK, int DV, bool OUT>
-__device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16],
-                             float (&Gseg)[DK / (DV / 16)], char* smem) {
-    using L = Lay<TIn, DK, DV, OUT>;
+template <typename TIn, typename TG, int DK, int DV>
+struct OutStep {
+    using L = Lay<TIn, DK, DV, true>;
     using PR = Prec<TIn>;
-    constexpr int NW = L::NW, DPW = L::DPW, NDB = DK / 16, NKS = DK / 32, NS = PR::NS, NX = PR::NX;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
-    const int d0 = wave * DPW;  // stage-1 key dims
-    const int c0 = wave * 16;   // stage-3 value columns
+    static constexpr int NW = L::NW, DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NKS = DK / 32;
+    static constexpr int NS = PR::NS, NX = PR::NX;
 
-    char* sQT = smem + L::OFF_QT;
-    char* sKT = smem + L::OFF_KT;
-    char* sKTT = smem + L::OFF_KTT;
-    char* sAT = smem + L::OFF_AT;
-    char* sVP = smem + L::OFF_VP + wave * PR::VPL * L::VPP;
-    float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
-    float* sEG = sEM + DK;
-    int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
-
-    ChunkIn<TIn, TG, DPW> cur, nxt;
-    int nv = (int)((wk.t_end - wk.t_begin) < CHUNK ? (wk.t_end - wk.t_begin) : CHUNK);
-    chunk_load<OUT>(cur, a, wk, h, wk.t_begin, nv, lane, d0, c0);
-
-    for (int64_t tc = wk.t_begin; tc < wk.t_end; tc += CHUNK) {
-        const int64_t tn = tc + CHUNK;
-        const int nvn = (int)((wk.t_end - tn) < CHUNK ? (wk.t_end - tn) : CHUNK);
-        if (tn < wk.t_end) chunk_load<OUT>(nxt, a, wk, h, tn, nvn, lane, d0, c0);
-        const bool valid = lane < nv;
+    // One chunk: stage 1 (factors, split operands -> LDS), stage 2 (A^T tiles), stage 3 (O, S).
+    __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+        const int tg = lane & 15, row = lane >> 4;
+        const int d0 = wave * DPW, c0 = wave * 16;
+        const int dl0 = d0 + DL * row;  // first key dim of this lane in stage 1
+        char* sQT = smem + L::OFF_QT;
+        char* sKT = smem + L::OFF_KT;
+        char* sKTT = smem + L::OFF_KTT;
+        char* sAT = smem + L::OFF_AT;
+        char* sVP = smem + L::OFF_VP + wave * PR::VPL * L::VPP;
+        float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
+        float* sEG = sEM + DK;
+        int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
         const bool tail_unclamped = (a.flags & 1) && (tc + nv == wk.len);
 
-        // ---------------- stage 1: decay, factors, split operands -> LDS -----------------
-        float gx[DPW], kx[DPW], eq[DPW], GC[DPW];
-        row_float(cur.g, gx, valid);
-        row_float(cur.k, kx, valid);
-        bool bad = tail_unclamped;
+        // ---------------- stage 1 -------------------------------------------------------
         {
-            float G[DPW];
+            float G[4][DL], GC[DL], x[4][DL];
+            chunk_float(cur.g, G, tg, nv);
 #pragma unroll
-            for (int d = 0; d < DPW; ++d) G[d] = fminf(gx[d], 0.f);
-            wave_inclusive_scan_n<DPW>(G);
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int d = 0; d < DPW; ++d) {
-                GC[d] = lane_value(G[d], 63);
-                bad |= !(GC[d] >= -SPAN_MAX);
-                eq[d] = fast_exp(G[d] - 0.5f * GC[d]);  // exp(G - m)
+                for (int i = 0; i < DL; ++i) G[j][i] = fminf(G[j][i], 0.f);
+            chunk_cumsum<DL>(G, GC, lane);
+            bool bad = tail_unclamped;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) bad |= !(GC[i] >= -SPAN_MAX);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < DL; ++i) G[j][i] = fast_exp(G[j][i] - 0.5f * GC[i]);  // exp(G - m)
+            if (tg == 0) {
+#pragma unroll
+                for (int i = 0; i < DL; ++i) {
+                    const float em = fast_exp(0.5f * GC[i]);
+                    sEM[dl0 + i] = em;
+                    sEG[dl0 + i] = em * em;
+                }
             }
-        }
-        if (tail_unclamped) {  // the unclamped tail token adds its positive part to the decay
+            const bool any_bad = __any(bad);
+            if (lane == 0) sFLAG[wave] = any_bad ? 1 : 0;
+            // Qt rows
+            chunk_float(cur.q, x, tg, nv);
 #pragma unroll
-            for (int d = 0; d < DPW; ++d) GC[d] += fmaxf(lane_value(gx[d], nv - 1), 0.f);
-        }
+            for (int j = 0; j < 4; ++j) {
 #pragma unroll
-        for (int d = 0; d < DPW; ++d) Gseg[d] += GC[d];
-        if (lane == 0) {
-#pragma unroll
-            for (int d = 0; d < DPW; ++d) {
-                const float em = fast_exp(0.5f * GC[d]);
-                sEM[d0 + d] = em;
-                sEG[d0 + d] = em * em;
+                for (int i = 0; i < DL; ++i) x[j][i] *= G[j][i];
+                lds_put_row<TIn, PR::DPL, DL>(sQT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
-            sFLAG[wave] = bad ? 1 : 0;
-        }
-        {
-            float kt[DPW];
+            // Kt rows and Kt^T (split once, both layouts)
+            chunk_float(cur.k, x, tg, nv);
 #pragma unroll
-            for (int d = 0; d < DPW; ++d) kt[d] = kx[d] * __builtin_amdgcn_rcpf(eq[d]);
-            if (OUT) lds_put_row<TIn, PR::DPL, DPW>(sKT, L::ROWP, lane * L::RS + d0, kt);
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int d = 0; d < DPW; ++d) lds_put<TIn, PR::DPL>(sKTT, L::KTTP, (d0 + d) * L::TS + lane, kt[d]);
-        }
-        if (OUT) {
-            float qx[DPW];
-            row_float(cur.q, qx, valid);
+                for (int i = 0; i < DL; ++i) x[j][i] *= __builtin_amdgcn_rcpf(G[j][i]);
+            if constexpr (PR::F32) {
 #pragma unroll
-            for (int d = 0; d < DPW; ++d) qx[d] *= eq[d];
-            lds_put_row<TIn, PR::DPL, DPW>(sQT, L::ROWP, lane * L::RS + d0, qx);
-        }
-        {
-            float vx[16];
-            row_float(cur.v, vx, valid);
+                for (int j = 0; j < 4; ++j) lds_put_row<TIn, 1, DL>(sKT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
 #pragma unroll
-            for (int c = 0; c < 16; ++c) lds_put<TIn, PR::VPL>(sVP, L::VPP, c * L::TS + lane, vx[c]);
+                for (int i = 0; i < DL; ++i)
+                    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(sKTT) + (dl0 + i) * L::TS + 4 * tg) =
+                        f32x4{x[0][i], x[1][i], x[2][i], x[3][i]};
+            } else {
+                __bf16 hi[4][DL], lo[4][DL];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int i = 0; i < DL; ++i) {
+                        hi[j][i] = (__bf16)x[j][i];
+                        lo[j][i] = (__bf16)(x[j][i] - (float)hi[j][i]);
+                    }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int c = 0; c < DL; c += 4) {
+                        const int idx = (4 * tg + j) * L::RS + dl0 + c;
+                        *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKT) + idx) =
+                            bf16x4{hi[j][c], hi[j][c + 1], hi[j][c + 2], hi[j][c + 3]};
+                        *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKT + L::ROWP) + idx) =
+                            bf16x4{lo[j][c], lo[j][c + 1], lo[j][c + 2], lo[j][c + 3]};
+                    }
+#pragma unroll
+                for (int i = 0; i < DL; ++i) {
+                    const int idx = (dl0 + i) * L::TS + 4 * tg;
+                    *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKTT) + idx) =
+                        bf16x4{hi[0][i], hi[1][i], hi[2][i], hi[3][i]};
+                    *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKTT + L::KTTP) + idx) =
+                        bf16x4{lo[0][i], lo[1][i], lo[2][i], lo[3][i]};
+                }
+            }
+            // V: columns c0 + 4*row + c, tokens 4*tg .. 4*tg+3 -> [column][token]
+            float vx[4][4];
+            chunk_float(cur.v, vx, tg, nv);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float col[4] = {vx[0][c], vx[1][c], vx[2][c], vx[3][c]};
+                lds_put_row<TIn, PR::VPL, 4>(sVP, L::VPP, (4 * row + c) * L::TS + 4 * tg, col);
+            }
         }
         __syncthreads();
         bool fast = true;
@@ -435,101 +484,93 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
         for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
 
         if (!fast) {
-            chunk_tokenwise<TIn, TG, DK, OUT>(a, wk, h, c0, tc, nv, g4, r16, S);
+            chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, c0, tc, nv, g4, r16, S);
         } else {
-            // ---------------- stage 2: causal tiles of A^T -> LDS ------------------------
-            if (OUT) {
-                for (int i = wave; i < 10; i += NW) {
-                    int sb, tb;
-                    tile_sb_tb(i, sb, tb);
-                    f32x4 acc = zero4();
+            // ---------------- stage 2: causal tiles of A^T -> LDS ----------------------------
+            for (int i = wave; i < 10; i += NW) {
+                int sb, tb;
+                tile_sb_tb(i, sb, tb);
+                f32x4 acc = zero4();
 #pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks) {
-                        const Split8<NS> kf = lds_frag<TIn, NS>(sKT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
-                        const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
-                        acc = mfma_split<NS, NS, NS>(kf, qf, acc);
-                    }
-                    if (sb == tb) {  // row = key 4*g4 + j, column = query r16
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) acc[j] = (4 * g4 + j > r16) ? 0.f : acc[j];
-                    }
-                    const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-                    lds_put_row<TIn, PR::DPL, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
+                for (int ks = 0; ks < NKS; ++ks) {
+                    const Split8<NS> kf = lds_frag<TIn, NS>(sKT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
+                    const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                    acc = mfma_split<NS, NS, NS>(kf, qf, acc);
                 }
-                __syncthreads();
+                if (sb == tb) {  // row = key 4*g4 + j, column = query r16
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[j] = (4 * g4 + j > r16) ? 0.f : acc[j];
+                }
+                const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+                lds_put_row<TIn, PR::DPL, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
             }
+            __syncthreads();
 
-            // ---------------- stage 3: outputs and state for columns [c0, c0+16) --------
+            // ---------------- stage 3: outputs and state for columns [c0, c0+16) ------------
             Split8<NX> vf[2];
 #pragma unroll
             for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag<TIn, NX>(sVP, L::VPP, L::TS, r16, 32 * k2, g4);
-            if (OUT) {
-                f32x4 Ot[4];
+            f32x4 Ot[4];
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) Ot[tb] = zero4();
-                // (exp(m) S)^T Qt^T
+            for (int tb = 0; tb < 4; ++tb) Ot[tb] = zero4();
 #pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    const f32x4 e0 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 4 * g4);
-                    const f32x4 e1 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 16 + 4 * g4);
-                    float x[8];
+            for (int ks = 0; ks < NKS; ++ks) {  // (exp(m) S)^T Qt^T
+                const f32x4 e0 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 4 * g4);
+                const f32x4 e1 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 16 + 4 * g4);
+                float x[8];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        x[i] = S[2 * ks][i] * e0[i];
-                        x[4 + i] = S[2 * ks + 1][i] * e1[i];
-                    }
-                    const Split8<NS> sf = split8<NS>(x);
-#pragma unroll
-                    for (int tb = 0; tb < 4; ++tb) {
-                        const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
-                        Ot[tb] = mfma_split<NS, NS, NS>(sf, qf, Ot[tb]);
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    x[i] = S[2 * ks][i] * e0[i];
+                    x[4 + i] = S[2 * ks + 1][i] * e1[i];
                 }
-                // V^T A^T: tiles (2*k2, tb) and (2*k2+1, tb) with key block <= query block
+                const Split8<NS> sf = split8<NS>(x);
 #pragma unroll
                 for (int tb = 0; tb < 4; ++tb) {
-#pragma unroll
-                    for (int k2 = 0; k2 < 2; ++k2) {
-                        if (2 * k2 > tb) continue;
-                        const int i0 = tile_index(2 * k2, tb);
-                        const bool has_hi = 2 * k2 + 1 <= tb;
-                        const int i1 = has_hi ? tile_index(2 * k2 + 1, tb) : i0;
-                        Split8<NS> af;
-                        if constexpr (PR::F32) {
-                            const float* p = reinterpret_cast<const float*>(sAT);
-                            const f32x4 lo = *reinterpret_cast<const f32x4*>(p + (i0 * 64 + lane) * 4);
-                            f32x4 hi = *reinterpret_cast<const f32x4*>(p + (i1 * 64 + lane) * 4);
-                            if (!has_hi) hi = zero4();
-                            float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                            af = split8<NS>(x);
-                        } else {
-#pragma unroll
-                            for (int pl = 0; pl < NS; ++pl) {
-                                const __bf16* p = reinterpret_cast<const __bf16*>(sAT + pl * L::ATP);
-                                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
-                                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
-                                const __bf16 z = (__bf16)0.f;
-                                af.p[pl] = has_hi ? bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}
-                                                  : bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
-                            }
-                        }
-                        Ot[tb] = mfma_split<NX, NS, NS>(vf[k2], af, Ot[tb]);
-                    }
-                }
-                // store: lane holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3]
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    const int t = 16 * tb + r16;
-                    if (t < nv) {
-                        const int64_t off = wk.b * a.o_sb + (wk.row0 + tc + t) * a.o_st + h * a.o_sh + c0 + 4 * g4;
-                        store4_dt(reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt), a.o_dt, Ot[tb][0], Ot[tb][1],
-                                  Ot[tb][2], Ot[tb][3]);
-                    }
+                    const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                    Ot[tb] = mfma_split<NS, NS, NS>(sf, qf, Ot[tb]);
                 }
             }
-            // S <- exp(G_C) S + exp(m) Kt^T V
 #pragma unroll
-            for (int db = 0; db < NDB; ++db) {
+            for (int tb = 0; tb < 4; ++tb) {  // V^T A^T over key blocks <= tb
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    if (2 * k2 > tb) continue;
+                    const int i0 = tile_index(2 * k2, tb);
+                    const bool has_hi = 2 * k2 + 1 <= tb;
+                    const int i1 = has_hi ? tile_index(2 * k2 + 1, tb) : i0;
+                    Split8<NS> af;
+                    if constexpr (PR::F32) {
+                        const float* p = reinterpret_cast<const float*>(sAT);
+                        const f32x4 lo = *reinterpret_cast<const f32x4*>(p + (i0 * 64 + lane) * 4);
+                        f32x4 hi = *reinterpret_cast<const f32x4*>(p + (i1 * 64 + lane) * 4);
+                        if (!has_hi) hi = zero4();
+                        float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        af = split8<NS>(x);
+                    } else {
+#pragma unroll
+                        for (int pl = 0; pl < NS; ++pl) {
+                            const __bf16* p = reinterpret_cast<const __bf16*>(sAT + pl * L::ATP);
+                            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
+                            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
+                            const __bf16 z = (__bf16)0.f;
+                            af.p[pl] = has_hi ? bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}
+                                              : bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
+                        }
+                    }
+                    Ot[tb] = mfma_split<NX, NS, NS>(vf[k2], af, Ot[tb]);
+                }
+            }
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {  // lane holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3]
+                const int t = 16 * tb + r16;
+                if (t < nv) {
+                    const int64_t off = wk.b * a.o_sb + (wk.row0 + tc + t) * a.o_st + h * a.o_sh + c0 + 4 * g4;
+                    store4_dt(reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt), a.o_dt, Ot[tb][0], Ot[tb][1],
+                              Ot[tb][2], Ot[tb][3]);
+                }
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {  // S <- exp(G_C) S + exp(m) Kt^T V
                 f32x4 P = zero4();
 #pragma unroll
                 for (int k2 = 0; k2 < 2; ++k2) {
@@ -543,8 +584,119 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
             }
         }
         __syncthreads();  // the next chunk rewrites LDS
-        cur = nxt;
-        nv = nvn;
+    }
+};
+
+// Outputs of one segment from its carried-in state S (K3).  Chunk inputs ping-pong between two
+// register sets: the next chunk is loaded while the current one is processed.
+template <typename TIn, typename TG, int DK, int DV>
+__device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
+    using St = OutStep<TIn, TG, DK, DV>;
+    constexpr int DL = St::DL;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane & 15, row = lane >> 4;
+    const int dcol = wave * St::DPW + DL * row, vcol = wave * 16 + 4 * row;
+    const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
+    auto chunk_nv = [&](int64_t c) {
+        const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
+        return (int)(r < CHUNK ? r : CHUNK);
+    };
+    ChunkIn<TIn, TG, DL> A, B;
+    chunk_load<true>(A, a, wk, h, wk.t_begin, chunk_nv(0), tg, dcol, vcol);
+    for (int64_t c = 0; c < nch; c += 2) {
+        if (c + 1 < nch) chunk_load<true>(B, a, wk, h, wk.t_begin + (c + 1) * CHUNK, chunk_nv(c + 1), tg, dcol, vcol);
+        St::run(a, wk, h, wk.t_begin + c * CHUNK, chunk_nv(c), A, S, smem);
+        if (c + 1 >= nch) break;
+        if (c + 2 < nch) chunk_load<true>(A, a, wk, h, wk.t_begin + (c + 2) * CHUNK, chunk_nv(c + 2), tg, dcol, vcol);
+        St::run(a, wk, h, wk.t_begin + (c + 1) * CHUNK, chunk_nv(c + 1), B, S, smem);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// Segment-local end state, chunks walked last to first.  With the decay of the later chunks
+// (sfx) known, every token's weight exp(sfx + G_C - G_t) = exp(decay from after t to the segment
+// end) is at most 1 (or e^{g} of an unclamped tail token), so the state accumulates directly in
+// the MFMA accumulators:  L += (k * weight)^T V  - no per-chunk rescale, no overflow guard.
+// L tile db holds L[16*db + 4*g4 + i][16*w + r16]; Gseg[i] = summed log-decay of key dim
+// d0 + DL*row + i of the segment.
+// ---------------------------------------------------------------------------------------
+template <typename TIn, typename TG, int DK, int DV>
+struct StateStep {
+    using L = Lay<TIn, DK, DV, false>;
+    using PR = Prec<TIn>;
+    static constexpr int DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NS = PR::NS, NX = PR::NX;
+
+    __device__ static void run(const PrefillParams& a, const Work& wk, int64_t tc, int nv,
+                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&Lst)[NDB], float (&Gseg)[DL], char* smem) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+        const int tg = lane & 15, row = lane >> 4;
+        const int dl0 = wave * DPW + DL * row;
+        char* sKTT = smem + L::OFF_KTT;
+        char* sVP = smem + L::OFF_VP + wave * PR::VPL * L::VPP;
+        {
+            float G[4][DL], GC[DL], x[4][DL];
+            chunk_float(cur.g, x, tg, nv);
+            const bool tail_chunk = (a.flags & 1) && (tc + nv == wk.len);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool unclamped = tail_chunk && (4 * tg + j == nv - 1);
+#pragma unroll
+                for (int i = 0; i < DL; ++i) G[j][i] = unclamped ? x[j][i] : fminf(x[j][i], 0.f);
+            }
+            chunk_cumsum<DL>(G, GC, lane);
+            chunk_float(cur.k, x, tg, nv);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < DL; ++i) x[j][i] *= fast_exp(Gseg[i] + GC[i] - G[j][i]);
+#pragma unroll
+            for (int i = 0; i < DL; ++i) {
+                Gseg[i] += GC[i];
+                const float col[4] = {x[0][i], x[1][i], x[2][i], x[3][i]};
+                lds_put_row<TIn, PR::DPL, 4>(sKTT, L::KTTP, (dl0 + i) * L::TS + 4 * tg, col);
+            }
+            float vx[4][4];
+            chunk_float(cur.v, vx, tg, nv);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float col[4] = {vx[0][c], vx[1][c], vx[2][c], vx[3][c]};
+                lds_put_row<TIn, PR::VPL, 4>(sVP, L::VPP, (4 * row + c) * L::TS + 4 * tg, col);
+            }
+        }
+        __syncthreads();
+        Split8<NX> vf[2];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag<TIn, NX>(sVP, L::VPP, L::TS, r16, 32 * k2, g4);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const Split8<NS> kf = lds_frag<TIn, NS>(sKTT, L::KTTP, L::TS, 16 * db + r16, 32 * k2, g4);
+                Lst[db] = mfma_split<NS, NX, NS>(kf, vf[k2], Lst[db]);
+            }
+        __syncthreads();  // the next chunk rewrites LDS
+    }
+};
+
+template <typename TIn, typename TG, int DK, int DV>
+__device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&Lst)[DK / 16],
+                                   float (&Gseg)[DK / (DV / 16) / 4], char* smem) {
+    using St = StateStep<TIn, TG, DK, DV>;
+    constexpr int DL = St::DL;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane & 15, row = lane >> 4;
+    const int dcol = wave * St::DPW + DL * row, vcol = wave * 16 + 4 * row;
+    const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
+    auto chunk_nv = [&](int64_t c) {
+        const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
+        return (int)(r < CHUNK ? r : CHUNK);
+    };
+    ChunkIn<TIn, TG, DL> A, B;
+    chunk_load<false>(A, a, wk, h, wk.t_begin + (nch - 1) * CHUNK, chunk_nv(nch - 1), tg, dcol, vcol);
+    for (int64_t c = nch - 1; c >= 0; c -= 2) {
+        if (c >= 1) chunk_load<false>(B, a, wk, h, wk.t_begin + (c - 1) * CHUNK, chunk_nv(c - 1), tg, dcol, vcol);
+        St::run(a, wk, wk.t_begin + c * CHUNK, chunk_nv(c), A, Lst, Gseg, smem);
+        if (c < 1) break;
+        if (c >= 2) chunk_load<false>(A, a, wk, h, wk.t_begin + (c - 2) * CHUNK, chunk_nv(c - 2), tg, dcol, vcol);
+        St::run(a, wk, wk.t_begin + (c - 1) * CHUNK, chunk_nv(c - 1), B, Lst, Gseg, smem);
     }
 }
 
@@ -554,34 +706,35 @@ __device__ __forceinline__ int64_t state_off(int db, int i, int g4, int r16, int
 }
 
 template <typename TIn, typename TG, int DK, int DV>
-__global__ __launch_bounds__(DV * 4) void gla_seg_state_kernel(PrefillParams a) {
+__global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 2 : 3) void gla_seg_state_kernel(PrefillParams a) {
     using L = Lay<TIn, DK, DV, false>;
+    constexpr int DL = L::DPW / 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
     f32x4 S[DK / 16];
-    float Gseg[L::DPW];
+    float Gseg[DL];
 #pragma unroll
     for (int db = 0; db < DK / 16; ++db) S[db] = zero4();
 #pragma unroll
-    for (int d = 0; d < L::DPW; ++d) Gseg[d] = 0.f;
-    segment_walk<TIn, TG, DK, DV, false>(a, wk, h, S, Gseg, smem);
+    for (int i = 0; i < DL; ++i) Gseg[i] = 0.f;
+    segment_state_walk<TIn, TG, DK, DV>(a, wk, h, S, Gseg, smem);
     float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
 #pragma unroll
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) st[state_off(db, i, g4, r16, wave, DV)] = S[db][i];
-    if (lane == 0) {
-        float* gs = a.ws_gamma + (w * a.H + h) * (int64_t)DK + wave * L::DPW;
+    if (r16 == 0) {  // lanes 16*row: key dims wave*DPW + DL*row + i
+        float* gs = a.ws_gamma + (w * a.H + h) * (int64_t)DK + wave * L::DPW + DL * g4;
 #pragma unroll
-        for (int d = 0; d < L::DPW; ++d) gs[d] = Gseg[d];
+        for (int i = 0; i < DL; ++i) gs[i] = Gseg[i];
     }
 }
 
 template <typename TIn, typename TG, int DK, int DV>
-__global__ __launch_bounds__(DV * 4) void gla_seg_output_kernel(PrefillParams a) {
+__global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void gla_seg_output_kernel(PrefillParams a) {
     using L = Lay<TIn, DK, DV, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
@@ -589,15 +742,12 @@ __global__ __launch_bounds__(DV * 4) void gla_seg_output_kernel(PrefillParams a)
     if (!find_work(a, w, wk)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
     f32x4 S[DK / 16];
-    float Gseg[L::DPW];
     const float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
 #pragma unroll
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, DV)];
-#pragma unroll
-    for (int d = 0; d < L::DPW; ++d) Gseg[d] = 0.f;
-    segment_walk<TIn, TG, DK, DV, true>(a, wk, h, S, Gseg, smem);
+    segment_walk<TIn, TG, DK, DV>(a, wk, h, S, smem);
 }
 
 // K0 (varlen): segment offsets from cu_seqlens, one thread block.
@@ -633,8 +783,7 @@ __global__ __launch_bounds__(256) void gla_varlen_plan_kernel(const int32_t* cu,
 // Host launchers.
 // ---------------------------------------------------------------------------------------
 bool prefill_shape_supported(int Dk, int Dv) {
-    return (Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128) ||
-           (Dk == 64 && Dv == 128) || (Dk == 128 && Dv == 64);
+    return (Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128) || (Dk == 128 && Dv == 64);
 }
 
 template <typename TIn, typename TG>
@@ -650,7 +799,6 @@ static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with
     TRIUNE_SEG_CASE(64, 64)
     TRIUNE_SEG_CASE(128, 128)
     TRIUNE_SEG_CASE(32, 32)
-    TRIUNE_SEG_CASE(64, 128)
     TRIUNE_SEG_CASE(128, 64)
 #undef TRIUNE_SEG_CASE
     return hipErrorInvalidValue;
@@ -682,7 +830,6 @@ int gla_seg_output_blocks_per_cu(int Dk, int Dv) {
     TRIUNE_OCC_CASE(64, 64)
     TRIUNE_OCC_CASE(128, 128)
     TRIUNE_OCC_CASE(32, 32)
-    TRIUNE_OCC_CASE(64, 128)
     TRIUNE_OCC_CASE(128, 64)
 #undef TRIUNE_OCC_CASE
     return (e == hipSuccess && nb > 0) ? nb : 1;

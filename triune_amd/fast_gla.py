@@ -33,7 +33,8 @@ __all__ = [
 ]
 
 _DIMS = (32, 64, 128)
-_PAIRS = ((32, 32), (64, 64), (64, 128), (128, 64), (128, 128))  # (Dk, Dv) the kernels support
+_PAIRS = ((32, 32), (64, 64), (128, 64), (128, 128))  # (Dk, Dv) the prefill kernels support
+_DECODE_PAIRS = ((32, 32), (64, 64), (64, 128), (128, 64), (128, 128))
 
 
 def _on_device(*ts):
@@ -49,10 +50,10 @@ def _round_dk(d: int) -> int:
     raise ValueError(f"key head dim {d} > 128 is not supported")
 
 
-def _pair(dk: int, dv: int) -> tuple[int, int]:
+def _pair(dk: int, dv: int, pairs=_PAIRS) -> tuple[int, int]:
     """Smallest supported (Dk, Dv) >= (dk, dv); inputs are zero-padded up to it."""
     best = None
-    for a, b in _PAIRS:
+    for a, b in pairs:
         if a >= dk and b >= dv and (best is None or a * b < best[0] * best[1]):
             best = (a, b)
     if best is None:
@@ -170,7 +171,7 @@ def gla_decode_step(q, k, v, g, state, out=None, *, inplace=False, slots=None, o
         q, k, v, g = q[:, 0], k[:, 0], v[:, 0], g[:, 0]
     B, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
-    Dk, Dv = _pair(Dk0, Dv0)
+    Dk, Dv = _pair(Dk0, Dv0, _DECODE_PAIRS)
     padded = (Dk, Dv) != (Dk0, Dv0)
     qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
     vp = _vec_layout(_pad_last(v, Dv))
