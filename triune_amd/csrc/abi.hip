@@ -78,6 +78,17 @@ int varlen_seg_chunks(int64_t chunk_jobs, int Dk, int Dv, int flags) {
 
 bool prefill_shape_ok(int Dk, int Dv) { return prefill_shape_supported(Dk, Dv); }
 
+// The prefill kernels address the 64 rows of a chunk as a uniform base plus a 32-bit per-lane
+// byte offset: 64 token strides plus one row must stay below 2^31 bytes.
+bool tok_strides_ok(const int64_t* st3_q, int io_dtype, int g_dtype, int o_dtype, int Dk, int Dv) {
+    auto ok = [](int64_t st, int dt, int D) {
+        const int64_t es = dt == TRIUNE_DT_F32 ? 4 : 2;
+        return st >= 0 && (64 * st + D) * es < ((int64_t)1 << 31);
+    };
+    return ok(st3_q[1], io_dtype, Dk) && ok(st3_q[4], io_dtype, Dk) && ok(st3_q[7], io_dtype, Dv) &&
+           ok(st3_q[10], g_dtype, Dk) && ok(st3_q[13], o_dtype, Dv);
+}
+
 bool gate_dtype_ok(int io_dtype, int g_dtype) { return g_dtype == io_dtype || g_dtype == TRIUNE_DT_F32; }
 
 struct PrefillPlan {
@@ -182,7 +193,7 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
         !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
         !vec_ok(o, o_dtype, strides + 12, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
-        reinterpret_cast<uintptr_t>(s_final) % 16)
+        reinterpret_cast<uintptr_t>(s_final) % 16 || !tok_strides_ok(strides, io_dtype, g_dtype, o_dtype, Dk, Dv))
         return TRIUNE_ERR_LAYOUT;
     hipStream_t st = (hipStream_t)stream;
     if (B == 0) return TRIUNE_OK;
@@ -253,7 +264,8 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
                              0, strides[6], strides[7], 0, strides[8], strides[9]};
     if (!vec_ok(q, io_dtype, st3 + 1, 2) || !vec_ok(k, io_dtype, st3 + 4, 2) || !vec_ok(v, io_dtype, st3 + 7, 2) ||
         !vec_ok(g, g_dtype, st3 + 10, 2) || !vec_ok(o, o_dtype, st3 + 13, 2) ||
-        reinterpret_cast<uintptr_t>(s0) % 16 || reinterpret_cast<uintptr_t>(s_final) % 16)
+        reinterpret_cast<uintptr_t>(s0) % 16 || reinterpret_cast<uintptr_t>(s_final) % 16 ||
+        !tok_strides_ok(st3, io_dtype, g_dtype, o_dtype, Dk, Dv))
         return TRIUNE_ERR_LAYOUT;
     const PrefillPlan pl = plan_varlen(n_seqs, total_tokens, H, Dk, Dv, flags);
     if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;

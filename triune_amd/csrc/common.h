@@ -170,6 +170,13 @@ __device__ __forceinline__ float row_shr(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x110 + N, 0xf, 0xf, true));
 }
 
+// Value of x in lane (lane + n) of the same 16-lane row, or 0 for the last n lanes of the row
+// (DPP row_shl with bound_ctrl).
+template <int N>
+__device__ __forceinline__ float row_shl(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x100 + N, 0xf, 0xf, true));
+}
+
 // Inclusive prefix sum across the 16 lanes of each row.
 __device__ __forceinline__ float row_inclusive_scan(float x) {
     x += row_shr<1>(x);

@@ -22,9 +22,9 @@
 // below the split depth are accumulated in fp32.
 //
 // One workgroup of NW = Dv/16 waves handles a (segment, head).  Per chunk:
-//   stage 1  wave w, lane = token: cumulative decay, factors and split Qt/Kt for key dims
-//            [w*DPW, (w+1)*DPW) -> LDS (row planes for Qt/Kt, a [dim][token] plane for Kt^T);
-//            its own 16 value columns of V -> LDS ([column][token] plane)
+//   stage 1  wave w (each lane 4 tokens x DPW/4 dims): cumulative decay, factors and split
+//            Qt/Kt for key dims [w*DPW, (w+1)*DPW) -> LDS (row planes for Qt/Kt, a [dim][token]
+//            plane for Kt^T); its own 16 value columns of V -> LDS ([column][token] plane)
 //   stage 2  the ten 16x16 causal tiles of A^T, spread over the waves -> LDS
 //   stage 3  wave w: O^T and the state update for value columns [16w, 16w+16)
 // The next chunk's inputs are loaded into registers while the current chunk is processed.
@@ -100,7 +100,9 @@ struct Lay {
     static constexpr int NW = DV / 16;            // waves per workgroup
     static constexpr int DPW = DK / NW;           // key dims per wave in stage 1
     static constexpr int RS = DK + PAD;           // row stride of [token][dim] planes
-    static constexpr int TS = CHUNK + PAD;        // row stride of [dim][token] / [column][token] planes
+    // row stride of [dim][token] / [column][token] planes: the stage-1 stores of 32 lanes (eight
+    // tg x four rows DL dims apart) and the fragment reads both land on distinct banks
+    static constexpr int TS = CHUNK + (DPW == 16 ? 8 : 4);
     static constexpr int ROWP = CHUNK * RS * P::DES;
     static constexpr int KTTP = DK * TS * P::DES;
     static constexpr int VPP = 16 * TS * P::DES;  // one wave's V, per plane
@@ -113,7 +115,11 @@ struct Lay {
     static constexpr int OFF_FAC = OFF_VP + NW * P::VPL * VPP;
     static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
     static constexpr int BYTES = OFF_FLAG + 16 * 4;
+    // fp32 staging of a wave's outputs, 32 tokens x 16 columns, row stride OS floats: the 16 lanes
+    // of an LDS cycle hit distinct banks both when the MFMA layout writes and when quads read rows
+    static constexpr int OS = 20;
     static_assert(DPW == 16 || DPW == 32, "stage-1 dims per wave");
+    static_assert(!OUT || NW * 32 * OS * 4 <= P::DPL * ROWP, "output staging fits in the Kt row planes");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -248,9 +254,61 @@ __device__ __forceinline__ float lane_value(float x, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
-// Stage-1 lane mapping: lane = 16*row + tg holds tokens 4*tg + j (j < 4) of key dims
-// d0 + DL*row + i (i < DL, DL = DPW/4) and value columns c0 + 4*row + c (c < 4).  Rows are DPP
-// rows, so a scan over tokens is a 4-step serial sum plus a 16-lane DPP scan.
+__device__ __forceinline__ int64_t uniform_i64(int64_t x) {
+    const uint64_t u = (uint64_t)x;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Addressing of one token-major input under the stage-1 lane mapping: a wave-uniform base
+// (token 0 of the sequence, head h) plus a 32-bit per-lane byte offset (token 4*tg of a chunk,
+// first column of the lane), so a full chunk's loads need no per-lane 64-bit arithmetic.
+// The host guarantees 64 * token stride + row bytes < 2^31.
+struct TokAddr {
+    const char* base;
+    int64_t st;    // token stride, bytes (uniform)
+    int32_t lane;  // 4*tg*st + col*sizeof(T)
+};
+
+template <typename T>
+__device__ __forceinline__ TokAddr tok_addr(const TokTensor& x, const Work& wk, int64_t h, int tg, int col) {
+    TokAddr r;
+    const int64_t es = (int64_t)sizeof(T);
+    r.base = reinterpret_cast<const char*>(x.p) + uniform_i64((wk.b * x.sb + wk.row0 * x.st + h * x.sh) * es);
+    r.st = x.st * es;
+    r.lane = (int32_t)(4 * tg * r.st + col * es);
+    return r;
+}
+
+// Row tc + 4*tg + j of a full chunk, or tc + min(4*tg + j, nv - 1) of a partial one.
+template <typename T, bool FULL>
+__device__ __forceinline__ const T* tok_ptr(const TokAddr& a, int64_t tc, int j, int tg, int nv) {
+    if (FULL) return reinterpret_cast<const T*>(a.base + (tc + j) * a.st + a.lane);
+    const int tl = min(4 * tg + j, nv - 1);
+    return reinterpret_cast<const T*>(a.base + tc * a.st + a.lane + (int64_t)(tl - 4 * tg) * a.st);
+}
+
+struct ChunkAddr {
+    TokAddr q, k, g, v;
+};
+
+template <bool OUT, typename TIn, typename TG>
+__device__ __forceinline__ ChunkAddr chunk_addr(const PrefillParams& a, const Work& wk, int64_t h, int tg, int dcol,
+                                                int vcol) {
+    ChunkAddr c;
+    if (OUT) c.q = tok_addr<TIn>(a.q, wk, h, tg, dcol);
+    c.k = tok_addr<TIn>(a.k, wk, h, tg, dcol);
+    c.g = tok_addr<TG>(a.g, wk, h, tg, dcol);
+    c.v = tok_addr<TIn>(a.v, wk, h, tg, vcol);
+    return c;
+}
+
+// Stage-1 lane mapping: lane = 4*tg + row (tg = lane >> 2, row = lane & 3) holds tokens 4*tg + j
+// (j < 4) of key dims d0 + DL*row + i (i < DL, DL = DPW/4) and value columns c0 + 4*row + c
+// (c < 4).  The four lanes of a quad read one contiguous 4*DL-element piece of a token row, so
+// each quad costs the L1 a single access; a scan over tokens is a serial sum over j, a DPP scan
+// over the four tg of each 16-lane row, and a scan over the four rows' totals.
 template <typename TIn, typename TG, int DL>
 struct ChunkIn {
     Vec<TIn, DL> q[4], k[4];
@@ -258,18 +316,24 @@ struct ChunkIn {
     Vec<TIn, 4> v[4];
 };
 
-template <bool OUT, typename TIn, typename TG, int DL>
-__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const PrefillParams& a, const Work& wk, int64_t h,
-                                           int64_t tc, int nv, int tg, int dcol, int vcol) {
+template <bool OUT, bool FULL, typename TIn, typename TG, int DL>
+__device__ __forceinline__ void chunk_load_rows(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, int nv,
+                                                int tg) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int tl = 4 * tg + j;
-        const int64_t t = tc + (tl < nv ? tl : nv - 1);  // every lane reads a row inside the chunk
-        if (OUT) vec_load(c.q[j], tok_row<TIn>(a.q, wk, t, h, dcol));
-        vec_load(c.k[j], tok_row<TIn>(a.k, wk, t, h, dcol));
-        vec_load(c.g[j], tok_row<TG>(a.g, wk, t, h, dcol));
-        vec_load(c.v[j], tok_row<TIn>(a.v, wk, t, h, vcol));
+        if (OUT) vec_load(c.q[j], tok_ptr<TIn, FULL>(ad.q, tc, j, tg, nv));
+        vec_load(c.k[j], tok_ptr<TIn, FULL>(ad.k, tc, j, tg, nv));
+        vec_load(c.g[j], tok_ptr<TG, FULL>(ad.g, tc, j, tg, nv));
+        vec_load(c.v[j], tok_ptr<TIn, FULL>(ad.v, tc, j, tg, nv));
     }
+}
+
+// Inputs of the chunk starting at token tc with nv valid tokens; in a partial chunk every lane
+// still reads a row inside the chunk (rows past nv repeat the last one and are zeroed later).
+template <bool OUT, typename TIn, typename TG, int DL>
+__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, int nv, int tg) {
+    if (nv == CHUNK) chunk_load_rows<OUT, true>(c, ad, tc, nv, tg);
+    else chunk_load_rows<OUT, false>(c, ad, tc, nv, tg);
 }
 
 // x[j][i] = element i of token j, zeroed for tokens at or past nv (partial chunks only).
@@ -288,10 +352,10 @@ __device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[
 }
 
 // In place: G[j][i] <- inclusive sum over tokens 0..4*tg+j of the chunk (per key dim i);
-// returns the chunk totals in GC[i] (identical across the 16 lanes of a row).
+// returns the chunk totals in GC[i] (identical across the lanes sharing `row`).
 template <int DL>
 __device__ __forceinline__ void chunk_cumsum(float (&G)[4][DL], float (&GC)[DL], int lane) {
-    float T[DL], I[DL];
+    float T[DL], I[DL], R[DL], P[DL];
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
         G[1][i] += G[0][i];
@@ -300,20 +364,78 @@ __device__ __forceinline__ void chunk_cumsum(float (&G)[4][DL], float (&GC)[DL],
         T[i] = G[3][i];
         I[i] = T[i];
     }
-#pragma unroll
-    for (int i = 0; i < DL; ++i) I[i] += row_shr<1>(I[i]);
-#pragma unroll
-    for (int i = 0; i < DL; ++i) I[i] += row_shr<2>(I[i]);
+    // the four tg of a 16-lane DPP row sit 4 lanes apart
 #pragma unroll
     for (int i = 0; i < DL; ++i) I[i] += row_shr<4>(I[i]);
 #pragma unroll
     for (int i = 0; i < DL; ++i) I[i] += row_shr<8>(I[i]);
+    // DPP row rr's total for this `row` is in lane 16*rr + 12 + row; P = inclusive scan of the
+    // totals over rr
+    const int rr = lane >> 4, own = (lane & 48) | 12 | (lane & 3);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) R[i] = lane_bcast(I[i], own);
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
-        const float E = I[i] - T[i];
+        const float prev = lane_bcast(R[i], (lane - 16) & 63);
+        P[i] = R[i] + (rr >= 1 ? prev : 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float prev = lane_bcast(P[i], (lane - 32) & 63);
+        P[i] += rr >= 2 ? prev : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float E = I[i] - T[i] + (P[i] - R[i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) G[j][i] += E;
-        GC[i] = lane_bcast(I[i], (lane & 48) | 15);
+        GC[i] = lane_bcast(P[i], 60 | (lane & 3));
+    }
+}
+
+// X[j][i] <- sum of g over the tokens after 4*tg + j in the chunk (exclusive suffix, per key dim
+// i), GC[i] <- the chunk total.  Every suffix is summed from the later tokens only, so its
+// rounding error scales with the suffix itself, not with the chunk total (a difference of two
+// prefix sums loses that accuracy when the total is large).
+template <int DL>
+__device__ __forceinline__ void chunk_suffix(const float (&g)[4][DL], float (&X)[4][DL], float (&GC)[DL], int lane) {
+    float T[DL], Y[DL], Z[DL], C[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        X[3][i] = 0.f;
+        X[2][i] = g[3][i];
+        X[1][i] = X[2][i] + g[2][i];
+        X[0][i] = X[1][i] + g[1][i];
+        T[i] = X[0][i] + g[0][i];
+    }
+    // Y = sum of T over the later tg of the same 16-lane DPP row (4 lanes apart)
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Y[i] = row_shl<4>(T[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Y[i] += row_shl<4>(Y[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Y[i] += row_shl<8>(Y[i]);
+    // Z = this DPP row's total (lane 16*rr + row, the row's first tg); C = inclusive suffix of Z
+    const int rr = lane >> 4, first = (lane & 48) | (lane & 3);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Z[i] = lane_bcast(Y[i] + T[i], first);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float next = lane_bcast(Z[i], (lane + 16) & 63);
+        C[i] = Z[i] + (rr <= 2 ? next : 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float next = lane_bcast(C[i], (lane + 32) & 63);
+        C[i] += rr <= 1 ? next : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float later_rows = lane_bcast(C[i], (lane + 16) & 63);
+        const float E = Y[i] + (rr <= 2 ? later_rows : 0.f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) X[j][i] += E;
+        GC[i] = lane_bcast(C[i], lane & 3);
     }
 }
 
@@ -378,10 +500,12 @@ struct OutStep {
     static constexpr int NS = PR::NS, NX = PR::NX;
 
     // One chunk: stage 1 (factors, split operands -> LDS), stage 2 (A^T tiles), stage 3 (O, S).
+    // after_inputs() runs once stage 1 has consumed `cur` (it may refill those registers).
+    template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem) {
+                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
-        const int tg = lane & 15, row = lane >> 4;
+        const int tg = lane >> 2, row = lane & 3;
         const int d0 = wave * DPW, c0 = wave * 16;
         const int dl0 = d0 + DL * row;  // first key dim of this lane in stage 1
         char* sQT = smem + L::OFF_QT;
@@ -478,6 +602,7 @@ struct OutStep {
                 lds_put_row<TIn, PR::VPL, 4>(sVP, L::VPP, (4 * row + c) * L::TS + 4 * tg, col);
             }
         }
+        after_inputs();
         __syncthreads();
         bool fast = true;
 #pragma unroll
@@ -560,13 +685,29 @@ struct OutStep {
                     Ot[tb] = mfma_split<NX, NS, NS>(vf[k2], af, Ot[tb]);
                 }
             }
+            // Lane (g4, r16) holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3].  Stage it, 32
+            // tokens at a time, through this wave's slice of the Kt row planes (free after stage
+            // 2), and store with the four lanes of a quad covering one token's 16 columns.
+            {
+                float* sO = reinterpret_cast<float*>(smem + L::OFF_KT) + wave * (32 * L::OS);
+                const int es = dt_size(a.o_dt);
+                const int64_t ost = a.o_st * es;
+                char* obase = reinterpret_cast<char*>(a.o) +
+                              uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
+                const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);  // token within 16
+                const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {  // lane holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3]
-                const int t = 16 * tb + r16;
-                if (t < nv) {
-                    const int64_t off = wk.b * a.o_sb + (wk.row0 + tc + t) * a.o_st + h * a.o_sh + c0 + 4 * g4;
-                    store4_dt(reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt), a.o_dt, Ot[tb][0], Ot[tb][1],
-                              Ot[tb][2], Ot[tb][3]);
+                for (int half = 0; half < 2; ++half) {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k)
+                        *reinterpret_cast<f32x4*>(sO + (16 * k + r16) * L::OS + 4 * g4) = Ot[2 * half + k];
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const int t = 32 * half + 16 * k + tq;
+                        const f32x4 x = *reinterpret_cast<const f32x4*>(sO + (16 * k + tq) * L::OS + 4 * q);
+                        if (t < nv)
+                            store4_dt(obase + (32 * half + 16 * k) * ost + olane, a.o_dt, x[0], x[1], x[2], x[3]);
+                    }
                 }
             }
 #pragma unroll
@@ -587,27 +728,32 @@ struct OutStep {
     }
 };
 
-// Outputs of one segment from its carried-in state S (K3).  Chunk inputs ping-pong between two
-// register sets: the next chunk is loaded while the current one is processed.
+// Outputs of one segment from its carried-in state S (K3).  Chunk inputs alternate between two
+// register sets; a set is refilled (two chunks ahead) as soon as stage 1 has consumed it, so two
+// chunks of loads are in flight while stages 2-3 run.
 template <typename TIn, typename TG, int DK, int DV>
 __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
     using St = OutStep<TIn, TG, DK, DV>;
     constexpr int DL = St::DL;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane & 15, row = lane >> 4;
-    const int dcol = wave * St::DPW + DL * row, vcol = wave * 16 + 4 * row;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane >> 2, row = lane & 3;
+    const ChunkAddr ad = chunk_addr<true, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
     const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
     auto chunk_nv = [&](int64_t c) {
         const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
         return (int)(r < CHUNK ? r : CHUNK);
     };
+    auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     ChunkIn<TIn, TG, DL> A, B;
-    chunk_load<true>(A, a, wk, h, wk.t_begin, chunk_nv(0), tg, dcol, vcol);
+    chunk_load<true>(A, ad, tok(0), chunk_nv(0), tg);
+    if (nch > 1) chunk_load<true>(B, ad, tok(1), chunk_nv(1), tg);
     for (int64_t c = 0; c < nch; c += 2) {
-        if (c + 1 < nch) chunk_load<true>(B, a, wk, h, wk.t_begin + (c + 1) * CHUNK, chunk_nv(c + 1), tg, dcol, vcol);
-        St::run(a, wk, h, wk.t_begin + c * CHUNK, chunk_nv(c), A, S, smem);
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem, [&] {
+            if (c + 2 < nch) chunk_load<true>(A, ad, tok(c + 2), chunk_nv(c + 2), tg);
+        });
         if (c + 1 >= nch) break;
-        if (c + 2 < nch) chunk_load<true>(A, a, wk, h, wk.t_begin + (c + 2) * CHUNK, chunk_nv(c + 2), tg, dcol, vcol);
-        St::run(a, wk, h, wk.t_begin + (c + 1) * CHUNK, chunk_nv(c + 1), B, S, smem);
+        St::run(a, wk, h, tok(c + 1), chunk_nv(c + 1), B, S, smem, [&] {
+            if (c + 3 < nch) chunk_load<true>(B, ad, tok(c + 3), chunk_nv(c + 3), tg);
+        });
     }
 }
 
@@ -625,10 +771,12 @@ struct StateStep {
     using PR = Prec<TIn>;
     static constexpr int DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NS = PR::NS, NX = PR::NX;
 
+    template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t tc, int nv,
-                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&Lst)[NDB], float (&Gseg)[DL], char* smem) {
+                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&Lst)[NDB], float (&Gseg)[DL], char* smem,
+                               Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
-        const int tg = lane & 15, row = lane >> 4;
+        const int tg = lane >> 2, row = lane & 3;
         const int dl0 = wave * DPW + DL * row;
         char* sKTT = smem + L::OFF_KTT;
         char* sVP = smem + L::OFF_VP + wave * PR::VPL * L::VPP;
@@ -642,12 +790,13 @@ struct StateStep {
 #pragma unroll
                 for (int i = 0; i < DL; ++i) G[j][i] = unclamped ? x[j][i] : fminf(x[j][i], 0.f);
             }
-            chunk_cumsum<DL>(G, GC, lane);
+            float X[4][DL];
+            chunk_suffix<DL>(G, X, GC, lane);
             chunk_float(cur.k, x, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int i = 0; i < DL; ++i) x[j][i] *= fast_exp(Gseg[i] + GC[i] - G[j][i]);
+                for (int i = 0; i < DL; ++i) x[j][i] *= fast_exp(Gseg[i] + X[j][i]);
 #pragma unroll
             for (int i = 0; i < DL; ++i) {
                 Gseg[i] += GC[i];
@@ -662,6 +811,7 @@ struct StateStep {
                 lds_put_row<TIn, PR::VPL, 4>(sVP, L::VPP, (4 * row + c) * L::TS + 4 * tg, col);
             }
         }
+        after_inputs();
         __syncthreads();
         Split8<NX> vf[2];
 #pragma unroll
@@ -682,21 +832,25 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
                                    float (&Gseg)[DK / (DV / 16) / 4], char* smem) {
     using St = StateStep<TIn, TG, DK, DV>;
     constexpr int DL = St::DL;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane & 15, row = lane >> 4;
-    const int dcol = wave * St::DPW + DL * row, vcol = wave * 16 + 4 * row;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane >> 2, row = lane & 3;
+    const ChunkAddr ad = chunk_addr<false, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
     const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
     auto chunk_nv = [&](int64_t c) {
         const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
         return (int)(r < CHUNK ? r : CHUNK);
     };
+    auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     ChunkIn<TIn, TG, DL> A, B;
-    chunk_load<false>(A, a, wk, h, wk.t_begin + (nch - 1) * CHUNK, chunk_nv(nch - 1), tg, dcol, vcol);
+    chunk_load<false>(A, ad, tok(nch - 1), chunk_nv(nch - 1), tg);
+    if (nch > 1) chunk_load<false>(B, ad, tok(nch - 2), chunk_nv(nch - 2), tg);
     for (int64_t c = nch - 1; c >= 0; c -= 2) {
-        if (c >= 1) chunk_load<false>(B, a, wk, h, wk.t_begin + (c - 1) * CHUNK, chunk_nv(c - 1), tg, dcol, vcol);
-        St::run(a, wk, wk.t_begin + c * CHUNK, chunk_nv(c), A, Lst, Gseg, smem);
+        St::run(a, wk, tok(c), chunk_nv(c), A, Lst, Gseg, smem, [&] {
+            if (c >= 2) chunk_load<false>(A, ad, tok(c - 2), chunk_nv(c - 2), tg);
+        });
         if (c < 1) break;
-        if (c >= 2) chunk_load<false>(A, a, wk, h, wk.t_begin + (c - 2) * CHUNK, chunk_nv(c - 2), tg, dcol, vcol);
-        St::run(a, wk, wk.t_begin + (c - 1) * CHUNK, chunk_nv(c - 1), B, Lst, Gseg, smem);
+        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, Lst, Gseg, smem, [&] {
+            if (c >= 3) chunk_load<false>(B, ad, tok(c - 3), chunk_nv(c - 3), tg);
+        });
     }
 }
 
@@ -706,7 +860,7 @@ __device__ __forceinline__ int64_t state_off(int db, int i, int g4, int r16, int
 }
 
 template <typename TIn, typename TG, int DK, int DV>
-__global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 2 : 3) void gla_seg_state_kernel(PrefillParams a) {
+__global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams a) {
     using L = Lay<TIn, DK, DV, false>;
     constexpr int DL = L::DPW / 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
@@ -726,8 +880,8 @@ __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 2 : 3) void
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) st[state_off(db, i, g4, r16, wave, DV)] = S[db][i];
-    if (r16 == 0) {  // lanes 16*row: key dims wave*DPW + DL*row + i
-        float* gs = a.ws_gamma + (w * a.H + h) * (int64_t)DK + wave * L::DPW + DL * g4;
+    if (lane < 4) {  // tg = 0, row = lane: key dims wave*DPW + DL*row + i
+        float* gs = a.ws_gamma + (w * a.H + h) * (int64_t)DK + wave * L::DPW + DL * lane;
 #pragma unroll
         for (int i = 0; i < DL; ++i) gs[i] = Gseg[i];
     }

@@ -36,10 +36,13 @@ __device__ __forceinline__ void st4_dt(void* p, int dt, int64_t i, const float (
     else store4_dt(reinterpret_cast<_Float16*>(p) + i, dt, x[0], x[1], x[2], x[3]);
 }
 
-// grid: (ceil(Dk*Dv/4 / 256), H, n_outer), block 256; each thread owns 4 consecutive elements.
-__global__ __launch_bounds__(256) void recurrent_scan_kernel(ScanParams a) {
+// grid: (ceil(Dk*Dv/4 / SCAN_TPB), H, n_outer), block SCAN_TPB; each thread owns 4 consecutive
+// elements.  Small blocks spread the (outer, head) rows over many CUs; the loop issues the
+// loads of U steps before the dependent chain consumes them.
+constexpr int SCAN_TPB = 64;
+__global__ __launch_bounds__(SCAN_TPB) void recurrent_scan_kernel(ScanParams a) {
     const int64_t DD = (int64_t)a.Dk * a.Dv;
-    const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const int64_t e = ((int64_t)blockIdx.x * SCAN_TPB + threadIdx.x) * 4;
     if (e >= DD) return;
     const int64_t h = blockIdx.y, o = blockIdx.z;
     const int row = (int)(e / a.Dv);
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(256) void recurrent_scan_kernel(ScanParams a) {
     const int64_t kv_base = o * a.kv_so + h * a.kv_sh + e;
     const int64_t sa_base = o * a.sa_so + h * a.sa_sh + e;
     const int64_t d_base = o * a.d_so + h * a.d_sh + row;
-    constexpr int U = 4;  // read U steps ahead of the dependent chain
+    constexpr int U = 8;
     int64_t n = 0;
     for (; n + U <= N; n += U) {
         float x[U][4], d[U];
@@ -90,8 +93,8 @@ __global__ __launch_bounds__(256) void recurrent_scan_kernel(ScanParams a) {
 
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream) {
     const int64_t DD = (int64_t)a.Dk * a.Dv;
-    dim3 grid((unsigned)((DD / 4 + 255) / 256), (unsigned)a.H, (unsigned)a.n_outer);
-    hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(256), 0, stream, a);
+    dim3 grid((unsigned)((DD / 4 + SCAN_TPB - 1) / SCAN_TPB), (unsigned)a.H, (unsigned)a.n_outer);
+    hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(SCAN_TPB), 0, stream, a);
     return hipGetLastError();
 }
 
