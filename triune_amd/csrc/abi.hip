@@ -178,8 +178,12 @@ size_t triune_hip_gla_prefill_workspace_size(int64_t B, int64_t T, int64_t H, in
     return plan_dense(B, T, H, Dk, Dv, flags).total;
 }
 
-static void fill_tok(TokTensor& t, const void* p, const int64_t* st3) {
+// extent: bytes from p to one past the last element of a [nb, nt, H, D] view (nb, nt >= 1).
+static void fill_tok(TokTensor& t, const void* p, const int64_t* st3, int64_t nb, int64_t nt, int64_t H, int D,
+                     int dt) {
     t.p = p; t.sb = st3[0]; t.st = st3[1]; t.sh = st3[2];
+    const int64_t es = dt == TRIUNE_DT_F32 ? 4 : 2;
+    t.extent = ((nb - 1) * t.sb + (nt - 1) * t.st + (H - 1) * t.sh + D) * es;
 }
 
 int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
@@ -189,7 +193,7 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
     if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
-    if (B < 0 || T < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return TRIUNE_ERR_SHAPE;
+    if (B < 0 || T < 0 || H <= 0 || !prefill_dtype_supported(Dk, Dv, io_dtype)) return TRIUNE_ERR_SHAPE;
     if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
         !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
         !vec_ok(o, o_dtype, strides + 12, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
@@ -212,10 +216,10 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
 
     PrefillParams a{};
-    fill_tok(a.q, q, strides + 0);
-    fill_tok(a.k, k, strides + 3);
-    fill_tok(a.v, v, strides + 6);
-    fill_tok(a.g, g, strides + 9);
+    fill_tok(a.q, q, strides + 0, B, T, H, Dk, io_dtype);
+    fill_tok(a.k, k, strides + 3, B, T, H, Dk, io_dtype);
+    fill_tok(a.v, v, strides + 6, B, T, H, Dv, io_dtype);
+    fill_tok(a.g, g, strides + 9, B, T, H, Dk, g_dtype);
     a.o = o; a.o_sb = strides[12]; a.o_st = strides[13]; a.o_sh = strides[14];
     a.g_dt = g_dtype; a.o_dt = o_dtype;
     a.s0 = s0;
@@ -258,7 +262,8 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
     if (!q || !k || !v || !g || !o || !strides || !cu_seqlens) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
     if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
-    if (n_seqs <= 0 || total_tokens < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return TRIUNE_ERR_SHAPE;
+    if (n_seqs <= 0 || total_tokens < 0 || H <= 0 || !prefill_dtype_supported(Dk, Dv, io_dtype))
+        return TRIUNE_ERR_SHAPE;
     // (token, head) strides; the batch stride is unused (single packed batch)
     const int64_t st3[15] = {0, strides[0], strides[1], 0, strides[2], strides[3], 0, strides[4], strides[5],
                              0, strides[6], strides[7], 0, strides[8], strides[9]};
@@ -274,10 +279,11 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
     hipStream_t st = (hipStream_t)stream;
 
     PrefillParams a{};
-    fill_tok(a.q, q, st3 + 0);
-    fill_tok(a.k, k, st3 + 3);
-    fill_tok(a.v, v, st3 + 6);
-    fill_tok(a.g, g, st3 + 9);
+    const int64_t nt = total_tokens > 0 ? total_tokens : 1;
+    fill_tok(a.q, q, st3 + 0, 1, nt, H, Dk, io_dtype);
+    fill_tok(a.k, k, st3 + 3, 1, nt, H, Dk, io_dtype);
+    fill_tok(a.v, v, st3 + 6, 1, nt, H, Dv, io_dtype);
+    fill_tok(a.g, g, st3 + 9, 1, nt, H, Dk, g_dtype);
     a.o = o; a.o_sb = 0; a.o_st = st3[13]; a.o_sh = st3[14];
     a.g_dt = g_dtype; a.o_dt = o_dtype;
     a.s0 = s0;

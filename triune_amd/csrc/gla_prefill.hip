@@ -45,6 +45,14 @@ struct Work {
     int p;
 };
 
+// x is the same in every lane; say so to the compiler (scalar registers, scalar branches).
+__device__ __forceinline__ int64_t uniform_i64(int64_t x) {
+    const uint64_t u = (uint64_t)x;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ bool find_work(const PrefillParams& a, int64_t w, Work& wk) {
     if (!a.varlen) {
         const int64_t seq = w / a.nseg_dense;
@@ -78,6 +86,12 @@ __device__ __forceinline__ bool find_work(const PrefillParams& a, int64_t w, Wor
         wk.t_end = wk.t_begin + (int64_t)a.P * CHUNK;
     }
     if (wk.t_end > wk.len) wk.t_end = wk.len;
+    // the segment is per workgroup: uniform loop bounds keep the chunk loops scalar
+    wk.b = uniform_i64(wk.b);
+    wk.row0 = uniform_i64(wk.row0);
+    wk.len = uniform_i64(wk.len);
+    wk.t_begin = uniform_i64(wk.t_begin);
+    wk.t_end = uniform_i64(wk.t_end);
     return wk.t_begin < wk.t_end;
 }
 
@@ -89,37 +103,34 @@ struct Prec {
     static constexpr bool F32 = std::is_same<TIn, float>::value;
     static constexpr int NS = F32 ? 3 : 2;                                             // parts of derived operands
     static constexpr int NX = F32 ? 3 : (std::is_same<TIn, _Float16>::value ? 2 : 1);  // parts of V
-    static constexpr int DPL = F32 ? 1 : NS;  // LDS planes of a derived matrix (fp32 I/O: one fp32 plane)
-    static constexpr int DES = F32 ? 4 : 2;   // bytes per element of such a plane
-    static constexpr int VPL = F32 ? 1 : NX;  // LDS planes of V
 };
 
+// Every LDS operand is stored token-major as NP planes of bf16 parts (x ~= p0 + p1 (+ p2)).
+// Fragments whose K index is the token come out of the same planes through the transposed
+// read (ds_read_b64_tr_b16), so no operand is stored twice.
 template <typename TIn, int DK, int DV, bool OUT>
 struct Lay {
     using P = Prec<TIn>;
-    static constexpr int NW = DV / 16;            // waves per workgroup
-    static constexpr int DPW = DK / NW;           // key dims per wave in stage 1
-    static constexpr int RS = DK + PAD;           // row stride of [token][dim] planes
-    // row stride of [dim][token] / [column][token] planes: the stage-1 stores of 32 lanes (eight
-    // tg x four rows DL dims apart) and the fragment reads both land on distinct banks
-    static constexpr int TS = CHUNK + (DPW == 16 ? 8 : 4);
-    static constexpr int ROWP = CHUNK * RS * P::DES;
-    static constexpr int KTTP = DK * TS * P::DES;
-    static constexpr int VPP = 16 * TS * P::DES;  // one wave's V, per plane
-    static constexpr int ATP = 10 * 64 * 4 * P::DES;
+    static constexpr int NW = DV / 16;             // waves per workgroup
+    static constexpr int DPW = DK / NW;            // key dims per wave in stage 1
+    static constexpr int RS = DK + PAD;            // row stride (elements) of [token][dim] planes
+    static constexpr int VS = 16;                  // row stride of a wave's [token][16 columns] V planes
+    static constexpr int ROWP = CHUNK * RS * 2;    // bytes per [token][dim] plane
+    static constexpr int VPP = CHUNK * VS * 2;     // bytes per V plane of one wave
+    static constexpr int ATP = 10 * 64 * 4 * 2;    // bytes per plane of the ten A^T tiles
+    // K3: Qt rows, Kt rows, A^T tiles.  K1: exp-weighted k rows (in the Kt slot).
     static constexpr int OFF_QT = 0;
-    static constexpr int OFF_KT = OFF_QT + (OUT ? P::DPL * ROWP : 0);
-    static constexpr int OFF_KTT = OFF_KT + (OUT ? P::DPL * ROWP : 0);
-    static constexpr int OFF_AT = OFF_KTT + P::DPL * KTTP;
-    static constexpr int OFF_VP = OFF_AT + (OUT ? P::DPL * ATP : 0);
-    static constexpr int OFF_FAC = OFF_VP + NW * P::VPL * VPP;
+    static constexpr int OFF_KT = OFF_QT + (OUT ? P::NS * ROWP : 0);
+    static constexpr int OFF_AT = OFF_KT + P::NS * ROWP;
+    static constexpr int OFF_VP = OFF_AT + (OUT ? P::NS * ATP : 0);
+    static constexpr int OFF_FAC = OFF_VP + NW * P::NX * VPP;
     static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
     static constexpr int BYTES = OFF_FLAG + 16 * 4;
-    // fp32 staging of a wave's outputs, 32 tokens x 16 columns, row stride OS floats: the 16 lanes
+    // fp32 staging of a wave's outputs, 16 tokens x 16 columns, row stride OS floats: the 16 lanes
     // of an LDS cycle hit distinct banks both when the MFMA layout writes and when quads read rows
     static constexpr int OS = 20;
     static_assert(DPW == 16 || DPW == 32, "stage-1 dims per wave");
-    static_assert(!OUT || NW * 32 * OS * 4 <= P::DPL * ROWP, "output staging fits in the Kt row planes");
+    static_assert(16 * OS * 4 <= P::NX * VPP, "output staging fits in a wave's V planes");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -131,70 +142,67 @@ __device__ __forceinline__ void tile_sb_tb(int i, int& sb, int& tb) {
 __device__ __forceinline__ int tile_index(int sb, int tb) { return tb * (tb + 1) / 2 + sb; }
 
 // ---- LDS plane access ------------------------------------------------------------------
-// Fragment of a plane set with row stride rs: lane (g4, r16) reads row `row`, elements
-// col0 + 4*g4 + [0,4) into K slots 0..3 and col0 + 16 + 4*g4 + [0,4) into slots 4..7.
-// 16-bit I/O: NP bf16 planes, one part each.  fp32 I/O: one fp32 plane split into NP parts.
-template <typename TIn, int NP>
+// Fragment whose lane index is a plane row (token-major plane, K index along the row): lane
+// (g4, r16) reads row `row`, elements col0 + 4*g4 + [0,4) into K slots 0..3 and
+// col0 + 16 + 4*g4 + [0,4) into slots 4..7, one bf16 part per plane.
+template <int NP>
 __device__ __forceinline__ Split8<NP> lds_frag(const char* base, int plane_bytes, int rs, int row, int col0, int g4) {
     Split8<NP> f;
-    if constexpr (Prec<TIn>::F32) {
-        const float* p = reinterpret_cast<const float*>(base) + row * rs + col0 + 4 * g4;
-        const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-        const f32x4 b = *reinterpret_cast<const f32x4*>(p + 16);
-        float x[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        f = split8<NP>(x);
-    } else {
 #pragma unroll
-        for (int pl = 0; pl < NP; ++pl) {
-            const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes) + row * rs + col0 + 4 * g4;
-            const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
-            const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
-            f.p[pl] = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        }
+    for (int pl = 0; pl < NP; ++pl) {
+        const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes) + row * rs + col0 + 4 * g4;
+        const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
+        const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+        f.p[pl] = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
     return f;
 }
 
-// One value, split into NP bf16 planes (16-bit I/O) or stored as fp32 (fp32 I/O).
-template <typename TIn, int NP>
-__device__ __forceinline__ void lds_put(char* base, int plane_bytes, int idx, float x) {
-    if constexpr (Prec<TIn>::F32) {
-        reinterpret_cast<float*>(base)[idx] = x;
-    } else {
-        float r = x;
-#pragma unroll
-        for (int pl = 0; pl < NP; ++pl) {
-            const __bf16 hb = (__bf16)r;
-            reinterpret_cast<__bf16*>(base + pl * plane_bytes)[idx] = hb;
-            r -= (float)hb;
-        }
-    }
+// ds_read_b64_tr_b16: within each 16-lane group, lane m supplies the address of four
+// consecutive 16-bit elements M[m][0..3]; lane i receives M[4j + (i >> 2)][i & 3], j = 0..3.
+__device__ __forceinline__ bf16x4 lds_read_tr(const __bf16* p) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+    return __builtin_bit_cast(bf16x4, r);
 }
 
-// N (multiple of 4) consecutive values at element index idx (a multiple of 4).
-template <typename TIn, int NP, int N>
+// Fragment whose lane index is a plane column (K index down the rows): lane (g4, r16) gets
+// column col0 + r16 of rows row0 + 4*g4 + [0,4) (K slots 0..3) and row0 + 16 + 4*g4 + [0,4)
+// (slots 4..7).  Lane (g4, m) addresses row row0 + 4*g4 + (m >> 2), columns col0 + 4*(m & 3).
+template <int NP>
+__device__ __forceinline__ Split8<NP> lds_frag_tr(const char* base, int plane_bytes, int rs, int row0, int col0,
+                                                  int g4, int r16) {
+    Split8<NP> f;
+    const int off = (row0 + 4 * g4 + (r16 >> 2)) * rs + col0 + 4 * (r16 & 3);
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+        const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes) + off;
+        const bf16x4 a = lds_read_tr(p);
+        const bf16x4 b = lds_read_tr(p + 16 * rs);
+        f.p[pl] = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    }
+    return f;
+}
+
+// N (multiple of 4) consecutive values at element index idx (a multiple of 4), split into NP
+// bf16 planes.
+template <int NP, int N>
 __device__ __forceinline__ void lds_put_row(char* base, int plane_bytes, int idx, const float* x) {
-    if constexpr (Prec<TIn>::F32) {
+    float r[N];
 #pragma unroll
-        for (int c = 0; c < N; c += 4)
-            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(base) + idx + c) =
-                f32x4{x[c], x[c + 1], x[c + 2], x[c + 3]};
-    } else {
-        float r[N];
+    for (int j = 0; j < N; ++j) r[j] = x[j];
 #pragma unroll
-        for (int j = 0; j < N; ++j) r[j] = x[j];
+    for (int pl = 0; pl < NP; ++pl) {
 #pragma unroll
-        for (int pl = 0; pl < NP; ++pl) {
+        for (int c = 0; c < N; c += 4) {
+            bf16x4 hb;
 #pragma unroll
-            for (int c = 0; c < N; c += 4) {
-                bf16x4 hb;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    hb[j] = (__bf16)r[c + j];
-                    r[c + j] -= (float)hb[j];
-                }
-                *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(base + pl * plane_bytes) + idx + c) = hb;
+            for (int j = 0; j < 4; ++j) {
+                hb[j] = (__bf16)r[c + j];
+                if (pl + 1 < NP) r[c + j] -= (float)hb[j];
             }
+            *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(base + pl * plane_bytes) + idx + c) = hb;
         }
     }
 }
@@ -208,19 +216,21 @@ struct Vec {
     uint32_t w[W];
 };
 
+// Raw buffer load of one Vec at byte offset voff + soff of the resource; bytes at or past the
+// resource's num_records read as zero without touching memory.
 template <typename T, int N>
-__device__ __forceinline__ void vec_load(Vec<T, N>& v, const T* p) {
+__device__ __forceinline__ void vec_load(Vec<T, N>& v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
     if constexpr (Vec<T, N>::BYTES % 16 == 0) {
 #pragma unroll
         for (int i = 0; i < Vec<T, N>::BYTES / 16; ++i) {
-            const uint4 u = reinterpret_cast<const uint4*>(p)[i];
-            v.w[4 * i] = u.x; v.w[4 * i + 1] = u.y; v.w[4 * i + 2] = u.z; v.w[4 * i + 3] = u.w;
+            const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * i, soff, 0);
+            v.w[4 * i] = u[0]; v.w[4 * i + 1] = u[1]; v.w[4 * i + 2] = u[2]; v.w[4 * i + 3] = u[3];
         }
     } else if constexpr (Vec<T, N>::BYTES == 8) {
-        const uint2 u = *reinterpret_cast<const uint2*>(p);
-        v.w[0] = u.x; v.w[1] = u.y;
+        const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+        v.w[0] = u[0]; v.w[1] = u[1];
     } else {
-        v.w[0] = *reinterpret_cast<const uint32_t*>(p);
+        v.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
     }
 }
 
@@ -254,39 +264,37 @@ __device__ __forceinline__ float lane_value(float x, int lane) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
 }
 
-__device__ __forceinline__ int64_t uniform_i64(int64_t x) {
-    const uint64_t u = (uint64_t)x;
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
-// Addressing of one token-major input under the stage-1 lane mapping: a wave-uniform base
-// (token 0 of the sequence, head h) plus a 32-bit per-lane byte offset (token 4*tg of a chunk,
-// first column of the lane), so a full chunk's loads need no per-lane 64-bit arithmetic.
-// The host guarantees 64 * token stride + row bytes < 2^31.
+// Addressing of one token-major input under the stage-1 lane mapping.  Each chunk gets a buffer
+// resource based at its first row (wave-uniform) whose num_records ends at the tensor's extent,
+// so rows past the end read as zero; lanes add a 32-bit offset (token 4*tg, their first column)
+// and the scalar offset selects token j of the four.  A resource with num_records 0 turns a
+// load into a no-op, which keeps the number of loads per chunk fixed.  The host guarantees
+// 64 * token stride + row bytes < 2^31.
 struct TokAddr {
-    const char* base;
-    int64_t st;    // token stride, bytes (uniform)
-    int32_t lane;  // 4*tg*st + col*sizeof(T)
+    const char* p0;  // token 0 of the sequence, head h (uniform)
+    int64_t rem;     // bytes readable from p0 (uniform)
+    int32_t st;      // token stride, bytes (uniform)
+    int32_t lane;    // 4*tg*st + col*sizeof(T)
 };
 
 template <typename T>
 __device__ __forceinline__ TokAddr tok_addr(const TokTensor& x, const Work& wk, int64_t h, int tg, int col) {
     TokAddr r;
     const int64_t es = (int64_t)sizeof(T);
-    r.base = reinterpret_cast<const char*>(x.p) + uniform_i64((wk.b * x.sb + wk.row0 * x.st + h * x.sh) * es);
-    r.st = x.st * es;
-    r.lane = (int32_t)(4 * tg * r.st + col * es);
+    const int64_t base = uniform_i64((wk.b * x.sb + wk.row0 * x.st + h * x.sh) * es);
+    r.p0 = reinterpret_cast<const char*>(x.p) + base;
+    r.rem = x.extent - base;
+    r.st = (int32_t)(x.st * es);
+    r.lane = 4 * tg * r.st + col * (int32_t)es;
     return r;
 }
 
-// Row tc + 4*tg + j of a full chunk, or tc + min(4*tg + j, nv - 1) of a partial one.
-template <typename T, bool FULL>
-__device__ __forceinline__ const T* tok_ptr(const TokAddr& a, int64_t tc, int j, int tg, int nv) {
-    if (FULL) return reinterpret_cast<const T*>(a.base + (tc + j) * a.st + a.lane);
-    const int tl = min(4 * tg + j, nv - 1);
-    return reinterpret_cast<const T*>(a.base + tc * a.st + a.lane + (int64_t)(tl - 4 * tg) * a.st);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const TokAddr& a, int64_t tc, bool valid) {
+    const int64_t off = tc * a.st;
+    int64_t n = a.rem - off;
+    n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(a.p0) + off, (short)0, valid ? (int)n : 0,
+                                             0x00020000);
 }
 
 struct ChunkAddr {
@@ -316,24 +324,22 @@ struct ChunkIn {
     Vec<TIn, 4> v[4];
 };
 
-template <bool OUT, bool FULL, typename TIn, typename TG, int DL>
-__device__ __forceinline__ void chunk_load_rows(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, int nv,
-                                                int tg) {
+// Inputs of the chunk starting at token tc (valid: false issues the same loads as no-ops).
+// In a partial chunk the rows past its end are other tokens of the tensor or zeros; stage 1
+// zeroes them.
+template <bool OUT, typename TIn, typename TG, int DL>
+__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, bool valid) {
+    __amdgpu_buffer_rsrc_t rq;
+    if (OUT) rq = chunk_rsrc(ad.q, tc, valid);
+    const __amdgpu_buffer_rsrc_t rk = chunk_rsrc(ad.k, tc, valid), rg = chunk_rsrc(ad.g, tc, valid),
+                                 rv = chunk_rsrc(ad.v, tc, valid);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        if (OUT) vec_load(c.q[j], tok_ptr<TIn, FULL>(ad.q, tc, j, tg, nv));
-        vec_load(c.k[j], tok_ptr<TIn, FULL>(ad.k, tc, j, tg, nv));
-        vec_load(c.g[j], tok_ptr<TG, FULL>(ad.g, tc, j, tg, nv));
-        vec_load(c.v[j], tok_ptr<TIn, FULL>(ad.v, tc, j, tg, nv));
+        if (OUT) vec_load(c.q[j], rq, ad.q.lane, j * ad.q.st);
+        vec_load(c.k[j], rk, ad.k.lane, j * ad.k.st);
+        vec_load(c.g[j], rg, ad.g.lane, j * ad.g.st);
+        vec_load(c.v[j], rv, ad.v.lane, j * ad.v.st);
     }
-}
-
-// Inputs of the chunk starting at token tc with nv valid tokens; in a partial chunk every lane
-// still reads a row inside the chunk (rows past nv repeat the last one and are zeroed later).
-template <bool OUT, typename TIn, typename TG, int DL>
-__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, int nv, int tg) {
-    if (nv == CHUNK) chunk_load_rows<OUT, true>(c, ad, tc, nv, tg);
-    else chunk_load_rows<OUT, false>(c, ad, tc, nv, tg);
 }
 
 // x[j][i] = element i of token j, zeroed for tokens at or past nv (partial chunks only).
@@ -439,12 +445,6 @@ __device__ __forceinline__ void chunk_suffix(const float (&g)[4][DL], float (&X)
     }
 }
 
-// Store 4 consecutive tokens (one lane's) of one row of a [row][token] plane set.
-template <typename TIn, int NP>
-__device__ __forceinline__ void lds_put_tok4(char* base, int plane_bytes, int idx, const float (&x)[4]) {
-    lds_put_row<TIn, NP, 4>(base, plane_bytes, idx, x);
-}
-
 // ---------------------------------------------------------------------------------------
 // Token-by-token update of one wave's state columns (large decay spans, unclamped tail).
 // S tile db holds S[16*db + 4*g4 + i][c0 + r16].
@@ -510,9 +510,8 @@ struct OutStep {
         const int dl0 = d0 + DL * row;  // first key dim of this lane in stage 1
         char* sQT = smem + L::OFF_QT;
         char* sKT = smem + L::OFF_KT;
-        char* sKTT = smem + L::OFF_KTT;
         char* sAT = smem + L::OFF_AT;
-        char* sVP = smem + L::OFF_VP + wave * PR::VPL * L::VPP;
+        char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
         float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
         float* sEG = sEM + DK;
         int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
@@ -550,57 +549,21 @@ struct OutStep {
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int i = 0; i < DL; ++i) x[j][i] *= G[j][i];
-                lds_put_row<TIn, PR::DPL, DL>(sQT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
+                lds_put_row<NS, DL>(sQT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
-            // Kt rows and Kt^T (split once, both layouts)
+            // Kt rows (stage 2 reads them as rows, the state update through the transposed read)
             chunk_float(cur.k, x, tg, nv);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int i = 0; i < DL; ++i) x[j][i] *= __builtin_amdgcn_rcpf(G[j][i]);
-            if constexpr (PR::F32) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) lds_put_row<TIn, 1, DL>(sKT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
-#pragma unroll
-                for (int i = 0; i < DL; ++i)
-                    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(sKTT) + (dl0 + i) * L::TS + 4 * tg) =
-                        f32x4{x[0][i], x[1][i], x[2][i], x[3][i]};
-            } else {
-                __bf16 hi[4][DL], lo[4][DL];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int i = 0; i < DL; ++i) {
-                        hi[j][i] = (__bf16)x[j][i];
-                        lo[j][i] = (__bf16)(x[j][i] - (float)hi[j][i]);
-                    }
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int c = 0; c < DL; c += 4) {
-                        const int idx = (4 * tg + j) * L::RS + dl0 + c;
-                        *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKT) + idx) =
-                            bf16x4{hi[j][c], hi[j][c + 1], hi[j][c + 2], hi[j][c + 3]};
-                        *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKT + L::ROWP) + idx) =
-                            bf16x4{lo[j][c], lo[j][c + 1], lo[j][c + 2], lo[j][c + 3]};
-                    }
-#pragma unroll
-                for (int i = 0; i < DL; ++i) {
-                    const int idx = (dl0 + i) * L::TS + 4 * tg;
-                    *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKTT) + idx) =
-                        bf16x4{hi[0][i], hi[1][i], hi[2][i], hi[3][i]};
-                    *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(sKTT + L::KTTP) + idx) =
-                        bf16x4{lo[0][i], lo[1][i], lo[2][i], lo[3][i]};
-                }
+                lds_put_row<NS, DL>(sKT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
-            // V: columns c0 + 4*row + c, tokens 4*tg .. 4*tg+3 -> [column][token]
+            // V rows: tokens 4*tg + j, this wave's columns 4*row .. 4*row+3
             float vx[4][4];
             chunk_float(cur.v, vx, tg, nv);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float col[4] = {vx[0][c], vx[1][c], vx[2][c], vx[3][c]};
-                lds_put_row<TIn, PR::VPL, 4>(sVP, L::VPP, (4 * row + c) * L::TS + 4 * tg, col);
-            }
+            for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
         after_inputs();
         __syncthreads();
@@ -618,8 +581,8 @@ struct OutStep {
                 f32x4 acc = zero4();
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    const Split8<NS> kf = lds_frag<TIn, NS>(sKT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
-                    const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                    const Split8<NS> kf = lds_frag<NS>(sKT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
+                    const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
                     acc = mfma_split<NS, NS, NS>(kf, qf, acc);
                 }
                 if (sb == tb) {  // row = key 4*g4 + j, column = query r16
@@ -627,14 +590,14 @@ struct OutStep {
                     for (int j = 0; j < 4; ++j) acc[j] = (4 * g4 + j > r16) ? 0.f : acc[j];
                 }
                 const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-                lds_put_row<TIn, PR::DPL, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
+                lds_put_row<NS, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
             }
             __syncthreads();
 
             // ---------------- stage 3: outputs and state for columns [c0, c0+16) ------------
             Split8<NX> vf[2];
 #pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag<TIn, NX>(sVP, L::VPP, L::TS, r16, 32 * k2, g4);
+            for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
             f32x4 Ot[4];
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) Ot[tb] = zero4();
@@ -651,7 +614,7 @@ struct OutStep {
                 const Split8<NS> sf = split8<NS>(x);
 #pragma unroll
                 for (int tb = 0; tb < 4; ++tb) {
-                    const Split8<NS> qf = lds_frag<TIn, NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                    const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
                     Ot[tb] = mfma_split<NS, NS, NS>(sf, qf, Ot[tb]);
                 }
             }
@@ -664,50 +627,16 @@ struct OutStep {
                     const bool has_hi = 2 * k2 + 1 <= tb;
                     const int i1 = has_hi ? tile_index(2 * k2 + 1, tb) : i0;
                     Split8<NS> af;
-                    if constexpr (PR::F32) {
-                        const float* p = reinterpret_cast<const float*>(sAT);
-                        const f32x4 lo = *reinterpret_cast<const f32x4*>(p + (i0 * 64 + lane) * 4);
-                        f32x4 hi = *reinterpret_cast<const f32x4*>(p + (i1 * 64 + lane) * 4);
-                        if (!has_hi) hi = zero4();
-                        float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        af = split8<NS>(x);
-                    } else {
 #pragma unroll
-                        for (int pl = 0; pl < NS; ++pl) {
-                            const __bf16* p = reinterpret_cast<const __bf16*>(sAT + pl * L::ATP);
-                            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
-                            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
-                            const __bf16 z = (__bf16)0.f;
-                            af.p[pl] = has_hi ? bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}
-                                              : bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
-                        }
+                    for (int pl = 0; pl < NS; ++pl) {
+                        const __bf16* p = reinterpret_cast<const __bf16*>(sAT + pl * L::ATP);
+                        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
+                        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
+                        const __bf16 z = (__bf16)0.f;
+                        af.p[pl] = has_hi ? bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}
+                                          : bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
                     }
                     Ot[tb] = mfma_split<NX, NS, NS>(vf[k2], af, Ot[tb]);
-                }
-            }
-            // Lane (g4, r16) holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3].  Stage it, 32
-            // tokens at a time, through this wave's slice of the Kt row planes (free after stage
-            // 2), and store with the four lanes of a quad covering one token's 16 columns.
-            {
-                float* sO = reinterpret_cast<float*>(smem + L::OFF_KT) + wave * (32 * L::OS);
-                const int es = dt_size(a.o_dt);
-                const int64_t ost = a.o_st * es;
-                char* obase = reinterpret_cast<char*>(a.o) +
-                              uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
-                const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);  // token within 16
-                const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-#pragma unroll
-                    for (int k = 0; k < 2; ++k)
-                        *reinterpret_cast<f32x4*>(sO + (16 * k + r16) * L::OS + 4 * g4) = Ot[2 * half + k];
-#pragma unroll
-                    for (int k = 0; k < 2; ++k) {
-                        const int t = 32 * half + 16 * k + tq;
-                        const f32x4 x = *reinterpret_cast<const f32x4*>(sO + (16 * k + tq) * L::OS + 4 * q);
-                        if (t < nv)
-                            store4_dt(obase + (32 * half + 16 * k) * ost + olane, a.o_dt, x[0], x[1], x[2], x[3]);
-                    }
                 }
             }
 #pragma unroll
@@ -715,13 +644,32 @@ struct OutStep {
                 f32x4 P = zero4();
 #pragma unroll
                 for (int k2 = 0; k2 < 2; ++k2) {
-                    const Split8<NS> kf = lds_frag<TIn, NS>(sKTT, L::KTTP, L::TS, 16 * db + r16, 32 * k2, g4);
+                    const Split8<NS> kf = lds_frag_tr<NS>(sKT, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
                     P = mfma_split<NS, NX, NS>(kf, vf[k2], P);
                 }
                 const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
                 const f32x4 eg = *reinterpret_cast<const f32x4*>(sEG + 16 * db + 4 * g4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) S[db][i] = eg[i] * S[db][i] + em[i] * P[i];
+            }
+            // Lane (g4, r16) holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3].  Stage it, 16
+            // tokens at a time, through this wave's V planes (only this wave reads them, and vf
+            // already holds them), then store with the four lanes of a quad covering one token's
+            // 16 columns.
+            {
+                float* sO = reinterpret_cast<float*>(sVP);
+                const int es = dt_size(a.o_dt);
+                const int64_t ost = a.o_st * es;
+                char* obase = reinterpret_cast<char*>(a.o) +
+                              uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
+                const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);  // token within 16
+                const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    *reinterpret_cast<f32x4*>(sO + r16 * L::OS + 4 * g4) = Ot[tb];
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(sO + tq * L::OS + 4 * q);
+                    if (16 * tb + tq < nv) store4_dt(obase + 16 * tb * ost + olane, a.o_dt, x[0], x[1], x[2], x[3]);
+                }
             }
         }
         __syncthreads();  // the next chunk rewrites LDS
@@ -744,17 +692,21 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     ChunkIn<TIn, TG, DL> A, B;
-    chunk_load<true>(A, ad, tok(0), chunk_nv(0), tg);
-    if (nch > 1) chunk_load<true>(B, ad, tok(1), chunk_nv(1), tg);
-    for (int64_t c = 0; c < nch; c += 2) {
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem, [&] {
-            if (c + 2 < nch) chunk_load<true>(A, ad, tok(c + 2), chunk_nv(c + 2), tg);
-        });
-        if (c + 1 >= nch) break;
-        St::run(a, wk, h, tok(c + 1), chunk_nv(c + 1), B, S, smem, [&] {
-            if (c + 3 < nch) chunk_load<true>(B, ad, tok(c + 3), chunk_nv(c + 3), tg);
-        });
+    // Loads must issue in chunk order on every path into the loop (A before B here, as in the
+    // loop body), or the wait-count pass falls back to waiting for both sets.
+    chunk_load<true>(A, ad, tok(0), true);
+    __builtin_amdgcn_sched_barrier(0);
+    chunk_load<true>(B, ad, tok(1), nch > 1);
+    // Pairs of chunks, then an odd last one: the loop has a single exit, so every path into a
+    // chunk has issued the same loads in the same order and the waits stay per set.
+    const int64_t last_pair = nch & ~(int64_t)1;
+    for (int64_t c = 0; c < last_pair; c += 2) {
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem,
+                [&] { chunk_load<true>(A, ad, tok(c + 2), c + 2 < nch); });
+        St::run(a, wk, h, tok(c + 1), chunk_nv(c + 1), B, S, smem,
+                [&] { chunk_load<true>(B, ad, tok(c + 3), c + 3 < nch); });
     }
+    if (nch & 1) St::run(a, wk, h, tok(last_pair), chunk_nv(last_pair), A, S, smem, [] {});
 }
 
 // ---------------------------------------------------------------------------------------
@@ -778,8 +730,8 @@ struct StateStep {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int dl0 = wave * DPW + DL * row;
-        char* sKTT = smem + L::OFF_KTT;
-        char* sVP = smem + L::OFF_VP + wave * PR::VPL * L::VPP;
+        char* sKW = smem + L::OFF_KT;  // exp-weighted k rows
+        char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
         {
             float G[4][DL], GC[DL], x[4][DL];
             chunk_float(cur.g, x, tg, nv);
@@ -794,33 +746,28 @@ struct StateStep {
             chunk_suffix<DL>(G, X, GC, lane);
             chunk_float(cur.k, x, tg, nv);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int i = 0; i < DL; ++i) x[j][i] *= fast_exp(Gseg[i] + X[j][i]);
-#pragma unroll
-            for (int i = 0; i < DL; ++i) {
-                Gseg[i] += GC[i];
-                const float col[4] = {x[0][i], x[1][i], x[2][i], x[3][i]};
-                lds_put_row<TIn, PR::DPL, 4>(sKTT, L::KTTP, (dl0 + i) * L::TS + 4 * tg, col);
+                lds_put_row<NS, DL>(sKW, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
+#pragma unroll
+            for (int i = 0; i < DL; ++i) Gseg[i] += GC[i];
             float vx[4][4];
             chunk_float(cur.v, vx, tg, nv);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const float col[4] = {vx[0][c], vx[1][c], vx[2][c], vx[3][c]};
-                lds_put_row<TIn, PR::VPL, 4>(sVP, L::VPP, (4 * row + c) * L::TS + 4 * tg, col);
-            }
+            for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
         after_inputs();
         __syncthreads();
         Split8<NX> vf[2];
 #pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag<TIn, NX>(sVP, L::VPP, L::TS, r16, 32 * k2, g4);
+        for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int k2 = 0; k2 < 2; ++k2) {
-                const Split8<NS> kf = lds_frag<TIn, NS>(sKTT, L::KTTP, L::TS, 16 * db + r16, 32 * k2, g4);
+                const Split8<NS> kf = lds_frag_tr<NS>(sKW, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
                 Lst[db] = mfma_split<NS, NX, NS>(kf, vf[k2], Lst[db]);
             }
         __syncthreads();  // the next chunk rewrites LDS
@@ -841,17 +788,17 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     ChunkIn<TIn, TG, DL> A, B;
-    chunk_load<false>(A, ad, tok(nch - 1), chunk_nv(nch - 1), tg);
-    if (nch > 1) chunk_load<false>(B, ad, tok(nch - 2), chunk_nv(nch - 2), tg);
-    for (int64_t c = nch - 1; c >= 0; c -= 2) {
-        St::run(a, wk, tok(c), chunk_nv(c), A, Lst, Gseg, smem, [&] {
-            if (c >= 2) chunk_load<false>(A, ad, tok(c - 2), chunk_nv(c - 2), tg);
-        });
-        if (c < 1) break;
-        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, Lst, Gseg, smem, [&] {
-            if (c >= 3) chunk_load<false>(B, ad, tok(c - 3), chunk_nv(c - 3), tg);
-        });
+    chunk_load<false>(A, ad, tok(nch - 1), true);
+    __builtin_amdgcn_sched_barrier(0);  // issue order A, B on every path (see segment_walk)
+    chunk_load<false>(B, ad, tok(nch - 2), nch > 1);
+    // pairs of chunks from the end, then chunk 0 if nch is odd (single-exit loop, as in segment_walk)
+    for (int64_t c = nch - 1; c >= 1; c -= 2) {
+        St::run(a, wk, tok(c), chunk_nv(c), A, Lst, Gseg, smem,
+                [&] { chunk_load<false>(A, ad, tok(c - 2), c >= 2); });
+        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, Lst, Gseg, smem,
+                [&] { chunk_load<false>(B, ad, tok(c - 3), c >= 3); });
     }
+    if (nch & 1) St::run(a, wk, tok(0), chunk_nv(0), A, Lst, Gseg, smem, [] {});
 }
 
 // S tile db of wave w: element i is S[16*db + 4*g4 + i][16*w + r16].
@@ -940,6 +887,12 @@ bool prefill_shape_supported(int Dk, int Dv) {
     return (Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128) || (Dk == 128 && Dv == 64);
 }
 
+// fp32 I/O keeps three bf16 parts of every LDS operand: at (128, 128) they exceed the 160 KB LDS,
+// so that pair is served as two 64-column halves by the caller.
+bool prefill_dtype_supported(int Dk, int Dv, int io_dt) {
+    return prefill_shape_supported(Dk, Dv) && !(io_dt == DT_F32 && Dk == 128 && Dv == 128);
+}
+
 template <typename TIn, typename TG>
 static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
     const dim3 grid((unsigned)n_work, (unsigned)a.H);
@@ -951,7 +904,9 @@ static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with
         return hipGetLastError();                                                                       \
     }
     TRIUNE_SEG_CASE(64, 64)
-    TRIUNE_SEG_CASE(128, 128)
+    if constexpr (!Prec<TIn>::F32) {
+        TRIUNE_SEG_CASE(128, 128)
+    }
     TRIUNE_SEG_CASE(32, 32)
     TRIUNE_SEG_CASE(128, 64)
 #undef TRIUNE_SEG_CASE

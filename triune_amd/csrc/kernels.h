@@ -8,6 +8,7 @@ namespace triune {
 struct TokTensor {
     const void* p;
     int64_t sb, st, sh;  // element strides: batch, token, head (innermost stride is 1)
+    int64_t extent;      // bytes readable from p (one past the last element)
 };
 
 struct PrefillParams {
@@ -85,6 +86,7 @@ hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_d
 hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream);
 bool prefill_shape_supported(int Dk, int Dv);
+bool prefill_dtype_supported(int Dk, int Dv, int io_dt);
 int gla_seg_output_blocks_per_cu(int Dk, int Dv);
 
 }  // namespace triune
