@@ -23,10 +23,12 @@
 //
 // One workgroup of NW = Dv/16 waves handles a (segment, head).  Per chunk:
 //   stage 1  wave w (each lane 4 tokens x DPW/4 dims): cumulative decay, factors and split
-//            Qt/Kt for key dims [w*DPW, (w+1)*DPW) -> LDS (row planes for Qt/Kt, a [dim][token]
-//            plane for Kt^T); its own 16 value columns of V -> LDS ([column][token] plane)
+//            Qt/Kt for key dims [w*DPW, (w+1)*DPW) -> token-major LDS planes; its own 16 value
+//            columns of V -> a token-major plane of its own
 //   stage 2  the ten 16x16 causal tiles of A^T, spread over the waves -> LDS
-//   stage 3  wave w: O^T and the state update for value columns [16w, 16w+16)
+//   stage 3  wave w: O^T and the state update for value columns [16w, 16w+16); fragments with
+//            the token as K index (Kt^T, V) come from the token-major planes through the
+//            transposed LDS read
 // The next chunk's inputs are loaded into registers while the current chunk is processed.
 // Chunks whose key-dim decay span exceeds SPAN_MAX (or that hold the reference's unclamped
 // 1-token tail) run token by token on the same state registers.
@@ -676,9 +678,7 @@ struct OutStep {
     }
 };
 
-// Outputs of one segment from its carried-in state S (K3).  Chunk inputs alternate between two
-// register sets; a set is refilled (two chunks ahead) as soon as stage 1 has consumed it, so two
-// chunks of loads are in flight while stages 2-3 run.
+// Outputs of one segment from its carried-in state S (K3).
 template <typename TIn, typename TG, int DK, int DV>
 __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
     using St = OutStep<TIn, TG, DK, DV>;
@@ -691,22 +691,13 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
         return (int)(r < CHUNK ? r : CHUNK);
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
-    ChunkIn<TIn, TG, DL> A, B;
-    // Loads must issue in chunk order on every path into the loop (A before B here, as in the
-    // loop body), or the wait-count pass falls back to waiting for both sets.
+    // One register set: stage 1 consumes it and the next chunk's loads refill it at once, so they
+    // are in flight during stages 2-3 (registers go to occupancy instead of a second set).
+    ChunkIn<TIn, TG, DL> A;
     chunk_load<true>(A, ad, tok(0), true);
-    __builtin_amdgcn_sched_barrier(0);
-    chunk_load<true>(B, ad, tok(1), nch > 1);
-    // Pairs of chunks, then an odd last one: the loop has a single exit, so every path into a
-    // chunk has issued the same loads in the same order and the waits stay per set.
-    const int64_t last_pair = nch & ~(int64_t)1;
-    for (int64_t c = 0; c < last_pair; c += 2) {
+    for (int64_t c = 0; c < nch; ++c)
         St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem,
-                [&] { chunk_load<true>(A, ad, tok(c + 2), c + 2 < nch); });
-        St::run(a, wk, h, tok(c + 1), chunk_nv(c + 1), B, S, smem,
-                [&] { chunk_load<true>(B, ad, tok(c + 3), c + 3 < nch); });
-    }
-    if (nch & 1) St::run(a, wk, h, tok(last_pair), chunk_nv(last_pair), A, S, smem, [] {});
+                [&] { chunk_load<true>(A, ad, tok(c + 1), c + 1 < nch); });
 }
 
 // ---------------------------------------------------------------------------------------

@@ -91,10 +91,58 @@ __global__ __launch_bounds__(SCAN_TPB) void recurrent_scan_kernel(ScanParams a) 
     if (a.fin) st4_dt(a.fin, a.fin_dt, o * a.f_so + h * a.f_sh + e, s);
 }
 
+// The prefill's carry over segments: fp32 kv and s_all (the same buffer), fp32 log-decay, fp32
+// init / fin.  All U loads of a block of steps are issued before the dependent chain runs, so a
+// typical sequence (at most U segments) pays one memory latency; the chain itself is four
+// independent FMA lanes per step with exp on the hardware exp2.
+template <int U>
+__global__ __launch_bounds__(SCAN_TPB) void seg_scan_f32_kernel(ScanParams a) {
+    const int64_t DD = (int64_t)a.Dk * a.Dv;
+    const int64_t e = ((int64_t)blockIdx.x * SCAN_TPB + threadIdx.x) * 4;
+    if (e >= DD) return;
+    const int64_t h = blockIdx.y, o = blockIdx.z;
+    const int row = (int)(e / a.Dv);
+    int64_t n0 = 0, N = a.N;
+    if (a.seg_off) {
+        n0 = a.seg_off[o];
+        N = (int64_t)a.seg_off[o + 1] - n0;
+    }
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.init) s = *reinterpret_cast<const float4*>(a.init + o * a.i_so + h * a.i_sh + e);
+    float* kv = const_cast<float*>(reinterpret_cast<const float*>(a.kv)) + o * a.kv_so + h * a.kv_sh + e;
+    const float* dec = reinterpret_cast<const float*>(a.dec) + o * a.d_so + h * a.d_sh + row;
+    for (int64_t n = 0; n < N; n += U) {
+        float4 x[U];
+        float d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = n0 + (n + u < N ? n + u : N - 1);
+            x[u] = *reinterpret_cast<const float4*>(kv + i * a.kv_sn);
+            d[u] = dec[i * a.d_sn];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (n + u < N) {
+                const float dd = fast_exp(d[u]);
+                *reinterpret_cast<float4*>(kv + (n0 + n + u) * a.kv_sn) = s;  // exclusive prefix
+                s.x = s.x * dd + x[u].x;
+                s.y = s.y * dd + x[u].y;
+                s.z = s.z * dd + x[u].z;
+                s.w = s.w * dd + x[u].w;
+            }
+        }
+    }
+    if (a.fin) *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.fin) + o * a.f_so + h * a.f_sh + e) = s;
+}
+
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream) {
     const int64_t DD = (int64_t)a.Dk * a.Dv;
     dim3 grid((unsigned)((DD / 4 + SCAN_TPB - 1) / SCAN_TPB), (unsigned)a.H, (unsigned)a.n_outer);
-    hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(SCAN_TPB), 0, stream, a);
+    const bool prefill_carry = a.kv_dt == DT_F32 && a.dec_dt == DT_F32 && a.dec_is_log && a.s_all == a.kv &&
+                               a.sa_dt == DT_F32 && a.sa_so == a.kv_so && a.sa_sh == a.kv_sh &&
+                               a.sa_sn == a.kv_sn && !a.init_any && (!a.fin || a.fin_dt == DT_F32);
+    if (prefill_carry) hipLaunchKernelGGL(seg_scan_f32_kernel<24>, grid, dim3(SCAN_TPB), 0, stream, a);
+    else hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(SCAN_TPB), 0, stream, a);
     return hipGetLastError();
 }
 
