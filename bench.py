@@ -118,6 +118,38 @@ def bench_decode(steps_total, dev, n_bufs=12):
     }
 
 
+def bench_gdn(dev, reps=3):
+    """Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta and decay)."""
+    from triune_amd import fast_chunk_gated_deltanet
+    from triune_amd.workloads import config3
+
+    q, k, v, g, beta = (x.to(dev) for x in config3())
+    fn = lambda: fast_chunk_gated_deltanet(q, k, v, g, beta=beta)  # noqa: E731
+    fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    B, T = q.shape[0], q.shape[1]
+    return {"workload": "Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16)",
+            "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1)}
+
+
+def bench_varlen(dev, reps=5):
+    """Packed ragged GLA prefill, config 4 (32 sequences of 128..8192 tokens, H=12, D=128, bf16)."""
+    from triune_amd import fast_chunk_gla_varlen
+    from triune_amd.workloads import config4
+
+    q, k, v, g, cu, s0 = config4()
+    q, k, v, g, cu, s0 = (x.to(dev) for x in (q, k, v, g, cu, s0))
+    out = torch.empty_like(v)
+    fn = lambda: fast_chunk_gla_varlen(q, k, v, g, cu, initial_state=s0, out=out)  # noqa: E731
+    fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    n_tok = q.shape[1]
+    return {"workload": f"varlen GLA prefill, config 4 ({cu.numel() - 1} sequences, {n_tok} tokens, H=12, D=128, bf16)",
+            "ms": round(ms, 4), "tok_s": round(n_tok / (ms * 1e-3), 1)}
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's PyTorch CPU scan, restated (oracle/ref_port.py), on the config-1 workload
     itself (B=4, H=6, T=16384, D=64; bf16 inputs widened to fp32, as the CPU path computes in
@@ -176,6 +208,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config-3 (GDN) and config-4 (varlen) lines")
     ap.add_argument(
         "--copy-probe",
         type=int,
@@ -204,6 +237,7 @@ def main():
         return
     pre = bench_prefill(args.steps, args.warmup, dev)
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
+    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev)}
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,
@@ -236,7 +270,7 @@ def main():
             "unit": "GB/s",
             "frac": round(pre["gbs"] / HBM_PEAK_GBS, 4),
             "traffic": _traffic_from_profiles(),
-            "kernel": "prefill pass = gla_seg_state + recurrent_scan + gla_seg_output (event-timed together)",
+            "kernel": "prefill pass = gla_seg_state + seg_scan_f32 + gla_seg_output (event-timed together)",
             "alg_bytes_per_pass": pre["alg_bytes"],
             "mfma_alg_tflops": round(pre["tflops"], 2),
             "mfma_alg_frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
@@ -259,6 +293,7 @@ def main():
                 "alg_bytes_per_step": dec["step_bytes"],
             },
         }
+    line.update(extra)
     print(json.dumps(line), flush=True)
 
 
