@@ -29,6 +29,7 @@
  *   triune_hip_gdn_prefill         <- fast_chunk_gated_deltanet, triune/kernels/fast_gla.py:839-904,
  *                                     with _triton_gated_deltanet_fwd (fast_gla.py:479-550) and
  *                                     fast_recurrent_gated_deltanet (fast_gla.py:781-836)
+ *   triune_hip_gdn_prefill_chunked <- the same operator (fast_gla.py:839-904), chunked form
  */
 #ifndef TRIUNE_HIP_H
 #define TRIUNE_HIP_H
@@ -140,6 +141,20 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
                            const void* beta, int beta_dtype, int beta_kind, const int64_t* strides, const float* s0,
                            void* o, int o_dtype, float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
                            void* stream);
+
+/* The same Gated DeltaNet forward in chunked WY/UT form (64-token chunks, MFMA, segment-parallel):
+ * same arguments and results as triune_hip_gdn_prefill, plus a workspace of at least
+ * triune_hip_gdn_prefill_chunked_workspace_size(B, T, H, Dk, Dv) bytes (16-byte aligned; 0 =
+ * unsupported sizes).  Supported: (Dk, Dv) == (64, 64); beta_kind NONE, HEAD (any dtype) or
+ * KEY (fp32, [B, T, H, Dk] with the strides given for beta); TRIUNE_BETA_VALUE returns
+ * TRIUNE_ERR_SHAPE (use triune_hip_gdn_prefill).
+ * Replaces: fast_chunk_gated_deltanet (fast_gla.py:839-904) for T > 1. */
+size_t triune_hip_gdn_prefill_chunked_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv);
+int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                   int g_dtype, const void* beta, int beta_dtype, int beta_kind,
+                                   const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
+                                   int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
+                                   size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

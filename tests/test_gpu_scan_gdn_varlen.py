@@ -88,6 +88,32 @@ def test_gdn_config3_shape_bf16(dev):
     assert _err(s.cpu(), rs) <= 2e-3
 
 
+def test_gdn_chunked_multichunk_segments_bf16(dev):
+    """Chunked WY/UT path with several chunks per segment (24 (b, h) rows share the resident
+    slots) and a ragged tail: against the fp64 token-serial oracle."""
+    q, k, v, g, beta = config3(T=2000, B=4, H=6)
+    s0 = 0.1 * torch.randn(4, 6, 64, 64, generator=torch.Generator().manual_seed(7))
+    o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),
+                                     initial_state=s0.to(dev))
+    torch.cuda.synchronize()
+    ro, rs = O.gdn_fwd(q, k, v, g, beta, s0)
+    ref = torch.from_numpy(ro)
+    assert float((o.cpu().double() - ref).abs().max()) <= float(ref.abs().max()) * 2**-8 + 2e-3
+    assert _err(s.cpu(), rs) <= 2e-3
+
+
+def test_gdn_chunked_extreme_decay_tokenwise_chunks(dev):
+    """Chunks whose decay span exceeds the factored range run token by token in the chunked path."""
+    q, k, v, g, beta, s0 = _gdn_case(256, 64, "head", seed=11)
+    g = g.clone()
+    g[:, 64:128] = -1.0 - 20.0 * torch.rand(2, 64, 2, 64, generator=torch.Generator().manual_seed(2))
+    o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),
+                                     initial_state=s0.to(dev))
+    torch.cuda.synchronize()
+    ro, rs = O.gdn_fwd(q, k, v, g, beta, s0)
+    assert _err(o.cpu(), ro) <= 1e-4 and _err(s.cpu(), rs) <= 1e-4
+
+
 def test_gdn_single_token(dev):
     q, k, v, g, beta, s0 = _gdn_case(1, 64, "head", seed=5)
     o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),

@@ -58,6 +58,12 @@ def _bind(lib):
             [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _vp],
             _i,
         ),
+        "triune_hip_gdn_prefill_chunked_workspace_size": ([_i64, _i64, _i64, _i, _i], _sz),
+        "triune_hip_gdn_prefill_chunked": (
+            [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _vp, _sz,
+             _vp],
+            _i,
+        ),
     }
     for name, (argtypes, restype) in sig.items():
         fn = getattr(lib, name)
@@ -76,6 +82,8 @@ EXPORTS = (
     "triune_hip_gla_prefill_varlen",
     "triune_hip_recurrent_scan_fwd",
     "triune_hip_gdn_prefill",
+    "triune_hip_gdn_prefill_chunked_workspace_size",
+    "triune_hip_gdn_prefill_chunked",
 )
 
 

@@ -374,3 +374,115 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
 }
 
 }  // extern "C"
+
+namespace {
+
+// Chunked GDN: segments per sequence fill the resident output-kernel slots once.
+struct GdnPlan {
+    int64_t nseg, n_work;
+    size_t off_m, total;
+};
+
+GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H) {
+    static std::mutex mu;
+    static std::map<int, int64_t> slots_cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    int64_t slots;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        auto it = slots_cache.find(dev);
+        if (it == slots_cache.end()) {
+            int ncu = 0;
+            if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                ncu <= 0)
+                ncu = 256;
+            it = slots_cache.emplace(dev, (int64_t)ncu * gdn_seg_out_blocks_per_cu()).first;
+        }
+        slots = it->second;
+    }
+    GdnPlan p{};
+    const int64_t nchunks = (T + 63) / 64;
+    p.nseg = slots / (B * H);
+    if (p.nseg < 1) p.nseg = 1;
+    if (p.nseg > nchunks) p.nseg = nchunks;
+    p.n_work = B * p.nseg;
+    p.off_m = align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
+    p.total = p.off_m + align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t triune_hip_gdn_prefill_chunked_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv) {
+    if (B <= 0 || T <= 0 || H <= 0 || Dk != 64 || Dv != 64) return 0;
+    return plan_gdn(B, T, H).total;
+}
+
+int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                   int g_dtype, const void* beta, int beta_dtype, int beta_kind,
+                                   const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
+                                   int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
+    if (beta_kind != TRIUNE_BETA_NONE && beta_kind != TRIUNE_BETA_HEAD && beta_kind != TRIUNE_BETA_KEY)
+        return TRIUNE_ERR_SHAPE;
+    if (beta_kind != TRIUNE_BETA_NONE && !beta) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype) || !gate_dtype_ok(io_dtype, g_dtype) ||
+        (beta_kind != TRIUNE_BETA_NONE && !dtype_ok(beta_dtype)) ||
+        (beta_kind == TRIUNE_BETA_KEY && beta_dtype != TRIUNE_DT_F32))
+        return TRIUNE_ERR_DTYPE;
+    if (B < 0 || T < 0 || H <= 0 || Dk != 64 || Dv != 64) return TRIUNE_ERR_SHAPE;
+    if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
+        !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
+        !vec_ok(o, o_dtype, strides + 15, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
+        reinterpret_cast<uintptr_t>(s_final) % 16 || !tok_strides_ok(strides, io_dtype, g_dtype, o_dtype, Dk, Dv) ||
+        (beta_kind == TRIUNE_BETA_KEY && !vec_ok(beta, TRIUNE_DT_F32, strides + 12, 3)))
+        return TRIUNE_ERR_LAYOUT;
+    // o strides sit at 15..17 here (beta takes 12..14); tok_strides_ok reads o's token stride at 13
+    const int64_t ost[15] = {strides[0], strides[1], strides[2], strides[3], strides[4], strides[5],
+                             strides[6], strides[7], strides[8], strides[9], strides[10], strides[11],
+                             strides[15], strides[16], strides[17]};
+    if (!tok_strides_ok(ost, io_dtype, g_dtype, o_dtype, Dk, Dv)) return TRIUNE_ERR_LAYOUT;
+    hipStream_t st = (hipStream_t)stream;
+    if (B == 0) return TRIUNE_OK;
+    if (T == 0) {
+        if (!s_final) return TRIUNE_OK;
+        ScanParams sc{};  // N = 0: fin = init (or zero)
+        sc.kv = s_final; sc.kv_dt = DT_F32; sc.dec = s_final; sc.dec_dt = DT_F32;
+        sc.init = s0; sc.i_so = H * (int64_t)Dk * Dv; sc.i_sh = (int64_t)Dk * Dv;
+        sc.fin = s_final; sc.fin_dt = DT_F32; sc.f_so = sc.i_so; sc.f_sh = sc.i_sh;
+        sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = 0;
+        return launch_status(launch_recurrent_scan(sc, st));
+    }
+    const GdnPlan pl = plan_gdn(B, T, H);
+    if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
+    char* ws = reinterpret_cast<char*>(workspace);
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
+
+    PrefillParams a{};
+    fill_tok(a.q, q, strides + 0, B, T, H, Dk, io_dtype);
+    fill_tok(a.k, k, strides + 3, B, T, H, Dk, io_dtype);
+    fill_tok(a.v, v, strides + 6, B, T, H, Dv, io_dtype);
+    fill_tok(a.g, g, strides + 9, B, T, H, Dk, g_dtype);
+    a.o = o; a.o_sb = strides[15]; a.o_st = strides[16]; a.o_sh = strides[17];
+    a.g_dt = g_dtype; a.o_dt = o_dtype;
+    a.s0 = s0;
+    a.ws_state = reinterpret_cast<float*>(ws);
+    a.ws_m = reinterpret_cast<float*>(ws + pl.off_m);
+    a.n_seqs = B; a.H = H; a.T = T; a.Dk = Dk; a.Dv = Dv;
+    a.P = 0; a.nseg_dense = (int)pl.nseg; a.varlen = 0; a.flags = 0;
+    a.beta = beta; a.beta_dt = beta_dtype; a.beta_kind = beta_kind;
+    a.b_sb = strides[12]; a.b_st = strides[13]; a.b_sh = strides[14];
+    if (beta_kind == TRIUNE_BETA_KEY) fill_tok(a.kb, beta, strides + 12, B, T, H, Dk, TRIUNE_DT_F32);
+
+    hipError_t e = launch_gdn_seg_mn(a, pl.n_work, io_dtype, st);
+    if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    e = launch_gdn_seg_scan(a, s_final, st);
+    if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    return launch_status(launch_gdn_seg_out(a, pl.n_work, io_dtype, st));
+}
+
+}  // extern "C"

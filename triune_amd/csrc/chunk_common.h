@@ -1,0 +1,402 @@
+// chunk_common.h -- device pieces shared by the chunked prefill kernels (GLA, Gated DeltaNet):
+// segment work assignment, the stage-1 lane mapping and its loads, decay scans, bf16-part LDS
+// planes and MFMA fragment reads (internal to libtriune_hip).
+#pragma once
+
+#include <type_traits>
+
+#include "kernels.h"
+
+namespace triune {
+
+constexpr int CHUNK = 64;
+constexpr float SPAN_MAX = 64.f;
+constexpr int PAD = 4;  // row padding (elements) of LDS planes: spreads rows over banks
+
+struct Work {
+    int64_t seq, b, row0, t_begin, t_end, len;
+    int p;
+};
+
+// x is the same in every lane; say so to the compiler (scalar registers, scalar branches).
+__device__ __forceinline__ int64_t uniform_i64(int64_t x) {
+    const uint64_t u = (uint64_t)x;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ bool find_work(const PrefillParams& a, int64_t w, Work& wk) {
+    if (!a.varlen) {
+        const int64_t seq = w / a.nseg_dense;
+        if (seq >= a.n_seqs) return false;
+        wk.seq = seq;
+        wk.b = seq;
+        wk.row0 = 0;
+        wk.p = (int)(w - seq * a.nseg_dense);
+        wk.len = a.T;
+    } else {
+        const int64_t total = a.seg_off[a.n_seqs];
+        if (w >= total) return false;
+        int64_t lo = 0, hi = a.n_seqs - 1;  // largest seq with seg_off[seq] <= w
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if (a.seg_off[mid] <= w) lo = mid;
+            else hi = mid - 1;
+        }
+        wk.seq = lo;
+        wk.b = 0;
+        wk.row0 = a.cu[lo];
+        wk.p = (int)(w - a.seg_off[lo]);
+        wk.len = (int64_t)a.cu[lo + 1] - (int64_t)a.cu[lo];
+    }
+    if (!a.varlen) {  // dense: nseg near-equal segments (chunk counts differ by at most one)
+        const int64_t nch = (wk.len + CHUNK - 1) / CHUNK;
+        wk.t_begin = (int64_t)wk.p * nch / a.nseg_dense * CHUNK;
+        wk.t_end = (int64_t)(wk.p + 1) * nch / a.nseg_dense * CHUNK;
+    } else {
+        wk.t_begin = (int64_t)wk.p * a.P * CHUNK;
+        wk.t_end = wk.t_begin + (int64_t)a.P * CHUNK;
+    }
+    if (wk.t_end > wk.len) wk.t_end = wk.len;
+    // the segment is per workgroup: uniform loop bounds keep the chunk loops scalar
+    wk.b = uniform_i64(wk.b);
+    wk.row0 = uniform_i64(wk.row0);
+    wk.len = uniform_i64(wk.len);
+    wk.t_begin = uniform_i64(wk.t_begin);
+    wk.t_end = uniform_i64(wk.t_end);
+    return wk.t_begin < wk.t_end;
+}
+
+// ---------------------------------------------------------------------------------------
+// Precision and LDS layout
+// ---------------------------------------------------------------------------------------
+template <typename TIn>
+struct Prec {
+    static constexpr bool F32 = std::is_same<TIn, float>::value;
+    static constexpr int NS = F32 ? 3 : 2;                                             // parts of derived operands
+    static constexpr int NX = F32 ? 3 : (std::is_same<TIn, _Float16>::value ? 2 : 1);  // parts of V
+};
+
+// Every LDS operand is stored token-major as NP planes of bf16 parts (x ~= p0 + p1 (+ p2)).
+// Fragments whose K index is the token come out of the same planes through the transposed
+// read (ds_read_b64_tr_b16), so no operand is stored twice.
+
+// Causal tiles of A^T (key block sb <= query block tb); index i = tb*(tb+1)/2 + sb.
+__device__ __forceinline__ void tile_sb_tb(int i, int& sb, int& tb) {
+    tb = i >= 6 ? 3 : (i >= 3 ? 2 : (i >= 1 ? 1 : 0));
+    sb = i - tb * (tb + 1) / 2;
+}
+__device__ __forceinline__ int tile_index(int sb, int tb) { return tb * (tb + 1) / 2 + sb; }
+
+// ---- LDS plane access ------------------------------------------------------------------
+// Fragment whose lane index is a plane row (token-major plane, K index along the row): lane
+// (g4, r16) reads row `row`, elements col0 + 4*g4 + [0,4) into K slots 0..3 and
+// col0 + 16 + 4*g4 + [0,4) into slots 4..7, one bf16 part per plane.
+template <int NP>
+__device__ __forceinline__ Split8<NP> lds_frag(const char* base, int plane_bytes, int rs, int row, int col0, int g4) {
+    Split8<NP> f;
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+        const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes) + row * rs + col0 + 4 * g4;
+        const bf16x4 a = *reinterpret_cast<const bf16x4*>(p);
+        const bf16x4 b = *reinterpret_cast<const bf16x4*>(p + 16);
+        f.p[pl] = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    }
+    return f;
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane m supplies the address of four
+// consecutive 16-bit elements M[m][0..3]; lane i receives M[4j + (i >> 2)][i & 3], j = 0..3.
+__device__ __forceinline__ bf16x4 lds_read_tr(const __bf16* p) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+    return __builtin_bit_cast(bf16x4, r);
+}
+
+// Fragment whose lane index is a plane column (K index down the rows): lane (g4, r16) gets
+// column col0 + r16 of rows row0 + 4*g4 + [0,4) (K slots 0..3) and row0 + 16 + 4*g4 + [0,4)
+// (slots 4..7).  Lane (g4, m) addresses row row0 + 4*g4 + (m >> 2), columns col0 + 4*(m & 3).
+template <int NP>
+__device__ __forceinline__ Split8<NP> lds_frag_tr(const char* base, int plane_bytes, int rs, int row0, int col0,
+                                                  int g4, int r16) {
+    Split8<NP> f;
+    const int off = (row0 + 4 * g4 + (r16 >> 2)) * rs + col0 + 4 * (r16 & 3);
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+        const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes) + off;
+        const bf16x4 a = lds_read_tr(p);
+        const bf16x4 b = lds_read_tr(p + 16 * rs);
+        f.p[pl] = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    }
+    return f;
+}
+
+// N (multiple of 4) consecutive values at element index idx (a multiple of 4), split into NP
+// bf16 planes.
+template <int NP, int N>
+__device__ __forceinline__ void lds_put_row(char* base, int plane_bytes, int idx, const float* x) {
+    float r[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) r[j] = x[j];
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+#pragma unroll
+        for (int c = 0; c < N; c += 4) {
+            bf16x4 hb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                hb[j] = (__bf16)r[c + j];
+                if (pl + 1 < NP) r[c + j] -= (float)hb[j];
+            }
+            *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(base + pl * plane_bytes) + idx + c) = hb;
+        }
+    }
+}
+
+// ---- global inputs -----------------------------------------------------------------------
+// N consecutive elements of T as 32-bit words (N * sizeof(T) is 4, 8, 16 or 32 bytes).
+template <typename T, int N>
+struct Vec {
+    static constexpr int BYTES = N * (int)sizeof(T);
+    static constexpr int W = BYTES / 4;
+    uint32_t w[W];
+};
+
+// Raw buffer load of one Vec at byte offset voff + soff of the resource; bytes at or past the
+// resource's num_records read as zero without touching memory.
+template <typename T, int N>
+__device__ __forceinline__ void vec_load(Vec<T, N>& v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    if constexpr (Vec<T, N>::BYTES % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < Vec<T, N>::BYTES / 16; ++i) {
+            const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * i, soff, 0);
+            v.w[4 * i] = u[0]; v.w[4 * i + 1] = u[1]; v.w[4 * i + 2] = u[2]; v.w[4 * i + 3] = u[3];
+        }
+    } else if constexpr (Vec<T, N>::BYTES == 8) {
+        const auto u = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+        v.w[0] = u[0]; v.w[1] = u[1];
+    } else {
+        v.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void vec_float(const Vec<T, N>& v, float* x) {
+    if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = __uint_as_float(v.w[i]);
+    } else if constexpr (std::is_same<T, __bf16>::value) {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) {
+            x[2 * i] = __uint_as_float(v.w[i] << 16);
+            x[2 * i + 1] = __uint_as_float(v.w[i] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) {
+            const uint32_t u = v.w[i];
+            x[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u & 0xffffu));
+            x[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
+        }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ const T* tok_row(const TokTensor& x, const Work& wk, int64_t t, int64_t h, int d) {
+    return reinterpret_cast<const T*>(x.p) + wk.b * x.sb + (wk.row0 + t) * x.st + h * x.sh + d;
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+// Addressing of one token-major input under the stage-1 lane mapping.  Each chunk gets a buffer
+// resource based at its first row (wave-uniform) whose num_records ends at the tensor's extent,
+// so rows past the end read as zero; lanes add a 32-bit offset (token 4*tg, their first column)
+// and the scalar offset selects token j of the four.  A resource with num_records 0 turns a
+// load into a no-op, which keeps the number of loads per chunk fixed.  The host guarantees
+// 64 * token stride + row bytes < 2^31.
+struct TokAddr {
+    const char* p0;  // token 0 of the sequence, head h (uniform)
+    int64_t rem;     // bytes readable from p0 (uniform)
+    int32_t st;      // token stride, bytes (uniform)
+    int32_t lane;    // 4*tg*st + col*sizeof(T)
+};
+
+template <typename T>
+__device__ __forceinline__ TokAddr tok_addr(const TokTensor& x, const Work& wk, int64_t h, int tg, int col) {
+    TokAddr r;
+    const int64_t es = (int64_t)sizeof(T);
+    const int64_t base = uniform_i64((wk.b * x.sb + wk.row0 * x.st + h * x.sh) * es);
+    r.p0 = reinterpret_cast<const char*>(x.p) + base;
+    r.rem = x.extent - base;
+    r.st = (int32_t)(x.st * es);
+    r.lane = 4 * tg * r.st + col * (int32_t)es;
+    return r;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const TokAddr& a, int64_t tc, bool valid) {
+    const int64_t off = tc * a.st;
+    int64_t n = a.rem - off;
+    n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(a.p0) + off, (short)0, valid ? (int)n : 0,
+                                             0x00020000);
+}
+
+struct ChunkAddr {
+    TokAddr q, k, g, v;
+};
+
+template <bool OUT, typename TIn, typename TG>
+__device__ __forceinline__ ChunkAddr chunk_addr(const PrefillParams& a, const Work& wk, int64_t h, int tg, int dcol,
+                                                int vcol) {
+    ChunkAddr c;
+    if (OUT) c.q = tok_addr<TIn>(a.q, wk, h, tg, dcol);
+    c.k = tok_addr<TIn>(a.k, wk, h, tg, dcol);
+    c.g = tok_addr<TG>(a.g, wk, h, tg, dcol);
+    c.v = tok_addr<TIn>(a.v, wk, h, tg, vcol);
+    return c;
+}
+
+// Stage-1 lane mapping: lane = 4*tg + row (tg = lane >> 2, row = lane & 3) holds tokens 4*tg + j
+// (j < 4) of key dims d0 + DL*row + i (i < DL, DL = DPW/4) and value columns c0 + 4*row + c
+// (c < 4).  The four lanes of a quad read one contiguous 4*DL-element piece of a token row, so
+// each quad costs the L1 a single access; a scan over tokens is a serial sum over j, a DPP scan
+// over the four tg of each 16-lane row, and a scan over the four rows' totals.
+template <typename TIn, typename TG, int DL>
+struct ChunkIn {
+    Vec<TIn, DL> q[4], k[4];
+    Vec<TG, DL> g[4];
+    Vec<TIn, 4> v[4];
+};
+
+// Inputs of the chunk starting at token tc (valid: false issues the same loads as no-ops).
+// In a partial chunk the rows past its end are other tokens of the tensor or zeros; stage 1
+// zeroes them.
+template <bool OUT, typename TIn, typename TG, int DL>
+__device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, bool valid) {
+    __amdgpu_buffer_rsrc_t rq;
+    if (OUT) rq = chunk_rsrc(ad.q, tc, valid);
+    const __amdgpu_buffer_rsrc_t rk = chunk_rsrc(ad.k, tc, valid), rg = chunk_rsrc(ad.g, tc, valid),
+                                 rv = chunk_rsrc(ad.v, tc, valid);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        if (OUT) vec_load(c.q[j], rq, ad.q.lane, j * ad.q.st);
+        vec_load(c.k[j], rk, ad.k.lane, j * ad.k.st);
+        vec_load(c.g[j], rg, ad.g.lane, j * ad.g.st);
+        vec_load(c.v[j], rv, ad.v.lane, j * ad.v.st);
+    }
+}
+
+// x[j][i] = element i of token j, zeroed for tokens at or past nv (partial chunks only).
+template <typename T, int N>
+__device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[4][N], int tg, int nv) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vec_float(v[j], x[j]);
+    if (nv < CHUNK) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = 4 * tg + j < nv;
+#pragma unroll
+            for (int i = 0; i < N; ++i) x[j][i] = ok ? x[j][i] : 0.f;
+        }
+    }
+}
+
+// In place: G[j][i] <- inclusive sum over tokens 0..4*tg+j of the chunk (per key dim i);
+// returns the chunk totals in GC[i] (identical across the lanes sharing `row`).
+template <int DL>
+__device__ __forceinline__ void chunk_cumsum(float (&G)[4][DL], float (&GC)[DL], int lane) {
+    float T[DL], I[DL], R[DL], P[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        G[1][i] += G[0][i];
+        G[2][i] += G[1][i];
+        G[3][i] += G[2][i];
+        T[i] = G[3][i];
+        I[i] = T[i];
+    }
+    // the four tg of a 16-lane DPP row sit 4 lanes apart
+#pragma unroll
+    for (int i = 0; i < DL; ++i) I[i] += row_shr<4>(I[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) I[i] += row_shr<8>(I[i]);
+    // DPP row rr's total for this `row` is in lane 16*rr + 12 + row; P = inclusive scan of the
+    // totals over rr
+    const int rr = lane >> 4, own = (lane & 48) | 12 | (lane & 3);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) R[i] = lane_bcast(I[i], own);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float prev = lane_bcast(R[i], (lane - 16) & 63);
+        P[i] = R[i] + (rr >= 1 ? prev : 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float prev = lane_bcast(P[i], (lane - 32) & 63);
+        P[i] += rr >= 2 ? prev : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float E = I[i] - T[i] + (P[i] - R[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) G[j][i] += E;
+        GC[i] = lane_bcast(P[i], 60 | (lane & 3));
+    }
+}
+
+// X[j][i] <- sum of g over the tokens after 4*tg + j in the chunk (exclusive suffix, per key dim
+// i), GC[i] <- the chunk total.  Every suffix is summed from the later tokens only, so its
+// rounding error scales with the suffix itself, not with the chunk total (a difference of two
+// prefix sums loses that accuracy when the total is large).
+template <int DL>
+__device__ __forceinline__ void chunk_suffix(const float (&g)[4][DL], float (&X)[4][DL], float (&GC)[DL], int lane) {
+    float T[DL], Y[DL], Z[DL], C[DL];
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        X[3][i] = 0.f;
+        X[2][i] = g[3][i];
+        X[1][i] = X[2][i] + g[2][i];
+        X[0][i] = X[1][i] + g[1][i];
+        T[i] = X[0][i] + g[0][i];
+    }
+    // Y = sum of T over the later tg of the same 16-lane DPP row (4 lanes apart)
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Y[i] = row_shl<4>(T[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Y[i] += row_shl<4>(Y[i]);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Y[i] += row_shl<8>(Y[i]);
+    // Z = this DPP row's total (lane 16*rr + row, the row's first tg); C = inclusive suffix of Z
+    const int rr = lane >> 4, first = (lane & 48) | (lane & 3);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) Z[i] = lane_bcast(Y[i] + T[i], first);
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float next = lane_bcast(Z[i], (lane + 16) & 63);
+        C[i] = Z[i] + (rr <= 2 ? next : 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float next = lane_bcast(C[i], (lane + 32) & 63);
+        C[i] += rr <= 1 ? next : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+        const float later_rows = lane_bcast(C[i], (lane + 16) & 63);
+        const float E = Y[i] + (rr <= 2 ? later_rows : 0.f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) X[j][i] += E;
+        GC[i] = lane_bcast(C[i], lane & 3);
+    }
+}
+
+
+// S tile db of wave w: element i is S[16*db + 4*g4 + i][16*w + r16].
+__device__ __forceinline__ int64_t state_off(int db, int i, int g4, int r16, int wave, int Dv) {
+    return (int64_t)(16 * db + 4 * g4 + i) * Dv + 16 * wave + r16;
+}
+
+}  // namespace triune

@@ -1,0 +1,639 @@
+// gdn_chunk.hip -- chunked Gated DeltaNet prefill for gfx950 (WY/UT form, LDS-staged, MFMA).
+//
+// Recurrence (reference: triune/kernels/fast_gla.py:781-836 fast_recurrent_gated_deltanet,
+// :383-477 the Triton per-token kernel), per (sequence, head):
+//   u_t = v_t - S_{t-1}^T k_t ,  S_t = D_t S_{t-1} + w_t u_t^T ,  o_t = S_t^T q_t
+// with D_t = diag(exp(min(g_t, 0))) and w_t = beta_t * k_t (beta per token, per key dim, or 1).
+//
+// Chunk form (C = 64 tokens, G = inclusive cumulative log-decay inside the chunk, Gp = G - g the
+// exclusive one, m = G_C / 2 per key dim, S0 the state at the chunk start, S' = e^m S0):
+//   Qt = q e^{G-m},  Wt = w e^{m-G},  Bt = k e^{Gp-m}          (|exponents| <= span / 2)
+//   L  = strictly_lower(Bt Wt^T),  A = lower(Qt Wt^T)
+//   U  = (I + L)^{-1} (V - Bt S')                                (the UT transform)
+//   O  = Qt S' + A U ,   S_C = e^m (S' + Wt^T U)
+// (I + L)^{-1} is applied block-wise on 16-token blocks: U_i = T_ii (R_i - sum_{j<i} L_ij U_j),
+// with each 16x16 unit-lower inverse T_ii = prod_k (I + M^(2^k)), M = -L_ii, by doubling.
+// The chunk map S0 -> S_C is affine with a full Dk x Dk matrix, so segments compose as
+// S_in[p+1] = M_p S_in[p] + N_p:
+//   K1 gdn_seg_mn   : per (segment, head, half) the segment map applied to [I | 0] (half 0 -> M_p,
+//                     V replaced by 0) or to 0 with the real V (half 1 -> N_p)
+//   K2 gdn_seg_scan : per (sequence, head, 16 columns) the carry S_in[p] (written in place of N_p)
+//   K3 gdn_seg_out  : per (segment, head) the chunk walk from S_in[p], writing o
+// Products run on v_mfma_f32_16x16x32_bf16 with operands split into bf16 parts (2 for 16-bit
+// I/O, 3 for fp32) and fp32 accumulation, as in the GLA prefill.  Chunks whose decay span
+// exceeds SPAN_MAX run token by token.
+#include "chunk_common.h"
+
+namespace triune {
+
+template <typename TIn, bool OUT>
+struct GLay {
+    using P = Prec<TIn>;
+    static constexpr int DK = 64, DV = 64, NW = 4, DPW = 16, DL = 4;
+    static constexpr int RS = DK + PAD, VS = 16;
+    static constexpr int ROWP = CHUNK * RS * 2;
+    static constexpr int VPP = CHUNK * VS * 2;
+    static constexpr int TILEP = 10 * 64 * 4 * 2;  // ten 16x16 tiles, one bf16 part
+    static constexpr int DIAGP = 4 * 64 * 4 * 2;   // four 16x16 tiles
+    static constexpr int OFF_QT = 0;
+    static constexpr int OFF_WT = OFF_QT + (OUT ? P::NS * ROWP : 0);
+    static constexpr int OFF_BT = OFF_WT + P::NS * ROWP;
+    static constexpr int OFF_AT = OFF_BT + P::NS * ROWP;
+    static constexpr int OFF_LT = OFF_AT + (OUT ? P::NS * TILEP : 0);
+    static constexpr int OFF_TI = OFF_LT + P::NS * TILEP;
+    static constexpr int OFF_VP = OFF_TI + P::NS * DIAGP;
+    static constexpr int OFF_FAC = OFF_VP + NW * P::NX * VPP;
+    static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
+    static constexpr int BYTES = OFF_FLAG + 16 * 4;
+    static constexpr int OS = 20;
+    static_assert(16 * OS * 4 <= P::NX * VPP, "output staging fits in a wave's V planes");
+    static_assert(BYTES <= 160 * 1024, "LDS budget");
+};
+
+// Four fp32 values (one D-layout column piece) as a K=16 operand: K slots 0..3, zeros above.
+template <int NP>
+__device__ __forceinline__ Split8<NP> split_k16(const f32x4& v) {
+    const float x[8] = {v[0], v[1], v[2], v[3], 0.f, 0.f, 0.f, 0.f};
+    return split8<NP>(x);
+}
+
+template <int NP>
+__device__ __forceinline__ Split8<NP> split_k32(const f32x4& lo, const f32x4& hi) {
+    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return split8<NP>(x);
+}
+
+// Tile fragment from a tile plane set: lane values at (tile, lane) in K slots 0..3 (K=16), or two
+// tiles in slots 0..3 / 4..7 (K=32).
+template <int NP>
+__device__ __forceinline__ Split8<NP> tile_frag(const char* base, int plane_bytes, int i0, int i1, bool has_hi,
+                                                int lane) {
+    Split8<NP> f;
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) {
+        const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes);
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
+        const __bf16 z = (__bf16)0.f;
+        if (has_hi) {
+            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
+            f.p[pl] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        } else {
+            f.p[pl] = bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
+        }
+    }
+    return f;
+}
+
+__device__ __forceinline__ float beta_value(const PrefillParams& a, const Work& wk, int64_t h, int64_t t) {
+    const int64_t i = wk.b * a.b_sb + (wk.row0 + t) * a.b_st + h * a.b_sh;
+    if (a.beta_dt == DT_F32) return reinterpret_cast<const float*>(a.beta)[i];
+    if (a.beta_dt == DT_BF16) return (float)reinterpret_cast<const __bf16*>(a.beta)[i];
+    return (float)reinterpret_cast<const _Float16*>(a.beta)[i];
+}
+
+// Token-by-token GDN update of one wave's 16 state columns (decay spans beyond SPAN_MAX).
+// S tile db holds S[16*db + 4*g4 + i][c0 + r16]; with_v false reads V as zero.
+template <typename TIn, typename TG, bool OUT>
+__device__ void gdn_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int c0, int64_t tc, int nv, int g4,
+                              int r16, bool with_v, f32x4 (&S)[4]) {
+    for (int t = 0; t < nv; ++t) {
+        const int64_t tt = tc + t;
+        float dcy[4][4], kk[4][4], ww[4][4], qq[4][4];
+        const float bh = a.beta_kind == BETA_HEAD ? beta_value(a, wk, h, tt) : 1.f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int d = 16 * db + 4 * g4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                dcy[db][i] = expf(fminf((float)tok_row<TG>(a.g, wk, tt, h, d)[i], 0.f));
+                kk[db][i] = (float)tok_row<TIn>(a.k, wk, tt, h, d)[i];
+                const float bk = a.beta_kind == BETA_KEY ? tok_row<float>(a.kb, wk, tt, h, d)[i] : bh;
+                ww[db][i] = bk * kk[db][i];
+                qq[db][i] = OUT ? (float)tok_row<TIn>(a.q, wk, tt, h, d)[i] : 0.f;
+            }
+        }
+        float pred = 0.f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pred += kk[db][i] * S[db][i];
+        pred += __shfl_xor(pred, 16);
+        pred += __shfl_xor(pred, 32);
+        const float u = (with_v ? (float)tok_row<TIn>(a.v, wk, tt, h, c0)[r16] : 0.f) - pred;
+        float part = 0.f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s = dcy[db][i] * S[db][i] + ww[db][i] * u;
+                S[db][i] = s;
+                part += qq[db][i] * s;
+            }
+        if (OUT) {
+            part += __shfl_xor(part, 16);
+            part += __shfl_xor(part, 32);
+            if (g4 == 0) {
+                const int64_t off = wk.b * a.o_sb + (wk.row0 + tt) * a.o_st + h * a.o_sh + c0 + r16;
+                char* op = reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt);
+                if (a.o_dt == DT_F32) *reinterpret_cast<float*>(op) = part;
+                else if (a.o_dt == DT_BF16) *reinterpret_cast<__bf16*>(op) = (__bf16)part;
+                else *reinterpret_cast<_Float16*>(op) = (_Float16)part;
+            }
+        }
+    }
+}
+
+// Inputs of a GDN chunk: the GLA chunk inputs plus per-key-dim beta (BETA_KEY, fp32).
+template <typename TIn, typename TG>
+struct GChunkIn {
+    ChunkIn<TIn, TG, 4> x;
+    Vec<float, 4> bk[4];
+};
+
+template <bool OUT, typename TIn, typename TG>
+__device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG>& c, const ChunkAddr& ad, const TokAddr& kb, bool key_beta,
+                                            int64_t tc, bool valid) {
+    chunk_load<OUT>(c.x, ad, tc, valid);
+    if (key_beta) {
+        const __amdgpu_buffer_rsrc_t r = chunk_rsrc(kb, tc, valid);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vec_load(c.bk[j], r, kb.lane, j * kb.st);
+    }
+}
+
+// One chunk of the GDN walk for (segment, head).  OUT: outputs (K3); otherwise the state map only
+// (K1; with_v false drives it with V = 0).
+template <typename TIn, typename TG, bool OUT>
+struct GdnStep {
+    using L = GLay<TIn, OUT>;
+    using PR = Prec<TIn>;
+    static constexpr int NS = PR::NS, NX = PR::NX, DL = 4;
+
+    template <typename Hook>
+    __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+                               const GChunkIn<TIn, TG>& cur, bool with_v, f32x4 (&S)[4], char* smem,
+                               Hook&& after_inputs) {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+        const int tg = lane >> 2, row = lane & 3;
+        const int c0 = wave * 16;
+        const int dl0 = wave * 16 + DL * row;
+        char* sQT = smem + L::OFF_QT;
+        char* sWT = smem + L::OFF_WT;
+        char* sBT = smem + L::OFF_BT;
+        char* sAT = smem + L::OFF_AT;
+        char* sLT = smem + L::OFF_LT;
+        char* sTI = smem + L::OFF_TI;
+        char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
+        float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
+        float* sEG = sEM + 64;
+        int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
+
+        // ---------------- stage 1: factors and split operands -> LDS ------------------------
+        {
+            float G[4][DL], Gc[4][DL], GC[DL], x[4][DL];
+            chunk_float(cur.x.g, G, tg, nv);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < DL; ++i) {
+                    G[j][i] = fminf(G[j][i], 0.f);
+                    Gc[j][i] = G[j][i];
+                }
+            chunk_cumsum<DL>(G, GC, lane);
+            bool bad = false;
+#pragma unroll
+            for (int i = 0; i < DL; ++i) bad |= !(GC[i] >= -SPAN_MAX);
+            float fq[4][DL];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int i = 0; i < DL; ++i) fq[j][i] = fast_exp(G[j][i] - 0.5f * GC[i]);  // exp(G - m)
+            if (tg == 0) {
+#pragma unroll
+                for (int i = 0; i < DL; ++i) {
+                    const float em = fast_exp(0.5f * GC[i]);
+                    sEM[dl0 + i] = em;
+                    sEG[dl0 + i] = em * em;
+                }
+            }
+            const bool any_bad = __any(bad);
+            if (lane == 0) sFLAG[wave] = any_bad ? 1 : 0;
+            if (OUT) {
+                chunk_float(cur.x.q, x, tg, nv);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                    for (int i = 0; i < DL; ++i) x[j][i] *= fq[j][i];
+                    lds_put_row<NS, DL>(sQT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
+                }
+            }
+            float kx[4][DL];
+            chunk_float(cur.x.k, kx, tg, nv);
+            // Bt = k exp(Gp - m)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int i = 0; i < DL; ++i) x[j][i] = kx[j][i] * fast_exp(G[j][i] - Gc[j][i] - 0.5f * GC[i]);
+                lds_put_row<NS, DL>(sBT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
+            }
+            // Wt = beta k exp(m - G)
+            float bt[4];
+            if (a.beta_kind == BETA_HEAD) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int tl = min(4 * tg + j, nv - 1);
+                    bt[j] = beta_value(a, wk, h, tc + tl);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) bt[j] = 1.f;
+            }
+            float bkx[4][DL];
+            if (a.beta_kind == BETA_KEY) {
+                chunk_float(cur.bk, bkx, tg, nv);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int i = 0; i < DL; ++i) bkx[j][i] = bt[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int i = 0; i < DL; ++i) x[j][i] = kx[j][i] * bkx[j][i] * __builtin_amdgcn_rcpf(fq[j][i]);
+                lds_put_row<NS, DL>(sWT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
+            }
+            // V rows of this wave's columns (zero when the map is driven without V)
+            float vx[4][4];
+            chunk_float(cur.x.v, vx, tg, nv);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (!with_v) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) vx[j][c] = 0.f;
+                }
+                lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
+            }
+        }
+        after_inputs();
+        __syncthreads();
+        bool fast = true;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) fast = fast && (sFLAG[w] == 0);
+        if (!fast) {
+            gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, with_v, S);
+            __syncthreads();
+            return;
+        }
+
+        // ---------------- stage 2: tiles -> LDS; diagonal-block inverses -------------------
+        // Tile list: the ten lower tiles of A^T = Wt Qt^T (OUT) and the six strictly lower
+        // off-diagonal tiles of L^T = Wt Bt^T; tile (sb, tb) holds rows s of block sb, columns t
+        // of block tb.
+        {
+            constexpr int NT = OUT ? 16 : 6;
+            for (int n = wave; n < NT; n += 4) {
+                const bool is_a = OUT && n < 10;
+                int sb, tb, idx;
+                if (is_a) {
+                    idx = n;
+                    tile_sb_tb(idx, sb, tb);
+                } else {
+                    const int m = OUT ? n - 10 : n;  // off-diagonal L tiles: (0,1) (0,2) (1,2) (0,3) (1,3) (2,3)
+                    tb = m >= 3 ? 3 : (m >= 1 ? 2 : 1);
+                    sb = m - (tb - 1) * tb / 2;
+                    idx = tile_index(sb, tb);
+                }
+                const char* rhs = is_a ? sQT : sBT;
+                f32x4 acc = zero4();
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const Split8<NS> wf = lds_frag<NS>(sWT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
+                    const Split8<NS> rf = lds_frag<NS>(rhs, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                    acc = mfma_split<NS, NS, NS>(wf, rf, acc);
+                }
+                if (is_a && sb == tb) {  // row = s (4*g4 + j), column = t (r16): keep s <= t
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[j] = (4 * g4 + j > r16) ? 0.f : acc[j];
+                }
+                const float xv[4] = {acc[0], acc[1], acc[2], acc[3]};
+                lds_put_row<NS, 4>(is_a ? sAT : sLT, L::TILEP, (idx * 64 + lane) * 4, xv);
+            }
+            // Diagonal block wave of the UT transform: T_ww = (I + L_ww)^-1 by doubling, kept as
+            // D-layout pairs (X, X^T) so every product reads its operands from registers.
+            {
+                const int ib = wave;
+                f32x4 Lm = zero4(), LmT = zero4();
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * ib + r16, 32 * ks, g4);
+                    const Split8<NS> wf = lds_frag<NS>(sWT, L::ROWP, L::RS, 16 * ib + r16, 32 * ks, g4);
+                    Lm = mfma_split<NS, NS, NS>(bf, wf, Lm);    // Lm[t = 4*g4+j][s = r16]
+                    LmT = mfma_split<NS, NS, NS>(wf, bf, LmT);  // LmT[s = 4*g4+j][t = r16]
+                }
+                f32x4 P, PT, Tm, TT;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int rr = 4 * g4 + j;
+                    P[j] = rr > r16 ? -Lm[j] : 0.f;    // M = -L (strictly lower: t > s)
+                    PT[j] = r16 > rr ? -LmT[j] : 0.f;  // M^T
+                    Tm[j] = P[j] + (rr == r16 ? 1.f : 0.f);
+                    TT[j] = PT[j] + (rr == r16 ? 1.f : 0.f);
+                }
+#pragma unroll
+                for (int step = 0; step < 3; ++step) {
+                    // A-layout of X = D-layout registers of X^T
+                    const Split8<NS> pA = split_k16<NS>(PT), pB = split_k16<NS>(P);
+                    const Split8<NS> ptA = split_k16<NS>(P), ptB = split_k16<NS>(PT);
+                    const f32x4 Pn = mfma_split<NS, NS, NS>(pA, pB, zero4());     // P P
+                    const f32x4 PTn = mfma_split<NS, NS, NS>(ptA, ptB, zero4());  // P^T P^T
+                    const Split8<NS> tA = split_k16<NS>(Tm), tB = split_k16<NS>(Tm);
+                    const Split8<NS> pnA = split_k16<NS>(PTn), ptnB = split_k16<NS>(PTn);
+                    const f32x4 TTn = mfma_split<NS, NS, NS>(tA, ptnB, TT);  // T^T + T^T (P^T)^2
+                    const f32x4 Tn = mfma_split<NS, NS, NS>(pnA, tB, Tm);    // T + P^2 T
+                    Tm = Tn;
+                    TT = TTn;
+                    P = Pn;
+                    PT = PTn;
+                }
+                const float xv[4] = {TT[0], TT[1], TT[2], TT[3]};  // A-layout of T_ww
+                lds_put_row<NS, 4>(sTI, L::DIAGP, (ib * 64 + lane) * 4, xv);
+            }
+        }
+        __syncthreads();
+
+        // ---------------- stage 3: residuals, UT solve, outputs, state ----------------------
+        {
+            f32x4 Sp[4];
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Sp[db][i] = S[db][i] * em[i];
+            }
+            Split8<NS> sf[2];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) sf[ks] = split_k32<NS>(Sp[2 * ks], Sp[2 * ks + 1]);
+            // R_i = V_i - Bt_i S'  (D layout: rows t = 16i + 4*g4 + k, column c0 + r16)
+            f32x4 R[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f32x4 p = zero4();
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4);
+                    p = mfma_split<NS, NS, NS>(bf, sf[ks], p);
+                }
+                const int off = (16 * i + 4 * g4 + (r16 >> 2)) * L::VS + 4 * (r16 & 3);
+                f32x4 vv = zero4();
+#pragma unroll
+                for (int pl = 0; pl < NX; ++pl) {
+                    const bf16x4 t4 = lds_read_tr(reinterpret_cast<const __bf16*>(sVP + pl * L::VPP) + off);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) vv[k] += (float)t4[k];
+                }
+#pragma unroll
+                for (int k = 0; k < 4; ++k) R[i][k] = vv[k] - p[k];
+            }
+            // U_i = T_ii (R_i - sum_{j<i} L_ij U_j)
+            f32x4 U[4];
+            Split8<NS> us[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f32x4 X = R[i];
+                if (i >= 1) {
+                    f32x4 p = zero4();
+                    if (i >= 2) {  // blocks 0 and 1 together (K = 32)
+                        const Split8<NS> lf = tile_frag<NS>(sLT, L::TILEP, tile_index(0, i), tile_index(1, i), true, lane);
+                        p = mfma_split<NS, NS, NS>(lf, split_k32<NS>(U[0], U[1]), p);
+                        if (i == 3) {
+                            const Split8<NS> lf2 = tile_frag<NS>(sLT, L::TILEP, tile_index(2, 3), 0, false, lane);
+                            p = mfma_split<NS, NS, NS>(lf2, us[2], p);
+                        }
+                    } else {
+                        const Split8<NS> lf = tile_frag<NS>(sLT, L::TILEP, tile_index(0, 1), 0, false, lane);
+                        p = mfma_split<NS, NS, NS>(lf, us[0], p);
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) X[k] -= p[k];
+                }
+                const Split8<NS> tf = tile_frag<NS>(sTI, L::DIAGP, i, 0, false, lane);
+                U[i] = mfma_split<NS, NS, NS>(tf, split_k16<NS>(X), zero4());
+                us[i] = split_k16<NS>(U[i]);
+            }
+            // U with K = tokens 32*k2 + pi(g4, j): A-operand of U^T, B-operand of U
+            Split8<NS> uf[2];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) uf[k2] = split_k32<NS>(U[2 * k2], U[2 * k2 + 1]);
+
+            if (OUT) {
+                f32x4 Ot[4];
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    f32x4 o = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                        o = mfma_split<NS, NS, NS>(sf[ks], qf, o);
+                    }
+#pragma unroll
+                    for (int k2 = 0; k2 < 2; ++k2) {
+                        if (2 * k2 > tb) continue;
+                        const bool has_hi = 2 * k2 + 1 <= tb;
+                        const Split8<NS> af = tile_frag<NS>(sAT, L::TILEP, tile_index(2 * k2, tb),
+                                                            has_hi ? tile_index(2 * k2 + 1, tb) : 0, has_hi, lane);
+                        o = mfma_split<NS, NS, NS>(uf[k2], af, o);
+                    }
+                    Ot[tb] = o;
+                }
+                // lane (g4, r16) holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3]; stage
+                // through this wave's V planes (read above) and store quad-coalesced rows
+                float* sO = reinterpret_cast<float*>(sVP);
+                const int es = dt_size(a.o_dt);
+                const int64_t ost = a.o_st * es;
+                char* obase = reinterpret_cast<char*>(a.o) +
+                              uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
+                const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);
+                const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    *reinterpret_cast<f32x4*>(sO + r16 * L::OS + 4 * g4) = Ot[tb];
+                    const f32x4 xo = *reinterpret_cast<const f32x4*>(sO + tq * L::OS + 4 * q);
+                    if (16 * tb + tq < nv) store4_dt(obase + 16 * tb * ost + olane, a.o_dt, xo[0], xo[1], xo[2], xo[3]);
+                }
+            }
+            // S <- e^m (S' + Wt^T U)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                f32x4 acc = Sp[db];
+#pragma unroll
+                for (int k2 = 0; k2 < 2; ++k2) {
+                    const Split8<NS> wf = lds_frag_tr<NS>(sWT, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
+                    acc = mfma_split<NS, NS, NS>(wf, uf[k2], acc);
+                }
+                const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) S[db][i] = em[i] * acc[i];
+            }
+        }
+        __syncthreads();  // the next chunk rewrites LDS
+    }
+};
+
+template <typename TIn, typename TG, bool OUT>
+__device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, bool with_v, f32x4 (&S)[4], char* smem) {
+    using St = GdnStep<TIn, TG, OUT>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane >> 2, row = lane & 3;
+    const ChunkAddr ad = chunk_addr<OUT, TIn, TG>(a, wk, h, tg, wave * 16 + 4 * row, wave * 16 + 4 * row);
+    const bool key_beta = a.beta_kind == BETA_KEY;
+    TokAddr kb{};
+    if (key_beta) kb = tok_addr<float>(a.kb, wk, h, tg, wave * 16 + 4 * row);
+    const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
+    auto chunk_nv = [&](int64_t c) {
+        const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
+        return (int)(r < CHUNK ? r : CHUNK);
+    };
+    auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
+    GChunkIn<TIn, TG> A;
+    gchunk_load<OUT>(A, ad, kb, key_beta, tok(0), true);
+    for (int64_t c = 0; c < nch; ++c)
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, with_v, S, smem,
+                [&] { gchunk_load<OUT>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch); });
+}
+
+// K1: blockIdx.z = 0 -> M_p (state [I | .], V = 0), 1 -> N_p (state 0, real V).
+template <typename TIn, typename TG>
+__global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel(PrefillParams a) {
+    using L = GLay<TIn, false>;
+    __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
+    const int64_t w = blockIdx.x, h = blockIdx.y;
+    const bool is_m = blockIdx.z == 0;
+    Work wk;
+    if (!find_work(a, w, wk)) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    f32x4 S[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[db][i] = (is_m && 16 * db + 4 * g4 + i == 16 * wave + r16) ? 1.f : 0.f;
+    gdn_walk<TIn, TG, false>(a, wk, h, !is_m, S, smem);
+    float* dst = (is_m ? a.ws_m : a.ws_state) + (w * a.H + h) * (int64_t)64 * 64;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[state_off(db, i, g4, r16, wave, 64)] = S[db][i];
+}
+
+// K3: outputs of one segment from S_in[p] (in the N slot after the scan).
+template <typename TIn, typename TG>
+__global__ __launch_bounds__(256, 1) void gdn_seg_out_kernel(PrefillParams a) {
+    using L = GLay<TIn, true>;
+    __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
+    const int64_t w = blockIdx.x, h = blockIdx.y;
+    Work wk;
+    if (!find_work(a, w, wk)) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    f32x4 S[4];
+    const float* st = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, 64)];
+    gdn_walk<TIn, TG, true>(a, wk, h, true, S, smem);
+}
+
+// K2: per (sequence, head, 16 columns): S_in[p] = carry, written in place of N_p; then
+// S <- M_p S + N_p.  256 threads: thread (row r = tid / 4, columns 4*(tid % 4) .. +3).
+__global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
+    __shared__ __attribute__((aligned(16))) float sS[64][16];
+    const int64_t seq = blockIdx.z, h = blockIdx.y;
+    const int cb = blockIdx.x * 16;
+    const int tid = threadIdx.x, r = tid >> 2, cq = 4 * (tid & 3);
+    int64_t p0, np;
+    if (a.varlen) {
+        p0 = a.seg_off[seq];
+        np = (int64_t)a.seg_off[seq + 1] - p0;
+    } else {
+        const int64_t nch = (a.T + CHUNK - 1) / CHUNK;
+        p0 = seq * a.nseg_dense;
+        np = a.nseg_dense < nch ? a.nseg_dense : nch;
+        if (a.T == 0) np = 0;
+    }
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.s0) s = *reinterpret_cast<const float4*>(a.s0 + ((seq * a.H + h) * 64 + r) * 64 + cb + cq);
+    for (int64_t p = 0; p < np; ++p) {
+        const int64_t w = p0 + p;
+        float* nslot = a.ws_state + ((w * a.H + h) * 64 + r) * 64 + cb + cq;
+        const float4 n = *reinterpret_cast<const float4*>(nslot);
+        *reinterpret_cast<float4*>(nslot) = s;  // S_in[p]
+        *reinterpret_cast<float4*>(&sS[r][cq]) = s;
+        __syncthreads();
+        const float* mrow = a.ws_m + ((w * a.H + h) * 64 + r) * 64;
+        float4 acc = n;
+#pragma unroll 4
+        for (int d = 0; d < 64; d += 4) {
+            const float4 m4 = *reinterpret_cast<const float4*>(mrow + d);
+            const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float4 sv = *reinterpret_cast<const float4*>(&sS[d + e][cq]);
+                acc.x += mv[e] * sv.x;
+                acc.y += mv[e] * sv.y;
+                acc.z += mv[e] * sv.z;
+                acc.w += mv[e] * sv.w;
+            }
+        }
+        __syncthreads();
+        s = acc;
+    }
+    if (s_final) *reinterpret_cast<float4*>(s_final + ((seq * a.H + h) * 64 + r) * 64 + cb + cq) = s;
+}
+
+// ---------------------------------------------------------------------------------------
+// Host launchers.
+// ---------------------------------------------------------------------------------------
+template <typename TIn, typename TG>
+static hipError_t launch_gdn_t(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
+    if (which == 0) {
+        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG>), dim3((unsigned)n_work, (unsigned)a.H, 2), dim3(256), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
+    }
+    return hipGetLastError();
+}
+
+static hipError_t launch_gdn(const PrefillParams& a, int64_t n_work, int io_dt, int which, hipStream_t stream) {
+    const bool g32 = a.g_dt == DT_F32;
+    if (io_dt == DT_BF16) {
+        if (g32) return launch_gdn_t<__bf16, float>(a, n_work, which, stream);
+        if (a.g_dt == DT_BF16) return launch_gdn_t<__bf16, __bf16>(a, n_work, which, stream);
+    } else if (io_dt == DT_F16) {
+        if (g32) return launch_gdn_t<_Float16, float>(a, n_work, which, stream);
+        if (a.g_dt == DT_F16) return launch_gdn_t<_Float16, _Float16>(a, n_work, which, stream);
+    } else if (io_dt == DT_F32 && g32) {
+        return launch_gdn_t<float, float>(a, n_work, which, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gdn_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream) {
+    return launch_gdn(a, n_work, io_dt, 0, stream);
+}
+
+hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream) {
+    return launch_gdn(a, n_work, io_dt, 1, stream);
+}
+
+hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, hipStream_t stream) {
+    hipLaunchKernelGGL(gdn_seg_scan_kernel, dim3(4, (unsigned)a.H, (unsigned)a.n_seqs), dim3(256), 0, stream, a, s_final);
+    return hipGetLastError();
+}
+
+int gdn_seg_out_blocks_per_cu() {
+    int nb = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &nb, reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16>), 256, 0);
+    return (e == hipSuccess && nb > 0) ? nb : 1;
+}
+
+}  // namespace triune

@@ -27,6 +27,13 @@ struct PrefillParams {
     const int32_t* cu;     // varlen: [n_seqs + 1] token offsets (device)
     const int32_t* seg_off;// varlen: [n_seqs + 1] segment offsets (device, from plan kernel)
     int flags;             // bit 0: the last token of each sequence keeps g unclamped
+    // Gated DeltaNet (chunked): write strength beta per token (BETA_HEAD, strides b_sb/b_st/b_sh,
+    // dtype beta_dt) or per (token, key dim) (BETA_KEY, fp32, in `kb`), or none.
+    const void* beta;
+    int beta_dt, beta_kind;
+    int64_t b_sb, b_st, b_sh;
+    TokTensor kb;
+    float* ws_m;           // [n_work, H, Dk, Dk] segment transition matrices
 };
 
 struct ScanParams {
@@ -85,6 +92,10 @@ hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t 
 hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream);
+hipError_t launch_gdn_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
+hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, hipStream_t stream);
+hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
+int gdn_seg_out_blocks_per_cu();
 bool prefill_shape_supported(int Dk, int Dv);
 bool prefill_dtype_supported(int Dk, int Dv, int io_dt);
 int gla_seg_output_blocks_per_cu(int Dk, int Dv);

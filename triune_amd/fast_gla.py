@@ -35,6 +35,9 @@ __all__ = [
 _DIMS = (32, 64, 128)
 _PAIRS = ((32, 32), (64, 64), (128, 64), (128, 128))  # (Dk, Dv) the prefill kernels support
 _DECODE_PAIRS = ((32, 32), (64, 64), (64, 128), (128, 64), (128, 128))
+# Gated DeltaNet prefill: the chunked WY/UT kernels (head dims <= 64) unless this is False, in
+# which case every call takes the token-serial kernel (kept for the per-value-dim beta).
+_chunked_gdn_enabled = True
 
 
 def _on_device(*ts):
@@ -340,13 +343,34 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind):
     o = torch.empty(B, T, H, D, device=q.device, dtype=v.dtype)
     s0 = _state_in(initial_state, D, D)
     sf = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
+    # chunked WY/UT path: (64, 64) heads (smaller ones zero-padded), per-token or per-key beta
+    chunked = (D <= 64 and T > 1 and beta_kind != _lib.BETA_VALUE and _chunked_gdn_enabled)
+    if chunked:
+        D = 64
+        qp, kp, gp, vp = (_vec_layout(_pad_last(x, D)) for x in (q, k, g, v))
+        if beta_kind == _lib.BETA_KEY:
+            bp = _pad_last(beta, D).to(torch.float32).contiguous()
+            bst = (bp.stride(0), bp.stride(1), bp.stride(2))
+        o = torch.empty(B, T, H, D, device=q.device, dtype=v.dtype)
+        s0 = _state_in(initial_state, D, D)
+        sf = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
     st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), bst, _tok3(o))
-    rc = lib().triune_hip_gdn_prefill(
-        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(bp),
-        dtype_code(bp) if bp is not None else 0, beta_kind, st, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
-        B, T, H, D, D, stream_of(q),
-    )
-    check(rc, "triune_hip_gdn_prefill")
+    if chunked:
+        ws_bytes = lib().triune_hip_gdn_prefill_chunked_workspace_size(B, T, H, D, D)
+        ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
+        rc = lib().triune_hip_gdn_prefill_chunked(
+            ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(bp),
+            dtype_code(bp) if bp is not None else 0, beta_kind, st, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
+            B, T, H, D, D, ptr(ws), ws_bytes, stream_of(q),
+        )
+        check(rc, "triune_hip_gdn_prefill_chunked")
+    else:
+        rc = lib().triune_hip_gdn_prefill(
+            ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(bp),
+            dtype_code(bp) if bp is not None else 0, beta_kind, st, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
+            B, T, H, D, D, stream_of(q),
+        )
+        check(rc, "triune_hip_gdn_prefill")
     if D != Dv0:
         o = o[..., :Dv0]
     if D != Dk0 or D != Dv0:
