@@ -380,7 +380,7 @@ namespace {
 // Chunked GDN: segments per sequence fill the resident output-kernel slots once.
 struct GdnPlan {
     int64_t nseg, n_work;
-    size_t off_m, total;
+    size_t off_m, off_spare, total;
 };
 
 GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H) {
@@ -408,7 +408,8 @@ GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H) {
     if (p.nseg > nchunks) p.nseg = nchunks;
     p.n_work = B * p.nseg;
     p.off_m = align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
-    p.total = p.off_m + align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
+    p.off_spare = p.off_m + align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
+    p.total = p.off_spare + align_up((size_t)B * H * 64 * 64 * sizeof(float));
     return p;
 }
 
@@ -472,6 +473,7 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     a.s0 = s0;
     a.ws_state = reinterpret_cast<float*>(ws);
     a.ws_m = reinterpret_cast<float*>(ws + pl.off_m);
+    a.ws_spare = reinterpret_cast<float*>(ws + pl.off_spare);
     a.n_seqs = B; a.H = H; a.T = T; a.Dk = Dk; a.Dv = Dv;
     a.P = 0; a.nseg_dense = (int)pl.nseg; a.varlen = 0; a.flags = 0;
     a.beta = beta; a.beta_dt = beta_dtype; a.beta_kind = beta_kind;

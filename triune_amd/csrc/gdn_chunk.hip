@@ -33,14 +33,15 @@ struct GLay {
     static constexpr int RS = DK + PAD, VS = 16;
     static constexpr int ROWP = CHUNK * RS * 2;
     static constexpr int VPP = CHUNK * VS * 2;
-    static constexpr int TILEP = 10 * 64 * 4 * 2;  // ten 16x16 tiles, one bf16 part
+    static constexpr int TILEP = 10 * 64 * 4 * 2;  // ten 16x16 tiles (causal blocks), one bf16 part
+    static constexpr int LTP = 6 * 64 * 4 * 2;     // the six off-diagonal blocks of L^T
     static constexpr int DIAGP = 4 * 64 * 4 * 2;   // four 16x16 tiles
     static constexpr int OFF_QT = 0;
     static constexpr int OFF_WT = OFF_QT + (OUT ? P::NS * ROWP : 0);
     static constexpr int OFF_BT = OFF_WT + P::NS * ROWP;
     static constexpr int OFF_AT = OFF_BT + P::NS * ROWP;
     static constexpr int OFF_LT = OFF_AT + (OUT ? P::NS * TILEP : 0);
-    static constexpr int OFF_TI = OFF_LT + P::NS * TILEP;
+    static constexpr int OFF_TI = OFF_LT + P::NS * LTP;
     static constexpr int OFF_VP = OFF_TI + P::NS * DIAGP;
     static constexpr int OFF_FAC = OFF_VP + NW * P::NX * VPP;
     static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
@@ -83,6 +84,9 @@ __device__ __forceinline__ Split8<NP> tile_frag(const char* base, int plane_byte
     }
     return f;
 }
+
+// Slot of the off-diagonal L^T block (sb < tb) in the compact six-tile plane.
+__device__ __forceinline__ int lt_index(int sb, int tb) { return (tb - 1) * tb / 2 + sb; }
 
 __device__ __forceinline__ float beta_value(const PrefillParams& a, const Work& wk, int64_t h, int64_t t) {
     const int64_t i = wk.b * a.b_sb + (wk.row0 + t) * a.b_st + h * a.b_sh;
@@ -302,7 +306,7 @@ struct GdnStep {
                     const int m = OUT ? n - 10 : n;  // off-diagonal L tiles: (0,1) (0,2) (1,2) (0,3) (1,3) (2,3)
                     tb = m >= 3 ? 3 : (m >= 1 ? 2 : 1);
                     sb = m - (tb - 1) * tb / 2;
-                    idx = tile_index(sb, tb);
+                    idx = m;
                 }
                 const char* rhs = is_a ? sQT : sBT;
                 f32x4 acc = zero4();
@@ -317,7 +321,7 @@ struct GdnStep {
                     for (int j = 0; j < 4; ++j) acc[j] = (4 * g4 + j > r16) ? 0.f : acc[j];
                 }
                 const float xv[4] = {acc[0], acc[1], acc[2], acc[3]};
-                lds_put_row<NS, 4>(is_a ? sAT : sLT, L::TILEP, (idx * 64 + lane) * 4, xv);
+                lds_put_row<NS, 4>(is_a ? sAT : sLT, is_a ? L::TILEP : L::LTP, (idx * 64 + lane) * 4, xv);
             }
             // Diagonal block wave of the UT transform: T_ww = (I + L_ww)^-1 by doubling, kept as
             // D-layout pairs (X, X^T) so every product reads its operands from registers.
@@ -404,14 +408,14 @@ struct GdnStep {
                 if (i >= 1) {
                     f32x4 p = zero4();
                     if (i >= 2) {  // blocks 0 and 1 together (K = 32)
-                        const Split8<NS> lf = tile_frag<NS>(sLT, L::TILEP, tile_index(0, i), tile_index(1, i), true, lane);
+                        const Split8<NS> lf = tile_frag<NS>(sLT, L::LTP, lt_index(0, i), lt_index(1, i), true, lane);
                         p = mfma_split<NS, NS, NS>(lf, split_k32<NS>(U[0], U[1]), p);
                         if (i == 3) {
-                            const Split8<NS> lf2 = tile_frag<NS>(sLT, L::TILEP, tile_index(2, 3), 0, false, lane);
+                            const Split8<NS> lf2 = tile_frag<NS>(sLT, L::LTP, lt_index(2, 3), 0, false, lane);
                             p = mfma_split<NS, NS, NS>(lf2, us[2], p);
                         }
                     } else {
-                        const Split8<NS> lf = tile_frag<NS>(sLT, L::TILEP, tile_index(0, 1), 0, false, lane);
+                        const Split8<NS> lf = tile_frag<NS>(sLT, L::LTP, lt_index(0, 1), 0, false, lane);
                         p = mfma_split<NS, NS, NS>(lf, us[0], p);
                     }
 #pragma unroll
@@ -526,7 +530,7 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel
 
 // K3: outputs of one segment from S_in[p] (in the N slot after the scan).
 template <typename TIn, typename TG>
-__global__ __launch_bounds__(256, 1) void gdn_seg_out_kernel(PrefillParams a) {
+__global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_out_kernel(PrefillParams a) {
     using L = GLay<TIn, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
@@ -561,22 +565,36 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
     }
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (a.s0) s = *reinterpret_cast<const float4*>(a.s0 + ((seq * a.H + h) * 64 + r) * 64 + cb + cq);
-    for (int64_t p = 0; p < np; ++p) {
+    // The M rows and N values of a segment do not depend on the carry: three register sets keep
+    // the loads two steps ahead of the dependent chain.
+    struct MN {
+        float4 m[16], n;
+    };
+    // Every path through the loop issues the same loads and stores (past the end: the last
+    // segment's rows are read again and the store goes to a spare slot), so the wait counts can
+    // leave the two sets in flight outstanding.
+    float* spare = a.ws_spare + ((seq * a.H + h) * 64 + r) * 64 + cb + cq;
+    auto fetch = [&](MN& x, int64_t p) {
+        const int64_t w = p0 + (p < np ? p : np - 1);
+        const float4* mrow = reinterpret_cast<const float4*>(a.ws_m + ((w * a.H + h) * 64 + r) * 64);
+#pragma unroll
+        for (int d = 0; d < 16; ++d) x.m[d] = mrow[d];
+        x.n = *reinterpret_cast<const float4*>(a.ws_state + ((w * a.H + h) * 64 + r) * 64 + cb + cq);
+    };
+    auto step = [&](const MN& x, int64_t p) {
+        const bool real = p < np;
         const int64_t w = p0 + p;
-        float* nslot = a.ws_state + ((w * a.H + h) * 64 + r) * 64 + cb + cq;
-        const float4 n = *reinterpret_cast<const float4*>(nslot);
-        *reinterpret_cast<float4*>(nslot) = s;  // S_in[p]
+        float4 acc = x.n;
+        float* dst = real ? a.ws_state + ((w * a.H + h) * 64 + r) * 64 + cb + cq : spare;
+        *reinterpret_cast<float4*>(dst) = s;  // S_in[p]
         *reinterpret_cast<float4*>(&sS[r][cq]) = s;
         __syncthreads();
-        const float* mrow = a.ws_m + ((w * a.H + h) * 64 + r) * 64;
-        float4 acc = n;
-#pragma unroll 4
-        for (int d = 0; d < 64; d += 4) {
-            const float4 m4 = *reinterpret_cast<const float4*>(mrow + d);
-            const float mv[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+            const float mv[4] = {x.m[d].x, x.m[d].y, x.m[d].z, x.m[d].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float4 sv = *reinterpret_cast<const float4*>(&sS[d + e][cq]);
+                const float4 sv = *reinterpret_cast<const float4*>(&sS[4 * d + e][cq]);
                 acc.x += mv[e] * sv.x;
                 acc.y += mv[e] * sv.y;
                 acc.z += mv[e] * sv.z;
@@ -584,7 +602,26 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
             }
         }
         __syncthreads();
-        s = acc;
+        // per-component selects: a select of whole float4 values is lowered through scratch
+        s.x = real ? acc.x : s.x;
+        s.y = real ? acc.y : s.y;
+        s.z = real ? acc.z : s.z;
+        s.w = real ? acc.w : s.w;
+    };
+    if (np > 0) {
+        MN x0, x1, x2;
+        fetch(x0, 0);
+        fetch(x1, 1);
+        const int64_t nit = (np + 2) / 3;
+        for (int64_t it = 0; it < nit; ++it) {
+            const int64_t p = 3 * it;
+            fetch(x2, p + 2);
+            step(x0, p);
+            fetch(x0, p + 3);
+            step(x1, p + 1);
+            fetch(x1, p + 4);
+            step(x2, p + 2);
+        }
     }
     if (s_final) *reinterpret_cast<float4*>(s_final + ((seq * a.H + h) * 64 + r) * 64 + cb + cq) = s;
 }

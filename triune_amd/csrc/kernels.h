@@ -34,6 +34,7 @@ struct PrefillParams {
     int64_t b_sb, b_st, b_sh;
     TokTensor kb;
     float* ws_m;           // [n_work, H, Dk, Dk] segment transition matrices
+    float* ws_spare;       // [n_seqs, H, Dk, Dv] sink for the segment scan's padding steps
 };
 
 struct ScanParams {
