@@ -6,8 +6,9 @@ fp32 state (config 1), with the batched decode step at B=256 (config 2) reported
   step (prefill) = one fast_chunk_gla forward over the whole [4, 16384, 6, 64] batch, inputs
                    resident in HBM, bf16 outputs and fp32 final states written to HBM.
   step (decode)  = one decode step for 256 sequences (H=6, D=64) on one of 12 rotating fp32
-                   state buffers (302 MB in total, larger than the 256 MB MALL); the 512-step
-                   loop is captured in a HIP graph and replayed.
+                   state buffers (302 MB in total, larger than the 256 MB MALL) with one of 12
+                   rotating q/k/v/g/o sets; the 512-step loop is captured in a HIP graph and
+                   replayed.  Also reported: the same loop with fresh inputs every step.
 
 Prints ONE JSON line.  Roofline: HBM-bound (algorithmic bytes per pass / measured pass time vs
 8 TB/s); MFMA fraction = algorithmic flops / time / 2.5 PFLOP/s (dense bf16).
@@ -85,25 +86,34 @@ def bench_decode(steps_total, dev, n_bufs=12):
     states = [s0.to(dev).clone() for _ in range(n_bufs)]
     outs = torch.empty(steps_total, B, 1, H, D, device=dev, dtype=torch.bfloat16)
 
-    def loop():
+    # Step t updates state buffer t % n_bufs.  Its q/k/v/g/o come from input set t % n_bufs (as in
+    # a model, where the projection that feeds the step rewrites the same buffers every token);
+    # the "cold" loop instead takes a fresh slice of [steps, ...] tensors every step, so the small
+    # inputs also miss every cache and TLB.
+    def loop(cold=False):
         for t in range(steps_total):
-            gla_decode_step(q[t], k[t], v[t], g[t], states[t % n_bufs], inplace=True, out=outs[t])
+            i = t if cold else t % n_bufs
+            gla_decode_step(q[i], k[i], v[i], g[i], states[t % n_bufs], inplace=True, out=outs[i])
 
-    # warm up on a side stream, then capture the whole loop in one graph
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        loop()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        loop()
-    graph.replay()
-    torch.cuda.synchronize()
+    def graphed(cold):
+        # warm up on a side stream, then capture the whole loop in one graph
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            loop(cold)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            loop(cold)
+        graph.replay()
+        torch.cuda.synchronize()
+        return graph
+
     stream = torch.cuda.current_stream()
     reps = 3
-    ms_loop = _events_time_ms(graph.replay, reps, stream)
+    ms_loop = _events_time_ms(graphed(False).replay, reps, stream)
+    ms_cold = _events_time_ms(graphed(True).replay, reps, stream)
     eager_ms = _events_time_ms(loop, 1, stream)
     step_us = ms_loop * 1e3 / steps_total
     state_bytes = B * H * D * D * 4
@@ -111,6 +121,7 @@ def bench_decode(steps_total, dev, n_bufs=12):
     return {
         "step_us": step_us,
         "eager_step_us": eager_ms * 1e3 / steps_total,
+        "cold_step_us": ms_cold * 1e3 / steps_total,
         "tok_s": B / (step_us * 1e-6),
         "step_bytes": step_bytes,
         "gbs": step_bytes / (step_us * 1e-6) / 1e9,
@@ -280,10 +291,11 @@ def main():
     if dec is not None:
         line["decode"] = {
             "workload": "batched decode step, config 2 (B=256, H=6, D=64, fp32 state, bf16 q/k/v/g/o), "
-            f"{args.decode_steps}-step graph, {dec['state_buffers']} rotating state buffers",
+            f"{args.decode_steps}-step graph, {dec['state_buffers']} rotating state buffers and input sets",
             "tok_s": round(dec["tok_s"], 1),
             "us_per_step": round(dec["step_us"], 3),
             "eager_us_per_step": round(dec["eager_step_us"], 3),
+            "cold_inputs_us_per_step": round(dec["cold_step_us"], 3),
             "roofline": {
                 "bound": "hbm",
                 "achieved": round(dec["gbs"], 1),

@@ -54,6 +54,22 @@ int64_t resident_slots(int Dk, int Dv) {
     return slots;
 }
 
+// Compute units of the current device, queried once per device (MI355X: 256).
+int device_cus() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int ncu = 0;
+    if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+        ncu = 256;
+    cache[dev] = ncu;
+    return ncu;
+}
+
 // Segments per sequence (dense): fill the resident workgroup slots once with near-equal
 // segments; never more segments than chunks.  flags bits 8..15 force a chunk count instead.
 int64_t dense_segments(int64_t B, int64_t H, int64_t nchunks, int Dk, int Dv, int flags) {
@@ -154,6 +170,7 @@ int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, cons
     if (!((Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128) ||
           (Dk == 64 && Dv == 128) || (Dk == 128 && Dv == 64)))
         return TRIUNE_ERR_SHAPE;
+    if (B > 0x7fffffff / H) return TRIUNE_ERR_SHAPE;  // rows (b, h) are indexed in 32 bits
     if (B == 0) return TRIUNE_OK;
     if (!vec_ok(q, io_dtype, strides + 0, 2) || !vec_ok(k, io_dtype, strides + 2, 2) ||
         !vec4_ok(v, io_dtype, strides + 4, 2) || !vec_ok(g, g_dtype, strides + 6, 2) ||
@@ -170,7 +187,7 @@ int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, cons
     a.o_sb = strides[8]; a.o_sh = strides[9];
     a.state_in = state_in; a.state_out = state_out; a.slots = slots;
     a.o = o; a.B = B; a.H = H;
-    return launch_status(launch_gla_decode(a, Dk, Dv, (hipStream_t)stream));
+    return launch_status(launch_gla_decode(a, Dk, Dv, 4 * device_cus(), (hipStream_t)stream));
 }
 
 size_t triune_hip_gla_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {

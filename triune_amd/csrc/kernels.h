@@ -87,7 +87,7 @@ struct GdnParams {
 };
 
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);
-hipError_t launch_gla_decode(const DecodeParams& a, int Dk, int Dv, hipStream_t stream);
+hipError_t launch_gla_decode(const DecodeParams& a, int Dk, int Dv, int max_blocks, hipStream_t stream);
 hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t stream);
 // Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).
 hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
