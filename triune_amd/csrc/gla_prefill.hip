@@ -193,22 +193,39 @@ struct OutStep {
             chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, c0, tc, nv, g4, r16, S);
         } else {
             // ---------------- stage 2: causal tiles of A^T -> LDS ----------------------------
-            for (int i = wave; i < 10; i += NW) {
-                int sb, tb;
-                tile_sb_tb(i, sb, tb);
-                f32x4 acc = zero4();
+            // Wave w owns tiles w, w + NW, ...: all of them are computed together (independent
+            // MFMA chains); a wave with one tile fewer recomputes its last tile and skips the store.
+            {
+                constexpr int MT = (10 + NW - 1) / NW;
+                int sb[MT], tb[MT];
+                f32x4 acc[MT];
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    tile_sb_tb(min(wave + t * NW, 9), sb[t], tb[t]);
+                    acc[t] = zero4();
+                }
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    const Split8<NS> kf = lds_frag<NS>(sKT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
-                    const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
-                    acc = mfma_split<NS, NS, NS>(kf, qf, acc);
-                }
-                if (sb == tb) {  // row = key 4*g4 + j, column = query r16
+                    Split8<NS> kf[MT], qf[MT];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[j] = (4 * g4 + j > r16) ? 0.f : acc[j];
+                    for (int t = 0; t < MT; ++t) {
+                        kf[t] = lds_frag<NS>(sKT, L::ROWP, L::RS, 16 * sb[t] + r16, 32 * ks, g4);
+                        qf[t] = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb[t] + r16, 32 * ks, g4);
+                    }
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) acc[t] = mfma_split<NS, NS, NS>(kf[t], qf[t], acc[t]);
                 }
-                const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-                lds_put_row<NS, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
+#pragma unroll
+                for (int t = 0; t < MT; ++t) {
+                    const int i = wave + t * NW;
+                    if (i >= 10) continue;
+                    if (sb[t] == tb[t]) {  // row = key 4*g4 + j, column = query r16
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[t][j] = (4 * g4 + j > r16) ? 0.f : acc[t][j];
+                    }
+                    const float x[4] = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
+                    lds_put_row<NS, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
+                }
             }
             __syncthreads();
 
