@@ -27,6 +27,8 @@ import time
 
 import torch
 
+from triune_amd._lib import check, lib
+
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "GLA prefill tok/s @B4 H6 T16k D64 (MFMA %); decode tok/s @B256 (HBM GB/s %)"
@@ -56,23 +58,44 @@ def bench_prefill(steps, warmup, dev):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    t0 = time.perf_counter()
-    ms = _events_time_ms(fn, steps, stream)
+    # One event pair per pass, recorded by the library on this stream around the output kernel
+    # (the dominant of the pass's three kernels); torch creates an event on its first record.
+    k3 = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for b, e in k3:
+        b.record(stream)
+        e.record(stream)
     torch.cuda.synchronize()
+    L = lib()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    try:
+        for b, e in k3:
+            check(L.triune_hip_set_output_kernel_events(b._as_parameter_, e._as_parameter_), "arm events")
+            fn()
+    finally:
+        L.triune_hip_set_output_kernel_events(None, None)
+    end.record(stream)
+    end.synchronize()
     wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / steps
+    k3_ms = sum(b.elapsed_time(e) for b, e in k3) / steps
     n_th = B * T * H
-    alg_bytes = gla_algorithmic_bytes(n_th, D, D, 2, 2, 2) + 2 * B * H * D * D * 4  # + S0 read, S write
+    k3_bytes = gla_algorithmic_bytes(n_th, D, D, 2, 2, 2)  # q, k, g, v read and o written once
+    alg_bytes = k3_bytes + 2 * B * H * D * D * 4  # the pass also reads S0 and writes the final S
     alg_flops = gla_algorithmic_flops(n_th, D, D)
-    gbs = alg_bytes / (ms * 1e-3) / 1e9
-    tflops = alg_flops / (ms * 1e-3) / 1e12
     return {
         "ms": ms,
         "wall_s": wall,
         "tok_s": B * T / (ms * 1e-3),
         "alg_bytes": alg_bytes,
         "alg_flops": alg_flops,
-        "gbs": gbs,
-        "tflops": tflops,
+        "gbs": alg_bytes / (ms * 1e-3) / 1e9,
+        "tflops": alg_flops / (ms * 1e-3) / 1e12,
+        "k3_ms": k3_ms,
+        "k3_bytes": k3_bytes,
+        "k3_gbs": k3_bytes / (k3_ms * 1e-3) / 1e9,
     }
 
 
@@ -129,14 +152,15 @@ def bench_decode(steps_total, dev, n_bufs=12):
     }
 
 
-def bench_gdn(dev, reps=3):
+def bench_gdn(dev, reps=10):
     """Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta and decay)."""
     from triune_amd import fast_chunk_gated_deltanet
     from triune_amd.workloads import config3
 
     q, k, v, g, beta = (x.to(dev) for x in config3())
     fn = lambda: fast_chunk_gated_deltanet(q, k, v, g, beta=beta)  # noqa: E731
-    fn()
+    for _ in range(3):
+        fn()
     torch.cuda.synchronize()
     ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
     B, T = q.shape[0], q.shape[1]
@@ -199,14 +223,14 @@ def cpu_baseline(budget_s=12.0):
     }
 
 
-def _traffic_from_profiles():
-    """HBM bytes per prefill pass measured with rocprofv3 FETCH_SIZE / WRITE_SIZE counters and
-    scaled by the same counters on a copy of known size (profiles/prefill_traffic.json, written
-    from those runs); None when no measurement has been recorded."""
+def _traffic_from_profiles(key="output_kernel_bytes_per_launch"):
+    """HBM bytes per output-kernel launch (or per pass) measured with rocprofv3 FETCH_SIZE /
+    WRITE_SIZE counters and scaled by the same counters on a copy of known size
+    (profiles/prefill_traffic.json, written from those runs); None when nothing is recorded."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "prefill_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get("bytes_per_pass")
+            return json.load(f).get(key)
     except (OSError, ValueError):
         return None
 
@@ -228,6 +252,12 @@ def main():
         help="only run a plain device copy of MIB MiB (steps times): the known-size reference used to "
         "scale rocprofv3 FETCH_SIZE / WRITE_SIZE readings",
     )
+    ap.add_argument(
+        "--only",
+        choices=("decode", "gdn", "varlen"),
+        default=None,
+        help="profiling aid: run one secondary workload alone and print its own JSON line",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -245,6 +275,13 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_mib": args.copy_probe, "launches": args.steps}), flush=True)
+        return
+    if args.only:
+        if args.only == "decode":
+            res = bench_decode(args.decode_steps, dev)
+        else:
+            res = bench_gdn(dev) if args.only == "gdn" else bench_varlen(dev)
+        print(json.dumps({"only": args.only, **res}), flush=True)
         return
     pre = bench_prefill(args.steps, args.warmup, dev)
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
@@ -276,13 +313,21 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(pre["gbs"], 1),
+            "achieved": round(pre["k3_gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(pre["gbs"] / HBM_PEAK_GBS, 4),
+            "frac": round(pre["k3_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": _traffic_from_profiles(),
-            "kernel": "prefill pass = gla_seg_state + seg_scan_f32 + gla_seg_output (event-timed together)",
-            "alg_bytes_per_pass": pre["alg_bytes"],
+            "kernel": "gla_seg_output_kernel<bf16,bf16,64,64> (HIP events around each launch)",
+            "kernel_us": round(pre["k3_ms"] * 1e3, 2),
+            "alg_bytes_per_launch": pre["k3_bytes"],
+            "pass": {
+                "kernels": "gla_seg_state + seg_scan_f32 + gla_seg_output",
+                "alg_bytes": pre["alg_bytes"],
+                "achieved_gbs": round(pre["gbs"], 1),
+                "frac": round(pre["gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": _traffic_from_profiles("bytes_per_pass"),
+            },
             "mfma_alg_tflops": round(pre["tflops"], 2),
             "mfma_alg_frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
         },

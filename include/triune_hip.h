@@ -74,6 +74,13 @@ enum {
 int triune_hip_abi_version(void);
 const char* triune_hip_error_string(int code);
 
+/* Measurement hook (no reference counterpart; for benchmarks and profilers): arm two hipEvent_t
+ * (passed as void*) that the following GLA prefill calls (dense and varlen) of this host thread
+ * record on their stream immediately before and after the output kernel (the dominant one of the
+ * three), so its duration can be read with hipEventElapsedTime.  Both NULL disarms; exactly one
+ * NULL returns TRIUNE_ERR_NULL.  Recording adds no device work. */
+int triune_hip_set_output_kernel_events(void* begin, void* end);
+
 /* Batched recurrent decode step, for every row (b, h):
  *     S <- diag(exp(g)) S + k v^T ;   o = S^T q          (g is NOT clamped, as in the reference)
  * q, k, g: [B, 1, H, Dk] (g may be fp32 when q/k/v are 16-bit: g_dtype), v: [B, 1, H, Dv],

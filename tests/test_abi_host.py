@@ -55,6 +55,13 @@ def test_error_strings_and_codes_match_header():
 _FAKE = ctypes.c_void_p(0x1000)  # 16-byte aligned, never dereferenced: validation fails first
 
 
+def test_output_kernel_event_hook_arms_and_disarms():
+    lib = L.lib()
+    assert lib.triune_hip_set_output_kernel_events(_FAKE, None) == -1  # exactly one NULL
+    assert lib.triune_hip_set_output_kernel_events(None, _FAKE) == -1
+    assert lib.triune_hip_set_output_kernel_events(None, None) == 0  # disarmed (nothing recorded)
+
+
 def _st(n):
     return (ctypes.c_int64 * n)(*([64] * n))
 

@@ -39,6 +39,7 @@ def _bind(lib):
     sig = {
         "triune_hip_abi_version": ([], _i),
         "triune_hip_error_string": ([_i], ctypes.c_char_p),
+        "triune_hip_set_output_kernel_events": ([_vp, _vp], _i),
         "triune_hip_gla_decode_step": (
             [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _vp, _vp, _i, _i64, _i64, _i, _i, _vp],
             _i,
@@ -75,6 +76,7 @@ def _bind(lib):
 EXPORTS = (
     "triune_hip_abi_version",
     "triune_hip_error_string",
+    "triune_hip_set_output_kernel_events",
     "triune_hip_gla_decode_step",
     "triune_hip_gla_prefill_workspace_size",
     "triune_hip_gla_prefill",

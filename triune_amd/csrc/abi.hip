@@ -141,11 +141,34 @@ PrefillPlan plan_varlen(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,
 
 int launch_status(hipError_t e) { return e == hipSuccess ? TRIUNE_OK : TRIUNE_ERR_LAUNCH; }
 
+// Events armed by triune_hip_set_output_kernel_events for this host thread (null: disarmed).
+struct OutputEvents {
+    hipEvent_t begin = nullptr, end = nullptr;
+};
+thread_local OutputEvents g_output_events;
+
+// The GLA output kernel, bracketed by the armed events on the same stream.
+int launch_output_timed(const PrefillParams& a, int64_t n_work, int io_dtype, hipStream_t st) {
+    const OutputEvents ev = g_output_events;
+    if (ev.begin && hipEventRecord(ev.begin, st) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    const int rc = launch_status(launch_gla_seg_output(a, n_work, io_dtype, st));
+    if (rc != TRIUNE_OK) return rc;
+    if (ev.end && hipEventRecord(ev.end, st) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    return TRIUNE_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 int triune_hip_abi_version(void) { return TRIUNE_HIP_ABI_VERSION; }
+
+int triune_hip_set_output_kernel_events(void* begin, void* end) {
+    if ((begin == nullptr) != (end == nullptr)) return TRIUNE_ERR_NULL;
+    g_output_events.begin = reinterpret_cast<hipEvent_t>(begin);
+    g_output_events.end = reinterpret_cast<hipEvent_t>(end);
+    return TRIUNE_OK;
+}
 
 const char* triune_hip_error_string(int code) {
     switch (code) {
@@ -262,7 +285,7 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     e = launch_recurrent_scan(sc, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
 
-    return launch_status(launch_gla_seg_output(a, pl.n_work, io_dtype, st));
+    return launch_output_timed(a, pl.n_work, io_dtype, st);
 }
 
 size_t triune_hip_gla_prefill_varlen_workspace_size(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,
@@ -330,7 +353,7 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
     sc.n_outer = n_seqs; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.seg_off = seg_off;
     e = launch_recurrent_scan(sc, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
-    if (pl.n_work > 0) return launch_status(launch_gla_seg_output(a, pl.n_work, io_dtype, st));
+    if (pl.n_work > 0) return launch_output_timed(a, pl.n_work, io_dtype, st);
     return TRIUNE_OK;
 }
 

@@ -15,8 +15,9 @@
 // with each 16x16 unit-lower inverse T_ii = prod_k (I + M^(2^k)), M = -L_ii, by doubling.
 // The chunk map S0 -> S_C is affine with a full Dk x Dk matrix, so segments compose as
 // S_in[p+1] = M_p S_in[p] + N_p:
-//   K1 gdn_seg_mn   : per (segment, head, half) the segment map applied to [I | 0] (half 0 -> M_p,
-//                     V replaced by 0) or to 0 with the real V (half 1 -> N_p)
+//   K1 gdn_seg_mn   : per (segment, head) the segment map applied to [I | 0] with V replaced by 0
+//                     (-> M_p) and to 0 with the real V (-> N_p), sharing the per-chunk factors,
+//                     tiles and inverses
 //   K2 gdn_seg_scan : per (sequence, head, 16 columns) the carry S_in[p] (written in place of N_p)
 //   K3 gdn_seg_out  : per (segment, head) the chunk walk from S_in[p], writing o
 // Products run on v_mfma_f32_16x16x32_bf16 with operands split into bf16 parts (2 for 16-bit
@@ -165,8 +166,9 @@ __device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG>& c, const ChunkAdd
     }
 }
 
-// One chunk of the GDN walk for (segment, head).  OUT: outputs (K3); otherwise the state map only
-// (K1; with_v false drives it with V = 0).
+// One chunk of the GDN walk for (segment, head).  OUT: outputs from the state S (K3).  Otherwise
+// (K1) the segment map on two states at once: S driven with V = 0 (the M columns) and SN with
+// the real V (the N columns); stages 1-2 (factors, tiles, inverses) are shared by both.
 template <typename TIn, typename TG, bool OUT>
 struct GdnStep {
     using L = GLay<TIn, OUT>;
@@ -175,7 +177,7 @@ struct GdnStep {
 
     template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                               const GChunkIn<TIn, TG>& cur, bool with_v, f32x4 (&S)[4], char* smem,
+                               const GChunkIn<TIn, TG>& cur, f32x4 (&S)[4], f32x4 (&SN)[4], char* smem,
                                Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
@@ -267,17 +269,11 @@ struct GdnStep {
                 for (int i = 0; i < DL; ++i) x[j][i] = kx[j][i] * bkx[j][i] * __builtin_amdgcn_rcpf(fq[j][i]);
                 lds_put_row<NS, DL>(sWT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
-            // V rows of this wave's columns (zero when the map is driven without V)
+            // V rows of this wave's columns
             float vx[4][4];
             chunk_float(cur.x.v, vx, tg, nv);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (!with_v) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) vx[j][c] = 0.f;
-                }
-                lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
-            }
+            for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
         after_inputs();
         __syncthreads();
@@ -285,7 +281,8 @@ struct GdnStep {
 #pragma unroll
         for (int w = 0; w < 4; ++w) fast = fast && (sFLAG[w] == 0);
         if (!fast) {
-            gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, with_v, S);
+            gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
+            if (!OUT) gdn_tokenwise<TIn, TG, false>(a, wk, h, c0, tc, nv, g4, r16, true, SN);
             __syncthreads();
             return;
         }
@@ -367,13 +364,15 @@ struct GdnStep {
         __syncthreads();
 
         // ---------------- stage 3: residuals, UT solve, outputs, state ----------------------
-        {
+        // One pass per state: K3 runs it on S with V; K1 on S with V = 0 and on SN with V.
+        auto pass = [&](auto with_v, f32x4 (&St)[4]) {
+            constexpr bool WV = decltype(with_v)::value;
             f32x4 Sp[4];
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
                 const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) Sp[db][i] = S[db][i] * em[i];
+                for (int i = 0; i < 4; ++i) Sp[db][i] = St[db][i] * em[i];
             }
             Split8<NS> sf[2];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
 #pragma unroll
@@ -388,13 +387,15 @@ struct GdnStep {
                     const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4);
                     p = mfma_split<NS, NS, NS>(bf, sf[ks], p);
                 }
-                const int off = (16 * i + 4 * g4 + (r16 >> 2)) * L::VS + 4 * (r16 & 3);
                 f32x4 vv = zero4();
+                if constexpr (WV) {
+                    const int off = (16 * i + 4 * g4 + (r16 >> 2)) * L::VS + 4 * (r16 & 3);
 #pragma unroll
-                for (int pl = 0; pl < NX; ++pl) {
-                    const bf16x4 t4 = lds_read_tr(reinterpret_cast<const __bf16*>(sVP + pl * L::VPP) + off);
+                    for (int pl = 0; pl < NX; ++pl) {
+                        const bf16x4 t4 = lds_read_tr(reinterpret_cast<const __bf16*>(sVP + pl * L::VPP) + off);
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) vv[k] += (float)t4[k];
+                        for (int k = 0; k < 4; ++k) vv[k] += (float)t4[k];
+                    }
                 }
 #pragma unroll
                 for (int k = 0; k < 4; ++k) R[i][k] = vv[k] - p[k];
@@ -430,7 +431,7 @@ struct GdnStep {
 #pragma unroll
             for (int k2 = 0; k2 < 2; ++k2) uf[k2] = split_k32<NS>(U[2 * k2], U[2 * k2 + 1]);
 
-            if (OUT) {
+            if constexpr (OUT) {
                 f32x4 Ot[4];
 #pragma unroll
                 for (int tb = 0; tb < 4; ++tb) {
@@ -477,15 +478,23 @@ struct GdnStep {
                 }
                 const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) S[db][i] = em[i] * acc[i];
+                for (int i = 0; i < 4; ++i) St[db][i] = em[i] * acc[i];
             }
+        };
+        if constexpr (OUT) {
+            pass(std::true_type{}, S);
+        } else {
+            pass(std::false_type{}, S);
+            __builtin_amdgcn_sched_barrier(0);  // one pass at a time: their temporaries never overlap
+            pass(std::true_type{}, SN);
         }
         __syncthreads();  // the next chunk rewrites LDS
     }
 };
 
 template <typename TIn, typename TG, bool OUT>
-__device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, bool with_v, f32x4 (&S)[4], char* smem) {
+__device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[4], f32x4 (&SN)[4],
+                         char* smem) {
     using St = GdnStep<TIn, TG, OUT>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<OUT, TIn, TG>(a, wk, h, tg, wave * 16 + 4 * row, wave * 16 + 4 * row);
@@ -501,31 +510,38 @@ __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, bool
     GChunkIn<TIn, TG> A;
     gchunk_load<OUT>(A, ad, kb, key_beta, tok(0), true);
     for (int64_t c = 0; c < nch; ++c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, with_v, S, smem,
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, SN, smem,
                 [&] { gchunk_load<OUT>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch); });
 }
 
-// K1: blockIdx.z = 0 -> M_p (state [I | .], V = 0), 1 -> N_p (state 0, real V).
+// K1: the segment map driven from [I | 0] with V = 0 (-> M_p, state M) and from 0 with the real
+// V (-> N_p, state N) in one chunk walk.
 template <typename TIn, typename TG>
 __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel(PrefillParams a) {
     using L = GLay<TIn, false>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
-    const bool is_m = blockIdx.z == 0;
     Work wk;
     if (!find_work(a, w, wk)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
-    f32x4 S[4];
+    f32x4 M[4], N[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S[db][i] = (is_m && 16 * db + 4 * g4 + i == 16 * wave + r16) ? 1.f : 0.f;
-    gdn_walk<TIn, TG, false>(a, wk, h, !is_m, S, smem);
-    float* dst = (is_m ? a.ws_m : a.ws_state) + (w * a.H + h) * (int64_t)64 * 64;
+        for (int i = 0; i < 4; ++i) {
+            M[db][i] = (16 * db + 4 * g4 + i == 16 * wave + r16) ? 1.f : 0.f;
+            N[db][i] = 0.f;
+        }
+    gdn_walk<TIn, TG, false>(a, wk, h, M, N, smem);
+    float* dm = a.ws_m + (w * a.H + h) * (int64_t)64 * 64;
+    float* dn = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[state_off(db, i, g4, r16, wave, 64)] = S[db][i];
+        for (int i = 0; i < 4; ++i) {
+            dm[state_off(db, i, g4, r16, wave, 64)] = M[db][i];
+            dn[state_off(db, i, g4, r16, wave, 64)] = N[db][i];
+        }
 }
 
 // K3: outputs of one segment from S_in[p] (in the N slot after the scan).
@@ -543,7 +559,7 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_out_kerne
     for (int db = 0; db < 4; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, 64)];
-    gdn_walk<TIn, TG, true>(a, wk, h, true, S, smem);
+    gdn_walk<TIn, TG, true>(a, wk, h, S, S, smem);
 }
 
 // K2: per (sequence, head, 16 columns): S_in[p] = carry, written in place of N_p; then
@@ -632,7 +648,7 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
 template <typename TIn, typename TG>
 static hipError_t launch_gdn_t(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
     if (which == 0) {
-        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG>), dim3((unsigned)n_work, (unsigned)a.H, 2), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
     } else {
         hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
     }

@@ -264,7 +264,13 @@ def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None):
     qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, _gate(g, q)))
     vp = _vec_layout(_pad_last(v, Dv))
     odt = out.dtype if out is not None else v.dtype
-    o = torch.empty(N, H, Dv, device=q.device, dtype=odt)
+    o = None
+    if out is not None and Dv == Dv0:
+        ov = out[0] if out.dim() == 4 else out
+        if tuple(ov.shape) == (N, H, Dv) and ov.stride(-1) == 1 and _vec_layout(ov) is ov:
+            o = ov  # write straight into the caller's buffer
+    if o is None:
+        o = torch.empty(N, H, Dv, device=q.device, dtype=odt)
     s0 = _state_in(initial_state, Dk, Dv)
     sf = torch.empty(n, H, Dk, Dv, device=q.device, dtype=torch.float32)
     L = lib()
@@ -279,11 +285,12 @@ def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None):
     o = o[..., :Dv0]
     if Dk != Dk0 or Dv != Dv0:
         sf = sf[..., :Dk0, :Dv0].contiguous()
+    if out is not None:
+        if o.data_ptr() != out.data_ptr():
+            out.copy_(o.reshape(out.shape))
+        return out, sf
     if lead1:
         o = o.unsqueeze(0)
-    if out is not None:
-        out.copy_(o)
-        o = out
     return o, sf
 
 
