@@ -448,7 +448,7 @@ GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H) {
     if (p.nseg > nchunks) p.nseg = nchunks;
     p.n_work = B * p.nseg;
     p.off_m = align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
-    p.off_spare = p.off_m + align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
+    p.off_spare = p.off_m + align_up((size_t)p.n_work * H * 3 * 64 * 64 * 2);  // up to 3 bf16 parts of M
     p.total = p.off_spare + align_up((size_t)B * H * 64 * 64 * sizeof(float));
     return p;
 }
@@ -522,7 +522,7 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
 
     hipError_t e = launch_gdn_seg_mn(a, pl.n_work, io_dtype, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
-    e = launch_gdn_seg_scan(a, s_final, st);
+    e = launch_gdn_seg_scan(a, s_final, io_dtype, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
     return launch_status(launch_gdn_seg_out(a, pl.n_work, io_dtype, st));
 }

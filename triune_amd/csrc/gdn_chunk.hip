@@ -27,6 +27,16 @@
 
 namespace triune {
 
+// Workspace layouts shared by the three segment kernels, both chosen so that every lane moves
+// whole 16-byte vectors:
+//  - M_p: up to 3 bf16 parts, each stored as the scan's A-operand fragments: element j of lane L
+//    for row tile t and K step kk at ((part*4 + t)*2 + kk)*512 + 8L + j;
+//  - N_p / S_in[p]: fp32 in MFMA D layout, element i of lane L for column strip c (16 columns)
+//    and row tile t at ((c*4 + t)*64 + L)*4 + i.
+constexpr int64_t MSLOT = 3 * 64 * 64;
+
+__device__ __forceinline__ int64_t dstate_off(int strip, int t, int lane) { return ((strip * 4 + t) * 64 + lane) * 4; }
+
 template <typename TIn, bool OUT>
 struct GLay {
     using P = Prec<TIn>;
@@ -533,15 +543,28 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel
             N[db][i] = 0.f;
         }
     gdn_walk<TIn, TG, false>(a, wk, h, M, N, smem);
-    float* dm = a.ws_m + (w * a.H + h) * (int64_t)64 * 64;
+    // M goes out already split into NS bf16 parts (the scan's MFMA operands): NS planes of
+    // [64][64] row-major per (segment, head), slot stride MSLOT elements
+    // M[16db + 4g4 + i][16w + r16] is element j = 4(w&1) + (r16&3) of scan lane
+    // 16(r16>>2) + 4g4 + i for row tile db and K step w>>1.
+    constexpr int NS = Prec<TIn>::NS;
+    __bf16* dm = reinterpret_cast<__bf16*>(a.ws_m) + (w * a.H + h) * (int64_t)MSLOT;
     float* dn = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            dm[state_off(db, i, g4, r16, wave, 64)] = M[db][i];
-            dn[state_off(db, i, g4, r16, wave, 64)] = N[db][i];
+            float m = M[db][i];
+            const int sl = 16 * (r16 >> 2) + 4 * g4 + i, j = 4 * (wave & 1) + (r16 & 3);
+#pragma unroll
+            for (int pl = 0; pl < NS; ++pl) {
+                const __bf16 hi = (__bf16)m;
+                dm[((pl * 4 + db) * 2 + (wave >> 1)) * 512 + 8 * sl + j] = hi;
+                m -= (float)hi;
+            }
         }
+        *reinterpret_cast<f32x4*>(dn + dstate_off(wave, db, lane)) = N[db];
+    }
 }
 
 // K3: outputs of one segment from S_in[p] (in the N slot after the scan).
@@ -556,19 +579,21 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_out_kerne
     f32x4 S[4];
     const float* st = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, 64)];
+    for (int db = 0; db < 4; ++db) S[db] = *reinterpret_cast<const f32x4*>(st + dstate_off(wave, db, lane));
     gdn_walk<TIn, TG, true>(a, wk, h, S, S, smem);
 }
 
-// K2: per (sequence, head, 16 columns): S_in[p] = carry, written in place of N_p; then
-// S <- M_p S + N_p.  256 threads: thread (row r = tid / 4, columns 4*(tid % 4) .. +3).
-__global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
-    __shared__ __attribute__((aligned(16))) float sS[64][16];
+// K2: one wave per (sequence, head, 16 state columns): S_in[p] = carry (written in place of N_p),
+// then S <- M_p S + N_p on MFMA.  The wave's 64x16 strip of S lives in D layout (tile t holds
+// rows 16t + 4*g4 + i, column r16), which is also the B operand of the next product once split;
+// M_p arrives pre-split in NS bf16 planes and is read straight into A-operand layout (row
+// 16t + r16, K slots 32kk + pi(g4, j)).  The M/N loads of a segment do not depend on the carry:
+// three register sets keep them two segments ahead.
+template <int NS>
+__global__ __launch_bounds__(64) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
     const int64_t seq = blockIdx.z, h = blockIdx.y;
     const int cb = blockIdx.x * 16;
-    const int tid = threadIdx.x, r = tid >> 2, cq = 4 * (tid & 3);
+    const int lane = threadIdx.x, r16 = lane & 15, g4 = lane >> 4;
     int64_t p0, np;
     if (a.varlen) {
         p0 = a.seg_off[seq];
@@ -579,50 +604,49 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
         np = a.nseg_dense < nch ? a.nseg_dense : nch;
         if (a.T == 0) np = 0;
     }
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (a.s0) s = *reinterpret_cast<const float4*>(a.s0 + ((seq * a.H + h) * 64 + r) * 64 + cb + cq);
-    // The M rows and N values of a segment do not depend on the carry: three register sets keep
-    // the loads two steps ahead of the dependent chain.
+    auto d_off = [&](int t, int i) { return (16 * t + 4 * g4 + i) * 64 + cb + r16; };  // D-layout element
+    f32x4 S[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[t][i] = a.s0 ? a.s0[(seq * a.H + h) * 4096 + d_off(t, i)] : 0.f;
     struct MN {
-        float4 m[16], n;
+        Split8<NS> m[4][2];  // [row tile][K step]
+        f32x4 n[4];
     };
-    // Every path through the loop issues the same loads and stores (past the end: the last
-    // segment's rows are read again and the store goes to a spare slot), so the wait counts can
-    // leave the two sets in flight outstanding.
-    float* spare = a.ws_spare + ((seq * a.H + h) * 64 + r) * 64 + cb + cq;
+    // Every path issues the same loads and stores (past the end: the last segment's rows again,
+    // and the store goes to a spare slot), so the wait counts leave the sets in flight.
+    float* spare = a.ws_spare + (seq * a.H + h) * 4096;
     auto fetch = [&](MN& x, int64_t p) {
         const int64_t w = p0 + (p < np ? p : np - 1);
-        const float4* mrow = reinterpret_cast<const float4*>(a.ws_m + ((w * a.H + h) * 64 + r) * 64);
+        const __bf16* mp = reinterpret_cast<const __bf16*>(a.ws_m) + (w * a.H + h) * (int64_t)MSLOT;
+        const float* np_ = a.ws_state + (w * a.H + h) * 4096;
 #pragma unroll
-        for (int d = 0; d < 16; ++d) x.m[d] = mrow[d];
-        x.n = *reinterpret_cast<const float4*>(a.ws_state + ((w * a.H + h) * 64 + r) * 64 + cb + cq);
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int pl = 0; pl < NS; ++pl)
+                    x.m[t][kk].p[pl] = *reinterpret_cast<const bf16x8*>(mp + ((pl * 4 + t) * 2 + kk) * 512 + 8 * lane);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x.n[t] = *reinterpret_cast<const f32x4*>(np_ + dstate_off(blockIdx.x, t, lane));
     };
     auto step = [&](const MN& x, int64_t p) {
         const bool real = p < np;
-        const int64_t w = p0 + p;
-        float4 acc = x.n;
-        float* dst = real ? a.ws_state + ((w * a.H + h) * 64 + r) * 64 + cb + cq : spare;
-        *reinterpret_cast<float4*>(dst) = s;  // S_in[p]
-        *reinterpret_cast<float4*>(&sS[r][cq]) = s;
-        __syncthreads();
+        float* dst = real ? a.ws_state + ((p0 + p) * a.H + h) * 4096 : spare;
 #pragma unroll
-        for (int d = 0; d < 16; ++d) {
-            const float mv[4] = {x.m[d].x, x.m[d].y, x.m[d].z, x.m[d].w};
+        for (int t = 0; t < 4; ++t) *reinterpret_cast<f32x4*>(dst + dstate_off(blockIdx.x, t, lane)) = S[t];  // S_in[p]
+        Split8<NS> sb[2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float4 sv = *reinterpret_cast<const float4*>(&sS[4 * d + e][cq]);
-                acc.x += mv[e] * sv.x;
-                acc.y += mv[e] * sv.y;
-                acc.z += mv[e] * sv.z;
-                acc.w += mv[e] * sv.w;
-            }
+        for (int kk = 0; kk < 2; ++kk) sb[kk] = split_k32<NS>(S[2 * kk], S[2 * kk + 1]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            f32x4 acc = x.n[t];
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) acc = mfma_split<NS, NS, NS>(x.m[t][kk], sb[kk], acc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[t][i] = real ? acc[i] : S[t][i];
         }
-        __syncthreads();
-        // per-component selects: a select of whole float4 values is lowered through scratch
-        s.x = real ? acc.x : s.x;
-        s.y = real ? acc.y : s.y;
-        s.z = real ? acc.z : s.z;
-        s.w = real ? acc.w : s.w;
     };
     if (np > 0) {
         MN x0, x1, x2;
@@ -639,7 +663,12 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
             step(x2, p + 2);
         }
     }
-    if (s_final) *reinterpret_cast<float4*>(s_final + ((seq * a.H + h) * 64 + r) * 64 + cb + cq) = s;
+    if (s_final) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s_final[(seq * a.H + h) * 4096 + d_off(t, i)] = S[t][i];
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -677,8 +706,10 @@ hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt,
     return launch_gdn(a, n_work, io_dt, 1, stream);
 }
 
-hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, hipStream_t stream) {
-    hipLaunchKernelGGL(gdn_seg_scan_kernel, dim3(4, (unsigned)a.H, (unsigned)a.n_seqs), dim3(256), 0, stream, a, s_final);
+hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream) {
+    const dim3 grid(4, (unsigned)a.H, (unsigned)a.n_seqs);
+    if (io_dt == DT_F32) hipLaunchKernelGGL(gdn_seg_scan_kernel<3>, grid, dim3(64), 0, stream, a, s_final);
+    else hipLaunchKernelGGL(gdn_seg_scan_kernel<2>, grid, dim3(64), 0, stream, a, s_final);
     return hipGetLastError();
 }
 

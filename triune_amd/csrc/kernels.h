@@ -33,7 +33,7 @@ struct PrefillParams {
     int beta_dt, beta_kind;
     int64_t b_sb, b_st, b_sh;
     TokTensor kb;
-    float* ws_m;           // [n_work, H, Dk, Dk] segment transition matrices
+    float* ws_m;           // GDN: [n_work, H] slots of the segment transition matrices as bf16 parts
     float* ws_spare;       // [n_seqs, H, Dk, Dv] sink for the segment scan's padding steps
 };
 
@@ -94,7 +94,7 @@ hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_d
 hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream);
 hipError_t launch_gdn_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
-hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, hipStream_t stream);
+hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream);
 hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 int gdn_seg_out_blocks_per_cu();
 bool prefill_shape_supported(int Dk, int Dv);
