@@ -395,6 +395,24 @@ __device__ __forceinline__ void chunk_suffix(const float (&g)[4][DL], float (&X)
 
 
 // S tile db of wave w: element i is S[16*db + 4*g4 + i][16*w + r16].
+// Four fp32 values (one D-layout column piece) as a K=16 operand: K slots 0..3, zeros above.
+template <int NP>
+__device__ __forceinline__ Split8<NP> split_k16(const f32x4& v) {
+    const float x[8] = {v[0], v[1], v[2], v[3], 0.f, 0.f, 0.f, 0.f};
+    return split8<NP>(x);
+}
+
+// Two D-layout tiles stacked along K (rows of tile lo in slots 0..3, of tile hi in 4..7): the
+// B operand (or the A operand of the transpose) of a K=32 product.
+template <int NP>
+__device__ __forceinline__ Split8<NP> split_k32(const f32x4& lo, const f32x4& hi) {
+    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return split8<NP>(x);
+}
+
+// Wave index within the workgroup as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 __device__ __forceinline__ int64_t state_off(int db, int i, int g4, int r16, int wave, int Dv) {
     return (int64_t)(16 * db + 4 * g4 + i) * Dv + 16 * wave + r16;
 }

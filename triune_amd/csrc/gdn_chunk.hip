@@ -62,19 +62,6 @@ struct GLay {
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-// Four fp32 values (one D-layout column piece) as a K=16 operand: K slots 0..3, zeros above.
-template <int NP>
-__device__ __forceinline__ Split8<NP> split_k16(const f32x4& v) {
-    const float x[8] = {v[0], v[1], v[2], v[3], 0.f, 0.f, 0.f, 0.f};
-    return split8<NP>(x);
-}
-
-template <int NP>
-__device__ __forceinline__ Split8<NP> split_k32(const f32x4& lo, const f32x4& hi) {
-    const float x[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    return split8<NP>(x);
-}
-
 // Tile fragment from a tile plane set: lane values at (tile, lane) in K slots 0..3 (K=16), or two
 // tiles in slots 0..3 / 4..7 (K=32).
 template <int NP>
@@ -189,7 +176,7 @@ struct GdnStep {
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
                                const GChunkIn<TIn, TG>& cur, f32x4 (&S)[4], f32x4 (&SN)[4], char* smem,
                                Hook&& after_inputs) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+        const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int c0 = wave * 16;
         const int dl0 = wave * 16 + DL * row;
@@ -506,7 +493,7 @@ template <typename TIn, typename TG, bool OUT>
 __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[4], f32x4 (&SN)[4],
                          char* smem) {
     using St = GdnStep<TIn, TG, OUT>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane >> 2, row = lane & 3;
+    const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<OUT, TIn, TG>(a, wk, h, tg, wave * 16 + 4 * row, wave * 16 + 4 * row);
     const bool key_beta = a.beta_kind == BETA_KEY;
     TokAddr kb{};
@@ -533,7 +520,7 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     f32x4 M[4], N[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -575,7 +562,7 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_out_kerne
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     f32x4 S[4];
     const float* st = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
 #pragma unroll

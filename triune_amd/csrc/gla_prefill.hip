@@ -122,7 +122,7 @@ struct OutStep {
     template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
                                const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, Hook&& after_inputs) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+        const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int d0 = wave * DPW, c0 = wave * 16;
         const int dl0 = d0 + DL * row;  // first key dim of this lane in stage 1
@@ -215,15 +215,16 @@ struct OutStep {
 #pragma unroll
                     for (int t = 0; t < MT; ++t) acc[t] = mfma_split<NS, NS, NS>(kf[t], qf[t], acc[t]);
                 }
+                // causal mask of a diagonal tile (row = key 4*g4 + j, column = query r16) as factors
+                f32x4 diag;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) diag[j] = (4 * g4 + j > r16) ? 0.f : 1.f;
 #pragma unroll
                 for (int t = 0; t < MT; ++t) {
                     const int i = wave + t * NW;
                     if (i >= 10) continue;
-                    if (sb[t] == tb[t]) {  // row = key 4*g4 + j, column = query r16
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) acc[t][j] = (4 * g4 + j > r16) ? 0.f : acc[t][j];
-                    }
-                    const float x[4] = {acc[t][0], acc[t][1], acc[t][2], acc[t][3]};
+                    const f32x4 m = sb[t] == tb[t] ? diag : f32x4{1.f, 1.f, 1.f, 1.f};
+                    const float x[4] = {acc[t][0] * m[0], acc[t][1] * m[1], acc[t][2] * m[2], acc[t][3] * m[3]};
                     lds_put_row<NS, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
                 }
             }
@@ -316,7 +317,7 @@ template <typename TIn, typename TG, int DK, int DV>
 __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
     using St = OutStep<TIn, TG, DK, DV>;
     constexpr int DL = St::DL;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane >> 2, row = lane & 3;
+    const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<true, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
     const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
     auto chunk_nv = [&](int64_t c) {
@@ -351,7 +352,7 @@ struct StateStep {
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t tc, int nv,
                                const ChunkIn<TIn, TG, DL>& cur, f32x4 (&Lst)[NDB], float (&Gseg)[DL], char* smem,
                                Hook&& after_inputs) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+        const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int dl0 = wave * DPW + DL * row;
         char* sKW = smem + L::OFF_KT;  // exp-weighted k rows
@@ -403,7 +404,7 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
                                    float (&Gseg)[DK / (DV / 16) / 4], char* smem) {
     using St = StateStep<TIn, TG, DK, DV>;
     constexpr int DL = St::DL;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tg = lane >> 2, row = lane & 3;
+    const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<false, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
     const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
     auto chunk_nv = [&](int64_t c) {
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     f32x4 S[DK / 16];
     float Gseg[DL];
 #pragma unroll
@@ -461,7 +462,7 @@ __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r16 = lane & 15, g4 = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     f32x4 S[DK / 16];
     const float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
 #pragma unroll
