@@ -410,6 +410,42 @@ __device__ __forceinline__ Split8<NP> split_k32(const f32x4& lo, const f32x4& hi
     return split8<NP>(x);
 }
 
+// ---- chunk outputs ------------------------------------------------------------------------
+// Output rows of one chunk for a wave's 16 columns: a buffer resource over rows [0, nv) from
+// `base` (row stride ost bytes, 16 columns of es bytes each), so rows past the chunk's end are
+// dropped by the hardware, and a second resource that is the same for fp32 and empty otherwise.
+struct OutRsrc {
+    __amdgpu_buffer_rsrc_t lo, hi;
+};
+
+__device__ __forceinline__ OutRsrc out_rsrc(char* base, int64_t ost, int es, int nv, bool f32) {
+    const int n = nv > 0 ? (int)((nv - 1) * ost + 16 * es) : 0;
+    OutRsrc r;
+    r.lo = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, n, 0x00020000);
+    r.hi = __builtin_amdgcn_make_buffer_rsrc(base, (short)0, f32 ? n : 0, 0x00020000);
+    return r;
+}
+
+// Four values of one output row as dtype dt at byte offset voff: always two 8-byte buffer
+// stores (the second one lands in the empty resource for 16-bit types), so the number of
+// outstanding memory operations never depends on dt or on the chunk length and the wait for the
+// next chunk's loads can leave the stores in flight.
+__device__ __forceinline__ void out_store4(const OutRsrc& r, int voff, int dt, const f32x4& x) {
+    // all three encodings, chosen by selects: no branch between the loads and the stores
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    const u32x2 b = __builtin_bit_cast(u32x2, bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]});
+    const u32x2 f = __builtin_bit_cast(u32x2, f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]});
+    const bool f32 = dt == DT_F32, bf = dt == DT_BF16;
+    u32x2 w0, w1;
+    w0[0] = f32 ? __float_as_uint(x[0]) : (bf ? b[0] : f[0]);
+    w0[1] = f32 ? __float_as_uint(x[1]) : (bf ? b[1] : f[1]);
+    w1[0] = __float_as_uint(x[2]);
+    w1[1] = __float_as_uint(x[3]);
+    __builtin_amdgcn_raw_buffer_store_b64(w0, r.lo, voff, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(w1, r.hi, voff + 8, 0, 0);
+}
+
 // Wave index within the workgroup as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 

@@ -457,11 +457,12 @@ struct GdnStep {
                               uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
                 const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);
                 const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
+                const OutRsrc orr = out_rsrc(obase, ost, es, nv, a.o_dt == DT_F32);
 #pragma unroll
                 for (int tb = 0; tb < 4; ++tb) {
                     *reinterpret_cast<f32x4*>(sO + r16 * L::OS + 4 * g4) = Ot[tb];
                     const f32x4 xo = *reinterpret_cast<const f32x4*>(sO + tq * L::OS + 4 * q);
-                    if (16 * tb + tq < nv) store4_dt(obase + 16 * tb * ost + olane, a.o_dt, xo[0], xo[1], xo[2], xo[3]);
+                    out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, xo);
                 }
             }
             // S <- e^m (S' + Wt^T U)

@@ -58,7 +58,11 @@ struct Lay {
     // of an LDS cycle hit distinct banks both when the MFMA layout writes and when quads read rows
     static constexpr int OS = 20;
     static_assert(DPW == 16 || DPW == 32, "stage-1 dims per wave");
-    static_assert(16 * OS * 4 <= P::NX * VPP, "output staging fits in a wave's V planes");
+    // Outputs are stored one chunk late (after the next chunk's loads are issued) where the
+    // registers allow it (not at DK = 128)
+    static constexpr bool DEFER = DK <= 64;
+    static_assert(!DEFER || NW * 16 * OS * 4 <= P::NS * ATP, "output staging of every wave fits in the A^T planes");
+    static_assert(DEFER || 16 * OS * 4 <= P::NX * VPP, "output staging fits in a wave's V planes");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
@@ -110,6 +114,37 @@ __device__ void chunk_tokenwise(const PrefillParams& a, const Work& wk, int64_t 
     }
 }
 
+// Outputs of one chunk for a wave's 16 columns (lane (g4, r16) holds O[token 16*tb + r16]
+// [columns 4*g4 .. 4*g4+3]), kept in registers until the next chunk has issued its loads.  On gfx9
+// one counter tracks loads and stores, and a wait for a load while a store is outstanding drains
+// both; stores issued right after the next loads are long complete when those loads are waited
+// for, one chunk later.
+struct PendingOut {
+    f32x4 o[4];
+    int64_t tc;
+    int nv;
+    bool valid;
+};
+
+// Stage the pending outputs 16 tokens at a time through `stage` (this wave's 16 x OS floats of
+// LDS) and store them with the four lanes of a quad covering one token's 16 columns.
+__device__ __forceinline__ void flush_out(const PrefillParams& a, const Work& wk, int64_t h, int c0, const PendingOut& p,
+                                          float* stage, int os) {
+    const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
+    const int es = dt_size(a.o_dt);
+    const int64_t ost = a.o_st * es;
+    char* obase = reinterpret_cast<char*>(a.o) + uniform_i64((wk.b * a.o_sb + (wk.row0 + p.tc) * a.o_st + h * a.o_sh + c0) * es);
+    const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);  // token within 16
+    const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
+    const OutRsrc orr = out_rsrc(obase, ost, es, p.nv, a.o_dt == DT_F32);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        *reinterpret_cast<f32x4*>(stage + r16 * os + 4 * g4) = p.o[tb];
+        const f32x4 x = *reinterpret_cast<const f32x4*>(stage + tq * os + 4 * q);
+        out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, x);
+    }
+}
+
 template <typename TIn, typename TG, int DK, int DV>
 struct OutStep {
     using L = Lay<TIn, DK, DV, true>;
@@ -121,7 +156,8 @@ struct OutStep {
     // after_inputs() runs once stage 1 has consumed `cur` (it may refill those registers).
     template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, Hook&& after_inputs) {
+                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, PendingOut& pend,
+                               Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int d0 = wave * DPW, c0 = wave * 16;
@@ -184,6 +220,10 @@ struct OutStep {
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
         after_inputs();
+        // The previous chunk's outputs, staged through this wave's slice of the A^T planes
+        // (nothing reads them again before this chunk's stage 2).
+        if (pend.valid) flush_out(a, wk, h, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
+        pend.valid = false;
         __syncthreads();
         bool fast = true;
 #pragma unroll
@@ -288,24 +328,14 @@ struct OutStep {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) S[db][i] = eg[i] * S[db][i] + em[i] * P[i];
             }
-            // Lane (g4, r16) holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3].  Stage it, 16
-            // tokens at a time, through this wave's V planes (only this wave reads them, and vf
-            // already holds them), then store with the four lanes of a quad covering one token's
-            // 16 columns.
-            {
-                float* sO = reinterpret_cast<float*>(sVP);
-                const int es = dt_size(a.o_dt);
-                const int64_t ost = a.o_st * es;
-                char* obase = reinterpret_cast<char*>(a.o) +
-                              uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
-                const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);  // token within 16
-                const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    *reinterpret_cast<f32x4*>(sO + r16 * L::OS + 4 * g4) = Ot[tb];
-                    const f32x4 x = *reinterpret_cast<const f32x4*>(sO + tq * L::OS + 4 * q);
-                    if (16 * tb + tq < nv) store4_dt(obase + 16 * tb * ost + olane, a.o_dt, x[0], x[1], x[2], x[3]);
-                }
+            for (int tb = 0; tb < 4; ++tb) pend.o[tb] = Ot[tb];
+            pend.tc = tc;
+            pend.nv = nv;
+            pend.valid = true;
+            if constexpr (!L::DEFER) {  // store now, staged through this wave's own V planes
+                flush_out(a, wk, h, c0, pend, reinterpret_cast<float*>(sVP), L::OS);
+                pend.valid = false;
             }
         }
         __syncthreads();  // the next chunk rewrites LDS
@@ -329,9 +359,14 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     // are in flight during stages 2-3 (registers go to occupancy instead of a second set).
     ChunkIn<TIn, TG, DL> A;
     chunk_load<true>(A, ad, tok(0), true);
+    PendingOut pend;
+    pend.valid = false;
     for (int64_t c = 0; c < nch; ++c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem,
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
                 [&] { chunk_load<true>(A, ad, tok(c + 1), c + 1 < nch); });
+    if (pend.valid)  // after the last chunk's closing barrier the A^T planes are free
+        flush_out(a, wk, h, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
+                  St::L::OS);
 }
 
 // ---------------------------------------------------------------------------------------
