@@ -30,6 +30,8 @@
  *                                     with _triton_gated_deltanet_fwd (fast_gla.py:479-550) and
  *                                     fast_recurrent_gated_deltanet (fast_gla.py:781-836)
  *   triune_hip_gdn_prefill_chunked <- the same operator (fast_gla.py:839-904), chunked form
+ *   triune_hip_gla_qkvg_prep       <- _fused_qkv_g_prep_inplace_kernel, triune/model/attention.py:14-79
+ *   triune_hip_gla_fused_decode_step <- _fused_qkvg_decode_step_kernel, triune/model/attention.py:81-179
  */
 #ifndef TRIUNE_HIP_H
 #define TRIUNE_HIP_H
@@ -162,6 +164,31 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
                                    const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
                                    int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
                                    size_t workspace_bytes, void* stream);
+
+/* GLA input pre-processing in place (VectorisedGLA's fused path): for every (b, t, h) row of HD
+ * elements, q and k <- RoPE(normalize(elu(x) + 1)) with normalize(a) = a / sqrt(max(sum a^2,
+ * 1e-12)) and RoPE pairing elements d and d + HD/2 (out[d] = a[d] cos[t][d] - a[d+HD/2] sin[t][d],
+ * out[d+HD/2] = a[d+HD/2] cos[t][d+HD/2] + a[d] sin[t][d+HD/2]); g <- logsigmoid(g); v untouched.
+ * qkv: [B, T, 3, H, HD] with element strides strides[0..3] = (batch, token, part, head); g:
+ * [B, T, H, HD] with strides[4..6] = (batch, token, head); innermost stride 1, rows 16-byte
+ * aligned.  cos/sin: [T, HD] rows cs_stride elements apart (used when use_rope != 0), dtype
+ * cs_dtype.  HD in {32, 64, 128}; q/k/v/g share io_dtype.
+ * Replaces: _fused_qkv_g_prep_inplace_kernel (triune/model/attention.py:14-79). */
+int triune_hip_gla_qkvg_prep(void* qkv, void* g, int io_dtype, const int64_t* strides, const void* cos,
+                             const void* sin, int cs_dtype, int64_t cs_stride, int use_rope, int64_t B, int64_t T,
+                             int64_t H, int HD, void* stream);
+
+/* One GLA decode step fused with the pre-processing above: qkvg [B, 4, H, HD] raw projections
+ * (strides[0..2] = batch, part, head; parts q, k, v, g), cos/sin [HD] of the step's position; q,
+ * k pre-processed as above, decay sigmoid(g) (= exp(logsigmoid(g))), then S <- diag(decay) S +
+ * k v^T and o = S^T q.  state_in / state_out: contiguous [B, H, HD, HD] in state_dtype (fp32 or
+ * io_dtype; state_in NULL = zero state, state_out NULL = state not stored, state_out may equal
+ * state_in).  o: [B, H, HD] (o_strides = batch, head).  cs_dtype: fp32 or io_dtype.
+ * Replaces: _fused_qkvg_decode_step_kernel (triune/model/attention.py:81-179). */
+int triune_hip_gla_fused_decode_step(const void* qkvg, int io_dtype, const int64_t* strides, const void* cos,
+                                     const void* sin, int cs_dtype, int use_rope, const void* state_in,
+                                     void* state_out, int state_dtype, void* o, int o_dtype,
+                                     const int64_t* o_strides, int64_t B, int64_t H, int HD, void* stream);
 
 #ifdef __cplusplus
 }

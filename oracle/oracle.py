@@ -162,6 +162,59 @@ def gdn_fwd(q, k, v, g, beta=None, s0=None, beta_kind=None):
 # ---------------------------------------------------------------------------------------
 
 
+# --- VectorisedGLA input pre-processing (reference: triune/model/attention.py:14-179, the fused
+# Triton kernels; unfused form :509-528).  Plain float64 numpy restatements. ---------------------
+def elu1(x):
+    """elu(x) + 1 = x + 1 for x >= 0, exp(x) otherwise (attention.py:39-40, 521)."""
+    x = _d(x)
+    return np.where(x >= 0.0, x + 1.0, np.exp(np.minimum(x, 0.0)))
+
+
+def logsigmoid(x):
+    """log(1 / (1 + exp(-x))), evaluated without overflow (attention.py:74-75)."""
+    x = _d(x)
+    return np.minimum(x, 0.0) - np.log1p(np.exp(-np.abs(x)))
+
+
+def qk_prep(x, cos=None, sin=None):
+    """RoPE(normalize(elu(x) + 1)) over the last axis (HD): normalize(a) = a / sqrt(max(sum a^2,
+    1e-12)) (attention.py:41-43); RoPE pairs element d with d + HD/2 (attention.py:53-61):
+    out[d] = a[d] cos[d] - a[d + HD/2] sin[d], out[d + HD/2] = a[d + HD/2] cos[d + HD/2] +
+    a[d] sin[d + HD/2].  cos/sin broadcast against x (None: no rotation)."""
+    a = elu1(x)
+    a = a / np.sqrt(np.maximum((a * a).sum(axis=-1, keepdims=True), 1e-12))
+    if cos is None:
+        return a
+    half = a.shape[-1] // 2
+    rot = np.concatenate([-a[..., half:], a[..., :half]], axis=-1)
+    return a * _d(cos) + rot * _d(sin)
+
+
+def qkv_g_prep(qkv, g, cos=None, sin=None):
+    """The in-place pre-processing of qkv [B, T, 3, H, HD] and g [B, T, H, HD], cos/sin [T, HD]
+    (attention.py:14-79).  Returns new (qkv, g) arrays; v is copied unchanged."""
+    qkv = _d(qkv).copy()
+    cs = sn = None
+    if cos is not None:
+        cs = _d(cos)[None, :, None, :]
+        sn = _d(sin)[None, :, None, :]
+    qkv[:, :, 0] = qk_prep(qkv[:, :, 0], cs, sn)
+    qkv[:, :, 1] = qk_prep(qkv[:, :, 1], cs, sn)
+    return qkv, logsigmoid(g)
+
+
+def fused_decode_step(qkvg, cos, sin, state):
+    """The decode step fused with the pre-processing (attention.py:81-179): qkvg [B, 4, H, HD]
+    raw, cos/sin [HD] or None, state [B, H, HD, HD] or None (zero).  q, k pre-processed, decay
+    sigmoid(g) = exp(logsigmoid(g)), then the GLA step.  Returns (o [B, H, HD], new state)."""
+    x = _d(qkvg)
+    B, _, H, HD = x.shape
+    q = qk_prep(x[:, 0], cos, sin)
+    k = qk_prep(x[:, 1], cos, sin)
+    s0 = np.zeros((B, H, HD, HD)) if state is None else _d(state)
+    return gla_decode_step(q, k, x[:, 2], logsigmoid(x[:, 3]), s0)
+
+
 def ref_library_path() -> Path:
     return _HERE / "_ref" / "libtriune_core_ref.so"
 

@@ -257,3 +257,71 @@ def test_port_fp32_factored_path_matches_oracle():
     o, s = fast_chunk_gla_cpu(q, k, v, g, None)
     ro, rs = O.gla_fwd(q, k, v, g, None)
     assert np.abs(o.double().numpy() - ro).max() < 1e-4 and np.abs(s.double().numpy() - rs).max() < 1e-4
+
+
+# ---------------------------------------------------------------------------------------------
+# VectorisedGLA input pre-processing (attention.py:14-179)
+# ---------------------------------------------------------------------------------------------
+def _rope_tables(T, HD, offset=0):
+    """cos/sin [T, HD] built like the reference's RotaryEmbedding (rotary.py:24-29), float64."""
+    inv_freq = 1.0 / (10000.0 ** (torch.arange(0, HD, 2, dtype=torch.float64) / HD))
+    t = torch.arange(offset, offset + T, dtype=torch.float64)
+    emb = torch.cat([torch.outer(t, inv_freq)] * 2, dim=-1)
+    return emb.cos(), emb.sin()
+
+
+@pytest.mark.parametrize("HD", [32, 64, 128])
+def test_prep_matches_unfused_torch_path(HD):
+    """The reference's unfused path (attention.py:509-528): F.normalize(F.elu(x) + 1, eps=1e-6),
+    then x * cos + cat(-x2, x1) * sin, evaluated by torch in float64."""
+    gen = torch.Generator().manual_seed(HD)
+    T = 9
+    x = 2.0 * torch.randn(2, T, 3, HD, generator=gen, dtype=torch.float64)
+    cos, sin = _rope_tables(T, HD, offset=5)
+    a = torch.nn.functional.normalize(torch.nn.functional.elu(x) + 1.0, p=2.0, dim=-1, eps=1e-6)
+    a1, a2 = a.chunk(2, dim=-1)
+    ref = a * cos[None, :, None] + torch.cat((-a2, a1), dim=-1) * sin[None, :, None]
+    got = O.qk_prep(x.numpy(), cos.numpy()[None, :, None], sin.numpy()[None, :, None])
+    assert np.abs(got - ref.numpy()).max() <= 1e-12
+    assert np.abs(O.qk_prep(x.numpy()) - a.numpy()).max() <= 1e-12
+
+
+def test_logsigmoid_matches_torch():
+    x = torch.tensor([-800.0, -40.0, -3.0, -1e-7, 0.0, 1e-7, 2.5, 40.0, 800.0], dtype=torch.float64)
+    assert np.abs(O.logsigmoid(x.numpy()) - torch.nn.functional.logsigmoid(x).numpy()).max() <= 1e-15
+    g = torch.randn(1000, generator=torch.Generator().manual_seed(3), dtype=torch.float64) * 6
+    assert np.abs(np.exp(O.logsigmoid(g.numpy())) - torch.sigmoid(g).numpy()).max() <= 1e-15
+
+
+def test_prep_invariants():
+    x = _rand(7, 4, 64) * 3
+    a = O.qk_prep(x)
+    assert np.allclose(np.linalg.norm(a, axis=-1), 1.0, atol=1e-14)  # unit rows without rotation
+    one, zero = np.ones(64), np.zeros(64)
+    assert np.abs(O.qk_prep(x, one, zero) - a).max() == 0.0  # angle 0 is the identity
+    cos, sin = (t.numpy() for t in _rope_tables(4, 64, offset=100))
+    r = O.qk_prep(x, cos, sin)
+    assert np.allclose(np.linalg.norm(r, axis=-1), 1.0, atol=1e-14)  # a rotation keeps the norm
+    # the eps guard: elu(x) + 1 = e^x underflows the 1e-12 floor for very negative rows
+    tiny = O.qk_prep(np.full((1, 8), -200.0))
+    assert np.allclose(tiny, np.exp(-200.0) * 1e6)
+
+
+def test_fused_decode_oracle_brute_force():
+    """prep q, k; decay sigmoid(g); S <- diag(decay) S + k v^T; o = S^T q, by explicit loops."""
+    rng = np.random.default_rng(11)
+    B, H, HD = 2, 3, 32
+    x = rng.standard_normal((B, 4, H, HD))
+    S0 = 0.1 * rng.standard_normal((B, H, HD, HD))
+    cos, sin = (t.numpy()[0] for t in _rope_tables(1, HD, offset=17))
+    o, S = O.fused_decode_step(x, cos, sin, S0)
+    for b in range(B):
+        for h in range(H):
+            q = O.qk_prep(x[b, 0, h], cos, sin)
+            k = O.qk_prep(x[b, 1, h], cos, sin)
+            d = 1.0 / (1.0 + np.exp(-x[b, 3, h]))
+            Sn = d[:, None] * S0[b, h] + np.outer(k, x[b, 2, h])
+            assert np.abs(Sn - S[b, h]).max() <= 1e-13
+            assert np.abs(q @ Sn - o[b, h]).max() <= 1e-13
+    o0, S0z = O.fused_decode_step(x, None, None, None)  # no rotation, zero state
+    assert np.abs(S0z - np.einsum("bhi,bhj->bhij", O.qk_prep(x[:, 1]), x[:, 2])).max() <= 1e-13

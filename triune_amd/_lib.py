@@ -59,6 +59,11 @@ def _bind(lib):
             [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _vp],
             _i,
         ),
+        "triune_hip_gla_qkvg_prep": ([_vp, _vp, _i, _i64p, _vp, _vp, _i, _i64, _i, _i64, _i64, _i64, _i, _vp], _i),
+        "triune_hip_gla_fused_decode_step": (
+            [_vp, _i, _i64p, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i64p, _i64, _i64, _i, _vp],
+            _i,
+        ),
         "triune_hip_gdn_prefill_chunked_workspace_size": ([_i64, _i64, _i64, _i, _i], _sz),
         "triune_hip_gdn_prefill_chunked": (
             [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _vp, _sz,
@@ -86,6 +91,8 @@ EXPORTS = (
     "triune_hip_gdn_prefill",
     "triune_hip_gdn_prefill_chunked_workspace_size",
     "triune_hip_gdn_prefill_chunked",
+    "triune_hip_gla_qkvg_prep",
+    "triune_hip_gla_fused_decode_step",
 )
 
 

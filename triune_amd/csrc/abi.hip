@@ -527,4 +527,51 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     return launch_status(launch_gdn_seg_out(a, pl.n_work, io_dtype, st));
 }
 
+int triune_hip_gla_qkvg_prep(void* qkv, void* g, int io_dtype, const int64_t* strides, const void* cos,
+                             const void* sin, int cs_dtype, int64_t cs_stride, int use_rope, int64_t B, int64_t T,
+                             int64_t H, int HD, void* stream) {
+    if (!qkv || !g || !strides || (use_rope && (!cos || !sin))) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || (use_rope && !dtype_ok(cs_dtype))) return TRIUNE_ERR_DTYPE;
+    if (B < 0 || T < 0 || H <= 0 || (HD != 32 && HD != 64 && HD != 128)) return TRIUNE_ERR_SHAPE;
+    const int64_t rows = B * T * H;
+    if (rows > (int64_t)16 * 0x7fffffff) return TRIUNE_ERR_SHAPE;  // grid: ceil(rows / rows-per-block >= 16) blocks
+    if (rows == 0) return TRIUNE_OK;
+    // qkv strides (b, t, part, h) and g strides (b, t, h), elements; rows of 8-element vectors
+    if (!vec_ok(qkv, io_dtype, strides + 0, 4) || !vec_ok(g, io_dtype, strides + 4, 3)) return TRIUNE_ERR_LAYOUT;
+    if (use_rope && (!vec_ok(cos, cs_dtype, &cs_stride, 1) || !vec_ok(sin, cs_dtype, &cs_stride, 1)))
+        return TRIUNE_ERR_LAYOUT;
+    PrepParams a{};
+    a.qkv = qkv; a.qkv_sb = strides[0]; a.qkv_st = strides[1]; a.qkv_sp = strides[2]; a.qkv_sh = strides[3];
+    a.g = g; a.g_sb = strides[4]; a.g_st = strides[5]; a.g_sh = strides[6];
+    a.cos = cos; a.sin = sin; a.cs_st = cs_stride; a.use_rope = use_rope ? 1 : 0;
+    a.B = B; a.T = T; a.H = H;
+    return launch_status(launch_gla_prep(a, HD, io_dtype, use_rope ? cs_dtype : TRIUNE_DT_F32, (hipStream_t)stream));
+}
+
+int triune_hip_gla_fused_decode_step(const void* qkvg, int io_dtype, const int64_t* strides, const void* cos,
+                                     const void* sin, int cs_dtype, int use_rope, const void* state_in,
+                                     void* state_out, int state_dtype, void* o, int o_dtype,
+                                     const int64_t* o_strides, int64_t B, int64_t H, int HD, void* stream) {
+    if (!qkvg || !strides || !o || !o_strides || (use_rope && (!cos || !sin))) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(o_dtype) || !dtype_ok(state_dtype)) return TRIUNE_ERR_DTYPE;
+    if (state_dtype != TRIUNE_DT_F32 && state_dtype != io_dtype) return TRIUNE_ERR_DTYPE;
+    if (use_rope && cs_dtype != TRIUNE_DT_F32 && cs_dtype != io_dtype) return TRIUNE_ERR_DTYPE;
+    if (B < 0 || H <= 0 || (HD != 32 && HD != 64 && HD != 128)) return TRIUNE_ERR_SHAPE;
+    if (B > 0x7fffffff / H) return TRIUNE_ERR_SHAPE;  // one block per (b, h)
+    if (B == 0) return TRIUNE_OK;
+    const int sal = state_dtype == TRIUNE_DT_F32 ? 16 : 8;
+    if (reinterpret_cast<uintptr_t>(state_in) % sal || reinterpret_cast<uintptr_t>(state_out) % sal ||
+        !vec4_ok(o, o_dtype, o_strides, 2))
+        return TRIUNE_ERR_LAYOUT;
+    FusedDecodeParams a{};
+    a.qkvg = qkvg; a.x_sb = strides[0]; a.x_sp = strides[1]; a.x_sh = strides[2];
+    a.cos = cos; a.sin = sin; a.use_rope = use_rope ? 1 : 0;
+    a.has_init = state_in != nullptr; a.save_final = state_out != nullptr;
+    a.state_in = state_in; a.state_out = state_out;
+    a.o = o; a.o_dt = o_dtype; a.o_sb = o_strides[0]; a.o_sh = o_strides[1];
+    a.B = B; a.H = H;
+    return launch_status(
+        launch_gla_fused_decode(a, HD, io_dtype, use_rope ? cs_dtype : TRIUNE_DT_F32, state_dtype, (hipStream_t)stream));
+}
+
 }  // extern "C"

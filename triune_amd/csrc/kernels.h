@@ -86,7 +86,40 @@ struct GdnParams {
     int64_t B, T, H;
 };
 
+// GLA input pre-processing (in place): q, k in qkv [B, T, 3, H, HD] (element strides sb, st, sp
+// between the q/k/v parts, sh), g [B, T, H, HD]; cos/sin [T, HD] rows cs_st apart.
+struct PrepParams {
+    void* qkv;
+    int64_t qkv_sb, qkv_st, qkv_sp, qkv_sh;
+    void* g;
+    int64_t g_sb, g_st, g_sh;
+    const void* cos;
+    const void* sin;
+    int64_t cs_st;
+    int use_rope;
+    int64_t B, T, H;
+};
+
+// Decode step fused with the pre-processing: qkvg [B, 4, H, HD] (element strides x_sb, x_sp, x_sh),
+// cos/sin [HD], state [B, H, HD, HD] contiguous (in: null = zero state; out: null = not stored).
+struct FusedDecodeParams {
+    const void* qkvg;
+    int64_t x_sb, x_sp, x_sh;
+    const void* cos;
+    const void* sin;
+    int use_rope, has_init, save_final;
+    const void* state_in;
+    void* state_out;
+    void* o;
+    int o_dt;
+    int64_t o_sb, o_sh;
+    int64_t B, H;
+};
+
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);
+hipError_t launch_gla_prep(const PrepParams& a, int HD, int io_dt, int cs_dt, hipStream_t stream);
+hipError_t launch_gla_fused_decode(const FusedDecodeParams& a, int HD, int io_dt, int cs_dt, int s_dt,
+                                   hipStream_t stream);
 hipError_t launch_gla_decode(const DecodeParams& a, int Dk, int Dv, int max_blocks, hipStream_t stream);
 hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t stream);
 // Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).
