@@ -152,6 +152,73 @@ def bench_decode(steps_total, dev, n_bufs=12):
     }
 
 
+def bench_prep(dev, reps=10):
+    """In-place GLA input pre-processing (ELU+1, L2 norm, RoPE on q and k; logsigmoid on g) at the
+    config-1 shape: qkv [4, 16384, 3, 6, 64] and g [4, 16384, 6, 64] bf16, fp32 RoPE tables."""
+    from triune_amd import fused_qkv_g_prep_inplace
+
+    B, T, H, HD = 4, 16384, 6, 64
+    gen = torch.Generator().manual_seed(5)
+    qkv = torch.randn(B, T, 3, H, HD, generator=gen).bfloat16().to(dev)
+    g = torch.randn(B, T, H, HD, generator=gen).bfloat16().to(dev)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))
+    emb = torch.cat([torch.outer(torch.arange(T, dtype=torch.float32), inv)] * 2, dim=-1)
+    cos, sin = emb.cos().to(dev), emb.sin().to(dev)
+    fn = lambda: fused_qkv_g_prep_inplace(qkv, g, cos, sin)  # noqa: E731
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    alg = 6 * B * T * H * HD * 2  # q, k, g read and written once (v untouched)
+    return {"workload": "VectorisedGLA pre-processing in place, config-1 shape (B=4, T=16384, H=6, HD=64, bf16, RoPE)",
+            "us": round(ms * 1e3, 2), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "roofline": {"bound": "hbm", "achieved": round(alg / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
+
+
+def bench_fused_decode(steps_total, dev, n_bufs=12):
+    """Decode step fused with the pre-processing at the config-2 shape (B=256, H=6, HD=64): raw
+    qkvg [256, 4, 6, 64] bf16, fp32 state updated in place; 12 rotating state buffers and input
+    sets, the loop captured in a graph."""
+    from triune_amd import fused_qkvg_decode_step
+
+    B, H, HD = 256, 6, 64
+    gen = torch.Generator().manual_seed(6)
+    xs = [torch.randn(B, 4, H, HD, generator=gen).bfloat16().to(dev) for _ in range(n_bufs)]
+    states = [(0.1 * torch.randn(B, H, HD, HD, generator=gen)).to(dev) for _ in range(n_bufs)]
+    outs = [torch.empty(B, 1, H, HD, device=dev, dtype=torch.bfloat16) for _ in range(n_bufs)]
+    inv = 1.0 / (10000.0 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))
+    emb = torch.cat([torch.outer(torch.arange(steps_total, dtype=torch.float32), inv)] * 2, dim=-1)
+    cos, sin = emb.cos().to(dev), emb.sin().to(dev)
+
+    def loop():
+        for t in range(steps_total):
+            i = t % n_bufs
+            fused_qkvg_decode_step(xs[i], cos[t], sin[t], initial_state=states[i], out=outs[i], inplace=True)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        loop()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loop()
+    graph.replay()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(graph.replay, 3, torch.cuda.current_stream())
+    step_us = ms * 1e3 / steps_total
+    step_bytes = 2 * B * H * HD * HD * 4 + B * 4 * H * HD * 2 + B * H * HD * 2
+    return {"workload": "decode step fused with the pre-processing, config-2 shape (B=256, H=6, HD=64), "
+            f"{steps_total}-step graph, {n_bufs} rotating fp32 state buffers and input sets",
+            "us_per_step": round(step_us, 3), "tok_s": round(B / (step_us * 1e-6), 1),
+            "roofline": {"bound": "hbm", "achieved": round(step_bytes / (step_us * 1e-6) / 1e9, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(step_bytes / (step_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "alg_bytes_per_step": step_bytes}}
+
+
 def bench_gdn(dev, reps=10):
     """Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta and decay)."""
     from triune_amd import fast_chunk_gated_deltanet
@@ -254,7 +321,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "varlen"),
+        choices=("decode", "gdn", "varlen", "prep", "fused_decode"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -279,13 +346,16 @@ def main():
     if args.only:
         if args.only == "decode":
             res = bench_decode(args.decode_steps, dev)
+        elif args.only == "fused_decode":
+            res = bench_fused_decode(args.decode_steps, dev)
         else:
-            res = bench_gdn(dev) if args.only == "gdn" else bench_varlen(dev)
+            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     pre = bench_prefill(args.steps, args.warmup, dev)
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
-    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev)}
+    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
+                                      "fused_decode": bench_fused_decode(args.decode_steps, dev)}
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,

@@ -561,7 +561,9 @@ int triune_hip_gla_fused_decode_step(const void* qkvg, int io_dtype, const int64
     if (B == 0) return TRIUNE_OK;
     const int sal = state_dtype == TRIUNE_DT_F32 ? 16 : 8;
     if (reinterpret_cast<uintptr_t>(state_in) % sal || reinterpret_cast<uintptr_t>(state_out) % sal ||
-        !vec4_ok(o, o_dtype, o_strides, 2))
+        !vec4_ok(o, o_dtype, o_strides, 2) || !vec4_ok(qkvg, io_dtype, strides, 3))
+        return TRIUNE_ERR_LAYOUT;
+    if (use_rope && (!vec4_ok(cos, cs_dtype, strides, 0) || !vec4_ok(sin, cs_dtype, strides, 0)))
         return TRIUNE_ERR_LAYOUT;
     FusedDecodeParams a{};
     a.qkvg = qkvg; a.x_sb = strides[0]; a.x_sp = strides[1]; a.x_sh = strides[2];
@@ -569,7 +571,7 @@ int triune_hip_gla_fused_decode_step(const void* qkvg, int io_dtype, const int64
     a.has_init = state_in != nullptr; a.save_final = state_out != nullptr;
     a.state_in = state_in; a.state_out = state_out;
     a.o = o; a.o_dt = o_dtype; a.o_sb = o_strides[0]; a.o_sh = o_strides[1];
-    a.B = B; a.H = H;
+    a.B = B; a.H = H; a.max_blocks = 4 * device_cus();
     return launch_status(
         launch_gla_fused_decode(a, HD, io_dtype, use_rope ? cs_dtype : TRIUNE_DT_F32, state_dtype, (hipStream_t)stream));
 }

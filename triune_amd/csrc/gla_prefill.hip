@@ -103,6 +103,9 @@ __device__ void chunk_tokenwise(const PrefillParams& a, const Work& wk, int64_t 
         if (OUT) {
             part += __shfl_xor(part, 16);
             part += __shfl_xor(part, 32);
+            // o may alias g (the reference's VectorisedGLA passes out=g): every wave has read
+            // token tt's gates before any wave overwrites them with outputs
+            __syncthreads();
             if (g4 == 0) {
                 const int64_t off = wk.b * a.o_sb + (wk.row0 + tt) * a.o_st + h * a.o_sh + c0 + r16;
                 char* op = reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt);

@@ -14,10 +14,11 @@
 // gla_prep_kernel: memory-bound, in place.  A row is covered by HD/8 consecutive lanes holding 8
 // elements each (16-byte accesses for 16-bit types); the sum of squares is reduced and the RoPE
 // partner exchanged with lane shuffles inside the row's lane group.
-// gla_fused_decode_kernel: the decode kernel's layout (a 256-thread block per (b, h) row, thread
+// gla_fused_decode_kernel: the decode kernel's layout (256-thread blocks walking (b, h) rows, thread
 // = RPT key rows x 4 value columns); every wave forms the two norms itself from one element per
 // lane, so no barrier separates the pre-processing from the state update.
 #include "kernels.h"
+#include "common.h"
 
 namespace triune {
 
@@ -48,12 +49,16 @@ __device__ __forceinline__ void st8(T* p, const float (&x)[8]) {
     *reinterpret_cast<V4<T>*>(p + 4) = b;
 }
 
-__device__ __forceinline__ float elu1(float x) { return x >= 0.f ? x + 1.f : expf(x); }
+__device__ __forceinline__ float elu1(float x) { return x >= 0.f ? x + 1.f : fast_exp(x); }
 
-__device__ __forceinline__ float logsigmoid(float x) { return fminf(x, 0.f) - log1pf(expf(-fabsf(x))); }
+// min(x, 0) - log(1 + e^-|x|) with the hardware exp2 / log2: for e^-|x| below 2^-24 the log term
+// rounds to 0, an absolute error under 6e-8.
+__device__ __forceinline__ float logsigmoid(float x) {
+    return fminf(x, 0.f) - 0.6931471805599453f * __builtin_amdgcn_logf(1.f + fast_exp(-fabsf(x)));
+}
 
 __device__ __forceinline__ float sigmoid(float x) {
-    const float e = expf(-fabsf(x));
+    const float e = fast_exp(-fabsf(x));
     return x >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
 }
 
@@ -123,106 +128,194 @@ __global__ __launch_bounds__(256) void gla_prep_kernel(PrepParams a) {
 
 // ---------------------------------------------------------------------------------------
 // Fused decode: qkvg [B, 4, H, HD] (q, k, v, g raw), cos/sin [HD] of the step's position,
-// state [B, H, HD, HD] in TS (fp32 or the I/O type), o [B, H, HD].
+// state [B, H, HD, HD] in TS (fp32 or the I/O type), o [B, H, HD].  A block walks rows
+// blockIdx.x, + gridDim.x, ... and issues the next row's state loads before storing the current
+// row (as the plain decode kernel does).  State accesses are buffer loads/stores over one row
+// whose record count is 0 without an initial state (loads return 0) or without a state output
+// (stores are dropped), so every path issues the same memory operations.
 // ---------------------------------------------------------------------------------------
+template <int HD>
+struct FusedDecodeTiling {
+    static constexpr int RPT = HD * HD / (4 * 256) > 4 ? HD * HD / (4 * 256) : 4;  // key rows per thread
+    static constexpr int CG = HD / 4;                                            // column groups
+    static constexpr int TPB = HD * HD / (4 * RPT);
+    static constexpr int WAVES = TPB / 64;
+    static constexpr int EPL = HD / 64 > 0 ? HD / 64 : 1;  // norm elements per lane
+};
+
 template <int HD, typename TIO, typename TCS, typename TS>
-__global__ __launch_bounds__(256) void gla_fused_decode_kernel(FusedDecodeParams a) {
-    constexpr int RPT = HD * HD / (4 * 256) > 4 ? HD * HD / (4 * 256) : 4;  // key rows per thread
-    constexpr int CG = HD / 4;                                            // column groups
-    constexpr int TPB = HD * HD / (4 * RPT);
-    constexpr int WAVES = TPB / 64;
-    constexpr int EPL = HD / 64 > 0 ? HD / 64 : 1;  // norm elements per lane
-    static_assert(TPB == 256 || TPB == 64 || TPB == 128, "fused decode tiling");
+__global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_kernel(FusedDecodeParams a, uint32_t rows) {
+    using Tl = FusedDecodeTiling<HD>;
+    constexpr int RPT = Tl::RPT, CG = Tl::CG, WAVES = Tl::WAVES, EPL = Tl::EPL;
+    constexpr int SB = (int)sizeof(TS);
+    static_assert(Tl::TPB == 256 || Tl::TPB == 64 || Tl::TPB == 128, "fused decode tiling");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cg = tid % CG, rg = tid / CG, r0 = rg * RPT;
     const uint32_t H32 = (uint32_t)a.H;
-    const int64_t b = blockIdx.x / H32, h = blockIdx.x % H32;
-    const TIO* base = reinterpret_cast<const TIO*>(a.qkvg) + b * a.x_sb + h * a.x_sh;
-    const TIO* qr = base;
-    const TIO* kr = base + a.x_sp;
-    const TIO* vr = base + 2 * a.x_sp;
-    const TIO* gr = base + 3 * a.x_sp;
-    const int64_t srow = (int64_t)blockIdx.x * HD * HD;
-
-    // state first (the large loads), then the row inputs
-    f32x4 st[RPT];
-    const TS* sin_p = reinterpret_cast<const TS*>(a.state_in) + srow + (int64_t)r0 * HD + 4 * cg;
+    const int32_t voff = (r0 * HD + 4 * cg) * SB;  // this thread's first state element in a row
+    auto row_rsrc = [&](const void* p, uint32_t row, bool on) {
+        char* base = reinterpret_cast<char*>(const_cast<void*>(p)) + (int64_t)row * HD * HD * SB;
+        return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, on ? HD * HD * SB : 0, 0x00020000);
+    };
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    struct Raw {
+        u32x4 w[RPT];  // 16-bit states use the first two words
+    };
+    auto fetch = [&](Raw& x, uint32_t row) {
+        const auto r = row_rsrc(a.state_in, row, a.has_init != 0);
 #pragma unroll
-    for (int m = 0; m < RPT; ++m) {
-        if (a.has_init) {
-            const V4<TS> x = __builtin_nontemporal_load(reinterpret_cast<const V4<TS>*>(sin_p + m * HD));
-            st[m] = f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+        for (int m = 0; m < RPT; ++m) {
+            if constexpr (SB == 4) {
+                x.w[m] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + m * HD * SB, 0, 2));
+            } else {
+                const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff + m * HD * SB, 0, 2));
+                x.w[m] = u32x4{v[0], v[1], 0u, 0u};
+            }
+        }
+    };
+    auto unpack = [&](const u32x4& w) -> f32x4 {
+        if constexpr (SB == 4) {
+            return __builtin_bit_cast(f32x4, w);
         } else {
-            st[m] = zero4();
+            const V4<TS> v = __builtin_bit_cast(V4<TS>, u32x2{w[0], w[1]});
+            return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
         }
-    }
-    // norms: every wave reduces the whole row from EPL elements per lane
-    float sq = 0.f, sk = 0.f;
+    };
+    const int tbytes = a.use_rope ? HD * (int)sizeof(TCS) : 0;
+    const auto rcos = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.cos), (short)0, tbytes, 0x00020000);
+    const auto rsin = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.sin), (short)0, tbytes, 0x00020000);
+    auto ld_table4 = [](__amdgpu_buffer_rsrc_t r, int off, float* x) {
+        if constexpr (sizeof(TCS) == 4) {
+            const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        const int d = lane + 64 * e;
-        if (d < HD) {
-            const float qa = elu1((float)qr[d]), ka = elu1((float)kr[d]);
-            sq += qa * qa;
-            sk += ka * ka;
+            for (int i = 0; i < 4; ++i) x[i] = v[i];
+        } else {
+            const V4<TCS> v = __builtin_bit_cast(V4<TCS>, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = (float)v[i];
         }
-    }
+    };
+    __shared__ f32x4 red[2][WAVES][CG];
+    // One row: compute from `cur`, issue the next row's state loads into `nxt`, store, reduce.
+    auto step = [&](const Raw& cur, Raw& nxt, uint32_t row, int buf) {
+        const int64_t b = row / H32, h = row % H32;
+        const TIO* base = reinterpret_cast<const TIO*>(a.qkvg) + b * a.x_sb + h * a.x_sh;
+        const TIO* qr = base;
+        const TIO* kr = base + a.x_sp;
+        const TIO* vr = base + 2 * a.x_sp;
+        const TIO* gr = base + 3 * a.x_sp;
+        // All of the row's small loads are issued together (no branch between them): the norm
+        // elements (one per lane), this thread's key rows of q, k, g and their RoPE partner rows,
+        // cos/sin (buffer loads over a table of HD entries, or of none when RoPE is off: then they
+        // read zeros and never touch memory, as cos and sin may be null), the 4 value columns.
+        float qa[EPL], ka[EPL];
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        sq += __shfl_xor(sq, m);
-        sk += __shfl_xor(sk, m);
-    }
-    const float iq = inv_norm(sq), ik = inv_norm(sk);
-    // this thread's key rows r0 .. r0+RPT-1 (and their RoPE partners), decays, value columns
-    float qv[RPT], kv[RPT], dv[RPT], vv[4];
-#pragma unroll
-    for (int m = 0; m < RPT; ++m) {
-        const int d = r0 + m;
-        float qn = elu1((float)qr[d]) * iq, kn = elu1((float)kr[d]) * ik;
-        if (a.use_rope) {
-            const int dp = d < HD / 2 ? d + HD / 2 : d - HD / 2;
-            const float qo = elu1((float)qr[dp]) * iq, ko = elu1((float)kr[dp]) * ik;
-            const float cs = (float)reinterpret_cast<const TCS*>(a.cos)[d];
-            const float sn = (float)reinterpret_cast<const TCS*>(a.sin)[d];
-            const float sgn = d < HD / 2 ? -1.f : 1.f;
-            qn = qn * cs + sgn * qo * sn;
-            kn = kn * cs + sgn * ko * sn;
+        for (int e = 0; e < EPL; ++e) {
+            const int d = (lane + 64 * e) % HD;  // HD = 32: lanes 32..63 repeat 0..31 (counted once below)
+            qa[e] = (float)qr[d];
+            ka[e] = (float)kr[d];
         }
-        qv[m] = qn;
-        kv[m] = kn;
-        dv[m] = sigmoid((float)gr[d]);
-    }
+        constexpr int PH = HD / 2;
+        const int rp = r0 < PH ? r0 + PH : r0 - PH;  // partner rows rp .. rp+RPT-1
+        float qo[RPT], qp[RPT], ko[RPT], kp[RPT], gg[RPT], cs[RPT], sn[RPT], vv[4];
+        auto ld4 = [](const auto* p, float* x) {
+            using T = std::remove_const_t<std::remove_pointer_t<decltype(p)>>;
+            const V4<T> v = *reinterpret_cast<const V4<T>*>(p);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) vv[c] = (float)vr[4 * cg + c];
+            for (int i = 0; i < 4; ++i) x[i] = (float)v[i];
+        };
+#pragma unroll
+        for (int m = 0; m < RPT; m += 4) {
+            ld4(qr + r0 + m, qo + m);
+            ld4(qr + rp + m, qp + m);
+            ld4(kr + r0 + m, ko + m);
+            ld4(kr + rp + m, kp + m);
+            ld4(gr + r0 + m, gg + m);
+            ld_table4(rcos, (r0 + m) * (int)sizeof(TCS), cs + m);
+            ld_table4(rsin, (r0 + m) * (int)sizeof(TCS), sn + m);
+        }
+        ld4(vr + 4 * cg, vv);
+        float sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const bool first = lane + 64 * e < HD;
+            const float q1 = elu1(qa[e]), k1 = elu1(ka[e]);
+            sq += first ? q1 * q1 : 0.f;
+            sk += first ? k1 * k1 : 0.f;
+        }
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            sq += __shfl_xor(sq, m);
+            sk += __shfl_xor(sk, m);
+        }
+        const float iq = inv_norm(sq), ik = inv_norm(sk);
+        const float sgn = r0 < PH ? -1.f : 1.f;
+        const float rope = a.use_rope ? 1.f : 0.f;
+        float qv[RPT], kv[RPT], dv[RPT];
+#pragma unroll
+        for (int m = 0; m < RPT; ++m) {
+            const float qn = elu1(qo[m]) * iq, kn = elu1(ko[m]) * ik;
+            const float qn2 = elu1(qp[m]) * iq, kn2 = elu1(kp[m]) * ik;
+            const float c = rope * cs[m] + (1.f - rope), sg = rope * sgn * sn[m];
+            qv[m] = qn * c + sg * qn2;
+            kv[m] = kn * c + sg * kn2;
+            dv[m] = sigmoid(gg[m]);
+        }
 
-    float o4[4] = {0.f, 0.f, 0.f, 0.f};
-    TS* sout_p = reinterpret_cast<TS*>(a.state_out) + srow + (int64_t)r0 * HD + 4 * cg;
+        f32x4 y[RPT];
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int m = 0; m < RPT; ++m) {
-        f32x4 s = st[m];
+        for (int m = 0; m < RPT; ++m) {
+            const f32x4 s = unpack(cur.w[m]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            s[c] = dv[m] * s[c] + kv[m] * vv[c];
-            o4[c] += qv[m] * s[c];
+            for (int c = 0; c < 4; ++c) {
+                y[m][c] = dv[m] * s[c] + kv[m] * vv[c];
+                o4[c] += qv[m] * y[m][c];
+            }
         }
-        if (a.save_final) {
-            const V4<TS> y = V4<TS>{(TS)s[0], (TS)s[1], (TS)s[2], (TS)s[3]};
-            __builtin_nontemporal_store(y, reinterpret_cast<V4<TS>*>(sout_p + m * HD));
+        const auto ro = row_rsrc(a.state_out, row, a.save_final != 0);
+#pragma unroll
+        for (int m = 0; m < RPT; ++m) {
+            if constexpr (SB == 4) {
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, y[m]), ro, voff + m * HD * SB, 0, 2);
+            } else {
+                const V4<TS> v = V4<TS>{(TS)y[m][0], (TS)y[m][1], (TS)y[m][2], (TS)y[m][3]};
+                __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), ro, voff + m * HD * SB, 0, 2);
+            }
         }
-    }
+        // the next row's state loads go out after this row's stores (a later wait for them then
+        // also covers these stores, which by then have long completed)
+        const uint32_t nrow = row + gridDim.x;
+        if (nrow < rows) fetch(nxt, nrow);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int sh = CG; sh < 64; sh <<= 1) o4[c] += __shfl_xor(o4[c], sh);
-    __shared__ f32x4 red[WAVES][CG];
-    if (lane < CG) red[wave][cg] = f32x4{o4[0], o4[1], o4[2], o4[3]};
-    __syncthreads();
-    if (tid < CG) {
-        f32x4 s = red[0][cg];
+            for (int sh = CG; sh < 64; sh <<= 1) o4[c] += __shfl_xor(o4[c], sh);
+        if (lane < CG) red[buf][wave][cg] = f32x4{o4[0], o4[1], o4[2], o4[3]};
+        // barrier ordering LDS only: the state stores need not complete before it
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if (tid < CG) {
+            f32x4 s = red[buf][0][cg];
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) s += red[w][cg];
-        store4_dt(reinterpret_cast<char*>(a.o) + (b * a.o_sb + h * a.o_sh + 4 * cg) * dt_size(a.o_dt), a.o_dt, s[0], s[1],
-                  s[2], s[3]);
+            for (int w = 1; w < WAVES; ++w) s += red[buf][w][cg];
+            store4_dt(reinterpret_cast<char*>(a.o) + (b * a.o_sb + h * a.o_sh + 4 * cg) * dt_size(a.o_dt), a.o_dt, s[0],
+                      s[1], s[2], s[3]);
+        }
+    };
+    // Two register sets used in turn, so no loaded state is ever copied between registers (a copy
+    // would wait for the prefetch before the current row's stores).
+    Raw A, B;
+    uint32_t row = blockIdx.x;
+    fetch(A, row);
+    while (row < rows) {
+        step(A, B, row, 0);
+        row += gridDim.x;
+        if (row >= rows) break;
+        step(B, A, row, 1);
+        row += gridDim.x;
     }
 }
 
@@ -261,9 +354,10 @@ hipError_t launch_gla_prep(const PrepParams& a, int HD, int io_dt, int cs_dt, hi
 
 template <int HD, typename TIO, typename TCS, typename TS>
 static hipError_t launch_fdec_t(const FusedDecodeParams& a, hipStream_t stream) {
-    constexpr int RPT = HD * HD / (4 * 256) > 4 ? HD * HD / (4 * 256) : 4;
-    constexpr int TPB = HD * HD / (4 * RPT);
-    hipLaunchKernelGGL((gla_fused_decode_kernel<HD, TIO, TCS, TS>), dim3((unsigned)(a.B * a.H)), dim3(TPB), 0, stream, a);
+    const uint32_t rows = (uint32_t)(a.B * a.H);
+    const uint32_t blocks = rows < (uint32_t)a.max_blocks ? rows : (uint32_t)a.max_blocks;
+    hipLaunchKernelGGL((gla_fused_decode_kernel<HD, TIO, TCS, TS>), dim3(blocks), dim3(FusedDecodeTiling<HD>::TPB), 0,
+                       stream, a, rows);
     return hipGetLastError();
 }
 

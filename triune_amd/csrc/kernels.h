@@ -114,6 +114,7 @@ struct FusedDecodeParams {
     int o_dt;
     int64_t o_sb, o_sh;
     int64_t B, H;
+    int max_blocks;  // grid cap (blocks then walk several rows)
 };
 
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);

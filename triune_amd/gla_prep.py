@@ -68,12 +68,13 @@ def fused_qkv_g_prep_inplace(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin=N
 
 
 def fused_qkvg_decode_step(qkvg: torch.Tensor, cos=None, sin=None, initial_state=None, save_final: bool = True,
-                           use_rope: bool = True, state_dtype=None, out=None):
+                           use_rope: bool = True, state_dtype=None, out=None, inplace: bool = False):
     """One decode step fused with the pre-processing (reference: attention.py:81-179, launched at
     :396-415).  qkvg: [B, 4, H, HD]; cos/sin: [1, HD] or [HD] of the step's position;
     initial_state: [B, H, HD, HD] or None (zero).  The state is kept in state_dtype (default: the
     initial state's dtype, else qkvg.dtype, as the reference does; fp32 is also accepted).
-    Returns (out [B, 1, H, HD] in qkvg.dtype, final state or None)."""
+    inplace=True writes the new state into initial_state (contiguous, of state_dtype) instead of a
+    new tensor.  Returns (out [B, 1, H, HD] in qkvg.dtype, final state or None)."""
     _cuda(qkvg, cos, sin, initial_state)
     if qkvg.dim() != 4 or qkvg.shape[1] != 4:
         raise ValueError("qkvg must be [B, 4, H, HD]")
@@ -91,7 +92,12 @@ def fused_qkvg_decode_step(qkvg: torch.Tensor, cos=None, sin=None, initial_state
         if tuple(initial_state.shape) != (B, H, HD, HD):
             raise ValueError(f"initial_state must be [B, H, HD, HD], got {tuple(initial_state.shape)}")
         s_in = initial_state.to(dtype=state_dtype).contiguous()
-    s_out = torch.empty(B, H, HD, HD, device=qkvg.device, dtype=state_dtype) if save_final else None
+    if inplace:
+        if s_in is None or s_in.data_ptr() != initial_state.data_ptr() or not save_final:
+            raise ValueError("inplace needs a contiguous initial_state of state_dtype and save_final")
+        s_out = s_in
+    else:
+        s_out = torch.empty(B, H, HD, HD, device=qkvg.device, dtype=state_dtype) if save_final else None
     cs_dt = 0
     if use_rope:
         if cos is None or sin is None:
