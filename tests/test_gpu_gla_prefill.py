@@ -155,6 +155,28 @@ def test_strided_qkv_views_and_out_aliasing_g(dev):
     assert s2.numel() == 1
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_out_aliasing_g_with_tokenwise_chunks(dev, D):
+    """out = g while some chunks run token by token (decay span past the factored range) and the
+    sequence ends in the reference's 1-token tail (T = 64k + 1): every gate read of a token must
+    land before any wave stores that token's output over it."""
+    B, T, H = 2, 257, 2
+    gen = torch.Generator().manual_seed(17 + D)
+    qkv = torch.randn(B, T, 3, H, D, generator=gen).bfloat16()
+    qkv[:, :, 0] *= D**-0.5
+    g = (torch.nn.functional.logsigmoid(torch.randn(B, T, H, D, generator=gen)) / 16).float()
+    g[:, 64:128] = -1.0 - 20.0 * torch.rand(B, 64, H, D, generator=gen)
+    g = g.bfloat16()
+    s0 = 0.1 * torch.randn(B, H, D, D, generator=gen)
+    ro, rs = O.gla_fwd(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, s0)
+    qkv_d, g_d = qkv.to(dev), g.to(dev)
+    o, s = _triton_chunk_gla_tc_fwd(qkv_d[:, :, 0], qkv_d[:, :, 1], qkv_d[:, :, 2], g_d, initial_state=s0.to(dev), out=g_d)
+    torch.cuda.synchronize()
+    assert o.data_ptr() == g_d.data_ptr()
+    _assert_bf16_close(o.cpu(), ro)
+    assert _err(s.cpu().double(), rs) <= TOL16
+
+
 def test_chunked_prefill_equals_full_prefill(dev):
     """Prefill in slices with a carried fp32 state == one prefill (test_long_context_performance.py:71-107)."""
     q, k, v, g, s0 = gla_inputs(2, 1100, 2, 64, seed=31, dtype=torch.bfloat16, init_std=0.1)
