@@ -212,6 +212,132 @@ ORACLE_API void oracle_recurrent_scan_fwd(const double* kv, const double* decay,
         }
 }
 
+/* Backward of the exclusive affine scan above (reference: _recurrent_scan_bwd,
+ * triune/kernels/fast_gla.py:67-107, and FusedRecurrentScan.backward :151-203):
+ *   d = d_fin;  for n = N-1..0:  d_kv[n] = d;  d_decay[n][i] = sum_j d[i][j] s_all[n][i][j];
+ *                                d = d_s_all[n] + decay[n] * d;
+ *   d_init = d.
+ * d_s_all / d_fin may be NULL (zero).  d_decay is [B,H,N,Dk] (summed over Dv). */
+ORACLE_API void oracle_recurrent_scan_bwd(const double* d_s_all, const double* d_fin, const double* decay,
+                                          const double* s_all, double* d_kv, double* d_decay, double* d_init,
+                                          long B, long H, long N, int Dk, int Dv) {
+    long DD = (long)Dk * Dv;
+#pragma omp parallel for schedule(static)
+    for (long bh = 0; bh < B * H; ++bh) {
+        double* d = (double*)malloc(sizeof(double) * (size_t)DD);
+        for (long e = 0; e < DD; ++e) d[e] = d_fin ? d_fin[bh * DD + e] : 0.0;
+        for (long n = N - 1; n >= 0; --n) {
+            long base = (bh * N + n) * DD;
+            for (int i = 0; i < Dk; ++i) {
+                double acc = 0.0, dec = decay[(bh * N + n) * Dk + i];
+                for (int j = 0; j < Dv; ++j) {
+                    long e = (long)i * Dv + j;
+                    d_kv[base + e] = d[e];
+                    acc += d[e] * s_all[base + e];
+                    d[e] = (d_s_all ? d_s_all[base + e] : 0.0) + dec * d[e];
+                }
+                d_decay[(bh * N + n) * Dk + i] = acc;
+            }
+        }
+        for (long e = 0; e < DD; ++e) d_init[bh * DD + e] = d[e];
+        free(d);
+    }
+}
+
+/* Gradients of oracle_gla_fwd (same clamp semantics) for upstream gradients do [B,T,H,Dv] and
+ * ds_fin [B,H,Dk,Dv] (either may be NULL = zero).  With D_t the total gradient reaching S_t:
+ *   D_{T-1} = ds_fin + q_{T-1} do_{T-1}^T ,  D_{t-1} = q_{t-1} do_{t-1}^T + diag(a_t) D_t
+ *   dq_t = S_t do_t ,  dk_t = D_t v_t ,  dv_t = D_t^T k_t ,
+ *   d(g_eff)_t[i] = a_t[i] sum_j D_t[i][j] S_{t-1}[i][j] ,  ds0 = diag(a_0) D_0
+ * with a_t = exp(g_eff_t).  A clamped token passes its gradient where g <= 0 (the derivative of
+ * torch.clamp(g, max=0), fast_gla.py:586) and none where g > 0; an unclamped token passes it all.
+ * The forward keeps every state (T+1 of them per head), so sizes stay test-sized. */
+static void gla_bwd_one_head(const double* q, const double* k, const double* v, const double* g,
+                             const double* dout, long T, long sk, long sv, int Dk, int Dv, const double* s0,
+                             const double* dsf, double* dq, double* dk, double* dv, double* dg, double* ds0,
+                             long chunk, int clamp_mode) {
+    const size_t DD = (size_t)Dk * Dv;
+    double* hist = (double*)malloc(sizeof(double) * DD * (size_t)(T + 1));  /* hist[t+1] = S_t */
+    double* D = (double*)malloc(sizeof(double) * DD);
+    if (s0) memcpy(hist, s0, sizeof(double) * DD);
+    else memset(hist, 0, sizeof(double) * DD);
+    for (long t = 0; t < T; ++t) {
+        const double* kt = k + t * sk;
+        const double* gt = g + t * sk;
+        const double* vt = v + t * sv;
+        int do_clamp = clamp_mode == 1 ? 1 : (clamp_mode == 0 ? 0 : clamp_token(t, T, chunk));
+        const double* P = hist + (size_t)t * DD;
+        double* S = hist + (size_t)(t + 1) * DD;
+        for (int i = 0; i < Dk; ++i) {
+            double gi = gt[i];
+            if (do_clamp && gi > 0.0) gi = 0.0;
+            double a = exp(gi);
+            for (int j = 0; j < Dv; ++j) S[(size_t)i * Dv + j] = a * P[(size_t)i * Dv + j] + kt[i] * vt[j];
+        }
+    }
+    for (size_t e = 0; e < DD; ++e) D[e] = dsf ? dsf[e] : 0.0;
+    for (long t = T - 1; t >= 0; --t) {
+        const double* qt = q + t * sk;
+        const double* kt = k + t * sk;
+        const double* gt = g + t * sk;
+        const double* vt = v + t * sv;
+        const double* dot = dout ? dout + t * sv : NULL;
+        int do_clamp = clamp_mode == 1 ? 1 : (clamp_mode == 0 ? 0 : clamp_token(t, T, chunk));
+        const double* S = hist + (size_t)(t + 1) * DD;
+        const double* P = hist + (size_t)t * DD;
+        if (dot)
+            for (int i = 0; i < Dk; ++i)
+                for (int j = 0; j < Dv; ++j) D[(size_t)i * Dv + j] += qt[i] * dot[j];
+        for (int i = 0; i < Dk; ++i) {
+            double aq = 0.0, ak = 0.0, ag = 0.0;
+            for (int j = 0; j < Dv; ++j) {
+                size_t e = (size_t)i * Dv + j;
+                if (dot) aq += S[e] * dot[j];
+                ak += D[e] * vt[j];
+                ag += D[e] * P[e];
+            }
+            double gi = gt[i];
+            int pass = !(do_clamp && gi > 0.0);
+            if (do_clamp && gi > 0.0) gi = 0.0;
+            double a = exp(gi);
+            dq[t * sk + i] = aq;
+            dk[t * sk + i] = ak;
+            dg[t * sk + i] = pass ? a * ag : 0.0;
+        }
+        for (int j = 0; j < Dv; ++j) {
+            double acc = 0.0;
+            for (int i = 0; i < Dk; ++i) acc += D[(size_t)i * Dv + j] * kt[i];
+            dv[t * sv + j] = acc;
+        }
+        for (int i = 0; i < Dk; ++i) {
+            double gi = gt[i];
+            if (do_clamp && gi > 0.0) gi = 0.0;
+            double a = exp(gi);
+            for (int j = 0; j < Dv; ++j) D[(size_t)i * Dv + j] *= a;
+        }
+    }
+    if (ds0) memcpy(ds0, D, sizeof(double) * DD);
+    free(D);
+    free(hist);
+}
+
+ORACLE_API void oracle_gla_bwd(const double* q, const double* k, const double* v, const double* g,
+                               const double* s0, const double* dout, const double* dsf, double* dq, double* dk,
+                               double* dv, double* dg, double* ds0, long B, long T, long H, int Dk, int Dv,
+                               long chunk, int clamp_mode) {
+#pragma omp parallel for schedule(dynamic)
+    for (long bh = 0; bh < B * H; ++bh) {
+        long b = bh / H, h = bh % H;
+        long sk = H * Dk, sv = H * Dv;
+        long ok = (b * T) * sk + h * Dk, ov = (b * T) * sv + h * Dv;
+        const double* s0b = s0 ? s0 + bh * (long)Dk * Dv : NULL;
+        const double* dsb = dsf ? dsf + bh * (long)Dk * Dv : NULL;
+        gla_bwd_one_head(q + ok, k + ok, v + ov, g + ok, dout ? dout + ov : NULL, T, sk, sv, Dk, Dv, s0b, dsb,
+                         dq + ok, dk + ok, dv + ov, dg + ok, ds0 ? ds0 + bh * (long)Dk * Dv : NULL, chunk,
+                         clamp_mode);
+    }
+}
+
 /* Gated DeltaNet, the reference variant (fast_gla.py:781-836 and :453-471):
  *   u_t   = v_t - S_{t-1}^T k_t              (prediction from the un-decayed state)
  *   S_t   = diag(exp(min(g_t,0))) S_{t-1} + W_t

@@ -43,6 +43,8 @@ def _lib():
         lib.oracle_gla_closed_form.argtypes = [_dp] * 7 + [_L, _L, _L, _I, _I]
         lib.oracle_gla_decode_step.argtypes = [_dp] * 6 + [_L, _I, _I]
         lib.oracle_recurrent_scan_fwd.argtypes = [_dp] * 5 + [_L, _L, _L, _I, _I]
+        lib.oracle_recurrent_scan_bwd.argtypes = [_dp] * 7 + [_L, _L, _L, _I, _I]
+        lib.oracle_gla_bwd.argtypes = [_dp] * 12 + [_L, _L, _L, _I, _I, _L, _I]
         lib.oracle_gdn_fwd.argtypes = [_dp] * 5 + [_I, _dp, _dp, _dp, _L, _L, _L, _I, _I]
         lib.oracle_num_threads.restype = _I
         _LIB = lib
@@ -129,6 +131,35 @@ def recurrent_scan_fwd(kv, decay_k, init):
     fin = np.empty((B, H, Dk, Dv))
     _lib().oracle_recurrent_scan_fwd(_p(kv), _p(dec), _p(init), _p(s_all), _p(fin), B, H, N, Dk, Dv)
     return s_all, fin
+
+
+def recurrent_scan_bwd(d_s_all, d_fin, decay_k, s_all):
+    """FusedRecurrentScan backward (fast_gla.py:67-107, :151-203): upstream gradients d_s_all
+    [B,H,N,Dk,Dv] and d_fin [B,H,Dk,Dv] (None = zero), decay_k [B,H,N,Dk,1], the forward's
+    s_all.  Returns (d_kv [B,H,N,Dk,Dv], d_decay [B,H,N,Dk,1], d_init [B,H,Dk,Dv])."""
+    s_all = _d(s_all)
+    B, H, N, Dk, Dv = s_all.shape
+    dec = np.ascontiguousarray(np.broadcast_to(_d(decay_k), (B, H, N, Dk, 1))[..., 0])
+    d_kv = np.empty_like(s_all)
+    d_dec = np.empty((B, H, N, Dk))
+    d_init = np.empty((B, H, Dk, Dv))
+    _lib().oracle_recurrent_scan_bwd(_p(_d(d_s_all)), _p(_d(d_fin)), _p(dec), _p(s_all), _p(d_kv), _p(d_dec),
+                                     _p(d_init), B, H, N, Dk, Dv)
+    return d_kv, d_dec[..., None], d_init
+
+
+def gla_bwd(q, k, v, g, s0=None, do=None, ds_fin=None, chunk=64, clamp_mode=2):
+    """Gradients of gla_fwd (same clamp semantics) for upstream do [B,T,H,Dv] and ds_fin
+    [B,H,Dk,Dv] (None = zero).  Returns (dq, dk, dv, dg, ds0)."""
+    q, k, v, g, s0, do, ds_fin = (_d(x) for x in (q, k, v, g, s0, do, ds_fin))
+    B, T, H, Dk = q.shape
+    Dv = v.shape[-1]
+    dq, dk, dg = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    dv = np.empty_like(v)
+    ds0 = np.empty((B, H, Dk, Dv))
+    _lib().oracle_gla_bwd(_p(q), _p(k), _p(v), _p(g), _p(s0), _p(do), _p(ds_fin), _p(dq), _p(dk), _p(dv), _p(dg),
+                          _p(ds0), B, T, H, Dk, Dv, chunk, clamp_mode)
+    return dq, dk, dv, dg, ds0
 
 
 BETA_NONE, BETA_HEAD, BETA_KEY, BETA_VALUE = 0, 1, 2, 3

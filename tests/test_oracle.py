@@ -325,3 +325,119 @@ def test_fused_decode_oracle_brute_force():
             assert np.abs(q @ Sn - o[b, h]).max() <= 1e-13
     o0, S0z = O.fused_decode_step(x, None, None, None)  # no rotation, zero state
     assert np.abs(S0z - np.einsum("bhi,bhj->bhij", O.qk_prep(x[:, 1]), x[:, 2])).max() <= 1e-13
+
+
+# ---------------------------------------------------------------------------------------------
+# Backward (gradients of the GLA recurrence and of the exclusive scan)
+# ---------------------------------------------------------------------------------------------
+def _torch_gla(q, k, v, g, s0, chunk):
+    """fp64 token recurrence with fast_chunk_gla's clamp dispatch, differentiated by autograd
+    (the reference's own gradient check recurrence, test_kernels.py:270-277)."""
+    B, T, H, Dk = q.shape
+    S = s0 if s0 is not None else torch.zeros(B, H, Dk, v.shape[-1], dtype=torch.float64)
+    outs = []
+    for t in range(T):
+        clamp = not (T == 1 or (T > chunk and T % chunk == 1 and t == T - 1))
+        gt = torch.clamp(g[:, t], max=0.0) if clamp else g[:, t]
+        S = S * torch.exp(gt).unsqueeze(-1) + k[:, t].unsqueeze(-1) @ v[:, t].unsqueeze(-2)
+        outs.append((q[:, t].unsqueeze(-2) @ S).squeeze(-2))
+    return torch.stack(outs, dim=1), S
+
+
+@pytest.mark.parametrize("T,chunk,with_init", [(1, 64, True), (17, 64, False), (65, 64, True), (70, 32, True),
+                                               (33, 32, False)])
+def test_gla_bwd_matches_autograd(T, chunk, with_init):
+    """Every gradient (q, k, v, g, S0) equals torch autograd through the fp64 recurrence,
+    including the clamp mask (positive and exactly-zero gates) and the unclamped tail."""
+    B, H, Dk, Dv = 2, 2, 5, 3
+    rng = np.random.default_rng(T)
+    q, k, v = (torch.tensor(rng.standard_normal((B, T, H, d)), requires_grad=True) for d in (Dk, Dk, Dv))
+    gn = -np.abs(rng.standard_normal((B, T, H, Dk)))
+    gn[:, ::3, :, 0] = 0.3 * np.abs(gn[:, ::3, :, 0]) + 0.05  # some positive gates (clamped -> zero grad)
+    gn[:, 1::4, :, 1] = 0.0  # exact zeros: torch.clamp passes the gradient at the boundary
+    gn[:, -1] = 0.2  # the final token's gates positive: unclamped iff it is a 1-token tail
+    g = torch.tensor(gn, requires_grad=True)
+    s0 = torch.tensor(rng.standard_normal((B, H, Dk, Dv)), requires_grad=True) if with_init else None
+    do = torch.tensor(rng.standard_normal((B, T, H, Dv)))
+    dsf = torch.tensor(rng.standard_normal((B, H, Dk, Dv)))
+    o, s = _torch_gla(q, k, v, g, s0, chunk)
+    ((o * do).sum() + (s * dsf).sum()).backward()
+    dq, dk, dv, dg, ds0 = O.gla_bwd(q, k, v, g, s0, do, dsf, chunk=chunk)
+    for got, ref in ((dq, q.grad), (dk, k.grad), (dv, v.grad), (dg, g.grad)):
+        np.testing.assert_allclose(got, ref.numpy(), rtol=1e-11, atol=1e-11)
+    if with_init:
+        np.testing.assert_allclose(ds0, s0.grad.numpy(), rtol=1e-11, atol=1e-11)
+
+
+def test_gla_bwd_finite_differences():
+    """Central differences of the oracle's own forward agree with its backward (no torch)."""
+    B, T, H, Dk, Dv = 1, 6, 1, 3, 2
+    rng = np.random.default_rng(3)
+    q, k = rng.standard_normal((2, B, T, H, Dk))
+    v = rng.standard_normal((B, T, H, Dv))
+    g = -0.2 - np.abs(rng.standard_normal((B, T, H, Dk)))  # away from the clamp boundary
+    s0 = rng.standard_normal((B, H, Dk, Dv))
+    W = rng.standard_normal((B, T, H, Dv))
+    U = rng.standard_normal((B, H, Dk, Dv))
+
+    def loss(q, k, v, g, s0):
+        o, s = O.gla_fwd(q, k, v, g, s0)
+        return float((o * W).sum() + (s * U).sum())
+
+    grads = O.gla_bwd(q, k, v, g, s0, W, U)
+    args = [q, k, v, g, s0]
+    eps = 1e-6
+    for a, ga in zip(range(5), grads):
+        x = args[a]
+        for idx in [tuple(rng.integers(0, n) for n in x.shape) for _ in range(6)]:
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            ap, am = list(args), list(args)
+            ap[a], am[a] = xp, xm
+            fd = (loss(*ap) - loss(*am)) / (2 * eps)
+            assert abs(fd - ga[idx]) <= 1e-7 * max(1.0, abs(fd)), (a, idx, fd, ga[idx])
+
+
+def test_gla_bwd_zero_gate_brute_force():
+    """g = 0: o_t = sum_{s<=t} (q_t . k_s) v_s + S0^T q_t, whose gradients have closed forms:
+    dq_t = sum_{s<=t} (do_t . v_s) k_s + S0 do_t, dv_s = sum_{t>=s} (q_t . k_s) do_t,
+    dk_s = sum_{t>=s} (do_t . v_s) q_t, dS0 = sum_t q_t do_t^T (no final-state gradient)."""
+    B, T, H, D = 1, 9, 1, 4
+    rng = np.random.default_rng(8)
+    q, k, v, do = rng.standard_normal((4, B, T, H, D))
+    s0 = rng.standard_normal((B, H, D, D))
+    g = np.zeros((B, T, H, D))
+    dq, dk, dv, dg, ds0 = O.gla_bwd(q, k, v, g, s0, do, None)
+    Q, K, V, DO = q[0, :, 0], k[0, :, 0], v[0, :, 0], do[0, :, 0]
+    M = np.tril(np.ones((T, T)))
+    np.testing.assert_allclose(dq[0, :, 0], (M * (DO @ V.T)) @ K + DO @ s0[0, 0].T, atol=1e-12)
+    np.testing.assert_allclose(dv[0, :, 0], (M * (Q @ K.T)).T @ DO, atol=1e-12)
+    np.testing.assert_allclose(dk[0, :, 0], (M * (DO @ V.T)).T @ Q, atol=1e-12)
+    np.testing.assert_allclose(ds0[0, 0], Q.T @ DO, atol=1e-12)
+
+
+@pytest.mark.parametrize("with_init", [False, True])
+def test_scan_bwd_matches_autograd(with_init):
+    """The reference's own check (test_kernels.py:236-264), in fp64: autograd through the
+    sequential addcmul loop."""
+    B, H, N, Dk, Dv = 2, 3, 7, 4, 5
+    rng = np.random.default_rng(11 + with_init)
+    kv = torch.tensor(rng.standard_normal((B, H, N, Dk, Dv)), requires_grad=True)
+    dec = torch.tensor(rng.random((B, H, N, Dk, 1)), requires_grad=True)
+    init = torch.tensor(rng.standard_normal((B, H, Dk, Dv)) if with_init else np.zeros((B, H, Dk, Dv)),
+                        requires_grad=True)
+    cur, states = init, []
+    for i in range(N):
+        states.append(cur)
+        cur = torch.addcmul(kv[:, :, i], cur, dec[:, :, i])
+    s_all = torch.stack(states, dim=2)
+    gs = torch.tensor(rng.standard_normal(s_all.shape))
+    gf = torch.tensor(rng.standard_normal(cur.shape))
+    ((s_all * gs).sum() + (cur * gf).sum()).backward()
+    d_kv, d_dec, d_init = O.recurrent_scan_bwd(gs, gf, dec, s_all.detach())
+    np.testing.assert_allclose(d_kv, kv.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(d_dec, dec.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(d_init, init.grad.numpy(), rtol=1e-12, atol=1e-12)
+    d_kv0, _, d_init0 = O.recurrent_scan_bwd(None, gf, dec, s_all.detach())
+    assert np.abs(d_kv0[:, :, -1] - gf.numpy()).max() == 0.0  # the last step sees only d_fin
