@@ -26,6 +26,8 @@
  *                                     fast_chunk_gla calls over the packed sequences
  *   triune_hip_recurrent_scan_fwd  <- FusedRecurrentScan.forward, triune/kernels/fast_gla.py:109-149
  *                                     (_recurrent_scan_fwd, fast_gla.py:34-64)
+ *   triune_hip_recurrent_scan_bwd  <- FusedRecurrentScan.backward, triune/kernels/fast_gla.py:151-203
+ *                                     (_recurrent_scan_bwd, fast_gla.py:67-107)
  *   triune_hip_gdn_prefill         <- fast_chunk_gated_deltanet, triune/kernels/fast_gla.py:839-904,
  *                                     with _triton_gated_deltanet_fwd (fast_gla.py:479-550) and
  *                                     fast_recurrent_gated_deltanet (fast_gla.py:781-836)
@@ -138,6 +140,21 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
 int triune_hip_recurrent_scan_fwd(const void* kv, int kv_dtype, const void* decay, int decay_dtype, const void* init,
                                   int init_dtype, void* s_all, void* fin, int out_dtype, int64_t B, int64_t H,
                                   int64_t N, int Dk, int Dv, void* stream);
+
+/* Backward of the exclusive scan (FusedRecurrentScan.backward), all tensors contiguous:
+ *     d = d_fin ;  for n = N-1 .. 0:  d_kv[b,h,n] = d ;
+ *         d_decay[b,h,n,i] = sum_j d[i,j] * s_all[b,h,n,i,j] ;  d = d_s_all[b,h,n] + decay[b,h,n,:,None] * d
+ *     d_init[b,h] = d
+ * d_s_all: [B, H, N, Dk, Dv] in d_s_all_dtype, d_fin: [B, H, Dk, Dv] in d_fin_dtype (either NULL =
+ * zero); decay: [B, H, N, Dk] in decay_dtype; s_all: the forward's exclusive states in fp32
+ * [B, H, N, Dk, Dv]; d_kv [B, H, N, Dk, Dv], d_decay [B, H, N, Dk] (summed over Dv) and d_init
+ * [B, H, Dk, Dv] in out_dtype (the reference returns kv.dtype gradients, fast_gla.py:199-203).
+ * Arithmetic in fp32.  Dv a multiple of 4, at most 256.
+ * Replaces: FusedRecurrentScan.backward (fast_gla.py:151-203, kernel :67-107). */
+int triune_hip_recurrent_scan_bwd(const void* d_s_all, int d_s_all_dtype, const void* d_fin, int d_fin_dtype,
+                                  const void* decay, int decay_dtype, const float* s_all, void* d_kv, void* d_decay,
+                                  void* d_init, int out_dtype, int64_t B, int64_t H, int64_t N, int Dk, int Dv,
+                                  void* stream);
 
 /* Gated DeltaNet forward, the reference's variant (fast_gla.py:781-836):
  *     u_t = v_t - S_{t-1}^T k_t ;  S_t = diag(exp(min(g_t,0))) S_{t-1} + beta_t . (k_t u_t^T) ;

@@ -101,6 +101,12 @@ def test_decode_and_gdn_and_scan_validation_errors():
     assert sc(None, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -1
     assert sc(_FAKE, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 6, None) == -2
     assert sc(_FAKE, 4, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -3
+    sb = lib.triune_hip_recurrent_scan_bwd
+    assert sb(None, 0, None, 0, None, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -1
+    assert sb(None, 0, None, 0, _FAKE, 0, None, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -1
+    assert sb(None, 0, None, 0, _FAKE, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 260, None) == -2
+    assert sb(None, 0, None, 0, _FAKE, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 6, None) == -2
+    assert sb(None, 0, _FAKE, 7, _FAKE, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -3
 
 
 def test_workspace_sizes():

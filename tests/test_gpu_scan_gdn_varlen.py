@@ -44,6 +44,53 @@ def test_recurrent_scan_bf16_returns_kv_dtype(dev):
     assert _err(fin.float().cpu(), rf) <= np.abs(rf).max() * 2**-7
 
 
+@pytest.mark.parametrize("N,Dk,Dv", [(1, 32, 32), (16, 32, 32), (37, 64, 64), (9, 5, 12), (7, 3, 256)])
+@pytest.mark.parametrize("with_init", [False, True])
+def test_recurrent_scan_backward_fp32(dev, N, Dk, Dv, with_init):
+    """Gradients through FusedRecurrentScan.apply (reference check: test_kernels.py:244-264) equal
+    the oracle's reverse scan; Dv that is not a power of two leaves lanes of a row idle."""
+    gen = torch.Generator().manual_seed(N + Dk + Dv)
+    B, H = 2, 3
+    kv = torch.randn(B, H, N, Dk, Dv, generator=gen)
+    decay = torch.rand(B, H, N, Dk, 1, generator=gen)
+    init = torch.randn(B, H, Dk, Dv, generator=gen) if with_init else torch.zeros(B, H, Dk, Dv)
+    gs = torch.randn(B, H, N, Dk, Dv, generator=gen)
+    gf = torch.randn(B, H, Dk, Dv, generator=gen)
+    kvd, dd, idd = (x.to(dev).requires_grad_(True) for x in (kv, decay, init))
+    s_all, fin = FusedRecurrentScan.apply(kvd, dd, idd)
+    ((s_all * gs.to(dev)).sum() + (fin * gf.to(dev)).sum()).backward()
+    torch.cuda.synchronize()
+    rs, _ = O.recurrent_scan_fwd(kv, decay, init)
+    r_kv, r_dec, r_init = O.recurrent_scan_bwd(gs, gf, decay, rs)
+    tol = 1e-5 * max(1.0, float(np.abs(r_kv).max()))
+    assert _err(kvd.grad.cpu(), r_kv) <= tol
+    assert _err(dd.grad.cpu(), r_dec) <= 1e-5 * max(1.0, float(np.abs(r_dec).max()))
+    assert _err(idd.grad.cpu(), r_init) <= tol
+    assert dd.grad.shape == decay.shape
+
+
+def test_recurrent_scan_backward_bf16_and_missing_grads(dev):
+    """bf16 kv: gradients come back in bf16 (fast_gla.py:199-203); only the final state used, so
+    the S_all gradient is absent (None) and every step sees the decayed d_fin alone."""
+    gen = torch.Generator().manual_seed(6)
+    B, H, N, D = 1, 2, 11, 64
+    kv = torch.randn(B, H, N, D, D, generator=gen).bfloat16()
+    decay = torch.rand(B, H, N, D, 1, generator=gen)
+    init = torch.randn(B, H, D, D, generator=gen)
+    gf = torch.randn(B, H, D, D, generator=gen)
+    kvd, dd, idd = (x.to(dev).requires_grad_(True) for x in (kv, decay, init))
+    _, fin = FusedRecurrentScan.apply(kvd, dd, idd)
+    (fin.float() * gf.to(dev)).sum().backward()
+    torch.cuda.synchronize()
+    assert kvd.grad.dtype == torch.bfloat16
+    rs, _ = O.recurrent_scan_fwd(kv, decay, init)
+    r_kv, r_dec, r_init = O.recurrent_scan_bwd(None, gf, decay, rs)
+    rel = 2**-7
+    assert _err(kvd.grad.float().cpu(), r_kv) <= rel * np.abs(r_kv).max()
+    assert _err(dd.grad.float().cpu(), r_dec) <= rel * np.abs(r_dec).max()
+    assert _err(idd.grad.float().cpu(), r_init) <= rel * np.abs(r_init).max()
+
+
 # --- Gated DeltaNet -----------------------------------------------------------------------------
 def _gdn_case(T, D, kind, seed):
     gen = torch.Generator().manual_seed(seed)

@@ -55,6 +55,10 @@ def _bind(lib):
             _i,
         ),
         "triune_hip_recurrent_scan_fwd": ([_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i, _i, _vp], _i),
+        "triune_hip_recurrent_scan_bwd": (
+            [_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i64, _i64, _i, _i, _vp],
+            _i,
+        ),
         "triune_hip_gdn_prefill": (
             [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _vp],
             _i,
@@ -88,6 +92,7 @@ EXPORTS = (
     "triune_hip_gla_prefill_varlen_workspace_size",
     "triune_hip_gla_prefill_varlen",
     "triune_hip_recurrent_scan_fwd",
+    "triune_hip_recurrent_scan_bwd",
     "triune_hip_gdn_prefill",
     "triune_hip_gdn_prefill_chunked_workspace_size",
     "triune_hip_gdn_prefill_chunked",

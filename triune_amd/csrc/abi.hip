@@ -382,6 +382,30 @@ int triune_hip_recurrent_scan_fwd(const void* kv, int kv_dtype, const void* deca
     return launch_status(launch_recurrent_scan(sc, (hipStream_t)stream));
 }
 
+int triune_hip_recurrent_scan_bwd(const void* d_s_all, int d_s_all_dtype, const void* d_fin, int d_fin_dtype,
+                                  const void* decay, int decay_dtype, const float* s_all, void* d_kv, void* d_decay,
+                                  void* d_init, int out_dtype, int64_t B, int64_t H, int64_t N, int Dk, int Dv,
+                                  void* stream) {
+    if (!decay || !d_kv || !d_decay || !d_init || (N > 0 && !s_all)) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(decay_dtype) || !dtype_ok(out_dtype) || (d_s_all && !dtype_ok(d_s_all_dtype)) ||
+        (d_fin && !dtype_ok(d_fin_dtype)))
+        return TRIUNE_ERR_DTYPE;
+    if (B < 0 || H < 0 || N < 0 || Dk <= 0 || Dv <= 0 || Dv % 4 != 0 || Dv > 256) return TRIUNE_ERR_SHAPE;
+    auto al = [](int dt) -> uintptr_t { return dt == TRIUNE_DT_F32 ? 16 : 8; };
+    auto mis = [](const void* p, uintptr_t m) { return reinterpret_cast<uintptr_t>(p) % m != 0; };
+    if ((d_s_all && mis(d_s_all, al(d_s_all_dtype))) || (d_fin && mis(d_fin, al(d_fin_dtype))) || mis(s_all, 16) ||
+        mis(d_kv, al(out_dtype)) || mis(d_init, al(out_dtype)))
+        return TRIUNE_ERR_LAYOUT;
+    if (B == 0 || H == 0) return TRIUNE_OK;
+    ScanBwdParams a{};
+    a.d_s_all = d_s_all; a.dsa_dt = d_s_all_dtype;
+    a.d_fin = d_fin; a.df_dt = d_fin_dtype;
+    a.dec = decay; a.dec_dt = decay_dtype;
+    a.s_all = s_all; a.d_kv = d_kv; a.d_dec = d_decay; a.d_init = d_init; a.out_dt = out_dtype;
+    a.n_outer = B; a.H = H; a.N = N; a.Dk = Dk; a.Dv = Dv;
+    return launch_status(launch_recurrent_scan_bwd(a, (hipStream_t)stream));
+}
+
 int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
                            const void* beta, int beta_dtype, int beta_kind, const int64_t* strides, const float* s0,
                            void* o, int o_dtype, float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv,

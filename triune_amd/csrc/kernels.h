@@ -61,6 +61,24 @@ struct ScanParams {
     const int32_t* seg_off; // per outer o: steps N_o = seg_off[o+1]-seg_off[o], first step seg_off[o]
 };
 
+// Backward of the exclusive scan (FusedRecurrentScan), all tensors contiguous:
+// d_s_all / s_all / d_kv [o][h][n][Dk][Dv], decay / d_decay [o][h][n][Dk], d_fin / d_init [o][h][Dk][Dv].
+struct ScanBwdParams {
+    const void* d_s_all;  // or null (zero)
+    int dsa_dt;
+    const void* d_fin;    // or null (zero)
+    int df_dt;
+    const void* dec;      // decay factors
+    int dec_dt;
+    const float* s_all;   // the forward's exclusive states, fp32
+    void* d_kv;
+    void* d_dec;
+    void* d_init;
+    int out_dt;
+    int64_t n_outer, H, N;
+    int Dk, Dv;
+};
+
 struct DecodeParams {
     const void* q; const void* k; const void* v; const void* g;
     int io_dt, g_dt, o_dt;
@@ -118,6 +136,7 @@ struct FusedDecodeParams {
 };
 
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);
+hipError_t launch_recurrent_scan_bwd(const ScanBwdParams& a, hipStream_t stream);
 hipError_t launch_gla_prep(const PrepParams& a, int HD, int io_dt, int cs_dt, hipStream_t stream);
 hipError_t launch_gla_fused_decode(const FusedDecodeParams& a, int HD, int io_dt, int cs_dt, int s_dt,
                                    hipStream_t stream);

@@ -135,6 +135,73 @@ __global__ __launch_bounds__(SCAN_TPB) void seg_scan_f32_kernel(ScanParams a) {
     if (a.fin) *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.fin) + o * a.f_so + h * a.f_sh + e) = s;
 }
 
+__device__ __forceinline__ void st1_dt(void* p, int dt, int64_t i, float x) {
+    if (dt == DT_F32) reinterpret_cast<float*>(p)[i] = x;
+    else if (dt == DT_BF16) reinterpret_cast<__bf16*>(p)[i] = (__bf16)x;
+    else reinterpret_cast<_Float16*>(p)[i] = (_Float16)x;
+}
+
+// Backward of the exclusive scan (reference: _recurrent_scan_bwd, fast_gla.py:67-107, and
+// FusedRecurrentScan.backward :151-203), for each (outer o, head h), walking n = N-1 .. 0:
+//   d_kv[n] = d ;  d_decay[n][i] = sum_j d[i][j] * s_all[n][i][j] ;  d = d_s_all[n] + decay[n] * d
+// from d = d_fin, and d_init = d at the end.  The reference sums d_decay over Dv afterwards
+// (d_decay * s_prev per element, then .sum(-1)); here the LPR lanes of a row reduce it in
+// registers.  grid: (ceil(Dk / (64 / LPR)), H, n_outer), one wave per block; lane = row-in-block
+// * LPR + c holds columns 4c .. 4c+3 of its row (LPR = smallest power of two >= Dv / 4).
+__global__ __launch_bounds__(64) void recurrent_scan_bwd_kernel(ScanBwdParams a, int lpr) {
+    const int lane = threadIdx.x;
+    const int row = blockIdx.x * (64 / lpr) + lane / lpr;
+    const int j0 = (lane % lpr) * 4;
+    const bool act = row < a.Dk && j0 < a.Dv;
+    const int64_t DD = (int64_t)a.Dk * a.Dv, N = a.N;
+    const int64_t bh = (int64_t)blockIdx.z * a.H + blockIdx.y;
+    const int64_t e = act ? (int64_t)row * a.Dv + j0 : 0;
+    const int64_t r = act ? row : 0;
+    float d[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.d_fin && act) ld4_dt(a.d_fin, a.df_dt, bh * DD + e, d);
+    constexpr int U = 4;
+    for (int64_t nn = N; nn > 0; nn -= U) {
+        float ds[U][4], sp[U][4], dc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t n = nn - 1 - u >= 0 ? nn - 1 - u : 0;
+            const int64_t i5 = (bh * N + n) * DD + e;
+            if (a.d_s_all) {
+                ld4_dt(a.d_s_all, a.dsa_dt, i5, ds[u]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) ds[u][c] = 0.f;
+            }
+            const float4 s4 = *reinterpret_cast<const float4*>(a.s_all + i5);
+            sp[u][0] = s4.x; sp[u][1] = s4.y; sp[u][2] = s4.z; sp[u][3] = s4.w;
+            dc[u] = ld_dt(a.dec, a.dec_dt, (bh * N + n) * a.Dk + r);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t n = nn - 1 - u;
+            if (n < 0) break;  // uniform
+            const int64_t i5 = (bh * N + n) * DD + e;
+            if (act) st4_dt(a.d_kv, a.out_dt, i5, d);
+            float part = act ? d[0] * sp[u][0] + d[1] * sp[u][1] + d[2] * sp[u][2] + d[3] * sp[u][3] : 0.f;
+            for (int off = lpr >> 1; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+            if (act && j0 == 0) st1_dt(a.d_dec, a.out_dt, (bh * N + n) * a.Dk + row, part);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) d[c] = ds[u][c] + dc[u] * d[c];
+        }
+    }
+    if (act) st4_dt(a.d_init, a.out_dt, bh * DD + e, d);
+}
+
+hipError_t launch_recurrent_scan_bwd(const ScanBwdParams& a, hipStream_t stream) {
+    int lpr = 1;
+    while (lpr * 4 < a.Dv) lpr <<= 1;
+    if (lpr > 64) return hipErrorInvalidValue;
+    const int rpb = 64 / lpr;
+    dim3 grid((unsigned)((a.Dk + rpb - 1) / rpb), (unsigned)a.H, (unsigned)a.n_outer);
+    hipLaunchKernelGGL(recurrent_scan_bwd_kernel, grid, dim3(64), 0, stream, a, lpr);
+    return hipGetLastError();
+}
+
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream) {
     const int64_t DD = (int64_t)a.Dk * a.Dv;
     dim3 grid((unsigned)((DD / 4 + SCAN_TPB - 1) / SCAN_TPB), (unsigned)a.H, (unsigned)a.n_outer);

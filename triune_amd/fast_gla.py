@@ -8,9 +8,7 @@ Differences from the reference, by design:
   * final states are returned in float32 (the reference returns q.dtype: fast_gla.py:332,
     :739-743); the recurrent state never round-trips through bf16 between calls;
   * beta of shape [B, T, H] at T == 1 is applied per (token, head); the reference's T == 1
-    branch broadcasts it against the wrong axes unless H == head_dim (fast_gla.py:880);
-  * backward passes are not provided (inference path only): FusedRecurrentScan.apply raises
-    if gradients are requested.
+    branch broadcasts it against the wrong axes unless H == head_dim (fast_gla.py:880).
 """
 
 from __future__ import annotations
@@ -295,21 +293,22 @@ def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None):
 
 
 # ---------------------------------------------------------------------------------------
-# FusedRecurrentScan (forward)
+# FusedRecurrentScan
 # ---------------------------------------------------------------------------------------
 
 
-class FusedRecurrentScan:
+class FusedRecurrentScan(torch.autograd.Function):
     """Exclusive affine scan over chunk states (reference: FusedRecurrentScan, fast_gla.py:109-203).
 
     apply(kv [B,H,N,Dk,Dv], decay_k [B,H,N,Dk,1], init_state [B,H,Dk,Dv]) ->
         (S_all [B,H,N,Dk,Dv], final [B,H,Dk,Dv]), both in kv.dtype, where S_all[:, :, n] is the
-    state before step n and each step is s <- decay * s + kv.  Forward only."""
+    state before step n and each step is s <- decay * s + kv.  Differentiable: when a gradient is
+    needed the forward keeps its states in fp32 (as the reference saves s_out, fast_gla.py:141)
+    and the backward runs triune_hip_recurrent_scan_bwd (reference kernel :67-107), returning
+    gradients in kv.dtype (:199-203)."""
 
     @staticmethod
-    def apply(kv: torch.Tensor, decay_k: torch.Tensor, init_state: torch.Tensor):
-        if torch.is_grad_enabled() and any(t.requires_grad for t in (kv, decay_k, init_state)):
-            raise NotImplementedError("FusedRecurrentScan backward is not implemented (inference path only)")
+    def forward(ctx, kv: torch.Tensor, decay_k: torch.Tensor, init_state: torch.Tensor):
         _on_device(kv, decay_k, init_state)
         B, H, N, Dk, Dv = kv.shape
         kvc = kv.contiguous()
@@ -317,14 +316,40 @@ class FusedRecurrentScan:
         init = init_state.expand(B, H, Dk, Dv).contiguous()
         if Dv % 4 != 0:
             raise ValueError("FusedRecurrentScan needs Dv % 4 == 0")
-        s_all = torch.empty_like(kvc)
-        fin = torch.empty(B, H, Dk, Dv, device=kv.device, dtype=kv.dtype)
+        grad = any(ctx.needs_input_grad)
+        sdt = torch.float32 if grad else kv.dtype
+        s_all = torch.empty(kvc.shape, device=kv.device, dtype=sdt)
+        fin = torch.empty(B, H, Dk, Dv, device=kv.device, dtype=sdt)
         rc = lib().triune_hip_recurrent_scan_fwd(
             ptr(kvc), dtype_code(kvc), ptr(dec), dtype_code(dec), ptr(init), dtype_code(init), ptr(s_all), ptr(fin),
             dtype_code(s_all), B, H, N, Dk, Dv, stream_of(kv),
         )
         check(rc, "triune_hip_recurrent_scan_fwd")
+        if grad:
+            if Dv > 256:
+                raise ValueError("FusedRecurrentScan backward supports Dv <= 256")
+            ctx.save_for_backward(dec, s_all)
+            ctx.kv_dtype = kv.dtype
+            return s_all.to(kv.dtype), fin.to(kv.dtype)
         return s_all, fin
+
+    @staticmethod
+    def backward(ctx, d_s_all, d_fin):
+        dec, s32 = ctx.saved_tensors
+        B, H, N, Dk, Dv = s32.shape
+        dsa = None if d_s_all is None else _vec_layout(d_s_all.contiguous())
+        dfi = None if d_fin is None else d_fin.contiguous()
+        odt = ctx.kv_dtype
+        d_kv = torch.empty(B, H, N, Dk, Dv, device=s32.device, dtype=odt)
+        d_dec = torch.empty(B, H, N, Dk, device=s32.device, dtype=odt)
+        d_init = torch.empty(B, H, Dk, Dv, device=s32.device, dtype=odt)
+        rc = lib().triune_hip_recurrent_scan_bwd(
+            ptr(dsa), dtype_code(dsa) if dsa is not None else 0, ptr(dfi), dtype_code(dfi) if dfi is not None else 0,
+            ptr(dec), dtype_code(dec), ptr(s32), ptr(d_kv), ptr(d_dec), ptr(d_init), dtype_code(d_kv),
+            B, H, N, Dk, Dv, stream_of(s32),
+        )
+        check(rc, "triune_hip_recurrent_scan_bwd")
+        return d_kv, d_dec.unsqueeze(-1), d_init
 
 
 # ---------------------------------------------------------------------------------------
