@@ -24,6 +24,9 @@
  *   triune_hip_gla_prefill_varlen  <- no reference counterpart (the reference has no
  *                                     cu_seqlens path); one launch = a Python loop of
  *                                     fast_chunk_gla calls over the packed sequences
+ *   triune_hip_gla_prefill_bwd     <- the gradients of fast_chunk_gla's training path (autograd through
+ *                                     _run_gla_chunks, triune/kernels/fast_gla.py:569-689, and
+ *                                     FusedRecurrentScan.backward, fast_gla.py:151-203)
  *   triune_hip_recurrent_scan_fwd  <- FusedRecurrentScan.forward, triune/kernels/fast_gla.py:109-149
  *                                     (_recurrent_scan_fwd, fast_gla.py:34-64)
  *   triune_hip_recurrent_scan_bwd  <- FusedRecurrentScan.backward, triune/kernels/fast_gla.py:151-203
@@ -128,6 +131,24 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
                                   int64_t total_tokens, const float* s0, void* o, int o_dtype, float* s_final,
                                   int64_t H, int Dk, int Dv, int flags, void* workspace, size_t workspace_bytes,
                                   void* stream);
+
+/* Gradients of triune_hip_gla_prefill (dense, same flags) for the upstream gradients dout (of o,
+ * [B, T, H, Dv] in io_dtype) and ds_final (of the final state, fp32 [B, H, Dk, Dv], or NULL = 0):
+ *     dq_t = S_t do_t ,  dk_t = D_t v_t ,  dv_t = D_t^T k_t ,  ds0 = diag(a_0) D_0 ,
+ *     dg_t[i] = sum_{r >= t} (q_r[i] dq_r[i] - k_r[i] dk_r[i]) + sum_j ds_final[i][j] S_T[i][j]
+ * with D_t the total gradient reaching S_t and a_t = exp(g_eff_t); dg is 0 where a clamped token
+ * had g > 0 (the derivative of torch.clamp(g, max=0), fast_gla.py:586).  strides[27] = (batch,
+ * token, head) element strides of q, k, v, g, dout, dq, dk, dv, dg.  dq, dk, dv in d_dtype, dg in
+ * dg_dtype; ds0 fp32 [B, H, Dk, Dv] or NULL.  Dk == Dv in {32, 64} (32 only for fp32 I/O); q, k, v,
+ * g, dout rows 16-byte aligned, gradient rows 8-byte aligned.  workspace: at least
+ * triune_hip_gla_prefill_bwd_workspace_size() bytes, 16-byte aligned.
+ * Replaces: the backward of fast_chunk_gla (fast_gla.py:692-778) for T > 1. */
+size_t triune_hip_gla_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags);
+int triune_hip_gla_prefill_bwd(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                               const void* dout, const int64_t* strides, const float* s0, const float* ds_final,
+                               void* dq, void* dk, void* dv, int d_dtype, void* dg, int dg_dtype, float* ds0,
+                               int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* Exclusive affine scan (FusedRecurrentScan forward), all tensors contiguous:
  *     s_all[b,h,n] = s ;  s = decay[b,h,n,:,None] * s + kv[b,h,n]      (s starts at init or 0)

@@ -55,6 +55,12 @@ def _bind(lib):
             _i,
         ),
         "triune_hip_recurrent_scan_fwd": ([_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i, _i, _vp], _i),
+        "triune_hip_gla_prefill_bwd_workspace_size": ([_i64, _i64, _i64, _i, _i, _i], ctypes.c_size_t),
+        "triune_hip_gla_prefill_bwd": (
+            [_vp, _vp, _vp, _vp, _i, _i, _vp, _i64p, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp,
+             _i64, _i64, _i64, _i, _i, _i, _vp, ctypes.c_size_t, _vp],
+            _i,
+        ),
         "triune_hip_recurrent_scan_bwd": (
             [_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _vp, _vp, _i, _i64, _i64, _i64, _i, _i, _vp],
             _i,
@@ -92,6 +98,8 @@ EXPORTS = (
     "triune_hip_gla_prefill_varlen_workspace_size",
     "triune_hip_gla_prefill_varlen",
     "triune_hip_recurrent_scan_fwd",
+    "triune_hip_gla_prefill_bwd_workspace_size",
+    "triune_hip_gla_prefill_bwd",
     "triune_hip_recurrent_scan_bwd",
     "triune_hip_gdn_prefill",
     "triune_hip_gdn_prefill_chunked_workspace_size",

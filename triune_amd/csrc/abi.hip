@@ -139,6 +139,26 @@ PrefillPlan plan_varlen(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,
     return p;
 }
 
+// Backward workspace: the forward's segment plan and workspaces, then the segment maps R (later
+// the gradient at each segment's end), the segment end states and every chunk's starting state.
+struct BwdPlan {
+    PrefillPlan f;
+    int64_t nchunks;
+    size_t off_r, off_send, off_chunk, total;
+};
+
+BwdPlan plan_bwd(int64_t B, int64_t T, int64_t H, int D, int flags) {
+    BwdPlan p{};
+    p.f = plan_dense(B, T, H, D, D, flags);
+    p.nchunks = (T + 63) / 64;
+    const size_t dd = (size_t)D * D * sizeof(float);
+    p.off_r = p.f.total;
+    p.off_send = p.off_r + align_up((size_t)p.f.n_work * H * dd);
+    p.off_chunk = p.off_send + align_up((size_t)p.f.n_work * H * dd);
+    p.total = p.off_chunk + align_up((size_t)B * H * p.nchunks * dd);
+    return p;
+}
+
 int launch_status(hipError_t e) { return e == hipSuccess ? TRIUNE_OK : TRIUNE_ERR_LAUNCH; }
 
 // Events armed by triune_hip_set_output_kernel_events for this host thread (null: disarmed).
@@ -286,6 +306,105 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
 
     return launch_output_timed(a, pl.n_work, io_dtype, st);
+}
+
+size_t triune_hip_gla_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {
+    if (B <= 0 || T <= 0 || H <= 0 || Dk != Dv || !gla_bwd_supported(Dk, TRIUNE_DT_BF16)) return 0;
+    return plan_bwd(B, T, H, Dk, flags).total;
+}
+
+int triune_hip_gla_prefill_bwd(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                               const void* dout, const int64_t* strides, const float* s0, const float* ds_final,
+                               void* dq, void* dk, void* dv, int d_dtype, void* dg, int dg_dtype, float* ds0,
+                               int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !g || !dout || !strides || !dq || !dk || !dv || !dg) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(d_dtype) || !dtype_ok(dg_dtype)) return TRIUNE_ERR_DTYPE;
+    if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
+    if (B < 0 || T < 0 || H <= 0 || Dk != Dv || !gla_bwd_supported(Dk, io_dtype)) return TRIUNE_ERR_SHAPE;
+    const int64_t* st = strides;  // q, k, v, g, dout, dq, dk, dv, dg: (batch, token, head) each
+    auto rows_ok = [&](int i, int dt, int D) {
+        const int64_t es = dt == TRIUNE_DT_F32 ? 4 : 2;
+        return st[3 * i + 1] >= 0 && (64 * st[3 * i + 1] + D) * es < ((int64_t)1 << 31);
+    };
+    if (!vec_ok(q, io_dtype, st + 0, 3) || !vec_ok(k, io_dtype, st + 3, 3) || !vec_ok(v, io_dtype, st + 6, 3) ||
+        !vec_ok(g, g_dtype, st + 9, 3) || !vec_ok(dout, io_dtype, st + 12, 3) || !vec4_ok(dq, d_dtype, st + 15, 3) ||
+        !vec4_ok(dk, d_dtype, st + 18, 3) || !vec4_ok(dv, d_dtype, st + 21, 3) || !vec4_ok(dg, dg_dtype, st + 24, 3) ||
+        reinterpret_cast<uintptr_t>(s0) % 16 || reinterpret_cast<uintptr_t>(ds_final) % 16 ||
+        reinterpret_cast<uintptr_t>(ds0) % 16)
+        return TRIUNE_ERR_LAYOUT;
+    if (!rows_ok(0, io_dtype, Dk) || !rows_ok(1, io_dtype, Dk) || !rows_ok(2, io_dtype, Dv) || !rows_ok(3, g_dtype, Dk) ||
+        !rows_ok(4, io_dtype, Dv) || !rows_ok(5, d_dtype, Dk) || !rows_ok(6, d_dtype, Dk) || !rows_ok(7, d_dtype, Dv) ||
+        !rows_ok(8, dg_dtype, Dk))
+        return TRIUNE_ERR_LAYOUT;
+    hipStream_t hs = (hipStream_t)stream;
+    const int64_t D = Dk, DD = (int64_t)Dk * Dv;
+    if (B == 0) return TRIUNE_OK;
+    if (T == 0) {  // dS0 = dS_final (or zero)
+        if (!ds0) return TRIUNE_OK;
+        ScanParams sc{};
+        sc.kv = ds0; sc.kv_dt = DT_F32; sc.dec = ds0; sc.dec_dt = DT_F32;
+        sc.init = ds_final; sc.i_so = H * DD; sc.i_sh = DD;
+        sc.fin = ds0; sc.fin_dt = DT_F32; sc.f_so = sc.i_so; sc.f_sh = sc.i_sh;
+        sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = 0;
+        return launch_status(launch_recurrent_scan(sc, hs));
+    }
+    const BwdPlan pl = plan_bwd(B, T, H, Dk, flags);
+    if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
+    char* ws = reinterpret_cast<char*>(workspace);
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
+
+    BwdParams a{};
+    PrefillParams& f = a.f;
+    fill_tok(f.q, q, st + 0, B, T, H, Dk, io_dtype);
+    fill_tok(f.k, k, st + 3, B, T, H, Dk, io_dtype);
+    fill_tok(f.v, v, st + 6, B, T, H, Dv, io_dtype);
+    fill_tok(f.g, g, st + 9, B, T, H, Dk, g_dtype);
+    f.g_dt = g_dtype; f.o_dt = d_dtype;
+    f.s0 = s0;
+    f.ws_state = reinterpret_cast<float*>(ws + pl.f.off_state);
+    f.ws_gamma = reinterpret_cast<float*>(ws + pl.f.off_gamma);
+    f.n_seqs = B; f.H = H; f.T = T; f.Dk = Dk; f.Dv = Dv;
+    f.P = pl.f.P; f.nseg_dense = (int)pl.f.nseg; f.varlen = 0; f.flags = flags & 0xff;
+    fill_tok(a.dout, dout, st + 12, B, T, H, Dv, io_dtype);
+    a.dq = dq; a.dq_sb = st[15]; a.dq_st = st[16]; a.dq_sh = st[17];
+    a.dk = dk; a.dk_sb = st[18]; a.dk_st = st[19]; a.dk_sh = st[20];
+    a.dv = dv; a.dv_sb = st[21]; a.dv_st = st[22]; a.dv_sh = st[23];
+    a.dg = dg; a.dg_sb = st[24]; a.dg_st = st[25]; a.dg_sh = st[26];
+    a.d_dt = d_dtype; a.dg_dt = dg_dtype;
+    a.ws_r = reinterpret_cast<float*>(ws + pl.off_r);
+    a.ws_send = reinterpret_cast<float*>(ws + pl.off_send);
+    a.ws_chunk = reinterpret_cast<float*>(ws + pl.off_chunk);
+    a.nchunks = pl.nchunks;
+    const int64_t nseg = pl.f.nseg;
+
+    // forward: segment-local states, then the carried-in state of every segment
+    if (launch_gla_seg_state(f, pl.f.n_work, io_dtype, hs) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    ScanParams sc{};
+    sc.kv = f.ws_state; sc.kv_dt = DT_F32;
+    sc.kv_so = nseg * H * DD; sc.kv_sh = DD; sc.kv_sn = H * DD;
+    sc.dec = f.ws_gamma; sc.dec_dt = DT_F32; sc.dec_is_log = 1;
+    sc.d_so = nseg * H * D; sc.d_sh = D; sc.d_sn = H * D;
+    sc.init = s0; sc.i_so = H * DD; sc.i_sh = DD;
+    sc.s_all = f.ws_state; sc.sa_dt = DT_F32; sc.sa_so = sc.kv_so; sc.sa_sh = sc.kv_sh; sc.sa_sn = sc.kv_sn;
+    sc.fin = nullptr; sc.fin_dt = DT_F32;
+    sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = nseg;
+    if (launch_recurrent_scan(sc, hs) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    // chunk starting states, segment end states, segment maps R
+    if (launch_gla_bwd_state(a, pl.f.n_work, io_dtype, hs) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    // the same scan over the segments in reverse order: the gradient reaching each segment's end
+    // (in place of R, starting from dS_final) and dS0
+    ScanParams rv{};
+    rv.kv = a.ws_r + (nseg - 1) * H * DD; rv.kv_dt = DT_F32;
+    rv.kv_so = nseg * H * DD; rv.kv_sh = DD; rv.kv_sn = -H * DD;
+    rv.dec = f.ws_gamma + (nseg - 1) * H * D; rv.dec_dt = DT_F32; rv.dec_is_log = 1;
+    rv.d_so = nseg * H * D; rv.d_sh = D; rv.d_sn = -H * D;
+    rv.init = ds_final; rv.i_so = H * DD; rv.i_sh = DD;
+    rv.s_all = a.ws_r + (nseg - 1) * H * DD; rv.sa_dt = DT_F32; rv.sa_so = rv.kv_so; rv.sa_sh = rv.kv_sh; rv.sa_sn = rv.kv_sn;
+    rv.fin = ds0; rv.fin_dt = DT_F32; rv.f_so = H * DD; rv.f_sh = DD;
+    rv.n_outer = B; rv.H = H; rv.Dk = Dk; rv.Dv = Dv; rv.N = nseg;
+    if (launch_recurrent_scan(rv, hs) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    return launch_status(launch_gla_bwd_chunk(a, pl.f.n_work, io_dtype, hs));
 }
 
 size_t triune_hip_gla_prefill_varlen_workspace_size(int64_t n_seqs, int64_t total_tokens, int64_t H, int Dk,

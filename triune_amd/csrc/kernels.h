@@ -61,6 +61,22 @@ struct ScanParams {
     const int32_t* seg_off; // per outer o: steps N_o = seg_off[o+1]-seg_off[o], first step seg_off[o]
 };
 
+// Gradients of the dense chunked GLA prefill (Dk == Dv == D).  f carries the forward inputs, the
+// segment plan and the forward workspaces (ws_state: carried-in state per segment after the
+// forward scan; ws_gamma: summed log-decay per segment).
+struct BwdParams {
+    PrefillParams f;
+    TokTensor dout;        // upstream gradient of o, in the I/O dtype, [B, T, H, D]
+    void* dq; void* dk; void* dv; void* dg;
+    int64_t dq_sb, dq_st, dq_sh, dk_sb, dk_st, dk_sh, dv_sb, dv_st, dv_sh, dg_sb, dg_st, dg_sh;
+    int d_dt;              // dtype of dq, dk, dv
+    int dg_dt;             // dtype of dg
+    float* ws_chunk;       // [B, H, nchunks, D, D] state at the start of every chunk
+    float* ws_r;           // [n_work, H, D, D] segment maps R, then the gradient reaching each segment's end
+    float* ws_send;        // [n_work, H, D, D] state at each segment's end
+    int64_t nchunks;       // chunks per sequence
+};
+
 // Backward of the exclusive scan (FusedRecurrentScan), all tensors contiguous:
 // d_s_all / s_all / d_kv [o][h][n][Dk][Dv], decay / d_decay [o][h][n][Dk], d_fin / d_init [o][h][Dk][Dv].
 struct ScanBwdParams {
@@ -137,6 +153,9 @@ struct FusedDecodeParams {
 
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);
 hipError_t launch_recurrent_scan_bwd(const ScanBwdParams& a, hipStream_t stream);
+bool gla_bwd_supported(int D, int io_dt);
+hipError_t launch_gla_bwd_state(const BwdParams& a, int64_t n_work, int io_dt, hipStream_t stream);
+hipError_t launch_gla_bwd_chunk(const BwdParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_prep(const PrepParams& a, int HD, int io_dt, int cs_dt, hipStream_t stream);
 hipError_t launch_gla_fused_decode(const FusedDecodeParams& a, int HD, int io_dt, int cs_dt, int s_dt,
                                    hipStream_t stream);

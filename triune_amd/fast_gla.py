@@ -211,6 +211,67 @@ def gla_decode_step(q, k, v, g, state, out=None, *, inplace=False, slots=None, o
     return o, s_out
 
 
+def _needs_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
+def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None):
+    """Gradients (dq, dk, dv, dg, ds0) of _prefill for upstream do (of o) and ds (of the fp32
+    final state), either of which may be None.  grad_dtype: dtype of dq, dk, dv, dg (default:
+    the inputs' own dtypes)."""
+    B, T, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    D = 32 if max(Dk0, Dv0) <= 32 else 64
+    if max(Dk0, Dv0) > 64 or (q.dtype == torch.float32 and D > 32):
+        raise NotImplementedError(
+            f"GLA backward supports head dims <= 64 (<= 32 for float32 inputs); got ({Dk0}, {Dv0}) {q.dtype}")
+    qp, kp, gp = (_vec_layout(_pad_last(x, D)) for x in (q, k, _gate(g, q)))
+    vp = _vec_layout(_pad_last(v, D))
+    if do is None:
+        do = torch.zeros(B, T, H, Dv0, device=q.device, dtype=q.dtype)
+    dop = _vec_layout(_pad_last(do.to(q.dtype), D))
+    dsf = None
+    if ds is not None:
+        dsf = _state_in(ds, D, D)
+    s0p = _state_in(s0, D, D)
+    dq = torch.empty(B, T, H, D, device=q.device, dtype=grad_dtype or q.dtype)
+    dk, dv = torch.empty_like(dq), torch.empty_like(dq)
+    dg = torch.empty(B, T, H, D, device=q.device, dtype=grad_dtype or gp.dtype)
+    ds0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32) if s0 is not None else None
+    L = lib()
+    wsb = L.triune_hip_gla_prefill_bwd_workspace_size(B, max(T, 1), H, D, D, flags)
+    ws = torch.empty(max(int(wsb), 256), device=q.device, dtype=torch.uint8)
+    st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), _tok3(dop), _tok3(dq), _tok3(dk), _tok3(dv), _tok3(dg))
+    rc = L.triune_hip_gla_prefill_bwd(
+        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(dop), st, ptr(s0p), ptr(dsf),
+        ptr(dq), ptr(dk), ptr(dv), dtype_code(dq), ptr(dg), dtype_code(dg), ptr(ds0), B, T, H, D, D, flags, ptr(ws),
+        ws.numel(), stream_of(q),
+    )
+    check(rc, "triune_hip_gla_prefill_bwd")
+    dq, dk, dv, dg = dq[..., :Dk0], dk[..., :Dk0], dv[..., :Dv0], dg[..., :Dk0].to(grad_dtype or g.dtype)
+    if ds0 is not None:
+        ds0 = ds0[..., :Dk0, :Dv0].to(s0.dtype)
+    return dq, dk, dv, dg, ds0
+
+
+class _ChunkGLA(torch.autograd.Function):
+    """fast_chunk_gla with gradients: forward on the prefill kernels (every T, the dispatch
+    flags carried in), backward on triune_hip_gla_prefill_bwd."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, initial_state, flags):
+        o, s = _prefill(q, k, v, g, initial_state, None, flags)
+        ctx.save_for_backward(q, k, v, g, initial_state)
+        ctx.flags = flags
+        return o, s
+
+    @staticmethod
+    def backward(ctx, do, ds):
+        q, k, v, g, s0 = ctx.saved_tensors
+        dq, dk, dv, dg, ds0 = _prefill_bwd(q, k, v, g, s0, do, ds, ctx.flags)
+        return dq, dk, dv, dg, ds0, None
+
+
 def fast_chunk_gla(q, k, v, g, initial_state=None, chunk_size=64, out=None):
     """Chunked GLA forward (reference: fast_chunk_gla, triune/kernels/fast_gla.py:692-778).
 
@@ -219,15 +280,23 @@ def fast_chunk_gla(q, k, v, g, initial_state=None, chunk_size=64, out=None):
     final_state in float32.  g is clamped at 0 for prefill tokens; T == 1 runs the decode step
     (no clamp), and a single-token remainder after whole chunks of `chunk_size` keeps its g
     unclamped, exactly as the reference's dispatch does (fast_gla.py:746-775).  chunk_size only
-    affects that dispatch rule: the kernels always use 64-token chunks internally."""
+    affects that dispatch rule: the kernels always use 64-token chunks internally.
+
+    Differentiable: when any input requires a gradient (and grad mode is on) the call goes
+    through an autograd.Function whose backward runs the HIP gradient kernels (the reference
+    differentiates its PyTorch chunk path, fast_gla.py:720-737); `out` is then not written,
+    as in the reference's training path, which ignores it."""
     _check_io(q, k, v, g)
     B, T, H, _ = q.shape
+    C = int(chunk_size)
+    if _needs_grad(q, k, v, g, initial_state):
+        flags = _lib.FLAG_TAIL_UNCLAMPED if (T == 1 or (C > 0 and T > C and T % C == 1)) else 0
+        return _ChunkGLA.apply(q, k, v, g, initial_state, flags)
     if T == 1:
         st = initial_state
         if st is None:
             st = torch.zeros(B, H, q.shape[-1], v.shape[-1], device=q.device, dtype=torch.float32)
         return gla_decode_step(q, k, v, g, st, out=out)
-    C = int(chunk_size)
     flags = _lib.FLAG_TAIL_UNCLAMPED if (C > 0 and T > C and T % C == 1) else 0
     return _prefill(q, k, v, g, initial_state, out, flags)
 
