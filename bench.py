@@ -252,6 +252,32 @@ def bench_varlen(dev, reps=5):
             "ms": round(ms, 4), "tok_s": round(n_tok / (ms * 1e-3), 1)}
 
 
+def bench_bwd(dev, reps=10):
+    """Chunked GLA backward at the config-1 shape (B=4, T=16384, H=6, D=64): bf16 inputs and
+    upstream gradient of o, fp32 initial state and final-state gradient, bf16 dq/dk/dv/dg and fp32
+    dS0 (the whole launch sequence: segment states, forward scan, chunk states, reverse scan,
+    gradient kernel)."""
+    from triune_amd.fast_gla import _prefill_bwd
+    from triune_amd.workloads import config1
+
+    q, k, v, g, s0 = (x.to(dev) for x in config1(T=16384, B=4, H=6, D=64))
+    gen = torch.Generator().manual_seed(11)
+    do = torch.randn(q.shape, generator=gen).bfloat16().to(dev)
+    ds = torch.randn(s0.shape, generator=gen).to(dev)
+    fn = lambda: _prefill_bwd(q, k, v, g, s0, do, ds, 0)  # noqa: E731
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    B, T, H, D = q.shape
+    alg = 9 * B * T * H * D * 2 + 3 * B * H * D * D * 4  # q,k,v,g,do read; dq,dk,dv,dg written; states
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "GLA prefill backward, config-1 shape (B=4, T=16384, H=6, D=64, bf16, fp32 states)",
+            "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's PyTorch CPU scan, restated (oracle/ref_port.py), on the config-1 workload
     itself (B=4, H=6, T=16384, D=64; bf16 inputs widened to fp32, as the CPU path computes in
@@ -310,7 +336,7 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the config-3 (GDN) and config-4 (varlen) lines")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary workload lines (GDN, varlen, pre-processing, fused decode, backward)")
     ap.add_argument(
         "--copy-probe",
         type=int,
@@ -321,7 +347,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "varlen", "prep", "fused_decode"),
+        choices=("decode", "gdn", "varlen", "prep", "fused_decode", "bwd"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -349,13 +375,13 @@ def main():
         elif args.only == "fused_decode":
             res = bench_fused_decode(args.decode_steps, dev)
         else:
-            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep}[args.only](dev)
+            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     pre = bench_prefill(args.steps, args.warmup, dev)
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
-                                      "fused_decode": bench_fused_decode(args.decode_steps, dev)}
+                                      "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev)}
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,
