@@ -27,6 +27,10 @@
  *   triune_hip_gla_prefill_bwd     <- the gradients of fast_chunk_gla's training path (autograd through
  *                                     _run_gla_chunks, triune/kernels/fast_gla.py:569-689, and
  *                                     FusedRecurrentScan.backward, fast_gla.py:151-203)
+ *   triune_hip_gla_prefill_varlen_pool <- no reference counterpart: the varlen prefill over a
+ *                                     device state pool, the device-side form of the reference's
+ *                                     per-session (state, offset) caches (triune/api/srsm.py:11-112,
+ *                                     triune/model/attention.py:333-358)
  *   triune_hip_recurrent_scan_fwd  <- FusedRecurrentScan.forward, triune/kernels/fast_gla.py:109-149
  *                                     (_recurrent_scan_fwd, fast_gla.py:34-64)
  *   triune_hip_recurrent_scan_bwd  <- FusedRecurrentScan.backward, triune/kernels/fast_gla.py:151-203
@@ -149,6 +153,17 @@ int triune_hip_gla_prefill_bwd(const void* q, const void* k, const void* v, cons
                                void* dq, void* dk, void* dv, int d_dtype, void* dg, int dg_dtype, float* ds0,
                                int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags, void* workspace,
                                size_t workspace_bytes, void* stream);
+
+/* triune_hip_gla_prefill_varlen over a device-resident state pool: sequence i starts from
+ * pool[slots[i]] and its final state is written back to pool[slots[i]] (in place).  pool: fp32
+ * [n_slots, H, Dk, Dv], contiguous, 16-byte aligned; slots: int32 [n_seqs] on the device, distinct;
+ * a slot outside [0, n_slots) starts from zero and is not written.  Same workspace as
+ * triune_hip_gla_prefill_varlen. */
+int triune_hip_gla_prefill_varlen_pool(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                       int g_dtype, const int64_t* strides, const int32_t* cu_seqlens,
+                                       int64_t n_seqs, int64_t total_tokens, const int32_t* slots, float* pool,
+                                       int64_t n_slots, void* o, int o_dtype, int64_t H, int Dk, int Dv, int flags,
+                                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Exclusive affine scan (FusedRecurrentScan forward), all tensors contiguous:
  *     s_all[b,h,n] = s ;  s = decay[b,h,n,:,None] * s + kv[b,h,n]      (s starts at init or 0)

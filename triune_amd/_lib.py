@@ -55,6 +55,11 @@ def _bind(lib):
             _i,
         ),
         "triune_hip_recurrent_scan_fwd": ([_vp, _i, _vp, _i, _vp, _i, _vp, _vp, _i, _i64, _i64, _i64, _i, _i, _vp], _i),
+        "triune_hip_gla_prefill_varlen_pool": (
+            [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _i64, _i64, _vp, _vp, _i64, _vp, _i, _i64, _i, _i, _i, _vp, _sz,
+             _vp],
+            _i,
+        ),
         "triune_hip_gla_prefill_bwd_workspace_size": ([_i64, _i64, _i64, _i, _i, _i], ctypes.c_size_t),
         "triune_hip_gla_prefill_bwd": (
             [_vp, _vp, _vp, _vp, _i, _i, _vp, _i64p, _vp, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp,
@@ -98,6 +103,7 @@ EXPORTS = (
     "triune_hip_gla_prefill_varlen_workspace_size",
     "triune_hip_gla_prefill_varlen",
     "triune_hip_recurrent_scan_fwd",
+    "triune_hip_gla_prefill_varlen_pool",
     "triune_hip_gla_prefill_bwd_workspace_size",
     "triune_hip_gla_prefill_bwd",
     "triune_hip_recurrent_scan_bwd",

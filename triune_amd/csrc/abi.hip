@@ -413,11 +413,12 @@ size_t triune_hip_gla_prefill_varlen_workspace_size(int64_t n_seqs, int64_t tota
     return plan_varlen(n_seqs, total_tokens, H, Dk, Dv, flags).total;
 }
 
-int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, const void* g, int io_dtype,
-                                  int g_dtype, const int64_t* strides, const int32_t* cu_seqlens, int64_t n_seqs,
-                                  int64_t total_tokens, const float* s0, void* o, int o_dtype, float* s_final,
-                                  int64_t H, int Dk, int Dv, int flags, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+// Packed ragged prefill; with `slots`, sequence i's initial and final states are row slots[i] of
+// s0 / s_final (which may be one pool updated in place).
+static int varlen_impl(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                       const int64_t* strides, const int32_t* cu_seqlens, int64_t n_seqs, int64_t total_tokens,
+                       const float* s0, void* o, int o_dtype, float* s_final, const int32_t* slots, int64_t n_slots,
+                       int64_t H, int Dk, int Dv, int flags, void* workspace, size_t workspace_bytes, void* stream) {
     if (!q || !k || !v || !g || !o || !strides || !cu_seqlens) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
     if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
@@ -470,10 +471,31 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
     sc.sa_so = 0; sc.sa_sh = DD; sc.sa_sn = H * DD;
     sc.fin = s_final; sc.fin_dt = DT_F32; sc.f_so = H * DD; sc.f_sh = DD;
     sc.n_outer = n_seqs; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.seg_off = seg_off;
+    sc.slots = slots; sc.n_slots = n_slots;
     e = launch_recurrent_scan(sc, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
     if (pl.n_work > 0) return launch_output_timed(a, pl.n_work, io_dtype, st);
     return TRIUNE_OK;
+}
+
+int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                  int g_dtype, const int64_t* strides, const int32_t* cu_seqlens, int64_t n_seqs,
+                                  int64_t total_tokens, const float* s0, void* o, int o_dtype, float* s_final,
+                                  int64_t H, int Dk, int Dv, int flags, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    return varlen_impl(q, k, v, g, io_dtype, g_dtype, strides, cu_seqlens, n_seqs, total_tokens, s0, o, o_dtype,
+                       s_final, nullptr, 0, H, Dk, Dv, flags, workspace, workspace_bytes, stream);
+}
+
+int triune_hip_gla_prefill_varlen_pool(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                       int g_dtype, const int64_t* strides, const int32_t* cu_seqlens,
+                                       int64_t n_seqs, int64_t total_tokens, const int32_t* slots, float* pool,
+                                       int64_t n_slots, void* o, int o_dtype, int64_t H, int Dk, int Dv, int flags,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+    if (!slots || !pool) return TRIUNE_ERR_NULL;
+    if (n_slots <= 0) return TRIUNE_ERR_SHAPE;
+    return varlen_impl(q, k, v, g, io_dtype, g_dtype, strides, cu_seqlens, n_seqs, total_tokens, pool, o, o_dtype,
+                       pool, slots, n_slots, H, Dk, Dv, flags, workspace, workspace_bytes, stream);
 }
 
 int triune_hip_recurrent_scan_fwd(const void* kv, int kv_dtype, const void* decay, int decay_dtype, const void* init,

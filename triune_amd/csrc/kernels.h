@@ -59,6 +59,11 @@ struct ScanParams {
     int Dk, Dv;
     int64_t N;              // steps when seg_off is null
     const int32_t* seg_off; // per outer o: steps N_o = seg_off[o+1]-seg_off[o], first step seg_off[o]
+    // Optional row indirection of init and fin (prefill carry only): outer o reads its initial
+    // state from row slots[o] of init and writes its final state to row slots[o] of fin; a slot
+    // outside [0, n_slots) starts from zero and is not written.
+    const int32_t* slots;
+    int64_t n_slots;
 };
 
 // Gradients of the dense chunked GLA prefill (Dk == Dv == D).  f carries the forward inputs, the

@@ -107,8 +107,15 @@ __global__ __launch_bounds__(SCAN_TPB) void seg_scan_f32_kernel(ScanParams a) {
         n0 = a.seg_off[o];
         N = (int64_t)a.seg_off[o + 1] - n0;
     }
+    int64_t srow = o;  // row of init / fin
+    bool has_row = true;
+    if (a.slots) {
+        const int32_t sl = a.slots[o];
+        has_row = sl >= 0 && sl < a.n_slots;
+        srow = has_row ? sl : 0;
+    }
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (a.init) s = *reinterpret_cast<const float4*>(a.init + o * a.i_so + h * a.i_sh + e);
+    if (a.init && has_row) s = *reinterpret_cast<const float4*>(a.init + srow * a.i_so + h * a.i_sh + e);
     float* kv = const_cast<float*>(reinterpret_cast<const float*>(a.kv)) + o * a.kv_so + h * a.kv_sh + e;
     const float* dec = reinterpret_cast<const float*>(a.dec) + o * a.d_so + h * a.d_sh + row;
     for (int64_t n = 0; n < N; n += U) {
@@ -132,7 +139,7 @@ __global__ __launch_bounds__(SCAN_TPB) void seg_scan_f32_kernel(ScanParams a) {
             }
         }
     }
-    if (a.fin) *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.fin) + o * a.f_so + h * a.f_sh + e) = s;
+    if (a.fin && has_row) *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.fin) + srow * a.f_so + h * a.f_sh + e) = s;
 }
 
 __device__ __forceinline__ void st1_dt(void* p, int dt, int64_t i, float x) {
@@ -208,6 +215,7 @@ hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream) {
     const bool prefill_carry = a.kv_dt == DT_F32 && a.dec_dt == DT_F32 && a.dec_is_log && a.s_all == a.kv &&
                                a.sa_dt == DT_F32 && a.sa_so == a.kv_so && a.sa_sh == a.kv_sh &&
                                a.sa_sn == a.kv_sn && !a.init_any && (!a.fin || a.fin_dt == DT_F32);
+    if (a.slots && !prefill_carry) return hipErrorInvalidValue;
     if (prefill_carry) hipLaunchKernelGGL(seg_scan_f32_kernel<24>, grid, dim3(SCAN_TPB), 0, stream, a);
     else hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(SCAN_TPB), 0, stream, a);
     return hipGetLastError();

@@ -312,12 +312,19 @@ def _triton_chunk_gla_tc_fwd(q, k, v, g, initial_state=None, out=None, save_fina
     return o, sf
 
 
-def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None):
+def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None, *, state_pool=None, slots=None):
     """Packed ragged GLA prefill (no reference counterpart; equals one fast_chunk_gla call per
     sequence).  q, k, g: [1, N, H, Dk] or [N, H, Dk]; v likewise with Dv; cu_seqlens: int32
     [n + 1] offsets (device or host); initial_state: [n, H, Dk, Dv] or None.
-    Returns (out shaped like v, final_states fp32 [n, H, Dk, Dv]).  g is clamped at 0."""
+    Returns (out shaped like v, final_states fp32 [n, H, Dk, Dv]).  g is clamped at 0.
+
+    With state_pool (fp32 contiguous [n_slots, H, Dk, Dv], (Dk, Dv) a kernel pair: 32x32, 64x64,
+    128x64 or 128x128) and slots (int32 [n], distinct), sequence i starts from state_pool[slots[i]]
+    and its final state is written back there in place; initial_state must then be None and the
+    second item returned is state_pool.  A slot of -1 starts from zero and keeps nothing."""
     _check_io(q, k, v, g)
+    if state_pool is not None:
+        return _varlen_pool(q, k, v, g, cu_seqlens, state_pool, slots, out, initial_state)
     lead1 = q.dim() == 4
     if lead1:
         if q.shape[0] != 1:
@@ -359,6 +366,54 @@ def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None):
     if lead1:
         o = o.unsqueeze(0)
     return o, sf
+
+
+def _varlen_pool(q, k, v, g, cu_seqlens, pool, slots, out, initial_state):
+    if initial_state is not None:
+        raise ValueError("pass either initial_state or state_pool, not both")
+    if slots is None:
+        raise ValueError("state_pool needs slots")
+    _on_device(pool)
+    lead1 = q.dim() == 4
+    if lead1:
+        if q.shape[0] != 1:
+            raise ValueError("packed varlen tensors have batch size 1")
+        q, k, v, g = q[0], k[0], v[0], g[0]
+    N, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    if pool.dtype != torch.float32 or not pool.is_contiguous() or pool.dim() != 4 or tuple(pool.shape[1:]) != (H, Dk0, Dv0):
+        raise ValueError(f"state_pool must be a contiguous float32 [n_slots, {H}, {Dk0}, {Dv0}] tensor")
+    if _pair(Dk0, Dv0) != (Dk0, Dv0):
+        raise ValueError(f"state_pool head dims ({Dk0}, {Dv0}) must be a kernel pair (no padding in place)")
+    cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
+    n = cu.numel() - 1
+    sl = slots.to(device=q.device, dtype=torch.int32).contiguous() if torch.is_tensor(slots) else torch.tensor(
+        list(slots), device=q.device, dtype=torch.int32)
+    if sl.numel() != n:
+        raise ValueError(f"{sl.numel()} slots for {n} sequences")
+    qp, kp, gp = (_vec_layout(x) for x in (q, k, _gate(g, q)))
+    vp = _vec_layout(v)
+    o = None
+    if out is not None:
+        ov = out[0] if out.dim() == 4 else out
+        if tuple(ov.shape) == (N, H, Dv0) and ov.stride(-1) == 1 and _vec_layout(ov) is ov:
+            o = ov
+    if o is None:
+        o = torch.empty(N, H, Dv0, device=q.device, dtype=out.dtype if out is not None else v.dtype)
+    L = lib()
+    wsb = L.triune_hip_gla_prefill_varlen_workspace_size(n, N, H, Dk0, Dv0, 0)
+    ws = torch.empty(max(int(wsb), 256), device=q.device, dtype=torch.uint8)
+    st = strides(qp.stride()[:2], kp.stride()[:2], vp.stride()[:2], gp.stride()[:2], o.stride()[:2])
+    rc = L.triune_hip_gla_prefill_varlen_pool(
+        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, ptr(cu), n, N, ptr(sl), ptr(pool),
+        pool.shape[0], ptr(o), dtype_code(o), H, Dk0, Dv0, 0, ptr(ws), ws.numel(), stream_of(q),
+    )
+    check(rc, "triune_hip_gla_prefill_varlen_pool")
+    if out is not None:
+        if o.data_ptr() != out.data_ptr():
+            out.copy_(o.reshape(out.shape))
+        return out, pool
+    return (o.unsqueeze(0) if lead1 else o), pool
 
 
 # ---------------------------------------------------------------------------------------
