@@ -230,9 +230,15 @@ def bench_gdn(dev, reps=10):
         fn()
     torch.cuda.synchronize()
     ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
-    B, T = q.shape[0], q.shape[1]
+    B, T, H, D = q.shape
+    # the operator's tensors: q, k, v, g (g broadcast to [B, T, H, D] at the reference surface) and
+    # per-head beta read, o written, all bf16; zero initial state, fp32 final state
+    alg = B * T * H * (5 * D * 2 + 2) + B * H * D * D * 4
+    gbs = alg / (ms * 1e-3) / 1e9
     return {"workload": "Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16)",
-            "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1)}
+            "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
 
 def bench_varlen(dev, reps=5):
@@ -247,9 +253,58 @@ def bench_varlen(dev, reps=5):
     fn()
     torch.cuda.synchronize()
     ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
-    n_tok = q.shape[1]
+    n_tok, H, D = q.shape[1], q.shape[2], q.shape[3]
+    from triune_amd.workloads import gla_algorithmic_bytes
+
+    alg = gla_algorithmic_bytes(n_tok * H, D, D, 2, 2, 2) + 2 * s0.numel() * 4
+    gbs = alg / (ms * 1e-3) / 1e9
     return {"workload": f"varlen GLA prefill, config 4 ({cu.numel() - 1} sequences, {n_tok} tokens, H=12, D=128, bf16)",
-            "ms": round(ms, 4), "tok_s": round(n_tok / (ms * 1e-3), 1)}
+            "ms": round(ms, 4), "tok_s": round(n_tok / (ms * 1e-3), 1), "alg_bytes": alg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
+def bench_scan(dev, reps=10):
+    """FusedRecurrentScan forward and backward at the chunk-state shape of config 1 (B=4, H=6,
+    N=256 chunks, Dk=Dv=64, fp32 kv and upstream gradients, as in the reference's own check)."""
+    from triune_amd import FusedRecurrentScan
+    from triune_amd._lib import dtype_code, lib, ptr, stream_of
+
+    B, H, N, D = 4, 6, 256, 64
+    gen = torch.Generator().manual_seed(13)
+    kv = torch.randn(B, H, N, D, D, generator=gen).to(dev)
+    dec = torch.rand(B, H, N, D, 1, generator=gen).to(dev)
+    init = torch.randn(B, H, D, D, generator=gen).to(dev)
+    with torch.no_grad():
+        fwd = lambda: FusedRecurrentScan.apply(kv, dec, init)  # noqa: E731
+        fwd()
+        torch.cuda.synchronize()
+        ms_f = _events_time_ms(fwd, reps, torch.cuda.current_stream())
+        s_all, _ = fwd()
+    d_s = torch.randn(B, H, N, D, D, generator=gen).to(dev)
+    d_f = torch.randn(B, H, D, D, generator=gen).to(dev)
+    dec4 = dec[..., 0].contiguous()
+    d_kv, d_init = torch.empty_like(kv), torch.empty_like(init)
+    d_dec = torch.empty(B, H, N, D, device=dev)
+
+    def bwd():
+        lib().triune_hip_recurrent_scan_bwd(ptr(d_s), dtype_code(d_s), ptr(d_f), dtype_code(d_f), ptr(dec4),
+                                            dtype_code(dec4), ptr(s_all), ptr(d_kv), ptr(d_dec), ptr(d_init),
+                                            dtype_code(d_kv), B, H, N, D, D, stream_of(kv))
+
+    bwd()
+    torch.cuda.synchronize()
+    ms_b = _events_time_ms(bwd, reps, torch.cuda.current_stream())
+    big, small = kv.numel() * 4, dec4.numel() * 4
+    alg_f = 2 * big + small + 2 * init.numel() * 4  # kv read, s_all written, decay, init and final
+    alg_b = 3 * big + 2 * small + 2 * init.numel() * 4  # d_s_all, s_all read, d_kv written; decay, d_decay
+    out = {"workload": f"FusedRecurrentScan, B={B}, H={H}, N={N}, Dk=Dv={D}, fp32"}
+    for name, ms, alg in (("forward", ms_f, alg_f), ("backward", ms_b, alg_b)):
+        gbs = alg / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 2), "alg_bytes": alg,
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    return out
 
 
 def bench_bwd(dev, reps=10):
@@ -347,7 +402,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "varlen", "prep", "fused_decode", "bwd"),
+        choices=("decode", "gdn", "varlen", "prep", "fused_decode", "bwd", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -375,13 +430,15 @@ def main():
         elif args.only == "fused_decode":
             res = bench_fused_decode(args.decode_steps, dev)
         else:
-            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd}[args.only](dev)
+            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd,
+                   "scan": bench_scan}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     pre = bench_prefill(args.steps, args.warmup, dev)
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
-                                      "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev)}
+                                      "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
+                                      "scan": bench_scan(dev)}
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,

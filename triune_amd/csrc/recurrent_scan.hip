@@ -6,6 +6,8 @@
 // FusedRecurrentScan (triune/kernels/fast_gla.py:34-64 kernel, :109-149 wrapper), and the
 // prefill's inter-segment carry (decay given as a log, kv = segment-local states, s_all
 // written in place of kv).  Arithmetic in fp32; kv / s_all / fin may be fp32, bf16 or fp16.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace triune {
@@ -36,10 +38,37 @@ __device__ __forceinline__ void st4_dt(void* p, int dt, int64_t i, const float (
     else store4_dt(reinterpret_cast<_Float16*>(p) + i, dt, x[0], x[1], x[2], x[3]);
 }
 
+template <typename T>
+__device__ __forceinline__ void ld4_t(const void* p, int64_t i, float (&x)[4]) {
+    const T* q = reinterpret_cast<const T*>(p) + i;
+    if constexpr (std::is_same<T, float>::value) {
+        const float4 a = *reinterpret_cast<const float4*>(q);
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    } else {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        const t4 a = *reinterpret_cast<const t4*>(q);
+        x[0] = (float)a[0]; x[1] = (float)a[1]; x[2] = (float)a[2]; x[3] = (float)a[3];
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void st4_t(void* p, int64_t i, const float (&x)[4]) {
+    T* q = reinterpret_cast<T*>(p) + i;
+    if constexpr (std::is_same<T, float>::value) {
+        *reinterpret_cast<float4*>(q) = make_float4(x[0], x[1], x[2], x[3]);
+    } else {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<t4*>(q) = t4{(T)x[0], (T)x[1], (T)x[2], (T)x[3]};
+    }
+}
+
 // grid: (ceil(Dk*Dv/4 / SCAN_TPB), H, n_outer), block SCAN_TPB; each thread owns 4 consecutive
-// elements.  Small blocks spread the (outer, head) rows over many CUs; the loop issues the
-// loads of U steps before the dependent chain consumes them.
+// elements.  Small blocks spread the (outer, head) rows over many CUs.  The grid holds only
+// B*H*Dk*Dv/256 waves (384 at the config-1 chunk-state shape), so each thread keeps the loads
+// of SCAN_U steps in flight (32 steps x 16 bytes per lane) before the dependent chain consumes
+// them; the steps' stores go out before the next batch's loads.
 constexpr int SCAN_TPB = 64;
+constexpr int SCAN_U = 32;
 __global__ __launch_bounds__(SCAN_TPB) void recurrent_scan_kernel(ScanParams a) {
     const int64_t DD = (int64_t)a.Dk * a.Dv;
     const int64_t e = ((int64_t)blockIdx.x * SCAN_TPB + threadIdx.x) * 4;
@@ -62,33 +91,66 @@ __global__ __launch_bounds__(SCAN_TPB) void recurrent_scan_kernel(ScanParams a) 
     const int64_t kv_base = o * a.kv_so + h * a.kv_sh + e;
     const int64_t sa_base = o * a.sa_so + h * a.sa_sh + e;
     const int64_t d_base = o * a.d_so + h * a.d_sh + row;
-    constexpr int U = 8;
-    int64_t n = 0;
-    for (; n + U <= N; n += U) {
+    constexpr int U = SCAN_U;
+    for (int64_t n = 0; n < N; n += U) {  // a partial last batch re-reads its last step (not used)
         float x[U][4], d[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            ld4_dt(a.kv, a.kv_dt, kv_base + (n0 + n + u) * a.kv_sn, x[u]);
-            d[u] = ld_dt(a.dec, a.dec_dt, d_base + (n0 + n + u) * a.d_sn);
+            const int64_t i = n0 + (n + u < N ? n + u : N - 1);
+            ld4_dt(a.kv, a.kv_dt, kv_base + i * a.kv_sn, x[u]);
+            d[u] = ld_dt(a.dec, a.dec_dt, d_base + i * a.d_sn);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float dd = a.dec_is_log ? expf(d[u]) : d[u];
+            if (n + u >= N) break;  // uniform
+            const float dd = a.dec_is_log ? expf(d[u]) : d[u];
             if (a.s_all) st4_dt(a.s_all, a.sa_dt, sa_base + (n0 + n + u) * a.sa_sn, s);
 #pragma unroll
             for (int c = 0; c < 4; ++c) s[c] = s[c] * dd + x[u][c];
         }
     }
-    for (; n < N; ++n) {
-        float x[4];
-        ld4_dt(a.kv, a.kv_dt, kv_base + (n0 + n) * a.kv_sn, x);
-        float dd = ld_dt(a.dec, a.dec_dt, d_base + (n0 + n) * a.d_sn);
-        if (a.dec_is_log) dd = expf(dd);
-        if (a.s_all) st4_dt(a.s_all, a.sa_dt, sa_base + (n0 + n) * a.sa_sn, s);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) s[c] = s[c] * dd + x[c];
-    }
     if (a.fin) st4_dt(a.fin, a.fin_dt, o * a.f_so + h * a.f_sh + e, s);
+}
+
+// The same scan with the dtypes fixed at compile time (kv in KT, s_all / fin in OT, decay factors
+// in fp32), so every load of a batch is one unconditional vector access and the compiler's waits
+// track them exactly.
+template <typename KT, typename OT>
+__global__ __launch_bounds__(SCAN_TPB) void recurrent_scan_typed_kernel(ScanParams a) {
+    const int64_t DD = (int64_t)a.Dk * a.Dv;
+    const int64_t e = ((int64_t)blockIdx.x * SCAN_TPB + threadIdx.x) * 4;
+    if (e >= DD) return;
+    const int64_t h = blockIdx.y, o = blockIdx.z;
+    const int row = (int)(e / a.Dv);
+    const int64_t N = a.N;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.init) {
+        const float4 v = *reinterpret_cast<const float4*>(a.init + o * a.i_so + h * a.i_sh + e);
+        s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
+    } else if (a.init_any) {
+        ld4_dt(a.init_any, a.init_dt, o * a.i_so + h * a.i_sh + e, s);
+    }
+    const int64_t kv_base = o * a.kv_so + h * a.kv_sh + e;
+    const int64_t sa_base = o * a.sa_so + h * a.sa_sh + e;
+    const float* dec = reinterpret_cast<const float*>(a.dec) + o * a.d_so + h * a.d_sh + row;
+    constexpr int U = SCAN_U;
+    for (int64_t n = 0; n < N; n += U) {
+        float x[U][4], d[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = n + u < N ? n + u : N - 1;
+            ld4_t<KT>(a.kv, kv_base + i * a.kv_sn, x[u]);
+            d[u] = dec[i * a.d_sn];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (n + u >= N) break;  // uniform
+            st4_t<OT>(a.s_all, sa_base + (n + u) * a.sa_sn, s);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s[c] = s[c] * d[u] + x[u][c];
+        }
+    }
+    st4_t<OT>(a.fin, o * a.f_so + h * a.f_sh + e, s);
 }
 
 // The prefill's carry over segments: fp32 kv and s_all (the same buffer), fp32 log-decay, fp32
@@ -166,7 +228,7 @@ __global__ __launch_bounds__(64) void recurrent_scan_bwd_kernel(ScanBwdParams a,
     const int64_t r = act ? row : 0;
     float d[4] = {0.f, 0.f, 0.f, 0.f};
     if (a.d_fin && act) ld4_dt(a.d_fin, a.df_dt, bh * DD + e, d);
-    constexpr int U = 4;
+    constexpr int U = SCAN_U;
     for (int64_t nn = N; nn > 0; nn -= U) {
         float ds[U][4], sp[U][4], dc[U];
 #pragma unroll
@@ -199,13 +261,65 @@ __global__ __launch_bounds__(64) void recurrent_scan_bwd_kernel(ScanBwdParams a,
     if (act) st4_dt(a.d_init, a.out_dt, bh * DD + e, d);
 }
 
+// The backward with the dtypes fixed at compile time: upstream gradient of s_all and every output
+// in GT, decay factors in fp32 (same work split as recurrent_scan_bwd_kernel).
+template <typename GT>
+__global__ __launch_bounds__(64) void recurrent_scan_bwd_typed_kernel(ScanBwdParams a, int lpr) {
+    const int lane = threadIdx.x;
+    const int row = blockIdx.x * (64 / lpr) + lane / lpr;
+    const int j0 = (lane % lpr) * 4;
+    const bool act = row < a.Dk && j0 < a.Dv;
+    const int64_t DD = (int64_t)a.Dk * a.Dv, N = a.N;
+    const int64_t bh = (int64_t)blockIdx.z * a.H + blockIdx.y;
+    const int64_t e = act ? (int64_t)row * a.Dv + j0 : 0;
+    const int64_t r = act ? row : 0;
+    const float* dec = reinterpret_cast<const float*>(a.dec);
+    float d[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.d_fin && act) ld4_dt(a.d_fin, a.df_dt, bh * DD + e, d);
+    constexpr int U = SCAN_U;
+    for (int64_t nn = N; nn > 0; nn -= U) {
+        float ds[U][4], sp[U][4], dc[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t n = nn - 1 - u >= 0 ? nn - 1 - u : 0;
+            const int64_t i5 = (bh * N + n) * DD + e;
+            if (a.d_s_all) {
+                ld4_t<GT>(a.d_s_all, i5, ds[u]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) ds[u][c] = 0.f;
+            }
+            const float4 s4 = *reinterpret_cast<const float4*>(a.s_all + i5);
+            sp[u][0] = s4.x; sp[u][1] = s4.y; sp[u][2] = s4.z; sp[u][3] = s4.w;
+            dc[u] = dec[(bh * N + n) * a.Dk + r];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t n = nn - 1 - u;
+            if (n < 0) break;  // uniform
+            const int64_t i5 = (bh * N + n) * DD + e;
+            if (act) st4_t<GT>(a.d_kv, i5, d);
+            float part = act ? d[0] * sp[u][0] + d[1] * sp[u][1] + d[2] * sp[u][2] + d[3] * sp[u][3] : 0.f;
+            for (int off = lpr >> 1; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+            if (act && j0 == 0) reinterpret_cast<GT*>(a.d_dec)[(bh * N + n) * a.Dk + row] = (GT)part;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) d[c] = ds[u][c] + dc[u] * d[c];
+        }
+    }
+    if (act) st4_t<GT>(a.d_init, bh * DD + e, d);
+}
+
 hipError_t launch_recurrent_scan_bwd(const ScanBwdParams& a, hipStream_t stream) {
     int lpr = 1;
     while (lpr * 4 < a.Dv) lpr <<= 1;
     if (lpr > 64) return hipErrorInvalidValue;
     const int rpb = 64 / lpr;
     dim3 grid((unsigned)((a.Dk + rpb - 1) / rpb), (unsigned)a.H, (unsigned)a.n_outer);
-    hipLaunchKernelGGL(recurrent_scan_bwd_kernel, grid, dim3(64), 0, stream, a, lpr);
+    const bool typed = a.dec_dt == DT_F32 && (!a.d_s_all || a.dsa_dt == a.out_dt);
+    if (typed && a.out_dt == DT_F32) hipLaunchKernelGGL(recurrent_scan_bwd_typed_kernel<float>, grid, dim3(64), 0, stream, a, lpr);
+    else if (typed && a.out_dt == DT_BF16) hipLaunchKernelGGL(recurrent_scan_bwd_typed_kernel<__bf16>, grid, dim3(64), 0, stream, a, lpr);
+    else if (typed && a.out_dt == DT_F16) hipLaunchKernelGGL(recurrent_scan_bwd_typed_kernel<_Float16>, grid, dim3(64), 0, stream, a, lpr);
+    else hipLaunchKernelGGL(recurrent_scan_bwd_kernel, grid, dim3(64), 0, stream, a, lpr);
     return hipGetLastError();
 }
 
@@ -216,8 +330,23 @@ hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream) {
                                a.sa_dt == DT_F32 && a.sa_so == a.kv_so && a.sa_sh == a.kv_sh &&
                                a.sa_sn == a.kv_sn && !a.init_any && (!a.fin || a.fin_dt == DT_F32);
     if (a.slots && !prefill_carry) return hipErrorInvalidValue;
-    if (prefill_carry) hipLaunchKernelGGL(seg_scan_f32_kernel<24>, grid, dim3(SCAN_TPB), 0, stream, a);
-    else hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(SCAN_TPB), 0, stream, a);
+    if (prefill_carry) {
+        hipLaunchKernelGGL(seg_scan_f32_kernel<24>, grid, dim3(SCAN_TPB), 0, stream, a);
+        return hipGetLastError();
+    }
+    // dense steps, fp32 decay factors, s_all and fin both present in one dtype that is kv's or fp32
+    const bool typed = !a.seg_off && a.dec_dt == DT_F32 && !a.dec_is_log && a.s_all && a.fin &&
+                       a.sa_dt == a.fin_dt && (a.sa_dt == a.kv_dt || a.sa_dt == DT_F32);
+    if (typed) {
+        const int k = a.kv_dt, t = a.sa_dt;
+        if (k == DT_F32) hipLaunchKernelGGL((recurrent_scan_typed_kernel<float, float>), grid, dim3(SCAN_TPB), 0, stream, a);
+        else if (k == DT_BF16 && t == DT_BF16) hipLaunchKernelGGL((recurrent_scan_typed_kernel<__bf16, __bf16>), grid, dim3(SCAN_TPB), 0, stream, a);
+        else if (k == DT_BF16) hipLaunchKernelGGL((recurrent_scan_typed_kernel<__bf16, float>), grid, dim3(SCAN_TPB), 0, stream, a);
+        else if (t == DT_F16) hipLaunchKernelGGL((recurrent_scan_typed_kernel<_Float16, _Float16>), grid, dim3(SCAN_TPB), 0, stream, a);
+        else hipLaunchKernelGGL((recurrent_scan_typed_kernel<_Float16, float>), grid, dim3(SCAN_TPB), 0, stream, a);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(recurrent_scan_kernel, grid, dim3(SCAN_TPB), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -436,7 +436,7 @@ class FusedRecurrentScan(torch.autograd.Function):
         _on_device(kv, decay_k, init_state)
         B, H, N, Dk, Dv = kv.shape
         kvc = kv.contiguous()
-        dec = decay_k.expand(B, H, N, Dk, 1)[..., 0].contiguous()
+        dec = decay_k.expand(B, H, N, Dk, 1)[..., 0].to(torch.float32).contiguous()  # [B,H,N,Dk]: small
         init = init_state.expand(B, H, Dk, Dv).contiguous()
         if Dv % 4 != 0:
             raise ValueError("FusedRecurrentScan needs Dv % 4 == 0")
