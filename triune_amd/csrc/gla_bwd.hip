@@ -431,6 +431,18 @@ struct BwdStep {
         float* sFK = reinterpret_cast<float*>(smem + L::OFF_FK);
         const bool tail_chunk = (a.f.flags & 1) && (tc + nv == wk.len);
 
+        // Rows i = c0 + r16 of the chunk's starting state (stage 3's dq term), loaded now so that
+        // stages 1 and 2 cover their latency.
+        f32x4 sprev[NKS][2];
+        {
+            const float* sp = a.ws_chunk + ((wk.b * a.f.H + h) * a.nchunks + tc / CHUNK) * (int64_t)D * D +
+                              (int64_t)(c0 + r16) * D;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                sprev[ks][0] = *reinterpret_cast<const f32x4*>(sp + 32 * ks + 4 * g4);
+                sprev[ks][1] = *reinterpret_cast<const f32x4*>(sp + 32 * ks + 16 + 4 * g4);
+            }
+        }
         // ---------------- stage 1: factors, split operands -> LDS ---------------------------
         float qx[4][DL], kx[4][DL], fq[4][DL];
         uint32_t pass = 0;  // bit 4*j + i: token 4*tg + j, dim dl0 + i passes its gate gradient
@@ -510,13 +522,10 @@ struct BwdStep {
             const bf16x8 z8 = {};
             // dQ^T[i][t] += (e^m S)[i][.] dO[t][.]: rows i = c0 + r16 of the chunk's starting state
             {
-                const float* sp = a.ws_chunk + ((wk.b * a.f.H + h) * a.nchunks + tc / CHUNK) * (int64_t)D * D +
-                                  (int64_t)(c0 + r16) * D;
                 const float emi = sEM[c0 + r16];
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    const f32x4 lo = *reinterpret_cast<const f32x4*>(sp + 32 * ks + 4 * g4);
-                    const f32x4 hi = *reinterpret_cast<const f32x4*>(sp + 32 * ks + 16 + 4 * g4);
+                    const f32x4 lo = sprev[ks][0], hi = sprev[ks][1];
                     const float x[8] = {lo[0] * emi, lo[1] * emi, lo[2] * emi, lo[3] * emi,
                                         hi[0] * emi, hi[1] * emi, hi[2] * emi, hi[3] * emi};
                     const Split8<NS> sf = split8<NS>(x);
