@@ -446,6 +446,12 @@ __device__ __forceinline__ void out_store4(const OutRsrc& r, int voff, int dt, c
     __builtin_amdgcn_raw_buffer_store_b64(w1, r.hi, voff + 8, 0, 0);
 }
 
+// s_waitcnt vmcnt(0) (the LDS and export counters are left free): every vector memory access of
+// this wave has completed.  On gfx9 one counter tracks loads and stores, so a later wait for a
+// load issued before a burst of stores also waits for those stores; draining the (long since
+// returned) prefetch loads right before the burst lets that later wait be skipped.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // Wave index within the workgroup as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 

@@ -623,6 +623,7 @@ struct BwdStep {
             bwd_tokenwise<TIn, TG, D>(a, wk, h, tc, nv, dH, sFQ, sFK, L::FS);
         }
         __syncthreads();  // stage 3 is done with every plane
+        wait_vmem();      // the previous chunk's inputs are in: this chunk's stores do not delay them
         if (fast) {
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
