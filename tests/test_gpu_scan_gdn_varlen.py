@@ -197,3 +197,16 @@ def test_varlen_equals_dense_batch(dev):
     torch.cuda.synchronize()
     assert float((ov.reshape(3, 333, 2, 64) - od).abs().max()) <= 1e-4
     assert float((sv - sd).abs().max()) <= 1e-4
+
+
+def test_gdn_refuses_gradients(dev):
+    """The GDN kernels are forward-only: a call that needs gradients raises instead of returning
+    outputs that silently carry none (the reference differentiates its PyTorch recurrence there)."""
+    q = torch.randn(1, 70, 2, 64, device=dev, requires_grad=True)
+    k, v = torch.randn(1, 70, 2, 64, device=dev), torch.randn(1, 70, 2, 64, device=dev)
+    g = -0.1 * torch.rand(1, 70, 2, 64, device=dev)
+    with pytest.raises(NotImplementedError):
+        fast_chunk_gated_deltanet(q, k, v, g)
+    with torch.no_grad():
+        o, s = fast_chunk_gated_deltanet(q, k, v, g)
+    assert o.shape == (1, 70, 2, 64) and not o.requires_grad

@@ -483,6 +483,12 @@ class FusedRecurrentScan(torch.autograd.Function):
 
 def _gdn(q, k, v, g, beta, initial_state, beta_kind):
     _check_io(q, k, v, g)
+    if _needs_grad(q, k, v, g, beta, initial_state):
+        # The reference differentiates its PyTorch recurrence here (fast_gla.py:885-904); these
+        # HIP kernels are forward-only, so refuse rather than return outputs without gradients.
+        raise NotImplementedError(
+            "Gated DeltaNet has no backward on this path; call it under torch.no_grad() or with inputs "
+            "that do not require gradients")
     _on_device(beta, initial_state)
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
