@@ -205,62 +205,99 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
         const TIO* kr = base + a.x_sp;
         const TIO* vr = base + 2 * a.x_sp;
         const TIO* gr = base + 3 * a.x_sp;
-        // All of the row's small loads are issued together (no branch between them): the norm
-        // elements (one per lane), this thread's key rows of q, k, g and their RoPE partner rows,
-        // cos/sin (buffer loads over a table of HD entries, or of none when RoPE is off: then they
-        // read zeros and never touch memory, as cos and sin may be null), the 4 value columns.
-        float qa[EPL], ka[EPL];
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const int d = (lane + 64 * e) % HD;  // HD = 32: lanes 32..63 repeat 0..31 (counted once below)
-            qa[e] = (float)qr[d];
-            ka[e] = (float)kr[d];
-        }
-        constexpr int PH = HD / 2;
-        const int rp = r0 < PH ? r0 + PH : r0 - PH;  // partner rows rp .. rp+RPT-1
-        float qo[RPT], qp[RPT], ko[RPT], kp[RPT], gg[RPT], cs[RPT], sn[RPT], vv[4];
+        float qv[RPT], kv[RPT], dv[RPT], gg[RPT], vv[4];
         auto ld4 = [](const auto* p, float* x) {
             using T = std::remove_const_t<std::remove_pointer_t<decltype(p)>>;
             const V4<T> v = *reinterpret_cast<const V4<T>*>(p);
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] = (float)v[i];
         };
-#pragma unroll
-        for (int m = 0; m < RPT; m += 4) {
-            ld4(qr + r0 + m, qo + m);
-            ld4(qr + rp + m, qp + m);
-            ld4(kr + r0 + m, ko + m);
-            ld4(kr + rp + m, kp + m);
-            ld4(gr + r0 + m, gg + m);
-            ld_table4(rcos, (r0 + m) * (int)sizeof(TCS), cs + m);
-            ld_table4(rsin, (r0 + m) * (int)sizeof(TCS), sn + m);
-        }
-        ld4(vr + 4 * cg, vv);
-        float sq = 0.f, sk = 0.f;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const bool first = lane + 64 * e < HD;
-            const float q1 = elu1(qa[e]), k1 = elu1(ka[e]);
-            sq += first ? q1 * q1 : 0.f;
-            sk += first ? k1 * k1 : 0.f;
-        }
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            sq += __shfl_xor(sq, m);
-            sk += __shfl_xor(sk, m);
-        }
-        const float iq = inv_norm(sq), ik = inv_norm(sk);
-        const float sgn = r0 < PH ? -1.f : 1.f;
+        constexpr int PH = HD / 2;
         const float rope = a.use_rope ? 1.f : 0.f;
-        float qv[RPT], kv[RPT], dv[RPT];
+        if constexpr (EPL == 1) {
+            // HD <= 64: lane d (mod HD) finishes element d of q and k once (ELU+1, norm, RoPE with
+            // the partner element d +- HD/2 from lane d ^ HD/2), then every thread gathers its key
+            // rows from those lanes.  All of the row's small loads are issued together: element d
+            // of q, k, cos, sin (buffer loads over a table of HD entries, or of none when RoPE is
+            // off: they then read zeros and never touch memory, as cos and sin may be null), this
+            // thread's key rows of g and its 4 value columns.
+            const int d = lane % HD;  // HD = 32: lanes 32..63 repeat 0..31 (counted once below)
+            const float qe = (float)qr[d], ke = (float)kr[d];
+            float ce, se;
+            if constexpr (sizeof(TCS) == 4) {
+                ce = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcos, d * 4, 0, 0));
+                se = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsin, d * 4, 0, 0));
+            } else {
+                ce = (float)__builtin_bit_cast(TCS, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rcos, d * 2, 0, 0));
+                se = (float)__builtin_bit_cast(TCS, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rsin, d * 2, 0, 0));
+            }
 #pragma unroll
-        for (int m = 0; m < RPT; ++m) {
-            const float qn = elu1(qo[m]) * iq, kn = elu1(ko[m]) * ik;
-            const float qn2 = elu1(qp[m]) * iq, kn2 = elu1(kp[m]) * ik;
-            const float c = rope * cs[m] + (1.f - rope), sg = rope * sgn * sn[m];
-            qv[m] = qn * c + sg * qn2;
-            kv[m] = kn * c + sg * kn2;
-            dv[m] = sigmoid(gg[m]);
+            for (int m = 0; m < RPT; m += 4) ld4(gr + r0 + m, gg + m);
+            ld4(vr + 4 * cg, vv);
+            const bool first = lane < HD;
+            const float q1 = elu1(qe), k1 = elu1(ke);
+            float sq = first ? q1 * q1 : 0.f, sk = first ? k1 * k1 : 0.f;
+#pragma unroll
+            for (int m = 1; m < 64; m <<= 1) {
+                sq += __shfl_xor(sq, m);
+                sk += __shfl_xor(sk, m);
+            }
+            const float qn = q1 * inv_norm(sq), kn = k1 * inv_norm(sk);
+            const float qo = __shfl_xor(qn, PH), ko = __shfl_xor(kn, PH);
+            const float c = rope * ce + (1.f - rope), sg = rope * (d < PH ? -se : se);
+            const float qr_d = qn * c + sg * qo, kr_d = kn * c + sg * ko;
+#pragma unroll
+            for (int m = 0; m < RPT; ++m) {
+                qv[m] = lane_bcast(qr_d, r0 + m);
+                kv[m] = lane_bcast(kr_d, r0 + m);
+                dv[m] = sigmoid(gg[m]);
+            }
+        } else {
+            // HD = 128 (two elements per lane): each thread forms its key rows and their RoPE
+            // partner rows itself; the norm elements, rows, partners, cos/sin and value columns are
+            // loaded together.
+            float qa[EPL], ka[EPL];
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                qa[e] = (float)qr[lane + 64 * e];
+                ka[e] = (float)kr[lane + 64 * e];
+            }
+            const int rp = r0 < PH ? r0 + PH : r0 - PH;  // partner rows rp .. rp+RPT-1
+            float qo[RPT], qp[RPT], ko[RPT], kp[RPT], cs[RPT], sn[RPT];
+#pragma unroll
+            for (int m = 0; m < RPT; m += 4) {
+                ld4(qr + r0 + m, qo + m);
+                ld4(qr + rp + m, qp + m);
+                ld4(kr + r0 + m, ko + m);
+                ld4(kr + rp + m, kp + m);
+                ld4(gr + r0 + m, gg + m);
+                ld_table4(rcos, (r0 + m) * (int)sizeof(TCS), cs + m);
+                ld_table4(rsin, (r0 + m) * (int)sizeof(TCS), sn + m);
+            }
+            ld4(vr + 4 * cg, vv);
+            float sq = 0.f, sk = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float q1 = elu1(qa[e]), k1 = elu1(ka[e]);
+                sq += q1 * q1;
+                sk += k1 * k1;
+            }
+#pragma unroll
+            for (int m = 1; m < 64; m <<= 1) {
+                sq += __shfl_xor(sq, m);
+                sk += __shfl_xor(sk, m);
+            }
+            const float iq = inv_norm(sq), ik = inv_norm(sk);
+            const float sgn = r0 < PH ? -1.f : 1.f;
+#pragma unroll
+            for (int m = 0; m < RPT; ++m) {
+                const float qn = elu1(qo[m]) * iq, kn = elu1(ko[m]) * ik;
+                const float qn2 = elu1(qp[m]) * iq, kn2 = elu1(kp[m]) * ik;
+                const float c = rope * cs[m] + (1.f - rope), sg = rope * sgn * sn[m];
+                qv[m] = qn * c + sg * qn2;
+                kv[m] = kn * c + sg * kn2;
+                dv[m] = sigmoid(gg[m]);
+            }
         }
 
         f32x4 y[RPT];
