@@ -64,6 +64,15 @@ __device__ __forceinline__ float sigmoid(float x) {
 
 __device__ __forceinline__ float inv_norm(float sumsq) { return 1.f / sqrtf(fmaxf(sumsq, 1e-12f)); }
 
+// Sum over the 64 lanes of a wave, in every lane: DPP inclusive scans of the four 16-lane rows,
+// then the rows' last lanes read into scalars (no LDS-routed shuffle on the path).
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row_inclusive_scan(x);
+    const int v = __float_as_int(x);
+    return (__int_as_float(__builtin_amdgcn_readlane(v, 15)) + __int_as_float(__builtin_amdgcn_readlane(v, 31))) +
+           (__int_as_float(__builtin_amdgcn_readlane(v, 47)) + __int_as_float(__builtin_amdgcn_readlane(v, 63)));
+}
+
 // ---------------------------------------------------------------------------------------
 // In-place pre-processing of qkv [B, T, 3, H, HD] (q, k; v untouched) and g [B, T, H, HD].
 // ---------------------------------------------------------------------------------------
@@ -236,12 +245,7 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
             ld4(vr + 4 * cg, vv);
             const bool first = lane < HD;
             const float q1 = elu1(qe), k1 = elu1(ke);
-            float sq = first ? q1 * q1 : 0.f, sk = first ? k1 * k1 : 0.f;
-#pragma unroll
-            for (int m = 1; m < 64; m <<= 1) {
-                sq += __shfl_xor(sq, m);
-                sk += __shfl_xor(sk, m);
-            }
+            const float sq = wave_sum(first ? q1 * q1 : 0.f), sk = wave_sum(first ? k1 * k1 : 0.f);
             const float qn = q1 * inv_norm(sq), kn = k1 * inv_norm(sk);
             const float qo = __shfl_xor(qn, PH), ko = __shfl_xor(kn, PH);
             const float c = rope * ce + (1.f - rope), sg = rope * (d < PH ? -se : se);
@@ -282,11 +286,8 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
                 sq += q1 * q1;
                 sk += k1 * k1;
             }
-#pragma unroll
-            for (int m = 1; m < 64; m <<= 1) {
-                sq += __shfl_xor(sq, m);
-                sk += __shfl_xor(sk, m);
-            }
+            sq = wave_sum(sq);
+            sk = wave_sum(sk);
             const float iq = inv_norm(sq), ik = inv_norm(sk);
             const float sgn = r0 < PH ? -1.f : 1.f;
 #pragma unroll
