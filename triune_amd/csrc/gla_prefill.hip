@@ -222,7 +222,10 @@ struct OutStep {
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
-        after_inputs();
+        // The next chunk's loads go out now and fly during stages 2-3, except at (128, 128),
+        // where their registers would push the wave past 256 VGPRs: there they go out after stage 3.
+        constexpr bool late_refill = DK == 128 && DV == 128;
+        if constexpr (!late_refill) after_inputs();
         // The previous chunk's outputs, staged through this wave's slice of the A^T planes
         // (nothing reads them again before this chunk's stage 2).
         if (pend.valid) flush_out(a, wk, h, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
@@ -341,6 +344,7 @@ struct OutStep {
                 pend.valid = false;
             }
         }
+        if constexpr (late_refill) after_inputs();
         __syncthreads();  // the next chunk rewrites LDS
     }
 };
