@@ -172,3 +172,50 @@ def test_backward_matches_finite_difference_of_forward_kernel(dev):
     ((o * do.to(dev)).sum() + (s * ds.to(dev)).sum()).backward()
     an = sum(float((x.grad.double() * d).sum()) for x, d in zip(xs, dirs))
     assert abs(fd - an) <= 2e-3 * max(1.0, abs(an)), (fd, an)
+
+
+@pytest.mark.parametrize("T", [63, 64, 65, 256])
+@pytest.mark.parametrize("with_init", [False, True])
+def test_chunk_boundary_lengths_fp32(dev, T, with_init):
+    """The lengths of the reference's fallback gradient check (test_attention_fallback.py:42-85:
+    T in {1, 63, 64, 65, 128, 256}, outputs, states and every gradient) at chunk_size 64, where
+    T = 65 ends in the unclamped one-token tail."""
+    gen = torch.Generator().manual_seed(T + 7 * with_init)
+    B, H, D = 2, 3, 32
+    q, k, v = (torch.randn(B, T, H, D, generator=gen) for _ in range(3))
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, D, generator=gen)) / 4
+    s0 = torch.randn(B, H, D, D, generator=gen) if with_init else None
+    do, ds = _upstream(B, T, H, D, D, T + 1)
+    xs = [x.to(dev).requires_grad_(True) for x in (q, k, v, g)]
+    s0d = s0.to(dev).requires_grad_(True) if with_init else None
+    o, s = fast_chunk_gla(*xs, initial_state=s0d, chunk_size=64)
+    ((o * do.to(dev)).sum() + (s * ds.to(dev)).sum()).backward()
+    torch.cuda.synchronize()
+    ref = O.gla_bwd(q, k, v, g, s0, do, ds, chunk=64)
+    for x, r in zip(xs + ([s0d] if with_init else []), ref):
+        assert _rel_err(x.grad, r) <= 1e-5, (T, _rel_err(x.grad, r))
+
+
+@pytest.mark.parametrize("use", ["final_only", "out_only"])
+def test_bf16_extreme_decay_gradient_flow(dev, use):
+    """bf16 inputs with gates in [-21, -1] (the reference's extreme-decay gradient case,
+    test_kernels.py:399-434): every gradient finite and equal to the oracle's, with only the
+    final state or only the output used."""
+    gen = torch.Generator().manual_seed(3 if use == "final_only" else 4)
+    B, T, H, D = 2, 200, 2, 64
+    q, k, v = (torch.randn(B, T, H, D, generator=gen).bfloat16() for _ in range(3))
+    g = (-1.0 - 20.0 * torch.rand(B, T, H, D, generator=gen)).bfloat16()
+    do, ds = _upstream(B, T, H, D, D, 9)
+    do = do.bfloat16()
+    xs = [x.to(dev).requires_grad_(True) for x in (q, k, v, g)]
+    o, s = fast_chunk_gla(*xs)
+    loss = (s * ds.to(dev)).sum() if use == "final_only" else (o.float() * do.float().to(dev)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    ref = O.gla_bwd(q, k, v, g, None, do if use == "out_only" else None, ds if use == "final_only" else None)
+    for x, r in zip(xs, ref[:4]):
+        assert bool(torch.isfinite(x.grad).all())
+        rt = torch.from_numpy(r)
+        scale = max(1.0, float(rt.abs().max()))
+        excess = (x.grad.double().cpu() - rt).abs() - (ulp_bf16(rt).double() + 2e-3 * scale)
+        assert float(excess.max()) <= 0.0, float(excess.max())
