@@ -137,21 +137,15 @@ __device__ __forceinline__ Split8<NP> lds_frag_tr(const char* base, int plane_by
 // bf16 planes.
 template <int NP, int N>
 __device__ __forceinline__ void lds_put_row(char* base, int plane_bytes, int idx, const float* x) {
-    float r[N];
 #pragma unroll
-    for (int j = 0; j < N; ++j) r[j] = x[j];
+    for (int c = 0; c < N; c += 4) {
+        float r[4] = {x[c], x[c + 1], x[c + 2], x[c + 3]};
+        uint32_t w[NP][2];
+        split_pairs<NP, 2>(r, w);
 #pragma unroll
-    for (int pl = 0; pl < NP; ++pl) {
-#pragma unroll
-        for (int c = 0; c < N; c += 4) {
-            bf16x4 hb;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                hb[j] = (__bf16)r[c + j];
-                if (pl + 1 < NP) r[c + j] -= (float)hb[j];
-            }
-            *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(base + pl * plane_bytes) + idx + c) = hb;
-        }
+        for (int pl = 0; pl < NP; ++pl)
+            *reinterpret_cast<uint2*>(reinterpret_cast<__bf16*>(base + pl * plane_bytes) + idx + c) =
+                uint2{w[pl][0], w[pl][1]};
     }
 }
 
@@ -302,6 +296,30 @@ __device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[
 #pragma unroll
             for (int i = 0; i < N; ++i) x[j][i] = ok ? x[j][i] : 0.f;
         }
+    }
+}
+
+// min(x, 0) in one instruction (fminf first quiets NaNs with an extra max in IEEE mode).
+__device__ __forceinline__ float min0(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, -__builtin_inff()); }
+
+// V rows of tokens 4*tg + j (this lane's four columns) into one bf16 plane.  bf16 V is copied
+// as loaded (no conversion round trip); rows at or past nv are zeroed.  Other types go through
+// the split.
+template <typename T, int NX>
+__device__ __forceinline__ void lds_put_v_rows(char* base, int plane_bytes, int rs, int col, const Vec<T, 4> (&v)[4],
+                                               int tg, int nv) {
+    if constexpr (std::is_same<T, __bf16>::value) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bool ok = nv >= CHUNK || 4 * tg + j < nv;
+            *reinterpret_cast<uint2*>(reinterpret_cast<__bf16*>(base) + (4 * tg + j) * rs + col) =
+                uint2{ok ? v[j].w[0] : 0u, ok ? v[j].w[1] : 0u};
+        }
+    } else {
+        float vx[4][4];
+        chunk_float(v, vx, tg, nv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(base, plane_bytes, (4 * tg + j) * rs + col, vx[j]);
     }
 }
 

@@ -39,21 +39,45 @@ struct Split8 {
     bf16x8 p[N];
 };
 
-template <int N>
-__device__ __forceinline__ Split8<N> split8(const float (&x)[8]) {
-    Split8<N> s;
-    float r[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = x[j];
+// Round-to-nearest bf16 of (a, b) in one packed conversion: a in bits 0-15, b in bits 16-31.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, b2));
+}
+
+// The two floats a packed bf16 pair stands for.
+__device__ __forceinline__ float pk_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float pk_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// Splits r[0..2W) into N packed planes w[n][0..W): pair by pair, one packed conversion gives
+// both the stored part and the value the residual subtracts.
+template <int N, int W>
+__device__ __forceinline__ void split_pairs(float (&r)[2 * W], uint32_t (&w)[N][W]) {
 #pragma unroll
     for (int n = 0; n < N; ++n) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            __bf16 h = (__bf16)r[j];
-            s.p[n][j] = h;
-            if (n + 1 < N) r[j] = r[j] - (float)h;
+        for (int j = 0; j < W; ++j) {
+            w[n][j] = pk_bf16(r[2 * j], r[2 * j + 1]);
+            if (n + 1 < N) {
+                r[2 * j] -= pk_lo(w[n][j]);
+                r[2 * j + 1] -= pk_hi(w[n][j]);
+            }
         }
     }
+}
+
+template <int N>
+__device__ __forceinline__ Split8<N> split8(const float (&x)[8]) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = x[j];
+    uint32_t w[N][4];
+    split_pairs<N, 4>(r, w);
+    Split8<N> s;
+#pragma unroll
+    for (int n = 0; n < N; ++n) s.p[n] = __builtin_bit_cast(bf16x8, u32x4{w[n][0], w[n][1], w[n][2], w[n][3]});
     return s;
 }
 
@@ -191,9 +215,11 @@ __device__ __forceinline__ float lane_bcast(float x, int src_lane) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
 }
 
+constexpr float LOG2E = 1.4426950408889634f;
+
 __device__ __forceinline__ float fast_exp(float x) {
     // exp(x) = 2^(x log2 e); v_exp_f32 is accurate to ~1 ulp over the range used here.
-    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+    return __builtin_amdgcn_exp2f(x * LOG2E);
 }
 
 }  // namespace triune

@@ -181,15 +181,18 @@ struct OutStep {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int i = 0; i < DL; ++i) G[j][i] = fminf(G[j][i], 0.f);
+                for (int i = 0; i < DL; ++i) G[j][i] = min0(G[j][i]);
             chunk_cumsum<DL>(G, GC, lane);
             bool bad = tail_unclamped;
 #pragma unroll
             for (int i = 0; i < DL; ++i) bad |= !(GC[i] >= -SPAN_MAX);
+            float mh[DL];  // -m log2(e), m = GC / 2
+#pragma unroll
+            for (int i = 0; i < DL; ++i) mh[i] = -0.5f * LOG2E * GC[i];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int i = 0; i < DL; ++i) G[j][i] = fast_exp(G[j][i] - 0.5f * GC[i]);  // exp(G - m)
+                for (int i = 0; i < DL; ++i) G[j][i] = __builtin_amdgcn_exp2f(fmaf(G[j][i], LOG2E, mh[i]));  // exp(G - m)
             if (tg == 0) {
 #pragma unroll
                 for (int i = 0; i < DL; ++i) {
@@ -217,10 +220,7 @@ struct OutStep {
                 lds_put_row<NS, DL>(sKT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
             // V rows: tokens 4*tg + j, this wave's columns 4*row .. 4*row+3
-            float vx[4][4];
-            chunk_float(cur.v, vx, tg, nv);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
+            lds_put_v_rows<TIn, NX>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
         }
         // The next chunk's loads go out now and fly during stages 2-3, except at (128, 128),
         // where their registers would push the wave past 256 VGPRs: there they go out after stage 3.
@@ -407,23 +407,23 @@ struct StateStep {
             for (int j = 0; j < 4; ++j) {
                 const bool unclamped = tail_chunk && (4 * tg + j == nv - 1);
 #pragma unroll
-                for (int i = 0; i < DL; ++i) G[j][i] = unclamped ? x[j][i] : fminf(x[j][i], 0.f);
+                for (int i = 0; i < DL; ++i) G[j][i] = unclamped ? x[j][i] : min0(x[j][i]);
             }
             float X[4][DL];
             chunk_suffix<DL>(G, X, GC, lane);
             chunk_float(cur.k, x, tg, nv);
+            float gs[DL];  // Gseg log2(e)
+#pragma unroll
+            for (int i = 0; i < DL; ++i) gs[i] = Gseg[i] * LOG2E;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
-                for (int i = 0; i < DL; ++i) x[j][i] *= fast_exp(Gseg[i] + X[j][i]);
+                for (int i = 0; i < DL; ++i) x[j][i] *= __builtin_amdgcn_exp2f(fmaf(X[j][i], LOG2E, gs[i]));
                 lds_put_row<NS, DL>(sKW, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
 #pragma unroll
             for (int i = 0; i < DL; ++i) Gseg[i] += GC[i];
-            float vx[4][4];
-            chunk_float(cur.v, vx, tg, nv);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
+            lds_put_v_rows<TIn, NX>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
         }
         after_inputs();
         __syncthreads();
