@@ -231,6 +231,12 @@ __device__ __forceinline__ TokAddr tok_addr(const TokTensor& x, const Work& wk, 
     return r;
 }
 
+// Token j of a lane's four rows is addressed through the scalar offset (j * st), but the buffer
+// range check covers only the vector and instruction offsets: a chunk whose 64 rows reach past
+// the tensor's extent (at most the last chunk of a tensor) must take them through the vector
+// offset, where the check zeroes every row past the end.
+__device__ __forceinline__ bool chunk_edge(const TokAddr& a, int64_t tc) { return (tc + CHUNK) * a.st > a.rem; }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const TokAddr& a, int64_t tc, bool valid) {
     const int64_t off = tc * a.st;
     int64_t n = a.rem - off;
@@ -268,19 +274,49 @@ struct ChunkIn {
 
 // Inputs of the chunk starting at token tc (valid: false issues the same loads as no-ops).
 // In a partial chunk the rows past its end are other tokens of the tensor or zeros; stage 1
-// zeroes them.
-template <bool OUT, typename TIn, typename TG, int DL>
+// zeroes them.  CK: a chunk may reach past a tensor's extent with rows of a lane's four (some
+// sequence length is not a multiple of 4), so such chunks address their rows through the
+// checked vector offset (see chunk_edge); without CK every load uses the scalar offset.
+template <bool OUT, bool CK = true, typename TIn, typename TG, int DL>
 __device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, bool valid) {
     __amdgpu_buffer_rsrc_t rq;
     if (OUT) rq = chunk_rsrc(ad.q, tc, valid);
     const __amdgpu_buffer_rsrc_t rk = chunk_rsrc(ad.k, tc, valid), rg = chunk_rsrc(ad.g, tc, valid),
                                  rv = chunk_rsrc(ad.v, tc, valid);
+    const bool edge = CK && ((OUT && chunk_edge(ad.q, tc)) || chunk_edge(ad.k, tc) || chunk_edge(ad.g, tc) ||
+                             chunk_edge(ad.v, tc));
+    if (edge) {  // rows through the checked vector offset (see chunk_edge)
+        int lq = ad.q.lane, lk = ad.k.lane, lg = ad.g.lane, lv = ad.v.lane;
+        asm volatile("" : "+v"(lq), "+v"(lk), "+v"(lg), "+v"(lv));  // offsets made here, not kept live
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        if (OUT) vec_load(c.q[j], rq, ad.q.lane, j * ad.q.st);
-        vec_load(c.k[j], rk, ad.k.lane, j * ad.k.st);
-        vec_load(c.g[j], rg, ad.g.lane, j * ad.g.st);
-        vec_load(c.v[j], rv, ad.v.lane, j * ad.v.st);
+        for (int j = 0; j < 4; ++j) {
+            if (OUT) vec_load(c.q[j], rq, lq + j * ad.q.st, 0);
+            vec_load(c.k[j], rk, lk + j * ad.k.st, 0);
+            vec_load(c.g[j], rg, lg + j * ad.g.st, 0);
+            vec_load(c.v[j], rv, lv + j * ad.v.st, 0);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (OUT) vec_load(c.q[j], rq, ad.q.lane, j * ad.q.st);
+            vec_load(c.k[j], rk, ad.k.lane, j * ad.k.st);
+            vec_load(c.g[j], rg, ad.g.lane, j * ad.g.st);
+            vec_load(c.v[j], rv, ad.v.lane, j * ad.v.st);
+        }
+    }
+}
+
+// Rows 4*tg + j (j < 4) of one input, as chunk_load takes them.
+template <bool CK = true, typename T, int N>
+__device__ __forceinline__ void rows_load(Vec<T, N> (&v)[4], __amdgpu_buffer_rsrc_t r, const TokAddr& a, int64_t tc) {
+    if (CK && chunk_edge(a, tc)) {
+        int l = a.lane;
+        asm volatile("" : "+v"(l));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vec_load(v[j], r, l + j * a.st, 0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vec_load(v[j], r, a.lane, j * a.st);
     }
 }
 

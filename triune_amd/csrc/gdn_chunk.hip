@@ -158,8 +158,7 @@ __device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG>& c, const ChunkAdd
     chunk_load<OUT>(c.x, ad, tc, valid);
     if (key_beta) {
         const __amdgpu_buffer_rsrc_t r = chunk_rsrc(kb, tc, valid);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) vec_load(c.bk[j], r, kb.lane, j * kb.st);
+        rows_load(c.bk, r, kb, tc);
     }
 }
 

@@ -54,12 +54,11 @@ __device__ __forceinline__ BwdAddr bwd_addr(const BwdParams& a, const Work& wk, 
     return r;
 }
 
-template <typename TIn, typename TG>
+template <bool CK, typename TIn, typename TG>
 __device__ __forceinline__ void bwd_load(BwdIn<TIn, TG>& x, const BwdAddr& ad, int64_t tc, bool valid) {
-    chunk_load<true>(x.c, ad.c, tc, valid);
+    chunk_load<true, CK>(x.c, ad.c, tc, valid);
     const __amdgpu_buffer_rsrc_t rd = chunk_rsrc(ad.d, tc, valid);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) vec_load(x.d[j], rd, ad.d.lane, j * ad.d.st);
+    rows_load<CK>(x.d, rd, ad.d, tc);
 }
 
 // Sum over the 16 lanes of each 16-lane group.
@@ -214,7 +213,8 @@ struct BwdStateStep {
     }
 };
 
-template <typename TIn, typename TG, int D>
+// CK: checked row addressing (T is not a multiple of 4; see chunk_load).
+template <typename TIn, typename TG, int D, bool CK>
 __global__ __launch_bounds__(D * 4, 2) void gla_bwd_state_kernel(BwdParams a) {
     using St = BwdStateStep<TIn, TG, D>;
     using L = typename St::L;
@@ -246,10 +246,10 @@ __global__ __launch_bounds__(D * 4, 2) void gla_bwd_state_kernel(BwdParams a) {
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     float* cbase = a.ws_chunk + (wk.b * a.f.H + h) * a.nchunks * DD;
     BwdIn<TIn, TG> A;
-    bwd_load(A, ad, tok(0), true);
+    bwd_load<CK>(A, ad, tok(0), true);
     for (int64_t c = 0; c < nch; ++c)
         St::run(a, wk, tok(c), chunk_nv(c), A, S, R, Gpre, cbase + (tok(c) / CHUNK) * DD, smem,
-                [&] { bwd_load(A, ad, tok(c + 1), c + 1 < nch); });
+                [&] { bwd_load<CK>(A, ad, tok(c + 1), c + 1 < nch); });
     float* so = a.ws_send + (w * a.f.H + h) * DD;
     float* ro = a.ws_r + (w * a.f.H + h) * DD;
 #pragma unroll
@@ -671,7 +671,7 @@ struct BwdStep {
     }
 };
 
-template <typename TIn, typename TG, int D>
+template <typename TIn, typename TG, int D, bool CK>
 __global__ __launch_bounds__(D * 4, 1) void gla_bwd_chunk_kernel(BwdParams a) {
     using St = BwdStep<TIn, TG, D>;
     using L = typename St::L;
@@ -714,9 +714,9 @@ __global__ __launch_bounds__(D * 4, 1) void gla_bwd_chunk_kernel(BwdParams a) {
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     BwdIn<TIn, TG> A;
-    bwd_load(A, ad, tok(nch - 1), true);
+    bwd_load<CK>(A, ad, tok(nch - 1), true);
     for (int64_t c = nch - 1; c >= 0; --c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, dH, acc, smem, [&] { bwd_load(A, ad, tok(c - 1), c >= 1); });
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, dH, acc, smem, [&] { bwd_load<CK>(A, ad, tok(c - 1), c >= 1); });
 }
 
 // ---------------------------------------------------------------------------------------
@@ -724,14 +724,14 @@ __global__ __launch_bounds__(D * 4, 1) void gla_bwd_chunk_kernel(BwdParams a) {
 // ---------------------------------------------------------------------------------------
 bool gla_bwd_supported(int D, int io_dt) { return D == 32 || (D == 64 && io_dt != DT_F32); }
 
-template <typename TIn, typename TG>
-static hipError_t launch_bwd_t(const BwdParams& a, int64_t n_work, bool chunk, hipStream_t stream) {
+template <typename TIn, typename TG, bool CK>
+static hipError_t launch_bwd_ck(const BwdParams& a, int64_t n_work, bool chunk, hipStream_t stream) {
     const dim3 grid((unsigned)n_work, (unsigned)a.f.H);
     const dim3 block((unsigned)(a.f.Dk * 4));
 #define TRIUNE_BWD_CASE(D_)                                                                                   \
     if (a.f.Dk == D_) {                                                                                       \
-        if (chunk) hipLaunchKernelGGL((gla_bwd_chunk_kernel<TIn, TG, D_>), grid, block, 0, stream, a);        \
-        else hipLaunchKernelGGL((gla_bwd_state_kernel<TIn, TG, D_>), grid, block, 0, stream, a);              \
+        if (chunk) hipLaunchKernelGGL((gla_bwd_chunk_kernel<TIn, TG, D_, CK>), grid, block, 0, stream, a);    \
+        else hipLaunchKernelGGL((gla_bwd_state_kernel<TIn, TG, D_, CK>), grid, block, 0, stream, a);          \
         return hipGetLastError();                                                                             \
     }
     TRIUNE_BWD_CASE(32)
@@ -740,6 +740,13 @@ static hipError_t launch_bwd_t(const BwdParams& a, int64_t n_work, bool chunk, h
     }
 #undef TRIUNE_BWD_CASE
     return hipErrorInvalidValue;
+}
+
+// Unchecked row addressing only when T is a whole number of four-row groups.
+template <typename TIn, typename TG>
+static hipError_t launch_bwd_t(const BwdParams& a, int64_t n_work, bool chunk, hipStream_t stream) {
+    if (!a.f.varlen && a.f.T % 4 == 0) return launch_bwd_ck<TIn, TG, false>(a, n_work, chunk, stream);
+    return launch_bwd_ck<TIn, TG, true>(a, n_work, chunk, stream);
 }
 
 static hipError_t launch_bwd(const BwdParams& a, int64_t n_work, int io_dt, bool chunk, hipStream_t stream) {

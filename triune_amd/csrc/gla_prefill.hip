@@ -350,7 +350,7 @@ struct OutStep {
 };
 
 // Outputs of one segment from its carried-in state S (K3).
-template <typename TIn, typename TG, int DK, int DV>
+template <typename TIn, typename TG, int DK, int DV, bool CK>
 __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
     using St = OutStep<TIn, TG, DK, DV>;
     constexpr int DL = St::DL;
@@ -365,12 +365,12 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     // One register set: stage 1 consumes it and the next chunk's loads refill it at once, so they
     // are in flight during stages 2-3 (registers go to occupancy instead of a second set).
     ChunkIn<TIn, TG, DL> A;
-    chunk_load<true>(A, ad, tok(0), true);
+    chunk_load<true, CK>(A, ad, tok(0), true);
     PendingOut pend;
     pend.valid = false;
     for (int64_t c = 0; c < nch; ++c)
         St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
-                [&] { chunk_load<true>(A, ad, tok(c + 1), c + 1 < nch); });
+                [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
     if (pend.valid)  // after the last chunk's closing barrier the A^T planes are free
         flush_out(a, wk, h, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
                   St::L::OS);
@@ -441,7 +441,7 @@ struct StateStep {
     }
 };
 
-template <typename TIn, typename TG, int DK, int DV>
+template <typename TIn, typename TG, int DK, int DV, bool CK>
 __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&Lst)[DK / 16],
                                    float (&Gseg)[DK / (DV / 16) / 4], char* smem) {
     using St = StateStep<TIn, TG, DK, DV>;
@@ -455,21 +455,22 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     ChunkIn<TIn, TG, DL> A, B;
-    chunk_load<false>(A, ad, tok(nch - 1), true);
+    chunk_load<false, CK>(A, ad, tok(nch - 1), true);
     __builtin_amdgcn_sched_barrier(0);  // issue order A, B on every path (see segment_walk)
-    chunk_load<false>(B, ad, tok(nch - 2), nch > 1);
+    chunk_load<false, CK>(B, ad, tok(nch - 2), nch > 1);
     // pairs of chunks from the end, then chunk 0 if nch is odd (single-exit loop, as in segment_walk)
     for (int64_t c = nch - 1; c >= 1; c -= 2) {
         St::run(a, wk, tok(c), chunk_nv(c), A, Lst, Gseg, smem,
-                [&] { chunk_load<false>(A, ad, tok(c - 2), c >= 2); });
+                [&] { chunk_load<false, CK>(A, ad, tok(c - 2), c >= 2); });
         St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, Lst, Gseg, smem,
-                [&] { chunk_load<false>(B, ad, tok(c - 3), c >= 3); });
+                [&] { chunk_load<false, CK>(B, ad, tok(c - 3), c >= 3); });
     }
     if (nch & 1) St::run(a, wk, tok(0), chunk_nv(0), A, Lst, Gseg, smem, [] {});
 }
 
 
-template <typename TIn, typename TG, int DK, int DV>
+// CK: checked row addressing (some sequence length is not a multiple of 4; see chunk_load).
+template <typename TIn, typename TG, int DK, int DV, bool CK>
 __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams a) {
     using L = Lay<TIn, DK, DV, false>;
     constexpr int DL = L::DPW / 4;
@@ -484,7 +485,7 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     for (int db = 0; db < DK / 16; ++db) S[db] = zero4();
 #pragma unroll
     for (int i = 0; i < DL; ++i) Gseg[i] = 0.f;
-    segment_state_walk<TIn, TG, DK, DV>(a, wk, h, S, Gseg, smem);
+    segment_state_walk<TIn, TG, DK, DV, CK>(a, wk, h, S, Gseg, smem);
     float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
 #pragma unroll
     for (int db = 0; db < DK / 16; ++db)
@@ -497,7 +498,7 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     }
 }
 
-template <typename TIn, typename TG, int DK, int DV>
+template <typename TIn, typename TG, int DK, int DV, bool CK>
 __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void gla_seg_output_kernel(PrefillParams a) {
     using L = Lay<TIn, DK, DV, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
@@ -511,7 +512,7 @@ __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, DV)];
-    segment_walk<TIn, TG, DK, DV>(a, wk, h, S, smem);
+    segment_walk<TIn, TG, DK, DV, CK>(a, wk, h, S, smem);
 }
 
 // K0 (varlen): segment offsets from cu_seqlens, one thread block.
@@ -556,14 +557,14 @@ bool prefill_dtype_supported(int Dk, int Dv, int io_dt) {
     return prefill_shape_supported(Dk, Dv) && !(io_dt == DT_F32 && Dk == 128 && Dv == 128);
 }
 
-template <typename TIn, typename TG>
-static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
+template <typename TIn, typename TG, bool CK>
+static hipError_t launch_seg_ck(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
     const dim3 grid((unsigned)n_work, (unsigned)a.H);
     const dim3 block((unsigned)(a.Dv * 4));
 #define TRIUNE_SEG_CASE(DK_, DV_)                                                                       \
     if (a.Dk == DK_ && a.Dv == DV_) {                                                                   \
-        if (with_out) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_>), grid, block, 0, stream, a); \
-        else hipLaunchKernelGGL((gla_seg_state_kernel<TIn, TG, DK_, DV_>), grid, block, 0, stream, a);          \
+        if (with_out) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_, CK>), grid, block, 0, stream, a); \
+        else hipLaunchKernelGGL((gla_seg_state_kernel<TIn, TG, DK_, DV_, CK>), grid, block, 0, stream, a);          \
         return hipGetLastError();                                                                       \
     }
     TRIUNE_SEG_CASE(64, 64)
@@ -574,6 +575,14 @@ static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with
     TRIUNE_SEG_CASE(128, 64)
 #undef TRIUNE_SEG_CASE
     return hipErrorInvalidValue;
+}
+
+// Unchecked row addressing only when every sequence is a whole number of four-row groups (dense
+// with T % 4 == 0): then no chunk reaches past a tensor's extent with part of a group.
+template <typename TIn, typename TG>
+static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
+    if (!a.varlen && a.T % 4 == 0) return launch_seg_ck<TIn, TG, false>(a, n_work, with_out, stream);
+    return launch_seg_ck<TIn, TG, true>(a, n_work, with_out, stream);
 }
 
 static hipError_t launch_seg(const PrefillParams& a, int64_t n_work, int io_dt, bool with_out, hipStream_t stream) {
@@ -598,7 +607,7 @@ int gla_seg_output_blocks_per_cu(int Dk, int Dv) {
 #define TRIUNE_OCC_CASE(DK_, DV_)                                                                             \
     if (Dk == DK_ && Dv == DV_)                                                                               \
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                                     \
-            &nb, reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_>), DV_ * 4, 0);
+            &nb, reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, true>), DV_ * 4, 0);
     TRIUNE_OCC_CASE(64, 64)
     TRIUNE_OCC_CASE(128, 128)
     TRIUNE_OCC_CASE(32, 32)
