@@ -261,9 +261,24 @@ __global__ __launch_bounds__(64) void recurrent_scan_bwd_kernel(ScanBwdParams a,
     if (act) st4_dt(a.d_init, a.out_dt, bh * DD + e, d);
 }
 
+// Sum over the 16 lanes of a DPP row, in every lane of it: quad swaps (lane ^ 1, lane ^ 2), then
+// the half-row mirror (quad q <-> quad q ^ 1) and the row mirror (half <-> half).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float dpp_sum16(float x) {
+    x = dpp_add<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    x = dpp_add<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    x = dpp_add<0x141>(x);  // row_half_mirror
+    return dpp_add<0x140>(x);  // row_mirror
+}
+
 // The backward with the dtypes fixed at compile time: upstream gradient of s_all and every output
-// in GT, decay factors in fp32 (same work split as recurrent_scan_bwd_kernel).
-template <typename GT>
+// in GT, decay factors in fp32 (same work split as recurrent_scan_bwd_kernel).  LPR16: a row's
+// partial products are summed over its 16 lanes (one DPP row, Dv = 64) without LDS round trips.
+template <typename GT, bool LPR16>
 __global__ __launch_bounds__(64) void recurrent_scan_bwd_typed_kernel(ScanBwdParams a, int lpr) {
     const int lane = threadIdx.x;
     const int row = blockIdx.x * (64 / lpr) + lane / lpr;
@@ -300,7 +315,11 @@ __global__ __launch_bounds__(64) void recurrent_scan_bwd_typed_kernel(ScanBwdPar
             const int64_t i5 = (bh * N + n) * DD + e;
             if (act) st4_t<GT>(a.d_kv, i5, d);
             float part = act ? d[0] * sp[u][0] + d[1] * sp[u][1] + d[2] * sp[u][2] + d[3] * sp[u][3] : 0.f;
-            for (int off = lpr >> 1; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+            if constexpr (LPR16) {
+                part = dpp_sum16(part);
+            } else {
+                for (int off = lpr >> 1; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+            }
             if (act && j0 == 0) reinterpret_cast<GT*>(a.d_dec)[(bh * N + n) * a.Dk + row] = (GT)part;
 #pragma unroll
             for (int c = 0; c < 4; ++c) d[c] = ds[u][c] + dc[u] * d[c];
@@ -316,9 +335,13 @@ hipError_t launch_recurrent_scan_bwd(const ScanBwdParams& a, hipStream_t stream)
     const int rpb = 64 / lpr;
     dim3 grid((unsigned)((a.Dk + rpb - 1) / rpb), (unsigned)a.H, (unsigned)a.n_outer);
     const bool typed = a.dec_dt == DT_F32 && (!a.d_s_all || a.dsa_dt == a.out_dt);
-    if (typed && a.out_dt == DT_F32) hipLaunchKernelGGL(recurrent_scan_bwd_typed_kernel<float>, grid, dim3(64), 0, stream, a, lpr);
-    else if (typed && a.out_dt == DT_BF16) hipLaunchKernelGGL(recurrent_scan_bwd_typed_kernel<__bf16>, grid, dim3(64), 0, stream, a, lpr);
-    else if (typed && a.out_dt == DT_F16) hipLaunchKernelGGL(recurrent_scan_bwd_typed_kernel<_Float16>, grid, dim3(64), 0, stream, a, lpr);
+    if (typed && lpr == 16) {
+        if (a.out_dt == DT_F32) hipLaunchKernelGGL((recurrent_scan_bwd_typed_kernel<float, true>), grid, dim3(64), 0, stream, a, lpr);
+        else if (a.out_dt == DT_BF16) hipLaunchKernelGGL((recurrent_scan_bwd_typed_kernel<__bf16, true>), grid, dim3(64), 0, stream, a, lpr);
+        else hipLaunchKernelGGL((recurrent_scan_bwd_typed_kernel<_Float16, true>), grid, dim3(64), 0, stream, a, lpr);
+    } else if (typed && a.out_dt == DT_F32) hipLaunchKernelGGL((recurrent_scan_bwd_typed_kernel<float, false>), grid, dim3(64), 0, stream, a, lpr);
+    else if (typed && a.out_dt == DT_BF16) hipLaunchKernelGGL((recurrent_scan_bwd_typed_kernel<__bf16, false>), grid, dim3(64), 0, stream, a, lpr);
+    else if (typed && a.out_dt == DT_F16) hipLaunchKernelGGL((recurrent_scan_bwd_typed_kernel<_Float16, false>), grid, dim3(64), 0, stream, a, lpr);
     else hipLaunchKernelGGL(recurrent_scan_bwd_kernel, grid, dim3(64), 0, stream, a, lpr);
     return hipGetLastError();
 }
