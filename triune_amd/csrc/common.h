@@ -210,6 +210,20 @@ __device__ __forceinline__ float row_inclusive_scan(float x) {
     return x;
 }
 
+// Sum over the 16 lanes of a DPP row, in every lane of it: quad swaps (lane ^ 1, lane ^ 2), then
+// the half-row mirror (quad q <-> quad q ^ 1) and the row mirror (half <-> half).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float dpp_sum16(float x) {
+    x = dpp_add<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    x = dpp_add<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    x = dpp_add<0x141>(x);  // row_half_mirror
+    return dpp_add<0x140>(x);  // row_mirror
+}
+
 // Value held by lane src_lane.
 __device__ __forceinline__ float lane_bcast(float x, int src_lane) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));

@@ -62,13 +62,7 @@ __device__ __forceinline__ void bwd_load(BwdIn<TIn, TG>& x, const BwdAddr& ad, i
 }
 
 // Sum over the 16 lanes of each 16-lane group.
-__device__ __forceinline__ float sum16(float x) {
-    x += __shfl_xor(x, 1);
-    x += __shfl_xor(x, 2);
-    x += __shfl_xor(x, 4);
-    x += __shfl_xor(x, 8);
-    return x;
-}
+__device__ __forceinline__ float sum16(float x) { return dpp_sum16(x); }
 
 // Four values at columns [col, col+4) of rows 4*tg + j (j < 4) of a [B, T, H, D] output: bounded
 // buffer stores over the chunk's nv rows (rows past the end are dropped).

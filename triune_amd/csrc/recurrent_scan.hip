@@ -261,20 +261,6 @@ __global__ __launch_bounds__(64) void recurrent_scan_bwd_kernel(ScanBwdParams a,
     if (act) st4_dt(a.d_init, a.out_dt, bh * DD + e, d);
 }
 
-// Sum over the 16 lanes of a DPP row, in every lane of it: quad swaps (lane ^ 1, lane ^ 2), then
-// the half-row mirror (quad q <-> quad q ^ 1) and the row mirror (half <-> half).
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float x) {
-    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float dpp_sum16(float x) {
-    x = dpp_add<0xB1>(x);   // quad_perm [1, 0, 3, 2]
-    x = dpp_add<0x4E>(x);   // quad_perm [2, 3, 0, 1]
-    x = dpp_add<0x141>(x);  // row_half_mirror
-    return dpp_add<0x140>(x);  // row_mirror
-}
-
 // The backward with the dtypes fixed at compile time: upstream gradient of s_all and every output
 // in GT, decay factors in fp32 (same work split as recurrent_scan_bwd_kernel).  LPR16: a row's
 // partial products are summed over its 16 lanes (one DPP row, Dv = 64) without LDS round trips.
