@@ -363,7 +363,7 @@ __device__ __forceinline__ void lds_put_v_rows(char* base, int plane_bytes, int 
 // returns the chunk totals in GC[i] (identical across the lanes sharing `row`).
 template <int DL>
 __device__ __forceinline__ void chunk_cumsum(float (&G)[4][DL], float (&GC)[DL], int lane) {
-    float T[DL], I[DL], R[DL], P[DL];
+    float T[DL], I[DL];
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
         G[1][i] += G[0][i];
@@ -377,27 +377,23 @@ __device__ __forceinline__ void chunk_cumsum(float (&G)[4][DL], float (&GC)[DL],
     for (int i = 0; i < DL; ++i) I[i] += row_shr<4>(I[i]);
 #pragma unroll
     for (int i = 0; i < DL; ++i) I[i] += row_shr<8>(I[i]);
-    // DPP row rr's total for this `row` is in lane 16*rr + 12 + row; P = inclusive scan of the
-    // totals over rr
-    const int rr = lane >> 4, own = (lane & 48) | 12 | (lane & 3);
-#pragma unroll
-    for (int i = 0; i < DL; ++i) R[i] = lane_bcast(I[i], own);
-#pragma unroll
-    for (int i = 0; i < DL; ++i) {
-        const float prev = lane_bcast(R[i], (lane - 16) & 63);
-        P[i] = R[i] + (rr >= 1 ? prev : 0.f);
-    }
+    // R = this DPP row's total for the lane's `row` (rotations by 4 and 8 sum its four tg); then
+    // an inclusive scan of R over the four DPP rows through whole-row swaps: the 16-lane swap
+    // gives odd rows their even neighbour and every row its pair's total, the 32-lane swap
+    // gives rows 2-3 the total of rows 0-1 and every lane the chunk total.
+    const int rr = lane >> 4;
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
-        const float prev = lane_bcast(P[i], (lane - 32) & 63);
-        P[i] += rr >= 2 ? prev : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < DL; ++i) {
-        const float E = I[i] - T[i] + (P[i] - R[i]);
+        float R = T[i] + row_ror<4>(T[i]);
+        R += row_ror<8>(R);
+        const RowPair p16 = swap16(R);
+        const float Q = p16.lo + p16.hi;  // the pair's total (rows 0+1 or 2+3)
+        const RowPair p32 = swap32(Q);
+        const float P = R + ((rr & 1) ? p16.lo : 0.f) + (rr >= 2 ? p32.lo : 0.f);
+        const float E = I[i] - T[i] + (P - R);
 #pragma unroll
         for (int j = 0; j < 4; ++j) G[j][i] += E;
-        GC[i] = lane_bcast(P[i], 60 | (lane & 3));
+        GC[i] = p32.lo + p32.hi;
     }
 }
 
@@ -407,7 +403,7 @@ __device__ __forceinline__ void chunk_cumsum(float (&G)[4][DL], float (&GC)[DL],
 // prefix sums loses that accuracy when the total is large).
 template <int DL>
 __device__ __forceinline__ void chunk_suffix(const float (&g)[4][DL], float (&X)[4][DL], float (&GC)[DL], int lane) {
-    float T[DL], Y[DL], Z[DL], C[DL];
+    float T[DL], Y[DL];
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
         X[3][i] = 0.f;
@@ -423,27 +419,20 @@ __device__ __forceinline__ void chunk_suffix(const float (&g)[4][DL], float (&X)
     for (int i = 0; i < DL; ++i) Y[i] += row_shl<4>(Y[i]);
 #pragma unroll
     for (int i = 0; i < DL; ++i) Y[i] += row_shl<8>(Y[i]);
-    // Z = this DPP row's total (lane 16*rr + row, the row's first tg); C = inclusive suffix of Z
-    const int rr = lane >> 4, first = (lane & 48) | (lane & 3);
-#pragma unroll
-    for (int i = 0; i < DL; ++i) Z[i] = lane_bcast(Y[i] + T[i], first);
-#pragma unroll
-    for (int i = 0; i < DL; ++i) {
-        const float next = lane_bcast(Z[i], (lane + 16) & 63);
-        C[i] = Z[i] + (rr <= 2 ? next : 0.f);
-    }
+    // Z = this DPP row's total for the lane's `row`; the rows after the lane's own add up through
+    // whole-row swaps (even rows take their odd neighbour; rows 0-1 take the total of rows 2-3).
+    const int rr = lane >> 4;
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
-        const float next = lane_bcast(C[i], (lane + 32) & 63);
-        C[i] += rr <= 1 ? next : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < DL; ++i) {
-        const float later_rows = lane_bcast(C[i], (lane + 16) & 63);
-        const float E = Y[i] + (rr <= 2 ? later_rows : 0.f);
+        float Z = T[i] + row_ror<4>(T[i]);
+        Z += row_ror<8>(Z);
+        const RowPair p16 = swap16(Z);
+        const RowPair p32 = swap32(p16.lo + p16.hi);
+        const float later_rows = ((rr & 1) ? 0.f : p16.hi) + (rr < 2 ? p32.hi : 0.f);
+        const float E = Y[i] + later_rows;
 #pragma unroll
         for (int j = 0; j < 4; ++j) X[j][i] += E;
-        GC[i] = lane_bcast(C[i], lane & 3);
+        GC[i] = p32.lo + p32.hi;
     }
 }
 

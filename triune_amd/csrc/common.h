@@ -224,6 +224,27 @@ __device__ __forceinline__ float dpp_sum16(float x) {
     return dpp_add<0x140>(x);  // row_mirror
 }
 
+// Rotation by N lanes within each 16-lane DPP row (lane p reads lane p - N of its row).
+template <int N>
+__device__ __forceinline__ float row_ror(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 + N, 0xf, 0xf, false));
+}
+
+// Whole-row exchanges (VALU, no LDS).  With rows x0..x3 of 16 lanes: swap16 returns
+// lo = [x0, x0, x2, x2] and hi = [x1, x1, x3, x3]; swap32 returns lo = [x0, x1, x0, x1] and
+// hi = [x2, x3, x2, x3].
+struct RowPair {
+    float lo, hi;
+};
+__device__ __forceinline__ RowPair swap16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ RowPair swap32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+
 // Value held by lane src_lane.
 __device__ __forceinline__ float lane_bcast(float x, int src_lane) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));
