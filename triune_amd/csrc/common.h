@@ -245,6 +245,29 @@ __device__ __forceinline__ RowPair swap32(float x) {
     return {__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
 
+// x + (the value of lane ^ SH): through whole-row swaps for SH = 16 and 32 (VALU), otherwise
+// through an LDS-pipe shuffle.  Both lanes of a pair get the same, identically rounded sum.
+template <int SH>
+__device__ __forceinline__ float xor_sum(float x) {
+    if constexpr (SH == 16) {
+        const RowPair p = swap16(x);
+        return p.lo + p.hi;
+    } else if constexpr (SH == 32) {
+        const RowPair p = swap32(x);
+        return p.lo + p.hi;
+    } else {
+        return x + __shfl_xor(x, SH);
+    }
+}
+
+// Sum over the lanes l ^ (SH * 2^k) of a wave (SH a power of two): every lane of the group
+// gets it.
+template <int SH>
+__device__ __forceinline__ float xor_group_sum(float x) {
+    if constexpr (SH < 64) return xor_group_sum<SH * 2>(xor_sum<SH>(x));
+    return x;
+}
+
 // Value held by lane src_lane.
 __device__ __forceinline__ float lane_bcast(float x, int src_lane) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(src_lane << 2, __float_as_int(x)));

@@ -103,9 +103,7 @@ __global__ __launch_bounds__(DK * DV / (4 * RPT)) void gla_decode_kernel(DecodeP
         for (int m = 0; m < RPT; ++m) __builtin_nontemporal_store(y[m], reinterpret_cast<f32x4*>(sout + m * DV));
         // reduce over the row groups of a wave (lanes tid ^ CG*2^k share a column group) ...
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int sh = CG; sh < 64; sh <<= 1) o4[c] += __shfl_xor(o4[c], sh);
+        for (int c = 0; c < 4; ++c) o4[c] = xor_group_sum<CG>(o4[c]);
         // ... then across the waves (double-buffered: the next row's writes follow a barrier)
         if ((tid % 64) < CG) red[buf][wave][cg] = f32x4{o4[0], o4[1], o4[2], o4[3]};
         __syncthreads();

@@ -327,9 +327,7 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
         const uint32_t nrow = row + gridDim.x;
         if (nrow < rows) fetch(nxt, nrow);
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int sh = CG; sh < 64; sh <<= 1) o4[c] += __shfl_xor(o4[c], sh);
+        for (int c = 0; c < 4; ++c) o4[c] = xor_group_sum<CG>(o4[c]);
         if (lane < CG) red[buf][wave][cg] = f32x4{o4[0], o4[1], o4[2], o4[3]};
         // barrier ordering LDS only: the state stores need not complete before it
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
