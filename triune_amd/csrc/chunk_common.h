@@ -489,6 +489,25 @@ __device__ __forceinline__ void out_store4(const OutRsrc& r, int voff, int dt, c
     __builtin_amdgcn_raw_buffer_store_b64(w1, r.hi, voff + 8, 0, 0);
 }
 
+// One output of a (sequence, head) of a [B, T, H, D] tensor: token 0's address and the token
+// stride in bytes, made once per workgroup so a chunk loop carries three scalars per output
+// instead of its strides.
+struct RowsOut {
+    char* base;
+    int64_t ost;
+    int es, dt;
+};
+
+__device__ __forceinline__ RowsOut rows_out(void* p, int64_t sb, int64_t st, int64_t sh, int dt, const Work& wk,
+                                            int64_t h) {
+    RowsOut r;
+    r.dt = dt;
+    r.es = dt_size(dt);
+    r.ost = st * r.es;
+    r.base = reinterpret_cast<char*>(p) + uniform_i64((wk.b * sb + wk.row0 * st + h * sh) * r.es);
+    return r;
+}
+
 // s_waitcnt vmcnt(0) (the LDS and export counters are left free): every vector memory access of
 // this wave has completed.  On gfx9 one counter tracks loads and stores, so a later wait for a
 // load issued before a burst of stores also waits for those stores; draining the (long since

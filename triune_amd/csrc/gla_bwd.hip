@@ -64,28 +64,9 @@ __device__ __forceinline__ void bwd_load(BwdIn<TIn, TG>& x, const BwdAddr& ad, i
 // Sum over the 16 lanes of each 16-lane group.
 __device__ __forceinline__ float sum16(float x) { return dpp_sum16(x); }
 
-// One gradient output of a (sequence, head) of a [B, T, H, D] tensor: token 0's address and the
-// token stride in bytes, made once per workgroup so the chunk loop carries three scalars per
-// output instead of its strides.
-struct GradOut {
-    char* base;
-    int64_t ost;
-    int es, dt;
-};
-
-__device__ __forceinline__ GradOut grad_out(void* p, int64_t sb, int64_t st, int64_t sh, int dt, const Work& wk,
-                                            int64_t h) {
-    GradOut r;
-    r.dt = dt;
-    r.es = dt_size(dt);
-    r.ost = st * r.es;
-    r.base = reinterpret_cast<char*>(p) + uniform_i64((wk.b * sb + wk.row0 * st + h * sh) * r.es);
-    return r;
-}
-
 // Four values at columns [col, col+4) of rows 4*tg + j (j < 4) of the chunk at tc: bounded
 // buffer stores over the chunk's nv rows (rows past the end are dropped).
-__device__ __forceinline__ void store_rows4(const GradOut& o, int D, int64_t tc, int nv, int tg, int col,
+__device__ __forceinline__ void store_rows4(const RowsOut& o, int D, int64_t tc, int nv, int tg, int col,
                                             const float (&x)[4][4]) {
     const int es = o.es, dt = o.dt;
     const int64_t ost = o.ost;
@@ -424,7 +405,7 @@ struct BwdStep {
     template <typename Hook>
     __device__ static void run(const BwdParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
                                const BwdIn<TIn, TG>& cur, f32x4 (&dH)[NDB], float (&acc)[DL], char* smem,
-                               const GradOut (&go)[4], Hook&& after_inputs) {
+                               const RowsOut (&go)[4], Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int c0 = 16 * wave;       // key dims of dq / dk, value columns of dv / dH
@@ -642,7 +623,7 @@ struct BwdStep {
                 *reinterpret_cast<f32x4*>(sFQ + (16 * tb + r16) * L::FS + c0 + 4 * g4) = dQ[tb];
                 *reinterpret_cast<f32x4*>(sFK + (16 * tb + r16) * L::FS + c0 + 4 * g4) = dK[tb];
             }
-            const GradOut& ov = go[2];
+            const RowsOut& ov = go[2];
             store_tiles(ov.base + uniform_i64(tc * ov.ost + c0 * ov.es), ov.ost, ov.es, ov.dt, nv, dV,
                         reinterpret_cast<float*>(sPH) + wave * 16 * L::OS, L::OS);
         }
@@ -723,10 +704,10 @@ __global__ __launch_bounds__(D * 4, 1) void gla_bwd_chunk_kernel(BwdParams a) {
         return (int)(r < CHUNK ? r : CHUNK);
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
-    const GradOut go[4] = {grad_out(a.dq, a.dq_sb, a.dq_st, a.dq_sh, a.d_dt, wk, h),
-                           grad_out(a.dk, a.dk_sb, a.dk_st, a.dk_sh, a.d_dt, wk, h),
-                           grad_out(a.dv, a.dv_sb, a.dv_st, a.dv_sh, a.d_dt, wk, h),
-                           grad_out(a.dg, a.dg_sb, a.dg_st, a.dg_sh, a.dg_dt, wk, h)};
+    const RowsOut go[4] = {rows_out(a.dq, a.dq_sb, a.dq_st, a.dq_sh, a.d_dt, wk, h),
+                           rows_out(a.dk, a.dk_sb, a.dk_st, a.dk_sh, a.d_dt, wk, h),
+                           rows_out(a.dv, a.dv_sb, a.dv_st, a.dv_sh, a.d_dt, wk, h),
+                           rows_out(a.dg, a.dg_sb, a.dg_st, a.dg_sh, a.dg_dt, wk, h)};
     BwdIn<TIn, TG> A;
     bwd_load<CK>(A, ad, tok(nch - 1), true);
     for (int64_t c = nch - 1; c >= 0; --c)
