@@ -554,9 +554,10 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel
     }
 }
 
-// K3: outputs of one segment from S_in[p] (in the N slot after the scan).
+// K3: outputs of one segment from S_in[p] (in the N slot after the scan).  Two workgroups per CU
+// where two fit in LDS (bf16 I/O); fp16 and fp32 I/O hold larger planes and run one.
 template <typename TIn, typename TG>
-__global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_out_kernel(PrefillParams a) {
+__global__ __launch_bounds__(256, ((2 * GLay<TIn, true>::BYTES <= 160 * 1024) ? 2 : 1)) void gdn_seg_out_kernel(PrefillParams a) {
     using L = GLay<TIn, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
