@@ -585,13 +585,14 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
 
 namespace {
 
-// Chunked GDN: segments per sequence fill the resident output-kernel slots once.
+// Chunked GDN: segments per sequence fill the resident output-kernel slots once (for I/O dtype
+// io_dt; bf16 holds the most workgroups per CU, so its plan bounds the workspace of every dtype).
 struct GdnPlan {
     int64_t nseg, n_work;
     size_t off_m, off_spare, total;
 };
 
-GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H) {
+GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt) {
     static std::mutex mu;
     static std::map<int, int64_t> slots_cache;
     int dev = 0;
@@ -599,13 +600,14 @@ GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H) {
     int64_t slots;
     {
         std::lock_guard<std::mutex> lock(mu);
-        auto it = slots_cache.find(dev);
+        const int key = 4 * dev + io_dt;
+        auto it = slots_cache.find(key);
         if (it == slots_cache.end()) {
             int ncu = 0;
             if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
                 ncu <= 0)
                 ncu = 256;
-            it = slots_cache.emplace(dev, (int64_t)ncu * gdn_seg_out_blocks_per_cu()).first;
+            it = slots_cache.emplace(key, (int64_t)ncu * gdn_seg_out_blocks_per_cu(io_dt)).first;
         }
         slots = it->second;
     }
@@ -627,7 +629,7 @@ extern "C" {
 
 size_t triune_hip_gdn_prefill_chunked_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv) {
     if (B <= 0 || T <= 0 || H <= 0 || Dk != 64 || Dv != 64) return 0;
-    return plan_gdn(B, T, H).total;
+    return plan_gdn(B, T, H, TRIUNE_DT_BF16).total;
 }
 
 int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* g, int io_dtype,
@@ -666,7 +668,7 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
         sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = 0;
         return launch_status(launch_recurrent_scan(sc, st));
     }
-    const GdnPlan pl = plan_gdn(B, T, H);
+    const GdnPlan pl = plan_gdn(B, T, H, io_dtype);
     if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
     if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;

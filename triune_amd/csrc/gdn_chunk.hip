@@ -701,10 +701,14 @@ hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt
     return hipGetLastError();
 }
 
-int gdn_seg_out_blocks_per_cu() {
+// Resident output-kernel workgroups per CU for I/O dtype io_dt (the gate dtype does not change
+// the kernel's LDS or register use).
+int gdn_seg_out_blocks_per_cu(int io_dt) {
+    const void* k = io_dt == DT_F16   ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16>)
+                    : io_dt == DT_F32 ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float>)
+                                      : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16>);
     int nb = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &nb, reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16>), 256, 0);
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0);
     return (e == hipSuccess && nb > 0) ? nb : 1;
 }
 
