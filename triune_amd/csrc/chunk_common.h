@@ -225,7 +225,9 @@ __device__ __forceinline__ TokAddr tok_addr(const TokTensor& x, const Work& wk, 
     const int64_t es = (int64_t)sizeof(T);
     const int64_t base = uniform_i64((wk.b * x.sb + wk.row0 * x.st + h * x.sh) * es);
     r.p0 = reinterpret_cast<const char*>(x.p) + base;
-    r.rem = x.extent - base;
+    // readable bytes: to the tensor's extent and at most to the segment's last token
+    const int64_t seg = wk.t_end * x.st * es;
+    r.rem = x.extent - base < seg ? x.extent - base : seg;
     r.st = (int32_t)(x.st * es);
     r.lane = 4 * tg * r.st + col * (int32_t)es;
     return r;
@@ -277,6 +279,9 @@ struct ChunkIn {
 // zeroes them.  CK: a chunk may reach past a tensor's extent with rows of a lane's four (some
 // sequence length is not a multiple of 4), so such chunks address their rows through the
 // checked vector offset (see chunk_edge); without CK every load uses the scalar offset.
+// Records end at the segment's last token (tok_addr), so without CK, where every sequence length
+// and hence every chunk's row count is a multiple of 4, whole four-row groups past a chunk read as
+// zero and stage 1 need not zero them.
 template <bool OUT, bool CK = true, typename TIn, typename TG, int DL>
 __device__ __forceinline__ void chunk_load(ChunkIn<TIn, TG, DL>& c, const ChunkAddr& ad, int64_t tc, bool valid) {
     __amdgpu_buffer_rsrc_t rq;
@@ -321,11 +326,12 @@ __device__ __forceinline__ void rows_load(Vec<T, N> (&v)[4], __amdgpu_buffer_rsr
 }
 
 // x[j][i] = element i of token j, zeroed for tokens at or past nv (partial chunks only).
-template <typename T, int N>
+// ZERO = false: the loads already returned zero past the chunk (chunk_load without CK).
+template <bool ZERO = true, typename T, int N>
 __device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[4][N], int tg, int nv) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) vec_float(v[j], x[j]);
-    if (nv < CHUNK) {
+    if (ZERO && nv < CHUNK) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const bool ok = 4 * tg + j < nv;
@@ -341,19 +347,19 @@ __device__ __forceinline__ float min0(float x) { return __builtin_amdgcn_fmed3f(
 // V rows of tokens 4*tg + j (this lane's four columns) into one bf16 plane.  bf16 V is copied
 // as loaded (no conversion round trip); rows at or past nv are zeroed.  Other types go through
 // the split.
-template <typename T, int NX>
+template <typename T, int NX, bool ZERO = true>
 __device__ __forceinline__ void lds_put_v_rows(char* base, int plane_bytes, int rs, int col, const Vec<T, 4> (&v)[4],
                                                int tg, int nv) {
     if constexpr (std::is_same<T, __bf16>::value) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const bool ok = nv >= CHUNK || 4 * tg + j < nv;
+            const bool ok = !ZERO || nv >= CHUNK || 4 * tg + j < nv;
             *reinterpret_cast<uint2*>(reinterpret_cast<__bf16*>(base) + (4 * tg + j) * rs + col) =
                 uint2{ok ? v[j].w[0] : 0u, ok ? v[j].w[1] : 0u};
         }
     } else {
         float vx[4][4];
-        chunk_float(v, vx, tg, nv);
+        chunk_float<ZERO>(v, vx, tg, nv);
 #pragma unroll
         for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(base, plane_bytes, (4 * tg + j) * rs + col, vx[j]);
     }

@@ -148,7 +148,8 @@ __device__ __forceinline__ void flush_out(const PrefillParams& a, const Work& wk
     }
 }
 
-template <typename TIn, typename TG, int DK, int DV>
+// CK: checked row addressing (see chunk_load); without it the loads zero rows past the chunk.
+template <typename TIn, typename TG, int DK, int DV, bool CK>
 struct OutStep {
     using L = Lay<TIn, DK, DV, true>;
     using PR = Prec<TIn>;
@@ -177,7 +178,7 @@ struct OutStep {
         // ---------------- stage 1 -------------------------------------------------------
         {
             float G[4][DL], GC[DL], x[4][DL];
-            chunk_float(cur.g, G, tg, nv);
+            chunk_float<CK>(cur.g, G, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -204,7 +205,7 @@ struct OutStep {
             const bool any_bad = __any(bad);
             if (lane == 0) sFLAG[wave] = any_bad ? 1 : 0;
             // Qt rows
-            chunk_float(cur.q, x, tg, nv);
+            chunk_float<CK>(cur.q, x, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -212,7 +213,7 @@ struct OutStep {
                 lds_put_row<NS, DL>(sQT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
             // Kt rows (stage 2 reads them as rows, the state update through the transposed read)
-            chunk_float(cur.k, x, tg, nv);
+            chunk_float<CK>(cur.k, x, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -220,7 +221,7 @@ struct OutStep {
                 lds_put_row<NS, DL>(sKT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
             // V rows: tokens 4*tg + j, this wave's columns 4*row .. 4*row+3
-            lds_put_v_rows<TIn, NX>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
+            lds_put_v_rows<TIn, NX, CK>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
         }
         // The next chunk's loads go out now and fly during stages 2-3, except at (128, 128),
         // where their registers would push the wave past 256 VGPRs: there they go out after stage 3.
@@ -352,7 +353,7 @@ struct OutStep {
 // Outputs of one segment from its carried-in state S (K3).
 template <typename TIn, typename TG, int DK, int DV, bool CK>
 __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
-    using St = OutStep<TIn, TG, DK, DV>;
+    using St = OutStep<TIn, TG, DK, DV, CK>;
     constexpr int DL = St::DL;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<true, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
@@ -384,7 +385,7 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
 // L tile db holds L[16*db + 4*g4 + i][16*w + r16]; Gseg[i] = summed log-decay of key dim
 // d0 + DL*row + i of the segment.
 // ---------------------------------------------------------------------------------------
-template <typename TIn, typename TG, int DK, int DV>
+template <typename TIn, typename TG, int DK, int DV, bool CK>
 struct StateStep {
     using L = Lay<TIn, DK, DV, false>;
     using PR = Prec<TIn>;
@@ -401,7 +402,7 @@ struct StateStep {
         char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
         {
             float G[4][DL], GC[DL], x[4][DL];
-            chunk_float(cur.g, x, tg, nv);
+            chunk_float<CK>(cur.g, x, tg, nv);
             const bool tail_chunk = (a.flags & 1) && (tc + nv == wk.len);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -411,7 +412,7 @@ struct StateStep {
             }
             float X[4][DL];
             chunk_suffix<DL>(G, X, GC, lane);
-            chunk_float(cur.k, x, tg, nv);
+            chunk_float<CK>(cur.k, x, tg, nv);
             float gs[DL];  // Gseg log2(e)
 #pragma unroll
             for (int i = 0; i < DL; ++i) gs[i] = Gseg[i] * LOG2E;
@@ -423,7 +424,7 @@ struct StateStep {
             }
 #pragma unroll
             for (int i = 0; i < DL; ++i) Gseg[i] += GC[i];
-            lds_put_v_rows<TIn, NX>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
+            lds_put_v_rows<TIn, NX, CK>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
         }
         after_inputs();
         __syncthreads();
@@ -444,7 +445,7 @@ struct StateStep {
 template <typename TIn, typename TG, int DK, int DV, bool CK>
 __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&Lst)[DK / 16],
                                    float (&Gseg)[DK / (DV / 16) / 4], char* smem) {
-    using St = StateStep<TIn, TG, DK, DV>;
+    using St = StateStep<TIn, TG, DK, DV, CK>;
     constexpr int DL = St::DL;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<false, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
