@@ -120,7 +120,8 @@ struct BLayS {
     static_assert(BYTES <= 80 * 1024, "two workgroups per CU");
 };
 
-template <typename TIn, typename TG, int D>
+// CK: checked row addressing; without it the loads zero rows past the chunk (see chunk_load).
+template <typename TIn, typename TG, int D, bool CK>
 struct BwdStateStep {
     using L = BLayS<TIn, D>;
     static constexpr int NS = L::NS, NX = L::NX, NDB = D / 16, DL = 4;
@@ -139,7 +140,7 @@ struct BwdStateStep {
         float* sEG = reinterpret_cast<float*>(smem + L::OFF_EG);
         {
             float G[4][DL], X[4][DL], GC[DL], x[4][DL];
-            chunk_float(cur.c.g, x, tg, nv);
+            chunk_float<CK>(cur.c.g, x, tg, nv);
             const bool tail_chunk = (a.f.flags & 1) && (tc + nv == wk.len);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -149,14 +150,14 @@ struct BwdStateStep {
             }
             chunk_suffix<DL>(G, X, GC, lane);  // X: decay after each token, within the chunk
             chunk_cumsum<DL>(G, GC, lane);     // G: decay from the chunk start, inclusive
-            chunk_float(cur.c.k, x, tg, nv);
+            chunk_float<CK>(cur.c.k, x, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
                 for (int i = 0; i < DL; ++i) x[j][i] *= fast_exp(X[j][i]);
                 lds_put_row<NS, DL>(sKW, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
             }
-            chunk_float(cur.c.q, x, tg, nv);
+            chunk_float<CK>(cur.c.q, x, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -170,10 +171,10 @@ struct BwdStateStep {
                 for (int i = 0; i < DL; ++i) sEG[dl0 + i] = fast_exp(GC[i]);
             }
             float vx[4][4];
-            chunk_float(cur.c.v, vx, tg, nv);
+            chunk_float<CK>(cur.c.v, vx, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
-            chunk_float(cur.d, vx, tg, nv);
+            chunk_float<CK>(cur.d, vx, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sDP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
@@ -209,7 +210,7 @@ struct BwdStateStep {
 // CK: checked row addressing (T is not a multiple of 4; see chunk_load).
 template <typename TIn, typename TG, int D, bool CK>
 __global__ __launch_bounds__(D * 4, 2) void gla_bwd_state_kernel(BwdParams a) {
-    using St = BwdStateStep<TIn, TG, D>;
+    using St = BwdStateStep<TIn, TG, D, CK>;
     using L = typename St::L;
     constexpr int NDB = D / 16, DL = 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
@@ -360,7 +361,7 @@ __device__ void bwd_tokenwise(const BwdParams& a, const Work& wk, int64_t h, int
     for (int db = 0; db < NDB; ++db) dH[db] = Dm[db];
 }
 
-template <typename TIn, typename TG, int D>
+template <typename TIn, typename TG, int D, bool CK>
 struct BwdStep {
     using L = BLay<TIn, D>;
     static constexpr int NS = L::NS, NX = L::NX, NW = L::NW, NDB = D / 16, NKS = D / 32, DL = 4;
@@ -441,7 +442,7 @@ struct BwdStep {
         uint32_t pass = 0;  // bit 4*j + i: token 4*tg + j, dim dl0 + i passes its gate gradient
         {
             float G[4][DL], GC[DL];
-            chunk_float(cur.c.g, G, tg, nv);
+            chunk_float<CK>(cur.c.g, G, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const bool unclamped = tail_chunk && (4 * tg + j == nv - 1);
@@ -470,8 +471,8 @@ struct BwdStep {
             }
             const bool any_bad = __any(bad);
             if (lane == 0) sFLAG[wave] = any_bad ? 1 : 0;
-            chunk_float(cur.c.q, qx, tg, nv);
-            chunk_float(cur.c.k, kx, tg, nv);
+            chunk_float<CK>(cur.c.q, qx, tg, nv);
+            chunk_float<CK>(cur.c.k, kx, tg, nv);
             float x[DL];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -483,10 +484,10 @@ struct BwdStep {
                 lds_put_row<NS, DL>(sKT, L::ROWP, (4 * tg + j) * L::RS + dl0, x);
             }
             float vx[4][4];
-            chunk_float(cur.c.v, vx, tg, nv);
+            chunk_float<CK>(cur.c.v, vx, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sV, L::ROWP, (4 * tg + j) * L::RS + c0 + 4 * row, vx[j]);
-            chunk_float(cur.d, vx, tg, nv);
+            chunk_float<CK>(cur.d, vx, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sDO, L::ROWP, (4 * tg + j) * L::RS + c0 + 4 * row, vx[j]);
         }
@@ -664,7 +665,7 @@ struct BwdStep {
 
 template <typename TIn, typename TG, int D, bool CK>
 __global__ __launch_bounds__(D * 4, 1) void gla_bwd_chunk_kernel(BwdParams a) {
-    using St = BwdStep<TIn, TG, D>;
+    using St = BwdStep<TIn, TG, D, CK>;
     using L = typename St::L;
     constexpr int NDB = D / 16, DL = 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
