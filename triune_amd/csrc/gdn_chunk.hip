@@ -152,20 +152,21 @@ struct GChunkIn {
     Vec<float, 4> bk[4];
 };
 
-template <bool OUT, typename TIn, typename TG>
+template <bool OUT, bool CK, typename TIn, typename TG>
 __device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG>& c, const ChunkAddr& ad, const TokAddr& kb, bool key_beta,
                                             int64_t tc, bool valid) {
-    chunk_load<OUT>(c.x, ad, tc, valid);
+    chunk_load<OUT, CK>(c.x, ad, tc, valid);
     if (key_beta) {
         const __amdgpu_buffer_rsrc_t r = chunk_rsrc(kb, tc, valid);
-        rows_load(c.bk, r, kb, tc);
+        rows_load<CK>(c.bk, r, kb, tc);
     }
 }
 
 // One chunk of the GDN walk for (segment, head).  OUT: outputs from the state S (K3).  Otherwise
 // (K1) the segment map on two states at once: S driven with V = 0 (the M columns) and SN with
 // the real V (the N columns); stages 1-2 (factors, tiles, inverses) are shared by both.
-template <typename TIn, typename TG, bool OUT>
+// CK: checked row addressing; without it the loads zero rows past the chunk (see chunk_load).
+template <typename TIn, typename TG, bool OUT, bool CK>
 struct GdnStep {
     using L = GLay<TIn, OUT>;
     using PR = Prec<TIn>;
@@ -193,7 +194,7 @@ struct GdnStep {
         // ---------------- stage 1: factors and split operands -> LDS ------------------------
         {
             float G[4][DL], Gc[4][DL], GC[DL], x[4][DL];
-            chunk_float(cur.x.g, G, tg, nv);
+            chunk_float<CK>(cur.x.g, G, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -221,7 +222,7 @@ struct GdnStep {
             const bool any_bad = __any(bad);
             if (lane == 0) sFLAG[wave] = any_bad ? 1 : 0;
             if (OUT) {
-                chunk_float(cur.x.q, x, tg, nv);
+                chunk_float<CK>(cur.x.q, x, tg, nv);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -230,7 +231,7 @@ struct GdnStep {
                 }
             }
             float kx[4][DL];
-            chunk_float(cur.x.k, kx, tg, nv);
+            chunk_float<CK>(cur.x.k, kx, tg, nv);
             // Bt = k exp(Gp - m)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -252,7 +253,7 @@ struct GdnStep {
             }
             float bkx[4][DL];
             if (a.beta_kind == BETA_KEY) {
-                chunk_float(cur.bk, bkx, tg, nv);
+                chunk_float<CK>(cur.bk, bkx, tg, nv);
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -267,7 +268,7 @@ struct GdnStep {
             }
             // V rows of this wave's columns
             float vx[4][4];
-            chunk_float(cur.x.v, vx, tg, nv);
+            chunk_float<CK>(cur.x.v, vx, tg, nv);
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
@@ -489,10 +490,10 @@ struct GdnStep {
     }
 };
 
-template <typename TIn, typename TG, bool OUT>
+template <typename TIn, typename TG, bool OUT, bool CK>
 __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[4], f32x4 (&SN)[4],
                          char* smem) {
-    using St = GdnStep<TIn, TG, OUT>;
+    using St = GdnStep<TIn, TG, OUT, CK>;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<OUT, TIn, TG>(a, wk, h, tg, wave * 16 + 4 * row, wave * 16 + 4 * row);
     const bool key_beta = a.beta_kind == BETA_KEY;
@@ -505,15 +506,15 @@ __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     GChunkIn<TIn, TG> A;
-    gchunk_load<OUT>(A, ad, kb, key_beta, tok(0), true);
+    gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(0), true);
     for (int64_t c = 0; c < nch; ++c)
         St::run(a, wk, h, tok(c), chunk_nv(c), A, S, SN, smem,
-                [&] { gchunk_load<OUT>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch); });
+                [&] { gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch); });
 }
 
 // K1: the segment map driven from [I | 0] with V = 0 (-> M_p, state M) and from 0 with the real
 // V (-> N_p, state N) in one chunk walk.
-template <typename TIn, typename TG>
+template <typename TIn, typename TG, bool CK>
 __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel(PrefillParams a) {
     using L = GLay<TIn, false>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
@@ -529,7 +530,7 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel
             M[db][i] = (16 * db + 4 * g4 + i == 16 * wave + r16) ? 1.f : 0.f;
             N[db][i] = 0.f;
         }
-    gdn_walk<TIn, TG, false>(a, wk, h, M, N, smem);
+    gdn_walk<TIn, TG, false, CK>(a, wk, h, M, N, smem);
     // M goes out already split into NS bf16 parts (the scan's MFMA operands): NS planes of
     // [64][64] row-major per (segment, head), slot stride MSLOT elements
     // M[16db + 4g4 + i][16w + r16] is element j = 4(w&1) + (r16&3) of scan lane
@@ -556,7 +557,7 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel
 
 // K3: outputs of one segment from S_in[p] (in the N slot after the scan).  Two workgroups per CU
 // where two fit in LDS (bf16 I/O); fp16 and fp32 I/O hold larger planes and run one.
-template <typename TIn, typename TG>
+template <typename TIn, typename TG, bool CK>
 __global__ __launch_bounds__(256, ((2 * GLay<TIn, true>::BYTES <= 160 * 1024) ? 2 : 1)) void gdn_seg_out_kernel(PrefillParams a) {
     using L = GLay<TIn, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
@@ -568,7 +569,7 @@ __global__ __launch_bounds__(256, ((2 * GLay<TIn, true>::BYTES <= 160 * 1024) ? 
     const float* st = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
 #pragma unroll
     for (int db = 0; db < 4; ++db) S[db] = *reinterpret_cast<const f32x4*>(st + dstate_off(wave, db, lane));
-    gdn_walk<TIn, TG, true>(a, wk, h, S, S, smem);
+    gdn_walk<TIn, TG, true, CK>(a, wk, h, S, S, smem);
 }
 
 // K2: one wave per (sequence, head, 16 state columns): S_in[p] = carry (written in place of N_p),
@@ -662,14 +663,21 @@ __global__ __launch_bounds__(64) void gdn_seg_scan_kernel(PrefillParams a, float
 // ---------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------
-template <typename TIn, typename TG>
-static hipError_t launch_gdn_t(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
+template <typename TIn, typename TG, bool CK>
+static hipError_t launch_gdn_ck(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
     if (which == 0) {
-        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG, CK>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG, CK>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
     }
     return hipGetLastError();
+}
+
+// Unchecked row addressing only when T is a whole number of four-row groups.
+template <typename TIn, typename TG>
+static hipError_t launch_gdn_t(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
+    if (a.T % 4 == 0) return launch_gdn_ck<TIn, TG, false>(a, n_work, which, stream);
+    return launch_gdn_ck<TIn, TG, true>(a, n_work, which, stream);
 }
 
 static hipError_t launch_gdn(const PrefillParams& a, int64_t n_work, int io_dt, int which, hipStream_t stream) {
@@ -704,9 +712,9 @@ hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt
 // Resident output-kernel workgroups per CU for I/O dtype io_dt (the gate dtype does not change
 // the kernel's LDS or register use).
 int gdn_seg_out_blocks_per_cu(int io_dt) {
-    const void* k = io_dt == DT_F16   ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16>)
-                    : io_dt == DT_F32 ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float>)
-                                      : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16>);
+    const void* k = io_dt == DT_F16   ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, true>)
+                    : io_dt == DT_F32 ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, true>)
+                                      : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, true>);
     int nb = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0);
     return (e == hipSuccess && nb > 0) ? nb : 1;
