@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define TRIUNE_HIP_ABI_VERSION 1
+#define TRIUNE_HIP_ABI_VERSION 2
 
 enum {
     TRIUNE_DT_F32 = 0,
@@ -97,13 +97,32 @@ int triune_hip_set_output_kernel_events(void* begin, void* end);
  * q, k, g: [B, 1, H, Dk] (g may be fp32 when q/k/v are 16-bit: g_dtype), v: [B, 1, H, Dv],
  * o: [B, 1, H, Dv] in o_dtype.  strides[10] = (batch, head) element strides of q, k, v, g, o.
  * state_in / state_out: fp32 [n_state_rows, H, Dk, Dv]; they may be the same buffer (in place).
- * slots: NULL (state row b for batch b) or int32 [B] state-row indices (a state pool).
+ * slots: NULL (state row b for batch b; n_state_rows >= B) or int32 [B] state-row indices (a
+ * state pool); a batch row whose slot lies outside [0, n_state_rows) (e.g. -1 for a padded row)
+ * reads and writes no state and gets zero outputs.
  * Supported (Dk, Dv): (32,32), (64,64), (128,128), (64,128), (128,64).
  * Replaces: triune_gla_recurrent_step_f32 (api.h:94-103), launch_gla_decode_step (gla.cu:97-114). */
 int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, const void* g, int io_dtype,
                                int g_dtype, const int64_t* strides, const float* state_in, float* state_out,
-                               const int32_t* slots, void* o, int o_dtype, int64_t B, int64_t H, int Dk, int Dv,
-                               void* stream);
+                               const int32_t* slots, int64_t n_state_rows, void* o, int o_dtype, int64_t B,
+                               int64_t H, int Dk, int Dv, void* stream);
+
+/* The reference's own decode-step signatures, for callers that bind them by name (device
+ * pointers instead of the reference's host pointers; both run triune_hip_gla_decode_step in
+ * place and return nothing, as the reference's do; the status of the last such call on this
+ * host thread is triune_hip_last_error()).
+ *   launch_gla_decode_step: bf16 Q, K, V, Out [B, 1, H, HD] and fp32 G [B, 1, H, HD], fp32
+ *     State [B, H, HD, HD] updated in place, all contiguous, on `stream` (a hipStream_t);
+ *     HD in {32, 64, 128}.  Replaces: launch_gla_decode_step, csrc/kernels/gla.cu:97-114.
+ *   triune_gla_recurrent_step_f32: fp32 q, k, v, g, out [batch_heads, head_dim] and state
+ *     [batch_heads, head_dim, head_dim] updated in place, on the null stream; head_dim in {32, 64,
+ *     128}.  Replaces: triune_gla_recurrent_step_f32, csrc/engine/api.h:94-103 (engine.cpp:419-475),
+ *     bound by triune/ops/_c_bridge.py:132-142. */
+int triune_hip_last_error(void);
+void launch_gla_decode_step(const void* Q, const void* K, const void* V, const float* G, float* State, void* Out,
+                            int B, int H, int HD, void* stream);
+void triune_gla_recurrent_step_f32(const float* q, const float* k, const float* v, const float* g, float* state,
+                                   float* out, int batch_heads, int head_dim);
 
 /* Chunked GLA prefill over dense [B, T, H, D] tensors:
  *     S_t = diag(exp(min(g_t, 0))) S_{t-1} + k_t v_t^T ;   o_t = S_t^T q_t ,   S_{-1} = s0 (or 0)

@@ -16,9 +16,15 @@ import triune_amd._lib as L
 HEADER = Path(__file__).resolve().parents[1] / "include" / "triune_hip.h"
 
 
+# entry points declared under the reference's own names (device twins of its decode step)
+REFERENCE_NAMED = ("launch_gla_decode_step", "triune_gla_recurrent_step_f32")
+
+
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"\b(triune_hip_\w+)\s*\(", text)))
+    names = set(re.findall(r"\b(triune_hip_\w+)\s*\(", text))
+    names |= {n for n in REFERENCE_NAMED if re.search(r"\bvoid\s+" + n + r"\s*\(", text)}
+    return sorted(names)
 
 
 def test_library_exports_every_declared_entry_point():
@@ -84,19 +90,38 @@ def test_prefill_validation_errors():
     assert call(H=0) == -2
     assert call(st=(ctypes.c_int64 * 15)(*([63] * 15))) == -4  # rows not 16-byte aligned
     assert call(q=ctypes.c_void_p(0x1002)) == -4
+    # token rows closer than a row width (a tensor broadcast along tokens) are refused
+    assert call(st=(ctypes.c_int64 * 15)(*([4096, 0, 64] * 5))) == -4
+    assert call(st=(ctypes.c_int64 * 15)(*([4096, 32, 64] * 5))) == -4
     assert call(ws=None, wsb=0) == -5  # workspace required once T > 0
 
 
 def test_decode_and_gdn_and_scan_validation_errors():
     lib = L.lib()
     d = lib.triune_hip_gla_decode_step
-    assert d(None, _FAKE, _FAKE, _FAKE, 1, 1, _st(10), _FAKE, _FAKE, None, _FAKE, 1, 1, 1, 64, 64, None) == -1
-    assert d(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _st(10), _FAKE, _FAKE, None, _FAKE, 1, 1, 1, 64, 32, None) == -2
-    assert d(_FAKE, _FAKE, _FAKE, _FAKE, 5, 1, _st(10), _FAKE, _FAKE, None, _FAKE, 1, 1, 1, 64, 64, None) == -3
+    assert d(None, _FAKE, _FAKE, _FAKE, 1, 1, _st(10), _FAKE, _FAKE, None, 1, _FAKE, 1, 1, 1, 64, 64, None) == -1
+    assert d(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _st(10), _FAKE, _FAKE, None, 1, _FAKE, 1, 1, 1, 64, 32, None) == -2
+    assert d(_FAKE, _FAKE, _FAKE, _FAKE, 5, 1, _st(10), _FAKE, _FAKE, None, 1, _FAKE, 1, 1, 1, 64, 64, None) == -3
+    # without slots the state must hold a row per batch entry
+    assert d(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _st(10), _FAKE, _FAKE, None, 1, _FAKE, 1, 2, 1, 64, 64, None) == -2
+    # the reference-signature twins report through triune_hip_last_error and launch nothing on bad sizes
+    lib.launch_gla_decode_step(_FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 1, 1, 48, None)
+    assert lib.triune_hip_last_error() == -2
+    lib.triune_gla_recurrent_step_f32(None, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 1, 64)
+    assert lib.triune_hip_last_error() == -1
     gdn = lib.triune_hip_gdn_prefill
     assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 1, _st(18), None, _FAKE, 1, None, 1, 8, 1, 64, 64, None) == -1
     assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 9, _st(18), None, _FAKE, 1, None, 1, 8, 1, 64, 64, None) == -2
     assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, _st(18), None, _FAKE, 1, None, 1, 8, 1, 48, 48, None) == -2
+    # chunked GDN: beta's strides (12..14, zero without beta) are not mistaken for o's (15..17);
+    # valid arguments without a workspace fail on the workspace, not on the layout
+    gc = lib.triune_hip_gdn_prefill_chunked
+    gst = (ctypes.c_int64 * 18)(*([64 * 64, 64, 64] * 4 + [0, 0, 0] + [64 * 64, 64, 64]))
+    assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, gst, None, _FAKE, 1, None, 1, 64, 1, 64, 64, None, 0,
+              None) == -5
+    gst[16] = 32  # o's token stride below the row width
+    assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, gst, None, _FAKE, 1, None, 1, 64, 1, 64, 64, None, 0,
+              None) == -4
     sc = lib.triune_hip_recurrent_scan_fwd
     assert sc(None, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -1
     assert sc(_FAKE, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 6, None) == -2

@@ -111,3 +111,90 @@ def test_decode_graph_replay_matches_eager(dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(state, eager)
+
+
+def test_decode_slots_out_of_place_keeps_other_rows(dev):
+    """slots with inplace=False: the returned pool holds the updated rows at the slots and the
+    input values everywhere else; the input pool is not modified."""
+    B, H, D = 8, 2, 64
+    q, k, v, g, _ = config2(steps=1, B=B, H=H, D=D)
+    gen = torch.Generator().manual_seed(12)
+    pool = torch.randn(20, H, D, D, generator=gen)
+    slots = torch.randperm(20, generator=gen)[:B].to(torch.int32)
+    pool_d = pool.to(dev)
+    o, st = gla_decode_step(q[0].to(dev), k[0].to(dev), v[0].to(dev), g[0].to(dev), pool_d, slots=slots.to(dev),
+                            out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert st.data_ptr() != pool_d.data_ptr() and torch.equal(pool_d.cpu(), pool)
+    ro, rs = O.gla_decode_step(q[0][:, 0], k[0][:, 0], v[0][:, 0], g[0][:, 0], pool[slots.long()].double().numpy())
+    got = st.cpu()
+    assert _maxerr(got[slots.long()], rs) <= 1e-5
+    untouched = torch.ones(20, dtype=torch.bool)
+    untouched[slots.long()] = False
+    assert torch.equal(got[untouched], pool[untouched])
+    assert _maxerr(o[:, 0].cpu(), ro) <= 1e-5 * max(1.0, float(np.abs(ro).max()))
+
+
+def test_decode_padded_slot_rows_are_skipped(dev):
+    """A batch row whose slot is -1 or past the pool (a padded row of a continuous batch) reads and
+    writes no state and outputs zeros; the other rows are unaffected."""
+    B, H, D = 6, 2, 64
+    q, k, v, g, _ = config2(steps=1, B=B, H=H, D=D)
+    gen = torch.Generator().manual_seed(13)
+    pool = torch.randn(10, H, D, D, generator=gen)
+    slots = torch.tensor([4, -1, 7, 10, 0, -5], dtype=torch.int32)
+    pool_d = pool.to(dev)
+    o, _ = gla_decode_step(q[0].to(dev), k[0].to(dev), v[0].to(dev), g[0].to(dev), pool_d, inplace=True,
+                           slots=slots.to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    live = torch.tensor([0, 2, 4])
+    rows = slots[live].long()
+    ro, rs = O.gla_decode_step(q[0][live, 0], k[0][live, 0], v[0][live, 0], g[0][live, 0], pool[rows].double().numpy())
+    got = pool_d.cpu()
+    assert _maxerr(got[rows], rs) <= 1e-5
+    untouched = torch.ones(10, dtype=torch.bool)
+    untouched[rows] = False
+    assert torch.equal(got[untouched], pool[untouched])
+    oc = o[:, 0].cpu()
+    assert _maxerr(oc[live], ro) <= 1e-5 * max(1.0, float(np.abs(ro).max()))
+    assert float(oc[torch.tensor([1, 3, 5])].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("HD", [32, 64, 128])
+def test_reference_signature_twins(dev, HD):
+    """launch_gla_decode_step (gla.cu:97-114: bf16 Q/K/V/Out, fp32 G, fp32 State in place) and
+    triune_gla_recurrent_step_f32 (api.h:94-103: fp32, [batch_heads, head_dim]) on device pointers,
+    bound by name the way the reference's ctypes bridge binds its library."""
+    from triune_amd._lib import lib
+
+    L = lib()
+    B, H = 5, 3
+    q, k, v, g, s0 = config2(steps=1, B=B, H=H, D=HD)
+    gf = g[0].float()
+    Q, K, V = (x[0].to(dev).contiguous() for x in (q, k, v))
+    G = gf.to(dev).contiguous()
+    S = s0.to(dev).contiguous()
+    Out = torch.empty(B, 1, H, HD, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream().cuda_stream
+    L.launch_gla_decode_step(Q.data_ptr(), K.data_ptr(), V.data_ptr(), G.data_ptr(), S.data_ptr(), Out.data_ptr(),
+                             B, H, HD, stream)
+    assert L.triune_hip_last_error() == 0
+    torch.cuda.synchronize()
+    ro, rs = O.gla_decode_step(q[0][:, 0], k[0][:, 0], v[0][:, 0], gf[:, 0], s0)
+    assert _maxerr(S.cpu(), rs) <= 1e-5
+    ref = torch.from_numpy(ro).float()
+    assert float((Out[:, 0].float().cpu() - ref).abs().max()) <= float(ref.abs().max()) * 2**-8
+
+    bh = B * H
+    f32 = lambda x: x[0][:, 0].float().reshape(bh, HD).to(dev).contiguous()  # noqa: E731
+    q3, k3, v3, g3 = f32(q), f32(k), f32(v), f32(g)
+    S3 = s0.reshape(bh, HD, HD).to(dev).contiguous()
+    o3 = torch.empty(bh, HD, device=dev)
+    torch.cuda.synchronize()
+    L.triune_gla_recurrent_step_f32(q3.data_ptr(), k3.data_ptr(), v3.data_ptr(), g3.data_ptr(), S3.data_ptr(),
+                                    o3.data_ptr(), bh, HD)
+    assert L.triune_hip_last_error() == 0
+    torch.cuda.synchronize()
+    ro3, rs3 = O.gla_decode_step(q3.cpu(), k3.cpu(), v3.cpu(), g3.cpu(), s0.reshape(bh, HD, HD))
+    assert _maxerr(S3.cpu(), rs3) <= 1e-5
+    assert _maxerr(o3.cpu(), ro3) <= 1e-5 * max(1.0, float(np.abs(ro3).max()))

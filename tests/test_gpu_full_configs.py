@@ -1,0 +1,127 @@
+"""GPU parity at the full BASELINE sizes (configs 1-4; config 0 is covered in full by
+test_gpu_gla_prefill.py) against the fp64 oracle on the same seeded, already-rounded inputs.
+
+Tolerances (the north star's protocol): 16-bit I/O with fp32 accumulation -> max-abs 2e-3 on
+fp32 outputs and fp32 states; bf16 outputs within one bf16 ULP of the oracle plus 2e-3 per
+element.  These sizes exercise what the reduced-size tests cannot: large offsets (config 4's
+packed rows pass 2^31 bytes of q/k/v/g together), the full segment plans (config 1: 20 segments
+of 12-13 chunks per sequence; config 4: 32 ragged sequences), and 512 chained decode steps.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from triune_amd import fast_chunk_gated_deltanet, fast_chunk_gla, fast_chunk_gla_varlen
+from triune_amd.serving import GLADecodeGraphRunner
+from triune_amd.workloads import config1, config2, config3, config4, ulp_bf16
+
+pytestmark = pytest.mark.gpu
+
+TOL16 = 2e-3
+
+
+def _max_err(a, ref):
+    return float((a.double() - ref).abs().max())
+
+
+def _bf16_excess(o_bf16, ref):
+    """max over elements of |o - ref| - (1 bf16 ULP of ref + 2e-3); <= 0 passes."""
+    return float(((o_bf16.double() - ref).abs() - (ulp_bf16(ref).double() + TOL16)).max())
+
+
+def test_config1_full_prefill(dev):
+    """B=4, H=6, T=16384, D=64, bf16 I/O, fp32 S0: fp32-output mode and bf16 outputs."""
+    q, k, v, g, s0 = config1()
+    ro, rs = O.gla_fwd(q, k, v, g, s0)
+    ro, rs = torch.from_numpy(ro), torch.from_numpy(rs)
+    qd, kd, vd, gd, sd = (x.to(dev) for x in (q, k, v, g, s0))
+    o32, s32 = fast_chunk_gla(qd, kd, vd, gd, initial_state=sd, out=torch.empty(v.shape, device=dev))
+    torch.cuda.synchronize()
+    e_o, e_s = _max_err(o32.cpu(), ro), _max_err(s32.cpu(), rs)
+    print(f"config1 fp32-out: o {e_o:.3e} S {e_s:.3e}", flush=True)
+    assert e_o <= TOL16 and e_s <= TOL16
+    del o32
+    ob, sb = fast_chunk_gla(qd, kd, vd, gd, initial_state=sd)
+    torch.cuda.synchronize()
+    assert ob.dtype == torch.bfloat16
+    ex = _bf16_excess(ob.cpu(), ro)
+    print(f"config1 bf16-out: excess over 1 ULP + 2e-3 {ex:.3e}", flush=True)
+    assert ex <= 0.0
+    assert _max_err(sb.cpu(), rs) <= TOL16
+
+
+def test_config2_full_decode_graph_runner(dev):
+    """B=256, H=6, D=64, 512 steps through GLADecodeGraphRunner (64 steps per graph, 8 replays
+    over a device state pool): outputs of every step and the pool state after every replay
+    against the oracle's token recurrence (the decode step does not clamp g)."""
+    steps, per = 512, 64
+    q, k, v, g, s0 = config2(steps=steps)
+    B, H, D = 256, 6, 64
+    pool = torch.zeros(B + 7, H, D, D, device=dev)  # a pool larger than the batch
+    slots = torch.arange(3, 3 + B, dtype=torch.int32, device=dev).flip(0)
+    sl = slots.cpu().long()
+    pool[sl] = s0.to(dev)
+    runner = GLADecodeGraphRunner(pool, slots, steps=per, dtype=torch.bfloat16)
+    ref_state = s0.double()
+    tok = lambda x, a, b: x[a:b, :, 0].permute(1, 0, 2, 3)  # noqa: E731  [steps, B, 1, H, D] -> [B, T, H, D]
+    for r in range(steps // per):
+        a, b = r * per, (r + 1) * per
+        for dst, src in ((runner.q, q), (runner.k, k), (runner.v, v), (runner.g, g)):
+            dst.copy_(src[a:b, :, 0].to(dev))
+        o = runner.replay()
+        torch.cuda.synchronize()
+        ro, rs = O.gla_fwd(tok(q, a, b), tok(k, a, b), tok(v, a, b), tok(g, a, b), ref_state, clamp_mode=0)
+        ref_state = torch.from_numpy(rs)
+        ref_o = torch.from_numpy(ro).permute(1, 0, 2, 3)  # [steps, B, H, D]
+        ex = _bf16_excess(o.cpu(), ref_o)
+        e_s = _max_err(pool[sl].cpu(), ref_state)
+        print(f"config2 replay {r}: o excess {ex:.3e}, state {e_s:.3e}", flush=True)
+        assert ex <= 0.0 and e_s <= TOL16
+    untouched = torch.ones(B + 7, dtype=torch.bool)
+    untouched[sl] = False
+    assert float(pool[untouched.to(dev)].abs().max()) == 0.0
+    runner.release()
+
+
+def test_config3_full_gdn(dev):
+    """Gated DeltaNet, B=4, H=6, T=8192, D=64, bf16, per-head beta and decay, zero S0."""
+    q, k, v, g, beta = config3()
+    ro, rs = O.gdn_fwd(q, k, v, g, beta, None)
+    ro, rs = torch.from_numpy(ro), torch.from_numpy(rs)
+    args = [x.to(dev) for x in (q, k, v, g)]
+    bd = beta.to(dev)
+    o32, s32 = fast_chunk_gated_deltanet(*args, beta=bd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    e_o, e_s = _max_err(o32.cpu(), ro), _max_err(s32.cpu(), rs)
+    print(f"config3 fp32-out: o {e_o:.3e} S {e_s:.3e}", flush=True)
+    assert e_o <= TOL16 and e_s <= TOL16
+    ob, sb = fast_chunk_gated_deltanet(*args, beta=bd)
+    torch.cuda.synchronize()
+    assert ob.dtype == torch.bfloat16
+    ex = _bf16_excess(ob.cpu(), ro)
+    print(f"config3 bf16-out: excess {ex:.3e}", flush=True)
+    assert ex <= 0.0 and _max_err(sb.cpu(), rs) <= TOL16
+
+
+def test_config4_full_varlen(dev):
+    """32 packed sequences of 128..8192 tokens, H=12, D=128, bf16, per-sequence fp32 S0."""
+    q, k, v, g, cu, s0 = config4()
+    ro, rs = O.gla_varlen_fwd(q[0], k[0], v[0], g[0], cu.numpy(), s0)
+    ro, rs = torch.from_numpy(ro), torch.from_numpy(rs)
+    qd, kd, vd, gd = (x.to(dev) for x in (q, k, v, g))
+    del q, k, g
+    out = torch.empty(v.shape, device=dev, dtype=torch.float32)
+    o32, s32 = fast_chunk_gla_varlen(qd, kd, vd, gd, cu.to(dev), initial_state=s0.to(dev), out=out)
+    torch.cuda.synchronize()
+    e_o, e_s = _max_err(o32[0].cpu(), ro), _max_err(s32.cpu(), rs)
+    print(f"config4 fp32-out: o {e_o:.3e} S {e_s:.3e}", flush=True)
+    assert e_o <= TOL16 and e_s <= TOL16
+    del o32, out
+    ob, sb = fast_chunk_gla_varlen(qd, kd, vd, gd, cu.to(dev), initial_state=s0.to(dev))
+    torch.cuda.synchronize()
+    ex = _bf16_excess(ob[0].cpu(), ro)
+    print(f"config4 bf16-out: excess {ex:.3e}", flush=True)
+    assert ex <= 0.0 and _max_err(sb.cpu(), rs) <= TOL16
+    assert np.asarray(cu)[-1] == v.shape[1]

@@ -54,20 +54,22 @@ def test_pool_prefill_then_decode_matches_oracle(dev):
     gen = torch.Generator().manual_seed(12)
     steps = [[torch.randn(3, H, D, generator=gen) for _ in range(4)] for _ in range(5)]
     for x in steps:
+        x[0] = x[0] * D**-0.5  # config magnitudes: q scaled by D^-1/2
         x[3] = torch.nn.functional.logsigmoid(x[3]) / 8
     outs = [pool.decode_step(1, *(t.to(dev) for t in x), slots) for x in steps]
     torch.cuda.synchronize()
-    assert [pool.offsets[1][s] for s in slots.tolist()] == [n + 5 for n in lens]
+    assert pool.offsets[1][slots.long()].tolist() == [n + 5 for n in lens]
     assert float(pool.states[0].abs().sum()) == 0.0  # other layer untouched
     c = cu.tolist()
     for i in range(3):
         cat = [torch.cat([x[0, c[i]:c[i + 1]], torch.stack([st[j][i] for st in steps])])[None] for j, x in
                enumerate((q, k, v, g))]
         ro, rs = O.gla_fwd(*cat, None, clamp_mode=1)
-        assert float(np.abs(o_pre[0, c[i]:c[i + 1]].cpu().numpy() - ro[0, :lens[i]]).max()) <= 1e-4
-        for t in range(5):
-            assert float(np.abs(outs[t][i].cpu().numpy() - ro[0, lens[i] + t]).max()) <= 1e-4
-        assert float(np.abs(pool.states[1, slots[i]].cpu().numpy() - rs[0]).max()) <= 1e-4
+        e_pre = float(np.abs(o_pre[0, c[i]:c[i + 1]].cpu().numpy() - ro[0, :lens[i]]).max())
+        e_dec = max(float(np.abs(outs[t][i].cpu().numpy() - ro[0, lens[i] + t]).max()) for t in range(5))
+        e_s = float(np.abs(pool.states[1, slots[i]].cpu().numpy() - rs[0]).max())
+        print(f"session {i}: prefill o {e_pre:.3e}, decode o {e_dec:.3e}, state {e_s:.3e}")
+        assert e_pre <= 1e-5 and e_dec <= 1e-5 and e_s <= 1e-5
 
 
 @pytest.mark.parametrize("steps", [1, 4])
@@ -106,3 +108,60 @@ def test_graph_runner_replays_match_eager(dev, steps):
         torch.cuda.synchronize()
         assert torch.equal(o1, oe[:, 0]) and torch.equal(pool, ref)
     runner.release()
+
+
+def test_pool_prefill_and_decode_captured_in_one_graph(dev):
+    """StateSlotPool.prefill followed by two decode steps, captured in one HIP graph (no host
+    synchronisation inside), replayed three times with fresh inputs written between replays and
+    eager work and syncs in between: every replay's outputs, states and offsets equal the same
+    calls made eagerly on a second pool."""
+    H, D, lens, n_slots = 2, 64, [100, 37, 64], 6
+    pools = [StateSlotPool(num_layers=1, n_slots=n_slots, H=H, Dk=D, Dv=D, device=dev) for _ in range(2)]
+    init = 0.1 * torch.randn(n_slots, H, D, D, generator=torch.Generator().manual_seed(21))
+    for p in pools:
+        p.states[0].copy_(init.to(dev))
+    slots = torch.tensor([4, 0, 2], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32, device=dev)
+    N = int(sum(lens))
+    stat = [torch.zeros(1, N, H, D, device=dev, dtype=torch.bfloat16) for _ in range(4)]
+    dec = [[torch.zeros(3, H, D, device=dev, dtype=torch.bfloat16) for _ in range(4)] for _ in range(2)]
+    outs = [torch.zeros(1, N, H, D, device=dev, dtype=torch.bfloat16)] + [
+        torch.zeros(3, H, D, device=dev, dtype=torch.bfloat16) for _ in range(2)]
+
+    def serve(pool, o):
+        pool.prefill(0, *stat, cu, slots, out=o[0])
+        for t in range(2):
+            pool.decode_step(0, *dec[t], slots, out=o[t + 1])
+
+    scratch = StateSlotPool(num_layers=1, n_slots=n_slots, H=H, Dk=D, Dv=D, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        serve(scratch, [torch.empty_like(x) for x in outs])  # warm-up off the live pools
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        serve(pools[0], outs)
+    torch.cuda.synchronize()
+    assert torch.equal(pools[0].states[0].cpu(), init)  # capture ran nothing
+    gen = torch.Generator().manual_seed(22)
+    for rep in range(3):
+        q, k, v, g, _ = gla_inputs(1, N, H, D, seed=30 + rep, dtype=torch.bfloat16)
+        for dst, src in zip(stat, (q, k, v, g)):
+            dst.copy_(src.to(dev))
+        for t in range(2):
+            xs = [torch.randn(3, H, D, generator=gen) for _ in range(4)]
+            xs[3] = torch.nn.functional.logsigmoid(xs[3]) / 8
+            for dst, src in zip(dec[t], xs):
+                dst.copy_(src.to(dev).bfloat16())
+        graph.replay()
+        eager = [torch.empty_like(x) for x in outs]
+        serve(pools[1], eager)
+        torch.cuda.synchronize()
+        for a, b in zip(outs, eager):
+            assert torch.equal(a, b), rep
+        assert torch.equal(pools[0].states, pools[1].states), rep
+        assert torch.equal(pools[0].offsets, pools[1].offsets), rep
+    assert pools[0].offsets[0][slots.long()].tolist() == [3 * (n + 2) for n in lens]
+    graph.reset()

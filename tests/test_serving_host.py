@@ -68,7 +68,7 @@ def test_pool_session_cache_views_and_updates():
     cache[0][0].add_(1.0)  # the returned states are views of the pool
     assert float(pool.states[0, slot].mean()) == 4.0
     pool.update_session_cache("x", [(cache[0][0], 18)])  # the pool's own row: no copy needed
-    assert float(pool.states[0, slot].mean()) == 4.0 and pool.offsets[0][slot] == 18
+    assert float(pool.states[0, slot].mean()) == 4.0 and int(pool.offsets[0, slot]) == 18
 
 
 def test_pool_ttl_expiry(monkeypatch):

@@ -14,6 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libtriune_hip.so"
+ABI_VERSION = 2
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 FLAG_TAIL_UNCLAMPED = 0x1
@@ -41,9 +42,12 @@ def _bind(lib):
         "triune_hip_error_string": ([_i], ctypes.c_char_p),
         "triune_hip_set_output_kernel_events": ([_vp, _vp], _i),
         "triune_hip_gla_decode_step": (
-            [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _vp, _vp, _i, _i64, _i64, _i, _i, _vp],
+            [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _vp, _i64, _vp, _i, _i64, _i64, _i, _i, _vp],
             _i,
         ),
+        "triune_hip_last_error": ([], _i),
+        "launch_gla_decode_step": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp], None),
+        "triune_gla_recurrent_step_f32": ([_vp, _vp, _vp, _vp, _vp, _vp, _i, _i], None),
         "triune_hip_gla_prefill_workspace_size": ([_i64, _i64, _i64, _i, _i, _i], _sz),
         "triune_hip_gla_prefill": (
             [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _i, _vp, _sz, _vp],
@@ -98,6 +102,9 @@ EXPORTS = (
     "triune_hip_error_string",
     "triune_hip_set_output_kernel_events",
     "triune_hip_gla_decode_step",
+    "triune_hip_last_error",
+    "launch_gla_decode_step",
+    "triune_gla_recurrent_step_f32",
     "triune_hip_gla_prefill_workspace_size",
     "triune_hip_gla_prefill",
     "triune_hip_gla_prefill_varlen_workspace_size",
@@ -124,7 +131,7 @@ def lib():
                 f"{LIB_PATH} is missing: build it with `python -m triune_amd.build` (hipcc, gfx950)"
             )
         _LIB = _bind(ctypes.CDLL(str(LIB_PATH)))
-        if _LIB.triune_hip_abi_version() != 1:
+        if _LIB.triune_hip_abi_version() != ABI_VERSION:
             raise TriuneHipError("libtriune_hip.so ABI version mismatch")
     return _LIB
 

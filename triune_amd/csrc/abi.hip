@@ -35,21 +35,23 @@ bool vec4_ok(const void* p, int dt, const int64_t* st, int n) {
     return true;
 }
 
-// Resident (segment, head) workgroups the device holds at once: CUs x output-kernel occupancy.
-// Queried once per device and cached (host-side runtime queries only; nothing is enqueued).
-int64_t resident_slots(int Dk, int Dv) {
+// Resident (segment, head) workgroups the device holds at once: CUs x output-kernel occupancy
+// of the instance that runs (ck: checked row addressing, used unless every sequence length is a
+// multiple of 4).  Queried once per device and cached (host-side runtime queries only; nothing
+// is enqueued).
+int64_t resident_slots(int Dk, int Dv, bool ck) {
     static std::mutex mu;
-    static std::map<std::tuple<int, int, int>, int64_t> cache;
+    static std::map<std::tuple<int, int, int, bool>, int64_t> cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = -1;
     std::lock_guard<std::mutex> lock(mu);
-    auto key = std::make_tuple(dev, Dk, Dv);
+    auto key = std::make_tuple(dev, Dk, Dv, ck);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
     int ncu = 0;
     if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
         ncu = 256;  // MI355X
-    const int64_t slots = (int64_t)ncu * gla_seg_output_blocks_per_cu(Dk, Dv);
+    const int64_t slots = (int64_t)ncu * gla_seg_output_blocks_per_cu(Dk, Dv, ck);
     cache[key] = slots;
     return slots;
 }
@@ -72,10 +74,10 @@ int device_cus() {
 
 // Segments per sequence (dense): fill the resident workgroup slots once with near-equal
 // segments; never more segments than chunks.  flags bits 8..15 force a chunk count instead.
-int64_t dense_segments(int64_t B, int64_t H, int64_t nchunks, int Dk, int Dv, int flags) {
+int64_t dense_segments(int64_t B, int64_t H, int64_t nchunks, int Dk, int Dv, int flags, bool ck) {
     const int forced = (flags >> TRIUNE_FLAG_SEG_SHIFT) & 0xff;
     if (forced > 0) return (nchunks + forced - 1) / forced;
-    int64_t nseg = resident_slots(Dk, Dv) / (B * H);
+    int64_t nseg = resident_slots(Dk, Dv, ck) / (B * H);
     if (nseg < 1) nseg = 1;
     if (nseg > nchunks) nseg = nchunks;
     return nseg;
@@ -88,7 +90,7 @@ int64_t dense_segments(int64_t B, int64_t H, int64_t nchunks, int Dk, int Dv, in
 int varlen_seg_chunks(int64_t chunk_jobs, int Dk, int Dv, int flags) {
     const int forced = (flags >> TRIUNE_FLAG_SEG_SHIFT) & 0xff;
     if (forced > 0) return forced;
-    const int64_t slots = resident_slots(Dk, Dv) * 8;
+    const int64_t slots = resident_slots(Dk, Dv, true) * 8;  // varlen runs the checked instances
     int64_t p = (chunk_jobs + slots - 1) / slots;
     if (p < 4) p = 4;
     if (p > 255) p = 255;
@@ -98,11 +100,14 @@ int varlen_seg_chunks(int64_t chunk_jobs, int Dk, int Dv, int flags) {
 bool prefill_shape_ok(int Dk, int Dv) { return prefill_shape_supported(Dk, Dv); }
 
 // The prefill kernels address the 64 rows of a chunk as a uniform base plus a 32-bit per-lane
-// byte offset: 64 token strides plus one row must stay below 2^31 bytes.
+// byte offset: 64 token strides plus one row must stay below 2^31 bytes.  Their loads read a
+// (sequence, head) only up to t_end token strides past its first row, which covers every row of
+// the sequence only when rows do not overlap: the token stride must be at least the row width
+// (a tensor broadcast along tokens, stride 0, is copied by the caller).
 bool tok_strides_ok(const int64_t* st3_q, int io_dtype, int g_dtype, int o_dtype, int Dk, int Dv) {
     auto ok = [](int64_t st, int dt, int D) {
         const int64_t es = dt == TRIUNE_DT_F32 ? 4 : 2;
-        return st >= 0 && (64 * st + D) * es < ((int64_t)1 << 31);
+        return st >= D && (64 * st + D) * es < ((int64_t)1 << 31);
     };
     return ok(st3_q[1], io_dtype, Dk) && ok(st3_q[4], io_dtype, Dk) && ok(st3_q[7], io_dtype, Dv) &&
            ok(st3_q[10], g_dtype, Dk) && ok(st3_q[13], o_dtype, Dv);
@@ -119,7 +124,7 @@ struct PrefillPlan {
 PrefillPlan plan_dense(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {
     PrefillPlan p{};
     const int64_t nchunks = (T + 63) / 64;
-    p.nseg = dense_segments(B, H, nchunks, Dk, Dv, flags);
+    p.nseg = dense_segments(B, H, nchunks, Dk, Dv, flags, T % 4 != 0);
     p.P = (int)((nchunks + p.nseg - 1) / p.nseg);
     p.n_work = B * p.nseg;
     p.off_segoff = 0;
@@ -208,11 +213,12 @@ const char* triune_hip_error_string(int code) {
 
 int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, const void* g, int io_dtype,
                                int g_dtype, const int64_t* strides, const float* state_in, float* state_out,
-                               const int32_t* slots, void* o, int o_dtype, int64_t B, int64_t H, int Dk, int Dv,
-                               void* stream) {
+                               const int32_t* slots, int64_t n_state_rows, void* o, int o_dtype, int64_t B,
+                               int64_t H, int Dk, int Dv, void* stream) {
     if (!q || !k || !v || !g || !strides || !state_in || !state_out || !o) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
-    if (B < 0 || H <= 0) return TRIUNE_ERR_SHAPE;
+    if (B < 0 || H <= 0 || n_state_rows < 0) return TRIUNE_ERR_SHAPE;
+    if (!slots && n_state_rows < B) return TRIUNE_ERR_SHAPE;  // row b of the state for batch b
     if (!((Dk == 32 && Dv == 32) || (Dk == 64 && Dv == 64) || (Dk == 128 && Dv == 128) ||
           (Dk == 64 && Dv == 128) || (Dk == 128 && Dv == 64)))
         return TRIUNE_ERR_SHAPE;
@@ -231,9 +237,31 @@ int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, cons
     a.v_sb = strides[4]; a.v_sh = strides[5];
     a.g_sb = strides[6]; a.g_sh = strides[7];
     a.o_sb = strides[8]; a.o_sh = strides[9];
-    a.state_in = state_in; a.state_out = state_out; a.slots = slots;
+    a.state_in = state_in; a.state_out = state_out; a.slots = slots; a.n_state_rows = n_state_rows;
     a.o = o; a.B = B; a.H = H;
     return launch_status(launch_gla_decode(a, Dk, Dv, 4 * device_cus(), (hipStream_t)stream));
+}
+
+// ---- the reference's own native decode signatures, on device pointers -----------------------
+static thread_local int g_last_error = TRIUNE_OK;
+
+int triune_hip_last_error(void) { return g_last_error; }
+
+void launch_gla_decode_step(const void* Q, const void* K, const void* V, const float* G, float* State, void* Out,
+                            int B, int H, int HD, void* stream) {
+    const int64_t row = HD, bat = (int64_t)H * HD;  // contiguous [B, 1, H, HD]
+    const int64_t st[10] = {bat, row, bat, row, bat, row, bat, row, bat, row};
+    g_last_error = triune_hip_gla_decode_step(Q, K, V, G, TRIUNE_DT_BF16, TRIUNE_DT_F32, st, State, State, nullptr,
+                                              B, Out, TRIUNE_DT_BF16, B, H, HD, HD, stream);
+}
+
+void triune_gla_recurrent_step_f32(const float* q, const float* k, const float* v, const float* g, float* state,
+                                   float* out, int batch_heads, int head_dim) {
+    const int64_t row = head_dim;  // contiguous [batch_heads, head_dim] rows: one head per row
+    const int64_t st[10] = {row, row, row, row, row, row, row, row, row, row};
+    g_last_error = triune_hip_gla_decode_step(q, k, v, g, TRIUNE_DT_F32, TRIUNE_DT_F32, st, state, state, nullptr,
+                                              batch_heads, out, TRIUNE_DT_F32, batch_heads, 1, head_dim, head_dim,
+                                              nullptr);
 }
 
 size_t triune_hip_gla_prefill_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {
@@ -326,9 +354,9 @@ int triune_hip_gla_prefill_bwd(const void* q, const void* k, const void* v, cons
     if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
     if (B < 0 || T < 0 || H <= 0 || Dk != Dv || !gla_bwd_supported(Dk, io_dtype)) return TRIUNE_ERR_SHAPE;
     const int64_t* st = strides;  // q, k, v, g, dout, dq, dk, dv, dg: (batch, token, head) each
-    auto rows_ok = [&](int i, int dt, int D) {
+    auto rows_ok = [&](int i, int dt, int D) {  // as tok_strides_ok: rows at least D apart
         const int64_t es = dt == TRIUNE_DT_F32 ? 4 : 2;
-        return st[3 * i + 1] >= 0 && (64 * st[3 * i + 1] + D) * es < ((int64_t)1 << 31);
+        return st[3 * i + 1] >= D && (64 * st[3 * i + 1] + D) * es < ((int64_t)1 << 31);
     };
     if (!vec_ok(q, io_dtype, st + 0, 3) || !vec_ok(k, io_dtype, st + 3, 3) || !vec_ok(v, io_dtype, st + 6, 3) ||
         !vec_ok(g, g_dtype, st + 9, 3) || !vec_ok(dout, io_dtype, st + 12, 3) || !vec4_ok(dq, d_dtype, st + 15, 3) ||
@@ -598,16 +626,17 @@ GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = -1;
     int64_t slots;
+    const bool ck = T % 4 != 0;  // the instance the launch picks (launch_gdn_t)
     {
         std::lock_guard<std::mutex> lock(mu);
-        const int key = 4 * dev + io_dt;
+        const int key = 8 * dev + 2 * io_dt + (ck ? 1 : 0);
         auto it = slots_cache.find(key);
         if (it == slots_cache.end()) {
             int ncu = 0;
             if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
                 ncu <= 0)
                 ncu = 256;
-            it = slots_cache.emplace(key, (int64_t)ncu * gdn_seg_out_blocks_per_cu(io_dt)).first;
+            it = slots_cache.emplace(key, (int64_t)ncu * gdn_seg_out_blocks_per_cu(io_dt, ck)).first;
         }
         slots = it->second;
     }
@@ -649,8 +678,9 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
         !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
         !vec_ok(o, o_dtype, strides + 15, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
-        reinterpret_cast<uintptr_t>(s_final) % 16 || !tok_strides_ok(strides, io_dtype, g_dtype, o_dtype, Dk, Dv) ||
-        (beta_kind == TRIUNE_BETA_KEY && !vec_ok(beta, TRIUNE_DT_F32, strides + 12, 3)))
+        reinterpret_cast<uintptr_t>(s_final) % 16 ||
+        (beta_kind == TRIUNE_BETA_KEY &&
+         (!vec_ok(beta, TRIUNE_DT_F32, strides + 12, 3) || strides[13] < Dk || (64 * strides[13] + Dk) * 4 >= ((int64_t)1 << 31))))
         return TRIUNE_ERR_LAYOUT;
     // o strides sit at 15..17 here (beta takes 12..14); tok_strides_ok reads o's token stride at 13
     const int64_t ost[15] = {strides[0], strides[1], strides[2], strides[3], strides[4], strides[5],

@@ -709,12 +709,18 @@ hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt
     return hipGetLastError();
 }
 
-// Resident output-kernel workgroups per CU for I/O dtype io_dt (the gate dtype does not change
-// the kernel's LDS or register use).
-int gdn_seg_out_blocks_per_cu(int io_dt) {
-    const void* k = io_dt == DT_F16   ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, true>)
-                    : io_dt == DT_F32 ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, true>)
-                                      : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, true>);
+// Resident output-kernel workgroups per CU for I/O dtype io_dt, on the instance that runs
+// (ck: checked row addressing, launched unless T % 4 == 0; the gate dtype does not change the
+// kernel's LDS or register use).
+int gdn_seg_out_blocks_per_cu(int io_dt, bool ck) {
+    const void* k =
+        io_dt == DT_F16
+            ? (ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, true>)
+                  : reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, false>))
+        : io_dt == DT_F32 ? (ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, true>)
+                                : reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, false>))
+                          : (ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, true>)
+                                : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, false>));
     int nb = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0);
     return (e == hipSuccess && nb > 0) ? nb : 1;

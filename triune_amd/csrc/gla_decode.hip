@@ -44,12 +44,21 @@ __global__ __launch_bounds__(DK * DV / (4 * RPT)) void gla_decode_kernel(DecodeP
         Vec4<TIO> q[RPT / 4], k[RPT / 4], v;
         Vec4<TG> g[RPT / 4];
     };
+    // State row of (b, h), or -1 when b's slot lies outside the pool (a padded batch row): such a
+    // row reads no state, stores none and outputs zeros.  The row is the same for the whole block.
     auto state_row = [&](uint32_t row) -> int64_t {
         const uint32_t b = row / H32, h = row % H32;
-        return a.slots ? (int64_t)a.slots[b] * a.H + h : (int64_t)row;
+        if (!a.slots) return (int64_t)row;
+        const int64_t sl = (int64_t)a.slots[b];
+        return (sl >= 0 && sl < a.n_state_rows) ? sl * a.H + h : -1;
     };
     auto fetch = [&](In& x, uint32_t row) {
         x.srow = state_row(row);
+        if (x.srow < 0) {
+#pragma unroll
+            for (int m = 0; m < RPT; ++m) x.st[m] = zero4();
+            return;
+        }
         const float* sin = a.state_in + x.srow * (int64_t)(DK * DV) + (int64_t)r0 * DV + 4 * cg;
 #pragma unroll
         for (int m = 0; m < RPT; ++m)
@@ -98,9 +107,11 @@ __global__ __launch_bounds__(DK * DV / (4 * RPT)) void gla_decode_kernel(DecodeP
         const int64_t srow = cur.srow;
         const uint32_t nrow = row + gridDim.x;
         if (nrow < rows) fetch(cur, nrow);
-        float* sout = a.state_out + srow * (int64_t)(DK * DV) + (int64_t)r0 * DV + 4 * cg;
+        if (srow >= 0) {
+            float* sout = a.state_out + srow * (int64_t)(DK * DV) + (int64_t)r0 * DV + 4 * cg;
 #pragma unroll
-        for (int m = 0; m < RPT; ++m) __builtin_nontemporal_store(y[m], reinterpret_cast<f32x4*>(sout + m * DV));
+            for (int m = 0; m < RPT; ++m) __builtin_nontemporal_store(y[m], reinterpret_cast<f32x4*>(sout + m * DV));
+        }
         // reduce over the row groups of a wave (lanes tid ^ CG*2^k share a column group) ...
 #pragma unroll
         for (int c = 0; c < 4; ++c) o4[c] = xor_group_sum<CG>(o4[c]);
@@ -111,6 +122,7 @@ __global__ __launch_bounds__(DK * DV / (4 * RPT)) void gla_decode_kernel(DecodeP
             f32x4 s = red[buf][0][cg];
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) s += red[buf][w][cg];
+            if (srow < 0) s = zero4();
             const int64_t b = row / H32, h = row % H32;
             const int64_t off = b * a.o_sb + h * a.o_sh + 4 * cg;
             store4_dt(reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt), a.o_dt, s[0], s[1], s[2], s[3]);

@@ -600,15 +600,19 @@ static hipError_t launch_seg(const PrefillParams& a, int64_t n_work, int io_dt, 
     return hipErrorInvalidValue;
 }
 
-// Resident workgroups per CU of the output kernel for (Dk, Dv) (bf16 I/O instance; the other
-// dtypes use at least as much LDS, so this is an upper bound that only costs balance).
-int gla_seg_output_blocks_per_cu(int Dk, int Dv) {
+// Resident workgroups per CU of the output kernel for (Dk, Dv) on the instance that runs (ck:
+// checked row addressing, see launch_seg_t; bf16 I/O instance: the other dtypes use at least as
+// much LDS, so this is an upper bound that only costs balance).
+int gla_seg_output_blocks_per_cu(int Dk, int Dv, bool ck) {
     int nb = 0;
     hipError_t e = hipErrorInvalidValue;
 #define TRIUNE_OCC_CASE(DK_, DV_)                                                                             \
     if (Dk == DK_ && Dv == DV_)                                                                               \
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                                     \
-            &nb, reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, true>), DV_ * 4, 0);
+            &nb,                                                                                              \
+            ck ? reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, true>)         \
+               : reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, false>),       \
+            DV_ * 4, 0);
     TRIUNE_OCC_CASE(64, 64)
     TRIUNE_OCC_CASE(128, 128)
     TRIUNE_OCC_CASE(32, 32)

@@ -107,6 +107,7 @@ struct DecodeParams {
     const float* state_in;  // [B, H, Dk, Dv]
     float* state_out;       // may equal state_in
     const int32_t* slots;   // optional: state row of batch b is slots[b] (state pool), or null
+    int64_t n_state_rows;   // rows of state_in / state_out; a slot outside [0, n_state_rows) is skipped
     void* o;
     int64_t B, H;
 };
@@ -173,9 +174,9 @@ hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int3
 hipError_t launch_gdn_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream);
 hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
-int gdn_seg_out_blocks_per_cu(int io_dt);
+int gdn_seg_out_blocks_per_cu(int io_dt, bool ck);
 bool prefill_shape_supported(int Dk, int Dv);
 bool prefill_dtype_supported(int Dk, int Dv, int io_dt);
-int gla_seg_output_blocks_per_cu(int Dk, int Dv);
+int gla_seg_output_blocks_per_cu(int Dk, int Dv, bool ck);
 
 }  // namespace triune

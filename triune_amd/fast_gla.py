@@ -62,10 +62,15 @@ def _pair(dk: int, dv: int, pairs=_PAIRS) -> tuple[int, int]:
     return best
 
 
-def _vec_layout(x: torch.Tensor) -> torch.Tensor:
-    """x with unit innermost stride, 16-byte aligned rows (a contiguous copy otherwise)."""
+def _vec_layout(x: torch.Tensor, tok_dim: int | None = None) -> torch.Tensor:
+    """x with unit innermost stride and 16-byte aligned rows (a contiguous copy otherwise).
+    tok_dim: the token axis of a token tensor ([B, T, H, D]: 1, packed [N, H, D]: 0), whose stride
+    must also be at least the row width (rows that overlap, e.g. a tensor expanded along the
+    tokens, are copied: the chunk kernels read a sequence's rows only up to its last token)."""
     m = 4 if x.dtype == torch.float32 else 8
     ok = x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % m == 0 for s in x.stride()[:-1])
+    if ok and tok_dim is not None and x.shape[tok_dim] > 1 and x.stride(tok_dim) < x.shape[-1]:
+        ok = False
     return x if ok else x.contiguous()
 
 
@@ -127,10 +132,10 @@ def _prefill(q, k, v, g, initial_state, out, flags, save_final=True, out_dtype=N
             return o, torch.zeros(B, H, Dk0, Dv0, device=q.device, dtype=torch.float32)
         return o, initial_state.to(torch.float32).clone()
     Dk, Dv = _pair(Dk0, Dv0)
-    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, _gate(g, q)))
-    vp = _vec_layout(_pad_last(v, Dv))
+    qp, kp, gp = (_vec_layout(_pad_last(x, Dk), 1) for x in (q, k, _gate(g, q)))
+    vp = _vec_layout(_pad_last(v, Dv), 1)
     odt = out.dtype if out is not None else (out_dtype or v.dtype)
-    if out is not None and out.shape[-1] == Dv and out.stride(-1) == 1 and _vec_layout(out) is out:
+    if out is not None and out.shape[-1] == Dv and out.stride(-1) == 1 and _vec_layout(out, 1) is out:
         o = out
     else:
         o = torch.empty(B, T, H, Dv, device=q.device, dtype=odt)
@@ -176,13 +181,16 @@ def gla_decode_step(q, k, v, g, state, out=None, *, inplace=False, slots=None, o
     padded = (Dk, Dv) != (Dk0, Dv0)
     qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, g))
     vp = _vec_layout(_pad_last(v, Dv))
+    if slots is None and state.shape[0] != B:
+        raise ValueError(f"state has {state.shape[0]} rows for a batch of {B} (pass slots to address a pool)")
     if inplace:
         if padded or state.dtype != torch.float32 or not state.is_contiguous():
             raise ValueError("inplace decode needs a contiguous float32 state with supported head dims")
         s_in = s_out = state
     else:
         s_in = _state_in(state, Dk, Dv)
-        s_out = torch.empty_like(s_in)
+        # with slots only the addressed rows are written: the others keep their input values
+        s_out = torch.empty_like(s_in) if slots is None else s_in.clone()
     odt = out.dtype if out is not None else (out_dtype or v.dtype)
     o = None
     if out is not None and Dv == Dv0:
@@ -196,7 +204,7 @@ def gla_decode_step(q, k, v, g, state, out=None, *, inplace=False, slots=None, o
     st = strides(qp.stride()[:2], kp.stride()[:2], vp.stride()[:2], gp.stride()[:2], o.stride()[:2])
     rc = lib().triune_hip_gla_decode_step(
         ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, ptr(s_in), ptr(s_out), ptr(slots),
-        ptr(o), dtype_code(o), B, H, Dk, Dv, stream_of(q),
+        s_in.shape[0], ptr(o), dtype_code(o), B, H, Dk, Dv, stream_of(q),
     )
     check(rc, "triune_hip_gla_decode_step")
     if not inplace and padded:
@@ -225,11 +233,11 @@ def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None):
     if max(Dk0, Dv0) > 64 or (q.dtype == torch.float32 and D > 32):
         raise NotImplementedError(
             f"GLA backward supports head dims <= 64 (<= 32 for float32 inputs); got ({Dk0}, {Dv0}) {q.dtype}")
-    qp, kp, gp = (_vec_layout(_pad_last(x, D)) for x in (q, k, _gate(g, q)))
-    vp = _vec_layout(_pad_last(v, D))
+    qp, kp, gp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, _gate(g, q)))
+    vp = _vec_layout(_pad_last(v, D), 1)
     if do is None:
         do = torch.zeros(B, T, H, Dv0, device=q.device, dtype=q.dtype)
-    dop = _vec_layout(_pad_last(do.to(q.dtype), D))
+    dop = _vec_layout(_pad_last(do.to(q.dtype), D), 1)
     dsf = None
     if ds is not None:
         dsf = _state_in(ds, D, D)
@@ -335,13 +343,13 @@ def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None, 
     Dk, Dv = _pair(Dk0, Dv0)
     cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     n = cu.numel() - 1
-    qp, kp, gp = (_vec_layout(_pad_last(x, Dk)) for x in (q, k, _gate(g, q)))
-    vp = _vec_layout(_pad_last(v, Dv))
+    qp, kp, gp = (_vec_layout(_pad_last(x, Dk), 0) for x in (q, k, _gate(g, q)))
+    vp = _vec_layout(_pad_last(v, Dv), 0)
     odt = out.dtype if out is not None else v.dtype
     o = None
     if out is not None and Dv == Dv0:
         ov = out[0] if out.dim() == 4 else out
-        if tuple(ov.shape) == (N, H, Dv) and ov.stride(-1) == 1 and _vec_layout(ov) is ov:
+        if tuple(ov.shape) == (N, H, Dv) and ov.stride(-1) == 1 and _vec_layout(ov, 0) is ov:
             o = ov  # write straight into the caller's buffer
     if o is None:
         o = torch.empty(N, H, Dv, device=q.device, dtype=odt)
@@ -391,12 +399,12 @@ def _varlen_pool(q, k, v, g, cu_seqlens, pool, slots, out, initial_state):
         list(slots), device=q.device, dtype=torch.int32)
     if sl.numel() != n:
         raise ValueError(f"{sl.numel()} slots for {n} sequences")
-    qp, kp, gp = (_vec_layout(x) for x in (q, k, _gate(g, q)))
-    vp = _vec_layout(v)
+    qp, kp, gp = (_vec_layout(x, 0) for x in (q, k, _gate(g, q)))
+    vp = _vec_layout(v, 0)
     o = None
     if out is not None:
         ov = out[0] if out.dim() == 4 else out
-        if tuple(ov.shape) == (N, H, Dv0) and ov.stride(-1) == 1 and _vec_layout(ov) is ov:
+        if tuple(ov.shape) == (N, H, Dv0) and ov.stride(-1) == 1 and _vec_layout(ov, 0) is ov:
             o = ov
     if o is None:
         o = torch.empty(N, H, Dv0, device=q.device, dtype=out.dtype if out is not None else v.dtype)
@@ -481,7 +489,7 @@ class FusedRecurrentScan(torch.autograd.Function):
 # ---------------------------------------------------------------------------------------
 
 
-def _gdn(q, k, v, g, beta, initial_state, beta_kind):
+def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
     _check_io(q, k, v, g)
     if _needs_grad(q, k, v, g, beta, initial_state):
         # The reference differentiates its PyTorch recurrence here (fast_gla.py:885-904); these
@@ -493,7 +501,7 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind):
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
     D = _round_dk(max(Dk0, Dv0))
-    qp, kp, gp, vp = (_vec_layout(_pad_last(x, D)) for x in (q, k, g, v))
+    qp, kp, gp, vp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, g, v))
     bp = None
     bst = (0, 0, 0)
     if beta is not None:
@@ -502,18 +510,18 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind):
             bp = _pad_last(beta, D)
         bp = bp.contiguous()
         bst = (bp.stride(0), bp.stride(1), bp.stride(2))
-    o = torch.empty(B, T, H, D, device=q.device, dtype=v.dtype)
+    o = torch.empty(B, T, H, D, device=q.device, dtype=out_dtype or v.dtype)
     s0 = _state_in(initial_state, D, D)
     sf = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
     # chunked WY/UT path: (64, 64) heads (smaller ones zero-padded), per-token or per-key beta
     chunked = (D <= 64 and T > 1 and beta_kind != _lib.BETA_VALUE and _chunked_gdn_enabled)
     if chunked:
         D = 64
-        qp, kp, gp, vp = (_vec_layout(_pad_last(x, D)) for x in (q, k, g, v))
+        qp, kp, gp, vp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, g, v))
         if beta_kind == _lib.BETA_KEY:
             bp = _pad_last(beta, D).to(torch.float32).contiguous()
             bst = (bp.stride(0), bp.stride(1), bp.stride(2))
-        o = torch.empty(B, T, H, D, device=q.device, dtype=v.dtype)
+        o = torch.empty(B, T, H, D, device=q.device, dtype=out_dtype or v.dtype)
         s0 = _state_in(initial_state, D, D)
         sf = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
     st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), bst, _tok3(o))
@@ -548,19 +556,21 @@ def _beta_kind(beta, orientation):
     return _lib.BETA_KEY if orientation == "key" else _lib.BETA_VALUE
 
 
-def fast_recurrent_gated_deltanet(q, k, v, g, beta=None, initial_state=None):
+def fast_recurrent_gated_deltanet(q, k, v, g, beta=None, initial_state=None, *, out_dtype=None):
     """Gated DeltaNet, reference variant (fast_gla.py:781-836):
         u_t = v_t - S_{t-1}^T k_t ; S_t = diag(exp(min(g_t,0))) S_{t-1} + beta_t (k_t u_t^T) ; o_t = S_t^T q_t
     beta None, [B, T, H] or [B, T, H, D]; a 4-D beta scales rows (key dim), as this reference
-    function does.  Returns (out, final_state fp32)."""
-    return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, "key"))
+    function does.  out_dtype: dtype of the output (default v.dtype; float32 keeps the fp32
+    accumulators unrounded).  Returns (out, final_state fp32)."""
+    return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, "key"), out_dtype)
 
 
-def fast_chunk_gated_deltanet(q, k, v, g, beta=None, initial_state=None, chunk_size=64):
+def fast_chunk_gated_deltanet(q, k, v, g, beta=None, initial_state=None, chunk_size=64, *, out_dtype=None):
     """Gated DeltaNet operator entry (reference: fast_chunk_gated_deltanet, fast_gla.py:839-904).
     A 4-D beta scales columns (value dim) as the reference's GPU kernel does for T > 1
     (fast_gla.py:464-465), and rows at T == 1 (fast_gla.py:880).  chunk_size is accepted for
-    signature parity.  Returns (out, final_state fp32)."""
+    signature parity.  out_dtype as for fast_recurrent_gated_deltanet.  Returns (out,
+    final_state fp32)."""
     T = q.shape[1]
     orientation = "key" if T == 1 else "value"
-    return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, orientation))
+    return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, orientation), out_dtype)

@@ -104,11 +104,17 @@ def scatter_cache(dst_cache: Optional[List[Any]], src_cache: Optional[List[Any]]
 class StateSlotPool:
     """Recurrent states of up to n_slots sessions for num_layers GLA layers, resident on one device.
 
-    states[layer] is an fp32 [n_slots, H, Dk, Dv] tensor; offsets[layer][slot] counts the tokens
-    a slot has absorbed (the reference's cache offset).  Sessions map to slots in LRU order with a
-    time-to-live, as in the reference's SessionRecurrentStateManager (srsm.py:11-112), whose
-    get / update / clear / stats interface this class keeps; a new session's slot starts from a
-    zero state.  Thread-safe for the bookkeeping; kernel calls follow the caller's stream order.
+    states[layer] is an fp32 [n_slots, H, Dk, Dv] tensor; offsets[layer, slot] (an int64 device
+    tensor [num_layers, n_slots]) counts the tokens a slot has absorbed (the reference's cache
+    offset).  Sessions map to slots in LRU order with a time-to-live, as in the reference's
+    SessionRecurrentStateManager (srsm.py:11-112), whose get / update / clear / stats interface
+    this class keeps; a new session's slot starts from a zero state.  Thread-safe for the
+    bookkeeping; kernel calls follow the caller's stream order.
+
+    prefill() and decode_step() run only device work (the kernels and a device-side update of
+    the offsets), with no host synchronisation, so a serving loop can capture them in one graph
+    when slots and cu_seqlens are device tensors; a slot outside [0, n_slots) (a padded batch
+    row) is skipped by the kernels and by the offset count.
     """
 
     def __init__(self, num_layers: int, n_slots: int, H: int, Dk: int, Dv: int, device="cuda",
@@ -119,7 +125,7 @@ class StateSlotPool:
         self.device = torch.device(device)
         self.session_ttl_seconds = session_ttl_seconds
         self.states = torch.zeros(num_layers, n_slots, H, Dk, Dv, device=self.device, dtype=torch.float32)
-        self.offsets = [[0] * n_slots for _ in range(num_layers)]
+        self.offsets = torch.zeros(num_layers, n_slots, device=self.device, dtype=torch.int64)
         self._lock = threading.Lock()
         self._free = collections.deque(range(n_slots))
         self._sessions: "collections.OrderedDict[str, Dict[str, Any]]" = collections.OrderedDict()
@@ -132,8 +138,7 @@ class StateSlotPool:
 
     def _reset_slot(self, slot: int) -> None:
         self.states[:, slot].zero_()
-        for layer in range(self.num_layers):
-            self.offsets[layer][slot] = 0
+        self.offsets[:, slot].zero_()
 
     def acquire(self, session_id: str) -> int:
         """The slot of session_id, creating the session (zero state, offset 0) if needed; when
@@ -197,7 +202,8 @@ class StateSlotPool:
             entry["last_active"] = time.time()
             self._sessions.move_to_end(session_id)
             slot, depth = entry["slot"], entry.get("depth")
-        cache = [(self.states[layer, slot:slot + 1], self.offsets[layer][slot]) for layer in range(self.num_layers)]
+        offs = self.offsets[:, slot].tolist()  # one device read per session lookup
+        cache = [(self.states[layer, slot:slot + 1], offs[layer]) for layer in range(self.num_layers)]
         return cache, depth
 
     def update_session_cache(self, session_id: str, cache: List[Any], depth: Optional[int] = None) -> None:
@@ -213,27 +219,33 @@ class StateSlotPool:
                 src = state.reshape(self.H, self.Dk, self.Dv)
                 if src.data_ptr() != dst.data_ptr():
                     dst.copy_(src.to(device=self.device, dtype=torch.float32))
-            self.offsets[layer][slot] = int(off)
+            self.offsets[layer, slot] = int(off)
         with self._lock:
             if session_id in self._sessions:
                 self._sessions[session_id]["depth"] = depth
 
     # -- kernels over slots --------------------------------------------------------------------
+    def _count(self, layer: int, slots: torch.Tensor, n: torch.Tensor) -> None:
+        """offsets[layer, slots[i]] += n[i] on the device, skipping slots outside the pool."""
+        sl = slots.to(device=self.device, dtype=torch.int64)
+        ok = (sl >= 0) & (sl < self.n_slots)
+        self.offsets[layer].index_add_(0, torch.where(ok, sl, torch.zeros_like(sl)),
+                                       torch.where(ok, n.to(device=self.device, dtype=torch.int64),
+                                                   torch.zeros_like(sl)))
+
     def prefill(self, layer: int, q, k, v, g, cu_seqlens, slots: torch.Tensor, out=None):
         """Packed prefill of len(slots) sequences from their slots' states, final states written
         back to the slots; returns the outputs."""
         o, _ = fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, out=out, state_pool=self.states[layer], slots=slots)
-        lens = (cu_seqlens[1:] - cu_seqlens[:-1]).tolist()
-        for s, n in zip(slots.tolist(), lens):
-            self.offsets[layer][s] += int(n)
+        cu = cu_seqlens.to(device=self.device)
+        self._count(layer, slots, cu[1:] - cu[:-1])
         return o
 
     def decode_step(self, layer: int, q, k, v, g, slots: torch.Tensor, out=None, count_tokens: bool = True):
         """One token for each of len(slots) sessions; states updated in place in their slots."""
         o, _ = gla_decode_step(q, k, v, g, self.states[layer], out=out, inplace=True, slots=slots)
         if count_tokens:
-            for s in slots.tolist():
-                self.offsets[layer][s] += 1
+            self._count(layer, slots, torch.ones_like(slots, dtype=torch.int64))
         return o
 
 
