@@ -68,6 +68,7 @@ enum {
     TRIUNE_ERR_LAYOUT = -4,      /* stride / alignment requirement not met */
     TRIUNE_ERR_WORKSPACE = -5,   /* workspace missing or smaller than required */
     TRIUNE_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
+    TRIUNE_ERR_SCRATCH = -7,     /* larger than the allocation-free entry point's static scratch */
 };
 
 /* Prefill flags. */
@@ -139,6 +140,24 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
                            const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
                            int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/* triune_hip_gla_prefill without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  The workspace is a static device array of
+ * TRIUNE_GLA_PREFILL_SCRATCH_BYTES (32 MiB) per GPU, held until the process ends; a call whose
+ * workspace (triune_hip_gla_prefill_workspace_size) exceeds it returns TRIUNE_ERR_SCRATCH and
+ * launches nothing.  Config 1 (B = 4, T = 16384, H = 6, D = 64) needs about 8 MB; at D = 128 the
+ * bound is reached near B * H = 500 (head, sequence) pairs.  Every call on a GPU shares that
+ * GPU's array (each call writes what it reads, so nothing needs clearing): calls that overlap on
+ * one GPU (other streams or host threads) race and must be serialised by the caller.  stream must
+ * belong to the current device.  Same arguments, semantics and results as
+ * triune_hip_gla_prefill otherwise.  No device memory is allocated or freed. */
+#define TRIUNE_GLA_PREFILL_SCRATCH_BYTES (32u << 20)
+size_t triune_hip_gla_prefill_noalloc_max_bytes(void);
+int triune_hip_gla_prefill_noalloc(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                   int g_dtype, const int64_t* strides, const float* s0, void* o, int o_dtype,
+                                   float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags,
+                                   void* stream);
 
 /* Packed ragged GLA prefill: sequence i covers rows [cu_seqlens[i], cu_seqlens[i+1]) of the
  * [total_tokens, H, D] tensors, starts from s0[i] (or 0) and ends in s_final[i]; every token's

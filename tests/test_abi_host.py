@@ -51,6 +51,7 @@ def test_error_strings_and_codes_match_header():
         "TRIUNE_ERR_LAYOUT": -4,
         "TRIUNE_ERR_WORKSPACE": -5,
         "TRIUNE_ERR_LAUNCH": -6,
+        "TRIUNE_ERR_SCRATCH": -7,
     }
     lib = L.lib()
     for c in [0, *codes.values()]:
@@ -132,6 +133,21 @@ def test_decode_and_gdn_and_scan_validation_errors():
     assert sb(None, 0, None, 0, _FAKE, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 260, None) == -2
     assert sb(None, 0, None, 0, _FAKE, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 6, None) == -2
     assert sb(None, 0, _FAKE, 7, _FAKE, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -3
+
+
+def test_noalloc_prefill_validation():
+    """The allocation-free prefill fails before any launch on bad arguments, and with
+    TRIUNE_ERR_SCRATCH when the workspace would exceed its static scratch."""
+    lib = L.lib()
+    f = lib.triune_hip_gla_prefill_noalloc
+    cap = int(lib.triune_hip_gla_prefill_noalloc_max_bytes())
+    assert cap == 32 << 20
+    st = (ctypes.c_int64 * 15)(*([64 * 128 * 64, 64 * 128, 128] * 5))
+    assert f(None, _FAKE, _FAKE, _FAKE, 1, 1, st, None, _FAKE, 1, None, 1, 64, 1, 128, 128, 0, None) == -1
+    assert f(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, st, None, _FAKE, 1, None, 1, 64, 1, 48, 48, 0, None) == -2
+    assert int(lib.triune_hip_gla_prefill_workspace_size(64, 4096, 64, 128, 128, 0)) > cap
+    assert f(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, st, None, _FAKE, 1, None, 64, 4096, 64, 128, 128, 0, None) == -7
+    assert b"static scratch" in lib.triune_hip_error_string(-7)
 
 
 def test_workspace_sizes():

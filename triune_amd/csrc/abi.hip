@@ -3,9 +3,9 @@
 #include "../../include/triune_hip.h"
 #include "kernels.h"
 
+#include <atomic>
 #include <map>
 #include <mutex>
-#include <tuple>
 
 using namespace triune;
 
@@ -35,41 +35,46 @@ bool vec4_ok(const void* p, int dt, const int64_t* st, int n) {
     return true;
 }
 
+// Per-device query caches: fixed arrays (no host allocation on any call path); 0 = not queried
+// yet.  Concurrent first queries store the same value.
+constexpr int kMaxDevices = 64;
+
+int current_device() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
+    return dev;
+}
+
+// Compute units of the current device, queried once per device (MI355X: 256).
+int device_cus() {
+    static std::atomic<int> cache[kMaxDevices];
+    const int dev = current_device();
+    if (dev >= 0) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int ncu = 0;
+    if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+        ncu = 256;  // MI355X
+    if (dev >= 0) cache[dev].store(ncu, std::memory_order_relaxed);
+    return ncu;
+}
+
 // Resident (segment, head) workgroups the device holds at once: CUs x output-kernel occupancy
 // of the instance that runs (ck: checked row addressing, used unless every sequence length is a
 // multiple of 4).  Queried once per device and cached (host-side runtime queries only; nothing
 // is enqueued).
 int64_t resident_slots(int Dk, int Dv, bool ck) {
-    static std::mutex mu;
-    static std::map<std::tuple<int, int, int, bool>, int64_t> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
-    std::lock_guard<std::mutex> lock(mu);
-    auto key = std::make_tuple(dev, Dk, Dv, ck);
-    auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
-    int ncu = 0;
-    if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
-        ncu = 256;  // MI355X
-    const int64_t slots = (int64_t)ncu * gla_seg_output_blocks_per_cu(Dk, Dv, ck);
-    cache[key] = slots;
+    static std::atomic<int64_t> cache[kMaxDevices][4][2];
+    const int pair = Dk == 32 ? 0 : (Dk == 64 ? 1 : (Dv == 64 ? 2 : 3));  // (32,32) (64,64) (128,64) (128,128)
+    const int dev = current_device();
+    if (dev >= 0) {
+        const int64_t c = cache[dev][pair][ck].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    const int64_t slots = (int64_t)device_cus() * gla_seg_output_blocks_per_cu(Dk, Dv, ck);
+    if (dev >= 0) cache[dev][pair][ck].store(slots, std::memory_order_relaxed);
     return slots;
-}
-
-// Compute units of the current device, queried once per device (MI355X: 256).
-int device_cus() {
-    static std::mutex mu;
-    static std::map<int, int> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(dev);
-    if (it != cache.end()) return it->second;
-    int ncu = 0;
-    if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
-        ncu = 256;
-    cache[dev] = ncu;
-    return ncu;
 }
 
 // Segments per sequence (dense): fill the resident workgroup slots once with near-equal
@@ -207,6 +212,9 @@ const char* triune_hip_error_string(int code) {
         case TRIUNE_ERR_LAYOUT: return "stride or alignment requirement not met";
         case TRIUNE_ERR_WORKSPACE: return "workspace missing or too small";
         case TRIUNE_ERR_LAUNCH: return "HIP kernel launch failed";
+        case TRIUNE_ERR_SCRATCH:
+            return "problem exceeds the static scratch of the allocation-free entry point "
+                   "(use the entry point that takes a workspace)";
         default: return "unknown error";
     }
 }
@@ -337,6 +345,58 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
 
     return launch_output_timed(a, pl.n_work, io_dtype, st);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Allocation-free prefill: the workspace of triune_hip_gla_prefill lives in this file-scope
+// device array instead of a caller buffer.  Each GPU holds its own copy until the process ends;
+// host code must use the address hipGetSymbolAddress returns for the current device (the
+// array's name is a host-side stand-in), fetched once per device on its first call.
+constexpr size_t kScratchBytes = (size_t)TRIUNE_GLA_PREFILL_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+// The scratch address on the current device (which must own `stream`), or nullptr.
+void* scratch_for(void* stream) {
+    static std::atomic<void*> ptrs[kMaxDevices];
+    const int dev = current_device();
+    if (dev < 0) return nullptr;
+    if (stream) {
+        hipDevice_t sdev = -1;
+        if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess || sdev != dev) return nullptr;
+    }
+    void* p = ptrs[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    void* q = nullptr;
+    if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return nullptr;
+    ptrs[dev].store(q, std::memory_order_release);
+    return q;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t triune_hip_gla_prefill_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int triune_hip_gla_prefill_noalloc(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                   int g_dtype, const int64_t* strides, const float* s0, void* o, int o_dtype,
+                                   float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags,
+                                   void* stream) {
+    // the checks that need no workspace run first, with the same codes as the allocating entry
+    if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
+    if (B < 0 || T < 0 || H <= 0 || !prefill_shape_ok(Dk, Dv)) return TRIUNE_ERR_SHAPE;
+    size_t need = 0;
+    if (B > 0 && T > 0) {
+        need = plan_dense(B, T, H, Dk, Dv, flags).total;
+        if (need > kScratchBytes) return TRIUNE_ERR_SCRATCH;
+    }
+    void* ws = need ? scratch_for(stream) : nullptr;
+    if (need && !ws) return TRIUNE_ERR_LAUNCH;
+    return triune_hip_gla_prefill(q, k, v, g, io_dtype, g_dtype, strides, s0, o, o_dtype, s_final, B, T, H, Dk, Dv,
+                                  flags, ws, need ? kScratchBytes : 0, stream);
 }
 
 size_t triune_hip_gla_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags) {

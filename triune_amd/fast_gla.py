@@ -27,6 +27,7 @@ __all__ = [
     "fast_chunk_gated_deltanet",
     "fast_recurrent_gated_deltanet",
     "_triton_chunk_gla_tc_fwd",
+    "gla_prefill_noalloc",
     "TriuneHipError",
 ]
 
@@ -62,16 +63,20 @@ def _pair(dk: int, dv: int, pairs=_PAIRS) -> tuple[int, int]:
     return best
 
 
-def _vec_layout(x: torch.Tensor, tok_dim: int | None = None) -> torch.Tensor:
-    """x with unit innermost stride and 16-byte aligned rows (a contiguous copy otherwise).
-    tok_dim: the token axis of a token tensor ([B, T, H, D]: 1, packed [N, H, D]: 0), whose stride
-    must also be at least the row width (rows that overlap, e.g. a tensor expanded along the
-    tokens, are copied: the chunk kernels read a sequence's rows only up to its last token)."""
+def _vec_ok(x: torch.Tensor, tok_dim: int | None = None) -> bool:
+    """Unit innermost stride and 16-byte aligned rows; tok_dim: the token axis of a token tensor
+    ([B, T, H, D]: 1, packed [N, H, D]: 0), whose stride must also be at least the row width (the
+    chunk kernels read a sequence's rows only up to its last token, so rows must not overlap)."""
     m = 4 if x.dtype == torch.float32 else 8
     ok = x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % m == 0 for s in x.stride()[:-1])
     if ok and tok_dim is not None and x.shape[tok_dim] > 1 and x.stride(tok_dim) < x.shape[-1]:
         ok = False
-    return x if ok else x.contiguous()
+    return ok
+
+
+def _vec_layout(x: torch.Tensor, tok_dim: int | None = None) -> torch.Tensor:
+    """x if _vec_ok(x, tok_dim), else a contiguous copy (e.g. of a tensor expanded along tokens)."""
+    return x if _vec_ok(x, tok_dim) else x.contiguous()
 
 
 def _pad_last(x: torch.Tensor, d: int) -> torch.Tensor:
@@ -307,6 +312,41 @@ def fast_chunk_gla(q, k, v, g, initial_state=None, chunk_size=64, out=None):
         return gla_decode_step(q, k, v, g, st, out=out)
     flags = _lib.FLAG_TAIL_UNCLAMPED if (C > 0 and T > C and T % C == 1) else 0
     return _prefill(q, k, v, g, initial_state, out, flags)
+
+
+def gla_prefill_noalloc(q, k, v, g, initial_state, out, final_state, *, flags=0):
+    """fast_chunk_gla's chunked prefill for callers that cannot allocate device memory (graph
+    capture, serving loops): runs triune_hip_gla_prefill_noalloc, whose workspace is a static
+    per-GPU device array, and allocates nothing itself.  No reference counterpart.
+
+    q, k, g [B, T, H, Dk], v and out [B, T, H, Dv] with (Dk, Dv) a kernel pair (32x32, 64x64,
+    128x64, 128x128), unit innermost stride, 16-byte aligned rows, token stride >= the row width
+    (nothing is padded or copied: other layouts raise ValueError); initial_state and final_state
+    contiguous float32 [B, H, Dk, Dv] or None.  g is clamped at 0 (flags: TRIUNE_FLAG_* as for
+    triune_hip_gla_prefill).  Calls on one GPU share its scratch, so calls that overlap (other
+    streams or threads) race.  Returns (out, final_state)."""
+    _check_io(q, k, v, g)
+    _on_device(initial_state, out, final_state)
+    B, T, H, Dk = q.shape
+    Dv = v.shape[-1]
+    if (Dk, Dv) not in _PAIRS:
+        raise ValueError(f"head dims ({Dk}, {Dv}) are not a kernel pair {_PAIRS}")
+    if tuple(out.shape) != (B, T, H, Dv):
+        raise ValueError("out must be [B, T, H, Dv]")
+    if not all(_vec_ok(x, 1) for x in (q, k, v, g, out)):
+        raise ValueError("gla_prefill_noalloc copies nothing: q, k, v, g, out need unit innermost stride, "
+                         "16-byte aligned rows and token strides of at least a row")
+    for st in (initial_state, final_state):
+        if st is not None and (st.dtype != torch.float32 or not st.is_contiguous() or
+                               tuple(st.shape) != (B, H, Dk, Dv)):
+            raise ValueError("states must be contiguous float32 [B, H, Dk, Dv]")
+    rc = lib().triune_hip_gla_prefill_noalloc(
+        ptr(q), ptr(k), ptr(v), ptr(g), dtype_code(q), dtype_code(g),
+        strides(_tok3(q), _tok3(k), _tok3(v), _tok3(g), _tok3(out)), ptr(initial_state), ptr(out),
+        dtype_code(out), ptr(final_state), B, T, H, Dk, Dv, flags, stream_of(q),
+    )
+    check(rc, "triune_hip_gla_prefill_noalloc")
+    return out, final_state
 
 
 def _triton_chunk_gla_tc_fwd(q, k, v, g, initial_state=None, out=None, save_final=True):
