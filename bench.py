@@ -4,8 +4,9 @@ Headline (BASELINE.json metric): GLA prefill tokens/s at B=4, H=6, T=16384, Dk=D
 fp32 state (config 1), with the batched decode step at B=256 (config 2) reported alongside.
 
   step (prefill) = one fast_chunk_gla forward over the whole [4, 16384, 6, 64] batch, inputs
-                   resident in HBM, bf16 outputs and fp32 final states written to HBM (three
-                   kernels, called directly; a HIP-graph replay of the pass measured no faster).
+                   resident in HBM (two input sets used in turn, together larger than the 256 MB
+                   MALL), bf16 outputs and fp32 final states written to HBM (three kernels,
+                   called directly; a HIP-graph replay of the pass measured no faster).
   step (decode)  = one decode step for 256 sequences (H=6, D=64) on one of 12 rotating fp32
                    state buffers (302 MB in total, larger than the 256 MB MALL) with one of 12
                    rotating q/k/v/g/o sets; the 512-step loop is captured in a HIP graph and
@@ -52,9 +53,18 @@ def bench_prefill(steps, warmup, dev):
 
     B, T, H, D = 4, 16384, 6, 64
     q, k, v, g, s0 = config1(T=T, B=B, H=H, D=D)
-    q, k, v, g, s0 = (x.to(dev) for x in (q, k, v, g, s0))
-    out = torch.empty_like(v)
-    fn = lambda: fast_chunk_gla(q, k, v, g, initial_state=s0, out=out)  # noqa: E731
+    # Two input sets used in turn (the second is the first rolled by one token): 2 x 201 MB of
+    # q/k/v/g exceeds the 256 MB MALL, so every pass reads its inputs from HBM.
+    sets = [[x.to(dev) for x in (q, k, v, g)], [x.roll(1, dims=1).to(dev) for x in (q, k, v, g)]]
+    s0 = s0.to(dev)
+    outs = [torch.empty_like(v, device=dev) for _ in sets]
+    turn = [0]
+
+    def fn():
+        i = turn[0] & 1
+        turn[0] += 1
+        fast_chunk_gla(*sets[i], initial_state=s0, out=outs[i])
+
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -166,7 +176,7 @@ def bench_prep(dev, reps=10):
     emb = torch.cat([torch.outer(torch.arange(T, dtype=torch.float32), inv)] * 2, dim=-1)
     cos, sin = emb.cos().to(dev), emb.sin().to(dev)
     fn = lambda: fused_qkv_g_prep_inplace(qkv, g, cos, sin)  # noqa: E731
-    for _ in range(3):
+    for _ in range(20):
         fn()
     torch.cuda.synchronize()
     ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
@@ -220,14 +230,14 @@ def bench_fused_decode(steps_total, dev, n_bufs=12):
                          "alg_bytes_per_step": step_bytes}}
 
 
-def bench_gdn(dev, reps=10):
+def bench_gdn(dev, reps=20):
     """Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta and decay)."""
     from triune_amd import fast_chunk_gated_deltanet
     from triune_amd.workloads import config3
 
     q, k, v, g, beta = (x.to(dev) for x in config3())
     fn = lambda: fast_chunk_gated_deltanet(q, k, v, g, beta=beta)  # noqa: E731
-    for _ in range(3):
+    for _ in range(20):
         fn()
     torch.cuda.synchronize()
     ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
@@ -251,7 +261,8 @@ def bench_varlen(dev, reps=5):
     q, k, v, g, cu, s0 = (x.to(dev) for x in (q, k, v, g, cu, s0))
     out = torch.empty_like(v)
     fn = lambda: fast_chunk_gla_varlen(q, k, v, g, cu, initial_state=s0, out=out)  # noqa: E731
-    fn()
+    for _ in range(5):
+        fn()
     torch.cuda.synchronize()
     ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
     n_tok, H, D = q.shape[1], q.shape[2], q.shape[3]
@@ -321,7 +332,7 @@ def bench_bwd(dev, reps=10):
     do = torch.randn(q.shape, generator=gen).bfloat16().to(dev)
     ds = torch.randn(s0.shape, generator=gen).to(dev)
     fn = lambda: _prefill_bwd(q, k, v, g, s0, do, ds, 0)  # noqa: E731
-    for _ in range(3):
+    for _ in range(10):
         fn()
     torch.cuda.synchronize()
     ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
@@ -435,12 +446,15 @@ def main():
                    "scan": bench_scan}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
-    pre = bench_prefill(args.steps, args.warmup, dev)
+    # Order: the CPU baseline first (the GPU idles meanwhile), then the secondary GPU legs, then
+    # the headline prefill, so no leg is timed right after the GPU sat idle for seconds.  The
+    # headline itself still does exactly `warmup` untimed passes before its `steps` timed ones.
+    cpu = None if args.no_cpu else cpu_baseline()
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "scan": bench_scan(dev)}
-    cpu = None if args.no_cpu else cpu_baseline()
+    pre = bench_prefill(args.steps, args.warmup, dev)
     line = {
         "metric": METRIC,
         "value": round(pre["tok_s"], 1),

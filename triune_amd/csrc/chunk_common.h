@@ -342,7 +342,11 @@ __device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[
 }
 
 // min(x, 0) in one instruction (fminf first quiets NaNs with an extra max in IEEE mode).
-__device__ __forceinline__ float min0(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, -__builtin_inff()); }
+__device__ __forceinline__ float min0(float x) {
+    // min(x, 0) as one integer min: a float with the sign bit set is a negative int32 and keeps
+    // its bits; every other float (positive, +0, positive NaN) maps to the bits of +0.0f.
+    return __int_as_float(min(__float_as_int(x), 0));
+}
 
 // V rows of tokens 4*tg + j (this lane's four columns) into one bf16 plane.  bf16 V is copied
 // as loaded (no conversion round trip); rows at or past nv are zeroed.  Other types go through

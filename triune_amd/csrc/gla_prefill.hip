@@ -131,6 +131,7 @@ struct PendingOut {
 
 // Stage the pending outputs 16 tokens at a time through `stage` (this wave's 16 x OS floats of
 // LDS) and store them with the four lanes of a quad covering one token's 16 columns.
+template <bool OBF>
 __device__ __forceinline__ void flush_out(const PrefillParams& a, const Work& wk, int64_t h, int c0, const PendingOut& p,
                                           float* stage, int os) {
     const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
@@ -144,12 +145,18 @@ __device__ __forceinline__ void flush_out(const PrefillParams& a, const Work& wk
     for (int tb = 0; tb < 4; ++tb) {
         *reinterpret_cast<f32x4*>(stage + r16 * os + 4 * g4) = p.o[tb];
         const f32x4 x = *reinterpret_cast<const f32x4*>(stage + tq * os + 4 * q);
-        out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, x);
+        if constexpr (OBF) {  // bf16 outputs known at compile time: one store of four packed values
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const u32x2 w = __builtin_bit_cast(u32x2, bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]});
+            __builtin_amdgcn_raw_buffer_store_b64(w, orr.lo, (int32_t)(16 * tb * ost) + olane, 0, 0);
+        } else {
+            out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, x);
+        }
     }
 }
 
 // CK: checked row addressing (see chunk_load); without it the loads zero rows past the chunk.
-template <typename TIn, typename TG, int DK, int DV, bool CK>
+template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF = false>
 struct OutStep {
     using L = Lay<TIn, DK, DV, true>;
     using PR = Prec<TIn>;
@@ -158,8 +165,11 @@ struct OutStep {
 
     // One chunk: stage 1 (factors, split operands -> LDS), stage 2 (A^T tiles), stage 3 (O, S).
     // after_inputs() runs once stage 1 has consumed `cur` (it may refill those registers).
-    template <typename Hook>
-    __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+    // FAST_ONLY: a chunk that needs the token-by-token path returns false right after stage 1
+    // (its inputs consumed, the next chunk's loads issued, the pending outputs stored) and the
+    // caller finishes it with finish_tokenwise; otherwise both paths are handled here.
+    template <bool FAST_ONLY, typename Hook>
+    __device__ static bool run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
                                const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, PendingOut& pend,
                                Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
@@ -229,14 +239,17 @@ struct OutStep {
         if constexpr (!late_refill) after_inputs();
         // The previous chunk's outputs, staged through this wave's slice of the A^T planes
         // (nothing reads them again before this chunk's stage 2).
-        if (pend.valid) flush_out(a, wk, h, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
+        if (pend.valid) flush_out<OBF>(a, wk, h, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
         pend.valid = false;
         __syncthreads();
         bool fast = true;
 #pragma unroll
         for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
 
-        if (!fast) {
+        if constexpr (FAST_ONLY) {
+            if (!fast) return false;
+        }
+        if (!FAST_ONLY && !fast) {
             chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, c0, tc, nv, g4, r16, S);
         } else {
             // ---------------- stage 2: causal tiles of A^T -> LDS ----------------------------
@@ -341,19 +354,31 @@ struct OutStep {
             pend.nv = nv;
             pend.valid = true;
             if constexpr (!L::DEFER) {  // store now, staged through this wave's own V planes
-                flush_out(a, wk, h, c0, pend, reinterpret_cast<float*>(sVP), L::OS);
+                flush_out<OBF>(a, wk, h, c0, pend, reinterpret_cast<float*>(sVP), L::OS);
                 pend.valid = false;
             }
         }
         if constexpr (late_refill) after_inputs();
         __syncthreads();  // the next chunk rewrites LDS
+        return true;
+    }
+
+    // The rest of a chunk that run<true> returned false for.
+    template <typename Hook>
+    __device__ static void finish_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+                                            f32x4 (&S)[NDB], Hook&& after_inputs) {
+        const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
+        chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, wave_id() * 16, tc, nv, g4, r16, S);
+        constexpr bool late_refill = DK == 128 && DV == 128;
+        if constexpr (late_refill) after_inputs();
+        __syncthreads();
     }
 };
 
 // Outputs of one segment from its carried-in state S (K3).
-template <typename TIn, typename TG, int DK, int DV, bool CK>
+template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF>
 __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
-    using St = OutStep<TIn, TG, DK, DV, CK>;
+    using St = OutStep<TIn, TG, DK, DV, CK, OBF>;
     constexpr int DL = St::DL;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<true, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
@@ -369,11 +394,23 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     chunk_load<true, CK>(A, ad, tok(0), true);
     PendingOut pend;
     pend.valid = false;
-    for (int64_t c = 0; c < nch; ++c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
-                [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
+    // Chunks take the MFMA path until one needs the token-by-token path (a decay span beyond the
+    // factored range, or the unclamped tail); from there a loop that handles both finishes the
+    // segment.  The fast loop has no merge with the token-wise code, so its state registers stay put.
+    int64_t c = 0;
+    for (; c < nch; ++c)
+        if (!St::template run<true>(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
+                                    [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); }))
+            break;
+    if (c < nch) {
+        St::finish_tokenwise(a, wk, h, tok(c), chunk_nv(c), S,
+                             [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
+        for (++c; c < nch; ++c)
+            St::template run<false>(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
+                                    [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
+    }
     if (pend.valid)  // after the last chunk's closing barrier the A^T planes are free
-        flush_out(a, wk, h, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
+        flush_out<OBF>(a, wk, h, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
                   St::L::OS);
 }
 
@@ -499,7 +536,7 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     }
 }
 
-template <typename TIn, typename TG, int DK, int DV, bool CK>
+template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF>
 __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void gla_seg_output_kernel(PrefillParams a) {
     using L = Lay<TIn, DK, DV, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
@@ -513,7 +550,7 @@ __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, DV)];
-    segment_walk<TIn, TG, DK, DV, CK>(a, wk, h, S, smem);
+    segment_walk<TIn, TG, DK, DV, CK, OBF>(a, wk, h, S, smem);
 }
 
 // K0 (varlen): segment offsets from cu_seqlens, one thread block.
@@ -562,9 +599,12 @@ template <typename TIn, typename TG, bool CK>
 static hipError_t launch_seg_ck(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
     const dim3 grid((unsigned)n_work, (unsigned)a.H);
     const dim3 block((unsigned)(a.Dv * 4));
+    constexpr bool OBF_ok = std::is_same<TIn, __bf16>::value;
+    const bool obf = OBF_ok && a.o_dt == DT_BF16;
 #define TRIUNE_SEG_CASE(DK_, DV_)                                                                       \
     if (a.Dk == DK_ && a.Dv == DV_) {                                                                   \
-        if (with_out) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_, CK>), grid, block, 0, stream, a); \
+        if (with_out && obf) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_, CK, OBF_ok>), grid, block, 0, stream, a); \
+        else if (with_out) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_, CK, false>), grid, block, 0, stream, a); \
         else hipLaunchKernelGGL((gla_seg_state_kernel<TIn, TG, DK_, DV_, CK>), grid, block, 0, stream, a);          \
         return hipGetLastError();                                                                       \
     }
@@ -610,8 +650,8 @@ int gla_seg_output_blocks_per_cu(int Dk, int Dv, bool ck) {
     if (Dk == DK_ && Dv == DV_)                                                                               \
         e = hipOccupancyMaxActiveBlocksPerMultiprocessor(                                                     \
             &nb,                                                                                              \
-            ck ? reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, true>)         \
-               : reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, false>),       \
+            ck ? reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, true, false>)         \
+               : reinterpret_cast<const void*>(gla_seg_output_kernel<__bf16, __bf16, DK_, DV_, false, false>),       \
             DV_ * 4, 0);
     TRIUNE_OCC_CASE(64, 64)
     TRIUNE_OCC_CASE(128, 128)
