@@ -187,6 +187,58 @@ def bench_prep(dev, reps=10):
                          "unit": "GB/s", "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
+def bench_fused_prefill(dev, reps=20, T=16384):
+    """VectorisedGLA's prefill from raw projections (qkv [4, T, 3, 6, 64] and gate logits
+    g [4, T, 6, 64] bf16, fp32 RoPE tables, fp32 S0; the bench line uses T = 1024, the tile
+    VectorisedGLA runs every prefill in, attention.py:458-499): fused_qkv_g_prep_chunk_gla against
+    the two-step pipeline the reference launches (in-place pre-processing, then the prefill)."""
+    from triune_amd import fast_chunk_gla, fused_qkv_g_prep_chunk_gla, fused_qkv_g_prep_inplace
+    from triune_amd.workloads import gla_algorithmic_bytes
+
+    B, H, HD = 4, 6, 64
+    gen = torch.Generator().manual_seed(15)
+    qkv = torch.randn(B, T, 3, H, HD, generator=gen).bfloat16().to(dev)
+    # raw gate logits N(3, 1): logsigmoid of them decays about 0.05 nats per token, the scale of
+    # config 1's logsigmoid(N(0, 1)) / 16
+    g = (torch.randn(B, T, H, HD, generator=gen) + 3.0).bfloat16().to(dev)
+    s0 = (0.1 * torch.randn(B, H, HD, HD, generator=gen)).to(dev)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))
+    emb = torch.cat([torch.outer(torch.arange(T, dtype=torch.float32), inv)] * 2, dim=-1)
+    cos, sin = emb.cos().to(dev), emb.sin().to(dev)
+    out = torch.empty(B, T, H, HD, device=dev, dtype=torch.bfloat16)
+    # Both pipelines pre-process qkv and g in place, as the reference does: every call gets the raw
+    # inputs restored first (outside its timed region) and is timed by an event pair of its own.
+    raw_qkv, raw_g = qkv.clone(), g.clone()
+    fused = lambda: fused_qkv_g_prep_chunk_gla(qkv, g, cos, sin, initial_state=s0, out=out)  # noqa: E731
+
+    def two_step():
+        fused_qkv_g_prep_inplace(qkv, g, cos, sin)
+        fast_chunk_gla(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, initial_state=s0, out=out)
+
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name, fn in (("fused", fused), ("prep_then_prefill", two_step)):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for i in range(10 + reps):
+            qkv.copy_(raw_qkv)
+            g.copy_(raw_g)
+            if i >= 10:
+                ev[i - 10][0].record(stream)
+            fn()
+            if i >= 10:
+                ev[i - 10][1].record(stream)
+        torch.cuda.synchronize()
+        res[name] = sorted(b.elapsed_time(e) for b, e in ev)[reps // 2]  # median
+    alg = gla_algorithmic_bytes(B * T * H, HD, HD, 2, 2, 2) + 2 * B * H * HD * HD * 4
+    gbs = alg / (res["fused"] * 1e-3) / 1e9
+    return {"workload": f"VectorisedGLA prefill from raw projections (B=4, T={T}, H=6, HD=64, bf16, "
+            "RoPE, gate logits N(3,1)): pre-processing inside the chunk kernels", "us": round(res["fused"] * 1e3, 2),
+            "tok_s": round(B * T / (res["fused"] * 1e-3), 1),
+            "prep_then_prefill_us": round(res["prep_then_prefill"] * 1e3, 2), "alg_bytes": alg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def bench_fused_decode(steps_total, dev, n_bufs=12):
     """Decode step fused with the pre-processing at the config-2 shape (B=256, H=6, HD=64): raw
     qkvg [256, 4, 6, 64] bf16, fp32 state updated in place; 12 rotating state buffers and input
@@ -414,7 +466,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "varlen", "prep", "fused_decode", "bwd", "scan"),
+        choices=("decode", "gdn", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -443,7 +495,7 @@ def main():
             res = bench_fused_decode(args.decode_steps, dev)
         else:
             res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd,
-                   "scan": bench_scan}[args.only](dev)
+                   "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=1024)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     # Order: the CPU baseline first (the GPU idles meanwhile), then the secondary GPU legs, then
@@ -452,6 +504,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline()
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
+                                      "fused_prefill": bench_fused_prefill(dev, T=1024),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "scan": bench_scan(dev)}
     pre = bench_prefill(args.steps, args.warmup, dev)

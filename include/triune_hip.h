@@ -141,6 +141,25 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
                            int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* triune_hip_gla_prefill on raw projections with the VectorisedGLA input pre-processing done by
+ * the prefill's segment-state kernel: q, k, v, g are the raw projections (e.g. the qkv[:, :, i]
+ * views of [B, T, 3, H, D] and g [B, T, H, D], all in io_dtype, bf16 or fp16).  While it forms the
+ * segment states, that kernel writes back, in place and rounded to io_dtype,
+ *     q <- RoPE(normalize(elu(q) + 1)),  k <- RoPE(normalize(elu(k) + 1)),  g <- logsigmoid(g)
+ * with normalize(a) = a / sqrt(max(sum a^2, 1e-12)) per (token, head) row and RoPE pairing d with
+ * d + D/2 from the fp32 tables cos/sin [T, D] (row t for token t, cs_stride elements apart; used
+ * when use_rope != 0), and uses those rounded values itself; the output kernel then reads them.
+ * Results and the in-place side effect are those of triune_hip_gla_qkvg_prep followed by
+ * triune_hip_gla_prefill.  strides[15] as for triune_hip_gla_prefill; o may alias g.  D in {32, 64,
+ * 128}; workspace as for triune_hip_gla_prefill(B, T, H, D, D, 0).
+ * Replaces: _fused_qkv_g_prep_inplace_kernel (triune/model/attention.py:14-79) followed by
+ * _triton_chunk_gla_tc_fwd (fast_gla.py:318-380), as VectorisedGLA launches them
+ * (attention.py:425-451), without the prep kernel's separate pass over q, k, g. */
+int triune_hip_gla_prefill_prep(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                const int64_t* strides, const float* cos, const float* sin, int64_t cs_stride,
+                                int use_rope, const float* s0, void* o, int o_dtype, float* s_final, int64_t B,
+                                int64_t T, int64_t H, int D, void* workspace, size_t workspace_bytes, void* stream);
+
 /* triune_hip_gla_prefill without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  The workspace is a static device array of

@@ -148,3 +148,152 @@ def test_fused_decode_steps_equal_prep_then_decode(dev):
         torch.cuda.synchronize()
         assert float((out - o2).abs().max()) <= 1e-5
         assert float((s - s_ref).abs().max()) <= 1e-5
+
+
+# --- the prefill with the pre-processing fused into the segment-state kernel -----------------------
+# (triune_hip_gla_prefill_prep): q, k, g are pre-processed in place while the segment states form,
+# exactly as the reference's in-place prep kernel leaves them (rounded to the I/O dtype), and the
+# scan then runs on those rounded values.  Checked in two parts: the values left in qkv and g
+# against oracle.qkv_g_prep (one ULP of the I/O dtype), and the outputs and final states against
+# oracle.gla_fwd on the values the device left (2e-3 for fp32 outputs, one bf16 ULP + 2e-3 for
+# bf16 outputs).
+def _fused_case(B, T, H, HD, seed, dtype=torch.bfloat16, gate_shift=0.0):
+    gen = torch.Generator().manual_seed(seed)
+    qkv = (2.0 * torch.randn(B, T, 3, H, HD, generator=gen)).to(dtype)
+    g = (3.0 * torch.randn(B, T, H, HD, generator=gen) + gate_shift).to(dtype)
+    s0 = 0.1 * torch.randn(B, H, HD, HD, generator=gen)
+    return qkv, g, s0
+
+
+def _ulp16(ref, dtype):
+    ref_t = torch.as_tensor(np.asarray(ref, dtype=np.float64))
+    if dtype == torch.bfloat16:
+        return ulp_bf16(ref_t).double()
+    a = ref_t.abs().clamp_min(2.0**-14)
+    return torch.exp2(torch.floor(torch.log2(a)) - 10)
+
+
+def _check_prepped(qd, gd_pre, qkv, g, cos, sin):
+    """The q, k, g left in place are the fp64 pre-processing rounded once (within one ULP)."""
+    rq, rg = O.qkv_g_prep(qkv, g, cos, sin)
+    for got, ref in ((qd[:, :, :2], rq[:, :, :2]), (gd_pre, rg)):
+        err = (got.double().cpu() - torch.from_numpy(np.asarray(ref))).abs()
+        assert bool((err <= _ulp16(ref, got.dtype) + 1e-6).all()), float(err.max())
+    assert torch.equal(qd[:, :, 2].cpu(), qkv[:, :, 2])  # v untouched
+
+
+@pytest.mark.parametrize("HD", [32, 64, 128])
+@pytest.mark.parametrize("T", [200, 301])
+@pytest.mark.parametrize("rope", [True, False])
+def test_fused_prep_prefill_matches_oracle(dev, HD, T, rope):
+    """T = 200 runs the unchecked-row instances with a partial last chunk, T = 301 the checked ones;
+    fp32 outputs in a separate buffer, so g keeps the pre-processed gate for the check."""
+    from triune_amd import fused_qkv_g_prep_chunk_gla
+
+    B, H = 2, 3
+    qkv, g, s0 = _fused_case(B, T, H, HD, seed=HD + T + rope)
+    cos, sin = _tables(T, HD, offset=5)
+    qd, gd = qkv.to(dev), g.to(dev)
+    out = torch.empty(B, T, H, HD, device=dev, dtype=torch.float32)
+    o, s = fused_qkv_g_prep_chunk_gla(qd, gd, cos.to(dev), sin.to(dev), initial_state=s0.to(dev), out=out,
+                                      use_rope=rope)
+    torch.cuda.synchronize()
+    assert o.data_ptr() == out.data_ptr()
+    _check_prepped(qd, gd, qkv, g, cos if rope else None, sin if rope else None)
+    ro, rs = O.gla_fwd(qd[:, :, 0].cpu(), qd[:, :, 1].cpu(), qd[:, :, 2].cpu(), gd.cpu(), s0)
+    e_o, e_s = float(np.abs(o.double().cpu().numpy() - ro).max()), float(np.abs(s.double().cpu().numpy() - rs).max())
+    assert e_o <= 2e-3 and e_s <= 2e-3, (e_o, e_s)
+
+
+@pytest.mark.parametrize("HD", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_prep_prefill_out_over_g(dev, HD, dtype):
+    """The reference's call shape (attention.py:443-451): outputs written over g in the I/O dtype."""
+    from triune_amd import fused_qkv_g_prep_chunk_gla
+
+    B, T, H = 2, 1024, 2
+    qkv, g, s0 = _fused_case(B, T, H, HD, seed=HD, dtype=dtype, gate_shift=3.0)
+    cos, sin = _tables(T, HD)
+    qd, gd = qkv.to(dev), g.to(dev)
+    # the pre-processed gate is overwritten by the outputs: take it from a run into a side buffer
+    q2, g2 = qkv.to(dev), g.to(dev)
+    fused_qkv_g_prep_chunk_gla(q2, g2, cos.to(dev), sin.to(dev), initial_state=s0.to(dev),
+                               out=torch.empty(B, T, H, HD, device=dev, dtype=dtype))
+    o, s = fused_qkv_g_prep_chunk_gla(qd, gd, cos.to(dev), sin.to(dev), initial_state=s0.to(dev))
+    torch.cuda.synchronize()
+    assert o.data_ptr() == gd.data_ptr() and torch.equal(qd, q2)
+    _check_prepped(q2, g2, qkv, g, cos, sin)
+    ro, rs = O.gla_fwd(q2[:, :, 0].cpu(), q2[:, :, 1].cpu(), q2[:, :, 2].cpu(), g2.cpu(), s0)
+    err = (o.double().cpu() - torch.from_numpy(ro)).abs()
+    assert bool((err <= _ulp16(ro, dtype) + 2e-3).all()), float(err.max())
+    assert float(np.abs(s.cpu().numpy() - rs).max()) <= 2e-3
+
+
+def test_fused_prep_prefill_tokenwise_chunks_and_no_final(dev):
+    """Very negative raw gates (logsigmoid(g) ~ g) push chunks past the factored decay range: the
+    output kernel runs them token by token on the pre-processed values; outputs over g."""
+    from triune_amd import fused_qkv_g_prep_chunk_gla
+
+    B, T, H, HD = 2, 260, 2, 64
+    qkv, g, s0 = _fused_case(B, T, H, HD, seed=77)
+    g = g.float()
+    g[:, 64:128] = -2.0 - 20.0 * torch.rand(B, 64, H, HD, generator=torch.Generator().manual_seed(3))
+    g = g.bfloat16()
+    cos, sin = _tables(T, HD)
+    q2, g2 = qkv.to(dev), g.to(dev)
+    fused_qkv_g_prep_chunk_gla(q2, g2, cos.to(dev), sin.to(dev), initial_state=s0.to(dev),
+                               out=torch.empty(B, T, H, HD, device=dev, dtype=torch.bfloat16))
+    qd, gd = qkv.to(dev), g.to(dev)
+    o, s = fused_qkv_g_prep_chunk_gla(qd, gd, cos.to(dev), sin.to(dev), initial_state=s0.to(dev))
+    torch.cuda.synchronize()
+    _check_prepped(q2, g2, qkv, g, cos, sin)
+    ro, rs = O.gla_fwd(q2[:, :, 0].cpu(), q2[:, :, 1].cpu(), q2[:, :, 2].cpu(), g2.cpu(), s0)
+    ok, err = _within_ulp(o, ro, slack=2e-3)
+    assert ok, err
+    assert float(np.abs(s.cpu().numpy() - rs).max()) <= 2e-3
+    o3, s3 = fused_qkv_g_prep_chunk_gla(qkv.to(dev), g.to(dev), cos.to(dev), sin.to(dev), save_final=False)
+    assert s3.numel() == 1
+
+
+def test_fused_prep_prefill_equals_prep_then_prefill(dev):
+    """Against this library's two-step pipeline (the in-place prep kernel, then the prefill): the
+    processed tensors agree to one ULP plus 1e-6 (the two kernels round the same fp32 values, formed
+    in a different order), and so do the outputs up to what such one-ULP input differences move."""
+    from triune_amd import fused_qkv_g_prep_chunk_gla
+
+    B, T, H, HD = 2, 512, 3, 64
+    qkv, g, s0 = _fused_case(B, T, H, HD, seed=9, gate_shift=3.0)
+    cos, sin = (x.to(dev) for x in _tables(T, HD))
+    qa, ga = qkv.to(dev), g.to(dev)
+    fused, sf = fused_qkv_g_prep_chunk_gla(qa, ga, cos, sin, initial_state=s0.to(dev),
+                                           out=torch.empty(B, T, H, HD, device=dev))
+    qb, gb = qkv.to(dev), g.to(dev)
+    fused_qkv_g_prep_inplace(qb, gb, cos, sin)
+    two, s2 = fast_chunk_gla(qb[:, :, 0], qb[:, :, 1], qb[:, :, 2], gb, initial_state=s0.to(dev),
+                             out=torch.empty(B, T, H, HD, device=dev))
+    torch.cuda.synchronize()
+    ulp = ulp_bf16(qb.double()).to(dev)
+    assert bool(((qa.double() - qb.double()).abs() <= ulp + 1e-6).all())
+    assert bool(((ga.double() - gb.double()).abs() <= ulp_bf16(gb.double()).to(dev) + 1e-6).all())
+    assert float((fused - two).abs().max()) <= 2.0**-7 * float(two.abs().max())
+    assert float((sf - s2).abs().max()) <= 2.0**-7 * float(s2.abs().max())
+
+
+def test_fused_prep_prefill_large_call_takes_two_step_path(dev):
+    """B * H * chunks beyond four per compute unit: the entry runs the prep kernel and then the
+    prefill (the faster arrangement there); same checks as the fused path."""
+    from triune_amd import fused_qkv_g_prep_chunk_gla
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    B, H, HD = 4, 8, 64
+    T = 64 * (4 * cus // (B * H) + 1)
+    qkv, g, s0 = _fused_case(B, T, H, HD, seed=31, gate_shift=3.0)
+    cos, sin = _tables(T, HD)
+    qd, gd = qkv.to(dev), g.to(dev)
+    out = torch.empty(B, T, H, HD, device=dev, dtype=torch.float32)
+    o, s = fused_qkv_g_prep_chunk_gla(qd, gd, cos.to(dev), sin.to(dev), initial_state=s0.to(dev), out=out)
+    torch.cuda.synchronize()
+    _check_prepped(qd, gd, qkv, g, cos, sin)
+    ro, rs = O.gla_fwd(qd[:, :, 0].cpu(), qd[:, :, 1].cpu(), qd[:, :, 2].cpu(), gd.cpu(), s0)
+    assert float(np.abs(o.double().cpu().numpy() - ro).max()) <= 2e-3
+    assert float(np.abs(s.double().cpu().numpy() - rs).max()) <= 2e-3

@@ -14,7 +14,7 @@ from .fast_gla import (
     gla_decode_step,
 )
 from .gla import gated_deltanet, gla
-from .gla_prep import fused_qkv_g_prep_inplace, fused_qkvg_decode_step
+from .gla_prep import fused_qkv_g_prep_chunk_gla, fused_qkv_g_prep_inplace, fused_qkvg_decode_step
 
 __all__ = [
     "FusedRecurrentScan",
@@ -23,6 +23,7 @@ __all__ = [
     "fast_chunk_gla",
     "fast_chunk_gla_varlen",
     "fast_recurrent_gated_deltanet",
+    "fused_qkv_g_prep_chunk_gla",
     "fused_qkv_g_prep_inplace",
     "fused_qkvg_decode_step",
     "gated_deltanet",

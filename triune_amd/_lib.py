@@ -53,6 +53,11 @@ def _bind(lib):
             [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _i, _vp, _sz, _vp],
             _i,
         ),
+        "triune_hip_gla_prefill_prep": (
+            [_vp, _vp, _vp, _vp, _i, _i64p, _vp, _vp, _i64, _i, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _vp, _sz,
+             _vp],
+            _i,
+        ),
         "triune_hip_gla_prefill_noalloc_max_bytes": ([], _sz),
         "triune_hip_gla_prefill_noalloc": (
             [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _i, _vp],
@@ -112,6 +117,7 @@ EXPORTS = (
     "triune_gla_recurrent_step_f32",
     "triune_hip_gla_prefill_workspace_size",
     "triune_hip_gla_prefill",
+    "triune_hip_gla_prefill_prep",
     "triune_hip_gla_prefill_noalloc_max_bytes",
     "triune_hip_gla_prefill_noalloc",
     "triune_hip_gla_prefill_varlen_workspace_size",

@@ -174,6 +174,9 @@ BwdPlan plan_bwd(int64_t B, int64_t T, int64_t H, int D, int flags) {
 
 int launch_status(hipError_t e) { return e == hipSuccess ? TRIUNE_OK : TRIUNE_ERR_LAUNCH; }
 
+int dense_launch(PrefillParams& a, const PrefillPlan& pl, const float* s0, float* s_final, int io_dtype, bool prep,
+                 hipStream_t st);
+
 // Events armed by triune_hip_set_output_kernel_events for this host thread (null: disarmed).
 struct OutputEvents {
     hipEvent_t begin = nullptr, end = nullptr;
@@ -326,8 +329,22 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     a.ws_gamma = reinterpret_cast<float*>(ws + pl.off_gamma);
     a.n_seqs = B; a.H = H; a.T = T; a.Dk = Dk; a.Dv = Dv;
     a.P = pl.P; a.nseg_dense = (int)pl.nseg; a.varlen = 0; a.flags = flags & 0xff;
+    return dense_launch(a, pl, s0, s_final, io_dtype, false, st);
+}
 
-    hipError_t e = launch_gla_seg_state(a, pl.n_work, io_dtype, st);
+}  // extern "C"
+
+namespace {
+
+// The dense launch sequence on a filled parameter block: segment states, the carry scan over the
+// segments (initial and final states), outputs.  prep: the segment-state kernel first
+// pre-processes q, k, g in place (the output kernel then reads the processed tensors).
+int dense_launch(PrefillParams& a, const PrefillPlan& pl, const float* s0, float* s_final, int io_dtype, bool prep,
+                 hipStream_t st) {
+    const int64_t H = a.H, B = a.n_seqs;
+    const int Dk = a.Dk, Dv = a.Dv;
+    hipError_t e = prep ? launch_gla_prep_seg_state(a, pl.n_work, io_dtype, st)
+                        : launch_gla_seg_state(a, pl.n_work, io_dtype, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
 
     const int64_t DD = (int64_t)Dk * Dv;
@@ -345,6 +362,63 @@ int triune_hip_gla_prefill(const void* q, const void* k, const void* v, const vo
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
 
     return launch_output_timed(a, pl.n_work, io_dtype, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int triune_hip_gla_prefill_prep(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                const int64_t* strides, const float* cos, const float* sin, int64_t cs_stride,
+                                int use_rope, const float* s0, void* o, int o_dtype, float* s_final, int64_t B,
+                                int64_t T, int64_t H, int D, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !g || !o || !strides || (use_rope && (!cos || !sin))) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
+    if (!prefill_prep_supported(D, io_dtype)) return io_dtype == TRIUNE_DT_F32 ? TRIUNE_ERR_DTYPE : TRIUNE_ERR_SHAPE;
+    if (B < 0 || T < 0 || H <= 0) return TRIUNE_ERR_SHAPE;
+    if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
+        !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, io_dtype, strides + 9, 3) ||
+        !vec_ok(o, o_dtype, strides + 12, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
+        reinterpret_cast<uintptr_t>(s_final) % 16 || !tok_strides_ok(strides, io_dtype, io_dtype, o_dtype, D, D))
+        return TRIUNE_ERR_LAYOUT;
+    if (use_rope && (!vec_ok(cos, TRIUNE_DT_F32, &cs_stride, 1) || !vec_ok(sin, TRIUNE_DT_F32, &cs_stride, 1) ||
+                     cs_stride < D || (64 * cs_stride + D) * 4 >= ((int64_t)1 << 31)))
+        return TRIUNE_ERR_LAYOUT;
+    hipStream_t st = (hipStream_t)stream;
+    if (B == 0) return TRIUNE_OK;
+    if (T == 0) {
+        if (!s_final) return TRIUNE_OK;
+        ScanParams sc{};  // N = 0: fin = init (or zero)
+        sc.kv = s_final; sc.kv_dt = DT_F32; sc.dec = s_final; sc.dec_dt = DT_F32;
+        sc.init = s0; sc.i_so = H * (int64_t)D * D; sc.i_sh = (int64_t)D * D;
+        sc.fin = s_final; sc.fin_dt = DT_F32; sc.f_so = sc.i_so; sc.f_sh = sc.i_sh;
+        sc.n_outer = B; sc.H = H; sc.Dk = D; sc.Dv = D; sc.N = 0;
+        return launch_status(launch_recurrent_scan(sc, st));
+    }
+    const PrefillPlan pl = plan_dense(B, T, H, D, D, 0);
+    if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
+    char* ws = reinterpret_cast<char*>(workspace);
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
+
+    PrefillParams a{};
+    fill_tok(a.q, q, strides + 0, B, T, H, D, io_dtype);
+    fill_tok(a.k, k, strides + 3, B, T, H, D, io_dtype);
+    fill_tok(a.v, v, strides + 6, B, T, H, D, io_dtype);
+    fill_tok(a.g, g, strides + 9, B, T, H, D, io_dtype);
+    a.o = o; a.o_sb = strides[12]; a.o_st = strides[13]; a.o_sh = strides[14];
+    a.g_dt = io_dtype; a.o_dt = o_dtype;
+    a.s0 = s0;
+    a.ws_state = reinterpret_cast<float*>(ws + pl.off_state);
+    a.ws_gamma = reinterpret_cast<float*>(ws + pl.off_gamma);
+    a.n_seqs = B; a.H = H; a.T = T; a.Dk = D; a.Dv = D;
+    a.P = pl.P; a.nseg_dense = (int)pl.nseg; a.varlen = 0; a.flags = 0;
+    a.use_rope = use_rope ? 1 : 0;
+    if (use_rope) {  // [T, D] tables shared by every sequence and head (batch and head strides 0)
+        const int64_t cst[3] = {0, cs_stride, 0};
+        fill_tok(a.cs, cos, cst, 1, T, 1, D, TRIUNE_DT_F32);
+        fill_tok(a.sn, sin, cst, 1, T, 1, D, TRIUNE_DT_F32);
+    }
+    return dense_launch(a, pl, s0, s_final, io_dtype, true, st);
 }
 
 }  // extern "C"

@@ -325,6 +325,57 @@ __device__ __forceinline__ void rows_load(Vec<T, N> (&v)[4], __amdgpu_buffer_rsr
     }
 }
 
+// N floats into a Vec of T (round to nearest even for 16-bit types).
+template <typename T, int N>
+__device__ __forceinline__ void vec_pack(const float* x, Vec<T, N>& v) {
+    if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) v.w[i] = __float_as_uint(x[i]);
+    } else if constexpr (std::is_same<T, __bf16>::value) {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i) v.w[i] = pk_bf16(x[2 * i], x[2 * i + 1]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N / 2; ++i)
+            v.w[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2 * i]) |
+                     ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2 * i + 1]) << 16);
+    }
+}
+
+// Raw buffer store of one Vec (the counterpart of vec_load): bytes at or past the resource's
+// num_records (in the vector offset) are dropped.
+template <typename T, int N>
+__device__ __forceinline__ void vec_store(const Vec<T, N>& v, __amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    if constexpr (Vec<T, N>::BYTES % 16 == 0) {
+#pragma unroll
+        for (int i = 0; i < Vec<T, N>::BYTES / 16; ++i)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.w[4 * i], v.w[4 * i + 1], v.w[4 * i + 2], v.w[4 * i + 3]}, r,
+                                                   voff + 16 * i, soff, 0);
+    } else if constexpr (Vec<T, N>::BYTES == 8) {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{v.w[0], v.w[1]}, r, voff, soff, 0);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b32(v.w[0], r, voff, soff, 0);
+    }
+}
+
+// Rows 4*tg + j (j < 4) of one tensor written back with rows_load's addressing (edge chunks through
+// the checked vector offset), so rows past the resource's records are not written.
+template <bool CK = true, typename T, int N>
+__device__ __forceinline__ void rows_store(const Vec<T, N> (&v)[4], __amdgpu_buffer_rsrc_t r, const TokAddr& a,
+                                           int64_t tc) {
+    if (CK && chunk_edge(a, tc)) {
+        int l = a.lane;
+        asm volatile("" : "+v"(l));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vec_store(v[j], r, l + j * a.st, 0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vec_store(v[j], r, a.lane, j * a.st);
+    }
+}
+
 // x[j][i] = element i of token j, zeroed for tokens at or past nv (partial chunks only).
 // ZERO = false: the loads already returned zero past the chunk (chunk_load without CK).
 template <bool ZERO = true, typename T, int N>

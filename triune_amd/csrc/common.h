@@ -280,4 +280,24 @@ __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(x * LOG2E);
 }
 
+// The GLA input pre-processing (VectorisedGLA, triune/model/attention.py:14-79): elu(x) + 1,
+// logsigmoid, and the inverse of a row's L2 norm with the reference's floor.
+__device__ __forceinline__ float elu1(float x) { return x >= 0.f ? x + 1.f : fast_exp(x); }
+
+// min(x, 0) - log(1 + e^-|x|) with the hardware exp2 / log2: for e^-|x| below 2^-24 the log term
+// rounds to 0, an absolute error under 6e-8.
+__device__ __forceinline__ float logsigmoid(float x) {
+    // min(x, 0) as one integer min (a float with the sign bit set keeps its bits, others map to +0)
+    const float lo = __int_as_float(min(__float_as_int(x), 0));
+    return lo - 0.6931471805599453f * __builtin_amdgcn_logf(1.f + fast_exp(-fabsf(x)));
+}
+
+__device__ __forceinline__ float sigmoid(float x) {
+    const float e = fast_exp(-fabsf(x));
+    return x >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
+}
+
+// The hardware reciprocal square root (about 1 ulp), as the reference's tl.rsqrt (attention.py:42).
+__device__ __forceinline__ float inv_norm(float sumsq) { return __builtin_amdgcn_rsqf(fmaxf(sumsq, 1e-12f)); }
+
 }  // namespace triune

@@ -1,557 +1,8 @@
-// gla_prefill.hip -- chunked GLA prefill for gfx950 (dense [B,T,H,D] and packed varlen).
-//
-// Semantics (reference: triune/kernels/fast_gla.py:569-689 _run_gla_chunks, :206-316 the
-// Triton TC kernel, :692-778 fast_chunk_gla dispatch):
-//   S_t = diag(exp(min(g_t, 0))) S_{t-1} + k_t v_t^T ,   o_t = S_t^T q_t
-// for every (sequence, head), starting from S0 (or zero), returning every o_t and S_T.
-//
-// Work decomposition.  A sequence is cut into segments of P chunks of 64 tokens.
-//   K1 seg_state : per (segment, head) the segment's local end state from zero and its summed
-//                  log-decay.
-//   K2 (recurrent_scan.hip): exclusive affine scan over the segments of each (sequence, head)
-//                  S_in[p+1] = exp(Gseg_p) * S_in[p] + L_p, written in place of L; final state.
-//   K3 seg_output: per (segment, head) walks its chunks from S_in[p] and writes o.
-// Within a chunk (C = 64 tokens, G = inclusive cumulative log-decay from the chunk start,
-// m = G_C / 2 per key dim):
-//   Qt = q * exp(G - m), Kt = k * exp(m - G)          (|exponents| <= span / 2)
-//   A^T[s][t] = sum_d Kt[s][d] Qt[t][d]  for s <= t   (causal, diagonal included)
-//   O^T = (exp(m) * S)^T Qt^T + V^T A^T
-//   S  <- exp(G_C) * S + exp(m) * (Kt^T V)
-// Products run on v_mfma_f32_16x16x32_bf16.  Operands that are not exactly bf16 are split
-// into 2 (16-bit I/O) or 3 (fp32 I/O) bf16 parts; part products whose combined order is
-// below the split depth are accumulated in fp32.
-//
-// One workgroup of NW = Dv/16 waves handles a (segment, head).  Per chunk:
-//   stage 1  wave w (each lane 4 tokens x DPW/4 dims): cumulative decay, factors and split
-//            Qt/Kt for key dims [w*DPW, (w+1)*DPW) -> token-major LDS planes; its own 16 value
-//            columns of V -> a token-major plane of its own
-//   stage 2  the ten 16x16 causal tiles of A^T, spread over the waves -> LDS
-//   stage 3  wave w: O^T and the state update for value columns [16w, 16w+16); fragments with
-//            the token as K index (Kt^T, V) come from the token-major planes through the
-//            transposed LDS read
-// The next chunk's inputs are loaded into registers while the current chunk is processed.
-// Chunks whose key-dim decay span exceeds SPAN_MAX (or that hold the reference's unclamped
-// 1-token tail) run token by token on the same state registers.
-#include "chunk_common.h"
+// gla_prefill.hip -- instances and host launchers of the chunked GLA prefill (gla_prefill.h):
+// raw q/k/g inputs, dense and varlen, and the varlen plan kernel.
+#include "gla_prefill.h"
 
 namespace triune {
-
-template <typename TIn, int DK, int DV, bool OUT>
-struct Lay {
-    using P = Prec<TIn>;
-    static constexpr int NW = DV / 16;             // waves per workgroup
-    static constexpr int DPW = DK / NW;            // key dims per wave in stage 1
-    static constexpr int RS = DK + PAD;            // row stride (elements) of [token][dim] planes
-    static constexpr int VS = 16;                  // row stride of a wave's [token][16 columns] V planes
-    static constexpr int ROWP = CHUNK * RS * 2;    // bytes per [token][dim] plane
-    static constexpr int VPP = CHUNK * VS * 2;     // bytes per V plane of one wave
-    static constexpr int ATP = 10 * 64 * 4 * 2;    // bytes per plane of the ten A^T tiles
-    // K3: Qt rows, Kt rows, A^T tiles.  K1: exp-weighted k rows (in the Kt slot).
-    static constexpr int OFF_QT = 0;
-    static constexpr int OFF_KT = OFF_QT + (OUT ? P::NS * ROWP : 0);
-    static constexpr int OFF_AT = OFF_KT + P::NS * ROWP;
-    static constexpr int OFF_VP = OFF_AT + (OUT ? P::NS * ATP : 0);
-    static constexpr int OFF_FAC = OFF_VP + NW * P::NX * VPP;
-    static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
-    static constexpr int BYTES = OFF_FLAG + 16 * 4;
-    // fp32 staging of a wave's outputs, 16 tokens x 16 columns, row stride OS floats: the 16 lanes
-    // of an LDS cycle hit distinct banks both when the MFMA layout writes and when quads read rows
-    static constexpr int OS = 20;
-    static_assert(DPW == 16 || DPW == 32, "stage-1 dims per wave");
-    // Outputs are stored one chunk late (after the next chunk's loads are issued) where the
-    // registers allow it (not at DK = 128)
-    static constexpr bool DEFER = DK <= 64;
-    static_assert(!DEFER || NW * 16 * OS * 4 <= P::NS * ATP, "output staging of every wave fits in the A^T planes");
-    static_assert(DEFER || 16 * OS * 4 <= P::NX * VPP, "output staging fits in a wave's V planes");
-    static_assert(BYTES <= 160 * 1024, "LDS budget");
-};
-
-
-// ---------------------------------------------------------------------------------------
-// Token-by-token update of one wave's state columns (large decay spans, unclamped tail).
-// S tile db holds S[16*db + 4*g4 + i][c0 + r16].
-// ---------------------------------------------------------------------------------------
-template <typename TIn, typename TG, int DK, bool OUT>
-__device__ void chunk_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int c0, int64_t tc, int nv,
-                                int g4, int r16, f32x4 (&S)[DK / 16]) {
-    constexpr int NDB = DK / 16;
-    for (int t = 0; t < nv; ++t) {
-        const int64_t tt = tc + t;
-        const bool unclamped = (a.flags & 1) && (tt == wk.len - 1);
-        float dcy[NDB][4], kk[NDB][4], qq[NDB][4];
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-            const int d = 16 * db + 4 * g4;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float gg = (float)tok_row<TG>(a.g, wk, tt, h, d)[i];
-                dcy[db][i] = expf(unclamped ? gg : fminf(gg, 0.f));
-                kk[db][i] = (float)tok_row<TIn>(a.k, wk, tt, h, d)[i];
-                qq[db][i] = OUT ? (float)tok_row<TIn>(a.q, wk, tt, h, d)[i] : 0.f;
-            }
-        }
-        const float vv = (float)tok_row<TIn>(a.v, wk, tt, h, c0)[r16];
-        float part = 0.f;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float s = dcy[db][i] * S[db][i] + kk[db][i] * vv;
-                S[db][i] = s;
-                part += qq[db][i] * s;
-            }
-        if (OUT) {
-            part += __shfl_xor(part, 16);
-            part += __shfl_xor(part, 32);
-            // o may alias g (the reference's VectorisedGLA passes out=g): every wave has read
-            // token tt's gates before any wave overwrites them with outputs
-            __syncthreads();
-            if (g4 == 0) {
-                const int64_t off = wk.b * a.o_sb + (wk.row0 + tt) * a.o_st + h * a.o_sh + c0 + r16;
-                char* op = reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt);
-                if (a.o_dt == DT_F32) *reinterpret_cast<float*>(op) = part;
-                else if (a.o_dt == DT_BF16) *reinterpret_cast<__bf16*>(op) = (__bf16)part;
-                else *reinterpret_cast<_Float16*>(op) = (_Float16)part;
-            }
-        }
-    }
-}
-
-// Outputs of one chunk for a wave's 16 columns (lane (g4, r16) holds O[token 16*tb + r16]
-// [columns 4*g4 .. 4*g4+3]), kept in registers until the next chunk has issued its loads.  On gfx9
-// one counter tracks loads and stores, and a wait for a load while a store is outstanding drains
-// both; stores issued right after the next loads are long complete when those loads are waited
-// for, one chunk later.
-struct PendingOut {
-    f32x4 o[4];
-    int64_t tc;
-    int nv;
-    bool valid;
-};
-
-// Stage the pending outputs 16 tokens at a time through `stage` (this wave's 16 x OS floats of
-// LDS) and store them with the four lanes of a quad covering one token's 16 columns.
-template <bool OBF>
-__device__ __forceinline__ void flush_out(const PrefillParams& a, const Work& wk, int64_t h, int c0, const PendingOut& p,
-                                          float* stage, int os) {
-    const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
-    const int es = dt_size(a.o_dt);
-    const int64_t ost = a.o_st * es;
-    char* obase = reinterpret_cast<char*>(a.o) + uniform_i64((wk.b * a.o_sb + (wk.row0 + p.tc) * a.o_st + h * a.o_sh + c0) * es);
-    const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);  // token within 16
-    const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
-    const OutRsrc orr = out_rsrc(obase, ost, es, p.nv, a.o_dt == DT_F32);
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-        *reinterpret_cast<f32x4*>(stage + r16 * os + 4 * g4) = p.o[tb];
-        const f32x4 x = *reinterpret_cast<const f32x4*>(stage + tq * os + 4 * q);
-        if constexpr (OBF) {  // bf16 outputs known at compile time: one store of four packed values
-            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-            const u32x2 w = __builtin_bit_cast(u32x2, bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]});
-            __builtin_amdgcn_raw_buffer_store_b64(w, orr.lo, (int32_t)(16 * tb * ost) + olane, 0, 0);
-        } else {
-            out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, x);
-        }
-    }
-}
-
-// CK: checked row addressing (see chunk_load); without it the loads zero rows past the chunk.
-template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF = false>
-struct OutStep {
-    using L = Lay<TIn, DK, DV, true>;
-    using PR = Prec<TIn>;
-    static constexpr int NW = L::NW, DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NKS = DK / 32;
-    static constexpr int NS = PR::NS, NX = PR::NX;
-
-    // One chunk: stage 1 (factors, split operands -> LDS), stage 2 (A^T tiles), stage 3 (O, S).
-    // after_inputs() runs once stage 1 has consumed `cur` (it may refill those registers).
-    // FAST_ONLY: a chunk that needs the token-by-token path returns false right after stage 1
-    // (its inputs consumed, the next chunk's loads issued, the pending outputs stored) and the
-    // caller finishes it with finish_tokenwise; otherwise both paths are handled here.
-    template <bool FAST_ONLY, typename Hook>
-    __device__ static bool run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, PendingOut& pend,
-                               Hook&& after_inputs) {
-        const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
-        const int tg = lane >> 2, row = lane & 3;
-        const int d0 = wave * DPW, c0 = wave * 16;
-        const int dl0 = d0 + DL * row;  // first key dim of this lane in stage 1
-        char* sQT = smem + L::OFF_QT;
-        char* sKT = smem + L::OFF_KT;
-        char* sAT = smem + L::OFF_AT;
-        char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
-        float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
-        float* sEG = sEM + DK;
-        int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
-        const bool tail_unclamped = (a.flags & 1) && (tc + nv == wk.len);
-
-        // ---------------- stage 1 -------------------------------------------------------
-        {
-            float G[4][DL], GC[DL], x[4][DL];
-            chunk_float<CK>(cur.g, G, tg, nv);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int i = 0; i < DL; ++i) G[j][i] = min0(G[j][i]);
-            chunk_cumsum<DL>(G, GC, lane);
-            bool bad = tail_unclamped;
-#pragma unroll
-            for (int i = 0; i < DL; ++i) bad |= !(GC[i] >= -SPAN_MAX);
-            float mh[DL];  // -m log2(e), m = GC / 2
-#pragma unroll
-            for (int i = 0; i < DL; ++i) mh[i] = -0.5f * LOG2E * GC[i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int i = 0; i < DL; ++i) G[j][i] = __builtin_amdgcn_exp2f(fmaf(G[j][i], LOG2E, mh[i]));  // exp(G - m)
-            if (tg == 0) {
-#pragma unroll
-                for (int i = 0; i < DL; ++i) {
-                    const float em = fast_exp(0.5f * GC[i]);
-                    sEM[dl0 + i] = em;
-                    sEG[dl0 + i] = em * em;
-                }
-            }
-            const bool any_bad = __any(bad);
-            if (lane == 0) sFLAG[wave] = any_bad ? 1 : 0;
-            // Qt rows
-            chunk_float<CK>(cur.q, x, tg, nv);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int i = 0; i < DL; ++i) x[j][i] *= G[j][i];
-                lds_put_row<NS, DL>(sQT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
-            }
-            // Kt rows (stage 2 reads them as rows, the state update through the transposed read)
-            chunk_float<CK>(cur.k, x, tg, nv);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int i = 0; i < DL; ++i) x[j][i] *= __builtin_amdgcn_rcpf(G[j][i]);
-                lds_put_row<NS, DL>(sKT, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
-            }
-            // V rows: tokens 4*tg + j, this wave's columns 4*row .. 4*row+3
-            lds_put_v_rows<TIn, NX, CK>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
-        }
-        // The next chunk's loads go out now and fly during stages 2-3, except at (128, 128),
-        // where their registers would push the wave past 256 VGPRs: there they go out after stage 3.
-        constexpr bool late_refill = DK == 128 && DV == 128;
-        if constexpr (!late_refill) after_inputs();
-        // The previous chunk's outputs, staged through this wave's slice of the A^T planes
-        // (nothing reads them again before this chunk's stage 2).
-        if (pend.valid) flush_out<OBF>(a, wk, h, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
-        pend.valid = false;
-        __syncthreads();
-        bool fast = true;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
-
-        if constexpr (FAST_ONLY) {
-            if (!fast) return false;
-        }
-        if (!FAST_ONLY && !fast) {
-            chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, c0, tc, nv, g4, r16, S);
-        } else {
-            // ---------------- stage 2: causal tiles of A^T -> LDS ----------------------------
-            // Wave w owns tiles w, w + NW, ...: all of them are computed together (independent
-            // MFMA chains); a wave with one tile fewer recomputes its last tile and skips the store.
-            {
-                constexpr int MT = (10 + NW - 1) / NW;
-                int sb[MT], tb[MT];
-                f32x4 acc[MT];
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    tile_sb_tb(min(wave + t * NW, 9), sb[t], tb[t]);
-                    acc[t] = zero4();
-                }
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    Split8<NS> kf[MT], qf[MT];
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) {
-                        kf[t] = lds_frag<NS>(sKT, L::ROWP, L::RS, 16 * sb[t] + r16, 32 * ks, g4);
-                        qf[t] = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb[t] + r16, 32 * ks, g4);
-                    }
-#pragma unroll
-                    for (int t = 0; t < MT; ++t) acc[t] = mfma_split<NS, NS, NS>(kf[t], qf[t], acc[t]);
-                }
-                // causal mask of a diagonal tile (row = key 4*g4 + j, column = query r16) as factors
-                f32x4 diag;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) diag[j] = (4 * g4 + j > r16) ? 0.f : 1.f;
-#pragma unroll
-                for (int t = 0; t < MT; ++t) {
-                    const int i = wave + t * NW;
-                    if (i >= 10) continue;
-                    const f32x4 m = sb[t] == tb[t] ? diag : f32x4{1.f, 1.f, 1.f, 1.f};
-                    const float x[4] = {acc[t][0] * m[0], acc[t][1] * m[1], acc[t][2] * m[2], acc[t][3] * m[3]};
-                    lds_put_row<NS, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
-                }
-            }
-            __syncthreads();
-
-            // ---------------- stage 3: outputs and state for columns [c0, c0+16) ------------
-            Split8<NX> vf[2];
-#pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
-            f32x4 Ot[4];
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) Ot[tb] = zero4();
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) {  // (exp(m) S)^T Qt^T
-                const f32x4 e0 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 4 * g4);
-                const f32x4 e1 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 16 + 4 * g4);
-                float x[8];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    x[i] = S[2 * ks][i] * e0[i];
-                    x[4 + i] = S[2 * ks + 1][i] * e1[i];
-                }
-                const Split8<NS> sf = split8<NS>(x);
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
-                    Ot[tb] = mfma_split<NS, NS, NS>(sf, qf, Ot[tb]);
-                }
-            }
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {  // V^T A^T over key blocks <= tb
-#pragma unroll
-                for (int k2 = 0; k2 < 2; ++k2) {
-                    if (2 * k2 > tb) continue;
-                    const int i0 = tile_index(2 * k2, tb);
-                    const bool has_hi = 2 * k2 + 1 <= tb;
-                    const int i1 = has_hi ? tile_index(2 * k2 + 1, tb) : i0;
-                    Split8<NS> af;
-#pragma unroll
-                    for (int pl = 0; pl < NS; ++pl) {
-                        const __bf16* p = reinterpret_cast<const __bf16*>(sAT + pl * L::ATP);
-                        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
-                        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
-                        const __bf16 z = (__bf16)0.f;
-                        af.p[pl] = has_hi ? bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}
-                                          : bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
-                    }
-                    Ot[tb] = mfma_split<NX, NS, NS>(vf[k2], af, Ot[tb]);
-                }
-            }
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {  // S <- exp(G_C) S + exp(m) Kt^T V
-                f32x4 P = zero4();
-#pragma unroll
-                for (int k2 = 0; k2 < 2; ++k2) {
-                    const Split8<NS> kf = lds_frag_tr<NS>(sKT, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
-                    P = mfma_split<NS, NX, NS>(kf, vf[k2], P);
-                }
-                const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
-                const f32x4 eg = *reinterpret_cast<const f32x4*>(sEG + 16 * db + 4 * g4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) S[db][i] = eg[i] * S[db][i] + em[i] * P[i];
-            }
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) pend.o[tb] = Ot[tb];
-            pend.tc = tc;
-            pend.nv = nv;
-            pend.valid = true;
-            if constexpr (!L::DEFER) {  // store now, staged through this wave's own V planes
-                flush_out<OBF>(a, wk, h, c0, pend, reinterpret_cast<float*>(sVP), L::OS);
-                pend.valid = false;
-            }
-        }
-        if constexpr (late_refill) after_inputs();
-        __syncthreads();  // the next chunk rewrites LDS
-        return true;
-    }
-
-    // The rest of a chunk that run<true> returned false for.
-    template <typename Hook>
-    __device__ static void finish_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                                            f32x4 (&S)[NDB], Hook&& after_inputs) {
-        const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
-        chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, wave_id() * 16, tc, nv, g4, r16, S);
-        constexpr bool late_refill = DK == 128 && DV == 128;
-        if constexpr (late_refill) after_inputs();
-        __syncthreads();
-    }
-};
-
-// Outputs of one segment from its carried-in state S (K3).
-template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF>
-__device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
-    using St = OutStep<TIn, TG, DK, DV, CK, OBF>;
-    constexpr int DL = St::DL;
-    const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
-    const ChunkAddr ad = chunk_addr<true, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
-    const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
-    auto chunk_nv = [&](int64_t c) {
-        const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
-        return (int)(r < CHUNK ? r : CHUNK);
-    };
-    auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
-    // One register set: stage 1 consumes it and the next chunk's loads refill it at once, so they
-    // are in flight during stages 2-3 (registers go to occupancy instead of a second set).
-    ChunkIn<TIn, TG, DL> A;
-    chunk_load<true, CK>(A, ad, tok(0), true);
-    PendingOut pend;
-    pend.valid = false;
-    // Chunks take the MFMA path until one needs the token-by-token path (a decay span beyond the
-    // factored range, or the unclamped tail); from there a loop that handles both finishes the
-    // segment.  The fast loop has no merge with the token-wise code, so its state registers stay put.
-    int64_t c = 0;
-    for (; c < nch; ++c)
-        if (!St::template run<true>(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
-                                    [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); }))
-            break;
-    if (c < nch) {
-        St::finish_tokenwise(a, wk, h, tok(c), chunk_nv(c), S,
-                             [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
-        for (++c; c < nch; ++c)
-            St::template run<false>(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
-                                    [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
-    }
-    if (pend.valid)  // after the last chunk's closing barrier the A^T planes are free
-        flush_out<OBF>(a, wk, h, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
-                  St::L::OS);
-}
-
-// ---------------------------------------------------------------------------------------
-// Segment-local end state, chunks walked last to first.  With the decay of the later chunks
-// (sfx) known, every token's weight exp(sfx + G_C - G_t) = exp(decay from after t to the segment
-// end) is at most 1 (or e^{g} of an unclamped tail token), so the state accumulates directly in
-// the MFMA accumulators:  L += (k * weight)^T V  - no per-chunk rescale, no overflow guard.
-// L tile db holds L[16*db + 4*g4 + i][16*w + r16]; Gseg[i] = summed log-decay of key dim
-// d0 + DL*row + i of the segment.
-// ---------------------------------------------------------------------------------------
-template <typename TIn, typename TG, int DK, int DV, bool CK>
-struct StateStep {
-    using L = Lay<TIn, DK, DV, false>;
-    using PR = Prec<TIn>;
-    static constexpr int DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NS = PR::NS, NX = PR::NX;
-
-    template <typename Hook>
-    __device__ static void run(const PrefillParams& a, const Work& wk, int64_t tc, int nv,
-                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&Lst)[NDB], float (&Gseg)[DL], char* smem,
-                               Hook&& after_inputs) {
-        const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
-        const int tg = lane >> 2, row = lane & 3;
-        const int dl0 = wave * DPW + DL * row;
-        char* sKW = smem + L::OFF_KT;  // exp-weighted k rows
-        char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
-        {
-            float G[4][DL], GC[DL], x[4][DL];
-            chunk_float<CK>(cur.g, x, tg, nv);
-            const bool tail_chunk = (a.flags & 1) && (tc + nv == wk.len);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bool unclamped = tail_chunk && (4 * tg + j == nv - 1);
-#pragma unroll
-                for (int i = 0; i < DL; ++i) G[j][i] = unclamped ? x[j][i] : min0(x[j][i]);
-            }
-            float X[4][DL];
-            chunk_suffix<DL>(G, X, GC, lane);
-            chunk_float<CK>(cur.k, x, tg, nv);
-            float gs[DL];  // Gseg log2(e)
-#pragma unroll
-            for (int i = 0; i < DL; ++i) gs[i] = Gseg[i] * LOG2E;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int i = 0; i < DL; ++i) x[j][i] *= __builtin_amdgcn_exp2f(fmaf(X[j][i], LOG2E, gs[i]));
-                lds_put_row<NS, DL>(sKW, L::ROWP, (4 * tg + j) * L::RS + dl0, x[j]);
-            }
-#pragma unroll
-            for (int i = 0; i < DL; ++i) Gseg[i] += GC[i];
-            lds_put_v_rows<TIn, NX, CK>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
-        }
-        after_inputs();
-        __syncthreads();
-        Split8<NX> vf[2];
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                const Split8<NS> kf = lds_frag_tr<NS>(sKW, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
-                Lst[db] = mfma_split<NS, NX, NS>(kf, vf[k2], Lst[db]);
-            }
-        __syncthreads();  // the next chunk rewrites LDS
-    }
-};
-
-template <typename TIn, typename TG, int DK, int DV, bool CK>
-__device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&Lst)[DK / 16],
-                                   float (&Gseg)[DK / (DV / 16) / 4], char* smem) {
-    using St = StateStep<TIn, TG, DK, DV, CK>;
-    constexpr int DL = St::DL;
-    const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
-    const ChunkAddr ad = chunk_addr<false, TIn, TG>(a, wk, h, tg, wave * St::DPW + DL * row, wave * 16 + 4 * row);
-    const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
-    auto chunk_nv = [&](int64_t c) {
-        const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
-        return (int)(r < CHUNK ? r : CHUNK);
-    };
-    auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
-    ChunkIn<TIn, TG, DL> A, B;
-    chunk_load<false, CK>(A, ad, tok(nch - 1), true);
-    __builtin_amdgcn_sched_barrier(0);  // issue order A, B on every path (see segment_walk)
-    chunk_load<false, CK>(B, ad, tok(nch - 2), nch > 1);
-    // pairs of chunks from the end, then chunk 0 if nch is odd (single-exit loop, as in segment_walk)
-    for (int64_t c = nch - 1; c >= 1; c -= 2) {
-        St::run(a, wk, tok(c), chunk_nv(c), A, Lst, Gseg, smem,
-                [&] { chunk_load<false, CK>(A, ad, tok(c - 2), c >= 2); });
-        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, Lst, Gseg, smem,
-                [&] { chunk_load<false, CK>(B, ad, tok(c - 3), c >= 3); });
-    }
-    if (nch & 1) St::run(a, wk, tok(0), chunk_nv(0), A, Lst, Gseg, smem, [] {});
-}
-
-
-// CK: checked row addressing (some sequence length is not a multiple of 4; see chunk_load).
-template <typename TIn, typename TG, int DK, int DV, bool CK>
-__global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams a) {
-    using L = Lay<TIn, DK, DV, false>;
-    constexpr int DL = L::DPW / 4;
-    __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
-    const int64_t w = blockIdx.x, h = blockIdx.y;
-    Work wk;
-    if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
-    f32x4 S[DK / 16];
-    float Gseg[DL];
-#pragma unroll
-    for (int db = 0; db < DK / 16; ++db) S[db] = zero4();
-#pragma unroll
-    for (int i = 0; i < DL; ++i) Gseg[i] = 0.f;
-    segment_state_walk<TIn, TG, DK, DV, CK>(a, wk, h, S, Gseg, smem);
-    float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
-#pragma unroll
-    for (int db = 0; db < DK / 16; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st[state_off(db, i, g4, r16, wave, DV)] = S[db][i];
-    if (lane < 4) {  // tg = 0, row = lane: key dims wave*DPW + DL*row + i
-        float* gs = a.ws_gamma + (w * a.H + h) * (int64_t)DK + wave * L::DPW + DL * lane;
-#pragma unroll
-        for (int i = 0; i < DL; ++i) gs[i] = Gseg[i];
-    }
-}
-
-template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF>
-__global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void gla_seg_output_kernel(PrefillParams a) {
-    using L = Lay<TIn, DK, DV, true>;
-    __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
-    const int64_t w = blockIdx.x, h = blockIdx.y;
-    Work wk;
-    if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
-    f32x4 S[DK / 16];
-    const float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
-#pragma unroll
-    for (int db = 0; db < DK / 16; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, DV)];
-    segment_walk<TIn, TG, DK, DV, CK, OBF>(a, wk, h, S, smem);
-}
 
 // K0 (varlen): segment offsets from cu_seqlens, one thread block.
 __global__ __launch_bounds__(256) void gla_varlen_plan_kernel(const int32_t* cu, int64_t n_seqs, int P,

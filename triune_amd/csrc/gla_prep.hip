@@ -49,20 +49,6 @@ __device__ __forceinline__ void st8(T* p, const float (&x)[8]) {
     *reinterpret_cast<V4<T>*>(p + 4) = b;
 }
 
-__device__ __forceinline__ float elu1(float x) { return x >= 0.f ? x + 1.f : fast_exp(x); }
-
-// min(x, 0) - log(1 + e^-|x|) with the hardware exp2 / log2: for e^-|x| below 2^-24 the log term
-// rounds to 0, an absolute error under 6e-8.
-__device__ __forceinline__ float logsigmoid(float x) {
-    return fminf(x, 0.f) - 0.6931471805599453f * __builtin_amdgcn_logf(1.f + fast_exp(-fabsf(x)));
-}
-
-__device__ __forceinline__ float sigmoid(float x) {
-    const float e = fast_exp(-fabsf(x));
-    return x >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
-}
-
-__device__ __forceinline__ float inv_norm(float sumsq) { return 1.f / sqrtf(fmaxf(sumsq, 1e-12f)); }
 
 // Sum over the 64 lanes of a wave, in every lane: DPP inclusive scans of the four 16-lane rows,
 // then the rows' last lanes read into scalars (no LDS-routed shuffle on the path).

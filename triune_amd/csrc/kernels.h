@@ -35,6 +35,10 @@ struct PrefillParams {
     TokTensor kb;
     float* ws_m;           // GDN: [n_work, H] slots of the segment transition matrices as bf16 parts
     float* ws_spare;       // [n_seqs, H, Dk, Dv] sink for the segment scan's padding steps
+    // Prefill with the VectorisedGLA pre-processing applied in stage 1 (q, k, g raw projections):
+    // fp32 RoPE tables [T, Dk] (row = token of the sequence, token stride cs.st; sb = sh = 0)
+    TokTensor cs, sn;
+    int use_rope;
 };
 
 struct ScanParams {
@@ -177,6 +181,9 @@ hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt,
 int gdn_seg_out_blocks_per_cu(int io_dt, bool ck);
 bool prefill_shape_supported(int Dk, int Dv);
 bool prefill_dtype_supported(int Dk, int Dv, int io_dt);
+// the segment-state kernel that also pre-processes q, k, g in place (gla_prefill_prep.hip)
+bool prefill_prep_supported(int D, int io_dt);
+hipError_t launch_gla_prep_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 int gla_seg_output_blocks_per_cu(int Dk, int Dv, bool ck);
 
 }  // namespace triune

@@ -10,6 +10,10 @@ _fused_qkvg_decode_step_kernel) and the way attention.py:405-450 launches them:
   fused_qkvg_decode_step(qkvg, cos, sin, initial_state, save_final, use_rope)
       qkvg [B, 4, H, HD] raw projections of one token per sequence; returns (out [B, 1, H, HD],
       final state [B, H, HD, HD] or None), with decay sigmoid(g).
+  fused_qkv_g_prep_chunk_gla(qkv, g, cos, sin, initial_state, out, save_final, use_rope)
+      fused_qkv_g_prep_inplace followed by _triton_chunk_gla_tc_fwd(qkv[:, :, 0], qkv[:, :, 1],
+      qkv[:, :, 2], g, initial_state, out=g), with the pre-processing done by the prefill's
+      segment-state kernel as it reads q, k, g (same in-place results, one pass fewer).
 
 normalize(a) = a / sqrt(max(sum a^2, 1e-12)) over the HD elements of a (token, head) row; RoPE
 pairs element d with d + HD/2.  HD in {32, 64, 128}.  Tensors must be on the GPU; there is no CPU
@@ -22,7 +26,7 @@ import torch
 
 from ._lib import check, dtype_code, lib, ptr, stream_of, strides
 
-__all__ = ["fused_qkv_g_prep_inplace", "fused_qkvg_decode_step"]
+__all__ = ["fused_qkv_g_prep_inplace", "fused_qkvg_decode_step", "fused_qkv_g_prep_chunk_gla"]
 
 _HD = (32, 64, 128)
 
@@ -121,3 +125,81 @@ def fused_qkvg_decode_step(qkvg: torch.Tensor, cos=None, sin=None, initial_state
     )
     check(rc, "triune_hip_gla_fused_decode_step")
     return out, s_out
+
+
+def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin=None, initial_state=None, out=None,
+                               save_final: bool = True, use_rope: bool = True):
+    """VectorisedGLA's prefill (attention.py:425-451): _fused_qkv_g_prep_inplace_kernel, then
+    _triton_chunk_gla_tc_fwd(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, initial_state, out=g).
+    triune_hip_gla_prefill_prep does the pre-processing inside the prefill's segment-state kernel:
+    it reads the raw q, k, v, g once, writes q, k <- RoPE(normalize(elu(x) + 1)) and
+    g <- logsigmoid(g) back in place (rounded to the I/O dtype, as the reference's prep kernel
+    leaves them) and forms the segment states from those values; the output kernel then reads the
+    processed tensors.
+
+    The fused form runs while the call is small enough for the chunk kernels to be latency-bound
+    (B * H * ceil(T / 64) at most 4 per compute unit, as at VectorisedGLA's 1024-token prefill tiles,
+    attention.py:458-499: 34.6 against 39.4 us for the two-step pipeline at B = 4, H = 6, T = 1024
+    on MI355X).  Past that the kernels are throughput-bound and the pre-processing work weighs more
+    inside the segment-state kernel than as a pass of its own (at T = 16384: 217 against 183 us), so
+    larger calls run fused_qkv_g_prep_inplace and then the prefill, with the same results.
+
+    qkv: [B, T, 3, H, HD] raw projections (bf16 or fp16), g: [B, T, H, HD] raw gate (same dtype),
+    cos/sin: [T, HD] (used when use_rope; converted to fp32 if needed), initial_state: [B, H, HD,
+    HD] or None.  out: [B, T, H, HD] output buffer (default: g's buffer, as the reference writes
+    the outputs over g).  HD in {32, 64, 128}.  Returns (out, final state fp32 [B, H, HD, HD], or a
+    1-element placeholder when save_final is False, as the reference)."""
+    _cuda(qkv, g, cos, sin, initial_state, out)
+    if qkv.dim() != 5 or qkv.shape[2] != 3 or g.dim() != 4:
+        raise ValueError("qkv must be [B, T, 3, H, HD] and g [B, T, H, HD]")
+    B, T, _, H, HD = qkv.shape
+    if tuple(g.shape) != (B, T, H, HD):
+        raise ValueError(f"g shape {tuple(g.shape)} does not match qkv {tuple(qkv.shape)}")
+    if HD not in _HD:
+        raise ValueError(f"head dim {HD} not supported (32, 64 or 128)")
+    if qkv.dtype not in (torch.bfloat16, torch.float16) or g.dtype != qkv.dtype:
+        raise TypeError("qkv and g must share one 16-bit dtype (bfloat16 or float16)")
+    from .fast_gla import _tok3, _triton_chunk_gla_tc_fwd, _vec_layout
+
+    if B * H * ((T + 63) // 64) > 4 * torch.cuda.get_device_properties(qkv.device).multi_processor_count:
+        fused_qkv_g_prep_inplace(qkv, g, cos, sin, use_rope=use_rope)
+        return _triton_chunk_gla_tc_fwd(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, initial_state=initial_state,
+                                        out=g if out is None else out, save_final=save_final)
+    views = [qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g]
+    q, k, v, gp = (_vec_layout(x, 1) for x in views)  # copies only for unaligned layouts
+    if out is None:
+        out = g
+    if tuple(out.shape) != (B, T, H, HD):
+        raise ValueError("out must be [B, T, H, HD]")
+    o = out if _vec_layout(out, 1) is out else torch.empty(B, T, H, HD, device=qkv.device, dtype=out.dtype)
+    cs_st = 0
+    if use_rope:
+        if cos is None or sin is None:
+            raise ValueError("use_rope needs cos and sin")
+        if tuple(cos.shape) != (T, HD) or tuple(sin.shape) != (T, HD):
+            raise ValueError("cos and sin must be [T, HD]")
+        cos, sin = (_vec_layout(x.to(torch.float32), 0) for x in (cos, sin))
+        if cos.stride(0) != sin.stride(0):
+            sin = sin.contiguous()
+            cos = cos.contiguous()
+        cs_st = cos.stride(0)
+    s0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    sf = torch.empty(B, H, HD, HD, device=qkv.device, dtype=torch.float32) if save_final else None
+    L = lib()
+    wsb = L.triune_hip_gla_prefill_workspace_size(B, T, H, HD, HD, 0)
+    ws = torch.empty(max(int(wsb), 256), device=qkv.device, dtype=torch.uint8)
+    st = strides(_tok3(q), _tok3(k), _tok3(v), _tok3(gp), _tok3(o))
+    rc = L.triune_hip_gla_prefill_prep(
+        ptr(q), ptr(k), ptr(v), ptr(gp), dtype_code(q), st, ptr(cos) if use_rope else None,
+        ptr(sin) if use_rope else None, cs_st, 1 if use_rope else 0, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
+        B, T, H, HD, ptr(ws), ws.numel(), stream_of(qkv),
+    )
+    check(rc, "triune_hip_gla_prefill_prep")
+    for dst, src in zip(views, (q, k, v, gp)):  # the in-place results reach copied inputs too
+        if src is not dst and not (src is gp and o.data_ptr() == gp.data_ptr()):
+            dst.copy_(src)
+    if o is not out:
+        out.copy_(o)
+    if sf is None:
+        sf = torch.empty((1,), device=qkv.device, dtype=torch.float32)
+    return out, sf
