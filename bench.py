@@ -283,25 +283,43 @@ def bench_fused_decode(steps_total, dev, n_bufs=12):
 
 
 def bench_gdn(dev, reps=20):
-    """Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta and decay)."""
+    """Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta, one decay per
+    token and head).  The gate reaches the operator as config 3 states it, broadcast over D (a
+    stride-0 view: the scalar-decay kernels); the same pass with the gate copied out to a full
+    [B, T, H, D] tensor (the per-key-dim kernels) is reported beside it."""
     from triune_amd import fast_chunk_gated_deltanet
-    from triune_amd.workloads import config3
+    from triune_amd.workloads import config3, to_device
 
-    q, k, v, g, beta = (x.to(dev) for x in config3())
-    fn = lambda: fast_chunk_gated_deltanet(q, k, v, g, beta=beta)  # noqa: E731
-    for _ in range(20):
-        fn()
-    torch.cuda.synchronize()
-    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    q, k, v, g, beta = config3()
+    q, k, v, beta = (x.to(dev) for x in (q, k, v, beta))
+    gv = to_device(g, dev)
+    gm = gv.contiguous()
     B, T, H, D = q.shape
-    # the operator's tensors: q, k, v, g (g broadcast to [B, T, H, D] at the reference surface) and
-    # per-head beta read, o written, all bf16; zero initial state, fp32 final state
-    alg = B * T * H * (5 * D * 2 + 2) + B * H * D * D * 4
+
+    def timed(gate):
+        fn = lambda: fast_chunk_gated_deltanet(q, k, v, gate, beta=beta)  # noqa: E731
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        return _events_time_ms(fn, reps, torch.cuda.current_stream())
+
+    ms = timed(gv)
+    ms_dim = timed(gm)
+    # the operator's tensors: q, k, v read, o written (bf16), one gate and one beta per
+    # (token, head) read (bf16); zero initial state, fp32 final state written
+    alg = B * T * H * (4 * D * 2 + 2 + 2) + B * H * D * D * 4
+    # with the gate materialised per key dim it is read as a [B, T, H, D] bf16 tensor
+    alg_dim = B * T * H * (5 * D * 2 + 2) + B * H * D * D * 4
     gbs = alg / (ms * 1e-3) / 1e9
-    return {"workload": "Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16)",
+    return {"workload": "Gated DeltaNet prefill, config 3 (B=4, H=6, T=8192, D=64, bf16, scalar decay)",
             "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "kernels": "gdn_sg_seg_mn + gdn_seg_scan + gdn_sg_seg_out",
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)},
+            "per_dim_gate": {"ms": round(ms_dim, 4), "tok_s": round(B * T / (ms_dim * 1e-3), 1),
+                             "alg_bytes": alg_dim,
+                             "kernels": "gdn_seg_mn + gdn_seg_scan + gdn_seg_out",
+                             "frac": round(alg_dim / (ms_dim * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
 def bench_varlen(dev, reps=5):

@@ -39,6 +39,8 @@
  *                                     with _triton_gated_deltanet_fwd (fast_gla.py:479-550) and
  *                                     fast_recurrent_gated_deltanet (fast_gla.py:781-836)
  *   triune_hip_gdn_prefill_chunked <- the same operator (fast_gla.py:839-904), chunked form
+ *   triune_hip_gdn_prefill_scalar_decay <- the same operator with g broadcast over the head dim
+ *                                     (one decay per token and head), chunked form
  *   triune_hip_gla_qkvg_prep       <- _fused_qkv_g_prep_inplace_kernel, triune/model/attention.py:14-79
  *   triune_hip_gla_fused_decode_step <- _fused_qkvg_decode_step_kernel, triune/model/attention.py:81-179
  */
@@ -274,6 +276,22 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
                                    const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
                                    int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
                                    size_t workspace_bytes, void* stream);
+
+/* The chunked Gated DeltaNet forward for a gate that is one value per (token, head): the
+ * scalar-decay form, which reaches the reference operator as g broadcast over the head dim
+ * (g.expand(B, T, H, HD), read with its head-dim stride by the Triton kernel, fast_gla.py:464).
+ * Same arguments and results as triune_hip_gdn_prefill_chunked except that g is [B, T, H]:
+ * element (b, t, h) at strides[9..11] (non-negative, any token stride, element-aligned pointer),
+ * and beta_kind is NONE or HEAD.  Workspace: at least
+ * triune_hip_gdn_prefill_scalar_decay_workspace_size(B, T, H, Dk, Dv) bytes (16-byte aligned).
+ * (Dk, Dv) == (64, 64).
+ * Replaces: fast_chunk_gated_deltanet (fast_gla.py:839-904) for T > 1 with a broadcast gate. */
+size_t triune_hip_gdn_prefill_scalar_decay_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv);
+int triune_hip_gdn_prefill_scalar_decay(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                        int g_dtype, const void* beta, int beta_dtype, int beta_kind,
+                                        const int64_t* strides, const float* s0, void* o, int o_dtype,
+                                        float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
+                                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* GLA input pre-processing in place (VectorisedGLA's fused path): for every (b, t, h) row of HD
  * elements, q and k <- RoPE(normalize(elu(x) + 1)) with normalize(a) = a / sqrt(max(sum a^2,

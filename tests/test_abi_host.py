@@ -123,6 +123,23 @@ def test_decode_and_gdn_and_scan_validation_errors():
     gst[16] = 32  # o's token stride below the row width
     assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, gst, None, _FAKE, 1, None, 1, 64, 1, 64, 64, None, 0,
               None) == -4
+    # scalar-decay GDN: g is [B, T, H] (any non-negative strides, element-aligned), beta none or per token
+    sg = lib.triune_hip_gdn_prefill_scalar_decay
+    sst = (ctypes.c_int64 * 18)(*([64 * 64, 64, 64] * 3 + [64, 1, 0] + [0, 0, 0] + [64 * 64, 64, 64]))
+    args = lambda g, bk, dk, sts: (_FAKE, _FAKE, _FAKE, g, 1, 1, _FAKE if bk else None, 1, bk, sts, None, _FAKE,  # noqa: E731
+                                    1, None, 1, 64, 1, dk, dk, None, 0, None)
+    assert sg(*args(_FAKE, 0, 64, sst)) == -5  # valid, no workspace
+    assert sg(*args(_FAKE, 1, 64, sst)) == -5  # per-token beta
+    assert sg(*args(_FAKE, 2, 64, sst)) == -2  # per-key-dim beta needs the per-dim kernels
+    assert sg(*args(_FAKE, 0, 128, sst)) == -2
+    assert sg(*args(ctypes.c_void_p(0x1001), 0, 64, sst)) == -4  # gate pointer not element-aligned
+    sst[10] = -1
+    assert sg(*args(_FAKE, 0, 64, sst)) == -4
+    sst[10] = 0  # one gate for every token: allowed
+    assert sg(*args(_FAKE, 0, 64, sst)) == -5
+    assert sg(*args(None, 0, 64, sst)) == -1
+    assert lib.triune_hip_gdn_prefill_scalar_decay_workspace_size(4, 8192, 6, 64, 64) > 0
+    assert lib.triune_hip_gdn_prefill_scalar_decay_workspace_size(4, 8192, 6, 128, 128) == 0
     sc = lib.triune_hip_recurrent_scan_fwd
     assert sc(None, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -1
     assert sc(_FAKE, 0, _FAKE, 0, None, 0, _FAKE, _FAKE, 0, 1, 1, 4, 8, 6, None) == -2

@@ -15,7 +15,7 @@ import torch
 from oracle import oracle as O
 from triune_amd import fast_chunk_gated_deltanet, fast_chunk_gla, fast_chunk_gla_varlen
 from triune_amd.serving import GLADecodeGraphRunner
-from triune_amd.workloads import config1, config2, config3, config4, ulp_bf16
+from triune_amd.workloads import config1, config2, config3, config4, to_device, ulp_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -85,23 +85,28 @@ def test_config2_full_decode_graph_runner(dev):
     runner.release()
 
 
-def test_config3_full_gdn(dev):
-    """Gated DeltaNet, B=4, H=6, T=8192, D=64, bf16, per-head beta and decay, zero S0."""
+@pytest.mark.parametrize("gate", ["broadcast", "materialised"])
+def test_config3_full_gdn(dev, gate):
+    """Gated DeltaNet, B=4, H=6, T=8192, D=64, bf16, per-head beta and decay, zero S0: the gate as
+    config 3 gives it (a broadcast view: the scalar-decay kernels) and copied out to a full
+    [B, T, H, D] tensor (the per-key-dim chunked kernels)."""
     q, k, v, g, beta = config3()
     ro, rs = O.gdn_fwd(q, k, v, g, beta, None)
     ro, rs = torch.from_numpy(ro), torch.from_numpy(rs)
-    args = [x.to(dev) for x in (q, k, v, g)]
+    args = [x.to(dev) for x in (q, k, v)]
+    args.append(to_device(g, dev) if gate == "broadcast" else g.to(dev).contiguous())
+    assert (args[-1].stride(-1) == 0) == (gate == "broadcast")
     bd = beta.to(dev)
     o32, s32 = fast_chunk_gated_deltanet(*args, beta=bd, out_dtype=torch.float32)
     torch.cuda.synchronize()
     e_o, e_s = _max_err(o32.cpu(), ro), _max_err(s32.cpu(), rs)
-    print(f"config3 fp32-out: o {e_o:.3e} S {e_s:.3e}", flush=True)
+    print(f"config3 {gate} fp32-out: o {e_o:.3e} S {e_s:.3e}", flush=True)
     assert e_o <= TOL16 and e_s <= TOL16
     ob, sb = fast_chunk_gated_deltanet(*args, beta=bd)
     torch.cuda.synchronize()
     assert ob.dtype == torch.bfloat16
     ex = _bf16_excess(ob.cpu(), ro)
-    print(f"config3 bf16-out: excess {ex:.3e}", flush=True)
+    print(f"config3 {gate} bf16-out: excess {ex:.3e}", flush=True)
     assert ex <= 0.0 and _max_err(sb.cpu(), rs) <= TOL16
 
 

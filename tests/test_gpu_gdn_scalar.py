@@ -1,0 +1,138 @@
+"""GPU parity of the scalar-decay Gated DeltaNet kernels (one log-decay per token and head).
+
+The reference operator takes g as [B, T, H, HD] (fast_gla.py:839-904) and its Triton kernel reads g
+with the tensor's own head-dim stride (fast_gla.py:464), so a per-(token, head) decay reaches it
+as g broadcast over HD.  Such a gate -- a stride-0 view, or [B, T, H] / [B, T, H, 1] -- takes the
+scalar-decay kernels here; every case is checked against the fp64 token-serial oracle with the
+gate broadcast, at 1e-5 for fp32 I/O and at one bf16 ULP plus 2e-3 per element for bf16 outputs."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import triune_amd.fast_gla as FG
+from oracle import oracle as O
+from triune_amd import fast_chunk_gated_deltanet
+from triune_amd.workloads import config3, to_device, ulp_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+def _err(a, b):
+    return float(np.abs(np.asarray(a, dtype=np.float64) - np.asarray(b, dtype=np.float64)).max())
+
+
+def _bf16_excess(o_bf16, ref):
+    """max over elements of |o - ref| - (1 bf16 ULP of ref + 2e-3); <= 0 passes."""
+    ref = torch.as_tensor(ref).double()
+    return float(((o_bf16.double() - ref).abs() - (ulp_bf16(ref).double() + 2e-3)).max())
+
+
+def _case(B, T, H, D, kind, seed, gate_lo=-0.2, gate_hi=0.0, init=True):
+    gen = torch.Generator().manual_seed(seed)
+    q = F.normalize(torch.randn(B, T, H, D, generator=gen), dim=-1)
+    k = F.normalize(torch.randn(B, T, H, D, generator=gen), dim=-1)
+    v = torch.randn(B, T, H, D, generator=gen)
+    la = gate_lo + (gate_hi - gate_lo) * torch.rand(B, T, H, generator=gen)
+    s0 = 0.1 * torch.randn(B, H, D, D, generator=gen) if init else None
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen)) if kind == "head" else None
+    return q, k, v, la, beta, s0
+
+
+def _bcast(la, D):
+    return la.unsqueeze(-1).expand(*la.shape, D)
+
+
+def _run(q, k, v, g, beta, s0, dev, **kw):
+    o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g, beta=None if beta is None else beta.to(dev),
+                                     initial_state=None if s0 is None else s0.to(dev), **kw)
+    torch.cuda.synchronize()
+    return o.cpu(), s.cpu()
+
+
+@pytest.mark.parametrize("form", ["view", "bth", "bth1"])
+@pytest.mark.parametrize("kind", ["none", "head"])
+@pytest.mark.parametrize("T", [150, 200, 1000])
+def test_scalar_gdn_fp32_matches_oracle(dev, form, kind, T):
+    """fp32 I/O at 1e-5: T = 150 (checked rows, ragged tail), 200 (T % 4 == 0, partial last
+    chunk: the unchecked instance), 1000 (several chunks per segment); the three gate forms."""
+    D = 64
+    q, k, v, la, beta, s0 = _case(2, T, 2, D, kind, seed=T + len(kind) + len(form))
+    gd = la.to(dev)
+    g = {"view": _bcast(gd, D), "bth": gd, "bth1": gd.unsqueeze(-1)}[form]
+    o, s = _run(q, k, v, g, beta, s0, dev)
+    ro, rs = O.gdn_fwd(q, k, v, _bcast(la, D), beta, s0)
+    print(f"scalar gdn fp32 {form} {kind} T={T}: o {_err(o, ro):.3e} S {_err(s, rs):.3e}", flush=True)
+    assert _err(o, ro) <= 1e-5 and _err(s, rs) <= 1e-5
+
+
+@pytest.mark.parametrize("D", [16, 32])
+def test_scalar_gdn_small_head_dims(dev, D):
+    """Head dims below 64 run zero-padded to 64 (padded keys contribute nothing)."""
+    q, k, v, la, beta, s0 = _case(1, 300, 3, D, "head", seed=D)
+    o, s = _run(q, k, v, _bcast(la.to(dev), D), beta, s0, dev)
+    ro, rs = O.gdn_fwd(q, k, v, _bcast(la, D), beta, s0)
+    assert o.shape == (1, 300, 3, D) and s.shape == (1, 3, D, D)
+    assert _err(o, ro) <= 1e-5 and _err(s, rs) <= 1e-5
+
+
+def test_scalar_gdn_positive_gates_clamped(dev):
+    """Gates above 0 are clamped to 0 (no growth), as the reference's clamp(g, max=0)."""
+    q, k, v, la, beta, s0 = _case(2, 256, 2, 64, "head", seed=3, gate_lo=-0.3, gate_hi=0.3)
+    o, s = _run(q, k, v, _bcast(la.to(dev), 64), beta, s0, dev)
+    ro, rs = O.gdn_fwd(q, k, v, _bcast(la, 64), beta, s0)
+    assert _err(o, ro) <= 1e-5 and _err(s, rs) <= 1e-5
+
+
+def test_scalar_gdn_tokenwise_chunks(dev):
+    """Chunks whose total log-decay is below -SPAN_MAX, or that hold a -inf gate (a state reset),
+    run token by token inside the chunked kernels; the other chunks stay on the MFMA path."""
+    q, k, v, la, beta, s0 = _case(2, 320, 2, 64, "head", seed=11)
+    la = la.clone()
+    la[:, 64:128] = -1.0 - 20.0 * torch.rand(2, 64, 2, generator=torch.Generator().manual_seed(2))
+    la[0, 200, 1] = -float("inf")
+    o, s = _run(q, k, v, _bcast(la.to(dev), 64), beta, s0, dev)
+    ro, rs = O.gdn_fwd(q, k, v, _bcast(la, 64), beta, s0)
+    print(f"scalar gdn tokenwise chunks: o {_err(o, ro):.3e} S {_err(s, rs):.3e}", flush=True)
+    assert np.isfinite(o.numpy()).all() and np.isfinite(s.numpy()).all()
+    assert _err(o, ro) <= 1e-5 and _err(s, rs) <= 1e-5
+
+
+def test_scalar_gdn_fp16_io(dev):
+    q, k, v, la, beta, s0 = _case(2, 333, 2, 64, "head", seed=16)
+    q, k, v = (x.half() for x in (q, k, v))
+    o, s = _run(q, k, v, _bcast(la.to(dev).half(), 64), beta, s0, dev, out_dtype=torch.float32)
+    ro, rs = O.gdn_fwd(q, k, v, _bcast(la.half(), 64), beta, s0)
+    assert _err(o, ro) <= 2e-3 and _err(s, rs) <= 2e-3
+
+
+@pytest.mark.parametrize("T,B,H,with_init", [(512, 1, 3, False), (2000, 4, 6, True)])
+def test_scalar_gdn_config3_distributions_bf16(dev, T, B, H, with_init):
+    """Config-3 distributions (bf16, per-head beta, scalar decay as a broadcast view): fp32
+    outputs and states within 2e-3 of the oracle, bf16 outputs within one ULP plus 2e-3."""
+    q, k, v, g, beta = config3(T=T, B=B, H=H)
+    assert g.stride(-1) == 0
+    s0 = 0.1 * torch.randn(B, H, 64, 64, generator=torch.Generator().manual_seed(7)) if with_init else None
+    gd = to_device(g, dev)
+    assert gd.stride(-1) == 0
+    o32, s32 = _run(q, k, v, gd, beta, s0, dev, out_dtype=torch.float32)
+    ob, sb = _run(q, k, v, gd, beta, s0, dev)
+    ro, rs = O.gdn_fwd(q, k, v, g, beta, s0)
+    assert o32.dtype == torch.float32 and ob.dtype == torch.bfloat16
+    print(f"scalar gdn config3 T={T}: o32 {_err(o32, ro):.3e} S {_err(s32, rs):.3e} "
+          f"bf16 excess {_bf16_excess(ob, ro):.3e}", flush=True)
+    assert _err(o32, ro) <= 2e-3 and _err(s32, rs) <= 2e-3
+    assert _bf16_excess(ob, ro) <= 0.0
+    assert _err(sb, rs) <= 2e-3
+
+
+def test_scalar_and_per_dim_kernels_agree(dev, monkeypatch):
+    """The same broadcast gate through the scalar-decay kernels and, with them switched off,
+    through the per-key-dim chunked kernels: both approximate the same recurrence."""
+    q, k, v, g, beta = config3(T=1000, B=2, H=3)
+    gd = to_device(g, dev)
+    o1, s1 = _run(q, k, v, gd, beta, None, dev, out_dtype=torch.float32)
+    monkeypatch.setattr(FG, "_scalar_gdn_enabled", False)
+    o2, s2 = _run(q, k, v, gd, beta, None, dev, out_dtype=torch.float32)
+    assert _err(o1, o2) <= 1e-4 and _err(s1, s2) <= 1e-4

@@ -754,23 +754,25 @@ struct GdnPlan {
     size_t off_m, off_spare, total;
 };
 
-GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt) {
+// sg: the scalar-gate kernels (gdn_scalar.hip), whose output kernel has its own occupancy.
+GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt, bool sg) {
     static std::mutex mu;
     static std::map<int, int64_t> slots_cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = -1;
     int64_t slots;
-    const bool ck = T % 4 != 0;  // the instance the launch picks (launch_gdn_t)
+    const bool ck = T % 4 != 0;  // the instance the launch picks (launch_gdn_t, launch_sg_t)
     {
         std::lock_guard<std::mutex> lock(mu);
-        const int key = 8 * dev + 2 * io_dt + (ck ? 1 : 0);
+        const int key = 16 * dev + 4 * io_dt + (sg ? 2 : 0) + (ck ? 1 : 0);
         auto it = slots_cache.find(key);
         if (it == slots_cache.end()) {
             int ncu = 0;
             if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
                 ncu <= 0)
                 ncu = 256;
-            it = slots_cache.emplace(key, (int64_t)ncu * gdn_seg_out_blocks_per_cu(io_dt, ck)).first;
+            const int per_cu = sg ? gdn_sg_seg_out_blocks_per_cu(io_dt, ck) : gdn_seg_out_blocks_per_cu(io_dt, ck);
+            it = slots_cache.emplace(key, (int64_t)ncu * per_cu).first;
         }
         slots = it->second;
     }
@@ -792,16 +794,27 @@ extern "C" {
 
 size_t triune_hip_gdn_prefill_chunked_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv) {
     if (B <= 0 || T <= 0 || H <= 0 || Dk != 64 || Dv != 64) return 0;
-    return plan_gdn(B, T, H, TRIUNE_DT_BF16).total;
+    return plan_gdn(B, T, H, TRIUNE_DT_BF16, false).total;
 }
 
-int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* g, int io_dtype,
-                                   int g_dtype, const void* beta, int beta_dtype, int beta_kind,
-                                   const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
-                                   int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
+size_t triune_hip_gdn_prefill_scalar_decay_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv) {
+    if (B <= 0 || T <= 0 || H <= 0 || Dk != 64 || Dv != 64) return 0;
+    return plan_gdn(B, T, H, TRIUNE_DT_BF16, true).total;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The chunked GDN forward for both gate forms.  sg: g holds one log-decay per (token, head),
+// element (b, t, h) at strides[9..11] (any non-negative strides, element-aligned); otherwise
+// g is [B, T, H, Dk] like q and k.
+int gdn_chunked_impl(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                     const void* beta, int beta_dtype, int beta_kind, const int64_t* strides, const float* s0, void* o,
+                     int o_dtype, float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
+                     size_t workspace_bytes, void* stream, bool sg) {
     if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
-    if (beta_kind != TRIUNE_BETA_NONE && beta_kind != TRIUNE_BETA_HEAD && beta_kind != TRIUNE_BETA_KEY)
+    if (beta_kind != TRIUNE_BETA_NONE && beta_kind != TRIUNE_BETA_HEAD && (sg || beta_kind != TRIUNE_BETA_KEY))
         return TRIUNE_ERR_SHAPE;
     if (beta_kind != TRIUNE_BETA_NONE && !beta) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype) || !gate_dtype_ok(io_dtype, g_dtype) ||
@@ -809,17 +822,20 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
         (beta_kind == TRIUNE_BETA_KEY && beta_dtype != TRIUNE_DT_F32))
         return TRIUNE_ERR_DTYPE;
     if (B < 0 || T < 0 || H <= 0 || Dk != 64 || Dv != 64) return TRIUNE_ERR_SHAPE;
+    const bool g_ok = sg ? (reinterpret_cast<uintptr_t>(g) % (g_dtype == TRIUNE_DT_F32 ? 4 : 2) == 0 &&
+                            strides[9] >= 0 && strides[10] >= 0 && strides[11] >= 0)
+                         : vec_ok(g, g_dtype, strides + 9, 3);
     if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
-        !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
-        !vec_ok(o, o_dtype, strides + 15, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
-        reinterpret_cast<uintptr_t>(s_final) % 16 ||
+        !vec_ok(v, io_dtype, strides + 6, 3) || !g_ok || !vec_ok(o, o_dtype, strides + 15, 3) ||
+        reinterpret_cast<uintptr_t>(s0) % 16 || reinterpret_cast<uintptr_t>(s_final) % 16 ||
         (beta_kind == TRIUNE_BETA_KEY &&
          (!vec_ok(beta, TRIUNE_DT_F32, strides + 12, 3) || strides[13] < Dk || (64 * strides[13] + Dk) * 4 >= ((int64_t)1 << 31))))
         return TRIUNE_ERR_LAYOUT;
-    // o strides sit at 15..17 here (beta takes 12..14); tok_strides_ok reads o's token stride at 13
+    // o strides sit at 15..17 here (beta takes 12..14); tok_strides_ok reads o's token stride at 13.
+    // A scalar gate is read one element per token, so its token stride has no lower bound.
     const int64_t ost[15] = {strides[0], strides[1], strides[2], strides[3], strides[4], strides[5],
-                             strides[6], strides[7], strides[8], strides[9], strides[10], strides[11],
-                             strides[15], strides[16], strides[17]};
+                             strides[6], strides[7], strides[8], strides[9], sg ? (int64_t)Dk : strides[10],
+                             strides[11], strides[15], strides[16], strides[17]};
     if (!tok_strides_ok(ost, io_dtype, g_dtype, o_dtype, Dk, Dv)) return TRIUNE_ERR_LAYOUT;
     hipStream_t st = (hipStream_t)stream;
     if (B == 0) return TRIUNE_OK;
@@ -832,7 +848,7 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
         sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = 0;
         return launch_status(launch_recurrent_scan(sc, st));
     }
-    const GdnPlan pl = plan_gdn(B, T, H, io_dtype);
+    const GdnPlan pl = plan_gdn(B, T, H, io_dtype, sg);
     if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
     if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
@@ -841,7 +857,7 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     fill_tok(a.q, q, strides + 0, B, T, H, Dk, io_dtype);
     fill_tok(a.k, k, strides + 3, B, T, H, Dk, io_dtype);
     fill_tok(a.v, v, strides + 6, B, T, H, Dv, io_dtype);
-    fill_tok(a.g, g, strides + 9, B, T, H, Dk, g_dtype);
+    fill_tok(a.g, g, strides + 9, B, T, H, sg ? 1 : Dk, g_dtype);
     a.o = o; a.o_sb = strides[15]; a.o_st = strides[16]; a.o_sh = strides[17];
     a.g_dt = g_dtype; a.o_dt = o_dtype;
     a.s0 = s0;
@@ -854,11 +870,34 @@ int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, 
     a.b_sb = strides[12]; a.b_st = strides[13]; a.b_sh = strides[14];
     if (beta_kind == TRIUNE_BETA_KEY) fill_tok(a.kb, beta, strides + 12, B, T, H, Dk, TRIUNE_DT_F32);
 
-    hipError_t e = launch_gdn_seg_mn(a, pl.n_work, io_dtype, st);
+    hipError_t e = sg ? launch_gdn_sg_seg_mn(a, pl.n_work, io_dtype, st) : launch_gdn_seg_mn(a, pl.n_work, io_dtype, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
     e = launch_gdn_seg_scan(a, s_final, io_dtype, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
-    return launch_status(launch_gdn_seg_out(a, pl.n_work, io_dtype, st));
+    return launch_status(sg ? launch_gdn_sg_seg_out(a, pl.n_work, io_dtype, st)
+                            : launch_gdn_seg_out(a, pl.n_work, io_dtype, st));
+}
+
+}  // namespace
+
+extern "C" {
+
+int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                   int g_dtype, const void* beta, int beta_dtype, int beta_kind,
+                                   const int64_t* strides, const float* s0, void* o, int o_dtype, float* s_final,
+                                   int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+    return gdn_chunked_impl(q, k, v, g, io_dtype, g_dtype, beta, beta_dtype, beta_kind, strides, s0, o, o_dtype,
+                            s_final, B, T, H, Dk, Dv, workspace, workspace_bytes, stream, false);
+}
+
+int triune_hip_gdn_prefill_scalar_decay(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                        int g_dtype, const void* beta, int beta_dtype, int beta_kind,
+                                        const int64_t* strides, const float* s0, void* o, int o_dtype,
+                                        float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+    return gdn_chunked_impl(q, k, v, g, io_dtype, g_dtype, beta, beta_dtype, beta_kind, strides, s0, o, o_dtype,
+                            s_final, B, T, H, Dk, Dv, workspace, workspace_bytes, stream, true);
 }
 
 int triune_hip_gla_qkvg_prep(void* qkv, void* g, int io_dtype, const int64_t* strides, const void* cos,

@@ -23,19 +23,9 @@
 // Products run on v_mfma_f32_16x16x32_bf16 with operands split into bf16 parts (2 for 16-bit
 // I/O, 3 for fp32) and fp32 accumulation, as in the GLA prefill.  Chunks whose decay span
 // exceeds SPAN_MAX run token by token.
-#include "chunk_common.h"
+#include "gdn_common.h"
 
 namespace triune {
-
-// Workspace layouts shared by the three segment kernels, both chosen so that every lane moves
-// whole 16-byte vectors:
-//  - M_p: up to 3 bf16 parts, each stored as the scan's A-operand fragments: element j of lane L
-//    for row tile t and K step kk at ((part*4 + t)*2 + kk)*512 + 8L + j;
-//  - N_p / S_in[p]: fp32 in MFMA D layout, element i of lane L for column strip c (16 columns)
-//    and row tile t at ((c*4 + t)*64 + L)*4 + i.
-constexpr int64_t MSLOT = 3 * 64 * 64;
-
-__device__ __forceinline__ int64_t dstate_off(int strip, int t, int lane) { return ((strip * 4 + t) * 64 + lane) * 4; }
 
 template <typename TIn, bool OUT>
 struct GLay {
@@ -61,89 +51,6 @@ struct GLay {
     static_assert(16 * OS * 4 <= P::NX * VPP, "output staging fits in a wave's V planes");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
-
-// Tile fragment from a tile plane set: lane values at (tile, lane) in K slots 0..3 (K=16), or two
-// tiles in slots 0..3 / 4..7 (K=32).
-template <int NP>
-__device__ __forceinline__ Split8<NP> tile_frag(const char* base, int plane_bytes, int i0, int i1, bool has_hi,
-                                                int lane) {
-    Split8<NP> f;
-#pragma unroll
-    for (int pl = 0; pl < NP; ++pl) {
-        const __bf16* p = reinterpret_cast<const __bf16*>(base + pl * plane_bytes);
-        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(p + (i0 * 64 + lane) * 4);
-        const __bf16 z = (__bf16)0.f;
-        if (has_hi) {
-            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(p + (i1 * 64 + lane) * 4);
-            f.p[pl] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        } else {
-            f.p[pl] = bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
-        }
-    }
-    return f;
-}
-
-// Slot of the off-diagonal L^T block (sb < tb) in the compact six-tile plane.
-__device__ __forceinline__ int lt_index(int sb, int tb) { return (tb - 1) * tb / 2 + sb; }
-
-__device__ __forceinline__ float beta_value(const PrefillParams& a, const Work& wk, int64_t h, int64_t t) {
-    const int64_t i = wk.b * a.b_sb + (wk.row0 + t) * a.b_st + h * a.b_sh;
-    if (a.beta_dt == DT_F32) return reinterpret_cast<const float*>(a.beta)[i];
-    if (a.beta_dt == DT_BF16) return (float)reinterpret_cast<const __bf16*>(a.beta)[i];
-    return (float)reinterpret_cast<const _Float16*>(a.beta)[i];
-}
-
-// Token-by-token GDN update of one wave's 16 state columns (decay spans beyond SPAN_MAX).
-// S tile db holds S[16*db + 4*g4 + i][c0 + r16]; with_v false reads V as zero.
-template <typename TIn, typename TG, bool OUT>
-__device__ void gdn_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int c0, int64_t tc, int nv, int g4,
-                              int r16, bool with_v, f32x4 (&S)[4]) {
-    for (int t = 0; t < nv; ++t) {
-        const int64_t tt = tc + t;
-        float dcy[4][4], kk[4][4], ww[4][4], qq[4][4];
-        const float bh = a.beta_kind == BETA_HEAD ? beta_value(a, wk, h, tt) : 1.f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int d = 16 * db + 4 * g4;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                dcy[db][i] = expf(fminf((float)tok_row<TG>(a.g, wk, tt, h, d)[i], 0.f));
-                kk[db][i] = (float)tok_row<TIn>(a.k, wk, tt, h, d)[i];
-                const float bk = a.beta_kind == BETA_KEY ? tok_row<float>(a.kb, wk, tt, h, d)[i] : bh;
-                ww[db][i] = bk * kk[db][i];
-                qq[db][i] = OUT ? (float)tok_row<TIn>(a.q, wk, tt, h, d)[i] : 0.f;
-            }
-        }
-        float pred = 0.f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pred += kk[db][i] * S[db][i];
-        pred += __shfl_xor(pred, 16);
-        pred += __shfl_xor(pred, 32);
-        const float u = (with_v ? (float)tok_row<TIn>(a.v, wk, tt, h, c0)[r16] : 0.f) - pred;
-        float part = 0.f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float s = dcy[db][i] * S[db][i] + ww[db][i] * u;
-                S[db][i] = s;
-                part += qq[db][i] * s;
-            }
-        if (OUT) {
-            part += __shfl_xor(part, 16);
-            part += __shfl_xor(part, 32);
-            if (g4 == 0) {
-                const int64_t off = wk.b * a.o_sb + (wk.row0 + tt) * a.o_st + h * a.o_sh + c0 + r16;
-                char* op = reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt);
-                if (a.o_dt == DT_F32) *reinterpret_cast<float*>(op) = part;
-                else if (a.o_dt == DT_BF16) *reinterpret_cast<__bf16*>(op) = (__bf16)part;
-                else *reinterpret_cast<_Float16*>(op) = (_Float16)part;
-            }
-        }
-    }
-}
 
 // Inputs of a GDN chunk: the GLA chunk inputs plus per-key-dim beta (BETA_KEY, fp32).
 template <typename TIn, typename TG>
@@ -521,38 +428,10 @@ __global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     f32x4 M[4], N[4];
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            M[db][i] = (16 * db + 4 * g4 + i == 16 * wave + r16) ? 1.f : 0.f;
-            N[db][i] = 0.f;
-        }
+    init_seg_map(M, N);
     gdn_walk<TIn, TG, false, CK>(a, wk, h, M, N, smem);
-    // M goes out already split into NS bf16 parts (the scan's MFMA operands): NS planes of
-    // [64][64] row-major per (segment, head), slot stride MSLOT elements
-    // M[16db + 4g4 + i][16w + r16] is element j = 4(w&1) + (r16&3) of scan lane
-    // 16(r16>>2) + 4g4 + i for row tile db and K step w>>1.
-    constexpr int NS = Prec<TIn>::NS;
-    __bf16* dm = reinterpret_cast<__bf16*>(a.ws_m) + (w * a.H + h) * (int64_t)MSLOT;
-    float* dn = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float m = M[db][i];
-            const int sl = 16 * (r16 >> 2) + 4 * g4 + i, j = 4 * (wave & 1) + (r16 & 3);
-#pragma unroll
-            for (int pl = 0; pl < NS; ++pl) {
-                const __bf16 hi = (__bf16)m;
-                dm[((pl * 4 + db) * 2 + (wave >> 1)) * 512 + 8 * sl + j] = hi;
-                m -= (float)hi;
-            }
-        }
-        *reinterpret_cast<f32x4*>(dn + dstate_off(wave, db, lane)) = N[db];
-    }
+    store_seg_map<Prec<TIn>::NS>(a, w, h, M, N);
 }
 
 // K3: outputs of one segment from S_in[p] (in the N slot after the scan).  Two workgroups per CU
@@ -564,11 +443,8 @@ __global__ __launch_bounds__(256, ((2 * GLay<TIn, true>::BYTES <= 160 * 1024) ? 
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     f32x4 S[4];
-    const float* st = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) S[db] = *reinterpret_cast<const f32x4*>(st + dstate_off(wave, db, lane));
+    load_seg_state(a, w, h, S);
     gdn_walk<TIn, TG, true, CK>(a, wk, h, S, S, smem);
 }
 

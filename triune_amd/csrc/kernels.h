@@ -179,6 +179,11 @@ hipError_t launch_gdn_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, 
 hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream);
 hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 int gdn_seg_out_blocks_per_cu(int io_dt, bool ck);
+// Scalar-gate chunked GDN (gdn_scalar.hip): g holds one log-decay per (token, head); same
+// workspace layout and segment scan as the per-key-dim kernels.
+hipError_t launch_gdn_sg_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
+hipError_t launch_gdn_sg_seg_out(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
+int gdn_sg_seg_out_blocks_per_cu(int io_dt, bool ck);
 bool prefill_shape_supported(int Dk, int Dv);
 bool prefill_dtype_supported(int Dk, int Dv, int io_dt);
 // the segment-state kernel that also pre-processes q, k, g in place (gla_prefill_prep.hip)

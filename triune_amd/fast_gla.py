@@ -37,6 +37,9 @@ _DECODE_PAIRS = ((32, 32), (64, 64), (64, 128), (128, 64), (128, 128))
 # Gated DeltaNet prefill: the chunked WY/UT kernels (head dims <= 64) unless this is False, in
 # which case every call takes the token-serial kernel (kept for the per-value-dim beta).
 _chunked_gdn_enabled = True
+# Gates with one value per (token, head) take the scalar-decay chunked kernels unless this is False
+# (then they run the per-key-dim chunked kernels on the broadcast gate).
+_scalar_gdn_enabled = True
 
 
 def _on_device(*ts):
@@ -529,8 +532,22 @@ class FusedRecurrentScan(torch.autograd.Function):
 # ---------------------------------------------------------------------------------------
 
 
+def _scalar_gate(g):
+    """The [B, T, H] view of a gate holding one log-decay per (token, head), or None: g of shape
+    [B, T, H], [B, T, H, 1], or [B, T, H, D] broadcast over the head dim (stride 0, as
+    g.unsqueeze(-1).expand(..., D) makes it)."""
+    if g.dim() == 3:
+        return g
+    if g.dim() == 4 and (g.shape[-1] == 1 or g.stride(-1) == 0):
+        return g[..., 0]
+    return None
+
+
 def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
     _check_io(q, k, v, g)
+    sg = _scalar_gate(g)
+    if g.dim() == 3 or g.shape[-1] != q.shape[-1]:  # one gate per (token, head): the per-dim kernels take it broadcast
+        g = sg.unsqueeze(-1).expand(*sg.shape, q.shape[-1])
     if _needs_grad(q, k, v, g, beta, initial_state):
         # The reference differentiates its PyTorch recurrence here (fast_gla.py:885-904); these
         # HIP kernels are forward-only, so refuse rather than return outputs without gradients.
@@ -541,31 +558,38 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
     D = _round_dk(max(Dk0, Dv0))
-    qp, kp, gp, vp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, g, v))
+    # chunked WY/UT path: (64, 64) heads (smaller ones zero-padded), per-token or per-key beta;
+    # a gate with one value per (token, head) and beta none or per token takes the scalar-decay kernels
+    chunked = (D <= 64 and T > 1 and beta_kind != _lib.BETA_VALUE and _chunked_gdn_enabled)
+    scalar = chunked and sg is not None and beta_kind in (_lib.BETA_NONE, _lib.BETA_HEAD) and _scalar_gdn_enabled
+    if chunked:
+        D = 64
+    qp, kp, vp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, v))
+    gp = sg if scalar else _vec_layout(_pad_last(g, D), 1)
     bp = None
     bst = (0, 0, 0)
     if beta is not None:
         bp = beta
         if beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE):
             bp = _pad_last(beta, D)
+        if chunked and beta_kind == _lib.BETA_KEY:
+            bp = bp.to(torch.float32)
         bp = bp.contiguous()
         bst = (bp.stride(0), bp.stride(1), bp.stride(2))
     o = torch.empty(B, T, H, D, device=q.device, dtype=out_dtype or v.dtype)
     s0 = _state_in(initial_state, D, D)
     sf = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
-    # chunked WY/UT path: (64, 64) heads (smaller ones zero-padded), per-token or per-key beta
-    chunked = (D <= 64 and T > 1 and beta_kind != _lib.BETA_VALUE and _chunked_gdn_enabled)
-    if chunked:
-        D = 64
-        qp, kp, gp, vp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, g, v))
-        if beta_kind == _lib.BETA_KEY:
-            bp = _pad_last(beta, D).to(torch.float32).contiguous()
-            bst = (bp.stride(0), bp.stride(1), bp.stride(2))
-        o = torch.empty(B, T, H, D, device=q.device, dtype=out_dtype or v.dtype)
-        s0 = _state_in(initial_state, D, D)
-        sf = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32)
     st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), bst, _tok3(o))
-    if chunked:
+    if scalar:
+        ws_bytes = lib().triune_hip_gdn_prefill_scalar_decay_workspace_size(B, T, H, D, D)
+        ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
+        rc = lib().triune_hip_gdn_prefill_scalar_decay(
+            ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(bp),
+            dtype_code(bp) if bp is not None else 0, beta_kind, st, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
+            B, T, H, D, D, ptr(ws), ws_bytes, stream_of(q),
+        )
+        check(rc, "triune_hip_gdn_prefill_scalar_decay")
+    elif chunked:
         ws_bytes = lib().triune_hip_gdn_prefill_chunked_workspace_size(B, T, H, D, D)
         ws = torch.empty(max(int(ws_bytes), 16), device=q.device, dtype=torch.uint8)
         rc = lib().triune_hip_gdn_prefill_chunked(

@@ -65,15 +65,25 @@ def config2(steps=512, B=256, H=6, D=64, dtype=torch.bfloat16):
 
 
 def config3(T=8192, B=4, H=6, D=64, dtype=torch.bfloat16):
-    """q, k, v, g [B,T,H,D], beta [B,T,H]; zero initial state."""
+    """q, k, v [B,T,H,D], g [B,T,H,D] broadcast over D (a stride-0 view of the per-(token, head)
+    log-decay), beta [B,T,H]; zero initial state.  Move g with to_device to keep it a view."""
     gen = _gen(3)
     q = F.normalize(torch.randn(B, T, H, D, generator=gen), dim=-1)
     k = F.normalize(torch.randn(B, T, H, D, generator=gen), dim=-1)
     v = torch.randn(B, T, H, D, generator=gen)
     beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
     alpha = torch.exp(-F.softplus(torch.randn(B, T, H, generator=gen)) / 8)
-    g = torch.log(alpha).unsqueeze(-1).expand(B, T, H, D).contiguous()
-    return q.to(dtype), k.to(dtype), v.to(dtype), g.to(dtype), beta.to(dtype)
+    g = torch.log(alpha).to(dtype).unsqueeze(-1).expand(B, T, H, D)
+    return q.to(dtype), k.to(dtype), v.to(dtype), g, beta.to(dtype)
+
+
+def to_device(x, dev):
+    """x on dev.  A tensor broadcast along some dims (stride 0 there, as expand makes it) moves
+    once and stays a broadcast view on dev; x.to(dev) would materialise it."""
+    if x.dim() and any(st == 0 and n > 1 for n, st in zip(x.shape, x.stride())):
+        idx = tuple(slice(0, 1) if (st == 0 and n > 1) else slice(None) for n, st in zip(x.shape, x.stride()))
+        return x[idx].to(dev).expand(x.shape)
+    return x.to(dev)
 
 
 def config4_lengths(n_seqs=32, lo=128, hi=8192, seed=4) -> list[int]:
