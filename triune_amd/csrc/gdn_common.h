@@ -1,7 +1,7 @@
 // gdn_common.h -- device pieces shared by the chunked Gated DeltaNet kernels (per-key-dim gates
 // in gdn_chunk.hip, one gate per token and head in gdn_scalar.hip): the segment-map workspace
-// layout read by the segment scan, tile fragments, beta and gate reads, the token-by-token
-// update and the segment-map store (internal to libtriune_hip).
+// layout read by the segment scan and its stores and loads, tile fragments, beta reads and the
+// token-by-token update of the per-key-dim kernels (internal to libtriune_hip).
 #pragma once
 
 #include "chunk_common.h"
@@ -49,34 +49,23 @@ __device__ __forceinline__ float beta_value(const PrefillParams& a, const Work& 
     return (float)reinterpret_cast<const _Float16*>(a.beta)[i];
 }
 
-// One log-decay per (token, head): element (b, t, h) of a gate whose strides are g.sb, g.st, g.sh
-// (dtype a.g_dt).
-__device__ __forceinline__ float scalar_gate(const PrefillParams& a, const Work& wk, int64_t h, int64_t t) {
-    const int64_t i = wk.b * a.g.sb + (wk.row0 + t) * a.g.st + h * a.g.sh;
-    if (a.g_dt == DT_F32) return reinterpret_cast<const float*>(a.g.p)[i];
-    if (a.g_dt == DT_BF16) return (float)reinterpret_cast<const __bf16*>(a.g.p)[i];
-    return (float)reinterpret_cast<const _Float16*>(a.g.p)[i];
-}
-
 // Token-by-token GDN update of one wave's 16 state columns (decay spans beyond SPAN_MAX).
-// S tile db holds S[16*db + 4*g4 + i][c0 + r16]; with_v false reads V as zero.  SG: the gate is
-// one value per (token, head) (scalar_gate); otherwise one per key dim, of type TG.
-template <typename TIn, typename TG, bool OUT, bool SG = false>
+// S tile db holds S[16*db + 4*g4 + i][c0 + r16]; with_v false reads V as zero.
+template <typename TIn, typename TG, bool OUT>
 __device__ void gdn_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int c0, int64_t tc, int nv, int g4,
                               int r16, bool with_v, f32x4 (&S)[4]) {
     for (int t = 0; t < nv; ++t) {
         const int64_t tt = tc + t;
         float dcy[4][4], kk[4][4], ww[4][4], qq[4][4];
         const float bh = a.beta_kind == BETA_HEAD ? beta_value(a, wk, h, tt) : 1.f;
-        const float ds = SG ? expf(fminf(scalar_gate(a, wk, h, tt), 0.f)) : 0.f;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
             const int d = 16 * db + 4 * g4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                dcy[db][i] = SG ? ds : expf(fminf((float)tok_row<TG>(a.g, wk, tt, h, d)[i], 0.f));
+                dcy[db][i] = expf(fminf((float)tok_row<TG>(a.g, wk, tt, h, d)[i], 0.f));
                 kk[db][i] = (float)tok_row<TIn>(a.k, wk, tt, h, d)[i];
-                const float bk = !SG && a.beta_kind == BETA_KEY ? tok_row<float>(a.kb, wk, tt, h, d)[i] : bh;
+                const float bk = a.beta_kind == BETA_KEY ? tok_row<float>(a.kb, wk, tt, h, d)[i] : bh;
                 ww[db][i] = bk * kk[db][i];
                 qq[db][i] = OUT ? (float)tok_row<TIn>(a.q, wk, tt, h, d)[i] : 0.f;
             }
