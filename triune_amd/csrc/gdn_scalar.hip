@@ -77,40 +77,63 @@ __device__ __forceinline__ Split8<NP> join4(const Split4<NP>& lo, const Split4<N
     return f;
 }
 
-// ---- fragment planes: fragment f of lane L occupies 16 bytes per part at (f * 64 + L) * 16 -------
-// A 16x16 tile is written as one half (8 bytes) of a fragment, so a K=32 operand made of two tiles
-// is one 16-byte read and a K=16 one an 8-byte read.
+// ---- fragment planes --------------------------------------------------------------------------
+// A fragment is one MFMA operand per lane: a pair (K=32, two 16x16 tiles, 16 bytes per lane) or a
+// single (K=16, one tile, 8 bytes per lane), stored lane-major so that every lane reads its operand
+// with one access.  A plane lists its fragments back to back; FragAt gives where fragment f starts.
+// A tile is written as one half of a pair fragment, or as a single one.
+struct FragAt {
+    int off;  // byte offset of the fragment within the plane
+    bool pair;
+};
+
 template <int NP>
-__device__ __forceinline__ void frag_put(char* base, int plane_bytes, int f, int half, int lane, const float (&x)[4]) {
+__device__ __forceinline__ void frag_put(char* base, int plane_bytes, FragAt f, int half, int lane,
+                                         const float (&x)[4]) {
     float r[4] = {x[0], x[1], x[2], x[3]};
     uint32_t w[NP][2];
     split_pairs<NP, 2>(r, w);
+    const int o = f.off + (f.pair ? lane * 16 + half * 8 : lane * 8);
 #pragma unroll
-    for (int pl = 0; pl < NP; ++pl)
-        *reinterpret_cast<uint2*>(base + pl * plane_bytes + (f * 64 + lane) * 16 + half * 8) = uint2{w[pl][0], w[pl][1]};
+    for (int pl = 0; pl < NP; ++pl) *reinterpret_cast<uint2*>(base + pl * plane_bytes + o) = uint2{w[pl][0], w[pl][1]};
 }
 
 template <int NP>
-__device__ __forceinline__ Split8<NP> frag_get8(const char* base, int plane_bytes, int f, int lane) {
+__device__ __forceinline__ Split8<NP> frag_get8(const char* base, int plane_bytes, FragAt f, int lane) {
     Split8<NP> r;
 #pragma unroll
-    for (int pl = 0; pl < NP; ++pl) r.p[pl] = *reinterpret_cast<const bf16x8*>(base + pl * plane_bytes + (f * 64 + lane) * 16);
+    for (int pl = 0; pl < NP; ++pl) r.p[pl] = *reinterpret_cast<const bf16x8*>(base + pl * plane_bytes + f.off + lane * 16);
     return r;
 }
 
 template <int NP>
-__device__ __forceinline__ Split4<NP> frag_get4(const char* base, int plane_bytes, int f, int lane) {
+__device__ __forceinline__ Split4<NP> frag_get4(const char* base, int plane_bytes, FragAt f, int lane) {
     Split4<NP> r;
 #pragma unroll
-    for (int pl = 0; pl < NP; ++pl) r.p[pl] = *reinterpret_cast<const bf16x4*>(base + pl * plane_bytes + (f * 64 + lane) * 16);
+    for (int pl = 0; pl < NP; ++pl) r.p[pl] = *reinterpret_cast<const bf16x4*>(base + pl * plane_bytes + f.off + lane * 8);
     return r;
 }
 
+constexpr int SINGLE_B = 64 * 8, PAIR_B = 64 * 16;
+
 // Fragments of A^T (tiles (sb, tb), sb <= tb): fragment (k2, tb) holds tiles (2*k2, tb) and
-// (2*k2 + 1, tb); the two fragments with 2*k2 == tb hold one tile.
-__device__ __forceinline__ int afrag(int k2, int tb) { return k2 == 0 ? tb : 2 + tb; }
-// Fragments of -P_ij (j < i): [P_10], [P_20 P_21], [P_30 P_31], [P_32].
-__device__ __forceinline__ int pfrag(int j, int i) { return i == 1 ? 0 : (j < 2 ? i - 1 : 3); }
+// (2*k2 + 1, tb), a single where 2*k2 == tb.  Order: (0,0) (0,1) (0,2) (0,3) (1,2) (1,3).
+__device__ __forceinline__ FragAt afrag(int k2, int tb) {
+    if (k2 == 0) return tb == 0 ? FragAt{0, false} : FragAt{SINGLE_B + (tb - 1) * PAIR_B, true};
+    return tb == 2 ? FragAt{SINGLE_B + 3 * PAIR_B, false} : FragAt{2 * SINGLE_B + 3 * PAIR_B, true};
+}
+constexpr int AF_BYTES = 2 * SINGLE_B + 4 * PAIR_B;
+// Fragments of the off-diagonal solve tiles X_ij (j < i; -L_ij or -P_ij): [X_10] [X_20 X_21]
+// [X_30 X_31] [X_32]; half = j for the pairs.
+__device__ __forceinline__ FragAt xfrag(int j, int i) {
+    if (i == 1) return FragAt{0, false};
+    if (j < 2) return FragAt{SINGLE_B + (i - 2) * PAIR_B, true};
+    return FragAt{SINGLE_B + 2 * PAIR_B, false};
+}
+constexpr int XF_BYTES = 2 * SINGLE_B + 2 * PAIR_B;
+// The diagonal inverses T_ii: four singles.
+__device__ __forceinline__ FragAt tfrag(int i) { return FragAt{i * SINGLE_B, false}; }
+constexpr int TF_BYTES = 4 * SINGLE_B;
 
 // Four V (or K) elements of one 16-token block down one column, through the transposed LDS read:
 // rows row0 + 4*g4 + [0, 4), column col, as a K=16 operand (one bf16 part per plane).
@@ -124,26 +147,24 @@ __device__ __forceinline__ Split4<NP> col_frag4(const char* base, int plane_byte
     return f;
 }
 
-template <typename TIn, bool OUT>
+// LDS of one chunk step.  PRE: the solve uses the precomputed products (-Bk planes, -P tiles);
+// otherwise the residual form (-L tiles).
+template <typename TIn, bool OUT, bool PRE>
 struct SLay {
     using P = Prec<TIn>;
     static constexpr int NX = P::NX, NS = P::NS;
     static constexpr int RS = 64 + PAD;
     static constexpr int ROWP = CHUNK * RS * 2;  // one bf16 plane of a token-major [64][64] operand
-    static constexpr int FRAG = 64 * 16;         // one fragment (16 bytes per lane), one bf16 part
-    static constexpr int AFP = 6 * FRAG;         // the fragments of A^T
-    static constexpr int PFP = 4 * FRAG;         // the fragments of -P
-    static constexpr int TFP = 4 * FRAG;         // T_ii (A-operand layout, one tile per fragment)
-    static constexpr int OS = 20;                // output staging row stride (floats)
+    static constexpr int OS = 16;                // output staging row stride (floats)
     static constexpr int WSB = 16 * OS * 4;      // per wave: fp32 L_ii (stage 2) / output staging
     static constexpr int OFF_Q = 0;
     static constexpr int OFF_K = OFF_Q + (OUT ? NX * ROWP : 0);
     static constexpr int OFF_V = OFF_K + NX * ROWP;
-    static constexpr int OFF_BK = OFF_V + NX * ROWP;  // -Bk = -T diag(e^{gamp}) K, token-major
-    static constexpr int OFF_AF = OFF_BK + NS * ROWP;
-    static constexpr int OFF_PF = OFF_AF + (OUT ? NS * AFP : 0);
-    static constexpr int OFF_TF = OFF_PF + NS * PFP;
-    static constexpr int OFF_WS = OFF_TF + NS * TFP;
+    static constexpr int OFF_BK = OFF_V + NX * ROWP;  // -Bk = -T diag(e^{gamp}) K, token-major (PRE)
+    static constexpr int OFF_AF = OFF_BK + (PRE ? NS * ROWP : 0);
+    static constexpr int OFF_XF = OFF_AF + (OUT ? NS * AF_BYTES : 0);
+    static constexpr int OFF_TF = OFF_XF + NS * XF_BYTES;
+    static constexpr int OFF_WS = OFF_TF + NS * TF_BYTES;
     static constexpr int OFF_F = OFF_WS + 4 * WSB;
     // per-token factor arrays (64 floats each; log-decays in log2 units):
     //   G2 gam, GP2 gamp, EG e^{gam}, EGP e^{gamp}, W beta e^{Gam - gam}, B beta,
@@ -284,15 +305,17 @@ __device__ __forceinline__ float group_bcast(float x) {
 // is bf16 (stores of one encoding).  Otherwise (K1) the segment map on two states at once: S
 // driven with V = 0 (the M columns) and SN with the real V (the N columns), sharing stages 1-2.
 //
-// The solve is arranged so that everything independent of the state is formed once per chunk:
-// with T_ii = (I + L_ii)^{-1}, P_ij = T_ii L_ij and Bk_i = T_ii diag(e^{gamp}) K_i,
-//   U_i = T_ii V_i - Bk_i S0 - sum_{j<i} P_ij U_j ,
-// so a pass over a state splits only S0 and U into bf16 parts.  Wave i forms everything of key
-// block i in stage 2 (its Gram block and T_ii, the tiles L_ij (j < i) and P_ij, Bk_i, and the A^T
-// tiles of key block i), from the key block it holds in registers.
-template <typename TIn, bool OUT, bool CK, bool OBF>
+// Solve: U_i = T_ii (R_i - sum_{j<i} L_ij U_j), R = V - diag(e^{gamp}) K S0, T_ii = (I + L_ii)^{-1}.
+// PRE (two passes per chunk, K1) forms the state-independent products once per chunk,
+// P_ij = T_ii L_ij and Bk_i = T_ii diag(e^{gamp}) K_i, so that
+//   U_i = T_ii V_i - Bk_i S0 - sum_{j<i} P_ij U_j
+// and a pass splits only S0 and U into bf16 parts; without PRE (one pass, K3) the pass forms R
+// and applies T_ii to each block, which needs no Bk planes in LDS.  Wave i forms everything of
+// key block i in stage 2 (its Gram block and T_ii, the tiles of row block i of L (or P), Bk_i, and
+// the A^T tiles of key block i) from the key block it holds in registers.
+template <typename TIn, bool OUT, bool CK, bool OBF, bool PRE>
 struct SgStep {
-    using L = SLay<TIn, OUT>;
+    using L = SLay<TIn, OUT, PRE>;
     static constexpr int NS = L::NS, NX = L::NX;
 
     template <typename Hook>
@@ -306,7 +329,7 @@ struct SgStep {
         char* sV = smem + L::OFF_V;
         char* sBK = smem + L::OFF_BK;
         char* sAF = smem + L::OFF_AF;
-        char* sPF = smem + L::OFF_PF;
+        char* sXF = smem + L::OFF_XF;
         char* sTF = smem + L::OFF_TF;
         float* sWS = reinterpret_cast<float*>(smem + L::OFF_WS + wave * L::WSB);
         float* sF = reinterpret_cast<float*>(smem + L::OFF_F);
@@ -414,42 +437,58 @@ struct SgStep {
                     for (int j = 0; j < 4; ++j) Y[j] -= lb[j] * yb;
                 }
                 const float xv[4] = {Y[0], Y[1], Y[2], Y[3]};
-                frag_put<NS>(sTF, L::TFP, ib, 0, lane, xv);
+                frag_put<NS>(sTF, TF_BYTES, tfrag(ib), 0, lane, xv);
             }
-            // -P_ij = -T_ii L_ij for j < ib.  L_ij as D[t][s] (rows t of block ib, columns s of
-            // block j): its D layout is the A operand of L_ij^T with K = t, and the A layout of
-            // T_ii is the B operand of T_ii^T, so one product gives P_ij^T in D layout, which is
-            // the A-operand layout of P_ij.
-            const Split4<NS> ysp = split4<NS>(Y);
-            for (int j = 0; j < ib; ++j) {
-                f32x4 lt = zero4();
+            if constexpr (PRE) {
+                // -P_ij = -T_ii L_ij for j < ib.  L_ij as D[t][s] (rows t of block ib, columns s of
+                // block j): its D layout is the A operand of L_ij^T with K = t, and the A layout of
+                // T_ii is the B operand of T_ii^T, so one product gives P_ij^T in D layout, which is
+                // the A-operand layout of P_ij.
+                const Split4<NS> ysp = split4<NS>(Y);
+                for (int j = 0; j < ib; ++j) {
+                    f32x4 lt = zero4();
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    const Split8<NX> kj = lds_frag<NX>(sK, L::ROWP, L::RS, 16 * j + r16, 32 * ks, g4);
-                    lt = mfma_split<NX, NX, NX>(kf[ks], kj, lt);
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const Split8<NX> kj = lds_frag<NX>(sK, L::ROWP, L::RS, 16 * j + r16, 32 * ks, g4);
+                        lt = mfma_split<NX, NX, NX>(kf[ks], kj, lt);
+                    }
+                    // beta_s e^{gamp_t - gam_s} = e^{gamp_t - gam_e(j)} * beta_s e^{gam_e(j) - gam_s}, negated
+                    const f32x4 cf = *reinterpret_cast<const f32x4*>(sF + L::F_CF + 64 * j + 16 * ib + 4 * g4);
+                    const float nbsb = -sF[L::F_BSB + 16 * j + r16];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) lt[k] *= cf[k] * nbsb;
+                    const f32x4 pt = mfma16_split<NS, NS, NS>(split4<NS>(lt), ysp, zero4());
+                    const float xv[4] = {pt[0], pt[1], pt[2], pt[3]};
+                    frag_put<NS>(sXF, XF_BYTES, xfrag(j, ib), j & 1, lane, xv);
                 }
-                // beta_s e^{gamp_t - gam_s} = e^{gamp_t - gam_e(j)} * beta_s e^{gam_e(j) - gam_s}
-                const f32x4 cf = *reinterpret_cast<const f32x4*>(sF + L::F_CF + 64 * j + 16 * ib + 4 * g4);
-                const float bsb = sF[L::F_BSB + 16 * j + r16];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) lt[k] *= cf[k] * bsb;
-                const f32x4 pt = mfma16_split<NS, NS, NS>(split4<NS>(lt), ysp, zero4());
-                const float xv[4] = {-pt[0], -pt[1], -pt[2], -pt[3]};
-                frag_put<NS>(sPF, L::PFP, pfrag(j, ib), ib >= 2 && j < 2 ? j : 0, lane, xv);
-            }
-            // -Bk_i = -T_ii diag(e^{gamp}) K_i as Bk^T tiles: A = K_i^T (transposed reads, K = the
-            // block's tokens), B = (T_ii diag(e^{gamp}))^T, whose B layout is the A layout of
-            // T_ii with column s scaled.  Lane (g4, r16) gets Bk[16*ib + r16][16*db + 4*g4 + j].
-            {
+                // -Bk_i = -T_ii diag(e^{gamp}) K_i as Bk^T tiles: A = K_i^T (transposed reads, K =
+                // the block's tokens), B = (-T_ii diag(e^{gamp}))^T, whose B layout is the A layout
+                // of T_ii with column s scaled.  Lane (g4, r16) gets -Bk[16*ib + r16][16*db + 4*g4 + j].
                 const f32x4 ep = *reinterpret_cast<const f32x4*>(sF + L::F_EGP + 16 * ib + 4 * g4);
-                const f32x4 te = {Y[0] * ep[0], Y[1] * ep[1], Y[2] * ep[2], Y[3] * ep[3]};
+                const f32x4 te = {-Y[0] * ep[0], -Y[1] * ep[1], -Y[2] * ep[2], -Y[3] * ep[3]};
                 const Split4<NS> tsp = split4<NS>(te);
 #pragma unroll
                 for (int db = 0; db < 4; ++db) {
                     const Split4<NX> kt = col_frag4<NX>(sK, L::ROWP, L::RS, 16 * ib, 16 * db, g4, r16);
                     const f32x4 bk = mfma16_split<NX, NS, NS>(kt, tsp, zero4());
-                    const float xv[4] = {-bk[0], -bk[1], -bk[2], -bk[3]};
+                    const float xv[4] = {bk[0], bk[1], bk[2], bk[3]};
                     lds_put_row<NS, 4>(sBK, L::ROWP, (16 * ib + r16) * L::RS + 16 * db + 4 * g4, xv);
+                }
+            } else {
+                // -L_ij for j < ib as D[s][t] (rows s of block j, columns t of block ib): its D layout
+                // is the A-operand layout of L_ij (row t, K = s).
+                for (int j = 0; j < ib; ++j) {
+                    f32x4 lt = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const Split8<NX> kj = lds_frag<NX>(sK, L::ROWP, L::RS, 16 * j + r16, 32 * ks, g4);
+                        lt = mfma_split<NX, NX, NX>(kj, kf[ks], lt);
+                    }
+                    const f32x4 bsb = *reinterpret_cast<const f32x4*>(sF + L::F_BSB + 16 * j + 4 * g4);
+                    const float ncf = -sF[L::F_CF + 64 * j + 16 * ib + r16];
+                    const float xv[4] = {lt[0] * (bsb[0] * ncf), lt[1] * (bsb[1] * ncf), lt[2] * (bsb[2] * ncf),
+                                         lt[3] * (bsb[3] * ncf)};
+                    frag_put<NS>(sXF, XF_BYTES, xfrag(j, ib), j & 1, lane, xv);
                 }
             }
             // A^T tiles (sb = ib, tb >= ib): rows s of key block ib, columns t of query block tb,
@@ -478,7 +517,7 @@ struct SgStep {
 #pragma unroll
                         for (int j = 0; j < 4; ++j) xv[j] = acc[j] * (bsb[j] * cfa);
                     }
-                    frag_put<NS>(sAF, L::AFP, afrag(ib >> 1, tb), ib & 1, lane, xv);
+                    frag_put<NS>(sAF, AF_BYTES, afrag(ib >> 1, tb), ib & 1, lane, xv);
                 }
             }
         }
@@ -491,25 +530,52 @@ struct SgStep {
             Split8<NS> sf[2];  // S0 with K = key dims (B operand of S0, A operand of S0^T)
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) sf[ks] = split_k32<NS>(St[2 * ks], St[2 * ks + 1]);
-            // U_i = T_ii V_i - Bk_i S0 - sum_{j<i} P_ij U_j  (D layout: rows 16i + 4*g4 + k, column c0 + r16)
+            // U_i in D layout: rows 16i + 4*g4 + k, column c0 + r16
             f32x4 U[4];
             Split4<NS> us[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 f32x4 acc = zero4();
-                if constexpr (WV)
-                    acc = mfma16_split<NS, NX, NS>(frag_get4<NS>(sTF, L::TFP, i, lane),
-                                                   col_frag4<NX>(sV, L::ROWP, L::RS, 16 * i, c0, g4, r16), acc);
+                if constexpr (PRE) {
+                    // T_ii V_i - Bk_i S0
+                    if constexpr (WV)
+                        acc = mfma16_split<NS, NX, NS>(frag_get4<NS>(sTF, TF_BYTES, tfrag(i), lane),
+                                                       col_frag4<NX>(sV, L::ROWP, L::RS, 16 * i, c0, g4, r16), acc);
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-                    acc = mfma_split<NS, NS, NS>(lds_frag<NS>(sBK, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4), sf[ks],
-                                                 acc);
-                if (i == 1) {
-                    acc = mfma16_split<NS, NS, NS>(frag_get4<NS>(sPF, L::PFP, 0, lane), us[0], acc);
-                } else if (i >= 2) {  // blocks 0 and 1 together (K = 32)
-                    acc = mfma_split<NS, NS, NS>(frag_get8<NS>(sPF, L::PFP, i - 1, lane), join4<NS>(us[0], us[1]), acc);
-                    if (i == 3) acc = mfma16_split<NS, NS, NS>(frag_get4<NS>(sPF, L::PFP, 3, lane), us[2], acc);
+                    for (int ks = 0; ks < 2; ++ks)
+                        acc = mfma_split<NS, NS, NS>(lds_frag<NS>(sBK, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4),
+                                                     sf[ks], acc);
+                } else {
+                    // R_i = V_i - e^{gamp} (K S0)_i
+                    f32x4 p = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        p = mfma_split<NX, NS, NS>(lds_frag<NX>(sK, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4), sf[ks],
+                                                   p);
+                    const f32x4 ep = *reinterpret_cast<const f32x4*>(sF + L::F_EGP + 16 * i + 4 * g4);
+                    f32x4 vv = zero4();
+                    if constexpr (WV) {
+                        const Split4<NX> vf = col_frag4<NX>(sV, L::ROWP, L::RS, 16 * i, c0, g4, r16);
+#pragma unroll
+                        for (int pl = 0; pl < NX; ++pl)
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) vv[k] += (float)vf.p[pl][k];
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) acc[k] = vv[k] - ep[k] * p[k];
                 }
+                // - sum_{j<i} X_ij U_j (X = P with PRE, else L; stored negated)
+                if (i == 1) {
+                    acc = mfma16_split<NS, NS, NS>(frag_get4<NS>(sXF, XF_BYTES, xfrag(0, 1), lane), us[0], acc);
+                } else if (i >= 2) {  // blocks 0 and 1 together (K = 32)
+                    acc = mfma_split<NS, NS, NS>(frag_get8<NS>(sXF, XF_BYTES, xfrag(0, i), lane), join4<NS>(us[0], us[1]),
+                                                 acc);
+                    if (i == 3)
+                        acc = mfma16_split<NS, NS, NS>(frag_get4<NS>(sXF, XF_BYTES, xfrag(2, 3), lane), us[2], acc);
+                }
+                if constexpr (!PRE)
+                    acc = mfma16_split<NS, NS, NS>(frag_get4<NS>(sTF, TF_BYTES, tfrag(i), lane), split4<NS>(acc),
+                                                   zero4());
                 U[i] = acc;
                 us[i] = split4<NS>(acc);
             }
@@ -529,13 +595,15 @@ struct SgStep {
 #pragma unroll
                     for (int k = 0; k < 4; ++k) o[k] *= eg;
                     if (tb == 0) {
-                        o = mfma16_split<NS, NS, NS>(us[0], frag_get4<NS>(sAF, L::AFP, afrag(0, 0), lane), o);
+                        o = mfma16_split<NS, NS, NS>(us[0], frag_get4<NS>(sAF, AF_BYTES, afrag(0, 0), lane), o);
                     } else {
-                        o = mfma_split<NS, NS, NS>(join4<NS>(us[0], us[1]), frag_get8<NS>(sAF, L::AFP, afrag(0, tb), lane), o);
+                        o = mfma_split<NS, NS, NS>(join4<NS>(us[0], us[1]),
+                                                   frag_get8<NS>(sAF, AF_BYTES, afrag(0, tb), lane), o);
                         if (tb == 2)
-                            o = mfma16_split<NS, NS, NS>(us[2], frag_get4<NS>(sAF, L::AFP, afrag(1, 2), lane), o);
+                            o = mfma16_split<NS, NS, NS>(us[2], frag_get4<NS>(sAF, AF_BYTES, afrag(1, 2), lane), o);
                         if (tb == 3)
-                            o = mfma_split<NS, NS, NS>(join4<NS>(us[2], us[3]), frag_get8<NS>(sAF, L::AFP, afrag(1, 3), lane), o);
+                            o = mfma_split<NS, NS, NS>(join4<NS>(us[2], us[3]),
+                                                       frag_get8<NS>(sAF, AF_BYTES, afrag(1, 3), lane), o);
                     }
                     Ot[tb] = o;
                 }
@@ -598,9 +666,9 @@ struct SgStep {
     }
 };
 
-template <typename TIn, bool OUT, bool CK, bool OBF>
+template <typename TIn, bool OUT, bool CK, bool OBF, bool PRE>
 __device__ void sg_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[4], f32x4 (&SN)[4], char* smem) {
-    using St = SgStep<TIn, OUT, CK, OBF>;
+    using St = SgStep<TIn, OUT, CK, OBF, PRE>;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const SgCtx x = sg_ctx<OUT, TIn>(a, wk, h, tg, wave * 16 + 4 * row);
     const int64_t t_end = wk.t_end;
@@ -619,32 +687,38 @@ __device__ void sg_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4
         });
 }
 
+// Workgroups per CU the launch bounds ask for: three where the LDS allows (16-bit I/O), else as many
+// as fit.
+template <typename Lay>
+constexpr int sg_occupancy() {
+    return 3 * Lay::BYTES <= 160 * 1024 ? 3 : (2 * Lay::BYTES <= 160 * 1024 ? 2 : 1);
+}
+
 // K1: the segment map driven from [I | 0] with V = 0 (-> M_p) and from 0 with the real V (-> N_p).
 template <typename TIn, bool CK>
-__global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_sg_seg_mn_kernel(PrefillParams a) {
-    using L = SLay<TIn, false>;
+__global__ __launch_bounds__(256, (sg_occupancy<SLay<TIn, false, true>>())) void gdn_sg_seg_mn_kernel(PrefillParams a) {
+    using L = SLay<TIn, false, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
     f32x4 M[4], N[4];
     init_seg_map(M, N);
-    sg_walk<TIn, false, CK, false>(a, wk, h, M, N, smem);
+    sg_walk<TIn, false, CK, false, true>(a, wk, h, M, N, smem);
     store_seg_map<Prec<TIn>::NS>(a, w, h, M, N);
 }
 
 // K3: outputs of one segment from S_in[p] (in the N slot after the scan).  OBF: bf16 output.
 template <typename TIn, bool CK, bool OBF>
-__global__ __launch_bounds__(256, ((2 * SLay<TIn, true>::BYTES <= 160 * 1024) ? 2 : 1)) void gdn_sg_seg_out_kernel(
-    PrefillParams a) {
-    using L = SLay<TIn, true>;
+__global__ __launch_bounds__(256, (sg_occupancy<SLay<TIn, true, false>>())) void gdn_sg_seg_out_kernel(PrefillParams a) {
+    using L = SLay<TIn, true, false>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
     f32x4 S[4];
     load_seg_state(a, w, h, S);
-    sg_walk<TIn, true, CK, OBF>(a, wk, h, S, S, smem);
+    sg_walk<TIn, true, CK, OBF, false>(a, wk, h, S, S, smem);
 }
 
 // ---------------------------------------------------------------------------------------
