@@ -18,7 +18,8 @@
 //   K1 gdn_seg_mn   : per (segment, head) the segment map applied to [I | 0] with V replaced by 0
 //                     (-> M_p) and to 0 with the real V (-> N_p), sharing the per-chunk factors,
 //                     tiles and inverses
-//   K2 gdn_seg_scan : per (sequence, head, 16 columns) the carry S_in[p] (written in place of N_p)
+//   K2 gdn_seg_scan : per (sequence, head, 16 columns; one wave per 16 rows) the carry S_in[p]
+//                     (written in place of N_p)
 //   K3 gdn_seg_out  : per (segment, head) the chunk walk from S_in[p], writing o
 // Products run on v_mfma_f32_16x16x32_bf16 with operands split into bf16 parts (2 for 16-bit
 // I/O, 3 for fp32) and fp32 accumulation, as in the GLA prefill.  Chunks whose decay span
@@ -448,17 +449,21 @@ __global__ __launch_bounds__(256, ((2 * GLay<TIn, true>::BYTES <= 160 * 1024) ? 
     gdn_walk<TIn, TG, true, CK>(a, wk, h, S, S, smem);
 }
 
-// K2: one wave per (sequence, head, 16 state columns): S_in[p] = carry (written in place of N_p),
-// then S <- M_p S + N_p on MFMA.  The wave's 64x16 strip of S lives in D layout (tile t holds
-// rows 16t + 4*g4 + i, column r16), which is also the B operand of the next product once split;
-// M_p arrives pre-split in NS bf16 planes and is read straight into A-operand layout (row
-// 16t + r16, K slots 32kk + pi(g4, j)).  The M/N loads of a segment do not depend on the carry:
-// three register sets keep them two segments ahead.
+// K2: one workgroup per (sequence, head, 16 state columns), one wave per 16-row tile t of that
+// column strip: S_in[p] = carry (written in place of N_p), then S <- M_p S + N_p on MFMA.  Wave t
+// holds rows 16t + 4*g4 + i of the strip in D layout; each step it writes its tile, split into NS
+// bf16 parts, as one half of a B-operand fragment in LDS (K step t >> 1, slots (t & 1) * 4 + i),
+// and after one barrier every wave reads the strip's two K=32 fragments and forms its new tile
+// with 2 * NS-part products.  M_p arrives pre-split in NS bf16 planes, read straight into A-operand
+// layout (row 16t + r16, K slots 32kk + pi(g4, j)).  The M/N loads of a segment do not depend on
+// the carry: a ring of register sets keeps them two segments ahead.  Two LDS buffers alternate,
+// so a step's writes never meet the previous step's reads.
 template <int NS>
-__global__ __launch_bounds__(64) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
+__global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
+    __shared__ __attribute__((aligned(16))) char sbuf[2][2][NS][64 * 16];
     const int64_t seq = blockIdx.z, h = blockIdx.y;
-    const int cb = blockIdx.x * 16;
-    const int lane = threadIdx.x, r16 = lane & 15, g4 = lane >> 4;
+    const int strip = blockIdx.x, cb = strip * 16;
+    const int lane = threadIdx.x & 63, t = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     int64_t p0, np;
     if (a.varlen) {
         p0 = a.seg_off[seq];
@@ -469,15 +474,13 @@ __global__ __launch_bounds__(64) void gdn_seg_scan_kernel(PrefillParams a, float
         np = a.nseg_dense < nch ? a.nseg_dense : nch;
         if (a.T == 0) np = 0;
     }
-    auto d_off = [&](int t, int i) { return (16 * t + 4 * g4 + i) * 64 + cb + r16; };  // D-layout element
-    f32x4 S[4];
+    auto d_off = [&](int i) { return (16 * t + 4 * g4 + i) * 64 + cb + r16; };  // D-layout element
+    f32x4 S;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) S[t][i] = a.s0 ? a.s0[(seq * a.H + h) * 4096 + d_off(t, i)] : 0.f;
+    for (int i = 0; i < 4; ++i) S[i] = a.s0 ? a.s0[(seq * a.H + h) * 4096 + d_off(i)] : 0.f;
     struct MN {
-        Split8<NS> m[4][2];  // [row tile][K step]
-        f32x4 n[4];
+        Split8<NS> m[2];  // [K step] of row tile t
+        f32x4 n;
     };
     // Every path issues the same loads and stores (past the end: the last segment's rows again,
     // and the store goes to a spare slot), so the wait counts leave the sets in flight.
@@ -487,52 +490,56 @@ __global__ __launch_bounds__(64) void gdn_seg_scan_kernel(PrefillParams a, float
         const __bf16* mp = reinterpret_cast<const __bf16*>(a.ws_m) + (w * a.H + h) * (int64_t)MSLOT;
         const float* np_ = a.ws_state + (w * a.H + h) * 4096;
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                for (int pl = 0; pl < NS; ++pl)
-                    x.m[t][kk].p[pl] = *reinterpret_cast<const bf16x8*>(mp + ((pl * 4 + t) * 2 + kk) * 512 + 8 * lane);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) x.n[t] = *reinterpret_cast<const f32x4*>(np_ + dstate_off(blockIdx.x, t, lane));
+            for (int pl = 0; pl < NS; ++pl)
+                x.m[kk].p[pl] = *reinterpret_cast<const bf16x8*>(mp + ((pl * 4 + t) * 2 + kk) * 512 + 8 * lane);
+        x.n = *reinterpret_cast<const f32x4*>(np_ + dstate_off(strip, t, lane));
     };
     auto step = [&](const MN& x, int64_t p) {
         const bool real = p < np;
         float* dst = real ? a.ws_state + ((p0 + p) * a.H + h) * 4096 : spare;
+        *reinterpret_cast<f32x4*>(dst + dstate_off(strip, t, lane)) = S;  // S_in[p]
+        // this tile as half (t & 1) of the strip's K-step (t >> 1) fragment
+        const int buf = (int)(p & 1);
+        {
+            float r[4] = {S[0], S[1], S[2], S[3]};
+            uint32_t w[NS][2];
+            split_pairs<NS, 2>(r, w);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) *reinterpret_cast<f32x4*>(dst + dstate_off(blockIdx.x, t, lane)) = S[t];  // S_in[p]
-        Split8<NS> sb[2];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) sb[kk] = split_k32<NS>(S[2 * kk], S[2 * kk + 1]);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            f32x4 acc = x.n[t];
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) acc = mfma_split<NS, NS, NS>(x.m[t][kk], sb[kk], acc);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) S[t][i] = real ? acc[i] : S[t][i];
+            for (int pl = 0; pl < NS; ++pl)
+                *reinterpret_cast<uint2*>(&sbuf[buf][t >> 1][pl][lane * 16 + (t & 1) * 8]) = uint2{w[pl][0], w[pl][1]};
         }
+        __syncthreads();
+        f32x4 acc = x.n;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            Split8<NS> sb;
+#pragma unroll
+            for (int pl = 0; pl < NS; ++pl) sb.p[pl] = *reinterpret_cast<const bf16x8*>(&sbuf[buf][kk][pl][lane * 16]);
+            acc = mfma_split<NS, NS, NS>(x.m[kk], sb, acc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[i] = real ? acc[i] : S[i];
     };
     if (np > 0) {
-        MN x0, x1, x2;
-        fetch(x0, 0);
-        fetch(x1, 1);
-        const int64_t nit = (np + 2) / 3;
+        constexpr int RING = 3;  // loads run RING - 1 segments ahead of the carry
+        MN x[RING];
+#pragma unroll
+        for (int r = 0; r < RING - 1; ++r) fetch(x[r], r);
+        const int64_t nit = (np + RING - 1) / RING;
         for (int64_t it = 0; it < nit; ++it) {
-            const int64_t p = 3 * it;
-            fetch(x2, p + 2);
-            step(x0, p);
-            fetch(x0, p + 3);
-            step(x1, p + 1);
-            fetch(x1, p + 4);
-            step(x2, p + 2);
+#pragma unroll
+            for (int r = 0; r < RING; ++r) {
+                const int64_t p = RING * it + r;
+                fetch(x[(r + RING - 1) % RING], p + RING - 1);
+                step(x[r], p);
+            }
         }
     }
     if (s_final) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s_final[(seq * a.H + h) * 4096 + d_off(t, i)] = S[t][i];
+        for (int i = 0; i < 4; ++i) s_final[(seq * a.H + h) * 4096 + d_off(i)] = S[i];
     }
 }
 
@@ -580,8 +587,8 @@ hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt,
 
 hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream) {
     const dim3 grid(4, (unsigned)a.H, (unsigned)a.n_seqs);
-    if (io_dt == DT_F32) hipLaunchKernelGGL(gdn_seg_scan_kernel<3>, grid, dim3(64), 0, stream, a, s_final);
-    else hipLaunchKernelGGL(gdn_seg_scan_kernel<2>, grid, dim3(64), 0, stream, a, s_final);
+    if (io_dt == DT_F32) hipLaunchKernelGGL(gdn_seg_scan_kernel<3>, grid, dim3(256), 0, stream, a, s_final);
+    else hipLaunchKernelGGL(gdn_seg_scan_kernel<2>, grid, dim3(256), 0, stream, a, s_final);
     return hipGetLastError();
 }
 

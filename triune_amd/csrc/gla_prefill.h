@@ -207,6 +207,71 @@ __device__ void chunk_tokenwise(const PrefillParams& a, const Work& wk, int64_t 
 // one counter tracks loads and stores, and a wait for a load while a store is outstanding drains
 // both; stores issued right after the next loads are long complete when those loads are waited
 // for, one chunk later.
+// The output rows of one (sequence, head): token 0's address and the token stride in bytes, made
+// once per workgroup so the chunk loop keeps two scalars instead of the output's strides.
+struct OutCtx {
+    char* op;
+    int64_t ost;
+    int dt;
+};
+
+__device__ __forceinline__ OutCtx out_ctx(const PrefillParams& a, const Work& wk, int64_t h) {
+    OutCtx o;
+    const int64_t es = dt_size(a.o_dt);
+    o.op = reinterpret_cast<char*>(a.o) + uniform_i64((wk.b * a.o_sb + wk.row0 * a.o_st + h * a.o_sh) * es);
+    o.ost = uniform_i64(a.o_st * es);
+    o.dt = a.o_dt;
+    return o;
+}
+
+// chunk_tokenwise for the output walk, reading rows through the walk's token-0 addresses (ad) and
+// writing through oc; t_unclamped: the token whose gate stays unclamped (-1: none).
+template <typename TIn, typename TG, int DK>
+__device__ void chunk_tokenwise_out(const ChunkAddr& ad, const OutCtx& oc, int64_t t_unclamped, int c0, int64_t tc,
+                                    int nv, int g4, int r16, f32x4 (&S)[DK / 16]) {
+    constexpr int NDB = DK / 16;
+    const int oes = dt_size(oc.dt);
+    for (int t = 0; t < nv; ++t) {
+        const int64_t tt = tc + t;
+        const bool unclamped = tt == t_unclamped;
+        const TG* gr = reinterpret_cast<const TG*>(ad.g.p0 + tt * ad.g.st);
+        const TIn* kr = reinterpret_cast<const TIn*>(ad.k.p0 + tt * ad.k.st);
+        const TIn* qr = reinterpret_cast<const TIn*>(ad.q.p0 + tt * ad.q.st);
+        float dcy[NDB][4], kk[NDB][4], qq[NDB][4];
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 16 * db + 4 * g4 + i;
+                const float gg = (float)gr[d];
+                dcy[db][i] = fast_exp(unclamped ? gg : min0(gg));
+                kk[db][i] = (float)kr[d];
+                qq[db][i] = (float)qr[d];
+            }
+        const float vv = (float)reinterpret_cast<const TIn*>(ad.v.p0 + tt * ad.v.st)[c0 + r16];
+        float part = 0.f;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float s = dcy[db][i] * S[db][i] + kk[db][i] * vv;
+                S[db][i] = s;
+                part += qq[db][i] * s;
+            }
+        part += __shfl_xor(part, 16);
+        part += __shfl_xor(part, 32);
+        // o may alias g (the reference's VectorisedGLA passes out=g): every wave has read token
+        // tt's gates before any wave overwrites them with outputs
+        __syncthreads();
+        if (g4 == 0) {
+            char* op = oc.op + tt * oc.ost + (int64_t)(c0 + r16) * oes;
+            if (oc.dt == DT_F32) *reinterpret_cast<float*>(op) = part;
+            else if (oc.dt == DT_BF16) *reinterpret_cast<__bf16*>(op) = (__bf16)part;
+            else *reinterpret_cast<_Float16*>(op) = (_Float16)part;
+        }
+    }
+}
+
 struct PendingOut {
     f32x4 o[4];
     int64_t tc;
@@ -217,15 +282,14 @@ struct PendingOut {
 // Stage the pending outputs 16 tokens at a time through `stage` (this wave's 16 x OS floats of
 // LDS) and store them with the four lanes of a quad covering one token's 16 columns.
 template <bool OBF>
-__device__ __forceinline__ void flush_out(const PrefillParams& a, const Work& wk, int64_t h, int c0, const PendingOut& p,
-                                          float* stage, int os) {
+__device__ __forceinline__ void flush_out(const OutCtx& oc, int c0, const PendingOut& p, float* stage, int os) {
     const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
-    const int es = dt_size(a.o_dt);
-    const int64_t ost = a.o_st * es;
-    char* obase = reinterpret_cast<char*>(a.o) + uniform_i64((wk.b * a.o_sb + (wk.row0 + p.tc) * a.o_st + h * a.o_sh + c0) * es);
+    const int es = OBF ? 2 : dt_size(oc.dt);
+    const int64_t ost = oc.ost;
+    char* obase = oc.op + p.tc * ost + c0 * es;
     const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);  // token within 16
     const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
-    const OutRsrc orr = out_rsrc(obase, ost, es, p.nv, a.o_dt == DT_F32);
+    const OutRsrc orr = out_rsrc(obase, ost, es, p.nv, !OBF && oc.dt == DT_F32);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
         *reinterpret_cast<f32x4*>(stage + r16 * os + 4 * g4) = p.o[tb];
@@ -235,7 +299,7 @@ __device__ __forceinline__ void flush_out(const PrefillParams& a, const Work& wk
             const u32x2 w = __builtin_bit_cast(u32x2, bf16x4{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]});
             __builtin_amdgcn_raw_buffer_store_b64(w, orr.lo, (int32_t)(16 * tb * ost) + olane, 0, 0);
         } else {
-            out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, x);
+            out_store4(orr, (int32_t)(16 * tb * ost) + olane, oc.dt, x);
         }
     }
 }
@@ -253,8 +317,10 @@ struct OutStep {
     // FAST_ONLY: a chunk that needs the token-by-token path returns false right after stage 1
     // (its inputs consumed, the next chunk's loads issued, the pending outputs stored) and the
     // caller finishes it with finish_tokenwise; otherwise both paths are handled here.
+    // oc / ad: the walk's output and input addresses (the token-wise path reads rows through them);
+    // t_unclamped: the token whose gate stays unclamped (-1: none).
     template <bool FAST_ONLY, typename Hook>
-    __device__ static bool run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+    __device__ static bool run(const OutCtx& oc, const ChunkAddr& ad, int64_t t_unclamped, int64_t tc, int nv,
                                const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, PendingOut& pend,
                                Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
@@ -268,7 +334,7 @@ struct OutStep {
         float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
         float* sEG = sEM + DK;
         int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
-        const bool tail_unclamped = (a.flags & 1) && (tc + nv == wk.len);
+        const bool tail_unclamped = t_unclamped == tc + nv - 1;
 
         // ---------------- stage 1 -------------------------------------------------------
         {
@@ -324,7 +390,7 @@ struct OutStep {
         if constexpr (!late_refill) after_inputs();
         // The previous chunk's outputs, staged through this wave's slice of the A^T planes
         // (nothing reads them again before this chunk's stage 2).
-        if (pend.valid) flush_out<OBF>(a, wk, h, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
+        if (pend.valid) flush_out<OBF>(oc, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
         pend.valid = false;
         __syncthreads();
         bool fast = true;
@@ -335,7 +401,7 @@ struct OutStep {
             if (!fast) return false;
         }
         if (!FAST_ONLY && !fast) {
-            chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, c0, tc, nv, g4, r16, S);
+            chunk_tokenwise_out<TIn, TG, DK>(ad, oc, t_unclamped, c0, tc, nv, g4, r16, S);
         } else {
             // ---------------- stage 2: causal tiles of A^T -> LDS ----------------------------
             // Wave w owns tiles w, w + NW, ...: all of them are computed together (independent
@@ -439,7 +505,7 @@ struct OutStep {
             pend.nv = nv;
             pend.valid = true;
             if constexpr (!L::DEFER) {  // store now, staged through this wave's own V planes
-                flush_out<OBF>(a, wk, h, c0, pend, reinterpret_cast<float*>(sVP), L::OS);
+                flush_out<OBF>(oc, c0, pend, reinterpret_cast<float*>(sVP), L::OS);
                 pend.valid = false;
             }
         }
@@ -450,10 +516,10 @@ struct OutStep {
 
     // The rest of a chunk that run<true> returned false for.
     template <typename Hook>
-    __device__ static void finish_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                                            f32x4 (&S)[NDB], Hook&& after_inputs) {
+    __device__ static void finish_tokenwise(const OutCtx& oc, const ChunkAddr& ad, int64_t t_unclamped, int64_t tc,
+                                            int nv, f32x4 (&S)[NDB], Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
-        chunk_tokenwise<TIn, TG, DK, true>(a, wk, h, wave_id() * 16, tc, nv, g4, r16, S);
+        chunk_tokenwise_out<TIn, TG, DK>(ad, oc, t_unclamped, wave_id() * 16, tc, nv, g4, r16, S);
         constexpr bool late_refill = DK == 128 && DV == 128;
         if constexpr (late_refill) after_inputs();
         __syncthreads();
@@ -475,6 +541,8 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     // One register set: stage 1 consumes it and the next chunk's loads refill it at once, so they
     // are in flight during stages 2-3 (registers go to occupancy instead of a second set).
+    const OutCtx oc = out_ctx(a, wk, h);
+    const int64_t t_unclamped = (a.flags & 1) ? wk.len - 1 : -1;
     ChunkIn<TIn, TG, DL> A;
     chunk_load<true, CK>(A, ad, tok(0), true);
     PendingOut pend;
@@ -484,19 +552,19 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     // segment.  The fast loop has no merge with the token-wise code, so its state registers stay put.
     int64_t c = 0;
     for (; c < nch; ++c)
-        if (!St::template run<true>(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
+        if (!St::template run<true>(oc, ad, t_unclamped, tok(c), chunk_nv(c), A, S, smem, pend,
                                     [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); }))
             break;
     if (c < nch) {
-        St::finish_tokenwise(a, wk, h, tok(c), chunk_nv(c), S,
+        St::finish_tokenwise(oc, ad, t_unclamped, tok(c), chunk_nv(c), S,
                              [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
         for (++c; c < nch; ++c)
-            St::template run<false>(a, wk, h, tok(c), chunk_nv(c), A, S, smem, pend,
+            St::template run<false>(oc, ad, t_unclamped, tok(c), chunk_nv(c), A, S, smem, pend,
                                     [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
     }
     if (pend.valid)  // after the last chunk's closing barrier the A^T planes are free
-        flush_out<OBF>(a, wk, h, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
-                  St::L::OS);
+        flush_out<OBF>(oc, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
+                       St::L::OS);
 }
 
 // ---------------------------------------------------------------------------------------
