@@ -415,6 +415,32 @@ def bench_bwd(dev, reps=10):
                          "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
 
+def bench_bwd128(dev, reps=5):
+    """Chunked GLA backward at the config-4 head size (H=12, Dk=Dv=128) on one dense sequence
+    (B=1, T=16384, bf16, config-1 distributions): the gradient kernels hold 64-wide heads, so this
+    runs as four (key block, value block) sub-problems whose gradients are summed."""
+    from triune_amd.fast_gla import _prefill_bwd
+    from triune_amd.workloads import gla_inputs
+
+    q, k, v, g, s0 = (x.to(dev) for x in gla_inputs(1, 16384, 12, 128, seed=128, dtype=torch.bfloat16,
+                                                     init_std=0.1))
+    gen = torch.Generator().manual_seed(12)
+    do = torch.randn(q.shape, generator=gen).bfloat16().to(dev)
+    ds = torch.randn(s0.shape, generator=gen).to(dev)
+    fn = lambda: _prefill_bwd(q, k, v, g, s0, do, ds, 0)  # noqa: E731
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    B, T, H, D = q.shape
+    alg = 9 * B * T * H * D * 2 + 3 * B * H * D * D * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "GLA prefill backward, config-4 head size (B=1, T=16384, H=12, D=128, bf16, fp32 states)",
+            "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's PyTorch CPU scan, restated (oracle/ref_port.py), on the config-1 workload
     itself (B=4, H=6, T=16384, D=64; bf16 inputs widened to fp32, as the CPU path computes in
@@ -484,7 +510,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "scan"),
+        choices=("decode", "gdn", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -512,7 +538,7 @@ def main():
         elif args.only == "fused_decode":
             res = bench_fused_decode(args.decode_steps, dev)
         else:
-            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd,
+            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
                    "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=1024)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
@@ -524,6 +550,7 @@ def main():
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_prefill": bench_fused_prefill(dev, T=1024),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
+                                      "bwd128": bench_bwd128(dev),
                                       "scan": bench_scan(dev)}
     pre = bench_prefill(args.steps, args.warmup, dev)
     line = {

@@ -219,3 +219,58 @@ def test_bf16_extreme_decay_gradient_flow(dev, use):
         scale = max(1.0, float(rt.abs().max()))
         excess = (x.grad.double().cpu() - rt).abs() - (ulp_bf16(rt).double() + 2e-3 * scale)
         assert float(excess.max()) <= 0.0, float(excess.max())
+
+
+# --- heads wider than the gradient kernels hold: block decomposition --------------------------
+@pytest.mark.parametrize("T", [130, 700])
+def test_bf16_head_dim_128_gradients(dev, T):
+    """The default model's head size (GLA_HEAD_DIM = 128, triune/model/config.py:21): gradients
+    as sums over 64-wide key / value blocks, fp32 gradients at the 2e-3 bar, and through autograd
+    in bf16 within one ULP plus that."""
+    B, H, D = 2, 2, 128
+    q, k, v, g, s0 = gla_inputs(B, T, H, D, seed=T, dtype=torch.bfloat16, init_std=0.1)
+    do, ds = _upstream(B, T, H, D, D, T)
+    do = do.bfloat16()
+    qd, kd, vd, gd = (x.to(dev) for x in (q, k, v, g))
+    got = _prefill_bwd(qd, kd, vd, gd, s0.to(dev), do.to(dev), ds.to(dev), 0, grad_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.gla_bwd(q, k, v, g, s0, do, ds)
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "ds0"), got, ref):
+        e = _rel_err(x, r)
+        print(f"D=128 T={T} {name}: {e:.3e}", flush=True)
+        assert e <= 2e-3, (name, e)
+    xs = [x.to(dev).requires_grad_(True) for x in (q, k, v, g)]
+    o, s = fast_chunk_gla(*xs, initial_state=s0.to(dev))
+    ((o.float() * do.float().to(dev)).sum() + (s * ds.to(dev)).sum()).backward()
+    torch.cuda.synchronize()
+    for x, r in zip(xs, ref[:4]):
+        assert x.grad.dtype == torch.bfloat16
+        rt = torch.from_numpy(r)
+        scale = max(1.0, float(rt.abs().max()))
+        excess = (x.grad.double().cpu() - rt).abs() - (ulp_bf16(rt).double() + 2e-3 * scale)
+        assert float(excess.max()) <= 0.0, float(excess.max())
+
+
+@pytest.mark.parametrize("Dk,Dv", [(64, 64), (48, 80), (128, 64)])
+def test_fp32_wide_heads_gradients(dev, Dk, Dv):
+    """fp32 inputs beyond the 32-wide fp32 kernels (including unequal and non-multiple head
+    dims): gradients at the fp32 bar against the oracle."""
+    B, T, H = 2, 150, 2
+    gen = torch.Generator().manual_seed(Dk + Dv)
+    q = torch.randn(B, T, H, Dk, generator=gen) * Dk**-0.5
+    k = torch.randn(B, T, H, Dk, generator=gen)
+    v = torch.randn(B, T, H, Dv, generator=gen)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, Dk, generator=gen)) / 16
+    s0 = 0.1 * torch.randn(B, H, Dk, Dv, generator=gen)
+    do, ds = _upstream(B, T, H, Dk, Dv, Dk)
+    xs = [x.to(dev).requires_grad_(True) for x in (q, k, v, g)]
+    s0d = s0.to(dev).requires_grad_(True)
+    o, s = fast_chunk_gla(*xs, initial_state=s0d)
+    ((o * do.to(dev)).sum() + (s * ds.to(dev)).sum()).backward()
+    torch.cuda.synchronize()
+    ref = O.gla_bwd(q, k, v, g, s0, do, ds)
+    for name, x, r in zip(("dq", "dk", "dv", "dg"), xs, ref[:4]):
+        e = _rel_err(x.grad, r)
+        print(f"fp32 ({Dk},{Dv}) {name}: {e:.3e}", flush=True)
+        assert x.grad.dtype == torch.float32 and e <= 1e-5, (name, e)
+    assert _rel_err(s0d.grad, ref[4]) <= 1e-5

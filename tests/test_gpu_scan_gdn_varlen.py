@@ -226,3 +226,30 @@ def test_gdn_refuses_gradients(dev):
     with torch.no_grad():
         o, s = fast_chunk_gated_deltanet(q, k, v, g)
     assert o.shape == (1, 70, 2, 64) and not o.requires_grad
+
+
+@pytest.mark.parametrize("Dk,Dv", [(128, 128), (48, 80), (100, 200)])
+def test_fp32_wide_value_heads_dense_and_varlen(dev, Dk, Dv):
+    """fp32 heads whose kernel pair would be (128, 128) (its fp32 planes exceed the LDS), and
+    value heads wider than 128: value columns run as slices (they evolve independently), dense
+    and packed, at the fp32 bar against the oracle."""
+    gen = torch.Generator().manual_seed(Dk + Dv)
+    lens = [70, 1, 200]
+    N, H = sum(lens), 2
+    q = torch.randn(1, N, H, Dk, generator=gen) * Dk**-0.5
+    k = torch.randn(1, N, H, Dk, generator=gen)
+    v = torch.randn(1, N, H, Dv, generator=gen)
+    g = torch.nn.functional.logsigmoid(torch.randn(1, N, H, Dk, generator=gen)) / 16
+    s0 = 0.1 * torch.randn(len(lens), H, Dk, Dv, generator=gen)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32)
+    o, s = fast_chunk_gla_varlen(q.to(dev), k.to(dev), v.to(dev), g.to(dev), cu.to(dev), initial_state=s0.to(dev))
+    torch.cuda.synchronize()
+    ro, rs = O.gla_varlen_fwd(q, k, v, g, cu.numpy(), s0)
+    assert o.shape == (1, N, H, Dv) and s.shape == (len(lens), H, Dk, Dv)
+    assert _err(o.cpu(), ro) <= 1e-5 and _err(s.cpu(), rs) <= 1e-5
+    # dense: the first sequence as a batch of one
+    od, sd = fast_chunk_gla(q[:, :70].to(dev), k[:, :70].to(dev), v[:, :70].to(dev), g[:, :70].to(dev),
+                            initial_state=s0[:1].to(dev))
+    torch.cuda.synchronize()
+    rd, rsd = O.gla_fwd(q[:, :70], k[:, :70], v[:, :70], g[:, :70], s0[:1])
+    assert _err(od.cpu(), rd) <= 1e-5 and _err(sd.cpu(), rsd) <= 1e-5

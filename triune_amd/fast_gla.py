@@ -119,11 +119,14 @@ def _gate(g, q):
 def _prefill(q, k, v, g, initial_state, out, flags, save_final=True, out_dtype=None):
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
-    if Dv0 > 128:  # value columns evolve independently: run 128-wide column slices
+    # value columns evolve independently: wide values run as column slices, 128 wide, or 64 wide
+    # for fp32 inputs whose pair would be (128, 128) (its fp32 planes exceed the LDS)
+    vcap = 64 if (q.dtype == torch.float32 and _pair(Dk0, min(Dv0, 128)) == (128, 128)) else 128
+    if Dv0 > vcap:
         outs, states = [], []
-        for c in range(0, Dv0, 128):
-            s0 = None if initial_state is None else initial_state[..., c:c + 128]
-            o_c, s_c = _prefill(q, k, v[..., c:c + 128], g, s0, None, flags, save_final,
+        for c in range(0, Dv0, vcap):
+            s0 = None if initial_state is None else initial_state[..., c:c + vcap]
+            o_c, s_c = _prefill(q, k, v[..., c:c + vcap], g, s0, None, flags, save_final,
                                 out.dtype if out is not None else (out_dtype or v.dtype))
             outs.append(o_c)
             states.append(s_c)
@@ -237,10 +240,10 @@ def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None):
     the inputs' own dtypes)."""
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
+    lim = 32 if q.dtype == torch.float32 else 64  # widest head the gradient kernels hold
+    if max(Dk0, Dv0) > lim:
+        return _prefill_bwd_blocks(q, k, v, g, s0, do, ds, flags, grad_dtype, lim)
     D = 32 if max(Dk0, Dv0) <= 32 else 64
-    if max(Dk0, Dv0) > 64 or (q.dtype == torch.float32 and D > 32):
-        raise NotImplementedError(
-            f"GLA backward supports head dims <= 64 (<= 32 for float32 inputs); got ({Dk0}, {Dv0}) {q.dtype}")
     qp, kp, gp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, _gate(g, q)))
     vp = _vec_layout(_pad_last(v, D), 1)
     if do is None:
@@ -268,6 +271,40 @@ def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None):
     if ds0 is not None:
         ds0 = ds0[..., :Dk0, :Dv0].to(s0.dtype)
     return dq, dk, dv, dg, ds0
+
+
+def _prefill_bwd_blocks(q, k, v, g, s0, do, ds, flags, grad_dtype, lim):
+    """_prefill_bwd for heads wider than the gradient kernels hold, as a sum over blocks of at
+    most `lim` key dims and `lim` value columns.  The recurrence is separable in both: state entry
+    S[d][c] evolves from k[d], g[d] and v[c] alone and o sums q[d] S[d][c] over d, so block (a, b)
+    of (key dims, value columns) is an independent GLA problem with inputs q_a, k_a, g_a, v_b,
+    S0[a][b] and upstream do_b, dS[a][b].  dq, dk and dg of key block a sum over the value blocks,
+    dv of value block b over the key blocks (in fp32, rounded once), and dS0[a][b] is block
+    (a, b)'s own."""
+    B, T, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    kbl = [(i, min(i + lim, Dk0)) for i in range(0, Dk0, lim)]
+    vbl = [(j, min(j + lim, Dv0)) for j in range(0, Dv0, lim)]
+    f32 = torch.float32
+    dq = torch.zeros(B, T, H, Dk0, device=q.device, dtype=f32)
+    dk, dg = torch.zeros_like(dq), torch.zeros_like(dq)
+    dv = torch.zeros(B, T, H, Dv0, device=q.device, dtype=f32)
+    ds0 = torch.empty(B, H, Dk0, Dv0, device=q.device, dtype=f32) if s0 is not None else None
+    for a0, a1 in kbl:
+        for b0, b1 in vbl:
+            r = _prefill_bwd(q[..., a0:a1], k[..., a0:a1], v[..., b0:b1], g[..., a0:a1],
+                             None if s0 is None else s0[..., a0:a1, b0:b1],
+                             None if do is None else do[..., b0:b1],
+                             None if ds is None else ds[..., a0:a1, b0:b1], flags, grad_dtype=f32)
+            dq[..., a0:a1] += r[0]
+            dk[..., a0:a1] += r[1]
+            dv[..., b0:b1] += r[2]
+            dg[..., a0:a1] += r[3]
+            if ds0 is not None:
+                ds0[..., a0:a1, b0:b1] = r[4]
+    gd = grad_dtype or q.dtype
+    return (dq.to(gd), dk.to(gd), dv.to(grad_dtype or v.dtype), dg.to(grad_dtype or g.dtype),
+            None if ds0 is None else ds0.to(s0.dtype))
 
 
 class _ChunkGLA(torch.autograd.Function):
@@ -383,6 +420,22 @@ def fast_chunk_gla_varlen(q, k, v, g, cu_seqlens, initial_state=None, out=None, 
         q, k, v, g = q[0], k[0], v[0], g[0]
     N, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
+    # value columns evolve independently: wide values run as column slices (as _prefill does)
+    vcap = 64 if (q.dtype == torch.float32 and _pair(Dk0, min(Dv0, 128)) == (128, 128)) else 128
+    if Dv0 > vcap:
+        outs, states = [], []
+        for c in range(0, Dv0, vcap):
+            sl = slice(c, c + vcap)
+            o_c, s_c = fast_chunk_gla_varlen(
+                q, k, v[..., sl], g, cu_seqlens, None if initial_state is None else initial_state[..., sl],
+                None if out is None else (out[0] if out.dim() == 4 else out)[..., sl])
+            outs.append(o_c)
+            states.append(s_c)
+        sf = torch.cat(states, dim=-1)
+        if out is not None:
+            return out, sf
+        o = torch.cat(outs, dim=-1)
+        return (o.unsqueeze(0) if lead1 else o), sf
     Dk, Dv = _pair(Dk0, Dv0)
     cu = cu_seqlens.to(device=q.device, dtype=torch.int32).contiguous()
     n = cu.numel() - 1
