@@ -392,6 +392,123 @@ __device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[
     }
 }
 
+// ---- chunk tiles loaded straight into LDS (2-byte inputs, 64-element rows) --------------------
+// A tile holds the 64 rows (128 B each) of one input's chunk in 32 pair-rows of 256 B: 16-byte
+// unit u of token t sits at position ((t & 1) * 8 + u) ^ ((t >> 2) & 15) of pair-row t >> 1.
+// A DMA instruction writes 1 KB in lane order (lane L at +16 L), i.e. four whole pair-rows, so
+// every instruction fetches eight whole 128-byte rows (the stage-1 register loads fetch 32 bytes
+// of sixteen rows each, which keeps the L1's miss tracking full with partial lines).  The XOR
+// spreads both stage-1 reads (the 16 lanes of a quad row on tokens 4*tg + j) and transposed
+// fragment reads over all 64 banks: two lanes per bank pair, the minimum for 8-byte reads.
+constexpr int TILE_BYTES = CHUNK * 128;
+
+__device__ __forceinline__ int tile_off(int t, int byte) {
+    return (t >> 1) * 256 + (((((t & 1) << 3) | (byte >> 4)) ^ ((t >> 2) & 15)) << 4) + (byte & 15);
+}
+
+// Buffer resource words (raw buffer, stride 0) of `records` bytes from `base`.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 raw_rsrc4(const void* base, int records) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), records, 0x00020000};
+}
+
+// 16 bytes at byte offset voff of resource r into LDS at lds + 16 * lane (lds wave-uniform).
+// Issued through asm so that the compiler does not track it: it would otherwise wait for every
+// tile DMA in flight before transposed LDS reads (ds_read_b64_tr_b16), whose addresses it cannot
+// tell apart from the tiles.  Nothing reads a tile before vm_drain and a barrier.  M0 carries
+// the LDS address and is restored afterwards; one wait state separates its write from the load.
+__device__ __forceinline__ void dma16(const char* lds, int voff, i32x4 r) {
+    const uint32_t l = (uint32_t)reinterpret_cast<uintptr_t>(lds);
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(l), "v"(voff), "s"(r)
+        : "memory");
+}
+
+// This wave's two 1 KB pieces of one input's tile: the rows of the resource `r` (based at the
+// chunk's first row, token stride st bytes; records end at the segment's last row, so rows past
+// it land as zeros).  Lane L of a piece fetches the 16 bytes that belong at +16 L.
+__device__ __forceinline__ void tile_dma(char* tile, i32x4 r, int st, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int m = 2 * wave + i;               // piece: pair-rows 4m .. 4m+3
+        const int p = 4 * m + (lane >> 4);        // this lane's pair-row
+        const int val = (lane & 15) ^ ((p >> 1) & 15);
+        const int t = 2 * p + (val >> 3);         // its token and 16-byte unit
+        dma16(tile + m * 1024, t * st + (val & 7) * 16, r);
+    }
+}
+
+// Elements [col, col + N) (2-byte T, N * 2 of 4 or 8 bytes, not crossing a 16-byte unit) of
+// token t of a tile.
+template <typename T, int N>
+__device__ __forceinline__ void tile_read(Vec<T, N>& v, const char* tile, int t, int col) {
+    static_assert(sizeof(T) == 2 && (N == 2 || N == 4), "tile reads of 4 or 8 bytes");
+    const char* p = tile + tile_off(t, col * 2);
+    if constexpr (N == 4) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        v.w[0] = u.x; v.w[1] = u.y;
+    } else {
+        v.w[0] = *reinterpret_cast<const uint32_t*>(p);
+    }
+}
+
+// Rows 4*tg + j (j < 4) of a tile, as rows_load takes them from memory.
+template <typename T, int N>
+__device__ __forceinline__ void tile_rows(Vec<T, N> (&v)[4], const char* tile, int tg, int col) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tile_read(v[j], tile, 4 * tg + j, col);
+}
+
+// Instances whose inputs arrive as tiles: 2-byte inputs, the gate in the same type, 64 x 64.
+template <typename TIn, typename TG, int DK, int DV>
+constexpr bool tile_dma_inputs() {
+    return sizeof(TIn) == 2 && std::is_same<TIn, TG>::value && DK == 64 && DV == 64;
+}
+
+// Workgroup barrier for LDS traffic only: this wave's LDS operations complete, then s_barrier.
+// Unlike __syncthreads it has no release fence, which would also wait for every tile DMA in
+// flight (they count as LDS stores); the empty asm statements keep the compiler from moving memory
+// operations across it.
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Wait until every vector memory operation of this wave has completed (its tile DMAs included).
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0)
+
+// Barrier of a kernel instance: the LDS-only one where tile DMAs may be in flight.
+template <bool DMA>
+__device__ __forceinline__ void block_sync() {
+    if constexpr (DMA) lds_sync();
+    else __syncthreads();
+}
+
+// This wave's share of the tiles of the chunk at token tc (TILE_BYTES apart): q, k, g (OUT, the
+// output kernel) or k, g, v (the segment-state kernel).
+template <bool OUT>
+__device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
+    const TokAddr* src[3] = {OUT ? &ad.q : &ad.k, OUT ? &ad.k : &ad.g, OUT ? &ad.g : &ad.v};
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const TokAddr& x = *src[i];
+        const int64_t off = tc * x.st;
+        int64_t n = x.rem - off;
+        n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
+        tile_dma(tiles + i * TILE_BYTES, raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
+    }
+}
+
 // min(x, 0) in one instruction (fminf first quiets NaNs with an extra max in IEEE mode).
 __device__ __forceinline__ float min0(float x) {
     // min(x, 0) as one integer min: a float with the sign bit set is a negative int32 and keeps

@@ -30,7 +30,8 @@
 //   stage 3  wave w: O^T and the state update for value columns [16w, 16w+16); fragments with
 //            the token as K index (Kt^T, V) come from the token-major planes through the
 //            transposed LDS read
-// The next chunk's inputs are loaded into registers while the current chunk is processed.
+// The next chunk's inputs are loaded while the current chunk is processed: into registers, or
+// (2-byte inputs at 64 x 64) q, k, g / k, g, v straight into LDS tiles of whole 128-byte rows.
 // Chunks whose key-dim decay span exceeds SPAN_MAX (or that hold the reference's unclamped
 // 1-token tail) run token by token on the same state registers.
 #pragma once
@@ -311,18 +312,23 @@ struct OutStep {
     using PR = Prec<TIn>;
     static constexpr int NW = L::NW, DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NKS = DK / 32;
     static constexpr int NS = PR::NS, NX = PR::NX;
+    // q, k, g arrive as LDS tiles (tile_dma) instead of registers, v stays in registers; where the
+    // tiles keep two workgroups per CU (80 KB of LDS each; not with fp16's two V planes)
+    static constexpr bool DMA = tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + 3 * TILE_BYTES <= 80 * 1024;
 
     // One chunk: stage 1 (factors, split operands -> LDS), stage 2 (A^T tiles), stage 3 (O, S).
-    // after_inputs() runs once stage 1 has consumed `cur` (it may refill those registers).
+    // after_inputs() runs once stage 1 has consumed `cur` (it may refill those registers);
+    // DMA: stage 1 first takes q, k, g from `tiles`, and issue_tiles() runs once every wave has
+    // read them (it may refill the tiles).
     // FAST_ONLY: a chunk that needs the token-by-token path returns false right after stage 1
     // (its inputs consumed, the next chunk's loads issued, the pending outputs stored) and the
     // caller finishes it with finish_tokenwise; otherwise both paths are handled here.
     // oc / ad: the walk's output and input addresses (the token-wise path reads rows through them);
     // t_unclamped: the token whose gate stays unclamped (-1: none).
-    template <bool FAST_ONLY, typename Hook>
+    template <bool FAST_ONLY, typename Hook, typename TileHook>
     __device__ static bool run(const OutCtx& oc, const ChunkAddr& ad, int64_t t_unclamped, int64_t tc, int nv,
-                               const ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, PendingOut& pend,
-                               Hook&& after_inputs) {
+                               ChunkIn<TIn, TG, DL>& cur, f32x4 (&S)[NDB], char* smem, const char* tiles,
+                               PendingOut& pend, Hook&& after_inputs, TileHook&& issue_tiles) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int d0 = wave * DPW, c0 = wave * 16;
@@ -337,6 +343,13 @@ struct OutStep {
         const bool tail_unclamped = t_unclamped == tc + nv - 1;
 
         // ---------------- stage 1 -------------------------------------------------------
+        if constexpr (DMA) {
+            vm_drain();  // this wave's tile pieces (and v rows) of the chunk have landed ...
+            lds_sync();  // ... and every other wave's
+            tile_rows(cur.q, tiles, tg, dl0);
+            tile_rows(cur.k, tiles + TILE_BYTES, tg, dl0);
+            tile_rows(cur.g, tiles + 2 * TILE_BYTES, tg, dl0);
+        }
         {
             float G[4][DL], GC[DL], x[4][DL];
             chunk_float<CK>(cur.g, G, tg, nv);
@@ -392,7 +405,8 @@ struct OutStep {
         // (nothing reads them again before this chunk's stage 2).
         if (pend.valid) flush_out<OBF>(oc, c0, pend, reinterpret_cast<float*>(sAT) + wave * 16 * L::OS, L::OS);
         pend.valid = false;
-        __syncthreads();
+        block_sync<DMA>();
+        if constexpr (DMA) issue_tiles();  // every wave has read this chunk's tiles
         bool fast = true;
 #pragma unroll
         for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
@@ -439,7 +453,7 @@ struct OutStep {
                     lds_put_row<NS, 4>(sAT, L::ATP, (i * 64 + lane) * 4, x);
                 }
             }
-            __syncthreads();
+            block_sync<DMA>();
 
             // ---------------- stage 3: outputs and state for columns [c0, c0+16) ------------
             Split8<NX> vf[2];
@@ -510,7 +524,8 @@ struct OutStep {
             }
         }
         if constexpr (late_refill) after_inputs();
-        __syncthreads();  // the next chunk rewrites LDS
+        // the next chunk rewrites LDS (DMA: after the barrier that opens it)
+        if constexpr (!DMA) __syncthreads();
         return true;
     }
 
@@ -522,13 +537,14 @@ struct OutStep {
         chunk_tokenwise_out<TIn, TG, DK>(ad, oc, t_unclamped, wave_id() * 16, tc, nv, g4, r16, S);
         constexpr bool late_refill = DK == 128 && DV == 128;
         if constexpr (late_refill) after_inputs();
-        __syncthreads();
+        block_sync<DMA>();
     }
 };
 
 // Outputs of one segment from its carried-in state S (K3).
 template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF>
-__device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem) {
+__device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[DK / 16], char* smem,
+                             char* tiles) {
     using St = OutStep<TIn, TG, DK, DV, CK, OBF>;
     constexpr int DL = St::DL;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
@@ -544,7 +560,18 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     const OutCtx oc = out_ctx(a, wk, h);
     const int64_t t_unclamped = (a.flags & 1) ? wk.len - 1 : -1;
     ChunkIn<TIn, TG, DL> A;
-    chunk_load<true, CK>(A, ad, tok(0), true);
+    // DMA: q, k, g of chunk c go to the tiles (issued once stage 1 of chunk c - 1 has read them),
+    // v rows to registers; otherwise every input to registers.
+    auto refill = [&](int64_t c1) {
+        if constexpr (St::DMA) rows_load<CK>(A.v, chunk_rsrc(ad.v, tok(c1), c1 < nch), ad.v, tok(c1));
+        else chunk_load<true, CK>(A, ad, tok(c1), c1 < nch);
+    };
+    auto tiles_for = [&](int64_t c1) {
+        if constexpr (St::DMA)
+            if (c1 < nch) chunk_tiles<true>(tiles, ad, tok(c1), wave, lane);
+    };
+    tiles_for(0);
+    refill(0);
     PendingOut pend;
     pend.valid = false;
     // Chunks take the MFMA path until one needs the token-by-token path (a decay span beyond the
@@ -552,16 +579,16 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     // segment.  The fast loop has no merge with the token-wise code, so its state registers stay put.
     int64_t c = 0;
     for (; c < nch; ++c)
-        if (!St::template run<true>(oc, ad, t_unclamped, tok(c), chunk_nv(c), A, S, smem, pend,
-                                    [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); }))
+        if (!St::template run<true>(oc, ad, t_unclamped, tok(c), chunk_nv(c), A, S, smem, tiles, pend,
+                                    [&] { refill(c + 1); }, [&] { tiles_for(c + 1); }))
             break;
     if (c < nch) {
-        St::finish_tokenwise(oc, ad, t_unclamped, tok(c), chunk_nv(c), S,
-                             [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
+        St::finish_tokenwise(oc, ad, t_unclamped, tok(c), chunk_nv(c), S, [&] { refill(c + 1); });
         for (++c; c < nch; ++c)
-            St::template run<false>(oc, ad, t_unclamped, tok(c), chunk_nv(c), A, S, smem, pend,
-                                    [&] { chunk_load<true, CK>(A, ad, tok(c + 1), c + 1 < nch); });
+            St::template run<false>(oc, ad, t_unclamped, tok(c), chunk_nv(c), A, S, smem, tiles, pend,
+                                    [&] { refill(c + 1); }, [&] { tiles_for(c + 1); });
     }
+    if constexpr (St::DMA) lds_sync();  // DMA: no closing barrier after a chunk
     if (pend.valid)  // after the last chunk's closing barrier the A^T planes are free
         flush_out<OBF>(oc, wave * 16, pend, reinterpret_cast<float*>(smem + St::L::OFF_AT) + wave * 16 * St::L::OS,
                        St::L::OS);
@@ -587,19 +614,34 @@ struct StateStep {
     using L = Lay<TIn, DK, DV, false, PREP>;
     using PR = Prec<TIn>;
     static constexpr int NW = L::NW, DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NS = PR::NS, NX = PR::NX;
+    // k, g, v arrive as LDS tiles (tile_dma), two tile sets: the next chunk's fly during this one;
+    // where they keep two workgroups per CU (80 KB of LDS each)
+    static constexpr bool DMA =
+        !PREP && tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + 6 * TILE_BYTES <= 80 * 1024;
 
     // PREP: rc holds this chunk's RoPE table rows; once consumed, the rows of chunk tc_next (the
     // chunk walked after this one) are loaded into it.
-    template <typename Hook>
+    // DMA: the chunk's k, g, v come from `tiles`; issue_next() runs once every wave is past the
+    // previous chunk (it may refill the other tile set).
+    template <typename Hook, typename TileHook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t tc, int nv,
-                               const ChunkIn<TIn, TG, DL>& cur, const ChunkAddr& ad, const RopeAddr& rad,
+                               ChunkIn<TIn, TG, DL>& cur, const ChunkAddr& ad, const RopeAddr& rad,
                                RopeIn<DL>& rc, int64_t tc_next, bool next_valid, f32x4 (&Lst)[NDB],
-                               float (&Gseg)[DL], char* smem, Hook&& after_inputs) {
+                               float (&Gseg)[DL], char* smem, const char* tiles, Hook&& after_inputs,
+                               TileHook&& issue_next) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int dl0 = stage1_dim0<DK, DPW, PREP>(wave, row);
         char* sKW = smem + L::OFF_KT;  // exp-weighted k rows
         char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
+        if constexpr (DMA) {
+            vm_drain();  // this wave's tile pieces of the chunk have landed ...
+            lds_sync();  // ... and every other wave's; every wave is done with the other set
+            issue_next();
+            tile_rows(cur.k, tiles, tg, dl0);
+            tile_rows(cur.g, tiles + TILE_BYTES, tg, dl0);
+            tile_rows(cur.v, tiles + 2 * TILE_BYTES, tg, wave * 16 + 4 * row);
+        }
         if constexpr (PREP) {
             float* sNRM = reinterpret_cast<float*>(smem + L::OFF_NRM);
             float G[4][DL], GC[DL], x[4][DL], y[4][DL];  // g, q, k
@@ -691,7 +733,7 @@ struct StateStep {
             lds_put_v_rows<TIn, NX, CK>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
         }
         after_inputs();
-        __syncthreads();
+        block_sync<DMA>();
         Split8<NX> vf[2];
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
@@ -702,13 +744,14 @@ struct StateStep {
                 const Split8<NS> kf = lds_frag_tr<NS>(sKW, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
                 Lst[db] = mfma_split<NS, NX, NS>(kf, vf[k2], Lst[db]);
             }
-        __syncthreads();  // the next chunk rewrites LDS
+        // the next chunk rewrites LDS (DMA: after the barrier that opens it)
+        if constexpr (!DMA) __syncthreads();
     }
 };
 
 template <typename TIn, typename TG, int DK, int DV, bool CK, bool PREP = false>
 __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&Lst)[DK / 16],
-                                   float (&Gseg)[DK / (DV / 16) / 4], char* smem) {
+                                   float (&Gseg)[DK / (DV / 16) / 4], char* smem, char* tiles) {
     using St = StateStep<TIn, TG, DK, DV, CK, PREP>;
     constexpr int DL = St::DL;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
@@ -728,18 +771,36 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     ChunkIn<TIn, TG, DL> A, B;
     RopeIn<DL> R;  // PREP: the RoPE table rows of the chunk being walked, loaded one chunk ahead
+    if constexpr (St::DMA) {
+        // tile set 0 holds even steps of the walk (chunks nch-1, nch-3, ...), set 1 odd steps
+        char* t0 = tiles;
+        char* t1 = tiles + 3 * TILE_BYTES;
+        auto fill = [&](char* t, int64_t c1) {
+            if (c1 >= 0) chunk_tiles<false>(t, ad, tok(c1), wave, lane);
+        };
+        fill(t0, nch - 1);
+        for (int64_t c = nch - 1; c >= 1; c -= 2) {
+            St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, 0, false, Lst, Gseg, smem, t0, [] {},
+                    [&] { fill(t1, c - 1); });
+            St::run(a, wk, tok(c - 1), chunk_nv(c - 1), A, ad, rad, R, 0, false, Lst, Gseg, smem, t1, [] {},
+                    [&] { fill(t0, c - 2); });
+        }
+        if (nch & 1) St::run(a, wk, tok(0), chunk_nv(0), A, ad, rad, R, 0, false, Lst, Gseg, smem, t0, [] {}, [] {});
+        return;
+    }
     if constexpr (PREP) rope_load<CK>(R, rad, tok(nch - 1), a.use_rope != 0);
     chunk_load<PREP, CK>(A, ad, tok(nch - 1), true);
     __builtin_amdgcn_sched_barrier(0);  // issue order A, B on every path (see segment_walk)
     chunk_load<PREP, CK>(B, ad, tok(nch - 2), nch > 1);
     // pairs of chunks from the end, then chunk 0 if nch is odd (single-exit loop, as in segment_walk)
     for (int64_t c = nch - 1; c >= 1; c -= 2) {
-        St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, tok(c - 1), true, Lst, Gseg, smem,
-                [&] { chunk_load<PREP, CK>(A, ad, tok(c - 2), c >= 2); });
-        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, ad, rad, R, tok(c - 2), c >= 2, Lst, Gseg, smem,
-                [&] { chunk_load<PREP, CK>(B, ad, tok(c - 3), c >= 3); });
+        St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, tok(c - 1), true, Lst, Gseg, smem, tiles,
+                [&] { chunk_load<PREP, CK>(A, ad, tok(c - 2), c >= 2); }, [] {});
+        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, ad, rad, R, tok(c - 2), c >= 2, Lst, Gseg, smem, tiles,
+                [&] { chunk_load<PREP, CK>(B, ad, tok(c - 3), c >= 3); }, [] {});
     }
-    if (nch & 1) St::run(a, wk, tok(0), chunk_nv(0), A, ad, rad, R, tok(0), false, Lst, Gseg, smem, [] {});
+    if (nch & 1)
+        St::run(a, wk, tok(0), chunk_nv(0), A, ad, rad, R, tok(0), false, Lst, Gseg, smem, tiles, [] {}, [] {});
 }
 
 
@@ -749,6 +810,7 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     using L = Lay<TIn, DK, DV, false, PREP>;
     constexpr int DL = L::DPW / 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
+    __shared__ __attribute__((aligned(16))) char tiles[StateStep<TIn, TG, DK, DV, CK, PREP>::DMA ? 6 * TILE_BYTES : 16];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
@@ -759,7 +821,7 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     for (int db = 0; db < DK / 16; ++db) S[db] = zero4();
 #pragma unroll
     for (int i = 0; i < DL; ++i) Gseg[i] = 0.f;
-    segment_state_walk<TIn, TG, DK, DV, CK, PREP>(a, wk, h, S, Gseg, smem);
+    segment_state_walk<TIn, TG, DK, DV, CK, PREP>(a, wk, h, S, Gseg, smem, tiles);
     float* st = a.ws_state + (w * a.H + h) * (int64_t)DK * DV;
 #pragma unroll
     for (int db = 0; db < DK / 16; ++db)
@@ -776,6 +838,9 @@ template <typename TIn, typename TG, int DK, int DV, bool CK, bool OBF>
 __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void gla_seg_output_kernel(PrefillParams a) {
     using L = Lay<TIn, DK, DV, true>;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
+    // input tiles: an array of their own, so the compiler knows that reads of smem never wait for
+    // the tile DMAs in flight
+    __shared__ __attribute__((aligned(16))) char tiles[OutStep<TIn, TG, DK, DV, CK, OBF>::DMA ? 3 * TILE_BYTES : 16];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
@@ -786,7 +851,7 @@ __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void
     for (int db = 0; db < DK / 16; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) S[db][i] = st[state_off(db, i, g4, r16, wave, DV)];
-    segment_walk<TIn, TG, DK, DV, CK, OBF>(a, wk, h, S, smem);
+    segment_walk<TIn, TG, DK, DV, CK, OBF>(a, wk, h, S, smem, tiles);
 }
 
 }  // namespace triune
