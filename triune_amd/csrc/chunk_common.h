@@ -392,18 +392,28 @@ __device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[
     }
 }
 
-// ---- chunk tiles loaded straight into LDS (2-byte inputs, 64-element rows) --------------------
-// A tile holds the 64 rows (128 B each) of one input's chunk in 32 pair-rows of 256 B: 16-byte
-// unit u of token t sits at position ((t & 1) * 8 + u) ^ ((t >> 2) & 15) of pair-row t >> 1.
-// A DMA instruction writes 1 KB in lane order (lane L at +16 L), i.e. four whole pair-rows, so
-// every instruction fetches eight whole 128-byte rows (the stage-1 register loads fetch 32 bytes
-// of sixteen rows each, which keeps the L1's miss tracking full with partial lines).  The XOR
-// spreads both stage-1 reads (the 16 lanes of a quad row on tokens 4*tg + j) and transposed
-// fragment reads over all 64 banks: two lanes per bank pair, the minimum for 8-byte reads.
-constexpr int TILE_BYTES = CHUNK * 128;
+// ---- chunk tiles loaded straight into LDS (2-byte inputs, rows of RB = 128 or 256 bytes) -----
+// A tile holds the 64 rows of one input's chunk with the 16-byte units of each row permuted:
+//   RB = 128 (D = 64): 32 pair-rows of 256 B; unit u of token t sits at position
+//            ((t & 1) * 8 + u) ^ ((t >> 2) & 15) of pair-row t >> 1;
+//   RB = 256 (D = 128): unit u of token t sits at position u ^ ((t >> 2) & 15) of row t.
+// A DMA instruction writes 1 KB in lane order (lane L at +16 L), i.e. whole rows, so every
+// instruction fetches whole 128/256-byte rows (the stage-1 register loads fetch 32 bytes of
+// sixteen rows each, which keeps the L1's miss tracking full with partial lines).  The XOR
+// spreads the stage-1 reads (the 16 lanes of a quad row on tokens 4*tg + j) over all 64 banks:
+// two lanes per bank pair, the minimum for 8-byte reads.
+template <int RB>
+constexpr int tile_bytes() {
+    static_assert(RB == 128 || RB == 256, "tile rows of 128 or 256 bytes");
+    return CHUNK * RB;
+}
 
+template <int RB>
 __device__ __forceinline__ int tile_off(int t, int byte) {
-    return (t >> 1) * 256 + (((((t & 1) << 3) | (byte >> 4)) ^ ((t >> 2) & 15)) << 4) + (byte & 15);
+    if constexpr (RB == 128)
+        return (t >> 1) * 256 + (((((t & 1) << 3) | (byte >> 4)) ^ ((t >> 2) & 15)) << 4) + (byte & 15);
+    else
+        return t * 256 + (((byte >> 4) ^ ((t >> 2) & 15)) << 4) + (byte & 15);
 }
 
 // Buffer resource words (raw buffer, stride 0) of `records` bytes from `base`.
@@ -432,26 +442,35 @@ __device__ __forceinline__ void dma16(const char* lds, int voff, i32x4 r) {
         : "memory");
 }
 
-// This wave's two 1 KB pieces of one input's tile: the rows of the resource `r` (based at the
-// chunk's first row, token stride st bytes; records end at the segment's last row, so rows past
-// it land as zeros).  Lane L of a piece fetches the 16 bytes that belong at +16 L.
+// This wave's two 1 KB pieces of one input's tile (a tile is 8 (RB = 128) or 16 (RB = 256) pieces,
+// two per wave of the workgroup): the rows of the resource `r` (based at the chunk's first row,
+// token stride st bytes; records end at the segment's last row, so rows past it land as zeros).
+// Lane L of a piece fetches the 16 bytes that belong at +16 L.
+template <int RB>
 __device__ __forceinline__ void tile_dma(char* tile, i32x4 r, int st, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int m = 2 * wave + i;               // piece: pair-rows 4m .. 4m+3
-        const int p = 4 * m + (lane >> 4);        // this lane's pair-row
-        const int val = (lane & 15) ^ ((p >> 1) & 15);
-        const int t = 2 * p + (val >> 3);         // its token and 16-byte unit
-        dma16(tile + m * 1024, t * st + (val & 7) * 16, r);
+        const int m = 2 * wave + i;
+        int t, u;
+        if constexpr (RB == 128) {             // piece m: pair-rows 4m .. 4m+3
+            const int p = 4 * m + (lane >> 4);
+            const int val = (lane & 15) ^ ((p >> 1) & 15);
+            t = 2 * p + (val >> 3);
+            u = val & 7;
+        } else {                               // piece m: rows 4m .. 4m+3
+            t = 4 * m + (lane >> 4);
+            u = (lane & 15) ^ (m & 15);
+        }
+        dma16(tile + m * 1024, t * st + u * 16, r);
     }
 }
 
 // Elements [col, col + N) (2-byte T, N * 2 of 4 or 8 bytes, not crossing a 16-byte unit) of
 // token t of a tile.
-template <typename T, int N>
+template <int RB, typename T, int N>
 __device__ __forceinline__ void tile_read(Vec<T, N>& v, const char* tile, int t, int col) {
     static_assert(sizeof(T) == 2 && (N == 2 || N == 4), "tile reads of 4 or 8 bytes");
-    const char* p = tile + tile_off(t, col * 2);
+    const char* p = tile + tile_off<RB>(t, col * 2);
     if constexpr (N == 4) {
         const uint2 u = *reinterpret_cast<const uint2*>(p);
         v.w[0] = u.x; v.w[1] = u.y;
@@ -461,16 +480,17 @@ __device__ __forceinline__ void tile_read(Vec<T, N>& v, const char* tile, int t,
 }
 
 // Rows 4*tg + j (j < 4) of a tile, as rows_load takes them from memory.
-template <typename T, int N>
+template <int RB, typename T, int N>
 __device__ __forceinline__ void tile_rows(Vec<T, N> (&v)[4], const char* tile, int tg, int col) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) tile_read(v[j], tile, 4 * tg + j, col);
+    for (int j = 0; j < 4; ++j) tile_read<RB>(v[j], tile, 4 * tg + j, col);
 }
 
-// Instances whose inputs arrive as tiles: 2-byte inputs, the gate in the same type, 64 x 64.
+// Instances whose inputs can arrive as tiles: 2-byte inputs, the gate in the same type, square
+// 64 or 128 heads (a tile row per token of each input; two 1 KB pieces per wave).
 template <typename TIn, typename TG, int DK, int DV>
 constexpr bool tile_dma_inputs() {
-    return sizeof(TIn) == 2 && std::is_same<TIn, TG>::value && DK == 64 && DV == 64;
+    return sizeof(TIn) == 2 && std::is_same<TIn, TG>::value && DK == DV && (DK == 64 || DK == 128);
 }
 
 // Workgroup barrier for LDS traffic only: this wave's LDS operations complete, then s_barrier.
@@ -494,9 +514,9 @@ __device__ __forceinline__ void block_sync() {
     else __syncthreads();
 }
 
-// This wave's share of the tiles of the chunk at token tc (TILE_BYTES apart): q, k, g (OUT, the
+// This wave's share of the tiles of the chunk at token tc (tile_bytes<RB>() apart): q, k, g (OUT, the
 // output kernel) or k, g, v (the segment-state kernel).
-template <bool OUT>
+template <bool OUT, int RB>
 __device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
     const TokAddr* src[3] = {OUT ? &ad.q : &ad.k, OUT ? &ad.k : &ad.g, OUT ? &ad.g : &ad.v};
 #pragma unroll
@@ -505,7 +525,7 @@ __device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, in
         const int64_t off = tc * x.st;
         int64_t n = x.rem - off;
         n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
-        tile_dma(tiles + i * TILE_BYTES, raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
+        tile_dma<RB>(tiles + i * tile_bytes<RB>(), raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
     }
 }
 

@@ -313,8 +313,10 @@ struct OutStep {
     static constexpr int NW = L::NW, DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NKS = DK / 32;
     static constexpr int NS = PR::NS, NX = PR::NX;
     // q, k, g arrive as LDS tiles (tile_dma) instead of registers, v stays in registers; where the
-    // tiles keep two workgroups per CU (80 KB of LDS each; not with fp16's two V planes)
-    static constexpr bool DMA = tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + 3 * TILE_BYTES <= 80 * 1024;
+    // tiles keep the kernel's workgroups per CU (MINB: two at 64, fp16's two V planes excluded)
+    static constexpr int RB = DK * 2, TB = CHUNK * RB;
+    static constexpr int MINB = (PR::NS == 3 || DK == 128) ? 1 : 2;
+    static constexpr bool DMA = tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + 3 * TB <= 160 * 1024 / MINB;
 
     // One chunk: stage 1 (factors, split operands -> LDS), stage 2 (A^T tiles), stage 3 (O, S).
     // after_inputs() runs once stage 1 has consumed `cur` (it may refill those registers);
@@ -346,9 +348,9 @@ struct OutStep {
         if constexpr (DMA) {
             vm_drain();  // this wave's tile pieces (and v rows) of the chunk have landed ...
             lds_sync();  // ... and every other wave's
-            tile_rows(cur.q, tiles, tg, dl0);
-            tile_rows(cur.k, tiles + TILE_BYTES, tg, dl0);
-            tile_rows(cur.g, tiles + 2 * TILE_BYTES, tg, dl0);
+            tile_rows<RB>(cur.q, tiles, tg, dl0);
+            tile_rows<RB>(cur.k, tiles + TB, tg, dl0);
+            tile_rows<RB>(cur.g, tiles + 2 * TB, tg, dl0);
         }
         {
             float G[4][DL], GC[DL], x[4][DL];
@@ -399,7 +401,7 @@ struct OutStep {
         }
         // The next chunk's loads go out now and fly during stages 2-3, except at (128, 128),
         // where their registers would push the wave past 256 VGPRs: there they go out after stage 3.
-        constexpr bool late_refill = DK == 128 && DV == 128;
+        constexpr bool late_refill = DK == 128 && DV == 128 && !DMA;
         if constexpr (!late_refill) after_inputs();
         // The previous chunk's outputs, staged through this wave's slice of the A^T planes
         // (nothing reads them again before this chunk's stage 2).
@@ -535,7 +537,7 @@ struct OutStep {
                                             int nv, f32x4 (&S)[NDB], Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
         chunk_tokenwise_out<TIn, TG, DK>(ad, oc, t_unclamped, wave_id() * 16, tc, nv, g4, r16, S);
-        constexpr bool late_refill = DK == 128 && DV == 128;
+        constexpr bool late_refill = DK == 128 && DV == 128 && !DMA;
         if constexpr (late_refill) after_inputs();
         block_sync<DMA>();
     }
@@ -568,7 +570,7 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     };
     auto tiles_for = [&](int64_t c1) {
         if constexpr (St::DMA)
-            if (c1 < nch) chunk_tiles<true>(tiles, ad, tok(c1), wave, lane);
+            if (c1 < nch) chunk_tiles<true, St::RB>(tiles, ad, tok(c1), wave, lane);
     };
     tiles_for(0);
     refill(0);
@@ -615,9 +617,11 @@ struct StateStep {
     using PR = Prec<TIn>;
     static constexpr int NW = L::NW, DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NS = PR::NS, NX = PR::NX;
     // k, g, v arrive as LDS tiles (tile_dma), two tile sets: the next chunk's fly during this one;
-    // where they keep two workgroups per CU (80 KB of LDS each)
-    static constexpr bool DMA =
-        !PREP && tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + 6 * TILE_BYTES <= 80 * 1024;
+    // where they keep the workgroups per CU the plan assumes (two at 64 x 64; at 128 x 128 its
+    // registers already hold one per CU)
+    static constexpr int RB = DK * 2, TB = CHUNK * RB;
+    static constexpr bool DMA = !PREP && tile_dma_inputs<TIn, TG, DK, DV>() &&
+                                L::BYTES + 6 * TB <= (DK == 128 ? 160 : 80) * 1024;
 
     // PREP: rc holds this chunk's RoPE table rows; once consumed, the rows of chunk tc_next (the
     // chunk walked after this one) are loaded into it.
@@ -638,9 +642,9 @@ struct StateStep {
             vm_drain();  // this wave's tile pieces of the chunk have landed ...
             lds_sync();  // ... and every other wave's; every wave is done with the other set
             issue_next();
-            tile_rows(cur.k, tiles, tg, dl0);
-            tile_rows(cur.g, tiles + TILE_BYTES, tg, dl0);
-            tile_rows(cur.v, tiles + 2 * TILE_BYTES, tg, wave * 16 + 4 * row);
+            tile_rows<RB>(cur.k, tiles, tg, dl0);
+            tile_rows<RB>(cur.g, tiles + TB, tg, dl0);
+            tile_rows<RB>(cur.v, tiles + 2 * TB, tg, wave * 16 + 4 * row);
         }
         if constexpr (PREP) {
             float* sNRM = reinterpret_cast<float*>(smem + L::OFF_NRM);
@@ -774,9 +778,9 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
     if constexpr (St::DMA) {
         // tile set 0 holds even steps of the walk (chunks nch-1, nch-3, ...), set 1 odd steps
         char* t0 = tiles;
-        char* t1 = tiles + 3 * TILE_BYTES;
+        char* t1 = tiles + 3 * St::TB;
         auto fill = [&](char* t, int64_t c1) {
-            if (c1 >= 0) chunk_tiles<false>(t, ad, tok(c1), wave, lane);
+            if (c1 >= 0) chunk_tiles<false, St::RB>(t, ad, tok(c1), wave, lane);
         };
         fill(t0, nch - 1);
         for (int64_t c = nch - 1; c >= 1; c -= 2) {
@@ -810,7 +814,8 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     using L = Lay<TIn, DK, DV, false, PREP>;
     constexpr int DL = L::DPW / 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
-    __shared__ __attribute__((aligned(16))) char tiles[StateStep<TIn, TG, DK, DV, CK, PREP>::DMA ? 6 * TILE_BYTES : 16];
+    using St = StateStep<TIn, TG, DK, DV, CK, PREP>;
+    __shared__ __attribute__((aligned(16))) char tiles[St::DMA ? 6 * St::TB : 16];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
@@ -840,7 +845,8 @@ __global__ __launch_bounds__(DV * 4, (Prec<TIn>::F32 || DK == 128) ? 1 : 2) void
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     // input tiles: an array of their own, so the compiler knows that reads of smem never wait for
     // the tile DMAs in flight
-    __shared__ __attribute__((aligned(16))) char tiles[OutStep<TIn, TG, DK, DV, CK, OBF>::DMA ? 3 * TILE_BYTES : 16];
+    using St = OutStep<TIn, TG, DK, DV, CK, OBF>;
+    __shared__ __attribute__((aligned(16))) char tiles[St::DMA ? 3 * St::TB : 16];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
