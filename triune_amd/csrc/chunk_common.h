@@ -529,6 +529,20 @@ __device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, in
     }
 }
 
+// The same for q, k, g, v (the pre-processing segment-state kernel).
+template <int RB>
+__device__ __forceinline__ void chunk_tiles4(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
+    const TokAddr* src[4] = {&ad.q, &ad.k, &ad.g, &ad.v};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const TokAddr& x = *src[i];
+        const int64_t off = tc * x.st;
+        int64_t n = x.rem - off;
+        n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
+        tile_dma<RB>(tiles + i * tile_bytes<RB>(), raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
+    }
+}
+
 // min(x, 0) in one instruction (fminf first quiets NaNs with an extra max in IEEE mode).
 __device__ __forceinline__ float min0(float x) {
     // min(x, 0) as one integer min: a float with the sign bit set is a negative int32 and keeps

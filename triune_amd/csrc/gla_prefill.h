@@ -611,17 +611,39 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
 // follows reads exactly what the reference's scan would.  A row's norm spans the NW waves' dims:
 // each wave stores its partial sums of squares and a barrier inside stage 1 separates the stores
 // from the reads.
+// Pre-processed q, k, g rows of one chunk waiting to be written back (PREP with tiles: a chunk's
+// rows go out at the start of the next step, right after its wait for the tiles, so that wait -
+// vector memory operations complete in order - never includes stores issued just before it).
+template <typename TIn, typename TG, int DL>
+struct PrepOut {
+    Vec<TIn, DL> q[4], k[4];
+    Vec<TG, DL> g[4];
+    int64_t tc;
+    bool valid;
+};
+
+template <bool CK, typename TIn, typename TG, int DL>
+__device__ __forceinline__ void prep_out_store(PrepOut<TIn, TG, DL>& po, const ChunkAddr& ad) {
+    if (!po.valid) return;
+    rows_store<CK>(po.q, chunk_rsrc(ad.q, po.tc, true), ad.q, po.tc);
+    rows_store<CK>(po.k, chunk_rsrc(ad.k, po.tc, true), ad.k, po.tc);
+    rows_store<CK>(po.g, chunk_rsrc(ad.g, po.tc, true), ad.g, po.tc);
+    po.valid = false;
+}
+
 template <typename TIn, typename TG, int DK, int DV, bool CK, bool PREP = false>
 struct StateStep {
     using L = Lay<TIn, DK, DV, false, PREP>;
     using PR = Prec<TIn>;
     static constexpr int NW = L::NW, DPW = L::DPW, DL = DPW / 4, NDB = DK / 16, NS = PR::NS, NX = PR::NX;
-    // k, g, v arrive as LDS tiles (tile_dma), two tile sets: the next chunk's fly during this one;
-    // where they keep the workgroups per CU the plan assumes (two at 64 x 64; at 128 x 128 its
-    // registers already hold one per CU)
+    // Inputs arrive as LDS tiles (tile_dma) where the tiles keep the workgroups per CU the plan
+    // assumes (two at 64 x 64; at 128 x 128 the registers already hold one per CU): k, g, v in two
+    // tile sets, the next chunk's in flight during this one; PREP: q, k, g, v in one set, the next
+    // chunk's issued once every wave has read this one (at the norm-partials barrier).
     static constexpr int RB = DK * 2, TB = CHUNK * RB;
-    static constexpr bool DMA = !PREP && tile_dma_inputs<TIn, TG, DK, DV>() &&
-                                L::BYTES + 6 * TB <= (DK == 128 ? 160 : 80) * 1024;
+    static constexpr int NT = PREP ? 4 : 6;  // tiles of the kernel
+    static constexpr bool DMA =
+        tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + NT * TB <= (DK == 128 ? 160 : 80) * 1024;
 
     // PREP: rc holds this chunk's RoPE table rows; once consumed, the rows of chunk tc_next (the
     // chunk walked after this one) are loaded into it.
@@ -631,8 +653,8 @@ struct StateStep {
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t tc, int nv,
                                ChunkIn<TIn, TG, DL>& cur, const ChunkAddr& ad, const RopeAddr& rad,
                                RopeIn<DL>& rc, int64_t tc_next, bool next_valid, f32x4 (&Lst)[NDB],
-                               float (&Gseg)[DL], char* smem, const char* tiles, Hook&& after_inputs,
-                               TileHook&& issue_next) {
+                               float (&Gseg)[DL], char* smem, const char* tiles, PrepOut<TIn, TG, DL>& po,
+                               Hook&& after_inputs, TileHook&& issue_next) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int dl0 = stage1_dim0<DK, DPW, PREP>(wave, row);
@@ -641,10 +663,18 @@ struct StateStep {
         if constexpr (DMA) {
             vm_drain();  // this wave's tile pieces of the chunk have landed ...
             lds_sync();  // ... and every other wave's; every wave is done with the other set
-            issue_next();
-            tile_rows<RB>(cur.k, tiles, tg, dl0);
-            tile_rows<RB>(cur.g, tiles + TB, tg, dl0);
-            tile_rows<RB>(cur.v, tiles + 2 * TB, tg, wave * 16 + 4 * row);
+            if constexpr (PREP) {
+                prep_out_store<CK>(po, ad);  // the previous chunk's pre-processed rows
+                tile_rows<RB>(cur.q, tiles, tg, dl0);
+                tile_rows<RB>(cur.k, tiles + TB, tg, dl0);
+                tile_rows<RB>(cur.g, tiles + 2 * TB, tg, dl0);
+                tile_rows<RB>(cur.v, tiles + 3 * TB, tg, wave * 16 + 4 * row);
+            } else {
+                issue_next();
+                tile_rows<RB>(cur.k, tiles, tg, dl0);
+                tile_rows<RB>(cur.g, tiles + TB, tg, dl0);
+                tile_rows<RB>(cur.v, tiles + 2 * TB, tg, wave * 16 + 4 * row);
+            }
         }
         if constexpr (PREP) {
             float* sNRM = reinterpret_cast<float*>(smem + L::OFF_NRM);
@@ -668,7 +698,8 @@ struct StateStep {
             norm_partials<DL>(x, sNRM + wave * 64, tg, row);
             norm_partials<DL>(y, sNRM + (NW + wave) * 64, tg, row);
             lds_put_v_rows<TIn, NX, CK>(sVP, L::VPP, L::VS, 4 * row, cur.v, tg, nv);
-            __syncthreads();  // every wave's norm partials
+            block_sync<DMA>();  // every wave's norm partials (and every wave has read the tiles)
+            if constexpr (DMA) issue_next();
             if (a.use_rope) {
                 rope_rows<DL>(x, rc, row);
                 rope_rows<DL>(y, rc, row);
@@ -688,9 +719,20 @@ struct StateStep {
                 vec_pack<TIn, DL>(y[j], ko[j]);
                 vec_pack<TG, DL>(G[j], go[j]);
             }
-            rows_store<CK>(qo, chunk_rsrc(ad.q, tc, true), ad.q, tc);
-            rows_store<CK>(ko, chunk_rsrc(ad.k, tc, true), ad.k, tc);
-            rows_store<CK>(go, chunk_rsrc(ad.g, tc, true), ad.g, tc);
+            if constexpr (DMA) {  // written back at the start of the next step (or after the walk)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    po.q[j] = qo[j];
+                    po.k[j] = ko[j];
+                    po.g[j] = go[j];
+                }
+                po.tc = tc;
+                po.valid = true;
+            } else {
+                rows_store<CK>(qo, chunk_rsrc(ad.q, tc, true), ad.q, tc);
+                rows_store<CK>(ko, chunk_rsrc(ad.k, tc, true), ad.k, tc);
+                rows_store<CK>(go, chunk_rsrc(ad.g, tc, true), ad.g, tc);
+            }
             // the state from the rounded values, as the output kernel will see them
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -775,7 +817,21 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     ChunkIn<TIn, TG, DL> A, B;
     RopeIn<DL> R;  // PREP: the RoPE table rows of the chunk being walked, loaded one chunk ahead
-    if constexpr (St::DMA) {
+    PrepOut<TIn, TG, DL> po;
+    po.valid = false;
+    if constexpr (St::DMA && PREP) {  // one tile set, refilled for the chunk walked next
+        auto fill = [&](int64_t c1) {
+            if (c1 >= 0) chunk_tiles4<St::RB>(tiles, ad, tok(c1), wave, lane);
+        };
+        rope_load<CK>(R, rad, tok(nch - 1), a.use_rope != 0);
+        fill(nch - 1);
+        for (int64_t c = nch - 1; c >= 0; --c)
+            St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, tok(c - 1), c >= 1, Lst, Gseg, smem, tiles, po, [] {},
+                    [&] { fill(c - 1); });
+        prep_out_store<CK>(po, ad);
+        return;
+    }
+    if constexpr (St::DMA && !PREP) {
         // tile set 0 holds even steps of the walk (chunks nch-1, nch-3, ...), set 1 odd steps
         char* t0 = tiles;
         char* t1 = tiles + 3 * St::TB;
@@ -784,12 +840,12 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
         };
         fill(t0, nch - 1);
         for (int64_t c = nch - 1; c >= 1; c -= 2) {
-            St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, 0, false, Lst, Gseg, smem, t0, [] {},
+            St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, 0, false, Lst, Gseg, smem, t0, po, [] {},
                     [&] { fill(t1, c - 1); });
-            St::run(a, wk, tok(c - 1), chunk_nv(c - 1), A, ad, rad, R, 0, false, Lst, Gseg, smem, t1, [] {},
+            St::run(a, wk, tok(c - 1), chunk_nv(c - 1), A, ad, rad, R, 0, false, Lst, Gseg, smem, t1, po, [] {},
                     [&] { fill(t0, c - 2); });
         }
-        if (nch & 1) St::run(a, wk, tok(0), chunk_nv(0), A, ad, rad, R, 0, false, Lst, Gseg, smem, t0, [] {}, [] {});
+        if (nch & 1) St::run(a, wk, tok(0), chunk_nv(0), A, ad, rad, R, 0, false, Lst, Gseg, smem, t0, po, [] {}, [] {});
         return;
     }
     if constexpr (PREP) rope_load<CK>(R, rad, tok(nch - 1), a.use_rope != 0);
@@ -798,13 +854,13 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
     chunk_load<PREP, CK>(B, ad, tok(nch - 2), nch > 1);
     // pairs of chunks from the end, then chunk 0 if nch is odd (single-exit loop, as in segment_walk)
     for (int64_t c = nch - 1; c >= 1; c -= 2) {
-        St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, tok(c - 1), true, Lst, Gseg, smem, tiles,
+        St::run(a, wk, tok(c), chunk_nv(c), A, ad, rad, R, tok(c - 1), true, Lst, Gseg, smem, tiles, po,
                 [&] { chunk_load<PREP, CK>(A, ad, tok(c - 2), c >= 2); }, [] {});
-        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, ad, rad, R, tok(c - 2), c >= 2, Lst, Gseg, smem, tiles,
+        St::run(a, wk, tok(c - 1), chunk_nv(c - 1), B, ad, rad, R, tok(c - 2), c >= 2, Lst, Gseg, smem, tiles, po,
                 [&] { chunk_load<PREP, CK>(B, ad, tok(c - 3), c >= 3); }, [] {});
     }
     if (nch & 1)
-        St::run(a, wk, tok(0), chunk_nv(0), A, ad, rad, R, tok(0), false, Lst, Gseg, smem, tiles, [] {}, [] {});
+        St::run(a, wk, tok(0), chunk_nv(0), A, ad, rad, R, tok(0), false, Lst, Gseg, smem, tiles, po, [] {}, [] {});
 }
 
 
@@ -815,7 +871,7 @@ __global__ __launch_bounds__(DV * 4, 2) void gla_seg_state_kernel(PrefillParams 
     constexpr int DL = L::DPW / 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     using St = StateStep<TIn, TG, DK, DV, CK, PREP>;
-    __shared__ __attribute__((aligned(16))) char tiles[St::DMA ? 6 * St::TB : 16];
+    __shared__ __attribute__((aligned(16))) char tiles[St::DMA ? St::NT * St::TB : 16];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
