@@ -393,27 +393,36 @@ __device__ __forceinline__ void chunk_float(const Vec<T, N> (&v)[4], float (&x)[
 }
 
 // ---- chunk tiles loaded straight into LDS (2-byte inputs, rows of RB = 128 or 256 bytes) -----
-// A tile holds the 64 rows of one input's chunk with the 16-byte units of each row permuted:
+// A tile holds the 64 rows of one input's chunk with the 16-byte units of each row permuted by
+// s = the token group g = (t >> 2) & 7 spread over the unit-index bits other than FB:
 //   RB = 128 (D = 64): 32 pair-rows of 256 B; unit u of token t sits at position
-//            ((t & 1) * 8 + u) ^ ((t >> 2) & 15) of pair-row t >> 1;
-//   RB = 256 (D = 128): unit u of token t sits at position u ^ ((t >> 2) & 15) of row t.
+//            ((t & 1) * 8 + u) ^ s of pair-row t >> 1;
+//   RB = 256 (D = 128): unit u of token t sits at position u ^ s of row t.
 // A DMA instruction writes 1 KB in lane order (lane L at +16 L), i.e. whole rows, so every
 // instruction fetches whole 128/256-byte rows (the stage-1 register loads fetch 32 bytes of
-// sixteen rows each, which keeps the L1's miss tracking full with partial lines).  The XOR
-// spreads the stage-1 reads (the 16 lanes of a quad row on tokens 4*tg + j) over all 64 banks:
-// two lanes per bank pair, the minimum for 8-byte reads.
+// sixteen rows each, which keeps the L1's miss tracking full with partial lines).  In a stage-1
+// read the 32 lanes of an LDS cycle cover token groups 0..7 (tokens 4*tg + j) and two units of
+// each row that differ in bit FB of the unit index (FB = 0 for the plain dim mapping; 2 or 3 for
+// the pre-processing one at 64 or 128 dims); s varies the other three bits, so those lanes land on
+// 32 distinct 8-byte bank pairs: no bank conflict.
 template <int RB>
 constexpr int tile_bytes() {
     static_assert(RB == 128 || RB == 256, "tile rows of 128 or 256 bytes");
     return CHUNK * RB;
 }
 
-template <int RB>
+template <int FB>
+__device__ __forceinline__ int tile_swz(int g) {
+    return (g & ((1 << FB) - 1)) | ((g >> FB) << (FB + 1));
+}
+
+template <int RB, int FB>
 __device__ __forceinline__ int tile_off(int t, int byte) {
+    const int s = tile_swz<FB>((t >> 2) & 7);
     if constexpr (RB == 128)
-        return (t >> 1) * 256 + (((((t & 1) << 3) | (byte >> 4)) ^ ((t >> 2) & 15)) << 4) + (byte & 15);
+        return (t >> 1) * 256 + (((((t & 1) << 3) | (byte >> 4)) ^ s) << 4) + (byte & 15);
     else
-        return t * 256 + (((byte >> 4) ^ ((t >> 2) & 15)) << 4) + (byte & 15);
+        return t * 256 + (((byte >> 4) ^ s) << 4) + (byte & 15);
 }
 
 // Buffer resource words (raw buffer, stride 0) of `records` bytes from `base`.
@@ -446,7 +455,7 @@ __device__ __forceinline__ void dma16(const char* lds, int voff, i32x4 r) {
 // two per wave of the workgroup): the rows of the resource `r` (based at the chunk's first row,
 // token stride st bytes; records end at the segment's last row, so rows past it land as zeros).
 // Lane L of a piece fetches the 16 bytes that belong at +16 L.
-template <int RB>
+template <int RB, int FB>
 __device__ __forceinline__ void tile_dma(char* tile, i32x4 r, int st, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -454,12 +463,12 @@ __device__ __forceinline__ void tile_dma(char* tile, i32x4 r, int st, int wave, 
         int t, u;
         if constexpr (RB == 128) {             // piece m: pair-rows 4m .. 4m+3
             const int p = 4 * m + (lane >> 4);
-            const int val = (lane & 15) ^ ((p >> 1) & 15);
+            const int val = (lane & 15) ^ tile_swz<FB>((p >> 1) & 7);
             t = 2 * p + (val >> 3);
             u = val & 7;
         } else {                               // piece m: rows 4m .. 4m+3
             t = 4 * m + (lane >> 4);
-            u = (lane & 15) ^ (m & 15);
+            u = (lane & 15) ^ tile_swz<FB>(m & 7);
         }
         dma16(tile + m * 1024, t * st + u * 16, r);
     }
@@ -467,10 +476,10 @@ __device__ __forceinline__ void tile_dma(char* tile, i32x4 r, int st, int wave, 
 
 // Elements [col, col + N) (2-byte T, N * 2 of 4 or 8 bytes, not crossing a 16-byte unit) of
 // token t of a tile.
-template <int RB, typename T, int N>
+template <int RB, int FB, typename T, int N>
 __device__ __forceinline__ void tile_read(Vec<T, N>& v, const char* tile, int t, int col) {
     static_assert(sizeof(T) == 2 && (N == 2 || N == 4), "tile reads of 4 or 8 bytes");
-    const char* p = tile + tile_off<RB>(t, col * 2);
+    const char* p = tile + tile_off<RB, FB>(t, col * 2);
     if constexpr (N == 4) {
         const uint2 u = *reinterpret_cast<const uint2*>(p);
         v.w[0] = u.x; v.w[1] = u.y;
@@ -480,10 +489,10 @@ __device__ __forceinline__ void tile_read(Vec<T, N>& v, const char* tile, int t,
 }
 
 // Rows 4*tg + j (j < 4) of a tile, as rows_load takes them from memory.
-template <int RB, typename T, int N>
+template <int RB, int FB, typename T, int N>
 __device__ __forceinline__ void tile_rows(Vec<T, N> (&v)[4], const char* tile, int tg, int col) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) tile_read<RB>(v[j], tile, 4 * tg + j, col);
+    for (int j = 0; j < 4; ++j) tile_read<RB, FB>(v[j], tile, 4 * tg + j, col);
 }
 
 // Instances whose inputs can arrive as tiles: 2-byte inputs, the gate in the same type, square
@@ -516,7 +525,7 @@ __device__ __forceinline__ void block_sync() {
 
 // This wave's share of the tiles of the chunk at token tc (tile_bytes<RB>() apart): q, k, g (OUT, the
 // output kernel) or k, g, v (the segment-state kernel).
-template <bool OUT, int RB>
+template <bool OUT, int RB, int FB>
 __device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
     const TokAddr* src[3] = {OUT ? &ad.q : &ad.k, OUT ? &ad.k : &ad.g, OUT ? &ad.g : &ad.v};
 #pragma unroll
@@ -525,12 +534,12 @@ __device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, in
         const int64_t off = tc * x.st;
         int64_t n = x.rem - off;
         n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
-        tile_dma<RB>(tiles + i * tile_bytes<RB>(), raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
+        tile_dma<RB, FB>(tiles + i * tile_bytes<RB>(), raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
     }
 }
 
 // The same for q, k, g, v (the pre-processing segment-state kernel).
-template <int RB>
+template <int RB, int FB>
 __device__ __forceinline__ void chunk_tiles4(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
     const TokAddr* src[4] = {&ad.q, &ad.k, &ad.g, &ad.v};
 #pragma unroll
@@ -539,7 +548,7 @@ __device__ __forceinline__ void chunk_tiles4(char* tiles, const ChunkAddr& ad, i
         const int64_t off = tc * x.st;
         int64_t n = x.rem - off;
         n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
-        tile_dma<RB>(tiles + i * tile_bytes<RB>(), raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
+        tile_dma<RB, FB>(tiles + i * tile_bytes<RB>(), raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
     }
 }
 

@@ -314,7 +314,7 @@ struct OutStep {
     static constexpr int NS = PR::NS, NX = PR::NX;
     // q, k, g arrive as LDS tiles (tile_dma) instead of registers, v stays in registers; where the
     // tiles keep the kernel's workgroups per CU (MINB: two at 64, fp16's two V planes excluded)
-    static constexpr int RB = DK * 2, TB = CHUNK * RB;
+    static constexpr int RB = DK * 2, TB = CHUNK * RB, FB = 0;
     static constexpr int MINB = (PR::NS == 3 || DK == 128) ? 1 : 2;
     static constexpr bool DMA = tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + 3 * TB <= 160 * 1024 / MINB;
 
@@ -348,9 +348,9 @@ struct OutStep {
         if constexpr (DMA) {
             vm_drain();  // this wave's tile pieces (and v rows) of the chunk have landed ...
             lds_sync();  // ... and every other wave's
-            tile_rows<RB>(cur.q, tiles, tg, dl0);
-            tile_rows<RB>(cur.k, tiles + TB, tg, dl0);
-            tile_rows<RB>(cur.g, tiles + 2 * TB, tg, dl0);
+            tile_rows<RB, FB>(cur.q, tiles, tg, dl0);
+            tile_rows<RB, FB>(cur.k, tiles + TB, tg, dl0);
+            tile_rows<RB, FB>(cur.g, tiles + 2 * TB, tg, dl0);
         }
         {
             float G[4][DL], GC[DL], x[4][DL];
@@ -570,7 +570,7 @@ __device__ void segment_walk(const PrefillParams& a, const Work& wk, int64_t h, 
     };
     auto tiles_for = [&](int64_t c1) {
         if constexpr (St::DMA)
-            if (c1 < nch) chunk_tiles<true, St::RB>(tiles, ad, tok(c1), wave, lane);
+            if (c1 < nch) chunk_tiles<true, St::RB, St::FB>(tiles, ad, tok(c1), wave, lane);
     };
     tiles_for(0);
     refill(0);
@@ -642,6 +642,8 @@ struct StateStep {
     // chunk's issued once every wave has read this one (at the norm-partials barrier).
     static constexpr int RB = DK * 2, TB = CHUNK * RB;
     static constexpr int NT = PREP ? 4 : 6;  // tiles of the kernel
+    // unit-index bit that varies within a quad row's stage-1 read (stage1_dim0)
+    static constexpr int FB = !PREP ? 0 : (RB == 128 ? 2 : 3);
     static constexpr bool DMA =
         tile_dma_inputs<TIn, TG, DK, DV>() && L::BYTES + NT * TB <= (DK == 128 ? 160 : 80) * 1024;
 
@@ -665,15 +667,15 @@ struct StateStep {
             lds_sync();  // ... and every other wave's; every wave is done with the other set
             if constexpr (PREP) {
                 prep_out_store<CK>(po, ad);  // the previous chunk's pre-processed rows
-                tile_rows<RB>(cur.q, tiles, tg, dl0);
-                tile_rows<RB>(cur.k, tiles + TB, tg, dl0);
-                tile_rows<RB>(cur.g, tiles + 2 * TB, tg, dl0);
-                tile_rows<RB>(cur.v, tiles + 3 * TB, tg, wave * 16 + 4 * row);
+                tile_rows<RB, FB>(cur.q, tiles, tg, dl0);
+                tile_rows<RB, FB>(cur.k, tiles + TB, tg, dl0);
+                tile_rows<RB, FB>(cur.g, tiles + 2 * TB, tg, dl0);
+                tile_rows<RB, FB>(cur.v, tiles + 3 * TB, tg, wave * 16 + 4 * row);
             } else {
                 issue_next();
-                tile_rows<RB>(cur.k, tiles, tg, dl0);
-                tile_rows<RB>(cur.g, tiles + TB, tg, dl0);
-                tile_rows<RB>(cur.v, tiles + 2 * TB, tg, wave * 16 + 4 * row);
+                tile_rows<RB, FB>(cur.k, tiles, tg, dl0);
+                tile_rows<RB, FB>(cur.g, tiles + TB, tg, dl0);
+                tile_rows<RB, FB>(cur.v, tiles + 2 * TB, tg, wave * 16 + 4 * row);
             }
         }
         if constexpr (PREP) {
@@ -821,7 +823,7 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
     po.valid = false;
     if constexpr (St::DMA && PREP) {  // one tile set, refilled for the chunk walked next
         auto fill = [&](int64_t c1) {
-            if (c1 >= 0) chunk_tiles4<St::RB>(tiles, ad, tok(c1), wave, lane);
+            if (c1 >= 0) chunk_tiles4<St::RB, St::FB>(tiles, ad, tok(c1), wave, lane);
         };
         rope_load<CK>(R, rad, tok(nch - 1), a.use_rope != 0);
         fill(nch - 1);
@@ -836,7 +838,7 @@ __device__ void segment_state_walk(const PrefillParams& a, const Work& wk, int64
         char* t0 = tiles;
         char* t1 = tiles + 3 * St::TB;
         auto fill = [&](char* t, int64_t c1) {
-            if (c1 >= 0) chunk_tiles<false, St::RB>(t, ad, tok(c1), wave, lane);
+            if (c1 >= 0) chunk_tiles<false, St::RB, St::FB>(t, ad, tok(c1), wave, lane);
         };
         fill(t0, nch - 1);
         for (int64_t c = nch - 1; c >= 1; c -= 2) {
