@@ -480,9 +480,11 @@ def cpu_baseline(budget_s=12.0):
 
 
 def _traffic_from_profiles(key="output_kernel_bytes_per_launch"):
-    """HBM bytes per output-kernel launch (or per pass) measured with rocprofv3 FETCH_SIZE /
-    WRITE_SIZE counters and scaled by the same counters on a copy of known size
-    (profiles/prefill_traffic.json, written from those runs); None when nothing is recorded."""
+    """A figure of the config-1 prefill measured with rocprofv3 counters on this build
+    (profiles/prefill_traffic.json, written from those runs): HBM bytes per output-kernel launch
+    or per pass (FETCH_SIZE / WRITE_SIZE scaled by the same counters on a copy of known size), or
+    the MFMA busy fraction of a kernel (the MfmaUtil counter: SQ_VALU_MFMA_BUSY_CYCLES over
+    GRBM_GUI_ACTIVE x SIMDs); None when nothing is recorded."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "prefill_traffic.json")
     try:
         with open(path) as f:
@@ -500,6 +502,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary workload lines (GDN, varlen, pre-processing, fused decode, backward)")
+    ap.add_argument("--fused-prefill-t", type=int, default=1024, metavar="T",
+                    help="sequence length of the fused pre-processing prefill leg (default 1024, the tile "
+                    "VectorisedGLA prefills in)")
     ap.add_argument(
         "--copy-probe",
         type=int,
@@ -539,7 +544,7 @@ def main():
             res = bench_fused_decode(args.decode_steps, dev)
         else:
             res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
-                   "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=1024)}[args.only](dev)
+                   "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     # Order: the CPU baseline first (the GPU idles meanwhile), then the secondary GPU legs, then
@@ -548,7 +553,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline()
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
-                                      "fused_prefill": bench_fused_prefill(dev, T=1024),
+                                      "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "bwd128": bench_bwd128(dev),
                                       "scan": bench_scan(dev)}
@@ -596,6 +601,8 @@ def main():
             },
             "mfma_alg_tflops": round(pre["tflops"], 2),
             "mfma_alg_frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
+            "mfma_busy": _traffic_from_profiles("mfma_busy_output_kernel"),
+            "mfma_busy_state_kernel": _traffic_from_profiles("mfma_busy_state_kernel"),
         },
         "cpu_baseline": cpu,
     }

@@ -139,10 +139,11 @@ def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin
 
     The fused form runs while the call is small enough for the chunk kernels to be latency-bound
     (B * H * ceil(T / 64) at most 4 per compute unit, as at VectorisedGLA's 1024-token prefill tiles,
-    attention.py:458-499: 34.6 against 39.4 us for the two-step pipeline at B = 4, H = 6, T = 1024
+    attention.py:458-499: 35.0 against 36.1 us for the two-step pipeline at B = 4, H = 6, T = 1024
     on MI355X).  Past that the kernels are throughput-bound and the pre-processing work weighs more
-    inside the segment-state kernel than as a pass of its own (at T = 16384: 217 against 183 us), so
-    larger calls run fused_qkv_g_prep_inplace and then the prefill, with the same results.
+    inside the segment-state kernel than as a pass of its own (T = 4096: 71 against 65 us; T = 16384:
+    206 against 173 us), so larger calls run fused_qkv_g_prep_inplace and then the prefill, with the
+    same results.
 
     qkv: [B, T, 3, H, HD] raw projections (bf16 or fp16), g: [B, T, H, HD] raw gate (same dtype),
     cos/sin: [T, HD] (used when use_rope; converted to fp32 if needed), initial_state: [B, H, HD,
