@@ -513,9 +513,6 @@ __device__ __forceinline__ void lds_sync() {
     asm volatile("" ::: "memory");
 }
 
-// Wait until every vector memory operation of this wave has completed (its tile DMAs included).
-__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0)
-
 // Barrier of a kernel instance: the LDS-only one where tile DMAs may be in flight.
 template <bool DMA>
 __device__ __forceinline__ void block_sync() {
@@ -523,13 +520,13 @@ __device__ __forceinline__ void block_sync() {
     else __syncthreads();
 }
 
-// This wave's share of the tiles of the chunk at token tc (tile_bytes<RB>() apart): q, k, g (OUT, the
-// output kernel) or k, g, v (the segment-state kernel).
-template <bool OUT, int RB, int FB>
-__device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
-    const TokAddr* src[3] = {OUT ? &ad.q : &ad.k, OUT ? &ad.k : &ad.g, OUT ? &ad.g : &ad.v};
+// This wave's share of the tiles of the chunk at token tc of the N inputs `src` (tile i at
+// tiles + i * tile_bytes<RB>()).
+template <int RB, int FB, int N>
+__device__ __forceinline__ void tiles_from(char* tiles, const TokAddr* const (&src)[N], int64_t tc, int wave,
+                                           int lane) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < N; ++i) {
         const TokAddr& x = *src[i];
         const int64_t off = tc * x.st;
         int64_t n = x.rem - off;
@@ -538,18 +535,18 @@ __device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, in
     }
 }
 
-// The same for q, k, g, v (the pre-processing segment-state kernel).
+// q, k, g (OUT, the output kernel) or k, g, v (the segment-state kernel).
+template <bool OUT, int RB, int FB>
+__device__ __forceinline__ void chunk_tiles(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
+    const TokAddr* const src[3] = {OUT ? &ad.q : &ad.k, OUT ? &ad.k : &ad.g, OUT ? &ad.g : &ad.v};
+    tiles_from<RB, FB>(tiles, src, tc, wave, lane);
+}
+
+// q, k, g, v (the pre-processing segment-state kernel).
 template <int RB, int FB>
 __device__ __forceinline__ void chunk_tiles4(char* tiles, const ChunkAddr& ad, int64_t tc, int wave, int lane) {
-    const TokAddr* src[4] = {&ad.q, &ad.k, &ad.g, &ad.v};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const TokAddr& x = *src[i];
-        const int64_t off = tc * x.st;
-        int64_t n = x.rem - off;
-        n = n < 0 ? 0 : (n > 0x7fffffff ? 0x7fffffff : n);
-        tile_dma<RB, FB>(tiles + i * tile_bytes<RB>(), raw_rsrc4(x.p0 + off, (int)n), x.st, wave, lane);
-    }
+    const TokAddr* const src[4] = {&ad.q, &ad.k, &ad.g, &ad.v};
+    tiles_from<RB, FB>(tiles, src, tc, wave, lane);
 }
 
 // min(x, 0) in one instruction (fminf first quiets NaNs with an extra max in IEEE mode).

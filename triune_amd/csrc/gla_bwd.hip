@@ -365,6 +365,12 @@ template <typename TIn, typename TG, int D, bool CK>
 struct BwdStep {
     using L = BLay<TIn, D>;
     static constexpr int NS = L::NS, NX = L::NX, NW = L::NW, NDB = D / 16, NKS = D / 32, DL = 4;
+    // q, k, g, v, dO arrive as one LDS tile set (tile_dma) where it fits beside the planes: the next
+    // chunk's tiles are issued once every wave has read this chunk's (after stage 1) and have
+    // landed by the wait before this chunk's stores, so the next step reads them after the
+    // barrier that follows those stores.
+    static constexpr int RB = D * 2, TB = CHUNK * RB;
+    static constexpr bool DMA = tile_dma_inputs<TIn, TG, D, D>() && L::BYTES + 5 * TB <= 160 * 1024;
 
     // Causal 16x16 tiles (key block sb <= query block tb) of X^T with X[t][s] = U_t . W_s over D,
     // for tiles first, first + NW, ... < 10; stored masked as rows of the plane P[t][s].
@@ -403,10 +409,11 @@ struct BwdStep {
         }
     }
 
-    template <typename Hook>
+    template <typename Hook, typename TileHook>
     __device__ static void run(const BwdParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                               const BwdIn<TIn, TG>& cur, f32x4 (&dH)[NDB], float (&acc)[DL], char* smem,
-                               const RowsOut (&go)[4], Hook&& after_inputs) {
+                               BwdIn<TIn, TG>& cur, f32x4 (&dH)[NDB], float (&acc)[DL], char* smem,
+                               const char* tiles, const RowsOut (&go)[4], Hook&& after_inputs,
+                               TileHook&& issue_tiles) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int c0 = 16 * wave;       // key dims of dq / dk, value columns of dv / dH
@@ -438,6 +445,13 @@ struct BwdStep {
             }
         }
         // ---------------- stage 1: factors, split operands -> LDS ---------------------------
+        if constexpr (DMA) {
+            tile_rows<RB, 0>(cur.c.q, tiles, tg, dl0);
+            tile_rows<RB, 0>(cur.c.k, tiles + TB, tg, dl0);
+            tile_rows<RB, 0>(cur.c.g, tiles + 2 * TB, tg, dl0);
+            tile_rows<RB, 0>(cur.c.v, tiles + 3 * TB, tg, c0 + 4 * row);
+            tile_rows<RB, 0>(cur.d, tiles + 4 * TB, tg, c0 + 4 * row);
+        }
         float qx[4][DL], kx[4][DL], fq[4][DL];
         uint32_t pass = 0;  // bit 4*j + i: token 4*tg + j, dim dl0 + i passes its gate gradient
         {
@@ -492,7 +506,14 @@ struct BwdStep {
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sDO, L::ROWP, (4 * tg + j) * L::RS + c0 + 4 * row, vx[j]);
         }
         after_inputs();
-        __syncthreads();
+        block_sync<DMA>();
+        if constexpr (DMA) {
+            // the starting-state rows (loaded at the top, stage 1 covered their latency) are in, so
+            // stage 3's use of them waits for nothing issued later; then the next chunk's tiles,
+            // every wave having read this chunk's
+            wait_vmem();
+            issue_tiles();
+        }
         bool fast = true;
 #pragma unroll
         for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
@@ -508,7 +529,7 @@ struct BwdStep {
             }
             causal_tiles<NS, NS>(sQT, sKT, L::ROWP, sPA, wave);                         // A[t][s] = Qt_t . Kt_s
             causal_tiles<NX, NX>(sDO, sV, L::ROWP, sPB, (wave + NW - 10 % NW) % NW);   // B[t][s] = dO_t . V_s
-            __syncthreads();
+            block_sync<DMA>();
 
             // ---------------- stage 3 ------------------------------------------------------
 #pragma unroll
@@ -613,11 +634,12 @@ struct BwdStep {
         } else {
             // token by token: zero the dq / dk planes (nobody reads the A / B planes now)
             for (int e = threadIdx.x; e < 2 * CHUNK * L::FS; e += NW * 64) sFQ[e] = 0.f;  // sFK follows sFQ
-            __syncthreads();
+            block_sync<DMA>();
             bwd_tokenwise<TIn, TG, D>(a, wk, h, tc, nv, dH, sFQ, sFK, L::FS);
         }
-        __syncthreads();  // stage 3 is done with every plane
-        wait_vmem();      // the previous chunk's inputs are in: this chunk's stores do not delay them
+        block_sync<DMA>();  // stage 3 is done with every plane
+        wait_vmem();  // the next chunk's inputs (registers, or tiles: read after the barrier below) are
+                      // in, so this chunk's stores do not delay them
         if (fast) {
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
@@ -628,7 +650,7 @@ struct BwdStep {
             store_tiles(ov.base + uniform_i64(tc * ov.ost + c0 * ov.es), ov.ost, ov.es, ov.dt, nv, dV,
                         reinterpret_cast<float*>(sPH) + wave * 16 * L::OS, L::OS);
         }
-        __syncthreads();
+        block_sync<DMA>();
 
         // ---------------- epilogue (stage-1 layout): dq, dk, dg ------------------------------
         {
@@ -669,6 +691,7 @@ __global__ __launch_bounds__(D * 4, 1) void gla_bwd_chunk_kernel(BwdParams a) {
     using L = typename St::L;
     constexpr int NDB = D / 16, DL = 4;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
+    __shared__ __attribute__((aligned(16))) char tiles[St::DMA ? 5 * St::TB : 16];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a.f, w, wk)) return;
@@ -710,10 +733,22 @@ __global__ __launch_bounds__(D * 4, 1) void gla_bwd_chunk_kernel(BwdParams a) {
                            rows_out(a.dv, a.dv_sb, a.dv_st, a.dv_sh, a.d_dt, wk, h),
                            rows_out(a.dg, a.dg_sb, a.dg_st, a.dg_sh, a.dg_dt, wk, h)};
     BwdIn<TIn, TG> A;
+    if constexpr (St::DMA) {
+        const TokAddr* const src[5] = {&ad.c.q, &ad.c.k, &ad.c.g, &ad.c.v, &ad.d};
+        auto fill = [&](int64_t c1) {
+            if (c1 >= 0) tiles_from<St::RB, 0>(tiles, src, tok(c1), wave, lane);
+        };
+        fill(nch - 1);
+        wait_vmem();  // the first chunk's tiles (later ones land before each chunk's stores)
+        lds_sync();
+        for (int64_t c = nch - 1; c >= 0; --c)
+            St::run(a, wk, h, tok(c), chunk_nv(c), A, dH, acc, smem, tiles, go, [] {}, [&] { fill(c - 1); });
+        return;
+    }
     bwd_load<CK>(A, ad, tok(nch - 1), true);
     for (int64_t c = nch - 1; c >= 0; --c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, dH, acc, smem, go,
-                [&] { bwd_load<CK>(A, ad, tok(c - 1), c >= 1); });
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, dH, acc, smem, tiles, go,
+                [&] { bwd_load<CK>(A, ad, tok(c - 1), c >= 1); }, [] {});
 }
 
 // ---------------------------------------------------------------------------------------

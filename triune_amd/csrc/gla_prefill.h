@@ -346,7 +346,7 @@ struct OutStep {
 
         // ---------------- stage 1 -------------------------------------------------------
         if constexpr (DMA) {
-            vm_drain();  // this wave's tile pieces (and v rows) of the chunk have landed ...
+            wait_vmem();  // this wave's tile pieces (and v rows) of the chunk have landed ...
             lds_sync();  // ... and every other wave's
             tile_rows<RB, FB>(cur.q, tiles, tg, dl0);
             tile_rows<RB, FB>(cur.k, tiles + TB, tg, dl0);
@@ -663,7 +663,7 @@ struct StateStep {
         char* sKW = smem + L::OFF_KT;  // exp-weighted k rows
         char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
         if constexpr (DMA) {
-            vm_drain();  // this wave's tile pieces of the chunk have landed ...
+            wait_vmem();  // this wave's tile pieces of the chunk have landed ...
             lds_sync();  // ... and every other wave's; every wave is done with the other set
             if constexpr (PREP) {
                 prep_out_store<CK>(po, ad);  // the previous chunk's pre-processed rows
