@@ -76,6 +76,8 @@ enum {
 /* Prefill flags. */
 #define TRIUNE_FLAG_TAIL_UNCLAMPED 0x1 /* last token of each sequence keeps g > 0 (see below) */
 #define TRIUNE_FLAG_SEG_SHIFT 8        /* bits 8..15: chunks per segment, 0 = automatic */
+#define TRIUNE_FLAG_BWD_ACC_QKG 0x2    /* backward: add dq, dk, dg into their fp32 buffers */
+#define TRIUNE_FLAG_BWD_ACC_V 0x4      /* backward: add dv into its fp32 buffer */
 
 /* Gated DeltaNet beta kinds. */
 enum {
@@ -205,6 +207,10 @@ int triune_hip_gla_prefill_varlen(const void* q, const void* k, const void* v, c
  * dg_dtype; ds0 fp32 [B, H, Dk, Dv] or NULL.  Dk == Dv in {32, 64} (32 only for fp32 I/O); q, k, v,
  * g, dout rows 16-byte aligned, gradient rows 8-byte aligned.  workspace: at least
  * triune_hip_gla_prefill_bwd_workspace_size() bytes, 16-byte aligned.
+ * flags: the prefill's, plus TRIUNE_FLAG_BWD_ACC_QKG / TRIUNE_FLAG_BWD_ACC_V: the call adds its
+ * dq, dk, dg / dv to what those buffers hold instead of writing them (fp32 buffers only, else
+ * TRIUNE_ERR_DTYPE), so a head wider than the kernels run as key/value blocks sums the blocks'
+ * gradients in place.
  * Replaces: the backward of fast_chunk_gla (fast_gla.py:692-778) for T > 1. */
 size_t triune_hip_gla_prefill_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int flags);
 int triune_hip_gla_prefill_bwd(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,

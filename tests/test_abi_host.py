@@ -167,6 +167,24 @@ def test_noalloc_prefill_validation():
     assert b"static scratch" in lib.triune_hip_error_string(-7)
 
 
+def test_bwd_accumulate_flags_need_fp32_gradients():
+    """TRIUNE_FLAG_BWD_ACC_QKG / _V add into the gradient buffers, which only fp32 buffers hold
+    exactly: with bf16 gradients the call is rejected before any launch."""
+    lib = L.lib()
+    f = lib.triune_hip_gla_prefill_bwd
+    st = (ctypes.c_int64 * 27)(*([64 * 128 * 64, 64 * 128, 128] * 9))
+
+    def call(d_dt, dg_dt, flags):
+        return f(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _FAKE, st, None, None, _FAKE, _FAKE, _FAKE, d_dt, _FAKE, dg_dt,
+                 None, 1, 64, 1, 64, 64, flags, None, 0, None)
+
+    assert call(1, 0, L.FLAG_BWD_ACC_QKG) == -3
+    assert call(0, 1, L.FLAG_BWD_ACC_QKG) == -3
+    assert call(1, 0, L.FLAG_BWD_ACC_V) == -3
+    # fp32 gradients pass the dtype check and stop at the missing workspace
+    assert call(0, 0, L.FLAG_BWD_ACC_QKG | L.FLAG_BWD_ACC_V) == -5
+
+
 def test_workspace_sizes():
     lib = L.lib()
     w1 = lib.triune_hip_gla_prefill_workspace_size(4, 16384, 6, 64, 64, 0)

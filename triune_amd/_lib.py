@@ -19,6 +19,8 @@ ABI_VERSION = 2
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 FLAG_TAIL_UNCLAMPED = 0x1
 FLAG_SEG_SHIFT = 8
+FLAG_BWD_ACC_QKG = 0x2
+FLAG_BWD_ACC_V = 0x4
 BETA_NONE, BETA_HEAD, BETA_KEY, BETA_VALUE = 0, 1, 2, 3
 
 _DT = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float16: DT_F16}

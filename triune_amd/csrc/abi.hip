@@ -486,6 +486,9 @@ int triune_hip_gla_prefill_bwd(const void* q, const void* k, const void* v, cons
     if (!q || !k || !v || !g || !dout || !strides || !dq || !dk || !dv || !dg) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(d_dtype) || !dtype_ok(dg_dtype)) return TRIUNE_ERR_DTYPE;
     if (!gate_dtype_ok(io_dtype, g_dtype)) return TRIUNE_ERR_DTYPE;
+    if ((flags & TRIUNE_FLAG_BWD_ACC_QKG) && (d_dtype != TRIUNE_DT_F32 || dg_dtype != TRIUNE_DT_F32))
+        return TRIUNE_ERR_DTYPE;
+    if ((flags & TRIUNE_FLAG_BWD_ACC_V) && d_dtype != TRIUNE_DT_F32) return TRIUNE_ERR_DTYPE;
     if (B < 0 || T < 0 || H <= 0 || Dk != Dv || !gla_bwd_supported(Dk, io_dtype)) return TRIUNE_ERR_SHAPE;
     const int64_t* st = strides;  // q, k, v, g, dout, dq, dk, dv, dg: (batch, token, head) each
     auto rows_ok = [&](int i, int dt, int D) {  // as tok_strides_ok: rows at least D apart
@@ -530,13 +533,14 @@ int triune_hip_gla_prefill_bwd(const void* q, const void* k, const void* v, cons
     f.ws_state = reinterpret_cast<float*>(ws + pl.f.off_state);
     f.ws_gamma = reinterpret_cast<float*>(ws + pl.f.off_gamma);
     f.n_seqs = B; f.H = H; f.T = T; f.Dk = Dk; f.Dv = Dv;
-    f.P = pl.f.P; f.nseg_dense = (int)pl.f.nseg; f.varlen = 0; f.flags = flags & 0xff;
+    f.P = pl.f.P; f.nseg_dense = (int)pl.f.nseg; f.varlen = 0; f.flags = flags & TRIUNE_FLAG_TAIL_UNCLAMPED;
     fill_tok(a.dout, dout, st + 12, B, T, H, Dv, io_dtype);
     a.dq = dq; a.dq_sb = st[15]; a.dq_st = st[16]; a.dq_sh = st[17];
     a.dk = dk; a.dk_sb = st[18]; a.dk_st = st[19]; a.dk_sh = st[20];
     a.dv = dv; a.dv_sb = st[21]; a.dv_st = st[22]; a.dv_sh = st[23];
     a.dg = dg; a.dg_sb = st[24]; a.dg_st = st[25]; a.dg_sh = st[26];
     a.d_dt = d_dtype; a.dg_dt = dg_dtype;
+    a.acc = ((flags & TRIUNE_FLAG_BWD_ACC_QKG) ? 1 : 0) | ((flags & TRIUNE_FLAG_BWD_ACC_V) ? 2 : 0);
     a.ws_r = reinterpret_cast<float*>(ws + pl.off_r);
     a.ws_send = reinterpret_cast<float*>(ws + pl.off_send);
     a.ws_chunk = reinterpret_cast<float*>(ws + pl.off_chunk);

@@ -64,10 +64,21 @@ __device__ __forceinline__ void bwd_load(BwdIn<TIn, TG>& x, const BwdAddr& ad, i
 // Sum over the 16 lanes of each 16-lane group.
 __device__ __forceinline__ float sum16(float x) { return dpp_sum16(x); }
 
+// fp32 x added to the four floats at voff (bounded like out_store4: past the records, loads
+// read zero and stores are dropped).
+__device__ __forceinline__ void out_acc4(const OutRsrc& r, int voff, f32x4 x) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 a = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r.lo, voff, 0, 0));
+    const f32x2 b = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r.hi, voff + 8, 0, 0));
+    x[0] += a[0]; x[1] += a[1]; x[2] += b[0]; x[3] += b[1];
+    out_store4(r, voff, DT_F32, x);
+}
+
 // Four values at columns [col, col+4) of rows 4*tg + j (j < 4) of the chunk at tc: bounded
-// buffer stores over the chunk's nv rows (rows past the end are dropped).
+// buffer stores over the chunk's nv rows (rows past the end are dropped).  acc: added to the
+// (fp32) values there.
 __device__ __forceinline__ void store_rows4(const RowsOut& o, int D, int64_t tc, int nv, int tg, int col,
-                                            const float (&x)[4][4]) {
+                                            const float (&x)[4][4], bool acc = false) {
     const int es = o.es, dt = o.dt;
     const int64_t ost = o.ost;
     char* b0 = o.base + uniform_i64(tc * ost);
@@ -75,6 +86,12 @@ __device__ __forceinline__ void store_rows4(const RowsOut& o, int D, int64_t tc,
     OutRsrc r;
     r.lo = __builtin_amdgcn_make_buffer_rsrc(b0, (short)0, n, 0x00020000);
     r.hi = __builtin_amdgcn_make_buffer_rsrc(b0, (short)0, dt == DT_F32 ? n : 0, 0x00020000);
+    if (acc) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            out_acc4(r, (int32_t)((4 * tg + j) * ost) + col * es, f32x4{x[j][0], x[j][1], x[j][2], x[j][3]});
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         out_store4(r, (int32_t)((4 * tg + j) * ost) + col * es, dt, f32x4{x[j][0], x[j][1], x[j][2], x[j][3]});
@@ -83,7 +100,7 @@ __device__ __forceinline__ void store_rows4(const RowsOut& o, int D, int64_t tc,
 // Four D-layout tiles o[tb] (lane (g4, r16): token 16*tb + r16, columns 4*g4 .. 4*g4+3 of the
 // wave's 16) staged through `stage` (16 x os floats of this wave) and stored as rows.
 __device__ __forceinline__ void store_tiles(char* obase, int64_t ost, int es, int dt, int nv, const f32x4 (&o)[4],
-                                            float* stage, int os) {
+                                            float* stage, int os, bool acc = false) {
     const int lane = threadIdx.x & 63, r16 = lane & 15, g4 = lane >> 4;
     const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);
     const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
@@ -92,7 +109,8 @@ __device__ __forceinline__ void store_tiles(char* obase, int64_t ost, int es, in
     for (int tb = 0; tb < 4; ++tb) {
         *reinterpret_cast<f32x4*>(stage + r16 * os + 4 * g4) = o[tb];
         const f32x4 x = *reinterpret_cast<const f32x4*>(stage + tq * os + 4 * q);
-        out_store4(orr, (int32_t)(16 * tb * ost) + olane, dt, x);
+        if (acc) out_acc4(orr, (int32_t)(16 * tb * ost) + olane, x);
+        else out_store4(orr, (int32_t)(16 * tb * ost) + olane, dt, x);
     }
 }
 
@@ -350,7 +368,8 @@ __device__ void bwd_tokenwise(const BwdParams& a, const Work& wk, int64_t h, int
         if (g4 == 0) {
             char* p = reinterpret_cast<char*>(a.dv) +
                       (wk.b * a.dv_sb + (wk.row0 + tt) * a.dv_st + h * a.dv_sh + c0 + r16) * es;
-            store1_dt(p, a.d_dt, dvp);
+            if (a.acc & 2) *reinterpret_cast<float*>(p) += dvp;
+            else store1_dt(p, a.d_dt, dvp);
         }
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
@@ -648,7 +667,7 @@ struct BwdStep {
             }
             const RowsOut& ov = go[2];
             store_tiles(ov.base + uniform_i64(tc * ov.ost + c0 * ov.es), ov.ost, ov.es, ov.dt, nv, dV,
-                        reinterpret_cast<float*>(sPH) + wave * 16 * L::OS, L::OS);
+                        reinterpret_cast<float*>(sPH) + wave * 16 * L::OS, L::OS, (a.acc & 2) != 0);
         }
         block_sync<DMA>();
 
@@ -678,9 +697,10 @@ struct BwdStep {
                 }
 #pragma unroll
             for (int i = 0; i < DL; ++i) acc[i] += tot[i];
-            store_rows4(go[0], D, tc, nv, tg, dl0, dq);
-            store_rows4(go[1], D, tc, nv, tg, dl0, dk);
-            store_rows4(go[3], D, tc, nv, tg, dl0, X);
+            const bool acc = (a.acc & 1) != 0;
+            store_rows4(go[0], D, tc, nv, tg, dl0, dq, acc);
+            store_rows4(go[1], D, tc, nv, tg, dl0, dk, acc);
+            store_rows4(go[3], D, tc, nv, tg, dl0, X, acc);
         }
     }
 };

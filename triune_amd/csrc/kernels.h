@@ -80,6 +80,7 @@ struct BwdParams {
     int64_t dq_sb, dq_st, dq_sh, dk_sb, dk_st, dk_sh, dv_sb, dv_st, dv_sh, dg_sb, dg_st, dg_sh;
     int d_dt;              // dtype of dq, dk, dv
     int dg_dt;             // dtype of dg
+    int acc;               // bit 0: dq, dk, dg added into their (fp32) buffers; bit 1: dv likewise
     float* ws_chunk;       // [B, H, nchunks, D, D] state at the start of every chunk
     float* ws_r;           // [n_work, H, D, D] segment maps R, then the gradient reaching each segment's end
     float* ws_send;        // [n_work, H, D, D] state at each segment's end

@@ -234,10 +234,12 @@ def _needs_grad(*ts) -> bool:
     return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
 
-def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None):
+def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None, outs=None, acc=0):
     """Gradients (dq, dk, dv, dg, ds0) of _prefill for upstream do (of o) and ds (of the fp32
     final state), either of which may be None.  grad_dtype: dtype of dq, dk, dv, dg (default:
-    the inputs' own dtypes)."""
+    the inputs' own dtypes).  outs: fp32 (dq, dk, dv, dg) views of exactly the kernel width to
+    write into (or, for the parts acc names, add into: _lib.FLAG_BWD_ACC_QKG / FLAG_BWD_ACC_V);
+    they are returned in place of new tensors."""
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
     lim = 32 if q.dtype == torch.float32 else 64  # widest head the gradient kernels hold
@@ -253,9 +255,14 @@ def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None):
     if ds is not None:
         dsf = _state_in(ds, D, D)
     s0p = _state_in(s0, D, D)
-    dq = torch.empty(B, T, H, D, device=q.device, dtype=grad_dtype or q.dtype)
-    dk, dv = torch.empty_like(dq), torch.empty_like(dq)
-    dg = torch.empty(B, T, H, D, device=q.device, dtype=grad_dtype or gp.dtype)
+    if outs is not None:
+        if Dk0 != D or Dv0 != D or any(t.dtype != torch.float32 or t.shape[-1] != D for t in outs):
+            raise ValueError("outs must be fp32 views of the kernel width")
+        dq, dk, dv, dg = outs
+    else:
+        dq = torch.empty(B, T, H, D, device=q.device, dtype=grad_dtype or q.dtype)
+        dk, dv = torch.empty_like(dq), torch.empty_like(dq)
+        dg = torch.empty(B, T, H, D, device=q.device, dtype=grad_dtype or gp.dtype)
     ds0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32) if s0 is not None else None
     L = lib()
     wsb = L.triune_hip_gla_prefill_bwd_workspace_size(B, max(T, 1), H, D, D, flags)
@@ -263,10 +270,12 @@ def _prefill_bwd(q, k, v, g, s0, do, ds, flags, grad_dtype=None):
     st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), _tok3(dop), _tok3(dq), _tok3(dk), _tok3(dv), _tok3(dg))
     rc = L.triune_hip_gla_prefill_bwd(
         ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(dop), st, ptr(s0p), ptr(dsf),
-        ptr(dq), ptr(dk), ptr(dv), dtype_code(dq), ptr(dg), dtype_code(dg), ptr(ds0), B, T, H, D, D, flags, ptr(ws),
-        ws.numel(), stream_of(q),
+        ptr(dq), ptr(dk), ptr(dv), dtype_code(dq), ptr(dg), dtype_code(dg), ptr(ds0), B, T, H, D, D, flags | acc,
+        ptr(ws), ws.numel(), stream_of(q),
     )
     check(rc, "triune_hip_gla_prefill_bwd")
+    if outs is not None:
+        return dq, dk, dv, dg, ds0
     dq, dk, dv, dg = dq[..., :Dk0], dk[..., :Dk0], dv[..., :Dv0], dg[..., :Dk0].to(grad_dtype or g.dtype)
     if ds0 is not None:
         ds0 = ds0[..., :Dk0, :Dv0].to(s0.dtype)
@@ -286,20 +295,29 @@ def _prefill_bwd_blocks(q, k, v, g, s0, do, ds, flags, grad_dtype, lim):
     kbl = [(i, min(i + lim, Dk0)) for i in range(0, Dk0, lim)]
     vbl = [(j, min(j + lim, Dv0)) for j in range(0, Dv0, lim)]
     f32 = torch.float32
-    dq = torch.zeros(B, T, H, Dk0, device=q.device, dtype=f32)
-    dk, dg = torch.zeros_like(dq), torch.zeros_like(dq)
-    dv = torch.zeros(B, T, H, Dv0, device=q.device, dtype=f32)
+    # Blocks of the full kernel width write into (first block) or add into (the others) the fp32
+    # gradients in place; a narrower tail block goes through padded temporaries and adds.
+    direct = Dk0 % lim == 0 and Dv0 % lim == 0
+    alloc = torch.empty if direct else torch.zeros
+    dq = alloc(B, T, H, Dk0, device=q.device, dtype=f32)
+    dk, dg = alloc(B, T, H, Dk0, device=q.device, dtype=f32), alloc(B, T, H, Dk0, device=q.device, dtype=f32)
+    dv = alloc(B, T, H, Dv0, device=q.device, dtype=f32)
     ds0 = torch.empty(B, H, Dk0, Dv0, device=q.device, dtype=f32) if s0 is not None else None
-    for a0, a1 in kbl:
-        for b0, b1 in vbl:
-            r = _prefill_bwd(q[..., a0:a1], k[..., a0:a1], v[..., b0:b1], g[..., a0:a1],
-                             None if s0 is None else s0[..., a0:a1, b0:b1],
-                             None if do is None else do[..., b0:b1],
-                             None if ds is None else ds[..., a0:a1, b0:b1], flags, grad_dtype=f32)
-            dq[..., a0:a1] += r[0]
-            dk[..., a0:a1] += r[1]
-            dv[..., b0:b1] += r[2]
-            dg[..., a0:a1] += r[3]
+    for ai, (a0, a1) in enumerate(kbl):
+        for bi, (b0, b1) in enumerate(vbl):
+            args = (q[..., a0:a1], k[..., a0:a1], v[..., b0:b1], g[..., a0:a1],
+                    None if s0 is None else s0[..., a0:a1, b0:b1], None if do is None else do[..., b0:b1],
+                    None if ds is None else ds[..., a0:a1, b0:b1], flags)
+            if direct:
+                acc = (_lib.FLAG_BWD_ACC_QKG if bi > 0 else 0) | (_lib.FLAG_BWD_ACC_V if ai > 0 else 0)
+                r = _prefill_bwd(*args, outs=(dq[..., a0:a1], dk[..., a0:a1], dv[..., b0:b1], dg[..., a0:a1]),
+                                 acc=acc)
+            else:
+                r = _prefill_bwd(*args, grad_dtype=f32)
+                dq[..., a0:a1] += r[0]
+                dk[..., a0:a1] += r[1]
+                dv[..., b0:b1] += r[2]
+                dg[..., a0:a1] += r[3]
             if ds0 is not None:
                 ds0[..., a0:a1, b0:b1] = r[4]
     gd = grad_dtype or q.dtype
