@@ -123,6 +123,16 @@ def test_decode_and_gdn_and_scan_validation_errors():
     gst[16] = 32  # o's token stride below the row width
     assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, gst, None, _FAKE, 1, None, 1, 64, 1, 64, 64, None, 0,
               None) == -4
+    # head dim 128: 16-bit I/O only (fp32 planes exceed the LDS), square heads only
+    g128 = (ctypes.c_int64 * 18)(*([128 * 128, 128, 128] * 4 + [0, 0, 0] + [128 * 128, 128, 128]))
+    for io, want in ((1, -5), (2, -5), (0, -3)):
+        assert gc(_FAKE, _FAKE, _FAKE, _FAKE, io, io, None, 1, 0, g128, None, _FAKE, io, None, 1, 64, 1, 128, 128,
+                  None, 0, None) == want
+    assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, g128, None, _FAKE, 1, None, 1, 64, 1, 128, 64, None, 0,
+              None) == -2
+    assert lib.triune_hip_gdn_prefill_chunked_workspace_size(4, 8192, 6, 128, 128) > 0
+    assert lib.triune_hip_gdn_prefill_chunked_workspace_size(4, 8192, 6, 128, 64) == 0
+    assert lib.triune_hip_gdn_prefill_chunked_workspace_size(4, 8192, 6, 32, 32) == 0
     # scalar-decay GDN: g is [B, T, H] (any non-negative strides, element-aligned), beta none or per token
     sg = lib.triune_hip_gdn_prefill_scalar_decay
     sst = (ctypes.c_int64 * 18)(*([64 * 64, 64, 64] * 3 + [64, 1, 0] + [0, 0, 0] + [64 * 64, 64, 64]))

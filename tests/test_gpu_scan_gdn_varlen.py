@@ -177,6 +177,98 @@ def test_gdn_chunked_extreme_decay_tokenwise_chunks(dev):
     assert _err(o.cpu(), ro) <= 1e-5 and _err(s.cpu(), rs) <= 1e-5
 
 
+def _excess16(o16, ref):
+    """max over elements of |o - ref| - (1 ULP of ref in o16's dtype + 2e-3); <= 0 passes."""
+    ref = torch.as_tensor(ref).double()
+    if o16.dtype == torch.bfloat16:
+        ulp = ulp_bf16(ref).double()
+    else:  # fp16: 10 fraction bits, subnormal spacing 2^-24
+        ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(2.0**-14))) - 10)
+    return float(((o16.double() - ref).abs() - (ulp + 2e-3)).max())
+
+
+@pytest.mark.parametrize("io", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("kind", ["none", "head", "key"])
+@pytest.mark.parametrize("T", [200, 301])
+def test_gdn_chunked_d128_16bit(dev, io, kind, T):
+    """Head dim 128 with 16-bit I/O on the chunked kernels (eight waves per workgroup, four K
+    steps per key-dim product): fp32 outputs and states within 2e-3 of the fp64 oracle on the same
+    rounded inputs, 16-bit outputs within one ULP plus 2e-3 per element.  T = 200 runs the
+    unchecked-row instances with a partial last chunk, T = 301 the checked ones."""
+    q, k, v, g, beta, s0 = _gdn_case(T, 128, kind, seed=T + 3 * len(kind))
+    q, k, v, g = (x.to(io) for x in (q, k, v, g))
+    args = [x.to(dev) for x in (q, k, v, g)]
+    bd = None if beta is None else beta.to(dev)
+    fn = fast_recurrent_gated_deltanet if kind == "key" else fast_chunk_gated_deltanet
+    o32, s32 = fn(*args, beta=bd, initial_state=s0.to(dev), out_dtype=torch.float32)
+    o16, s16 = fn(*args, beta=bd, initial_state=s0.to(dev))
+    torch.cuda.synchronize()
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0, beta_kind=O.BETA_KEY)
+    e_o, e_s = _err(o32.cpu(), ro), _err(s32.cpu(), rs)
+    print(f"gdn D=128 {io} {kind} T={T}: o {e_o:.3e} S {e_s:.3e}")
+    assert o16.dtype == io and s16.dtype == torch.float32
+    assert e_o <= 2e-3 and e_s <= 2e-3
+    assert _excess16(o16.cpu(), ro) <= 0.0
+    assert _err(s16.cpu(), rs) <= 2e-3
+
+
+def test_gdn_chunked_d128_model_distributions(dev):
+    """The reference model's GDN call at its default head dim (attention.py:509-536: q, k =
+    normalize(elu(x) + 1), g = logsigmoid(x), no beta), bf16, 24 (b, h) rows over several
+    segments; chunk decay spans of about 52 +- 5 per key dim."""
+    gen = torch.Generator().manual_seed(21)
+    B, T, H, D = 2, 1500, 12, 128
+    qk = torch.nn.functional.normalize(torch.nn.functional.elu(torch.randn(B, T, 2, H, D, generator=gen)) + 1.0,
+                                       dim=-1)
+    q, k = qk[:, :, 0].bfloat16(), qk[:, :, 1].bfloat16()
+    v = torch.randn(B, T, H, D, generator=gen).bfloat16()
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, D, generator=gen)).bfloat16()
+    args = [x.to(dev) for x in (q, k, v, g)]
+    o32, s32 = fast_chunk_gated_deltanet(*args, out_dtype=torch.float32)
+    ob, sb = fast_chunk_gated_deltanet(*args)
+    torch.cuda.synchronize()
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), None, None)
+    e_o, e_s = _err(o32.cpu(), ro), _err(s32.cpu(), rs)
+    print(f"gdn D=128 model distributions: o {e_o:.3e} S {e_s:.3e}")
+    assert e_o <= 2e-3 and e_s <= 2e-3
+    assert _excess16(ob.cpu(), ro) <= 0.0
+
+
+def test_gdn_chunked_d128_extreme_decay_tokenwise_chunks(dev):
+    """D = 128: chunks whose decay span exceeds the factored range run token by token inside the
+    chunked kernels (both states of the map kernel, the output kernel), at fp32 outputs."""
+    q, k, v, g, beta, s0 = _gdn_case(256, 128, "head", seed=12)
+    g = g.clone()
+    g[:, 64:128] = -1.0 - 20.0 * torch.rand(2, 64, 2, 128, generator=torch.Generator().manual_seed(2))
+    q, k, v, g = (x.bfloat16() for x in (q, k, v, g))
+    o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),
+                                     initial_state=s0.to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0)
+    e_o, e_s = _err(o.cpu(), ro), _err(s.cpu(), rs)
+    print(f"gdn D=128 extreme decay: o {e_o:.3e} S {e_s:.3e}")
+    assert e_o <= 2e-3 and e_s <= 2e-3
+
+
+@pytest.mark.parametrize("D,io", [(64, torch.float32), (64, torch.bfloat16), (128, torch.bfloat16)])
+def test_gdn_chunked_wide_decay_span(dev, D, io):
+    """Chunk decay spans of 112-125 per key dim (just inside the factored form's 128): factors
+    reach e^+-62, non-causal products overflow and must be masked out, and the results keep the
+    fp32 bar at fp32 I/O and 2e-3 at bf16 I/O."""
+    q, k, v, g, beta, s0 = _gdn_case(300, D, "head", seed=D + 1)
+    g = -1.75 - 0.2 * torch.rand(g.shape, generator=torch.Generator().manual_seed(5))
+    q, k, v, g = (x.to(io) for x in (q, k, v, g))
+    o, s = fast_chunk_gated_deltanet(*(x.to(dev) for x in (q, k, v, g)), beta=beta.to(dev),
+                                     initial_state=s0.to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0)
+    e_o, e_s = _err(o.cpu(), ro), _err(s.cpu(), rs)
+    print(f"gdn wide span D={D} {io}: o {e_o:.3e} S {e_s:.3e}")
+    assert np.isfinite(o.cpu().numpy()).all() and np.isfinite(s.cpu().numpy()).all()
+    tol = 1e-5 if io == torch.float32 else 2e-3
+    assert e_o <= tol and e_s <= tol
+
+
 def test_gdn_single_token(dev):
     q, k, v, g, beta, s0 = _gdn_case(1, 64, "head", seed=5)
     o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),

@@ -753,13 +753,14 @@ namespace {
 
 // Chunked GDN: segments per sequence fill the resident output-kernel slots once (for I/O dtype
 // io_dt; bf16 holds the most workgroups per CU, so its plan bounds the workspace of every dtype).
+// D: head dim (Dk = Dv), 64 or 128; the workspace holds D x D fp32 states and M maps per segment.
 struct GdnPlan {
     int64_t nseg, n_work;
     size_t off_m, off_spare, total;
 };
 
-// sg: the scalar-gate kernels (gdn_scalar.hip), whose output kernel has its own occupancy.
-GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt, bool sg) {
+// sg: the scalar-gate kernels (gdn_scalar.hip, D = 64), whose output kernel has its own occupancy.
+GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt, bool sg, int D) {
     static std::mutex mu;
     static std::map<int, int64_t> slots_cache;
     int dev = 0;
@@ -768,27 +769,28 @@ GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt, bool sg) {
     const bool ck = T % 4 != 0;  // the instance the launch picks (launch_gdn_t, launch_sg_t)
     {
         std::lock_guard<std::mutex> lock(mu);
-        const int key = 16 * dev + 4 * io_dt + (sg ? 2 : 0) + (ck ? 1 : 0);
+        const int key = 32 * dev + 8 * io_dt + (D == 128 ? 4 : 0) + (sg ? 2 : 0) + (ck ? 1 : 0);
         auto it = slots_cache.find(key);
         if (it == slots_cache.end()) {
             int ncu = 0;
             if (dev < 0 || hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
                 ncu <= 0)
                 ncu = 256;
-            const int per_cu = sg ? gdn_sg_seg_out_blocks_per_cu(io_dt, ck) : gdn_seg_out_blocks_per_cu(io_dt, ck);
+            const int per_cu = sg ? gdn_sg_seg_out_blocks_per_cu(io_dt, ck) : gdn_seg_out_blocks_per_cu(io_dt, ck, D);
             it = slots_cache.emplace(key, (int64_t)ncu * per_cu).first;
         }
         slots = it->second;
     }
     GdnPlan p{};
     const int64_t nchunks = (T + 63) / 64;
+    const size_t dd = (size_t)D * D;
     p.nseg = slots / (B * H);
     if (p.nseg < 1) p.nseg = 1;
     if (p.nseg > nchunks) p.nseg = nchunks;
     p.n_work = B * p.nseg;
-    p.off_m = align_up((size_t)p.n_work * H * 64 * 64 * sizeof(float));
-    p.off_spare = p.off_m + align_up((size_t)p.n_work * H * 3 * 64 * 64 * 2);  // up to 3 bf16 parts of M
-    p.total = p.off_spare + align_up((size_t)B * H * 64 * 64 * sizeof(float));
+    p.off_m = align_up((size_t)p.n_work * H * dd * sizeof(float));
+    p.off_spare = p.off_m + align_up((size_t)p.n_work * H * 3 * dd * 2);  // up to 3 bf16 parts of M
+    p.total = p.off_spare + align_up((size_t)B * H * dd * sizeof(float));
     return p;
 }
 
@@ -797,13 +799,13 @@ GdnPlan plan_gdn(int64_t B, int64_t T, int64_t H, int io_dt, bool sg) {
 extern "C" {
 
 size_t triune_hip_gdn_prefill_chunked_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv) {
-    if (B <= 0 || T <= 0 || H <= 0 || Dk != 64 || Dv != 64) return 0;
-    return plan_gdn(B, T, H, TRIUNE_DT_BF16, false).total;
+    if (B <= 0 || T <= 0 || H <= 0 || Dk != Dv || (Dk != 64 && Dk != 128)) return 0;
+    return plan_gdn(B, T, H, TRIUNE_DT_BF16, false, Dk).total;
 }
 
 size_t triune_hip_gdn_prefill_scalar_decay_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv) {
     if (B <= 0 || T <= 0 || H <= 0 || Dk != 64 || Dv != 64) return 0;
-    return plan_gdn(B, T, H, TRIUNE_DT_BF16, true).total;
+    return plan_gdn(B, T, H, TRIUNE_DT_BF16, true, 64).total;
 }
 
 }  // extern "C"
@@ -825,7 +827,8 @@ int gdn_chunked_impl(const void* q, const void* k, const void* v, const void* g,
         (beta_kind != TRIUNE_BETA_NONE && !dtype_ok(beta_dtype)) ||
         (beta_kind == TRIUNE_BETA_KEY && beta_dtype != TRIUNE_DT_F32))
         return TRIUNE_ERR_DTYPE;
-    if (B < 0 || T < 0 || H <= 0 || Dk != 64 || Dv != 64) return TRIUNE_ERR_SHAPE;
+    if (B < 0 || T < 0 || H <= 0 || Dk != Dv || (Dk != 64 && (sg || Dk != 128))) return TRIUNE_ERR_SHAPE;
+    if (Dk == 128 && io_dtype == TRIUNE_DT_F32) return TRIUNE_ERR_DTYPE;  // fp32 planes exceed LDS at D = 128
     const bool g_ok = sg ? (reinterpret_cast<uintptr_t>(g) % (g_dtype == TRIUNE_DT_F32 ? 4 : 2) == 0 &&
                             strides[9] >= 0 && strides[10] >= 0 && strides[11] >= 0)
                          : vec_ok(g, g_dtype, strides + 9, 3);
@@ -852,7 +855,7 @@ int gdn_chunked_impl(const void* q, const void* k, const void* v, const void* g,
         sc.n_outer = B; sc.H = H; sc.Dk = Dk; sc.Dv = Dv; sc.N = 0;
         return launch_status(launch_recurrent_scan(sc, st));
     }
-    const GdnPlan pl = plan_gdn(B, T, H, io_dtype, sg);
+    const GdnPlan pl = plan_gdn(B, T, H, io_dtype, sg, Dk);
     if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
     char* ws = reinterpret_cast<char*>(workspace);
     if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;

@@ -23,15 +23,24 @@
 //   K3 gdn_seg_out  : per (segment, head) the chunk walk from S_in[p], writing o
 // Products run on v_mfma_f32_16x16x32_bf16 with operands split into bf16 parts (2 for 16-bit
 // I/O, 3 for fp32) and fp32 accumulation, as in the GLA prefill.  Chunks whose decay span
-// exceeds SPAN_MAX run token by token.
+// exceeds GDN_SPAN_MAX run token by token.
 #include "gdn_common.h"
 
 namespace triune {
 
-template <typename TIn, bool OUT>
+// Largest chunk decay span (-G_C per key dim) of the factored form.  Every factor then lies in
+// e^[-64, 64], where all bf16 parts of an operand (the third one, 2^-18 below it, included) are
+// normal numbers; only products of non-causal pairs (up to e^128) overflow, and every one of
+// those sits in a diagonal tile that a select (never a multiply) replaces with 0.  The
+// reference's bf16 GLA chunk kernel allows 160 (fast_gla.py:377).
+constexpr float GDN_SPAN_MAX = 128.f;
+
+// LDS layout of one (segment, head) workgroup at head dim D (Dk = Dv = D, one wave per 16 value
+// columns; stage 1 gives every wave 16 key dims).
+template <typename TIn, bool OUT, int D>
 struct GLay {
     using P = Prec<TIn>;
-    static constexpr int DK = 64, DV = 64, NW = 4, DPW = 16, DL = 4;
+    static constexpr int DK = D, DV = D, NW = D / 16, DPW = 16, DL = 4;
     static constexpr int RS = DK + PAD, VS = 16;
     static constexpr int ROWP = CHUNK * RS * 2;
     static constexpr int VPP = CHUNK * VS * 2;
@@ -46,27 +55,31 @@ struct GLay {
     static constexpr int OFF_TI = OFF_LT + P::NS * LTP;
     static constexpr int OFF_VP = OFF_TI + P::NS * DIAGP;
     static constexpr int OFF_FAC = OFF_VP + NW * P::NX * VPP;
-    static constexpr int OFF_FLAG = OFF_FAC + 2 * DK * 4;
-    static constexpr int BYTES = OFF_FLAG + 16 * 4;
+    static constexpr int OFF_FLAG = OFF_FAC + DK * 4;
+    static constexpr int BYTES = OFF_FLAG + NW * 4;
     static constexpr int OS = 20;
     static_assert(16 * OS * 4 <= P::NX * VPP, "output staging fits in a wave's V planes");
     static_assert(BYTES <= 160 * 1024, "LDS budget");
 };
 
-// Inputs of a GDN chunk: the GLA chunk inputs plus per-key-dim beta (BETA_KEY, fp32).
-template <typename TIn, typename TG>
+// Inputs of a GDN chunk: the GLA chunk inputs plus, when PBK, per-key-dim beta (BETA_KEY, fp32)
+// loaded a chunk ahead with them.  Without PBK (D = 128, where those 16 registers would spill)
+// stage 1 reads the beta rows of its own chunk.
+template <typename TIn, typename TG, bool PBK>
 struct GChunkIn {
     ChunkIn<TIn, TG, 4> x;
-    Vec<float, 4> bk[4];
+    Vec<float, 4> bk[PBK ? 4 : 1];
 };
 
-template <bool OUT, bool CK, typename TIn, typename TG>
-__device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG>& c, const ChunkAddr& ad, const TokAddr& kb, bool key_beta,
-                                            int64_t tc, bool valid) {
+template <bool OUT, bool CK, typename TIn, typename TG, bool PBK>
+__device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG, PBK>& c, const ChunkAddr& ad, const TokAddr& kb,
+                                            bool key_beta, int64_t tc, bool valid) {
     chunk_load<OUT, CK>(c.x, ad, tc, valid);
-    if (key_beta) {
-        const __amdgpu_buffer_rsrc_t r = chunk_rsrc(kb, tc, valid);
-        rows_load<CK>(c.bk, r, kb, tc);
+    if constexpr (PBK) {
+        if (key_beta) {
+            const __amdgpu_buffer_rsrc_t r = chunk_rsrc(kb, tc, valid);
+            rows_load<CK>(c.bk, r, kb, tc);
+        }
     }
 }
 
@@ -74,17 +87,27 @@ __device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG>& c, const ChunkAdd
 // (K1) the segment map on two states at once: S driven with V = 0 (the M columns) and SN with
 // the real V (the N columns); stages 1-2 (factors, tiles, inverses) are shared by both.
 // CK: checked row addressing; without it the loads zero rows past the chunk (see chunk_load).
-template <typename TIn, typename TG, bool OUT, bool CK>
+// D: head dim (NDB = D/16 state row tiles per wave, NKS = D/32 K steps over key dims).
+template <typename TIn, typename TG, bool OUT, bool CK, int D>
 struct GdnStep {
-    using L = GLay<TIn, OUT>;
+    using L = GLay<TIn, OUT, D>;
     using PR = Prec<TIn>;
-    static constexpr int NS = PR::NS, NX = PR::NX, DL = 4;
+    static constexpr int NS = PR::NS, NX = PR::NX, DL = 4, NW = L::NW, NDB = D / 16, NKS = D / 32;
+    // Stage 2 at D = 128: waves 0-3 form the A^T / L^T tiles, waves 4-7 the four diagonal
+    // inverses (about as much MFMA work as four tiles each); at D = 64 every wave does both.
+    static constexpr int TW = NW >= 8 ? 4 : NW, DW0 = NW >= 8 ? 4 : 0;
+    static constexpr bool PBK = D == 64;
 
     template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                               const GChunkIn<TIn, TG>& cur, f32x4 (&S)[4], f32x4 (&SN)[4], char* smem,
-                               Hook&& after_inputs) {
-        const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
+                               const GChunkIn<TIn, TG, PBK>& cur, const TokAddr& kb, f32x4 (&S)[NDB],
+                               f32x4 (&SN)[NDB], char* smem, Hook&& after_inputs) {
+        int lane = threadIdx.x & 63;
+        // At D = 128 the planes span more than the 64 KB reach of an LDS instruction's offset, so
+        // every operand read needs its own lane address; computed once per kernel they outlive
+        // the register file and spill.  An opaque lane index per chunk keeps them in the step.
+        if constexpr (D > 64) asm volatile("" : "+v"(lane));
+        const int wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int c0 = wave * 16;
         const int dl0 = wave * 16 + DL * row;
@@ -96,7 +119,6 @@ struct GdnStep {
         char* sTI = smem + L::OFF_TI;
         char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
         float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
-        float* sEG = sEM + 64;
         int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
 
         // ---------------- stage 1: factors and split operands -> LDS ------------------------
@@ -113,7 +135,7 @@ struct GdnStep {
             chunk_cumsum<DL>(G, GC, lane);
             bool bad = false;
 #pragma unroll
-            for (int i = 0; i < DL; ++i) bad |= !(GC[i] >= -SPAN_MAX);
+            for (int i = 0; i < DL; ++i) bad |= !(GC[i] >= -GDN_SPAN_MAX);
             float fq[4][DL];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -121,11 +143,7 @@ struct GdnStep {
                 for (int i = 0; i < DL; ++i) fq[j][i] = fast_exp(G[j][i] - 0.5f * GC[i]);  // exp(G - m)
             if (tg == 0) {
 #pragma unroll
-                for (int i = 0; i < DL; ++i) {
-                    const float em = fast_exp(0.5f * GC[i]);
-                    sEM[dl0 + i] = em;
-                    sEG[dl0 + i] = em * em;
-                }
+                for (int i = 0; i < DL; ++i) sEM[dl0 + i] = fast_exp(0.5f * GC[i]);
             }
             const bool any_bad = __any(bad);
             if (lane == 0) sFLAG[wave] = any_bad ? 1 : 0;
@@ -161,7 +179,13 @@ struct GdnStep {
             }
             float bkx[4][DL];
             if (a.beta_kind == BETA_KEY) {
-                chunk_float<CK>(cur.bk, bkx, tg, nv);
+                if constexpr (PBK) {
+                    chunk_float<CK>(cur.bk, bkx, tg, nv);
+                } else {
+                    Vec<float, 4> bk[4];
+                    rows_load<CK>(bk, chunk_rsrc(kb, tc, true), kb, tc);
+                    chunk_float<CK>(bk, bkx, tg, nv);
+                }
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
@@ -184,7 +208,7 @@ struct GdnStep {
         __syncthreads();
         bool fast = true;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) fast = fast && (sFLAG[w] == 0);
+        for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
         if (!fast) {
             gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
             if (!OUT) gdn_tokenwise<TIn, TG, false>(a, wk, h, c0, tc, nv, g4, r16, true, SN);
@@ -198,7 +222,7 @@ struct GdnStep {
         // of block tb.
         {
             constexpr int NT = OUT ? 16 : 6;
-            for (int n = wave; n < NT; n += 4) {
+            for (int n = wave; wave < TW && n < NT; n += TW) {
                 const bool is_a = OUT && n < 10;
                 int sb, tb, idx;
                 if (is_a) {
@@ -213,7 +237,7 @@ struct GdnStep {
                 const char* rhs = is_a ? sQT : sBT;
                 f32x4 acc = zero4();
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
+                for (int ks = 0; ks < NKS; ++ks) {
                     const Split8<NS> wf = lds_frag<NS>(sWT, L::ROWP, L::RS, 16 * sb + r16, 32 * ks, g4);
                     const Split8<NS> rf = lds_frag<NS>(rhs, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
                     acc = mfma_split<NS, NS, NS>(wf, rf, acc);
@@ -227,11 +251,11 @@ struct GdnStep {
             }
             // Diagonal block wave of the UT transform: T_ww = (I + L_ww)^-1 by doubling, kept as
             // D-layout pairs (X, X^T) so every product reads its operands from registers.
-            {
-                const int ib = wave;
+            if (wave >= DW0 && wave < DW0 + 4) {
+                const int ib = wave - DW0;
                 f32x4 Lm = zero4(), LmT = zero4();
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
+                for (int ks = 0; ks < NKS; ++ks) {
                     const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * ib + r16, 32 * ks, g4);
                     const Split8<NS> wf = lds_frag<NS>(sWT, L::ROWP, L::RS, 16 * ib + r16, 32 * ks, g4);
                     Lm = mfma_split<NS, NS, NS>(bf, wf, Lm);    // Lm[t = 4*g4+j][s = r16]
@@ -270,25 +294,25 @@ struct GdnStep {
 
         // ---------------- stage 3: residuals, UT solve, outputs, state ----------------------
         // One pass per state: K3 runs it on S with V; K1 on S with V = 0 and on SN with V.
-        auto pass = [&](auto with_v, f32x4 (&St)[4]) {
+        auto pass = [&](auto with_v, f32x4 (&St)[NDB]) {
             constexpr bool WV = decltype(with_v)::value;
-            f32x4 Sp[4];
+            f32x4 Sp[NDB];
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
+            for (int db = 0; db < NDB; ++db) {
                 const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) Sp[db][i] = St[db][i] * em[i];
             }
-            Split8<NS> sf[2];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
+            Split8<NS> sf[NKS];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) sf[ks] = split_k32<NS>(Sp[2 * ks], Sp[2 * ks + 1]);
+            for (int ks = 0; ks < NKS; ++ks) sf[ks] = split_k32<NS>(Sp[2 * ks], Sp[2 * ks + 1]);
             // R_i = V_i - Bt_i S'  (D layout: rows t = 16i + 4*g4 + k, column c0 + r16)
             f32x4 R[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 f32x4 p = zero4();
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
+                for (int ks = 0; ks < NKS; ++ks) {
                     const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4);
                     p = mfma_split<NS, NS, NS>(bf, sf[ks], p);
                 }
@@ -304,6 +328,21 @@ struct GdnStep {
                 }
 #pragma unroll
                 for (int k = 0; k < 4; ++k) R[i][k] = vv[k] - p[k];
+            }
+            // O^T from the carried state first (Qt S'), so that S' in split form is dead before
+            // the UT solve
+            f32x4 Ot[4];
+            if constexpr (OUT) {
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) {
+                    f32x4 o = zero4();
+#pragma unroll
+                    for (int ks = 0; ks < NKS; ++ks) {
+                        const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                        o = mfma_split<NS, NS, NS>(sf[ks], qf, o);
+                    }
+                    Ot[tb] = o;
+                }
             }
             // U_i = T_ii (R_i - sum_{j<i} L_ij U_j)
             f32x4 U[4];
@@ -337,15 +376,9 @@ struct GdnStep {
             for (int k2 = 0; k2 < 2; ++k2) uf[k2] = split_k32<NS>(U[2 * k2], U[2 * k2 + 1]);
 
             if constexpr (OUT) {
-                f32x4 Ot[4];
 #pragma unroll
                 for (int tb = 0; tb < 4; ++tb) {
-                    f32x4 o = zero4();
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
-                        o = mfma_split<NS, NS, NS>(sf[ks], qf, o);
-                    }
+                    f32x4 o = Ot[tb];
 #pragma unroll
                     for (int k2 = 0; k2 < 2; ++k2) {
                         if (2 * k2 > tb) continue;
@@ -375,7 +408,7 @@ struct GdnStep {
             }
             // S <- e^m (S' + Wt^T U)
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
+            for (int db = 0; db < NDB; ++db) {
                 f32x4 acc = Sp[db];
 #pragma unroll
                 for (int k2 = 0; k2 < 2; ++k2) {
@@ -398,10 +431,10 @@ struct GdnStep {
     }
 };
 
-template <typename TIn, typename TG, bool OUT, bool CK>
-__device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[4], f32x4 (&SN)[4],
-                         char* smem) {
-    using St = GdnStep<TIn, TG, OUT, CK>;
+template <typename TIn, typename TG, bool OUT, bool CK, int D>
+__device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[D / 16],
+                         f32x4 (&SN)[D / 16], char* smem) {
+    using St = GdnStep<TIn, TG, OUT, CK, D>;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<OUT, TIn, TG>(a, wk, h, tg, wave * 16 + 4 * row, wave * 16 + 4 * row);
     const bool key_beta = a.beta_kind == BETA_KEY;
@@ -413,54 +446,67 @@ __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x
         return (int)(r < CHUNK ? r : CHUNK);
     };
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
-    GChunkIn<TIn, TG> A;
+    GChunkIn<TIn, TG, St::PBK> A;
     gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(0), true);
     for (int64_t c = 0; c < nch; ++c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, S, SN, smem,
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, kb, S, SN, smem,
                 [&] { gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch); });
 }
 
-// K1: the segment map driven from [I | 0] with V = 0 (-> M_p, state M) and from 0 with the real
-// V (-> N_p, state N) in one chunk walk.
-template <typename TIn, typename TG, bool CK>
-__global__ __launch_bounds__(256, Prec<TIn>::F32 ? 1 : 2) void gdn_seg_mn_kernel(PrefillParams a) {
-    using L = GLay<TIn, false>;
+// Waves per SIMD the chunk kernels ask for: two at D = 64 where the LDS of two workgroups fits
+// (K1 at fp32 I/O keeps one for registers), two at D = 128 (one workgroup of eight waves per CU).
+template <typename TIn, bool OUT, int D>
+constexpr int gdn_min_waves() {
+    if (D == 128) return 2;
+    if (!OUT) return Prec<TIn>::F32 ? 1 : 2;
+    return 2 * GLay<TIn, true, D>::BYTES <= 160 * 1024 ? 2 : 1;
+}
+
+// K1: the segment map driven from I with V = 0 (-> M_p, state M) and from 0 with the real V
+// (-> N_p, state N) in one chunk walk.
+template <typename TIn, typename TG, bool CK, int D>
+__global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, false, D>())) void gdn_seg_mn_kernel(PrefillParams a) {
+    using L = GLay<TIn, false, D>;
+    constexpr int NDB = D / 16;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    f32x4 M[4], N[4];
+    f32x4 M[NDB], N[NDB];
     init_seg_map(M, N);
-    gdn_walk<TIn, TG, false, CK>(a, wk, h, M, N, smem);
+    gdn_walk<TIn, TG, false, CK, D>(a, wk, h, M, N, smem);
     store_seg_map<Prec<TIn>::NS>(a, w, h, M, N);
 }
 
-// K3: outputs of one segment from S_in[p] (in the N slot after the scan).  Two workgroups per CU
-// where two fit in LDS (bf16 I/O); fp16 and fp32 I/O hold larger planes and run one.
-template <typename TIn, typename TG, bool CK>
-__global__ __launch_bounds__(256, ((2 * GLay<TIn, true>::BYTES <= 160 * 1024) ? 2 : 1)) void gdn_seg_out_kernel(PrefillParams a) {
-    using L = GLay<TIn, true>;
+// K3: outputs of one segment from S_in[p] (in the N slot after the scan).  At D = 64 two
+// workgroups per CU where two fit in LDS (bf16 I/O); fp16 and fp32 I/O hold larger planes and run
+// one.  At D = 128 (16-bit I/O) one workgroup of eight waves per CU.
+template <typename TIn, typename TG, bool CK, int D>
+__global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, true, D>())) void gdn_seg_out_kernel(PrefillParams a) {
+    using L = GLay<TIn, true, D>;
+    constexpr int NDB = D / 16;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     const int64_t w = blockIdx.x, h = blockIdx.y;
     Work wk;
     if (!find_work(a, w, wk)) return;
-    f32x4 S[4];
+    f32x4 S[NDB];
     load_seg_state(a, w, h, S);
-    gdn_walk<TIn, TG, true, CK>(a, wk, h, S, S, smem);
+    gdn_walk<TIn, TG, true, CK, D>(a, wk, h, S, S, smem);
 }
 
 // K2: one workgroup per (sequence, head, 16 state columns), one wave per 16-row tile t of that
-// column strip: S_in[p] = carry (written in place of N_p), then S <- M_p S + N_p on MFMA.  Wave t
-// holds rows 16t + 4*g4 + i of the strip in D layout; each step it writes its tile, split into NS
-// bf16 parts, as one half of a B-operand fragment in LDS (K step t >> 1, slots (t & 1) * 4 + i),
-// and after one barrier every wave reads the strip's two K=32 fragments and forms its new tile
-// with 2 * NS-part products.  M_p arrives pre-split in NS bf16 planes, read straight into A-operand
-// layout (row 16t + r16, K slots 32kk + pi(g4, j)).  The M/N loads of a segment do not depend on
-// the carry: a ring of register sets keeps them two segments ahead.  Two LDS buffers alternate,
-// so a step's writes never meet the previous step's reads.
-template <int NS>
-__global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
-    __shared__ __attribute__((aligned(16))) char sbuf[2][2][NS][64 * 16];
+// column strip (D / 16 waves): S_in[p] = carry (written in place of N_p), then S <- M_p S + N_p on
+// MFMA.  Wave t holds rows 16t + 4*g4 + i of the strip in D layout; each step it writes its tile,
+// split into NS bf16 parts, as one half of a B-operand fragment in LDS (K step t >> 1, slots
+// (t & 1) * 4 + i), and after one barrier every wave reads the strip's D / 32 K=32 fragments and
+// forms its new tile with NS-part products.  M_p arrives pre-split in NS bf16 planes, read straight
+// into A-operand layout (row 16t + r16, K slots 32kk + pi(g4, j)).  The M/N loads of a segment do
+// not depend on the carry: a ring of register sets keeps them two segments ahead.  Two LDS buffers
+// alternate, so a step's writes never meet the previous step's reads.
+template <int NS, int D>
+__global__ __launch_bounds__(4 * D) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
+    constexpr int NKS = D / 32, NDB = D / 16, DD = D * D;
+    __shared__ __attribute__((aligned(16))) char sbuf[2][NKS][NS][64 * 16];
     const int64_t seq = blockIdx.z, h = blockIdx.y;
     const int strip = blockIdx.x, cb = strip * 16;
     const int lane = threadIdx.x & 63, t = wave_id(), r16 = lane & 15, g4 = lane >> 4;
@@ -474,32 +520,32 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
         np = a.nseg_dense < nch ? a.nseg_dense : nch;
         if (a.T == 0) np = 0;
     }
-    auto d_off = [&](int i) { return (16 * t + 4 * g4 + i) * 64 + cb + r16; };  // D-layout element
+    auto d_off = [&](int i) { return (16 * t + 4 * g4 + i) * D + cb + r16; };  // D-layout element
     f32x4 S;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) S[i] = a.s0 ? a.s0[(seq * a.H + h) * 4096 + d_off(i)] : 0.f;
+    for (int i = 0; i < 4; ++i) S[i] = a.s0 ? a.s0[(seq * a.H + h) * DD + d_off(i)] : 0.f;
     struct MN {
-        Split8<NS> m[2];  // [K step] of row tile t
+        Split8<NS> m[NKS];  // [K step] of row tile t
         f32x4 n;
     };
     // Every path issues the same loads and stores (past the end: the last segment's rows again,
     // and the store goes to a spare slot), so the wait counts leave the sets in flight.
-    float* spare = a.ws_spare + (seq * a.H + h) * 4096;
+    float* spare = a.ws_spare + (seq * a.H + h) * DD;
     auto fetch = [&](MN& x, int64_t p) {
         const int64_t w = p0 + (p < np ? p : np - 1);
-        const __bf16* mp = reinterpret_cast<const __bf16*>(a.ws_m) + (w * a.H + h) * (int64_t)MSLOT;
-        const float* np_ = a.ws_state + (w * a.H + h) * 4096;
+        const __bf16* mp = reinterpret_cast<const __bf16*>(a.ws_m) + (w * a.H + h) * mslot<D>();
+        const float* np_ = a.ws_state + (w * a.H + h) * DD;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int kk = 0; kk < NKS; ++kk)
 #pragma unroll
             for (int pl = 0; pl < NS; ++pl)
-                x.m[kk].p[pl] = *reinterpret_cast<const bf16x8*>(mp + ((pl * 4 + t) * 2 + kk) * 512 + 8 * lane);
-        x.n = *reinterpret_cast<const f32x4*>(np_ + dstate_off(strip, t, lane));
+                x.m[kk].p[pl] = *reinterpret_cast<const bf16x8*>(mp + ((pl * NDB + t) * NKS + kk) * 512 + 8 * lane);
+        x.n = *reinterpret_cast<const f32x4*>(np_ + dstate_off<NDB>(strip, t, lane));
     };
     auto step = [&](const MN& x, int64_t p) {
         const bool real = p < np;
-        float* dst = real ? a.ws_state + ((p0 + p) * a.H + h) * 4096 : spare;
-        *reinterpret_cast<f32x4*>(dst + dstate_off(strip, t, lane)) = S;  // S_in[p]
+        float* dst = real ? a.ws_state + ((p0 + p) * a.H + h) * DD : spare;
+        *reinterpret_cast<f32x4*>(dst + dstate_off<NDB>(strip, t, lane)) = S;  // S_in[p]
         // this tile as half (t & 1) of the strip's K-step (t >> 1) fragment
         const int buf = (int)(p & 1);
         {
@@ -513,7 +559,7 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
         __syncthreads();
         f32x4 acc = x.n;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < NKS; ++kk) {
             Split8<NS> sb;
 #pragma unroll
             for (int pl = 0; pl < NS; ++pl) sb.p[pl] = *reinterpret_cast<const bf16x8*>(&sbuf[buf][kk][pl][lane * 16]);
@@ -539,28 +585,39 @@ __global__ __launch_bounds__(256) void gdn_seg_scan_kernel(PrefillParams a, floa
     }
     if (s_final) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s_final[(seq * a.H + h) * 4096 + d_off(i)] = S[i];
+        for (int i = 0; i < 4; ++i) s_final[(seq * a.H + h) * DD + d_off(i)] = S[i];
     }
 }
 
 // ---------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------
-template <typename TIn, typename TG, bool CK>
+template <typename TIn, typename TG, bool CK, int D>
 static hipError_t launch_gdn_ck(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
     if (which == 0) {
-        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG, CK>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG, CK, D>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D), 0,
+                           stream, a);
     } else {
-        hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG, CK>), dim3((unsigned)n_work, (unsigned)a.H), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG, CK, D>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D), 0,
+                           stream, a);
     }
     return hipGetLastError();
 }
 
-// Unchecked row addressing only when T is a whole number of four-row groups.
+// Unchecked row addressing only when T is a whole number of four-row groups.  Head dim 128 takes
+// 16-bit I/O only (fp32 planes do not fit in LDS).
 template <typename TIn, typename TG>
 static hipError_t launch_gdn_t(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
-    if (a.T % 4 == 0) return launch_gdn_ck<TIn, TG, false>(a, n_work, which, stream);
-    return launch_gdn_ck<TIn, TG, true>(a, n_work, which, stream);
+    if (a.Dk == 128) {
+        if constexpr (Prec<TIn>::F32) {
+            return hipErrorInvalidValue;
+        } else {
+            if (a.T % 4 == 0) return launch_gdn_ck<TIn, TG, false, 128>(a, n_work, which, stream);
+            return launch_gdn_ck<TIn, TG, true, 128>(a, n_work, which, stream);
+        }
+    }
+    if (a.T % 4 == 0) return launch_gdn_ck<TIn, TG, false, 64>(a, n_work, which, stream);
+    return launch_gdn_ck<TIn, TG, true, 64>(a, n_work, which, stream);
 }
 
 static hipError_t launch_gdn(const PrefillParams& a, int64_t n_work, int io_dt, int which, hipStream_t stream) {
@@ -586,26 +643,40 @@ hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt,
 }
 
 hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream) {
-    const dim3 grid(4, (unsigned)a.H, (unsigned)a.n_seqs);
-    if (io_dt == DT_F32) hipLaunchKernelGGL(gdn_seg_scan_kernel<3>, grid, dim3(256), 0, stream, a, s_final);
-    else hipLaunchKernelGGL(gdn_seg_scan_kernel<2>, grid, dim3(256), 0, stream, a, s_final);
+    const int D = a.Dk;
+    const dim3 grid((unsigned)(D / 16), (unsigned)a.H, (unsigned)a.n_seqs);
+    if (D == 128) {
+        if (io_dt == DT_F32) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gdn_seg_scan_kernel<2, 128>), grid, dim3(4 * D), 0, stream, a, s_final);
+    } else if (io_dt == DT_F32) {
+        hipLaunchKernelGGL((gdn_seg_scan_kernel<3, 64>), grid, dim3(4 * D), 0, stream, a, s_final);
+    } else {
+        hipLaunchKernelGGL((gdn_seg_scan_kernel<2, 64>), grid, dim3(4 * D), 0, stream, a, s_final);
+    }
     return hipGetLastError();
 }
 
-// Resident output-kernel workgroups per CU for I/O dtype io_dt, on the instance that runs
-// (ck: checked row addressing, launched unless T % 4 == 0; the gate dtype does not change the
-// kernel's LDS or register use).
-int gdn_seg_out_blocks_per_cu(int io_dt, bool ck) {
-    const void* k =
-        io_dt == DT_F16
-            ? (ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, true>)
-                  : reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, false>))
-        : io_dt == DT_F32 ? (ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, true>)
-                                : reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, false>))
-                          : (ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, true>)
-                                : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, false>));
+// Resident output-kernel workgroups per CU for I/O dtype io_dt and head dim D, on the instance
+// that runs (ck: checked row addressing, launched unless T % 4 == 0; the gate dtype does not change
+// the kernel's LDS or register use).
+template <int D>
+static const void* gdn_out_kernel_ptr(int io_dt, bool ck) {
+    if (io_dt == DT_F16)
+        return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, true, D>)
+                  : reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, false, D>);
+    if constexpr (D == 64) {
+        if (io_dt == DT_F32)
+            return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, true, D>)
+                      : reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, false, D>);
+    }
+    return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, true, D>)
+              : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, false, D>);
+}
+
+int gdn_seg_out_blocks_per_cu(int io_dt, bool ck, int D) {
+    const void* k = D == 128 ? gdn_out_kernel_ptr<128>(io_dt, ck) : gdn_out_kernel_ptr<64>(io_dt, ck);
     int nb = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, 0);
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 4 * D, 0);
     return (e == hipSuccess && nb > 0) ? nb : 1;
 }
 

@@ -8,15 +8,18 @@
 
 namespace triune {
 
-// Workspace layouts shared by the three segment kernels, both chosen so that every lane moves
-// whole 16-byte vectors:
+// Workspace layouts shared by the three segment kernels (head dim D = 16 * NDB, NDB row tiles of
+// 16 and NDB / 2 K steps of 32), both chosen so that every lane moves whole 16-byte vectors:
 //  - M_p: up to 3 bf16 parts, each stored as the scan's A-operand fragments: element j of lane L
-//    for row tile t and K step kk at ((part*4 + t)*2 + kk)*512 + 8L + j;
+//    for row tile t and K step kk at ((part*NDB + t)*(NDB/2) + kk)*512 + 8L + j;
 //  - N_p / S_in[p]: fp32 in MFMA D layout, element i of lane L for column strip c (16 columns)
-//    and row tile t at ((c*4 + t)*64 + L)*4 + i.
-constexpr int64_t MSLOT = 3 * 64 * 64;
+//    and row tile t at ((c*NDB + t)*64 + L)*4 + i.
+template <int D>
+constexpr int64_t mslot() { return 3 * D * D; }
+constexpr int64_t MSLOT = mslot<64>();
 
-__device__ __forceinline__ int64_t dstate_off(int strip, int t, int lane) { return ((strip * 4 + t) * 64 + lane) * 4; }
+template <int NDB = 4>
+__device__ __forceinline__ int64_t dstate_off(int strip, int t, int lane) { return ((strip * NDB + t) * 64 + lane) * 4; }
 
 // Tile fragment from a tile plane set: lane values at (tile, lane) in K slots 0..3 (K=16), or two
 // tiles in slots 0..3 / 4..7 (K=32).
@@ -50,43 +53,40 @@ __device__ __forceinline__ float beta_value(const PrefillParams& a, const Work& 
 }
 
 // Token-by-token GDN update of one wave's 16 state columns (decay spans beyond SPAN_MAX).
-// S tile db holds S[16*db + 4*g4 + i][c0 + r16]; with_v false reads V as zero.
-template <typename TIn, typename TG, bool OUT>
+// S tile db holds S[16*db + 4*g4 + i][c0 + r16] (NDB tiles: key dim 16 * NDB); with_v false reads
+// V as zero.
+template <typename TIn, typename TG, bool OUT, int NDB>
 __device__ void gdn_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int c0, int64_t tc, int nv, int g4,
-                              int r16, bool with_v, f32x4 (&S)[4]) {
+                              int r16, bool with_v, f32x4 (&S)[NDB]) {
     for (int t = 0; t < nv; ++t) {
         const int64_t tt = tc + t;
-        float dcy[4][4], kk[4][4], ww[4][4], qq[4][4];
         const float bh = a.beta_kind == BETA_HEAD ? beta_value(a, wk, h, tt) : 1.f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const int d = 16 * db + 4 * g4;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                dcy[db][i] = expf(fminf((float)tok_row<TG>(a.g, wk, tt, h, d)[i], 0.f));
-                kk[db][i] = (float)tok_row<TIn>(a.k, wk, tt, h, d)[i];
-                const float bk = a.beta_kind == BETA_KEY ? tok_row<float>(a.kb, wk, tt, h, d)[i] : bh;
-                ww[db][i] = bk * kk[db][i];
-                qq[db][i] = OUT ? (float)tok_row<TIn>(a.q, wk, tt, h, d)[i] : 0.f;
-            }
-        }
+        // k . S first, then the update one 16-row tile at a time (k read again), so that no
+        // per-tile factor array stays live across the whole state (32 rows per lane at D = 128).
         float pred = 0.f;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < NDB; ++db) {
+            const int d = 16 * db + 4 * g4;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) pred += kk[db][i] * S[db][i];
+            for (int i = 0; i < 4; ++i) pred += (float)tok_row<TIn>(a.k, wk, tt, h, d)[i] * S[db][i];
+        }
         pred += __shfl_xor(pred, 16);
         pred += __shfl_xor(pred, 32);
         const float u = (with_v ? (float)tok_row<TIn>(a.v, wk, tt, h, c0)[r16] : 0.f) - pred;
         float part = 0.f;
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < NDB; ++db) {
+            const int d = 16 * db + 4 * g4;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float s = dcy[db][i] * S[db][i] + ww[db][i] * u;
+                const float dcy = expf(fminf((float)tok_row<TG>(a.g, wk, tt, h, d)[i], 0.f));
+                const float kk = (float)tok_row<TIn>(a.k, wk, tt, h, d)[i];
+                const float bk = a.beta_kind == BETA_KEY ? tok_row<float>(a.kb, wk, tt, h, d)[i] : bh;
+                const float s = dcy * S[db][i] + bk * kk * u;
                 S[db][i] = s;
-                part += qq[db][i] * s;
+                if (OUT) part += (float)tok_row<TIn>(a.q, wk, tt, h, d)[i] * s;
             }
+        }
         if (OUT) {
             part += __shfl_xor(part, 16);
             part += __shfl_xor(part, 32);
@@ -101,18 +101,20 @@ __device__ void gdn_tokenwise(const PrefillParams& a, const Work& wk, int64_t h,
     }
 }
 
-// K1 epilogue: the segment map of one (segment w, head h).  M goes out split into NS bf16 parts
-// (the scan's MFMA operands): NS planes of [64][64] row-major per (segment, head), slot stride
-// MSLOT elements; M[16db + 4g4 + i][16*wave + r16] is element j = 4(wave&1) + (r16&3) of scan lane
-// 16(r16>>2) + 4g4 + i for row tile db and K step wave>>1.  N goes out in the D layout of the scan.
-template <int NS>
-__device__ __forceinline__ void store_seg_map(const PrefillParams& a, int64_t w, int64_t h, const f32x4 (&M)[4],
-                                              const f32x4 (&N)[4]) {
+// K1 epilogue: the segment map of one (segment w, head h), D = 16 * NDB.  M goes out split into
+// NS bf16 parts (the scan's MFMA operands): NS planes of [D][D] per (segment, head), slot stride
+// mslot<D>() elements; M[16db + 4g4 + i][16*wave + r16] is element j = 4(wave&1) + (r16&3) of scan
+// lane 16(r16>>2) + 4g4 + i for row tile db and K step wave>>1.  N goes out in the D layout of the
+// scan.
+template <int NS, int NDB>
+__device__ __forceinline__ void store_seg_map(const PrefillParams& a, int64_t w, int64_t h, const f32x4 (&M)[NDB],
+                                              const f32x4 (&N)[NDB]) {
+    constexpr int D = 16 * NDB, NKS = NDB / 2;
     const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
-    __bf16* dm = reinterpret_cast<__bf16*>(a.ws_m) + (w * a.H + h) * (int64_t)MSLOT;
-    float* dn = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
+    __bf16* dm = reinterpret_cast<__bf16*>(a.ws_m) + (w * a.H + h) * mslot<D>();
+    float* dn = a.ws_state + (w * a.H + h) * (int64_t)D * D;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < NDB; ++db) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float m = M[db][i];
@@ -120,27 +122,30 @@ __device__ __forceinline__ void store_seg_map(const PrefillParams& a, int64_t w,
 #pragma unroll
             for (int pl = 0; pl < NS; ++pl) {
                 const __bf16 hi = (__bf16)m;
-                dm[((pl * 4 + db) * 2 + (wave >> 1)) * 512 + 8 * sl + j] = hi;
+                dm[((pl * NDB + db) * NKS + (wave >> 1)) * 512 + 8 * sl + j] = hi;
                 m -= (float)hi;
             }
         }
-        *reinterpret_cast<f32x4*>(dn + dstate_off(wave, db, lane)) = N[db];
+        *reinterpret_cast<f32x4*>(dn + dstate_off<NDB>(wave, db, lane)) = N[db];
     }
 }
 
 // K2 and K3 read the carried-in state S_in[p] of (segment w, head h) from the N slot.
-__device__ __forceinline__ void load_seg_state(const PrefillParams& a, int64_t w, int64_t h, f32x4 (&S)[4]) {
+template <int NDB>
+__device__ __forceinline__ void load_seg_state(const PrefillParams& a, int64_t w, int64_t h, f32x4 (&S)[NDB]) {
+    constexpr int D = 16 * NDB;
     const int lane = threadIdx.x & 63, wave = wave_id();
-    const float* st = a.ws_state + (w * a.H + h) * (int64_t)64 * 64;
+    const float* st = a.ws_state + (w * a.H + h) * (int64_t)D * D;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) S[db] = *reinterpret_cast<const f32x4*>(st + dstate_off(wave, db, lane));
+    for (int db = 0; db < NDB; ++db) S[db] = *reinterpret_cast<const f32x4*>(st + dstate_off<NDB>(wave, db, lane));
 }
 
-// The segment map's starting states: M = [I | 0] restricted to this wave's 16 columns, N = 0.
-__device__ __forceinline__ void init_seg_map(f32x4 (&M)[4], f32x4 (&N)[4]) {
+// The segment map's starting states: M = I restricted to this wave's 16 columns, N = 0.
+template <int NDB>
+__device__ __forceinline__ void init_seg_map(f32x4 (&M)[NDB], f32x4 (&N)[NDB]) {
     const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             M[db][i] = (16 * db + 4 * g4 + i == 16 * wave + r16) ? 1.f : 0.f;

@@ -179,7 +179,7 @@ hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int3
 hipError_t launch_gdn_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream);
 hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
-int gdn_seg_out_blocks_per_cu(int io_dt, bool ck);
+int gdn_seg_out_blocks_per_cu(int io_dt, bool ck, int D);
 // Scalar-gate chunked GDN (gdn_scalar.hip): g holds one log-decay per (token, head); same
 // workspace layout and segment scan as the per-key-dim kernels.
 hipError_t launch_gdn_sg_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
