@@ -322,6 +322,36 @@ def bench_gdn(dev, reps=20):
                              "frac": round(alg_dim / (ms_dim * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
+def bench_gdn128(dev, reps=10):
+    """Gated DeltaNet prefill as the reference model calls it at its default head dim
+    (triune/model/attention.py:509-536, config.py GLA_HEAD_DIM = 128): q, k = normalize(elu(x) + 1),
+    g = logsigmoid(x) per key dim, no beta, zero initial state; B=4, T=8192, H=12 (d_model 1536),
+    bf16 (the per-key-dim chunked kernels at D = 128)."""
+    from triune_amd import fast_chunk_gated_deltanet
+
+    B, T, H, D = 4, 8192, 12, 128
+    gen = torch.Generator(device=dev).manual_seed(3)
+    qk = torch.randn(B, T, 2, H, D, device=dev, generator=gen)
+    qk = torch.nn.functional.normalize(torch.nn.functional.elu(qk) + 1.0, dim=-1).bfloat16()
+    q, k = qk[:, :, 0], qk[:, :, 1]
+    v = torch.randn(B, T, H, D, device=dev, generator=gen).bfloat16()
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, D, device=dev, generator=gen)).bfloat16()
+    fn = lambda: fast_chunk_gated_deltanet(q, k, v, g)  # noqa: E731
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    # q, k, v, g read and o written (bf16), the fp32 final state written
+    alg = B * T * H * 5 * D * 2 + B * H * D * D * 4
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "Gated DeltaNet prefill, model call at head dim 128 (B=4, H=12, T=8192, D=128, bf16, "
+                        "per-key-dim logsigmoid gate, no beta)",
+            "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "kernels": "gdn_seg_mn + gdn_seg_scan + gdn_seg_out (D=128)",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def bench_varlen(dev, reps=5):
     """Packed ragged GLA prefill, config 4 (32 sequences of 128..8192 tokens, H=12, D=128, bf16)."""
     from triune_amd import fast_chunk_gla_varlen
@@ -515,7 +545,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
+        choices=("decode", "gdn", "gdn128", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -543,7 +573,7 @@ def main():
         elif args.only == "fused_decode":
             res = bench_fused_decode(args.decode_steps, dev)
         else:
-            res = {"gdn": bench_gdn, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
+            res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
                    "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
@@ -552,7 +582,7 @@ def main():
     # headline itself still does exactly `warmup` untimed passes before its `steps` timed ones.
     cpu = None if args.no_cpu else cpu_baseline()
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
-    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
+    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "bwd128": bench_bwd128(dev),

@@ -86,6 +86,8 @@ __device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG, PBK>& c, const Chu
 // One chunk of the GDN walk for (segment, head).  OUT: outputs from the state S (K3).  Otherwise
 // (K1) the segment map on two states at once: S driven with V = 0 (the M columns) and SN with
 // the real V (the N columns); stages 1-2 (factors, tiles, inverses) are shared by both.
+// skip_m (K1): S is left as it is (the map of a segment whose carried-in state is zero is
+// never used).
 // CK: checked row addressing; without it the loads zero rows past the chunk (see chunk_load).
 // D: head dim (NDB = D/16 state row tiles per wave, NKS = D/32 K steps over key dims).
 template <typename TIn, typename TG, bool OUT, bool CK, int D>
@@ -101,7 +103,7 @@ struct GdnStep {
     template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
                                const GChunkIn<TIn, TG, PBK>& cur, const TokAddr& kb, f32x4 (&S)[NDB],
-                               f32x4 (&SN)[NDB], char* smem, Hook&& after_inputs) {
+                               f32x4 (&SN)[NDB], bool skip_m, char* smem, Hook&& after_inputs) {
         int lane = threadIdx.x & 63;
         // At D = 128 the planes span more than the 64 KB reach of an LDS instruction's offset, so
         // every operand read needs its own lane address; computed once per kernel they outlive
@@ -210,7 +212,7 @@ struct GdnStep {
 #pragma unroll
         for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
         if (!fast) {
-            gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
+            if (!skip_m) gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
             if (!OUT) gdn_tokenwise<TIn, TG, false>(a, wk, h, c0, tc, nv, g4, r16, true, SN);
             __syncthreads();
             return;
@@ -423,7 +425,7 @@ struct GdnStep {
         if constexpr (OUT) {
             pass(std::true_type{}, S);
         } else {
-            pass(std::false_type{}, S);
+            if (!skip_m) pass(std::false_type{}, S);
             __builtin_amdgcn_sched_barrier(0);  // one pass at a time: their temporaries never overlap
             pass(std::true_type{}, SN);
         }
@@ -433,7 +435,7 @@ struct GdnStep {
 
 template <typename TIn, typename TG, bool OUT, bool CK, int D>
 __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[D / 16],
-                         f32x4 (&SN)[D / 16], char* smem) {
+                         f32x4 (&SN)[D / 16], bool skip_m, char* smem) {
     using St = GdnStep<TIn, TG, OUT, CK, D>;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<OUT, TIn, TG>(a, wk, h, tg, wave * 16 + 4 * row, wave * 16 + 4 * row);
@@ -449,7 +451,7 @@ __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x
     GChunkIn<TIn, TG, St::PBK> A;
     gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(0), true);
     for (int64_t c = 0; c < nch; ++c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, kb, S, SN, smem,
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, kb, S, SN, skip_m, smem,
                 [&] { gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch); });
 }
 
@@ -463,7 +465,8 @@ constexpr int gdn_min_waves() {
 }
 
 // K1: the segment map driven from I with V = 0 (-> M_p, state M) and from 0 with the real V
-// (-> N_p, state N) in one chunk walk.
+// (-> N_p, state N) in one chunk walk.  A sequence's first segment without an initial state
+// carries in S_in = 0, so its M is left at I (the scan's product with 0 stays 0) and only N runs.
 template <typename TIn, typename TG, bool CK, int D>
 __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, false, D>())) void gdn_seg_mn_kernel(PrefillParams a) {
     using L = GLay<TIn, false, D>;
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, false, D>())) void gdn_s
     if (!find_work(a, w, wk)) return;
     f32x4 M[NDB], N[NDB];
     init_seg_map(M, N);
-    gdn_walk<TIn, TG, false, CK, D>(a, wk, h, M, N, smem);
+    gdn_walk<TIn, TG, false, CK, D>(a, wk, h, M, N, wk.p == 0 && a.s0 == nullptr, smem);
     store_seg_map<Prec<TIn>::NS>(a, w, h, M, N);
 }
 
@@ -491,7 +494,7 @@ __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, true, D>())) void gdn_se
     if (!find_work(a, w, wk)) return;
     f32x4 S[NDB];
     load_seg_state(a, w, h, S);
-    gdn_walk<TIn, TG, true, CK, D>(a, wk, h, S, S, smem);
+    gdn_walk<TIn, TG, true, CK, D>(a, wk, h, S, S, false, smem);
 }
 
 // K2: one workgroup per (sequence, head, 16 state columns), one wave per 16-row tile t of that
