@@ -99,6 +99,11 @@ struct GdnStep {
     // inverses (about as much MFMA work as four tiles each); at D = 64 every wave does both.
     static constexpr int TW = NW >= 8 ? 4 : NW, DW0 = NW >= 8 ? 4 : 0;
     static constexpr bool PBK = D == 64;
+    // K1 at D = 128 holds two 128-row states: the next chunk's input registers are issued between
+    // its two passes (live through one of them) rather than after stage 1, where they spilled.
+    static constexpr bool LATE_LOAD = !OUT && D > 64;
+    // K3 at D = 128: issued after the chunk's output stores, before its state update.
+    static constexpr bool LATE_LOAD_OUT = OUT && D > 64;
 
     template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
@@ -206,7 +211,7 @@ struct GdnStep {
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
-        after_inputs();
+        if constexpr (!LATE_LOAD && !LATE_LOAD_OUT) after_inputs();
         __syncthreads();
         bool fast = true;
 #pragma unroll
@@ -214,6 +219,7 @@ struct GdnStep {
         if (!fast) {
             if (!skip_m) gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
             if (!OUT) gdn_tokenwise<TIn, TG, false>(a, wk, h, c0, tc, nv, g4, r16, true, SN);
+            if constexpr (LATE_LOAD || LATE_LOAD_OUT) after_inputs();
             __syncthreads();
             return;
         }
@@ -408,6 +414,7 @@ struct GdnStep {
                     out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, xo);
                 }
             }
+            if constexpr (LATE_LOAD_OUT) after_inputs();
             // S <- e^m (S' + Wt^T U)
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
@@ -426,6 +433,7 @@ struct GdnStep {
             pass(std::true_type{}, S);
         } else {
             if (!skip_m) pass(std::false_type{}, S);
+            if constexpr (LATE_LOAD) after_inputs();
             __builtin_amdgcn_sched_barrier(0);  // one pass at a time: their temporaries never overlap
             pass(std::true_type{}, SN);
         }
