@@ -274,8 +274,8 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
  * triune_hip_gdn_prefill_chunked_workspace_size(B, T, H, Dk, Dv) bytes (16-byte aligned; 0 =
  * unsupported sizes).  Supported: (Dk, Dv) == (64, 64) with any io_dtype, and (128, 128) with
  * bf16 or fp16 I/O (fp32 I/O at 128 returns TRIUNE_ERR_DTYPE: use triune_hip_gdn_prefill);
- * beta_kind NONE, HEAD (any dtype) or KEY (fp32, [B, T, H, Dk] with the strides given for beta);
- * TRIUNE_BETA_VALUE returns TRIUNE_ERR_SHAPE (use triune_hip_gdn_prefill).
+ * beta_kind NONE, HEAD (any dtype), KEY or VALUE (fp32, [B, T, H, Dk] resp. [B, T, H, Dv] with the
+ * strides given for beta).
  * Replaces: fast_chunk_gated_deltanet (fast_gla.py:839-904) for T > 1. */
 size_t triune_hip_gdn_prefill_chunked_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv);
 int triune_hip_gdn_prefill_chunked(const void* q, const void* k, const void* v, const void* g, int io_dtype,

@@ -130,6 +130,15 @@ def test_decode_and_gdn_and_scan_validation_errors():
                   None, 0, None) == want
     assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 0, g128, None, _FAKE, 1, None, 1, 64, 1, 128, 64, None, 0,
               None) == -2
+    # beta per value dim: fp32 only
+    vst = (ctypes.c_int64 * 18)(*([64 * 64, 64, 64] * 5 + [64 * 64, 64, 64]))
+    assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _FAKE, 0, 3, vst, None, _FAKE, 1, None, 1, 64, 1, 64, 64, None, 0,
+              None) == -5
+    assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _FAKE, 1, 3, vst, None, _FAKE, 1, None, 1, 64, 1, 64, 64, None, 0,
+              None) == -3
+    vst[13] = 32  # beta rows narrower than Dv
+    assert gc(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, _FAKE, 0, 3, vst, None, _FAKE, 1, None, 1, 64, 1, 64, 64, None, 0,
+              None) == -4
     assert lib.triune_hip_gdn_prefill_chunked_workspace_size(4, 8192, 6, 128, 128) > 0
     assert lib.triune_hip_gdn_prefill_chunked_workspace_size(4, 8192, 6, 128, 64) == 0
     assert lib.triune_hip_gdn_prefill_chunked_workspace_size(4, 8192, 6, 32, 32) == 0

@@ -150,30 +150,35 @@ def test_gdn_config3_distributions_bf16(dev, T, B, H, with_init):
     assert _err(sb.cpu(), rs) <= 2e-3
 
 
-@pytest.mark.parametrize("kind", ["head", "key"])
-@pytest.mark.parametrize("T", [200, 1000])
+@pytest.mark.parametrize("kind", ["head", "key", "value"])
+@pytest.mark.parametrize("T", [200, 1000, 301])
 def test_gdn_chunked_fp32_partial_last_chunk(dev, kind, T):
-    """fp32 I/O through the chunked kernels with T % 4 == 0 and a partial last chunk (the
-    unchecked-row instances), per-head and per-key beta, at the fp32 bar."""
+    """fp32 I/O through the chunked kernels with a partial last chunk (T % 4 == 0: the
+    unchecked-row instances; T = 301: the checked ones), beta per head, per key dim and per value
+    dim (the column solves), at the fp32 bar."""
     q, k, v, g, beta, s0 = _gdn_case(T, 64, kind, seed=T + len(kind))
     args = [x.to(dev) for x in (q, k, v, g)]
     fn = fast_recurrent_gated_deltanet if kind == "key" else fast_chunk_gated_deltanet
     o, s = fn(*args, beta=beta.to(dev), initial_state=s0.to(dev))
     torch.cuda.synchronize()
-    ro, rs = O.gdn_fwd(q, k, v, g, beta, s0, beta_kind=O.BETA_KEY)
-    assert _err(o.cpu(), ro) <= 1e-5 and _err(s.cpu(), rs) <= 1e-5
+    ro, rs = O.gdn_fwd(q, k, v, g, beta, s0, beta_kind=O.BETA_VALUE if kind == "value" else O.BETA_KEY)
+    e_o, e_s = _err(o.cpu(), ro), _err(s.cpu(), rs)
+    print(f"gdn fp32 {kind} T={T}: o {e_o:.3e} S {e_s:.3e}")
+    assert e_o <= 1e-5 and e_s <= 1e-5
 
 
-def test_gdn_chunked_extreme_decay_tokenwise_chunks(dev):
-    """Chunks whose decay span exceeds the factored range run token by token in the chunked path."""
-    q, k, v, g, beta, s0 = _gdn_case(256, 64, "head", seed=11)
+@pytest.mark.parametrize("kind", ["head", "value"])
+def test_gdn_chunked_extreme_decay_tokenwise_chunks(dev, kind):
+    """Chunks whose decay span exceeds the factored range run token by token in the chunked path
+    (beta per head, and per value dim)."""
+    q, k, v, g, beta, s0 = _gdn_case(256, 64, kind, seed=11)
     g = g.clone()
     g[:, 64:128] = -1.0 - 20.0 * torch.rand(2, 64, 2, 64, generator=torch.Generator().manual_seed(2))
     o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),
                                      initial_state=s0.to(dev))
     torch.cuda.synchronize()
-    ro, rs = O.gdn_fwd(q, k, v, g, beta, s0)
-    print(f"gdn extreme decay: o {_err(o.cpu(), ro):.3e} S {_err(s.cpu(), rs):.3e}")
+    ro, rs = O.gdn_fwd(q, k, v, g, beta, s0, beta_kind=O.BETA_VALUE)
+    print(f"gdn extreme decay {kind}: o {_err(o.cpu(), ro):.3e} S {_err(s.cpu(), rs):.3e}")
     assert _err(o.cpu(), ro) <= 1e-5 and _err(s.cpu(), rs) <= 1e-5
 
 
@@ -188,7 +193,7 @@ def _excess16(o16, ref):
 
 
 @pytest.mark.parametrize("io", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("kind", ["none", "head", "key"])
+@pytest.mark.parametrize("kind", ["none", "head", "key", "value"])
 @pytest.mark.parametrize("T", [200, 301])
 def test_gdn_chunked_d128_16bit(dev, io, kind, T):
     """Head dim 128 with 16-bit I/O on the chunked kernels (eight waves per workgroup, four K
@@ -203,7 +208,8 @@ def test_gdn_chunked_d128_16bit(dev, io, kind, T):
     o32, s32 = fn(*args, beta=bd, initial_state=s0.to(dev), out_dtype=torch.float32)
     o16, s16 = fn(*args, beta=bd, initial_state=s0.to(dev))
     torch.cuda.synchronize()
-    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0, beta_kind=O.BETA_KEY)
+    bk = O.BETA_VALUE if kind == "value" else O.BETA_KEY
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0, beta_kind=bk)
     e_o, e_s = _err(o32.cpu(), ro), _err(s32.cpu(), rs)
     print(f"gdn D=128 {io} {kind} T={T}: o {e_o:.3e} S {e_s:.3e}")
     assert o16.dtype == io and s16.dtype == torch.float32
@@ -234,19 +240,21 @@ def test_gdn_chunked_d128_model_distributions(dev):
     assert _excess16(ob.cpu(), ro) <= 0.0
 
 
-def test_gdn_chunked_d128_extreme_decay_tokenwise_chunks(dev):
+@pytest.mark.parametrize("kind", ["head", "value"])
+def test_gdn_chunked_d128_extreme_decay_tokenwise_chunks(dev, kind):
     """D = 128: chunks whose decay span exceeds the factored range run token by token inside the
-    chunked kernels (both states of the map kernel, the output kernel), at fp32 outputs."""
-    q, k, v, g, beta, s0 = _gdn_case(256, 128, "head", seed=12)
+    chunked kernels (both states of the map kernel, the output kernel), at fp32 outputs; beta per
+    head, and per value dim (the column-solve instances' token-by-token update)."""
+    q, k, v, g, beta, s0 = _gdn_case(256, 128, kind, seed=12)
     g = g.clone()
     g[:, 64:128] = -1.0 - 20.0 * torch.rand(2, 64, 2, 128, generator=torch.Generator().manual_seed(2))
     q, k, v, g = (x.bfloat16() for x in (q, k, v, g))
     o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),
                                      initial_state=s0.to(dev), out_dtype=torch.float32)
     torch.cuda.synchronize()
-    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0)
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0, beta_kind=O.BETA_VALUE)
     e_o, e_s = _err(o.cpu(), ro), _err(s.cpu(), rs)
-    print(f"gdn D=128 extreme decay: o {e_o:.3e} S {e_s:.3e}")
+    print(f"gdn D=128 extreme decay {kind}: o {e_o:.3e} S {e_s:.3e}")
     assert e_o <= 2e-3 and e_s <= 2e-3
 
 

@@ -820,12 +820,13 @@ int gdn_chunked_impl(const void* q, const void* k, const void* v, const void* g,
                      int o_dtype, float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv, void* workspace,
                      size_t workspace_bytes, void* stream, bool sg) {
     if (!q || !k || !v || !g || !o || !strides) return TRIUNE_ERR_NULL;
-    if (beta_kind != TRIUNE_BETA_NONE && beta_kind != TRIUNE_BETA_HEAD && (sg || beta_kind != TRIUNE_BETA_KEY))
-        return TRIUNE_ERR_SHAPE;
+    // beta per key dim or per value dim: fp32 rows of Dk (= Dv) values, read by the per-dim kernels
+    const bool vec_beta = beta_kind == TRIUNE_BETA_KEY || beta_kind == TRIUNE_BETA_VALUE;
+    if (beta_kind != TRIUNE_BETA_NONE && beta_kind != TRIUNE_BETA_HEAD && (sg || !vec_beta)) return TRIUNE_ERR_SHAPE;
     if (beta_kind != TRIUNE_BETA_NONE && !beta) return TRIUNE_ERR_NULL;
     if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype) || !gate_dtype_ok(io_dtype, g_dtype) ||
         (beta_kind != TRIUNE_BETA_NONE && !dtype_ok(beta_dtype)) ||
-        (beta_kind == TRIUNE_BETA_KEY && beta_dtype != TRIUNE_DT_F32))
+        (vec_beta && beta_dtype != TRIUNE_DT_F32))
         return TRIUNE_ERR_DTYPE;
     if (B < 0 || T < 0 || H <= 0 || Dk != Dv || (Dk != 64 && (sg || Dk != 128))) return TRIUNE_ERR_SHAPE;
     if (Dk == 128 && io_dtype == TRIUNE_DT_F32) return TRIUNE_ERR_DTYPE;  // fp32 planes exceed LDS at D = 128
@@ -835,7 +836,7 @@ int gdn_chunked_impl(const void* q, const void* k, const void* v, const void* g,
     if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
         !vec_ok(v, io_dtype, strides + 6, 3) || !g_ok || !vec_ok(o, o_dtype, strides + 15, 3) ||
         reinterpret_cast<uintptr_t>(s0) % 16 || reinterpret_cast<uintptr_t>(s_final) % 16 ||
-        (beta_kind == TRIUNE_BETA_KEY &&
+        (vec_beta &&
          (!vec_ok(beta, TRIUNE_DT_F32, strides + 12, 3) || strides[13] < Dk || (64 * strides[13] + Dk) * 4 >= ((int64_t)1 << 31))))
         return TRIUNE_ERR_LAYOUT;
     // o strides sit at 15..17 here (beta takes 12..14); tok_strides_ok reads o's token stride at 13.
@@ -875,8 +876,16 @@ int gdn_chunked_impl(const void* q, const void* k, const void* v, const void* g,
     a.P = 0; a.nseg_dense = (int)pl.nseg; a.varlen = 0; a.flags = 0;
     a.beta = beta; a.beta_dt = beta_dtype; a.beta_kind = beta_kind;
     a.b_sb = strides[12]; a.b_st = strides[13]; a.b_sh = strides[14];
-    if (beta_kind == TRIUNE_BETA_KEY) fill_tok(a.kb, beta, strides + 12, B, T, H, Dk, TRIUNE_DT_F32);
+    if (vec_beta) fill_tok(a.kb, beta, strides + 12, B, T, H, Dk, TRIUNE_DT_F32);
 
+    if (beta_kind == TRIUNE_BETA_VALUE) {
+        // beta per value column: every column has its own segment map, so each sequence is one
+        // segment, walked by the output kernel alone (it writes the final state)
+        a.nseg_dense = 1;
+        a.gdn_whole = 1;
+        a.seq_final = s_final;
+        return launch_status(launch_gdn_seg_out(a, B, io_dtype, st));
+    }
     hipError_t e = sg ? launch_gdn_sg_seg_mn(a, pl.n_work, io_dtype, st) : launch_gdn_seg_mn(a, pl.n_work, io_dtype, st);
     if (e != hipSuccess) return TRIUNE_ERR_LAUNCH;
     e = launch_gdn_seg_scan(a, s_final, io_dtype, st);

@@ -89,8 +89,49 @@ __device__ __forceinline__ void gchunk_load(GChunkIn<TIn, TG, PBK>& c, const Chu
 // skip_m (K1): S is left as it is (the map of a segment whose carried-in state is zero is
 // never used).
 // CK: checked row addressing; without it the loads zero rows past the chunk (see chunk_load).
-// D: head dim (NDB = D/16 state row tiles per wave, NKS = D/32 K steps over key dims).
-template <typename TIn, typename TG, bool OUT, bool CK, int D>
+// Per-value-column beta (BV): with y_t = beta_t (.) u_t the recurrence is S_t = D_t S + k_t y_t^T,
+// so the factors are the beta-free ones (W0 = k e^{m-G}, L0 = strictly_lower(Bt W0^T),
+// A0 = lower(Qt W0^T)) and, column by column,
+//   y_t = beta_t (R_t - sum_{s<t} L0[t,s] y_s),   O = Qt S' + A0 Y,   S_C = e^m (S' + W0^T Y).
+// Blocks of 16 tokens keep the MFMA form for every off-diagonal term; inside a diagonal block each
+// column has its own triangular system (its own beta), solved here by forward substitution.
+// Lane (g4, r16) holds tokens 4*g4 .. 4*g4 + 3 of column r16 (the MFMA D layout), so the block
+// runs as four 4-token steps: lanes g4 == o solve their own 4x4 system in registers, the four
+// results go to the column's other lanes (ds_bpermute), and every lane subtracts their
+// contributions with its rows of L0.  sL: the block's L0 in fp32, [16][16] row-major with the
+// four-column group of row t stored at group (group ^ (t >> 2)), so the 16 lanes of a g4 group read
+// one address and the four groups four bank ranges; entries with t <= s hold 0.
+__device__ __forceinline__ f32x4 col_solve(const f32x4& X0, const f32x4& bt, const float* sL, int g4, int r16) {
+    f32x4 X = X0, Y = zero4();
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+        f32x4 Lg[4];  // L0[4*g4 + k][4*o + j]: the own diagonal block where g4 == o
+#pragma unroll
+        for (int k = 0; k < 4; ++k) Lg[k] = *reinterpret_cast<const f32x4*>(sL + (4 * g4 + k) * 16 + 4 * (o ^ g4));
+        float y[4];
+        y[0] = bt[0] * X[0];
+        y[1] = bt[1] * (X[1] - Lg[1][0] * y[0]);
+        y[2] = bt[2] * (X[2] - Lg[2][0] * y[0] - Lg[2][1] * y[1]);
+        y[3] = bt[3] * (X[3] - Lg[3][0] * y[0] - Lg[3][1] * y[1] - Lg[3][2] * y[2]);
+        const bool own = g4 == o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) Y[j] = own ? y[j] : Y[j];
+        float yb[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) yb[j] = __shfl(y[j], 16 * o + r16);
+        // rows below sub-block o (lanes g4 > o); zeros of L0 above the diagonal make it a no-op
+        // for g4 < o, and lanes g4 == o no longer read X
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) X[k] -= Lg[k][j] * yb[j];
+    }
+    return Y;
+}
+
+// D: head dim (NDB = D/16 state row tiles per wave, NKS = D/32 K steps over key dims).  BV: beta
+// per value column (BETA_VALUE, fp32 in `kb`).
+template <typename TIn, typename TG, bool OUT, bool CK, int D, bool BV>
 struct GdnStep {
     using L = GLay<TIn, OUT, D>;
     using PR = Prec<TIn>;
@@ -217,8 +258,8 @@ struct GdnStep {
 #pragma unroll
         for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
         if (!fast) {
-            if (!skip_m) gdn_tokenwise<TIn, TG, OUT>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
-            if (!OUT) gdn_tokenwise<TIn, TG, false>(a, wk, h, c0, tc, nv, g4, r16, true, SN);
+            if (!skip_m) gdn_tokenwise<TIn, TG, OUT, BV>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
+            if (!OUT) gdn_tokenwise<TIn, TG, false, BV>(a, wk, h, c0, tc, nv, g4, r16, true, SN);
             if constexpr (LATE_LOAD || LATE_LOAD_OUT) after_inputs();
             __syncthreads();
             return;
@@ -259,7 +300,23 @@ struct GdnStep {
             }
             // Diagonal block wave of the UT transform: T_ww = (I + L_ww)^-1 by doubling, kept as
             // D-layout pairs (X, X^T) so every product reads its operands from registers.
-            if (wave >= DW0 && wave < DW0 + 4) {
+            if (BV && wave >= DW0 && wave < DW0 + 4) {
+                // per-value beta: the diagonal block of L0 itself, fp32, for the column solves
+                const int ib = wave - DW0;
+                f32x4 Lm = zero4();
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) {
+                    const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * ib + r16, 32 * ks, g4);
+                    const Split8<NS> wf = lds_frag<NS>(sWT, L::ROWP, L::RS, 16 * ib + r16, 32 * ks, g4);
+                    Lm = mfma_split<NS, NS, NS>(bf, wf, Lm);  // Lm[t = 4*g4+j][s = r16]
+                }
+                float* sL = reinterpret_cast<float*>(sTI) + ib * 256;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 4 * g4 + j;
+                    sL[t * 16 + 4 * ((r16 >> 2) ^ g4) + (r16 & 3)] = t > r16 ? Lm[j] : 0.f;
+                }
+            } else if (!BV && wave >= DW0 && wave < DW0 + 4) {
                 const int ib = wave - DW0;
                 f32x4 Lm = zero4(), LmT = zero4();
 #pragma unroll
@@ -310,6 +367,14 @@ struct GdnStep {
                 const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) Sp[db][i] = St[db][i] * em[i];
+            }
+            f32x4 bv[4];  // BV: beta of rows 16i + 4*g4 + k, column c0 + r16 (rows past nv: the last row's)
+            if constexpr (BV) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        bv[i][k] = tok_row<float>(a.kb, wk, tc + min(16 * i + 4 * g4 + k, nv - 1), h, c0)[r16];
             }
             Split8<NS> sf[NKS];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
 #pragma unroll
@@ -374,8 +439,12 @@ struct GdnStep {
 #pragma unroll
                     for (int k = 0; k < 4; ++k) X[k] -= p[k];
                 }
-                const Split8<NS> tf = tile_frag<NS>(sTI, L::DIAGP, i, 0, false, lane);
-                U[i] = mfma_split<NS, NS, NS>(tf, split_k16<NS>(X), zero4());
+                if constexpr (BV) {
+                    U[i] = col_solve(X, bv[i], reinterpret_cast<const float*>(sTI) + i * 256, g4, r16);
+                } else {
+                    const Split8<NS> tf = tile_frag<NS>(sTI, L::DIAGP, i, 0, false, lane);
+                    U[i] = mfma_split<NS, NS, NS>(tf, split_k16<NS>(X), zero4());
+                }
                 us[i] = split_k16<NS>(U[i]);
             }
             // U with K = tokens 32*k2 + pi(g4, j): A-operand of U^T, B-operand of U
@@ -441,10 +510,10 @@ struct GdnStep {
     }
 };
 
-template <typename TIn, typename TG, bool OUT, bool CK, int D>
+template <typename TIn, typename TG, bool OUT, bool CK, int D, bool BV>
 __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[D / 16],
                          f32x4 (&SN)[D / 16], bool skip_m, char* smem) {
-    using St = GdnStep<TIn, TG, OUT, CK, D>;
+    using St = GdnStep<TIn, TG, OUT, CK, D, BV>;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const ChunkAddr ad = chunk_addr<OUT, TIn, TG>(a, wk, h, tg, wave * 16 + 4 * row, wave * 16 + 4 * row);
     const bool key_beta = a.beta_kind == BETA_KEY;
@@ -475,7 +544,7 @@ constexpr int gdn_min_waves() {
 // K1: the segment map driven from I with V = 0 (-> M_p, state M) and from 0 with the real V
 // (-> N_p, state N) in one chunk walk.  A sequence's first segment without an initial state
 // carries in S_in = 0, so its M is left at I (the scan's product with 0 stays 0) and only N runs.
-template <typename TIn, typename TG, bool CK, int D>
+template <typename TIn, typename TG, bool CK, int D, bool BV>
 __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, false, D>())) void gdn_seg_mn_kernel(PrefillParams a) {
     using L = GLay<TIn, false, D>;
     constexpr int NDB = D / 16;
@@ -485,14 +554,16 @@ __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, false, D>())) void gdn_s
     if (!find_work(a, w, wk)) return;
     f32x4 M[NDB], N[NDB];
     init_seg_map(M, N);
-    gdn_walk<TIn, TG, false, CK, D>(a, wk, h, M, N, wk.p == 0 && a.s0 == nullptr, smem);
+    gdn_walk<TIn, TG, false, CK, D, BV>(a, wk, h, M, N, wk.p == 0 && a.s0 == nullptr, smem);
     store_seg_map<Prec<TIn>::NS>(a, w, h, M, N);
 }
 
 // K3: outputs of one segment from S_in[p] (in the N slot after the scan).  At D = 64 two
 // workgroups per CU where two fit in LDS (bf16 I/O); fp16 and fp32 I/O hold larger planes and run
 // one.  At D = 128 (16-bit I/O) one workgroup of eight waves per CU.
-template <typename TIn, typename TG, bool CK, int D>
+// gdn_whole (beta per value column, BV): each value column then has its own segment map, so there
+// is one segment per sequence, walked from s0 (or zero), and the final state is written here.
+template <typename TIn, typename TG, bool CK, int D, bool BV>
 __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, true, D>())) void gdn_seg_out_kernel(PrefillParams a) {
     using L = GLay<TIn, true, D>;
     constexpr int NDB = D / 16;
@@ -501,8 +572,23 @@ __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, true, D>())) void gdn_se
     Work wk;
     if (!find_work(a, w, wk)) return;
     f32x4 S[NDB];
-    load_seg_state(a, w, h, S);
-    gdn_walk<TIn, TG, true, CK, D>(a, wk, h, S, S, false, smem);
+    const int lane = threadIdx.x & 63, c = wave_id() * 16 + (lane & 15), g4 = lane >> 4;
+    const int64_t sb = (wk.seq * a.H + h) * (int64_t)D * D;  // [seq, h] of s0 / seq_final
+    if (BV && a.gdn_whole) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[db][i] = a.s0 ? a.s0[sb + (16 * db + 4 * g4 + i) * D + c] : 0.f;
+    } else {
+        load_seg_state(a, w, h, S);
+    }
+    gdn_walk<TIn, TG, true, CK, D, BV>(a, wk, h, S, S, false, smem);
+    if (BV && a.gdn_whole && a.seq_final) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a.seq_final[sb + (16 * db + 4 * g4 + i) * D + c] = S[db][i];
+    }
 }
 
 // K2: one workgroup per (sequence, head, 16 state columns), one wave per 16-row tile t of that
@@ -603,16 +689,24 @@ __global__ __launch_bounds__(4 * D) void gdn_seg_scan_kernel(PrefillParams a, fl
 // ---------------------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------------------
-template <typename TIn, typename TG, bool CK, int D>
-static hipError_t launch_gdn_ck(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
+template <typename TIn, typename TG, bool CK, int D, bool BV>
+static hipError_t launch_gdn_bv(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
     if (which == 0) {
-        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG, CK, D>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D), 0,
-                           stream, a);
+        hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG, CK, D, BV>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D),
+                           0, stream, a);
     } else {
-        hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG, CK, D>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D), 0,
-                           stream, a);
+        hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG, CK, D, BV>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D),
+                           0, stream, a);
     }
     return hipGetLastError();
+}
+
+// Per-value-column beta runs its own instances (the column solves), so the other beta kinds keep
+// their register allocation.
+template <typename TIn, typename TG, bool CK, int D>
+static hipError_t launch_gdn_ck(const PrefillParams& a, int64_t n_work, int which, hipStream_t stream) {
+    if (a.beta_kind == BETA_VALUE) return launch_gdn_bv<TIn, TG, CK, D, true>(a, n_work, which, stream);
+    return launch_gdn_bv<TIn, TG, CK, D, false>(a, n_work, which, stream);
 }
 
 // Unchecked row addressing only when T is a whole number of four-row groups.  Head dim 128 takes
@@ -673,15 +767,15 @@ hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt
 template <int D>
 static const void* gdn_out_kernel_ptr(int io_dt, bool ck) {
     if (io_dt == DT_F16)
-        return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, true, D>)
-                  : reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, false, D>);
+        return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, true, D, false>)
+                  : reinterpret_cast<const void*>(gdn_seg_out_kernel<_Float16, _Float16, false, D, false>);
     if constexpr (D == 64) {
         if (io_dt == DT_F32)
-            return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, true, D>)
-                      : reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, false, D>);
+            return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, true, D, false>)
+                      : reinterpret_cast<const void*>(gdn_seg_out_kernel<float, float, false, D, false>);
     }
-    return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, true, D>)
-              : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, false, D>);
+    return ck ? reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, true, D, false>)
+              : reinterpret_cast<const void*>(gdn_seg_out_kernel<__bf16, __bf16, false, D, false>);
 }
 
 int gdn_seg_out_blocks_per_cu(int io_dt, bool ck, int D) {

@@ -52,10 +52,10 @@ __device__ __forceinline__ float beta_value(const PrefillParams& a, const Work& 
     return (float)reinterpret_cast<const _Float16*>(a.beta)[i];
 }
 
-// Token-by-token GDN update of one wave's 16 state columns (decay spans beyond SPAN_MAX).
-// S tile db holds S[16*db + 4*g4 + i][c0 + r16] (NDB tiles: key dim 16 * NDB); with_v false reads
-// V as zero.
-template <typename TIn, typename TG, bool OUT, int NDB>
+// Token-by-token GDN update of one wave's 16 state columns (decay spans beyond the factored form's
+// limit).  S tile db holds S[16*db + 4*g4 + i][c0 + r16] (NDB tiles: key dim 16 * NDB); with_v
+// false reads V as zero.  BV: beta per value column (BETA_VALUE, fp32 in `kb`) scales u.
+template <typename TIn, typename TG, bool OUT, bool BV = false, int NDB>
 __device__ void gdn_tokenwise(const PrefillParams& a, const Work& wk, int64_t h, int c0, int64_t tc, int nv, int g4,
                               int r16, bool with_v, f32x4 (&S)[NDB]) {
     for (int t = 0; t < nv; ++t) {
@@ -72,7 +72,8 @@ __device__ void gdn_tokenwise(const PrefillParams& a, const Work& wk, int64_t h,
         }
         pred += __shfl_xor(pred, 16);
         pred += __shfl_xor(pred, 32);
-        const float u = (with_v ? (float)tok_row<TIn>(a.v, wk, tt, h, c0)[r16] : 0.f) - pred;
+        float u = (with_v ? (float)tok_row<TIn>(a.v, wk, tt, h, c0)[r16] : 0.f) - pred;
+        if constexpr (BV) u *= tok_row<float>(a.kb, wk, tt, h, c0)[r16];
         float part = 0.f;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {

@@ -28,13 +28,18 @@ struct PrefillParams {
     const int32_t* seg_off;// varlen: [n_seqs + 1] segment offsets (device, from plan kernel)
     int flags;             // bit 0: the last token of each sequence keeps g unclamped
     // Gated DeltaNet (chunked): write strength beta per token (BETA_HEAD, strides b_sb/b_st/b_sh,
-    // dtype beta_dt) or per (token, key dim) (BETA_KEY, fp32, in `kb`), or none.
+    // dtype beta_dt), per (token, key dim) (BETA_KEY) or per (token, value dim) (BETA_VALUE), both
+    // fp32 in `kb`, or none.
     const void* beta;
     int beta_dt, beta_kind;
     int64_t b_sb, b_st, b_sh;
     TokTensor kb;
     float* ws_m;           // GDN: [n_work, H] slots of the segment transition matrices as bf16 parts
     float* ws_spare;       // [n_seqs, H, Dk, Dv] sink for the segment scan's padding steps
+    // GDN with beta per value column: one segment per sequence, the output kernel walks it from
+    // s0 (or zero) and writes the final state here ([n_seqs, H, Dk, Dv] fp32, or null).
+    float* seq_final;
+    int gdn_whole;
     // Prefill with the VectorisedGLA pre-processing applied in stage 1 (q, k, g raw projections):
     // fp32 RoPE tables [T, Dk] (row = token of the sequence, token stride cs.st; sb = sh = 0)
     TokTensor cs, sn;

@@ -35,8 +35,8 @@ _DIMS = (32, 64, 128)
 _PAIRS = ((32, 32), (64, 64), (128, 64), (128, 128))  # (Dk, Dv) the prefill kernels support
 _DECODE_PAIRS = ((32, 32), (64, 64), (64, 128), (128, 64), (128, 128))
 # Gated DeltaNet prefill: the chunked WY/UT kernels (head dims <= 64, and 128 with 16-bit I/O)
-# unless this is False, in which case every call takes the token-serial kernel (kept for the
-# per-value-dim beta and fp32 I/O at head dim 128).
+# unless this is False, in which case every call takes the token-serial kernel (kept for fp32 I/O
+# at head dim 128 and single tokens).
 _chunked_gdn_enabled = True
 # Gates with one value per (token, head) take the scalar-decay chunked kernels unless this is False
 # (then they run the per-key-dim chunked kernels on the broadcast gate).
@@ -631,10 +631,9 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
     Dv0 = v.shape[-1]
     D = _round_dk(max(Dk0, Dv0))
     # chunked WY/UT path: (64, 64) heads (smaller ones zero-padded) and (128, 128) heads with 16-bit
-    # I/O, per-token or per-key beta; a gate with one value per (token, head) and beta none or per
-    # token takes the scalar-decay kernels at D <= 64
-    chunked = ((D <= 64 or (D == 128 and q.dtype != torch.float32)) and T > 1
-               and beta_kind != _lib.BETA_VALUE and _chunked_gdn_enabled)
+    # I/O, every beta kind; a gate with one value per (token, head) and beta none or per token
+    # takes the scalar-decay kernels at D <= 64
+    chunked = (D <= 64 or (D == 128 and q.dtype != torch.float32)) and T > 1 and _chunked_gdn_enabled
     scalar = (chunked and D <= 64 and sg is not None and beta_kind in (_lib.BETA_NONE, _lib.BETA_HEAD)
               and _scalar_gdn_enabled)
     if chunked and D <= 64:
@@ -647,7 +646,7 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
         bp = beta
         if beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE):
             bp = _pad_last(beta, D)
-        if chunked and beta_kind == _lib.BETA_KEY:
+        if chunked and beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE):
             bp = bp.to(torch.float32)
         bp = bp.contiguous()
         bst = (bp.stride(0), bp.stride(1), bp.stride(2))
