@@ -600,12 +600,21 @@ __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, true, D>())) void gdn_se
 // into A-operand layout (row 16t + r16, K slots 32kk + pi(g4, j)).  The M/N loads of a segment do
 // not depend on the carry: a ring of register sets keeps them two segments ahead.  Two LDS buffers
 // alternate, so a step's writes never meet the previous step's reads.
+// Placement: workgroups are dispatched round-robin over the XCDs, each with its own L2, and every
+// strip of a (sequence, head) reads that pair's whole segment maps, so a 1-D grid puts the D / 16
+// strips of a pair on one XCD (workgroup b runs on XCD b % SCAN_XCDS; its slot b / SCAN_XCDS
+// there holds strip slot % (D / 16) of pair (slot / (D / 16)) * SCAN_XCDS + b % SCAN_XCDS).
+constexpr int SCAN_XCDS = 8;
+
 template <int NS, int D>
 __global__ __launch_bounds__(4 * D) void gdn_seg_scan_kernel(PrefillParams a, float* s_final) {
     constexpr int NKS = D / 32, NDB = D / 16, DD = D * D;
     __shared__ __attribute__((aligned(16))) char sbuf[2][NKS][NS][64 * 16];
-    const int64_t seq = blockIdx.z, h = blockIdx.y;
-    const int strip = blockIdx.x, cb = strip * 16;
+    const int64_t slot = blockIdx.x / SCAN_XCDS;
+    const int64_t pair = (slot / NDB) * SCAN_XCDS + blockIdx.x % SCAN_XCDS;
+    if (pair >= a.n_seqs * a.H) return;  // the grid's padding to whole rounds of the XCDs
+    const int64_t seq = pair / a.H, h = pair % a.H;
+    const int strip = (int)(slot % NDB), cb = strip * 16;
     const int lane = threadIdx.x & 63, t = wave_id(), r16 = lane & 15, g4 = lane >> 4;
     int64_t p0, np;
     if (a.varlen) {
@@ -749,7 +758,8 @@ hipError_t launch_gdn_seg_out(const PrefillParams& a, int64_t n_work, int io_dt,
 
 hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream) {
     const int D = a.Dk;
-    const dim3 grid((unsigned)(D / 16), (unsigned)a.H, (unsigned)a.n_seqs);
+    const int64_t pairs = a.n_seqs * a.H;
+    const dim3 grid((unsigned)((pairs + SCAN_XCDS - 1) / SCAN_XCDS * SCAN_XCDS * (D / 16)));
     if (D == 128) {
         if (io_dt == DT_F32) return hipErrorInvalidValue;
         hipLaunchKernelGGL((gdn_seg_scan_kernel<2, 128>), grid, dim3(4 * D), 0, stream, a, s_final);

@@ -318,9 +318,11 @@ struct SgStep {
     using L = SLay<TIn, OUT, PRE>;
     static constexpr int NS = L::NS, NX = L::NX;
 
+    // skip_m (K1): S is left as it is (the map of a segment whose carried-in state is zero is
+    // never used).
     template <typename Hook>
     __device__ static void run(const SgCtx& x, int64_t tc, int nv, const SIn<TIn>& cur, f32x4 (&S)[4],
-                               f32x4 (&SN)[4], char* smem, Hook&& after_inputs) {
+                               f32x4 (&SN)[4], bool skip_m, char* smem, Hook&& after_inputs) {
         const int lane = threadIdx.x & 63, wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
         const int tg = lane >> 2, row = lane & 3;
         const int c0 = wave * 16;
@@ -388,7 +390,7 @@ struct SgStep {
         after_inputs();
         __syncthreads();
         if (__builtin_amdgcn_readfirstlane(__float_as_int(sF[L::F_MISC + 1])) != 0) {
-            sg_tokenwise<TIn, OUT>(x, c0, tc, nv, g4, r16, OUT, S);
+            if (!skip_m) sg_tokenwise<TIn, OUT>(x, c0, tc, nv, g4, r16, OUT, S);
             if (!OUT) sg_tokenwise<TIn, false>(x, c0, tc, nv, g4, r16, true, SN);
             __syncthreads();
             return;
@@ -658,7 +660,7 @@ struct SgStep {
         if constexpr (OUT) {
             pass(std::true_type{}, S);
         } else {
-            pass(std::false_type{}, S);
+            if (!skip_m) pass(std::false_type{}, S);
             __builtin_amdgcn_sched_barrier(0);  // one pass at a time: their temporaries never overlap
             pass(std::true_type{}, SN);
         }
@@ -667,7 +669,8 @@ struct SgStep {
 };
 
 template <typename TIn, bool OUT, bool CK, bool OBF, bool PRE>
-__device__ void sg_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[4], f32x4 (&SN)[4], char* smem) {
+__device__ void sg_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4 (&S)[4], f32x4 (&SN)[4], bool skip_m,
+                        char* smem) {
     using St = SgStep<TIn, OUT, CK, OBF, PRE>;
     const int lane = threadIdx.x & 63, wave = wave_id(), tg = lane >> 2, row = lane & 3;
     const SgCtx x = sg_ctx<OUT, TIn>(a, wk, h, tg, wave * 16 + 4 * row);
@@ -681,7 +684,7 @@ __device__ void sg_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4
     int64_t tc = wk.t_begin;
     sg_load<OUT, CK>(A, x, tc, chunk_nv(tc), true);
     for (int64_t c = 0; c < nch; ++c, tc += CHUNK)
-        St::run(x, tc, chunk_nv(tc), A, S, SN, smem, [&] {
+        St::run(x, tc, chunk_nv(tc), A, S, SN, skip_m, smem, [&] {
             const bool more = c + 1 < nch;
             sg_load<OUT, CK>(A, x, tc + CHUNK, more ? chunk_nv(tc + CHUNK) : 0, more);
         });
@@ -695,6 +698,8 @@ constexpr int sg_occupancy() {
 }
 
 // K1: the segment map driven from [I | 0] with V = 0 (-> M_p) and from 0 with the real V (-> N_p).
+// A sequence's first segment without an initial state carries in zero: its M stays I and only N
+// runs.
 template <typename TIn, bool CK>
 __global__ __launch_bounds__(256, (sg_occupancy<SLay<TIn, false, true>>())) void gdn_sg_seg_mn_kernel(PrefillParams a) {
     using L = SLay<TIn, false, true>;
@@ -704,7 +709,7 @@ __global__ __launch_bounds__(256, (sg_occupancy<SLay<TIn, false, true>>())) void
     if (!find_work(a, w, wk)) return;
     f32x4 M[4], N[4];
     init_seg_map(M, N);
-    sg_walk<TIn, false, CK, false, true>(a, wk, h, M, N, smem);
+    sg_walk<TIn, false, CK, false, true>(a, wk, h, M, N, wk.p == 0 && a.s0 == nullptr, smem);
     store_seg_map<Prec<TIn>::NS>(a, w, h, M, N);
 }
 
@@ -718,7 +723,7 @@ __global__ __launch_bounds__(256, (sg_occupancy<SLay<TIn, true, false>>())) void
     if (!find_work(a, w, wk)) return;
     f32x4 S[4];
     load_seg_state(a, w, h, S);
-    sg_walk<TIn, true, CK, OBF, false>(a, wk, h, S, S, smem);
+    sg_walk<TIn, true, CK, OBF, false>(a, wk, h, S, S, false, smem);
 }
 
 // ---------------------------------------------------------------------------------------
