@@ -3,7 +3,9 @@
 // Recurrence (reference: triune/kernels/fast_gla.py:781-836 fast_recurrent_gated_deltanet,
 // :383-477 the Triton per-token kernel), per (sequence, head):
 //   u_t = v_t - S_{t-1}^T k_t ,  S_t = D_t S_{t-1} + w_t u_t^T ,  o_t = S_t^T q_t
-// with D_t = diag(exp(min(g_t, 0))) and w_t = beta_t * k_t (beta per token, per key dim, or 1).
+// with D_t = diag(exp(min(g_t, 0))) and w_t = beta_t * k_t (beta per token, per key dim, or 1;
+// beta per value dim scales u_t instead, see col_solve).  Head dims Dk = Dv = D in {64, 128}: one
+// wave per 16 value columns.
 //
 // Chunk form (C = 64 tokens, G = inclusive cumulative log-decay inside the chunk, Gp = G - g the
 // exclusive one, m = G_C / 2 per key dim, S0 the state at the chunk start, S' = e^m S0):
@@ -20,7 +22,8 @@
 //                     tiles and inverses
 //   K2 gdn_seg_scan : per (sequence, head, 16 columns; one wave per 16 rows) the carry S_in[p]
 //                     (written in place of N_p)
-//   K3 gdn_seg_out  : per (segment, head) the chunk walk from S_in[p], writing o
+//   K3 gdn_seg_out  : per (segment, head) the chunk walk from S_in[p], writing o (beta per value
+//                     dim: the whole sequence from s0, writing the final state too)
 // Products run on v_mfma_f32_16x16x32_bf16 with operands split into bf16 parts (2 for 16-bit
 // I/O, 3 for fp32) and fp32 accumulation, as in the GLA prefill.  Chunks whose decay span
 // exceeds GDN_SPAN_MAX run token by token.
