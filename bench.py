@@ -352,6 +352,36 @@ def bench_gdn128(dev, reps=10):
                          "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
 
+def bench_gdn_vbeta(dev, reps=10):
+    """Gated DeltaNet prefill with beta per value column (the reference's Triton orientation,
+    fast_gla.py:464-465; [B, T, H, D] beta through fast_chunk_gated_deltanet): config 3's shape
+    (B=4, H=6, T=8192, D=64) and the model's head dim (B=4, H=12, T=8192, D=128), bf16, q and k
+    L2-normalised, g = logsigmoid(x) per key dim, beta = sigmoid(x).  Each sequence is one segment
+    (the per-column segment maps differ), walked by the output kernel."""
+    from triune_amd import fast_chunk_gated_deltanet
+
+    out = {"workload": "Gated DeltaNet prefill, beta per value column (bf16, per-key-dim logsigmoid gates)"}
+    for key, (B, T, H, D) in (("d64", (4, 8192, 6, 64)), ("d128", (4, 8192, 12, 128))):
+        gen = torch.Generator(device=dev).manual_seed(5)
+        qk = torch.nn.functional.normalize(torch.randn(B, T, 2, H, D, device=dev, generator=gen), dim=-1).bfloat16()
+        q, k = qk[:, :, 0], qk[:, :, 1]
+        v = torch.randn(B, T, H, D, device=dev, generator=gen).bfloat16()
+        g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, D, device=dev, generator=gen)).bfloat16()
+        beta = torch.sigmoid(torch.randn(B, T, H, D, device=dev, generator=gen))
+        fn = lambda: fast_chunk_gated_deltanet(q, k, v, g, beta=beta)  # noqa: E731
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+        # q, k, v, g read and o written (bf16), beta read (fp32), the fp32 final state written
+        alg = B * T * H * D * (5 * 2 + 4) + B * H * D * D * 4
+        gbs = alg / (ms * 1e-3) / 1e9
+        out[key] = {"shape": f"B={B}, H={H}, T={T}, D={D}", "ms": round(ms, 4), "tok_s": round(B * T / (ms * 1e-3), 1),
+                    "alg_bytes": alg, "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                                   "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    return out
+
+
 def bench_varlen(dev, reps=5):
     """Packed ragged GLA prefill, config 4 (32 sequences of 128..8192 tokens, H=12, D=128, bf16)."""
     from triune_amd import fast_chunk_gla_varlen
@@ -545,7 +575,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "gdn128", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
+        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -573,7 +603,7 @@ def main():
         elif args.only == "fused_decode":
             res = bench_fused_decode(args.decode_steps, dev)
         else:
-            res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
+            res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "gdn_vbeta": bench_gdn_vbeta, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
                    "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
@@ -582,7 +612,8 @@ def main():
     # headline itself still does exactly `warmup` untimed passes before its `steps` timed ones.
     cpu = None if args.no_cpu else cpu_baseline()
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
-    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
+    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev),
+                                      "gdn_vbeta": bench_gdn_vbeta(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "bwd128": bench_bwd128(dev),
