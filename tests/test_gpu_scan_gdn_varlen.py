@@ -218,6 +218,21 @@ def test_gdn_chunked_d128_16bit(dev, io, kind, T):
     assert _err(s16.cpu(), rs) <= 2e-3
 
 
+@pytest.mark.parametrize("kind", ["head", "value"])
+@pytest.mark.parametrize("T", [2, 5, 64, 65])
+def test_gdn_chunked_d128_short_sequences(dev, kind, T):
+    """D = 128, bf16: sequences of one partial chunk, exactly one chunk and one chunk plus a token
+    (one segment; checked and unchecked row instances), fp32 outputs and states at 2e-3."""
+    q, k, v, g, beta, s0 = _gdn_case(T, 128, kind, seed=T + 40)
+    q, k, v, g = (x.bfloat16() for x in (q, k, v, g))
+    o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),
+                                     initial_state=s0.to(dev), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0, beta_kind=O.BETA_VALUE)
+    assert o.shape == (2, T, 2, 128) and s.shape == (2, 2, 128, 128)
+    assert _err(o.cpu(), ro) <= 2e-3 and _err(s.cpu(), rs) <= 2e-3
+
+
 def test_gdn_chunked_d128_model_distributions(dev):
     """The reference model's GDN call at its default head dim (attention.py:509-536: q, k =
     normalize(elu(x) + 1), g = logsigmoid(x), no beta), bf16, 24 (b, h) rows over several
