@@ -163,6 +163,60 @@ def bench_decode(steps_total, dev, n_bufs=12):
     }
 
 
+def bench_gdn_decode(dev, steps=64, n_bufs=12):
+    """Gated DeltaNet decode step (T == 1) at config 2's batch shape (B=256, H=6, D=64), beta per
+    head, bf16 q/k/v/g/o, fp32 state, through the C-ABI entry the operator calls
+    (triune_hip_gdn_prefill, which runs the decode kernel for T == 1).  `steps` steps in one HIP
+    graph; step t reads state buffer t % n_bufs and writes buffer (t - 1) % n_bufs, which is read
+    again n_bufs - 1 steps later (12 x 25 MB: more than the 256 MB MALL between a write and its
+    read), and takes input set t % n_bufs."""
+    from triune_amd._lib import check, dtype_code, lib, ptr, stream_of, strides
+
+    B, H, D = 256, 6, 64
+    gen = torch.Generator(device=dev).manual_seed(6)
+    nq = lambda: torch.nn.functional.normalize(torch.randn(n_bufs, B, 1, H, D, device=dev, generator=gen), dim=-1)  # noqa: E731
+    q, k = nq().bfloat16(), nq().bfloat16()
+    v = torch.randn(n_bufs, B, 1, H, D, device=dev, generator=gen).bfloat16()
+    g = torch.nn.functional.logsigmoid(torch.randn(n_bufs, B, 1, H, D, device=dev, generator=gen)).bfloat16()
+    beta = torch.sigmoid(torch.randn(n_bufs, B, 1, H, device=dev, generator=gen))
+    states = [0.1 * torch.randn(B, H, D, D, device=dev, generator=gen) for _ in range(n_bufs)]
+    outs = torch.empty(n_bufs, B, 1, H, D, device=dev, dtype=torch.bfloat16)
+    tok3 = lambda x: (x.stride(0), x.stride(1), x.stride(2))  # noqa: E731
+    st = strides(tok3(q[0]), tok3(k[0]), tok3(v[0]), tok3(g[0]), tok3(beta[0]), tok3(outs[0]))
+    lb = lib()
+
+    def loop():
+        for t in range(steps):
+            i = t % n_bufs
+            rc = lb.triune_hip_gdn_prefill(ptr(q[i]), ptr(k[i]), ptr(v[i]), ptr(g[i]), dtype_code(q), dtype_code(g),
+                                           ptr(beta[i]), dtype_code(beta), 1, st, ptr(states[i]), ptr(outs[i]),
+                                           dtype_code(outs), ptr(states[(t - 1) % n_bufs]), B, 1, H, D, D,
+                                           stream_of(q))
+            check(rc, "triune_hip_gdn_prefill")
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        loop()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        loop()
+    graph.replay()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(graph.replay, 5, torch.cuda.current_stream())
+    step_us = ms * 1e3 / steps
+    # state read + written (fp32); q, k, v, g read and o written (bf16); beta read (fp32)
+    step_bytes = 2 * B * H * D * D * 4 + B * H * D * 2 * 5 + B * H * 4
+    gbs = step_bytes / (step_us * 1e-6) / 1e9
+    return {"workload": "Gated DeltaNet decode step (T == 1), config-2 shape (B=256, H=6, D=64), beta per head, "
+                        f"{steps}-step graph, {n_bufs} rotating state buffers and input sets",
+            "us_per_step": round(step_us, 3), "tok_s": round(B / (step_us * 1e-6), 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes_per_step": step_bytes}}
+
+
 def bench_prep(dev, reps=10):
     """In-place GLA input pre-processing (ELU+1, L2 norm, RoPE on q and k; logsigmoid on g) at the
     config-1 shape: qkv [4, 16384, 3, 6, 64] and g [4, 16384, 6, 64] bf16, fp32 RoPE tables."""
@@ -575,7 +629,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
+        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "gdn_decode", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -603,7 +657,8 @@ def main():
         elif args.only == "fused_decode":
             res = bench_fused_decode(args.decode_steps, dev)
         else:
-            res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "gdn_vbeta": bench_gdn_vbeta, "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
+            res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "gdn_vbeta": bench_gdn_vbeta, "gdn_decode": bench_gdn_decode,
+                   "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
                    "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
@@ -613,7 +668,8 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline()
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev),
-                                      "gdn_vbeta": bench_gdn_vbeta(dev), "varlen": bench_varlen(dev), "prep": bench_prep(dev),
+                                      "gdn_vbeta": bench_gdn_vbeta(dev), "gdn_decode": bench_gdn_decode(dev),
+                                      "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "bwd128": bench_bwd128(dev),

@@ -292,6 +292,47 @@ def test_gdn_chunked_wide_decay_span(dev, D, io):
     assert e_o <= tol and e_s <= tol
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("kind", ["none", "head", "key", "value"])
+@pytest.mark.parametrize("io", [torch.float32, torch.bfloat16])
+def test_gdn_decode_step_many_rows(dev, D, kind, io):
+    """T == 1 of 200 x 6 rows (more rows than decode workgroups, so each walks several) runs the
+    decode step; every beta kind (per value dim through the operator's internal entry, as the
+    public T == 1 calls apply a 4-D beta to rows), fp32 outputs and states at the fp32 bar, and
+    three chained steps against the three-token recurrence."""
+    import triune_amd._lib as LB
+    from triune_amd import fast_gla as FG
+    gen = torch.Generator().manual_seed(D + len(kind))
+    B, H, T = 200, 6, 3
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, D, generator=gen), dim=-1).to(io)
+    k = torch.nn.functional.normalize(torch.randn(B, T, H, D, generator=gen), dim=-1).to(io)
+    v = torch.randn(B, T, H, D, generator=gen).to(io)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, D, generator=gen)).to(io)
+    g[:, :, 0, :3] = 0.5  # positive gates: clamped to 0
+    s0 = 0.1 * torch.randn(B, H, D, D, generator=gen)
+    beta = None
+    if kind == "head":
+        beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    elif kind in ("key", "value"):
+        beta = torch.sigmoid(torch.randn(B, T, H, D, generator=gen))
+    bk = {"none": LB.BETA_NONE, "head": LB.BETA_HEAD, "key": LB.BETA_KEY, "value": LB.BETA_VALUE}[kind]
+    s = s0.to(dev)
+    outs = []
+    for t in range(T):
+        sl = slice(t, t + 1)
+        bt = None if beta is None else beta[:, sl].to(dev)
+        o, s = FG._gdn(q[:, sl].to(dev), k[:, sl].to(dev), v[:, sl].to(dev), g[:, sl].to(dev), bt, s, bk,
+                       out_dtype=torch.float32)
+        outs.append(o)
+    torch.cuda.synchronize()
+    o = torch.cat(outs, dim=1).cpu()
+    okind = O.BETA_VALUE if kind == "value" else O.BETA_KEY
+    ro, rs = O.gdn_fwd(q.float(), k.float(), v.float(), g.float(), beta, s0, beta_kind=okind)
+    e_o, e_s = _err(o, ro), _err(s.cpu(), rs)
+    print(f"gdn decode D={D} {kind} {io}: o {e_o:.3e} S {e_s:.3e}")
+    assert e_o <= 1e-5 and e_s <= 1e-5
+
+
 def test_gdn_single_token(dev):
     q, k, v, g, beta, s0 = _gdn_case(1, 64, "head", seed=5)
     o, s = fast_chunk_gated_deltanet(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta=beta.to(dev),

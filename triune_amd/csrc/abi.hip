@@ -744,6 +744,15 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
     a.o_sb = strides[15]; a.o_st = strides[16]; a.o_sh = strides[17];
     a.o = o; a.s0 = s0; a.s_final = s_final;
     a.B = B; a.T = T; a.H = H;
+    // A single token of many rows: the decode step (float4 state streaming) where the rows allow
+    // vector loads (q, k, g, v rows aligned, beta fp32 and aligned); else the token-serial kernel.
+    const bool vec_beta = beta_kind == TRIUNE_BETA_KEY || beta_kind == TRIUNE_BETA_VALUE;
+    if (T == 1 && Dk == Dv && (Dk == 64 || Dk == 128) && gate_dtype_ok(io_dtype, g_dtype) &&
+        vec_ok(v, io_dtype, strides + 6, 3) && vec4_ok(o, o_dtype, strides + 15, 3) &&
+        (beta_kind == TRIUNE_BETA_NONE || beta_dtype == TRIUNE_DT_F32) &&
+        (beta_kind != TRIUNE_BETA_HEAD || reinterpret_cast<uintptr_t>(beta) % 4 == 0) &&
+        (!vec_beta || vec_ok(beta, TRIUNE_DT_F32, strides + 12, 3)))
+        return launch_status(launch_gdn_decode(a, Dk, 4 * device_cus(), (hipStream_t)stream));
     return launch_status(launch_gdn_tokenwise(a, Dk, Dv, (hipStream_t)stream));
 }
 

@@ -104,6 +104,163 @@ static hipError_t launch_gdn_t(const GdnParams& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------
+// One decode step (T == 1) of many rows: the reference's single-token branch
+// (fast_gla.py:873-884: prediction from the un-decayed state, decay exp(min(g, 0))), with beta
+// per head, per key dim or per value dim as in the chunked forms, and the fp32 state streamed
+// once (s0 read, s_final written, nontemporal float4).  The thread layout is the GLA decode
+// step's (gla_decode.hip): a 256-thread block takes one state row (b, h) at a time, thread
+// (rg, cg) owning rows rg*RPT .. rg*RPT+RPT-1 and columns 4*cg .. 4*cg+3, and walks rows
+// blockIdx.x, + gridDim.x, ... with the next row's state loads issued before this row's state
+// is stored.  Two reductions over the row groups per row: the prediction S^T k (before the
+// update; every thread needs its four columns of it) and the readout S'^T q.  beta (BK != NONE)
+// is fp32.
+// ---------------------------------------------------------------------------------------
+template <typename T>
+using DVec4 = T __attribute__((ext_vector_type(4)));
+
+template <int DK, int DV, int RPT, typename TIO, typename TG, int BK>
+__global__ __launch_bounds__(DK * DV / (4 * RPT)) void gdn_decode_kernel(GdnParams a, uint32_t rows) {
+    constexpr int TPB = DK * DV / (4 * RPT), CG = DV / 4, WAVES = TPB / 64;
+    static_assert(TPB % 64 == 0 && CG <= 64 && RPT % 4 == 0, "unsupported decode tiling");
+    const int tid = threadIdx.x;
+    const int cg = tid % CG, rg = tid / CG, r0 = rg * RPT, wave = tid / 64;
+    const uint32_t H32 = (uint32_t)a.H;  // rows = B * H < 2^31
+    __shared__ f32x4 redp[2][WAVES][CG], redo[2][WAVES][CG];
+    auto fetch = [&](f32x4 (&st)[RPT], uint32_t row) {
+        if (!a.s0) {
+#pragma unroll
+            for (int m = 0; m < RPT; ++m) st[m] = zero4();
+            return;
+        }
+        const float* sin = a.s0 + (int64_t)row * (DK * DV) + (int64_t)r0 * DV + 4 * cg;
+#pragma unroll
+        for (int m = 0; m < RPT; ++m) st[m] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sin + m * DV));
+    };
+    uint32_t row = blockIdx.x;
+    f32x4 cur[RPT];
+    fetch(cur, row);
+    for (int buf = 0; row < rows; row += gridDim.x, buf ^= 1) {
+        const int64_t b = row / H32, h = row % H32;
+        DVec4<TIO> q4[RPT / 4], k4[RPT / 4], v4;
+        DVec4<TG> g4[RPT / 4];
+        {
+            const DVec4<TIO>* qp = reinterpret_cast<const DVec4<TIO>*>(reinterpret_cast<const TIO*>(a.q) + b * a.q_sb + h * a.q_sh + r0);
+            const DVec4<TIO>* kp = reinterpret_cast<const DVec4<TIO>*>(reinterpret_cast<const TIO*>(a.k) + b * a.k_sb + h * a.k_sh + r0);
+            const DVec4<TG>* gp = reinterpret_cast<const DVec4<TG>*>(reinterpret_cast<const TG*>(a.g) + b * a.g_sb + h * a.g_sh + r0);
+#pragma unroll
+            for (int i = 0; i < RPT / 4; ++i) {
+                q4[i] = qp[i];
+                k4[i] = kp[i];
+                g4[i] = gp[i];
+            }
+            v4 = *reinterpret_cast<const DVec4<TIO>*>(reinterpret_cast<const TIO*>(a.v) + b * a.v_sb + h * a.v_sh + 4 * cg);
+        }
+        const float* bp = reinterpret_cast<const float*>(a.beta) + b * a.b_sb + h * a.b_sh;
+        float bh = 1.f;
+        f32x4 bkr[RPT / 4], bvc = f32x4{1.f, 1.f, 1.f, 1.f};
+        if constexpr (BK == BETA_HEAD) bh = bp[0];
+        if constexpr (BK == BETA_KEY) {
+#pragma unroll
+            for (int i = 0; i < RPT / 4; ++i) bkr[i] = reinterpret_cast<const f32x4*>(bp + r0)[i];
+        }
+        if constexpr (BK == BETA_VALUE) bvc = *reinterpret_cast<const f32x4*>(bp + 4 * cg);
+        // prediction S^T k for this thread's four columns
+        float p4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < RPT; ++m) {
+            const float km = (float)k4[m / 4][m % 4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) p4[c] += km * cur[m][c];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) p4[c] = xor_group_sum<CG>(p4[c]);
+        if ((tid % 64) < CG) redp[buf][wave][cg] = f32x4{p4[0], p4[1], p4[2], p4[3]};
+        __syncthreads();
+        f32x4 pred = redp[buf][0][cg];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) pred += redp[buf][w][cg];
+        float y[4];  // the written values u (beta per value column: beta (.) u)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = bvc[c] * ((float)v4[c] - pred[c]);
+        f32x4 ns[RPT];
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = 0; m < RPT; ++m) {
+            const float d = expf(fminf((float)g4[m / 4][m % 4], 0.f));
+            float wm = (float)k4[m / 4][m % 4];
+            if constexpr (BK == BETA_HEAD) wm *= bh;
+            if constexpr (BK == BETA_KEY) wm *= bkr[m / 4][m % 4];
+            const float qm = (float)q4[m / 4][m % 4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                ns[m][c] = d * cur[m][c] + wm * y[c];
+                o4[c] += qm * ns[m][c];
+            }
+        }
+        const uint32_t nrow = row + gridDim.x;
+        if (nrow < rows) fetch(cur, nrow);
+        if (a.s_final) {
+            float* sout = a.s_final + (int64_t)row * (DK * DV) + (int64_t)r0 * DV + 4 * cg;
+#pragma unroll
+            for (int m = 0; m < RPT; ++m) __builtin_nontemporal_store(ns[m], reinterpret_cast<f32x4*>(sout + m * DV));
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o4[c] = xor_group_sum<CG>(o4[c]);
+        if ((tid % 64) < CG) redo[buf][wave][cg] = f32x4{o4[0], o4[1], o4[2], o4[3]};
+        __syncthreads();
+        if (tid < CG) {
+            f32x4 sum = redo[buf][0][cg];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) sum += redo[buf][w][cg];
+            const int64_t off = b * a.o_sb + h * a.o_sh + 4 * cg;
+            store4_dt(reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt), a.o_dt, sum[0], sum[1], sum[2], sum[3]);
+        }
+    }
+}
+
+// 256 threads: 4 rows per thread at D = 64, 16 at D = 128 (as the GLA decode step).
+template <int D, typename TIO, typename TG, int BK>
+static hipError_t launch_gdn_decode_t(const GdnParams& a, int max_blocks, hipStream_t stream) {
+    constexpr int RPT = (D * D / (4 * 256)) > 4 ? (D * D / (4 * 256)) : 4;
+    constexpr int TPB = D * D / (4 * RPT);
+    const uint32_t rows = (uint32_t)(a.B * a.H);
+    const uint32_t blocks = rows < (uint32_t)max_blocks ? rows : (uint32_t)max_blocks;
+    hipLaunchKernelGGL((gdn_decode_kernel<D, D, RPT, TIO, TG, BK>), dim3(blocks), dim3(TPB), 0, stream, a, rows);
+    return hipGetLastError();
+}
+
+template <int D, typename TIO, typename TG>
+static hipError_t launch_gdn_decode_b(const GdnParams& a, int max_blocks, hipStream_t stream) {
+    switch (a.beta_kind) {
+        case BETA_HEAD: return launch_gdn_decode_t<D, TIO, TG, BETA_HEAD>(a, max_blocks, stream);
+        case BETA_KEY: return launch_gdn_decode_t<D, TIO, TG, BETA_KEY>(a, max_blocks, stream);
+        case BETA_VALUE: return launch_gdn_decode_t<D, TIO, TG, BETA_VALUE>(a, max_blocks, stream);
+        default: return launch_gdn_decode_t<D, TIO, TG, BETA_NONE>(a, max_blocks, stream);
+    }
+}
+
+template <int D>
+static hipError_t launch_gdn_decode_d(const GdnParams& a, int max_blocks, hipStream_t stream) {
+    const bool g32 = a.g_dt == DT_F32;
+    if (a.io_dt == DT_BF16) {
+        if (g32) return launch_gdn_decode_b<D, __bf16, float>(a, max_blocks, stream);
+        if (a.g_dt == DT_BF16) return launch_gdn_decode_b<D, __bf16, __bf16>(a, max_blocks, stream);
+    } else if (a.io_dt == DT_F16) {
+        if (g32) return launch_gdn_decode_b<D, _Float16, float>(a, max_blocks, stream);
+        if (a.g_dt == DT_F16) return launch_gdn_decode_b<D, _Float16, _Float16>(a, max_blocks, stream);
+    } else if (a.io_dt == DT_F32 && g32) {
+        return launch_gdn_decode_b<D, float, float>(a, max_blocks, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gdn_decode(const GdnParams& a, int D, int max_blocks, hipStream_t stream) {
+    if (D == 64) return launch_gdn_decode_d<64>(a, max_blocks, stream);
+    if (D == 128) return launch_gdn_decode_d<128>(a, max_blocks, stream);
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t stream) {
     if (Dk == 64 && Dv == 64) return launch_gdn_t<64, 64, 8>(a, stream);
     if (Dk == 128 && Dv == 128) return launch_gdn_t<128, 128, 8>(a, stream);

@@ -177,6 +177,8 @@ hipError_t launch_gla_fused_decode(const FusedDecodeParams& a, int HD, int io_dt
                                    hipStream_t stream);
 hipError_t launch_gla_decode(const DecodeParams& a, int Dk, int Dv, int max_blocks, hipStream_t stream);
 hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t stream);
+// T == 1 of many rows (Dk = Dv = D in {64, 128}; q, k, g, v rows and beta vector-aligned, beta fp32)
+hipError_t launch_gdn_decode(const GdnParams& a, int D, int max_blocks, hipStream_t stream);
 // Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).
 hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);

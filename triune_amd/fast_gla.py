@@ -646,8 +646,8 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
         bp = beta
         if beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE):
             bp = _pad_last(beta, D)
-        if chunked and beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE):
-            bp = bp.to(torch.float32)
+        if (chunked and beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE)) or T == 1:
+            bp = bp.to(torch.float32)  # the per-dim chunked kernels and the decode step read fp32
         bp = bp.contiguous()
         bst = (bp.stride(0), bp.stride(1), bp.stride(2))
     o = torch.empty(B, T, H, D, device=q.device, dtype=out_dtype or v.dtype)
