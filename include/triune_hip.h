@@ -325,6 +325,18 @@ int triune_hip_gla_fused_decode_step(const void* qkvg, int io_dtype, const int64
                                      void* state_out, int state_dtype, void* o, int o_dtype,
                                      const int64_t* o_strides, int64_t B, int64_t H, int HD, void* stream);
 
+/* The same fused decode step over a state pool, in place: state_pool [n_slots, H, HD, HD] in
+ * state_dtype (16-byte aligned for fp32, 8 for 16-bit), and batch row b reads and writes pool row
+ * slots[b] (int32, device); a slot outside [0, n_slots) (a padded batch row) reads no state,
+ * stores none and outputs zeros.  Other arguments as triune_hip_gla_fused_decode_step.
+ * Replaces: _fused_qkvg_decode_step_kernel (triune/model/attention.py:81-179) on a serving
+ * pool's rows, the per-session cache of triune/api/srsm.py:11-112 kept on the device. */
+int triune_hip_gla_fused_decode_step_slots(const void* qkvg, int io_dtype, const int64_t* strides, const void* cos,
+                                           const void* sin, int cs_dtype, int use_rope, void* state_pool,
+                                           int state_dtype, const int32_t* slots, int64_t n_slots, void* o,
+                                           int o_dtype, const int64_t* o_strides, int64_t B, int64_t H, int HD,
+                                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -171,6 +171,23 @@ def test_decode_and_gdn_and_scan_validation_errors():
     assert sb(None, 0, _FAKE, 7, _FAKE, 0, _FAKE, _FAKE, _FAKE, _FAKE, 0, 1, 1, 4, 8, 8, None) == -3
 
 
+def test_fused_decode_pool_validation():
+    """The pool form of the fused decode step: slots and the pool are required, sizes checked
+    before any launch (no GPU call is made on these paths)."""
+    lib = L.lib()
+    f = lib.triune_hip_gla_fused_decode_step_slots
+    st = (ctypes.c_int64 * 3)(4 * 3 * 64, 3 * 64, 64)
+    ost = (ctypes.c_int64 * 2)(3 * 64, 64)
+    args = lambda pool, slots, n, hd, sdt=0: (_FAKE, 1, st, None, None, 0, 0, pool, sdt, slots, n, _FAKE, 1, ost,  # noqa: E731
+                                              2, 3, hd, None)
+    assert f(*args(None, _FAKE, 4, 64)) == -1
+    assert f(*args(_FAKE, None, 4, 64)) == -1
+    assert f(*args(_FAKE, _FAKE, -1, 64)) == -2
+    assert f(*args(_FAKE, _FAKE, 4, 48)) == -2
+    assert f(*args(_FAKE, _FAKE, 4, 64, sdt=2)) == -3  # fp16 state with bf16 I/O
+    assert f(*args(ctypes.c_void_p(0x1008), _FAKE, 4, 64)) == -4  # fp32 pool not 16-byte aligned
+
+
 def test_noalloc_prefill_validation():
     """The allocation-free prefill fails before any launch on bad arguments, and with
     TRIUNE_ERR_SCRATCH when the workspace would exceed its static scratch."""

@@ -6,7 +6,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from triune_amd import fast_chunk_gla, fused_qkv_g_prep_inplace, fused_qkvg_decode_step
+from triune_amd import fast_chunk_gla, fused_qkv_g_prep_inplace, fused_qkvg_decode_step, fused_qkvg_decode_step_pool
 from triune_amd.workloads import ulp_bf16
 
 pytestmark = pytest.mark.gpu
@@ -115,6 +115,37 @@ def test_fused_decode_matches_oracle(dev, HD, state):
         else:
             ok, err = _within_ulp(fin, rs, slack=1e-6)
             assert ok, err
+
+
+@pytest.mark.parametrize("HD", [32, 64, 128])
+def test_fused_decode_pool_rows(dev, HD):
+    """The fused decode step on rows of an fp32 state pool, in place: rows with a slot in the pool
+    equal the dense step on the gathered states (bitwise: the same arithmetic) and the fp64 oracle;
+    a padded row (slot -1) and a slot past the pool output zeros and touch no state; the other pool
+    rows stay as they were."""
+    gen = torch.Generator().manual_seed(HD + 7)
+    B, H, n_slots = 5, 3, 7
+    qkvg = torch.randn(B, 4, H, HD, generator=gen).bfloat16()
+    pool0 = 0.1 * torch.randn(n_slots, H, HD, HD, generator=gen)
+    cos, sin = _tables(1, HD, offset=9)
+    slots = torch.tensor([3, 0, 6, -1, 9], dtype=torch.int32)
+    pool = pool0.to(dev)
+    out = fused_qkvg_decode_step_pool(qkvg.to(dev), pool, slots.to(dev), cos.to(dev), sin.to(dev))
+    valid = [0, 1, 2]
+    dense_in = pool0[slots[valid].long()]
+    dout, dfin = fused_qkvg_decode_step(qkvg[valid].to(dev), cos.to(dev), sin.to(dev), initial_state=dense_in.to(dev),
+                                        state_dtype=torch.float32)
+    torch.cuda.synchronize()
+    out, pool = out.cpu(), pool.cpu()
+    assert torch.equal(out[valid], dout.cpu())
+    assert torch.equal(pool[slots[valid].long()], dfin.cpu())
+    assert torch.count_nonzero(out[3:]) == 0
+    untouched = [i for i in range(n_slots) if i not in (3, 0, 6)]
+    assert torch.equal(pool[untouched], pool0[untouched])
+    ro, rs = O.fused_decode_step(qkvg[valid], cos[0], sin[0], dense_in.double())
+    ok, err = _within_ulp(out[valid, 0], ro, slack=1e-4)
+    assert ok, err
+    assert float(np.abs(pool[slots[valid].long()].numpy() - rs).max()) <= 1e-5
 
 
 def test_fused_decode_fp32_no_rope_no_save(dev):

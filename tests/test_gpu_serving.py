@@ -72,6 +72,32 @@ def test_pool_prefill_then_decode_matches_oracle(dev):
         assert e_pre <= 1e-5 and e_dec <= 1e-5 and e_s <= 1e-5
 
 
+def test_pool_fused_decode_step_counts_and_updates(dev):
+    """StateSlotPool.fused_decode_step: the slots' states advance in place through the fused
+    pre-processing decode step (equal to the dense step on the gathered states) and each session's
+    token offset grows by one."""
+    from triune_amd import fused_qkvg_decode_step
+
+    gen = torch.Generator().manual_seed(31)
+    H, HD, L = 2, 64, 2
+    pool = StateSlotPool(num_layers=L, n_slots=6, H=H, Dk=HD, Dv=HD, device=dev)
+    slots = pool.slots_tensor(["a", "b", "c"])
+    for layer in range(L):
+        pool.states[layer].copy_(0.1 * torch.randn(pool.states[layer].shape, generator=gen).to(dev))
+    before = pool.states[1].clone()
+    off0 = pool.offsets[1].clone()
+    qkvg = torch.randn(3, 4, H, HD, generator=gen).bfloat16().to(dev)
+    ang = torch.arange(HD // 2, dtype=torch.float32) * 0.01
+    cos = torch.cos(torch.cat([ang, ang])).to(dev)
+    sin = torch.sin(torch.cat([ang, ang])).to(dev)
+    o = pool.fused_decode_step(1, qkvg, slots, cos, sin)
+    do, dfin = fused_qkvg_decode_step(qkvg, cos, sin, initial_state=before[slots.long()], state_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(o, do)
+    assert torch.equal(pool.states[1][slots.long()], dfin)
+    assert torch.equal((pool.offsets[1] - off0)[slots.long()].cpu(), torch.ones(3, dtype=pool.offsets.dtype))
+
+
 @pytest.mark.parametrize("steps", [1, 4])
 def test_graph_runner_replays_match_eager(dev, steps):
     """Each replay (with fresh inputs written between replays, eager work and syncs in between)

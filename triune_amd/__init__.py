@@ -14,7 +14,8 @@ from .fast_gla import (
     gla_decode_step,
 )
 from .gla import gated_deltanet, gla
-from .gla_prep import fused_qkv_g_prep_chunk_gla, fused_qkv_g_prep_inplace, fused_qkvg_decode_step
+from .gla_prep import (fused_qkv_g_prep_chunk_gla, fused_qkv_g_prep_inplace, fused_qkvg_decode_step,
+                       fused_qkvg_decode_step_pool)
 
 __all__ = [
     "FusedRecurrentScan",
@@ -26,6 +27,7 @@ __all__ = [
     "fused_qkv_g_prep_chunk_gla",
     "fused_qkv_g_prep_inplace",
     "fused_qkvg_decode_step",
+    "fused_qkvg_decode_step_pool",
     "gated_deltanet",
     "gla",
     "gla_decode_step",

@@ -95,6 +95,10 @@ def _bind(lib):
             [_vp, _i, _i64p, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _i64p, _i64, _i64, _i, _vp],
             _i,
         ),
+        "triune_hip_gla_fused_decode_step_slots": (
+            [_vp, _i, _i64p, _vp, _vp, _i, _i, _vp, _i, _vp, _i64, _vp, _i, _i64p, _i64, _i64, _i, _vp],
+            _i,
+        ),
         "triune_hip_gdn_prefill_chunked_workspace_size": ([_i64, _i64, _i64, _i, _i], _sz),
         "triune_hip_gdn_prefill_chunked": (
             [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _vp, _sz,
@@ -142,6 +146,7 @@ EXPORTS = (
     "triune_hip_gdn_prefill_scalar_decay",
     "triune_hip_gla_qkvg_prep",
     "triune_hip_gla_fused_decode_step",
+    "triune_hip_gla_fused_decode_step_slots",
 )
 
 

@@ -974,4 +974,35 @@ int triune_hip_gla_fused_decode_step(const void* qkvg, int io_dtype, const int64
         launch_gla_fused_decode(a, HD, io_dtype, use_rope ? cs_dtype : TRIUNE_DT_F32, state_dtype, (hipStream_t)stream));
 }
 
+int triune_hip_gla_fused_decode_step_slots(const void* qkvg, int io_dtype, const int64_t* strides, const void* cos,
+                                           const void* sin, int cs_dtype, int use_rope, void* state_pool,
+                                           int state_dtype, const int32_t* slots, int64_t n_slots, void* o,
+                                           int o_dtype, const int64_t* o_strides, int64_t B, int64_t H, int HD,
+                                           void* stream) {
+    if (!qkvg || !strides || !o || !o_strides || !state_pool || !slots || (use_rope && (!cos || !sin)))
+        return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(o_dtype) || !dtype_ok(state_dtype)) return TRIUNE_ERR_DTYPE;
+    if (state_dtype != TRIUNE_DT_F32 && state_dtype != io_dtype) return TRIUNE_ERR_DTYPE;
+    if (use_rope && cs_dtype != TRIUNE_DT_F32 && cs_dtype != io_dtype) return TRIUNE_ERR_DTYPE;
+    if (B < 0 || H <= 0 || n_slots < 0 || (HD != 32 && HD != 64 && HD != 128)) return TRIUNE_ERR_SHAPE;
+    if (B > 0x7fffffff / H || n_slots > 0x7fffffff / H) return TRIUNE_ERR_SHAPE;
+    if (B == 0) return TRIUNE_OK;
+    const int sal = state_dtype == TRIUNE_DT_F32 ? 16 : 8;
+    if (reinterpret_cast<uintptr_t>(state_pool) % sal || reinterpret_cast<uintptr_t>(slots) % 4 ||
+        !vec4_ok(o, o_dtype, o_strides, 2) || !vec4_ok(qkvg, io_dtype, strides, 3))
+        return TRIUNE_ERR_LAYOUT;
+    if (use_rope && (!vec4_ok(cos, cs_dtype, strides, 0) || !vec4_ok(sin, cs_dtype, strides, 0)))
+        return TRIUNE_ERR_LAYOUT;
+    FusedDecodeParams a{};
+    a.qkvg = qkvg; a.x_sb = strides[0]; a.x_sp = strides[1]; a.x_sh = strides[2];
+    a.cos = cos; a.sin = sin; a.use_rope = use_rope ? 1 : 0;
+    a.has_init = 1; a.save_final = 1;
+    a.state_in = state_pool; a.state_out = state_pool;
+    a.slots = slots; a.n_state_rows = n_slots;
+    a.o = o; a.o_dt = o_dtype; a.o_sb = o_strides[0]; a.o_sh = o_strides[1];
+    a.B = B; a.H = H; a.max_blocks = 4 * device_cus();
+    return launch_status(
+        launch_gla_fused_decode(a, HD, io_dtype, use_rope ? cs_dtype : TRIUNE_DT_F32, state_dtype, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -148,9 +148,16 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
     const int cg = tid % CG, rg = tid / CG, r0 = rg * RPT;
     const uint32_t H32 = (uint32_t)a.H;
     const int32_t voff = (r0 * HD + 4 * cg) * SB;  // this thread's first state element in a row
-    auto row_rsrc = [&](const void* p, uint32_t row, bool on) {
-        char* base = reinterpret_cast<char*>(const_cast<void*>(p)) + (int64_t)row * HD * HD * SB;
+    auto row_rsrc = [&](const void* p, int64_t srow, bool on) {
+        char* base = reinterpret_cast<char*>(const_cast<void*>(p)) + (on ? srow : 0) * HD * HD * SB;
         return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, on ? HD * HD * SB : 0, 0x00020000);
+    };
+    // State row of (b, h): row itself, or through the pool's slots (-1: b's slot lies outside the
+    // pool, a padded batch row; its buffer resources then hold no records).
+    auto state_row = [&](uint32_t row) -> int64_t {
+        if (!a.slots) return (int64_t)row;
+        const int64_t sl = (int64_t)a.slots[row / H32];
+        return (sl >= 0 && sl < a.n_state_rows) ? sl * a.H + row % H32 : -1;
     };
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -158,7 +165,8 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
         u32x4 w[RPT];  // 16-bit states use the first two words
     };
     auto fetch = [&](Raw& x, uint32_t row) {
-        const auto r = row_rsrc(a.state_in, row, a.has_init != 0);
+        const int64_t sr = state_row(row);
+        const auto r = row_rsrc(a.state_in, sr, a.has_init != 0 && sr >= 0);
 #pragma unroll
         for (int m = 0; m < RPT; ++m) {
             if constexpr (SB == 4) {
@@ -298,7 +306,8 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
                 o4[c] += qv[m] * y[m][c];
             }
         }
-        const auto ro = row_rsrc(a.state_out, row, a.save_final != 0);
+        const int64_t sr = state_row(row);
+        const auto ro = row_rsrc(a.state_out, sr, a.save_final != 0 && sr >= 0);
 #pragma unroll
         for (int m = 0; m < RPT; ++m) {
             if constexpr (SB == 4) {
@@ -323,6 +332,7 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
             f32x4 s = red[buf][0][cg];
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) s += red[buf][w][cg];
+            if (sr < 0) s = zero4();
             store4_dt(reinterpret_cast<char*>(a.o) + (b * a.o_sb + h * a.o_sh + 4 * cg) * dt_size(a.o_dt), a.o_dt, s[0],
                       s[1], s[2], s[3]);
         }

@@ -165,6 +165,10 @@ struct FusedDecodeParams {
     int64_t o_sb, o_sh;
     int64_t B, H;
     int max_blocks;  // grid cap (blocks then walk several rows)
+    // Optional state pool: row (b, h) reads and writes state row slots[b] * H + h of state_in /
+    // state_out; a slot outside [0, n_state_rows) reads no state, stores none and outputs zeros.
+    const int32_t* slots;
+    int64_t n_state_rows;
 };
 
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);

@@ -26,7 +26,8 @@ import torch
 
 from ._lib import check, dtype_code, lib, ptr, stream_of, strides
 
-__all__ = ["fused_qkv_g_prep_inplace", "fused_qkvg_decode_step", "fused_qkv_g_prep_chunk_gla"]
+__all__ = ["fused_qkv_g_prep_inplace", "fused_qkvg_decode_step", "fused_qkvg_decode_step_pool",
+           "fused_qkv_g_prep_chunk_gla"]
 
 _HD = (32, 64, 128)
 
@@ -125,6 +126,52 @@ def fused_qkvg_decode_step(qkvg: torch.Tensor, cos=None, sin=None, initial_state
     )
     check(rc, "triune_hip_gla_fused_decode_step")
     return out, s_out
+
+
+def fused_qkvg_decode_step_pool(qkvg: torch.Tensor, state_pool: torch.Tensor, slots: torch.Tensor, cos=None, sin=None,
+                                use_rope: bool = True, out=None):
+    """fused_qkvg_decode_step on rows of a state pool, in place (the decode half of serving with a
+    device-resident session cache): state_pool [n_slots, H, HD, HD] contiguous, float32 or
+    qkvg.dtype; slots: int32 [B] on the device, batch row b updating pool row slots[b].  A slot
+    outside [0, n_slots) (a padded batch row) reads no state, stores none and outputs zeros.
+    Returns the output [B, 1, H, HD] in qkvg.dtype."""
+    _cuda(qkvg, cos, sin, state_pool, slots)
+    if qkvg.dim() != 4 or qkvg.shape[1] != 4:
+        raise ValueError("qkvg must be [B, 4, H, HD]")
+    B, _, H, HD = qkvg.shape
+    if HD not in _HD:
+        raise ValueError(f"head dim {HD} not supported (32, 64 or 128)")
+    if qkvg.stride(-1) != 1:
+        raise ValueError("the head dim of qkvg must be contiguous")
+    if state_pool.dim() != 4 or tuple(state_pool.shape[1:]) != (H, HD, HD) or not state_pool.is_contiguous():
+        raise ValueError(f"state_pool must be a contiguous [n_slots, {H}, {HD}, {HD}] tensor")
+    if state_pool.dtype not in (torch.float32, qkvg.dtype):
+        raise TypeError("the state dtype must be float32 or the dtype of qkvg")
+    if slots.dtype != torch.int32 or slots.dim() != 1 or slots.numel() != B:
+        raise ValueError("slots must be an int32 [B] tensor")
+    slots = slots.contiguous()
+    cs_dt = 0
+    if use_rope:
+        if cos is None or sin is None:
+            raise ValueError("use_rope needs cos and sin")
+        cos, sin = cos.reshape(-1), sin.reshape(-1)
+        if cos.numel() != HD or sin.numel() != HD or cos.dtype != sin.dtype:
+            raise ValueError("cos and sin must hold HD values of one dtype")
+        cos, sin = cos.contiguous(), sin.contiguous()
+        cs_dt = dtype_code(cos)
+    if out is None:
+        out = torch.empty(B, 1, H, HD, device=qkvg.device, dtype=qkvg.dtype)
+    if tuple(out.shape) != (B, 1, H, HD) or out.stride(-1) != 1:
+        raise ValueError("out must be [B, 1, H, HD] with a contiguous head dim")
+    ov = out[:, 0]
+    rc = lib().triune_hip_gla_fused_decode_step_slots(
+        ptr(qkvg), dtype_code(qkvg), strides(qkvg.stride()[:3]), ptr(cos) if use_rope else None,
+        ptr(sin) if use_rope else None, cs_dt, 1 if use_rope else 0, ptr(state_pool), dtype_code(state_pool),
+        ptr(slots), state_pool.shape[0], ptr(ov), dtype_code(ov), strides(ov.stride()[:2]), B, H, HD,
+        stream_of(qkvg),
+    )
+    check(rc, "triune_hip_gla_fused_decode_step_slots")
+    return out
 
 
 def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin=None, initial_state=None, out=None,

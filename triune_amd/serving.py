@@ -27,6 +27,7 @@ from typing import Any, Dict, List, Optional, Tuple
 import torch
 
 from .fast_gla import _DECODE_PAIRS, fast_chunk_gla_varlen, gla_decode_step
+from .gla_prep import fused_qkvg_decode_step_pool
 
 __all__ = [
     "parse_cache",
@@ -244,6 +245,16 @@ class StateSlotPool:
     def decode_step(self, layer: int, q, k, v, g, slots: torch.Tensor, out=None, count_tokens: bool = True):
         """One token for each of len(slots) sessions; states updated in place in their slots."""
         o, _ = gla_decode_step(q, k, v, g, self.states[layer], out=out, inplace=True, slots=slots)
+        if count_tokens:
+            self._count(layer, slots, torch.ones_like(slots, dtype=torch.int64))
+        return o
+
+    def fused_decode_step(self, layer: int, qkvg, slots: torch.Tensor, cos=None, sin=None, use_rope: bool = True,
+                          out=None, count_tokens: bool = True):
+        """decode_step from raw projections (qkvg [B, 4, H, HD]): VectorisedGLA's fused decode
+        (attention.py:81-179; ELU+1, L2 norm, RoPE, logsigmoid, then the update) on the slots'
+        states, in place."""
+        o = fused_qkvg_decode_step_pool(qkvg, self.states[layer], slots, cos, sin, use_rope=use_rope, out=out)
         if count_tokens:
             self._count(layer, slots, torch.ones_like(slots, dtype=torch.int64))
         return o
