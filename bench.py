@@ -376,6 +376,35 @@ def bench_gdn(dev, reps=20):
                              "frac": round(alg_dim / (ms_dim * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
+def bench_gdn_bwd(dev, reps=3):
+    """Gated DeltaNet backward, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta, one decay
+    per token and head, zero initial state): the gradients of q, k, v, g and beta for an upstream
+    gradient of o, as fast_chunk_gated_deltanet's autograd returns them (the reference
+    differentiates its PyTorch recurrence, fast_gla.py:885-904)."""
+    from triune_amd import _lib
+    from triune_amd.fast_gla import _gdn_bwd
+    from triune_amd.workloads import config3, to_device
+
+    q, k, v, g, beta = config3()
+    q, k, v, beta = (x.to(dev) for x in (q, k, v, beta))
+    g = to_device(g, dev)
+    B, T, H, D = q.shape
+    do = torch.randn(B, T, H, D, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).to(dev)
+    fn = lambda: _gdn_bwd(q, k, v, g, beta, None, _lib.BETA_HEAD, do, None)  # noqa: E731
+    fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    # q, k, v, do read and dq, dk, dv, dg written ([B, T, H, D] bf16), the gate read per (token,
+    # head) and materialised per key dim by the call, beta read and its gradient written
+    alg = B * T * H * (8 * D * 2 + D * 2 + 2 + 2)
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "Gated DeltaNet backward, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta)",
+            "ms": round(ms, 3), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "kernels": "gdn_ckpt + gdn_bwd + gdn_slice_sum (token-serial, states recomputed from checkpoints)",
+            "roofline": {"bound": "latency (token-serial)", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def bench_gdn128(dev, reps=10):
     """Gated DeltaNet prefill as the reference model calls it at its default head dim
     (triune/model/attention.py:509-536, config.py GLA_HEAD_DIM = 128): q, k = normalize(elu(x) + 1),
@@ -629,7 +658,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "gdn_decode", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
+        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "gdn_decode", "gdn_bwd", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -658,6 +687,7 @@ def main():
             res = bench_fused_decode(args.decode_steps, dev)
         else:
             res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "gdn_vbeta": bench_gdn_vbeta, "gdn_decode": bench_gdn_decode,
+                   "gdn_bwd": bench_gdn_bwd,
                    "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
                    "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)

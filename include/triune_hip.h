@@ -41,6 +41,10 @@
  *   triune_hip_gdn_prefill_chunked <- the same operator (fast_gla.py:839-904), chunked form
  *   triune_hip_gdn_prefill_scalar_decay <- the same operator with g broadcast over the head dim
  *                                     (one decay per token and head), chunked form
+ *   triune_hip_gdn_bwd             <- the gradients of fast_chunk_gated_deltanet's training path:
+ *                                     autograd through fast_recurrent_gated_deltanet
+ *                                     (triune/kernels/fast_gla.py:781-836), which the operator runs
+ *                                     whenever a gradient is needed (fast_gla.py:885-904)
  *   triune_hip_gla_qkvg_prep       <- _fused_qkv_g_prep_inplace_kernel, triune/model/attention.py:14-79
  *   triune_hip_gla_fused_decode_step <- _fused_qkvg_decode_step_kernel, triune/model/attention.py:81-179
  */
@@ -299,6 +303,24 @@ int triune_hip_gdn_prefill_scalar_decay(const void* q, const void* k, const void
                                         const int64_t* strides, const float* s0, void* o, int o_dtype,
                                         float* s_final, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
                                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* Gradients of the Gated DeltaNet recurrence above (triune_hip_gdn_prefill's arithmetic, from s0)
+ * for the upstream gradients dout (o's, [B, T, H, Dv] in dout_dtype, NULL = zero) and ds_final
+ * (fp32 [B, H, Dk, Dv], NULL = zero).  strides[18] = (batch, token, head) element strides of q, k,
+ * v, g, beta, dout.  Outputs, contiguous: dq, dk, dv [B, T, H, D] in io_dtype, dg [B, T, H, D] in
+ * g_dtype (zero where g > 0: the clamp passes no gradient there), dbeta in beta_dtype ([B, T, H]
+ * for TRIUNE_BETA_HEAD, [B, T, H, D] for KEY and VALUE), ds0 fp32 [B, H, D, D] or NULL.  Dk == Dv
+ * in {64, 128}; q, k, v, g, dout (and a per-dim beta) rows 16-byte aligned.  Arithmetic in fp32:
+ * the states are recomputed token by token from checkpoints.  workspace: at least
+ * triune_hip_gdn_bwd_workspace_size(B, T, H, Dk, Dv, beta_kind) bytes, 16-byte aligned.
+ * Replaces: autograd through fast_recurrent_gated_deltanet (fast_gla.py:781-836), the path
+ * fast_chunk_gated_deltanet takes when a gradient is needed (fast_gla.py:885-904). */
+size_t triune_hip_gdn_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int beta_kind);
+int triune_hip_gdn_bwd(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                       const void* beta, int beta_dtype, int beta_kind, const int64_t* strides, const float* s0,
+                       const void* dout, int dout_dtype, const float* ds_final, void* dq, void* dk, void* dv,
+                       void* dg, void* dbeta, float* ds0, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* GLA input pre-processing in place (VectorisedGLA's fused path): for every (b, t, h) row of HD
  * elements, q and k <- RoPE(normalize(elu(x) + 1)) with normalize(a) = a / sqrt(max(sum a^2,

@@ -391,6 +391,111 @@ ORACLE_API void oracle_gdn_fwd(const double* q, const double* k, const double* v
     }
 }
 
+/* Gradients of oracle_gdn_fwd for upstream gradients do [B,T,H,Dv] and ds_fin [B,H,Dk,Dv] (NULL =
+ * zero): the reference differentiates fast_recurrent_gated_deltanet (fast_gla.py:781-836) with
+ * autograd whenever a gradient is needed (fast_chunk_gated_deltanet, fast_gla.py:885-904).  With
+ * P = S_{t-1}, a = exp(min(g_t, 0)), W = w uu^T where w_i = rs_i k_i, uu_j = cs_j u_j (rs, cs the
+ * row and column beta factors, 1 where the kind has none), and D the gradient reaching S_t:
+ *   D += q do^T ;  dq_i = sum_j S_t[i][j] do_j
+ *   c_j = sum_i D[i][j] w_i ;  du_j = cs_j c_j ;  dv_j = du_j ;  dpred_j = -du_j
+ *   e_i = sum_j D[i][j] uu_j ;  dk_i = rs_i e_i + sum_j P[i][j] dpred_j
+ *   dbeta: head sum_j u_j c_j ; key k_i e_i ; value u_j c_j
+ *   dg_i = a_i sum_j D[i][j] P[i][j] where g_i <= 0 (torch.clamp(max=0) passes its gradient
+ *          there), else 0
+ *   D <- diag(a) D + k dpred^T ;  ds0 = D after token 0.
+ * dbeta has beta's shape ([B,T,H] or [B,T,H,D]); every state is kept (test sizes). */
+ORACLE_API void oracle_gdn_bwd(const double* q, const double* k, const double* v, const double* g,
+                               const double* beta, int beta_kind, const double* s0, const double* dout,
+                               const double* dsf, double* dq, double* dk, double* dv, double* dg,
+                               double* dbeta, double* ds0, long B, long T, long H, int Dk, int Dv) {
+#pragma omp parallel for schedule(dynamic)
+    for (long bh = 0; bh < B * H; ++bh) {
+        long b = bh / H, h = bh % H;
+        long sk = H * Dk, sv = H * Dv;
+        const size_t DD = (size_t)Dk * Dv;
+        double* hist = (double*)malloc(sizeof(double) * DD * (size_t)(T + 1)); /* hist[t] = S_{t-1} */
+        double* U = (double*)malloc(sizeof(double) * (size_t)(T > 0 ? T : 1) * Dv); /* u_t */
+        double* D = (double*)malloc(sizeof(double) * DD);
+        double* c = (double*)malloc(sizeof(double) * (size_t)Dv);
+        double* dp = (double*)malloc(sizeof(double) * (size_t)Dv);
+        if (s0) memcpy(hist, s0 + bh * (long)DD, sizeof(double) * DD);
+        else memset(hist, 0, sizeof(double) * DD);
+#define RS(t, i) (beta_kind == 2 ? beta[(b * T + (t)) * sk + h * Dk + (i)] : 1.0)
+#define CS(t, j) (beta_kind == 1 ? beta[(b * T + (t)) * H + h] : beta_kind == 3 ? beta[(b * T + (t)) * sv + h * Dv + (j)] : 1.0)
+        for (long t = 0; t < T; ++t) {
+            const double* kt = k + (b * T + t) * sk + h * Dk;
+            const double* gt = g + (b * T + t) * sk + h * Dk;
+            const double* vt = v + (b * T + t) * sv + h * Dv;
+            const double* P = hist + (size_t)t * DD;
+            double* S = hist + (size_t)(t + 1) * DD;
+            double* u = U + t * Dv;
+            for (int j = 0; j < Dv; ++j) {
+                double pred = 0.0;
+                for (int i = 0; i < Dk; ++i) pred += kt[i] * P[(size_t)i * Dv + j];
+                u[j] = vt[j] - pred;
+            }
+            for (int i = 0; i < Dk; ++i) {
+                double a = exp(gt[i] > 0.0 ? 0.0 : gt[i]);
+                for (int j = 0; j < Dv; ++j)
+                    S[(size_t)i * Dv + j] = a * P[(size_t)i * Dv + j] + RS(t, i) * kt[i] * CS(t, j) * u[j];
+            }
+        }
+        for (size_t e = 0; e < DD; ++e) D[e] = dsf ? dsf[bh * (long)DD + e] : 0.0;
+        for (long t = T - 1; t >= 0; --t) {
+            const long ok = (b * T + t) * sk + h * Dk, ov = (b * T + t) * sv + h * Dv;
+            const double* qt = q + ok;
+            const double* kt = k + ok;
+            const double* gt = g + ok;
+            const double* dot = dout ? dout + ov : NULL;
+            const double* P = hist + (size_t)t * DD;
+            const double* S = hist + (size_t)(t + 1) * DD;
+            const double* u = U + t * Dv;
+            if (dot)
+                for (int i = 0; i < Dk; ++i)
+                    for (int j = 0; j < Dv; ++j) D[(size_t)i * Dv + j] += qt[i] * dot[j];
+            double dbh = 0.0;
+            for (int j = 0; j < Dv; ++j) {
+                double acc = 0.0;
+                for (int i = 0; i < Dk; ++i) acc += D[(size_t)i * Dv + j] * RS(t, i) * kt[i];
+                c[j] = acc;
+                const double du = CS(t, j) * acc;
+                dv[ov + j] = du;
+                dp[j] = -du;
+                dbh += u[j] * acc;
+                if (beta_kind == 3) dbeta[ov + j] = u[j] * acc;
+            }
+            if (beta_kind == 1) dbeta[(b * T + t) * H + h] = dbh;
+            for (int i = 0; i < Dk; ++i) {
+                double aq = 0.0, e = 0.0, f = 0.0, ag = 0.0;
+                for (int j = 0; j < Dv; ++j) {
+                    const size_t x = (size_t)i * Dv + j;
+                    if (dot) aq += S[x] * dot[j];
+                    e += D[x] * CS(t, j) * u[j];
+                    f += P[x] * dp[j];
+                    ag += D[x] * P[x];
+                }
+                const double a = exp(gt[i] > 0.0 ? 0.0 : gt[i]);
+                dq[ok + i] = aq;
+                dk[ok + i] = RS(t, i) * e + f;
+                dg[ok + i] = gt[i] <= 0.0 ? a * ag : 0.0;
+                if (beta_kind == 2) dbeta[ok + i] = kt[i] * e;
+            }
+            for (int i = 0; i < Dk; ++i) {
+                const double a = exp(gt[i] > 0.0 ? 0.0 : gt[i]);
+                for (int j = 0; j < Dv; ++j) D[(size_t)i * Dv + j] = a * D[(size_t)i * Dv + j] + kt[i] * dp[j];
+            }
+        }
+#undef RS
+#undef CS
+        if (ds0) memcpy(ds0 + bh * (long)DD, D, sizeof(double) * DD);
+        free(dp);
+        free(c);
+        free(D);
+        free(U);
+        free(hist);
+    }
+}
+
 ORACLE_API int oracle_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

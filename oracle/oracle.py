@@ -46,6 +46,7 @@ def _lib():
         lib.oracle_recurrent_scan_bwd.argtypes = [_dp] * 7 + [_L, _L, _L, _I, _I]
         lib.oracle_gla_bwd.argtypes = [_dp] * 12 + [_L, _L, _L, _I, _I, _L, _I]
         lib.oracle_gdn_fwd.argtypes = [_dp] * 5 + [_I, _dp, _dp, _dp, _L, _L, _L, _I, _I]
+        lib.oracle_gdn_bwd.argtypes = [_dp] * 5 + [_I] + [_dp] * 9 + [_L, _L, _L, _I, _I]
         lib.oracle_num_threads.restype = _I
         _LIB = lib
     return _LIB
@@ -184,6 +185,28 @@ def gdn_fwd(q, k, v, g, beta=None, s0=None, beta_kind=None):
     s = np.empty((B, H, Dk, Dv))
     _lib().oracle_gdn_fwd(_p(q), _p(k), _p(v), _p(g), _p(bt), kind, _p(s0), _p(o), _p(s), B, T, H, Dk, Dv)
     return o, s
+
+
+def gdn_bwd(q, k, v, g, beta=None, s0=None, do=None, ds_fin=None, beta_kind=None):
+    """Gradients of gdn_fwd (same beta conventions) for upstream do [B,T,H,Dv] and ds_fin
+    [B,H,Dk,Dv] (None = zero): the reference's autograd through fast_recurrent_gated_deltanet
+    (fast_gla.py:781-836), which fast_chunk_gated_deltanet runs whenever a gradient is needed
+    (:885-904).  Returns (dq, dk, dv, dg, dbeta or None, ds0)."""
+    q, k, v, g, s0, do, ds_fin = (_d(x) for x in (q, k, v, g, s0, do, ds_fin))
+    B, T, H, Dk = q.shape
+    Dv = v.shape[-1]
+    if beta is None:
+        kind, bt = BETA_NONE, None
+    else:
+        bt = _d(beta)
+        kind = BETA_HEAD if bt.ndim == 3 else (BETA_KEY if beta_kind is None else beta_kind)
+    dq, dk, dg = np.empty_like(q), np.empty_like(q), np.empty_like(q)
+    dv = np.empty_like(v)
+    db = None if bt is None else np.empty_like(bt)
+    ds0 = np.empty((B, H, Dk, Dv))
+    _lib().oracle_gdn_bwd(_p(q), _p(k), _p(v), _p(g), _p(bt), kind, _p(s0), _p(do), _p(ds_fin), _p(dq), _p(dk),
+                          _p(dv), _p(dg), _p(db), _p(ds0), B, T, H, Dk, Dv)
+    return dq, dk, dv, dg, db, ds0
 
 
 # ---------------------------------------------------------------------------------------

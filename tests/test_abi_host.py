@@ -221,6 +221,33 @@ def test_bwd_accumulate_flags_need_fp32_gradients():
     assert call(0, 0, L.FLAG_BWD_ACC_QKG | L.FLAG_BWD_ACC_V) == -5
 
 
+def test_gdn_bwd_validation():
+    """The Gated DeltaNet backward entry: square heads of 64 or 128, the gradient buffers and (with
+    a beta) its gradient required, rows vector-aligned; valid arguments stop at the workspace."""
+    lib = L.lib()
+    f = lib.triune_hip_gdn_bwd
+    st = (ctypes.c_int64 * 18)(*([64 * 64, 64, 64] * 6))
+
+    def call(bk=0, beta=None, db=None, dk=64, dv=64, dq=_FAKE, sts=st, ws=None):
+        return f(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, beta, 0, bk, sts, None, _FAKE, 1, None, dq, _FAKE, _FAKE, _FAKE,
+                 db, None, 1, 64, 1, dk, dv, ws, 0, None)
+
+    assert call() == -5  # valid, no workspace
+    assert call(dq=None) == -1
+    assert call(bk=1, beta=_FAKE) == -1  # beta without its gradient buffer
+    assert call(bk=1, beta=_FAKE, db=_FAKE) == -5
+    assert call(bk=4, beta=_FAKE, db=_FAKE) == -2
+    assert call(dk=32, dv=32) == -2
+    assert call(dk=128, dv=64) == -2
+    bad = (ctypes.c_int64 * 18)(*([64 * 64, 64, 64] * 6))
+    bad[16] = 60  # dout's token stride not a multiple of 8 elements
+    assert call(sts=bad) == -4
+    assert lib.triune_hip_gdn_bwd_workspace_size(4, 8192, 6, 64, 64, 0) > 0
+    assert lib.triune_hip_gdn_bwd_workspace_size(4, 8192, 6, 64, 64, 2) > lib.triune_hip_gdn_bwd_workspace_size(
+        4, 8192, 6, 64, 64, 0)
+    assert lib.triune_hip_gdn_bwd_workspace_size(4, 8192, 6, 48, 48, 0) == 0
+
+
 def test_workspace_sizes():
     lib = L.lib()
     w1 = lib.triune_hip_gla_prefill_workspace_size(4, 16384, 6, 64, 64, 0)

@@ -371,16 +371,24 @@ def test_varlen_equals_dense_batch(dev):
     assert float((sv - sd).abs().max()) <= 1e-4
 
 
-def test_gdn_refuses_gradients(dev):
-    """The GDN kernels are forward-only: a call that needs gradients raises instead of returning
-    outputs that silently carry none (the reference differentiates its PyTorch recurrence there)."""
-    q = torch.randn(1, 70, 2, 64, device=dev, requires_grad=True)
-    k, v = torch.randn(1, 70, 2, 64, device=dev), torch.randn(1, 70, 2, 64, device=dev)
-    g = -0.1 * torch.rand(1, 70, 2, 64, device=dev)
-    with pytest.raises(NotImplementedError):
-        fast_chunk_gated_deltanet(q, k, v, g)
+def test_gdn_gradients_only_where_requested(dev):
+    """A call that needs gradients goes through the autograd function (the reference
+    differentiates its PyTorch recurrence there): q's gradient matches the oracle, inputs that do
+    not require one get none; under no_grad the outputs carry no graph."""
+    gen = torch.Generator().manual_seed(70)
+    q, k = (torch.nn.functional.normalize(torch.randn(1, 70, 2, 64, generator=gen), dim=-1) for _ in range(2))
+    v = torch.randn(1, 70, 2, 64, generator=gen)
+    g = -0.1 * torch.rand(1, 70, 2, 64, generator=gen)
+    qd = q.to(dev).requires_grad_(True)
+    kd, vd, gd = k.to(dev), v.to(dev), g.to(dev)
+    o, s = fast_chunk_gated_deltanet(qd, kd, vd, gd)
+    assert o.requires_grad
+    o.sum().backward()
+    ref = O.gdn_bwd(q, k, v, g, None, None, torch.ones(1, 70, 2, 64), None)
+    assert float(np.abs(qd.grad.double().cpu().numpy() - ref[0]).max()) <= 1e-5 * max(1.0, np.abs(ref[0]).max())
+    assert kd.grad is None
     with torch.no_grad():
-        o, s = fast_chunk_gated_deltanet(q, k, v, g)
+        o, s = fast_chunk_gated_deltanet(qd, kd, vd, gd)
     assert o.shape == (1, 70, 2, 64) and not o.requires_grad
 
 

@@ -417,6 +417,92 @@ def test_gla_bwd_zero_gate_brute_force():
     np.testing.assert_allclose(ds0[0, 0], Q.T @ DO, atol=1e-12)
 
 
+def _torch_gdn(q, k, v, g, beta, s0, kind):
+    """fp64 restatement of the reference's fast_recurrent_gated_deltanet loop (fast_gla.py:811-834)
+    for autograd; kind 3 scales columns (the Triton kernel's per-value beta, fast_gla.py:464-465)."""
+    B, T, H, Dk = q.shape
+    S = s0 if s0 is not None else torch.zeros(B, H, Dk, v.shape[-1], dtype=torch.float64)
+    d = torch.exp(torch.clamp(g, max=0.0))
+    outs = []
+    for t in range(T):
+        u = v[:, t] - (k[:, t].unsqueeze(-2) @ S).squeeze(-2)
+        W = k[:, t].unsqueeze(-1) @ u.unsqueeze(-2)
+        if kind == 1:
+            W = beta[:, t][..., None, None] * W
+        elif kind == 2:
+            W = beta[:, t].unsqueeze(-1) * W
+        elif kind == 3:
+            W = beta[:, t].unsqueeze(-2) * W
+        S = S * d[:, t].unsqueeze(-1) + W
+        outs.append((q[:, t].unsqueeze(-2) @ S).squeeze(-2))
+    return torch.stack(outs, dim=1), S
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+@pytest.mark.parametrize("T,with_init", [(1, True), (9, False), (23, True)])
+def test_gdn_bwd_matches_autograd(kind, T, with_init):
+    """Every gradient (q, k, v, g, beta, S0) of the Gated DeltaNet variant equals torch autograd
+    through the fp64 loop, including the clamp mask (positive and exactly-zero gates)."""
+    B, H, D = 2, 2, 5
+    rng = np.random.default_rng(100 * kind + T)
+    q, k, v = (torch.tensor(rng.standard_normal((B, T, H, D)), requires_grad=True) for _ in range(3))
+    gn = -np.abs(rng.standard_normal((B, T, H, D)))
+    gn[:, ::3, :, 0] = 0.2  # clamped: zero gradient
+    gn[:, 1::4, :, 1] = 0.0  # the clamp's boundary: the gradient passes
+    g = torch.tensor(gn, requires_grad=True)
+    beta = None
+    if kind == 1:
+        beta = torch.tensor(rng.uniform(0.1, 1.0, (B, T, H)), requires_grad=True)
+    elif kind in (2, 3):
+        beta = torch.tensor(rng.uniform(0.1, 1.0, (B, T, H, D)), requires_grad=True)
+    s0 = torch.tensor(rng.standard_normal((B, H, D, D)), requires_grad=True) if with_init else None
+    do = torch.tensor(rng.standard_normal((B, T, H, D)))
+    dsf = torch.tensor(rng.standard_normal((B, H, D, D)))
+    o, s = _torch_gdn(q, k, v, g, beta, s0, kind)
+    ((o * do).sum() + (s * dsf).sum()).backward()
+    dq, dk, dv, dg, db, ds0 = O.gdn_bwd(q, k, v, g, beta, s0, do, dsf, beta_kind=kind if kind >= 2 else None)
+    for got, ref in ((dq, q.grad), (dk, k.grad), (dv, v.grad), (dg, g.grad)):
+        np.testing.assert_allclose(got, ref.numpy(), rtol=1e-11, atol=1e-11)
+    if beta is not None:
+        np.testing.assert_allclose(db, beta.grad.numpy(), rtol=1e-11, atol=1e-11)
+    if with_init:
+        np.testing.assert_allclose(ds0, s0.grad.numpy(), rtol=1e-11, atol=1e-11)
+    # the loop itself is the oracle's forward
+    of, sf = O.gdn_fwd(q, k, v, g, beta, s0, beta_kind=kind if kind >= 2 else None)
+    np.testing.assert_allclose(of, o.detach().numpy(), atol=1e-12)
+
+
+@pytest.mark.parametrize("kind", [1, 2])
+def test_gdn_bwd_finite_differences(kind):
+    """Central differences of the oracle's own Gated DeltaNet forward agree with its backward."""
+    B, T, H, D = 1, 5, 1, 3
+    rng = np.random.default_rng(7 + kind)
+    q, k, v = rng.standard_normal((3, B, T, H, D))
+    g = -0.2 - np.abs(rng.standard_normal((B, T, H, D)))
+    beta = rng.uniform(0.2, 0.9, (B, T, H) if kind == 1 else (B, T, H, D))
+    s0 = rng.standard_normal((B, H, D, D))
+    W = rng.standard_normal((B, T, H, D))
+    U = rng.standard_normal((B, H, D, D))
+
+    def loss(q, k, v, g, beta, s0):
+        o, s = O.gdn_fwd(q, k, v, g, beta, s0)
+        return float((o * W).sum() + (s * U).sum())
+
+    dq, dk, dv, dg, db, ds0 = O.gdn_bwd(q, k, v, g, beta, s0, W, U)
+    args = [q, k, v, g, beta, s0]
+    eps = 1e-6
+    for a, ga in enumerate((dq, dk, dv, dg, db, ds0)):
+        x = args[a]
+        for idx in [tuple(rng.integers(0, n) for n in x.shape) for _ in range(5)]:
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            ap, am = list(args), list(args)
+            ap[a], am[a] = xp, xm
+            fd = (loss(*ap) - loss(*am)) / (2 * eps)
+            assert abs(fd - ga[idx]) <= 1e-7 * max(1.0, abs(fd)), (a, idx, fd, ga[idx])
+
+
 @pytest.mark.parametrize("with_init", [False, True])
 def test_scan_bwd_matches_autograd(with_init):
     """The reference's own check (test_kernels.py:236-264), in fp64: autograd through the

@@ -105,6 +105,12 @@ def _bind(lib):
              _vp],
             _i,
         ),
+        "triune_hip_gdn_bwd_workspace_size": ([_i64, _i64, _i64, _i, _i, _i], _sz),
+        "triune_hip_gdn_bwd": (
+            [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+             _i64, _i64, _i, _i, _vp, _sz, _vp],
+            _i,
+        ),
         "triune_hip_gdn_prefill_scalar_decay_workspace_size": ([_i64, _i64, _i64, _i, _i], _sz),
         "triune_hip_gdn_prefill_scalar_decay": (
             [_vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _vp, _sz,
@@ -144,6 +150,8 @@ EXPORTS = (
     "triune_hip_gdn_prefill_chunked",
     "triune_hip_gdn_prefill_scalar_decay_workspace_size",
     "triune_hip_gdn_prefill_scalar_decay",
+    "triune_hip_gdn_bwd_workspace_size",
+    "triune_hip_gdn_bwd",
     "triune_hip_gla_qkvg_prep",
     "triune_hip_gla_fused_decode_step",
     "triune_hip_gla_fused_decode_step_slots",

@@ -756,6 +756,97 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
     return launch_status(launch_gdn_tokenwise(a, Dk, Dv, (hipStream_t)stream));
 }
 
+// Gated DeltaNet backward: checkpoints every L = 1024 / D tokens, per-slice partial sums.
+struct GdnBwdPlan {
+    int64_t nc, nsl, nq;
+    size_t off_part, off_bh, total;
+};
+
+static GdnBwdPlan plan_gdn_bwd(int64_t B, int64_t T, int64_t H, int D, int beta_kind) {
+    GdnBwdPlan p{};
+    const int64_t L = gdn_bwd_chunk_tokens(D);
+    p.nc = T > 0 ? (T + L - 1) / L : 0;
+    p.nsl = D / 16;
+    p.nq = beta_kind == TRIUNE_BETA_KEY ? 4 : 3;
+    const int64_t n = B * T * H;
+    p.off_part = align_up((size_t)(B * H * p.nc) * D * D * sizeof(float));
+    p.off_bh = p.off_part + align_up((size_t)(p.nq * p.nsl * n) * D * sizeof(float));
+    p.total = p.off_bh + align_up((size_t)(beta_kind == TRIUNE_BETA_HEAD ? p.nsl * n : 0) * sizeof(float));
+    return p;
+}
+
+size_t triune_hip_gdn_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int Dk, int Dv, int beta_kind) {
+    if (B < 0 || T < 0 || H <= 0 || Dk != Dv || (Dk != 64 && Dk != 128)) return 0;
+    const size_t t = plan_gdn_bwd(B, T, H, Dk, beta_kind).total;
+    return t > 0 ? t : 16;
+}
+
+int triune_hip_gdn_bwd(const void* q, const void* k, const void* v, const void* g, int io_dtype, int g_dtype,
+                       const void* beta, int beta_dtype, int beta_kind, const int64_t* strides, const float* s0,
+                       const void* dout, int dout_dtype, const float* ds_final, void* dq, void* dk, void* dv,
+                       void* dg, void* dbeta, float* ds0, int64_t B, int64_t T, int64_t H, int Dk, int Dv,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !g || !strides || !dq || !dk || !dv || !dg) return TRIUNE_ERR_NULL;
+    if (beta_kind < TRIUNE_BETA_NONE || beta_kind > TRIUNE_BETA_VALUE) return TRIUNE_ERR_SHAPE;
+    if (beta_kind != TRIUNE_BETA_NONE && (!beta || !dbeta)) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || (dout && !dtype_ok(dout_dtype)) ||
+        (beta_kind != TRIUNE_BETA_NONE && !dtype_ok(beta_dtype)))
+        return TRIUNE_ERR_DTYPE;
+    if (B < 0 || T < 0 || H <= 0 || Dk != Dv || (Dk != 64 && Dk != 128)) return TRIUNE_ERR_SHAPE;
+    const int D = Dk;
+    const bool vec_beta = beta_kind == TRIUNE_BETA_KEY || beta_kind == TRIUNE_BETA_VALUE;
+    if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
+        !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
+        (vec_beta && !vec_ok(beta, beta_dtype, strides + 12, 3)) ||
+        (dout && !vec_ok(dout, dout_dtype, strides + 15, 3)) || reinterpret_cast<uintptr_t>(s0) % 16 ||
+        reinterpret_cast<uintptr_t>(ds_final) % 16 || reinterpret_cast<uintptr_t>(ds0) % 16)
+        return TRIUNE_ERR_LAYOUT;
+    if (B == 0) return TRIUNE_OK;
+    const GdnBwdPlan pl = plan_gdn_bwd(B, T, H, D, beta_kind);
+    hipStream_t st = (hipStream_t)stream;
+    if (T == 0) {  // no tokens: the gradient of the initial state is that of the final state
+        if (!ds0) return TRIUNE_OK;
+        return launch_status(launch_gdn_slice_sum(ds_final, 1, 0, B * H * (int64_t)D * D, ds0, DT_F32, st));
+    }
+    if (!workspace || workspace_bytes < pl.total) return TRIUNE_ERR_WORKSPACE;
+    char* ws = reinterpret_cast<char*>(workspace);
+    if (reinterpret_cast<uintptr_t>(ws) % 16) return TRIUNE_ERR_LAYOUT;
+    GdnBwdParams p{};
+    GdnParams& a = p.f;
+    a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
+    a.io_dt = io_dtype; a.g_dt = g_dtype; a.beta_dt = beta_dtype; a.beta_kind = beta_kind;
+    a.q_sb = strides[0]; a.q_st = strides[1]; a.q_sh = strides[2];
+    a.k_sb = strides[3]; a.k_st = strides[4]; a.k_sh = strides[5];
+    a.v_sb = strides[6]; a.v_st = strides[7]; a.v_sh = strides[8];
+    a.g_sb = strides[9]; a.g_st = strides[10]; a.g_sh = strides[11];
+    a.b_sb = strides[12]; a.b_st = strides[13]; a.b_sh = strides[14];
+    a.s0 = s0;
+    a.B = B; a.T = T; a.H = H;
+    p.dout = dout; p.do_dt = dout_dtype; p.do_sb = strides[15]; p.do_st = strides[16]; p.do_sh = strides[17];
+    p.dsf = ds_final;
+    p.ckpt = reinterpret_cast<float*>(ws);
+    p.part = reinterpret_cast<float*>(ws + pl.off_part);
+    p.part_bh = reinterpret_cast<float*>(ws + pl.off_bh);
+    p.dv = dv;
+    p.dbeta_v = beta_kind == TRIUNE_BETA_VALUE ? dbeta : nullptr;
+    p.dbeta_dt = beta_dtype;
+    p.ds0 = ds0;
+    p.nc = pl.nc;
+    if (launch_gdn_bwd(p, D, st) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    const int64_t n = B * T * H * D;
+    if (launch_gdn_slice_sum(p.part, (int)pl.nsl, n, n, dq, io_dtype, st) != hipSuccess ||
+        launch_gdn_slice_sum(p.part + pl.nsl * n, (int)pl.nsl, n, n, dk, io_dtype, st) != hipSuccess ||
+        launch_gdn_slice_sum(p.part + 2 * pl.nsl * n, (int)pl.nsl, n, n, dg, g_dtype, st) != hipSuccess)
+        return TRIUNE_ERR_LAUNCH;
+    if (beta_kind == TRIUNE_BETA_KEY &&
+        launch_gdn_slice_sum(p.part + 3 * pl.nsl * n, (int)pl.nsl, n, n, dbeta, beta_dtype, st) != hipSuccess)
+        return TRIUNE_ERR_LAUNCH;
+    if (beta_kind == TRIUNE_BETA_HEAD &&
+        launch_gdn_slice_sum(p.part_bh, (int)pl.nsl, B * T * H, B * T * H, dbeta, beta_dtype, st) != hipSuccess)
+        return TRIUNE_ERR_LAUNCH;
+    return TRIUNE_OK;
+}
+
 }  // extern "C"
 
 namespace {

@@ -136,6 +136,23 @@ struct GdnParams {
     int64_t B, T, H;
 };
 
+// Gradients of the Gated DeltaNet reference variant (gdn_bwd.hip); D = Dk = Dv in {64, 128}.
+struct GdnBwdParams {
+    GdnParams f;             // forward inputs and shapes; f.s0 the initial state or null
+    const void* dout;        // [B, T, H, Dv] upstream gradient of o (element strides below) or null
+    int do_dt;
+    int64_t do_sb, do_st, do_sh;
+    const float* dsf;        // [B, H, D, D] upstream gradient of the final state or null
+    float* ckpt;             // [B, H, NC, D, D] state before tokens 0, L, 2L, ...
+    float* part;             // [NQ][NSL][B, T, H, D] per-slice sums over columns: dq, dk, dg, key-beta
+    float* part_bh;          // [NSL][B, T, H] head-beta partials
+    void* dv;                // [B, T, H, D] contiguous, io dtype
+    void* dbeta_v;           // value beta: [B, T, H, D] contiguous in dbeta_dt
+    int dbeta_dt;
+    float* ds0;              // [B, H, D, D] or null
+    int64_t nc;              // sub-chunks per sequence
+};
+
 // GLA input pre-processing (in place): q, k in qkv [B, T, 3, H, HD] (element strides sb, st, sp
 // between the q/k/v parts, sh), g [B, T, H, HD]; cos/sin [T, HD] rows cs_st apart.
 struct PrepParams {
@@ -183,6 +200,12 @@ hipError_t launch_gla_decode(const DecodeParams& a, int Dk, int Dv, int max_bloc
 hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t stream);
 // T == 1 of many rows (Dk = Dv = D in {64, 128}; q, k, g, v rows and beta vector-aligned, beta fp32)
 hipError_t launch_gdn_decode(const GdnParams& a, int D, int max_blocks, hipStream_t stream);
+// GDN backward: checkpoint forward + reverse walk (part, part_bh, ckpt sized by the caller), then
+// the per-slice sums are added by launch_gdn_slice_sum.
+int gdn_bwd_chunk_tokens(int D);
+hipError_t launch_gdn_bwd(const GdnBwdParams& p, int D, hipStream_t stream);
+hipError_t launch_gdn_slice_sum(const float* src, int nsl, int64_t stride, int64_t n, void* out, int dt,
+                                hipStream_t stream);
 // Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).
 hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);

@@ -617,16 +617,82 @@ def _scalar_gate(g):
 
 def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
     _check_io(q, k, v, g)
-    sg = _scalar_gate(g)
     if g.dim() == 3 or g.shape[-1] != q.shape[-1]:  # one gate per (token, head): the per-dim kernels take it broadcast
+        sg = _scalar_gate(g)
         g = sg.unsqueeze(-1).expand(*sg.shape, q.shape[-1])
-    if _needs_grad(q, k, v, g, beta, initial_state):
-        # The reference differentiates its PyTorch recurrence here (fast_gla.py:885-904); these
-        # HIP kernels are forward-only, so refuse rather than return outputs without gradients.
-        raise NotImplementedError(
-            "Gated DeltaNet has no backward on this path; call it under torch.no_grad() or with inputs "
-            "that do not require gradients")
     _on_device(beta, initial_state)
+    if _needs_grad(q, k, v, g, beta, initial_state):
+        # the reference differentiates its PyTorch recurrence here (fast_gla.py:885-904)
+        return _GatedDeltaNet.apply(q, k, v, g, beta, initial_state, beta_kind, out_dtype)
+    return _gdn_fwd(q, k, v, g, beta, initial_state, beta_kind, out_dtype)
+
+
+def _gdn_bwd(q, k, v, g, beta, initial_state, beta_kind, do, ds):
+    """Gradients (dq, dk, dv, dg, dbeta, ds0) of _gdn_fwd for upstream do (of o) and ds (of the
+    fp32 final state), either of which may be None, on triune_hip_gdn_bwd.  Head dims are
+    zero-padded to the kernels' 64 or 128 (padded rows and columns of the state stay zero)."""
+    B, T, H, Dk0 = q.shape
+    Dv0 = v.shape[-1]
+    D = 64 if max(Dk0, Dv0) <= 64 else 128
+    if max(Dk0, Dv0) > 128:
+        raise ValueError("Gated DeltaNet backward supports head dims up to 128")
+    qp, kp, vp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, v))
+    gp = _vec_layout(_pad_last(g, D), 1)
+    bp, bst = None, (0, 0, 0)
+    if beta is not None:
+        bp = beta
+        if beta_kind in (_lib.BETA_KEY, _lib.BETA_VALUE):
+            bp = _vec_layout(_pad_last(beta, D), 1)
+        bst = (bp.stride(0), bp.stride(1), bp.stride(2))
+    dop = None if do is None else _vec_layout(_pad_last(do, D), 1)
+    s0 = _state_in(initial_state, D, D)
+    dsf = _state_in(ds, D, D)
+    dq, dk, dv = (torch.empty(B, T, H, D, device=q.device, dtype=q.dtype) for _ in range(3))
+    dg = torch.empty(B, T, H, D, device=q.device, dtype=gp.dtype)
+    db = None
+    if beta is not None:
+        db = torch.empty(bp.shape if beta_kind == _lib.BETA_HEAD else (B, T, H, D), device=q.device, dtype=bp.dtype)
+    ds0 = torch.empty(B, H, D, D, device=q.device, dtype=torch.float32) if initial_state is not None else None
+    L = lib()
+    wsb = L.triune_hip_gdn_bwd_workspace_size(B, T, H, D, D, beta_kind)
+    ws = torch.empty(max(int(wsb), 16), device=q.device, dtype=torch.uint8)
+    st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), bst, _tok3(dop) if dop is not None else (0, 0, 0))
+    rc = L.triune_hip_gdn_bwd(
+        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), ptr(bp),
+        dtype_code(bp) if bp is not None else 0, beta_kind, st, ptr(s0), ptr(dop),
+        dtype_code(dop) if dop is not None else 0, ptr(dsf), ptr(dq), ptr(dk), ptr(dv), ptr(dg), ptr(db), ptr(ds0),
+        B, T, H, D, D, ptr(ws), ws.numel(), stream_of(q),
+    )
+    check(rc, "triune_hip_gdn_bwd")
+    dq, dk, dg = dq[..., :Dk0], dk[..., :Dk0], dg[..., :Dk0]
+    dv = dv[..., :Dv0]
+    if db is not None and beta_kind != _lib.BETA_HEAD:
+        db = db[..., :(Dk0 if beta_kind == _lib.BETA_KEY else Dv0)]
+    if ds0 is not None:
+        ds0 = ds0[..., :Dk0, :Dv0].to(initial_state.dtype)
+    return dq, dk, dv, dg.to(g.dtype), None if db is None else db.to(beta.dtype), ds0
+
+
+class _GatedDeltaNet(torch.autograd.Function):
+    """Gated DeltaNet with gradients: forward on the HIP forward kernels, backward on
+    triune_hip_gdn_bwd (states recomputed from checkpoints)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, beta_kind, out_dtype):
+        o, s = _gdn_fwd(q, k, v, g, beta, initial_state, beta_kind, out_dtype)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state)
+        ctx.beta_kind = beta_kind
+        return o, s
+
+    @staticmethod
+    def backward(ctx, do, ds):
+        q, k, v, g, beta, s0 = ctx.saved_tensors
+        dq, dk, dv, dg, db, ds0 = _gdn_bwd(q, k, v, g, beta, s0, ctx.beta_kind, do, ds)
+        return dq, dk, dv, dg, db, ds0, None, None
+
+
+def _gdn_fwd(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
+    sg = _scalar_gate(g)
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
     D = _round_dk(max(Dk0, Dv0))
@@ -699,16 +765,21 @@ def fast_recurrent_gated_deltanet(q, k, v, g, beta=None, initial_state=None, *, 
         u_t = v_t - S_{t-1}^T k_t ; S_t = diag(exp(min(g_t,0))) S_{t-1} + beta_t (k_t u_t^T) ; o_t = S_t^T q_t
     beta None, [B, T, H] or [B, T, H, D]; a 4-D beta scales rows (key dim), as this reference
     function does.  out_dtype: dtype of the output (default v.dtype; float32 keeps the fp32
-    accumulators unrounded).  Returns (out, final_state fp32)."""
+    accumulators unrounded).  Differentiable in q, k, v, g, beta and initial_state, as the
+    reference's autograd through this loop (backward: triune_hip_gdn_bwd).  Returns (out,
+    final_state fp32)."""
     return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, "key"), out_dtype)
 
 
 def fast_chunk_gated_deltanet(q, k, v, g, beta=None, initial_state=None, chunk_size=64, *, out_dtype=None):
     """Gated DeltaNet operator entry (reference: fast_chunk_gated_deltanet, fast_gla.py:839-904).
     A 4-D beta scales columns (value dim) as the reference's GPU kernel does for T > 1
-    (fast_gla.py:464-465), and rows at T == 1 (fast_gla.py:880).  chunk_size is accepted for
-    signature parity.  out_dtype as for fast_recurrent_gated_deltanet.  Returns (out,
-    final_state fp32)."""
+    (fast_gla.py:464-465), and rows at T == 1 (fast_gla.py:880) and whenever a gradient is needed
+    (the reference then runs its PyTorch recurrence, fast_gla.py:885-904, which scales rows).
+    Differentiable in q, k, v, g, beta and initial_state (backward: triune_hip_gdn_bwd).
+    chunk_size is accepted for signature parity.  out_dtype as for
+    fast_recurrent_gated_deltanet.  Returns (out, final_state fp32)."""
     T = q.shape[1]
-    orientation = "key" if T == 1 else "value"
+    grad = _needs_grad(q, k, v, g, beta, initial_state)
+    orientation = "key" if (T == 1 or grad) else "value"
     return _gdn(q, k, v, g, beta, initial_state, _beta_kind(beta, orientation), out_dtype)
