@@ -699,6 +699,7 @@ def main():
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev),
                                       "gdn_vbeta": bench_gdn_vbeta(dev), "gdn_decode": bench_gdn_decode(dev),
+                                      "gdn_bwd": bench_gdn_bwd(dev),
                                       "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
