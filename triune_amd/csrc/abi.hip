@@ -766,7 +766,7 @@ static GdnBwdPlan plan_gdn_bwd(int64_t B, int64_t T, int64_t H, int D, int beta_
     GdnBwdPlan p{};
     const int64_t L = gdn_bwd_chunk_tokens(D);
     p.nc = T > 0 ? (T + L - 1) / L : 0;
-    p.nsl = D / 16;
+    p.nsl = gdn_bwd_col_slices(D);
     p.nq = beta_kind == TRIUNE_BETA_KEY ? 4 : 3;
     const int64_t n = B * T * H;
     p.off_part = align_up((size_t)(B * H * p.nc) * D * D * sizeof(float));

@@ -13,28 +13,31 @@
 //   dg_i = a_i sum_j D[i][j] P[i][j] where g_i <= 0 (torch.clamp(max=0) passes its gradient there)
 //   D <- diag(a) D + k dpred^T ;  ds0 = D after token 0.
 //
-// Value columns evolve independently in the forward, so a wave owns 16 columns of one (b, h)
-// (lane (rg, c): rows rg*RPT .. rg*RPT+RPT-1 of column c, RPT = D/4) and walks the tokens:
+// Value columns evolve independently in the forward, so a wave owns 8 columns of one (b, h)
+// (lane (rg, c): rows rg*RPT .. rg*RPT+RPT-1 of column c, RPT = D/8) and walks the tokens:
 //   gdn_ckpt_kernel   forward from s0, storing the state before every L-th token (L = 1024/D);
 //   gdn_bwd_kernel    sub-chunks of L tokens last to first: the sub-chunk's inputs are staged in
 //                     LDS, its L states before each token recomputed from the checkpoint into LDS,
 //                     then the tokens walked backwards; sums over key rows stay in the wave, sums
-//                     over value columns (dq, dk, dg, key-beta) are reduced over the wave's 16
-//                     columns (a reduce-scatter over the DPP row) and written per column slice;
-//   gdn_slice_sum_kernel adds the D/16 slices and writes the gradient in its dtype.
+//                     over value columns (dq, dk, dg, key-beta) are reduced over the wave's 8
+//                     columns (a reduce-scatter inside each half DPP row) and written per column
+//                     slice;
+//   gdn_slice_sum_kernel adds the D/8 slices and writes the gradient in its dtype.
 #include "kernels.h"
 
 namespace triune {
 
 namespace {
 
-constexpr int GB_CW = 16;  // value columns per wave
+// value columns per wave: 8 (the lane's serial work per token is D/8 rows of one column)
+constexpr int GB_CW = 8;
 
-template <int D>
+template <int D, int CW>
 struct GbLay {
-    static constexpr int RPT = D / 4;           // rows per lane
+    static constexpr int NRG = 64 / CW;         // row groups
+    static constexpr int RPT = D / NRG;         // rows per lane
     static constexpr int L = 1024 / D;          // tokens per sub-chunk (checkpoint interval)
-    static constexpr int RPL = RPT / 16;        // rows per lane after the column reduce-scatter
+    static constexpr int RPL = RPT / CW;        // rows per lane after the column reduce-scatter (D / 64)
 };
 
 // Rows [t0, t0 + nv) of a token tensor (element strides sb, st, sh; W elements from col0) into LDS
@@ -83,17 +86,32 @@ __device__ __forceinline__ void lds_read(const float* p, float (&x)[N]) {
     }
 }
 
-// Sum over the four row groups (lanes c, c + 16, c + 32, c + 48) in every lane.
-__device__ __forceinline__ float rg_sum(float x) { return xor_sum<32>(xor_sum<16>(x)); }
+// Sum over the row groups (lanes c, c + CW, c + 2 CW, ...) in every lane; lane ^ 8 inside a DPP
+// row is the rotation by 8.
+template <int CW>
+__device__ __forceinline__ float rg_sum(float x) {
+    if constexpr (CW == 8) x += row_ror<8>(x);
+    return xor_sum<32>(xor_sum<16>(x));
+}
+
+// Sum over the CW lanes of a column group (a DPP row for 16, a half row for 8) in every lane.
+template <int CW>
+__device__ __forceinline__ float cw_sum(float x) {
+    x = dpp_add<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    x = dpp_add<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    x = dpp_add<0x141>(x);  // row_half_mirror
+    if constexpr (CW == 16) x = dpp_add<0x140>(x);  // row_mirror
+    return x;
+}
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
-// One butterfly step of the reduce-scatter over the 16 lanes of a DPP row: the partner (lane ^ m,
-// m = 15, 7, 3, 1 through row_mirror, row_half_mirror and two quad permutes) differs in bit BIT;
-// a lane keeps the half of its N values that its BIT selects and adds the partner's copy of it.
+// One butterfly step of the reduce-scatter over the CW lanes of a column group: the partner
+// (lane ^ m, m = 15, 7, 3, 1 through row_mirror, row_half_mirror and two quad permutes) differs in
+// bit BIT; a lane keeps the half of its N values that its BIT selects and adds the partner's copy.
 template <int RB, int N, int CTRL, int BIT>
 __device__ __forceinline__ void rs_step(float (&x)[RB], int c) {
     const bool up = (c >> BIT) & 1;
@@ -105,26 +123,27 @@ __device__ __forceinline__ void rs_step(float (&x)[RB], int c) {
     }
 }
 
-// Reduce-scatter over the 16 columns of a DPP row: on entry x[0..RPT) holds this lane's terms of
-// rows r0 .. r0+RPT; on exit x[0..RPT/16) holds the sums over the 16 lanes of rows
-// r0 + c*RPT/16 + [0, RPT/16).
-template <int RPT>
+// Reduce-scatter over the CW columns of a group: on entry x[0..RPT) holds this lane's terms of
+// rows r0 .. r0+RPT; on exit x[0..RPT/CW) holds the sums over the CW lanes of rows
+// r0 + c*RPT/CW + [0, RPT/CW).
+template <int RPT, int CW>
 __device__ __forceinline__ void col_reduce_scatter(float (&x)[RPT], int c) {
-    static_assert(RPT % 16 == 0, "rows per lane");
-    rs_step<RPT, RPT, 0x140, 3>(x, c);      // row_mirror: lane ^ 15
-    rs_step<RPT, RPT / 2, 0x141, 2>(x, c);  // row_half_mirror: lane ^ 7
-    rs_step<RPT, RPT / 4, 0x1B, 1>(x, c);   // quad_perm [3, 2, 1, 0]: lane ^ 3
-    rs_step<RPT, RPT / 8, 0xB1, 0>(x, c);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+    static_assert(RPT % CW == 0, "rows per lane");
+    constexpr int N0 = CW == 16 ? RPT : 2 * RPT;  // CW = 8 starts at the half-row mirror
+    if constexpr (CW == 16) rs_step<RPT, N0, 0x140, 3>(x, c);  // row_mirror: lane ^ 15
+    rs_step<RPT, N0 / 2, 0x141, 2>(x, c);  // row_half_mirror: lane ^ 7
+    rs_step<RPT, N0 / 4, 0x1B, 1>(x, c);   // quad_perm [3, 2, 1, 0]: lane ^ 3
+    rs_step<RPT, N0 / 8, 0xB1, 0>(x, c);   // quad_perm [1, 0, 3, 2]: lane ^ 1
 }
 
 // One forward token on the lane's RPT rows of column c: returns u_j (before beta); S updated.
-template <int RPT, int BK>
+template <int RPT, int CW, int BK>
 __device__ __forceinline__ float gb_forward_token(float (&S)[RPT], const float* kq, const float* gg,
                                                   const float* brow, float vj, float bc) {
     float pred = 0.f;
 #pragma unroll
     for (int m = 0; m < RPT; ++m) pred = fmaf(kq[m], S[m], pred);
-    pred = rg_sum(pred);
+    pred = rg_sum<CW>(pred);
     const float u = vj - pred;
     const float uu = (BK == BETA_HEAD || BK == BETA_VALUE) ? bc * u : u;
 #pragma unroll
@@ -141,14 +160,14 @@ __device__ __forceinline__ float gb_forward_token(float (&S)[RPT], const float* 
 
 template <int D, int BK>
 __global__ __launch_bounds__(64) void gdn_ckpt_kernel(GdnBwdParams p) {
-    using Ly = GbLay<D>;
+    using Ly = GbLay<D, GB_CW>;
     constexpr int RPT = Ly::RPT, L = Ly::L;
     const GdnParams& a = p.f;
     __shared__ __attribute__((aligned(16))) float sK[L * D];
     __shared__ __attribute__((aligned(16))) float sG[L * D];
     __shared__ __attribute__((aligned(16))) float sV[L * GB_CW];
     __shared__ __attribute__((aligned(16))) float sB[BK == BETA_KEY ? L * D : (BK == BETA_VALUE ? L * GB_CW : L)];
-    const int lane = threadIdx.x, c = lane & 15, rg = lane >> 4, r0 = rg * RPT;
+    const int lane = threadIdx.x, c = lane % GB_CW, rg = lane / GB_CW, r0 = rg * RPT;
     const int64_t bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
     const int col0 = blockIdx.x * GB_CW, col = col0 + c;
     float S[RPT];
@@ -183,14 +202,14 @@ __global__ __launch_bounds__(64) void gdn_ckpt_kernel(GdnBwdParams p) {
             lds_read<RPT>(sG + tt * D + r0, gg);
             if constexpr (BK == BETA_KEY) lds_read<RPT>(sB + tt * D + r0, br);
             const float bc = BK == BETA_HEAD ? sB[tt] : (BK == BETA_VALUE ? sB[tt * GB_CW + c] : 1.f);
-            gb_forward_token<RPT, BK>(S, kq, gg, br, sV[tt * GB_CW + c], bc);
+            gb_forward_token<RPT, GB_CW, BK>(S, kq, gg, br, sV[tt * GB_CW + c], bc);
         }
     }
 }
 
 template <int D, int BK>
 __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
-    using Ly = GbLay<D>;
+    using Ly = GbLay<D, GB_CW>;
     constexpr int RPT = Ly::RPT, L = Ly::L, RPL = Ly::RPL;
     const GdnParams& a = p.f;
     __shared__ __attribute__((aligned(16))) float sQ[L * D];
@@ -201,7 +220,7 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
     __shared__ __attribute__((aligned(16))) float sB[BK == BETA_KEY ? L * D : (BK == BETA_VALUE ? L * GB_CW : L)];
     __shared__ __attribute__((aligned(16))) float sP[L * 64 * RPT];  // [token][RPT/4][lane] float4
     __shared__ __attribute__((aligned(16))) float sU[L * 64];
-    const int lane = threadIdx.x, c = lane & 15, rg = lane >> 4, r0 = rg * RPT;
+    const int lane = threadIdx.x, c = lane % GB_CW, rg = lane / GB_CW, r0 = rg * RPT;
     const int64_t bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
     const int slice = blockIdx.x, nsl = gridDim.x;
     const int col0 = slice * GB_CW, col = col0 + c;
@@ -247,7 +266,7 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
             lds_read<RPT>(sG + tt * D + r0, gg);
             if constexpr (BK == BETA_KEY) lds_read<RPT>(sB + tt * D + r0, br);
             const float bc = BK == BETA_HEAD ? sB[tt] : (BK == BETA_VALUE ? sB[tt * GB_CW + c] : 1.f);
-            sU[tt * 64 + lane] = gb_forward_token<RPT, BK>(S, kq, gg, br, sV[tt * GB_CW + c], bc);
+            sU[tt * 64 + lane] = gb_forward_token<RPT, GB_CW, BK>(S, kq, gg, br, sV[tt * GB_CW + c], bc);
         }
         __syncthreads();
         for (int tt = nv - 1; tt >= 0; --tt) {
@@ -278,7 +297,7 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
                 dS[m] = fmaf(qq[m], doj, dS[m]);
                 cpart = fmaf(dS[m], w[m], cpart);
             }
-            const float cj = rg_sum(cpart);
+            const float cj = rg_sum<GB_CW>(cpart);
             const float du = (BK == BETA_HEAD || BK == BETA_VALUE) ? bc * cj : cj;
             const float dpred = -du;
 #pragma unroll
@@ -302,13 +321,13 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
                 }
             }
             if constexpr (BK == BETA_HEAD) {
-                const float db = dpp_sum16(u * cj);  // the same in every row group
+                const float db = cw_sum<GB_CW>(u * cj);  // the same in every row group
                 if (lane == 0) p.part_bh[(int64_t)slice * BTH + (b * a.T + t) * a.H + h] = db;
             }
-            col_reduce_scatter<RPT>(xq, c);
-            col_reduce_scatter<RPT>(xk, c);
-            col_reduce_scatter<RPT>(xg, c);
-            if constexpr (BK == BETA_KEY) col_reduce_scatter<RPT>(xb, c);
+            col_reduce_scatter<RPT, GB_CW>(xq, c);
+            col_reduce_scatter<RPT, GB_CW>(xk, c);
+            col_reduce_scatter<RPT, GB_CW>(xg, c);
+            if constexpr (BK == BETA_KEY) col_reduce_scatter<RPT, GB_CW>(xb, c);
             // lane (rg, c) now holds rows rg*RPT + c*RPL + [0, RPL): row = lane * RPL + i
             const int64_t tok = ((b * a.T + t) * a.H + h) * D + lane * RPL;
             float* pq = p.part + ((int64_t)0 * nsl + slice) * BTH * D + tok;
@@ -346,6 +365,7 @@ __global__ __launch_bounds__(256) void gdn_slice_sum_kernel(const float* src, in
 }
 
 int gdn_bwd_chunk_tokens(int D) { return 1024 / D; }
+int gdn_bwd_col_slices(int D) { return D / GB_CW; }
 
 template <int D, int BK>
 static hipError_t launch_gdn_bwd_dk(const GdnBwdParams& p, hipStream_t stream) {

@@ -203,6 +203,7 @@ hipError_t launch_gdn_decode(const GdnParams& a, int D, int max_blocks, hipStrea
 // GDN backward: checkpoint forward + reverse walk (part, part_bh, ckpt sized by the caller), then
 // the per-slice sums are added by launch_gdn_slice_sum.
 int gdn_bwd_chunk_tokens(int D);
+int gdn_bwd_col_slices(int D);
 hipError_t launch_gdn_bwd(const GdnBwdParams& p, int D, hipStream_t stream);
 hipError_t launch_gdn_slice_sum(const float* src, int nsl, int64_t stride, int64_t n, void* out, int dt,
                                 hipStream_t stream);
