@@ -69,10 +69,10 @@ def _oracle(q, k, v, g, beta, s0, do, ds, kind):
 
 @pytest.mark.parametrize("kind", ["none", "head", "key", "value"])
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("T", [1, 7, 16, 17, 100])
+@pytest.mark.parametrize("T", [1, 7, 16, 17, 33, 100])
 def test_gdn_bwd_fp32(dev, kind, D, T):
     """Every gradient (q, k, v, g, beta, initial state) through the C-ABI entry, fp32, sub-chunk
-    tails (16 tokens per checkpoint at D = 64, 8 at 128)."""
+    tails (32 tokens per checkpoint at D = 64, 16 at 128)."""
     B, H = 2, 3
     q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, kind, seed=T * 7 + D)
     args = [x.to(dev) if x is not None else None for x in (q, k, v, g, beta)]

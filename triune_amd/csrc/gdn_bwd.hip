@@ -15,7 +15,7 @@
 //
 // Value columns evolve independently in the forward, so a wave owns 8 columns of one (b, h)
 // (lane (rg, c): rows rg*RPT .. rg*RPT+RPT-1 of column c, RPT = D/8) and walks the tokens:
-//   gdn_ckpt_kernel   forward from s0, storing the state before every L-th token (L = 1024/D);
+//   gdn_ckpt_kernel   forward from s0, storing the state before every L-th token (L = 2048/D);
 //   gdn_bwd_kernel    sub-chunks of L tokens last to first: the sub-chunk's inputs are staged in
 //                     LDS, its L states before each token recomputed from the checkpoint into LDS,
 //                     then the tokens walked backwards; sums over key rows stay in the wave, sums
@@ -36,7 +36,7 @@ template <int D, int CW>
 struct GbLay {
     static constexpr int NRG = 64 / CW;         // row groups
     static constexpr int RPT = D / NRG;         // rows per lane
-    static constexpr int L = 1024 / D;          // tokens per sub-chunk (checkpoint interval)
+    static constexpr int L = 2048 / D;          // tokens per sub-chunk (checkpoint interval)
     static constexpr int RPL = RPT / CW;        // rows per lane after the column reduce-scatter (D / 64)
 };
 
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256) void gdn_slice_sum_kernel(const float* src, in
     else reinterpret_cast<_Float16*>(out)[i] = (_Float16)s;
 }
 
-int gdn_bwd_chunk_tokens(int D) { return 1024 / D; }
+int gdn_bwd_chunk_tokens(int D) { return 2048 / D; }
 int gdn_bwd_col_slices(int D) { return D / GB_CW; }
 
 template <int D, int BK>
