@@ -159,3 +159,54 @@ def test_no_upstream_state_gradient(dev):
     ref = O.gdn_bwd(q, k, v, g, beta, None, do, None, beta_kind=_lib.BETA_KEY)
     for x, r in zip(xs, ref[:5]):
         assert _rel_err(x.grad, r) <= 1e-5, _rel_err(x.grad, r)
+
+
+def test_fp16_and_fp32_gate(dev):
+    """fp16 I/O with an fp32 gate: dq, dk, dv come back in fp16 and dg in fp32 (each gradient in
+    its input's dtype), within one bf16 ULP (coarser than fp16's) plus 2e-3 of the oracle."""
+    B, T, H, D = 1, 90, 2, 64
+    q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, "key", seed=21, dtype=torch.float16)
+    g = g.float()
+    args = [x.to(dev) for x in (q, k, v, g, beta)]
+    got = _gdn_bwd(*args, s0.to(dev), _lib.BETA_KEY, do.to(dev), ds.to(dev))
+    torch.cuda.synchronize()
+    ref = O.gdn_bwd(q, k, v, g, beta, s0, do, ds, beta_kind=_lib.BETA_KEY)
+    for name, x, r, dt in zip(("dq", "dk", "dv", "dg", "dbeta"), got[:5], ref[:5],
+                              (torch.float16, torch.float16, torch.float16, torch.float32, torch.float16)):
+        assert x.dtype == dt, name
+        assert _ulp_excess(x, r) <= 2e-3, (name, _ulp_excess(x, r))
+
+
+def test_unequal_head_dims_zero_padded(dev):
+    """Dk = 48, Dv = 80 (run zero-padded to 128): gradients of the unpadded tensors, through the
+    operator's autograd, fp32."""
+    gen = torch.Generator().manual_seed(4880)
+    B, T, H, Dk, Dv = 1, 37, 2, 48, 80
+    q, k = (F.normalize(torch.randn(B, T, H, Dk, generator=gen), dim=-1) for _ in range(2))
+    v = torch.randn(B, T, H, Dv, generator=gen)
+    g = F.logsigmoid(torch.randn(B, T, H, Dk, generator=gen) + 2.0) / 8
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    s0 = 0.2 * torch.randn(B, H, Dk, Dv, generator=gen)
+    do, ds = torch.randn(B, T, H, Dv, generator=gen), torch.randn(B, H, Dk, Dv, generator=gen)
+    xs = [x.to(dev).requires_grad_(True) for x in (q, k, v, g, beta, s0)]
+    o, s = fast_recurrent_gated_deltanet(*xs[:4], beta=xs[4], initial_state=xs[5])
+    ((o * do.to(dev)).sum() + (s * ds.to(dev)).sum()).backward()
+    torch.cuda.synchronize()
+    ref = O.gdn_bwd(q, k, v, g, beta, s0, do, ds)
+    for x, r in zip(xs, (ref[0], ref[1], ref[2], ref[3], ref[4], ref[5])):
+        assert tuple(x.grad.shape) == tuple(x.shape)
+        assert _rel_err(x.grad, r) <= 1e-5, _rel_err(x.grad, r)
+
+
+def test_zero_tokens(dev):
+    """T = 0: no token gradients, and the initial state's gradient is the final state's."""
+    B, H, D = 2, 2, 64
+    q = torch.zeros(B, 0, H, D, device=dev, requires_grad=True)
+    k, v, g = (torch.zeros(B, 0, H, D, device=dev) for _ in range(3))
+    s0 = torch.randn(B, H, D, D, device=dev, requires_grad=True)
+    o, s = fast_recurrent_gated_deltanet(q, k, v, g, initial_state=s0)
+    ds = torch.randn(B, H, D, D, device=dev)
+    (s * ds).sum().backward()
+    torch.cuda.synchronize()
+    assert q.grad.shape == q.shape
+    assert float((s0.grad - ds).abs().max()) == 0.0

@@ -636,6 +636,12 @@ def _gdn_bwd(q, k, v, g, beta, initial_state, beta_kind, do, ds):
     D = 64 if max(Dk0, Dv0) <= 64 else 128
     if max(Dk0, Dv0) > 128:
         raise ValueError("Gated DeltaNet backward supports head dims up to 128")
+    if T == 0 or B == 0:  # no tokens: the initial state's gradient is the final state's
+        z = lambda x: torch.zeros_like(x)  # noqa: E731
+        ds0 = None
+        if initial_state is not None:
+            ds0 = (ds if ds is not None else torch.zeros_like(initial_state)).to(initial_state.dtype)
+        return z(q), z(k), z(v), z(g), None if beta is None else z(beta), ds0
     qp, kp, vp = (_vec_layout(_pad_last(x, D), 1) for x in (q, k, v))
     gp = _vec_layout(_pad_last(g, D), 1)
     bp, bst = None, (0, 0, 0)
@@ -695,6 +701,11 @@ def _gdn_fwd(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
     sg = _scalar_gate(g)
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
+    if T == 0 or B == 0:  # nothing to scan: the final state is the initial state
+        o = torch.empty(B, T, H, Dv0, device=q.device, dtype=out_dtype or v.dtype)
+        if initial_state is None:
+            return o, torch.zeros(B, H, Dk0, Dv0, device=q.device, dtype=torch.float32)
+        return o, initial_state.to(torch.float32).clone()
     D = _round_dk(max(Dk0, Dv0))
     # chunked WY/UT path: (64, 64) heads (smaller ones zero-padded) and (128, 128) heads with 16-bit
     # I/O, every beta kind; a gate with one value per (token, head) and beta none or per token
