@@ -210,3 +210,19 @@ def test_zero_tokens(dev):
     torch.cuda.synchronize()
     assert q.grad.shape == q.shape
     assert float((s0.grad - ds).abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_more_waves_than_cus_short_sub_chunks(dev, D):
+    """B * H * D / 8 waves above the CU count (256 on MI355X) select the short sub-chunks (1024/D
+    tokens, three workgroups per CU); fp32 against the oracle with a tail past the last
+    checkpoint."""
+    B, T, H = 4, 45, 9 if D == 64 else 5
+    assert B * H * D // 8 > torch.cuda.get_device_properties(dev).multi_processor_count
+    q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, "head", seed=D + 1)
+    args = [x.to(dev) for x in (q, k, v, g, beta)]
+    got = _gdn_bwd(*args, s0.to(dev), _lib.BETA_HEAD, do.to(dev), ds.to(dev))
+    torch.cuda.synchronize()
+    ref = _oracle(q, k, v, g, beta, s0, do, ds, "head")
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), got, ref):
+        assert _rel_err(x, r) <= 1e-5, (name, _rel_err(x, r))

@@ -759,14 +759,15 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
 // Gated DeltaNet backward: checkpoints every L = 1024 / D tokens, per-slice partial sums.
 struct GdnBwdPlan {
     int64_t nc, nsl, nq;
+    int L;
     size_t off_part, off_bh, total;
 };
 
 static GdnBwdPlan plan_gdn_bwd(int64_t B, int64_t T, int64_t H, int D, int beta_kind) {
     GdnBwdPlan p{};
-    const int64_t L = gdn_bwd_chunk_tokens(D);
-    p.nc = T > 0 ? (T + L - 1) / L : 0;
     p.nsl = gdn_bwd_col_slices(D);
+    p.L = gdn_bwd_chunk_tokens(D, B * H * p.nsl, device_cus());
+    p.nc = T > 0 ? (T + p.L - 1) / p.L : 0;
     p.nq = beta_kind == TRIUNE_BETA_KEY ? 4 : 3;
     const int64_t n = B * T * H;
     p.off_part = align_up((size_t)(B * H * p.nc) * D * D * sizeof(float));
@@ -832,6 +833,7 @@ int triune_hip_gdn_bwd(const void* q, const void* k, const void* v, const void* 
     p.dbeta_dt = beta_dtype;
     p.ds0 = ds0;
     p.nc = pl.nc;
+    p.L = pl.L;
     if (launch_gdn_bwd(p, D, st) != hipSuccess) return TRIUNE_ERR_LAUNCH;
     const int64_t n = B * T * H * D;
     if (launch_gdn_slice_sum(p.part, (int)pl.nsl, n, n, dq, io_dtype, st) != hipSuccess ||

@@ -15,7 +15,8 @@
 //
 // Value columns evolve independently in the forward, so a wave owns 8 columns of one (b, h)
 // (lane (rg, c): rows rg*RPT .. rg*RPT+RPT-1 of column c, RPT = D/8) and walks the tokens:
-//   gdn_ckpt_kernel   forward from s0, storing the state before every L-th token (L = 2048/D);
+//   gdn_ckpt_kernel   forward from s0, storing the state before every L-th token (L = 1024/D or
+//                     2048/D);
 //   gdn_bwd_kernel    sub-chunks of L tokens last to first: the sub-chunk's inputs are staged in
 //                     LDS, its L states before each token recomputed from the checkpoint into LDS,
 //                     then the tokens walked backwards; sums over key rows stay in the wave, sums
@@ -32,11 +33,12 @@ namespace {
 // value columns per wave: 8 (the lane's serial work per token is D/8 rows of one column)
 constexpr int GB_CW = 8;
 
-template <int D, int CW>
+// SL: tokens per sub-chunk (the checkpoint interval), 1024/D or 2048/D (see gdn_bwd_chunk_tokens)
+template <int D, int CW, int SL>
 struct GbLay {
     static constexpr int NRG = 64 / CW;         // row groups
     static constexpr int RPT = D / NRG;         // rows per lane
-    static constexpr int L = 2048 / D;          // tokens per sub-chunk (checkpoint interval)
+    static constexpr int L = SL;
     static constexpr int RPL = RPT / CW;        // rows per lane after the column reduce-scatter (D / 64)
 };
 
@@ -158,9 +160,9 @@ __device__ __forceinline__ float gb_forward_token(float (&S)[RPT], const float* 
 }  // namespace
 
 
-template <int D, int BK>
+template <int D, int SL, int BK>
 __global__ __launch_bounds__(64) void gdn_ckpt_kernel(GdnBwdParams p) {
-    using Ly = GbLay<D, GB_CW>;
+    using Ly = GbLay<D, GB_CW, SL>;
     constexpr int RPT = Ly::RPT, L = Ly::L;
     const GdnParams& a = p.f;
     __shared__ __attribute__((aligned(16))) float sK[L * D];
@@ -207,9 +209,9 @@ __global__ __launch_bounds__(64) void gdn_ckpt_kernel(GdnBwdParams p) {
     }
 }
 
-template <int D, int BK>
+template <int D, int SL, int BK>
 __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
-    using Ly = GbLay<D, GB_CW>;
+    using Ly = GbLay<D, GB_CW, SL>;
     constexpr int RPT = Ly::RPT, L = Ly::L, RPL = Ly::RPL;
     const GdnParams& a = p.f;
     __shared__ __attribute__((aligned(16))) float sQ[L * D];
@@ -364,17 +366,27 @@ __global__ __launch_bounds__(256) void gdn_slice_sum_kernel(const float* src, in
     else reinterpret_cast<_Float16*>(out)[i] = (_Float16)s;
 }
 
-int gdn_bwd_chunk_tokens(int D) { return 2048 / D; }
+// Tokens per sub-chunk: 2048/D where every wave has a CU of its own (the longer sub-chunk halves
+// the staging round trips; its LDS, about 100 KB, leaves one workgroup per CU), else 1024/D
+// (about 50 KB: three per CU, so every wave stays resident).
+int gdn_bwd_chunk_tokens(int D, int64_t waves, int64_t cus) { return waves <= cus ? 2048 / D : 1024 / D; }
 int gdn_bwd_col_slices(int D) { return D / GB_CW; }
+
+template <int D, int SL, int BK>
+static hipError_t launch_gdn_bwd_lk(const GdnBwdParams& p, hipStream_t stream) {
+    const dim3 grid(D / GB_CW, (unsigned)(p.f.B * p.f.H));
+    hipLaunchKernelGGL((gdn_ckpt_kernel<D, SL, BK>), grid, dim3(64), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((gdn_bwd_kernel<D, SL, BK>), grid, dim3(64), 0, stream, p);
+    return hipGetLastError();
+}
 
 template <int D, int BK>
 static hipError_t launch_gdn_bwd_dk(const GdnBwdParams& p, hipStream_t stream) {
-    const dim3 grid(D / GB_CW, (unsigned)(p.f.B * p.f.H));
-    hipLaunchKernelGGL((gdn_ckpt_kernel<D, BK>), grid, dim3(64), 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gdn_bwd_kernel<D, BK>), grid, dim3(64), 0, stream, p);
-    return hipGetLastError();
+    if (p.L == 2048 / D) return launch_gdn_bwd_lk<D, 2048 / D, BK>(p, stream);
+    if (p.L == 1024 / D) return launch_gdn_bwd_lk<D, 1024 / D, BK>(p, stream);
+    return hipErrorInvalidValue;
 }
 
 template <int D>

@@ -151,6 +151,7 @@ struct GdnBwdParams {
     int dbeta_dt;
     float* ds0;              // [B, H, D, D] or null
     int64_t nc;              // sub-chunks per sequence
+    int L;                   // tokens per sub-chunk (gdn_bwd_chunk_tokens)
 };
 
 // GLA input pre-processing (in place): q, k in qkv [B, T, 3, H, HD] (element strides sb, st, sp
@@ -202,7 +203,7 @@ hipError_t launch_gdn_tokenwise(const GdnParams& a, int Dk, int Dv, hipStream_t 
 hipError_t launch_gdn_decode(const GdnParams& a, int D, int max_blocks, hipStream_t stream);
 // GDN backward: checkpoint forward + reverse walk (part, part_bh, ckpt sized by the caller), then
 // the per-slice sums are added by launch_gdn_slice_sum.
-int gdn_bwd_chunk_tokens(int D);
+int gdn_bwd_chunk_tokens(int D, int64_t waves, int64_t cus);
 int gdn_bwd_col_slices(int D);
 hipError_t launch_gdn_bwd(const GdnBwdParams& p, int D, hipStream_t stream);
 hipError_t launch_gdn_slice_sum(const float* src, int nsl, int64_t stride, int64_t n, void* out, int dt,
