@@ -400,7 +400,7 @@ def bench_gdn_bwd(dev, reps=3):
     gbs = alg / (ms * 1e-3) / 1e9
     return {"workload": "Gated DeltaNet backward, config 3 (B=4, H=6, T=8192, D=64, bf16, per-head beta)",
             "ms": round(ms, 3), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
-            "kernels": "gdn_ckpt + gdn_bwd + gdn_slice_sum (token-serial, states recomputed from checkpoints)",
+            "kernels": "gdn_segmap + gdn_carry + gdn_ckpt + gdn_dloc + gdn_carry + gdn_bwd + gdn_slice_sum (token-serial inside segments walked in parallel, states recomputed from checkpoints)",
             "roofline": {"bound": "latency (token-serial)", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 

@@ -226,3 +226,22 @@ def test_more_waves_than_cus_short_sub_chunks(dev, D):
     ref = _oracle(q, k, v, g, beta, s0, do, ds, "head")
     for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), got, ref):
         assert _rel_err(x, r) <= 1e-5, (name, _rel_err(x, r))
+
+
+@pytest.mark.parametrize("kind", ["none", "head", "key"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_segments_walked_in_parallel(dev, kind, D):
+    """Few (b, h) pairs leave resident slots free, so the tokens are cut into segments walked in
+    parallel (segment maps, carries both ways, then the per-segment walks): T = 1000 gives segments
+    of several sub-chunks and a partial last sub-chunk; fp32 against the oracle at 1e-5."""
+    B, T, H = 1, 1000, 2
+    q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, kind, seed=D + 11)
+    args = [x.to(dev) if x is not None else None for x in (q, k, v, g, beta)]
+    got = _gdn_bwd(*args, s0.to(dev), KINDS[kind], do.to(dev), ds.to(dev))
+    torch.cuda.synchronize()
+    ref = _oracle(q, k, v, g, beta, s0, do, ds, kind)
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), got, ref):
+        if r is None:
+            assert x is None
+            continue
+        assert _rel_err(x, r) <= 1e-5, (name, _rel_err(x, r))

@@ -756,23 +756,39 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
     return launch_status(launch_gdn_tokenwise(a, Dk, Dv, (hipStream_t)stream));
 }
 
-// Gated DeltaNet backward: checkpoints every L = 1024 / D tokens, per-slice partial sums.
+// Gated DeltaNet backward: checkpoints every L tokens, per-slice partial sums.  Where one wave per
+// (b, h, 8 value columns) leaves resident slots free (six one-wave gradient workgroups of about
+// 25 KB of LDS per CU at L = 512 / D), the tokens are cut into segments walked in parallel (not for
+// beta per value column): the gradient kernel's NB segments, each of up to four segments of the
+// lighter kernels (at most about 16 of those per sequence, so the carries stay short).
 struct GdnBwdPlan {
-    int64_t nc, nsl, nq;
+    int64_t nc, nsl, nq, nseg, segc, bsegc, bsegr;
     int L;
-    size_t off_part, off_bh, total;
+    size_t off_part, off_bh, off_seg, total;
 };
 
 static GdnBwdPlan plan_gdn_bwd(int64_t B, int64_t T, int64_t H, int D, int beta_kind) {
     GdnBwdPlan p{};
     p.nsl = gdn_bwd_col_slices(D);
-    p.L = gdn_bwd_chunk_tokens(D, B * H * p.nsl, device_cus());
+    const int64_t waves = B * H * p.nsl, cus = device_cus();
+    p.nseg = beta_kind != TRIUNE_BETA_VALUE && waves > 0 ? 6 * cus / waves : 1;
+    p.L = p.nseg >= 2 ? 512 / D : gdn_bwd_chunk_tokens(D, waves, cus);
     p.nc = T > 0 ? (T + p.L - 1) / p.L : 0;
+    if (p.nseg > p.nc) p.nseg = p.nc;
+    if (p.nseg < 2) p.nseg = 1;
+    p.bsegc = p.nseg > 1 ? (p.nc + p.nseg - 1) / p.nseg : p.nc;  // sub-chunks per gradient-kernel segment
+    const int64_t rmax = p.nseg >= 16 ? 1 : (p.nseg >= 8 ? 2 : 4);
+    p.bsegr = p.bsegc < rmax ? p.bsegc : rmax;
+    if (p.nseg < 2) p.bsegr = 1;
+    p.segc = (p.bsegc + p.bsegr - 1) / p.bsegr;
+    p.bsegc = p.segc * p.bsegr;
+    p.nseg = p.nc > 0 ? (p.nc + p.segc - 1) / p.segc : 1;
     p.nq = beta_kind == TRIUNE_BETA_KEY ? 4 : 3;
     const int64_t n = B * T * H;
     p.off_part = align_up((size_t)(B * H * p.nc) * D * D * sizeof(float));
     p.off_bh = p.off_part + align_up((size_t)(p.nq * p.nsl * n) * D * sizeof(float));
-    p.total = p.off_bh + align_up((size_t)(beta_kind == TRIUNE_BETA_HEAD ? p.nsl * n : 0) * sizeof(float));
+    p.off_seg = p.off_bh + align_up((size_t)(beta_kind == TRIUNE_BETA_HEAD ? p.nsl * n : 0) * sizeof(float));
+    p.total = p.off_seg + (p.nseg > 1 ? 4 * align_up((size_t)(B * H * p.nseg) * D * D * sizeof(float)) : 0);
     return p;
 }
 
@@ -834,6 +850,17 @@ int triune_hip_gdn_bwd(const void* q, const void* k, const void* v, const void* 
     p.ds0 = ds0;
     p.nc = pl.nc;
     p.L = pl.L;
+    p.nseg = pl.nseg;
+    p.segc = pl.segc;
+    p.bsegc = pl.bsegc;
+    p.bsegr = pl.bsegr;
+    if (pl.nseg > 1) {
+        const size_t seg_bytes = align_up((size_t)(B * H * pl.nseg) * D * D * sizeof(float));
+        p.seg_m = reinterpret_cast<float*>(ws + pl.off_seg);
+        p.seg_n = reinterpret_cast<float*>(ws + pl.off_seg + seg_bytes);
+        p.seg_dl = reinterpret_cast<float*>(ws + pl.off_seg + 2 * seg_bytes);
+        p.seg_de = reinterpret_cast<float*>(ws + pl.off_seg + 3 * seg_bytes);
+    }
     if (launch_gdn_bwd(p, D, st) != hipSuccess) return TRIUNE_ERR_LAUNCH;
     const int64_t n = B * T * H * D;
     if (launch_gdn_slice_sum(p.part, (int)pl.nsl, n, n, dq, io_dtype, st) != hipSuccess ||

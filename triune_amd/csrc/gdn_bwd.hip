@@ -24,6 +24,20 @@
 //                     columns (a reduce-scatter inside each half DPP row) and written per column
 //                     slice;
 //   gdn_slice_sum_kernel adds the D/8 slices and writes the gradient in its dtype.
+//
+// Segments (beta none, per head or per key dim).  D's recurrence does not involve S: per token
+// D <- F_t^T (D + q do^T) with F_t = diag(a) - w cs k^T the forward's linear map on a state column
+// (S_t = F_t P + w (cs v)^T).  Over a segment of tokens the forward map is S_end = M S_start + N
+// (M = F_last ... F_first) and the backward one D_first = M^T D_last + D_loc.  With NSEG segments of
+// segc sub-chunks, walked in parallel:
+//   gdn_segmap_kernel  per segment: M (walking the identity's columns with v = 0) and N (from zero);
+//   gdn_carry_kernel   S_start[s+1] = M_s S_start[s] + N_s into the checkpoints; then, reversed,
+//                      D_end[s-1] = M_s^T D_end[s] + D_loc[s] from D_end[NSEG-1] = dS_final;
+//   gdn_dloc_kernel    per segment s >= 1: D_loc[s], the walk of D from zero;
+//   gdn_ckpt_kernel / gdn_bwd_kernel  per segment from S_start[s] and D_end[s]; the gradient
+//                      kernel (about 50 KB of LDS per wave against 13 KB for the others) walks
+//                      coarser segments made of whole ones.
+// Beta per value column has a map per column (cs_j differs), so it keeps one segment.
 #include "kernels.h"
 
 namespace triune {
@@ -174,7 +188,12 @@ __global__ __launch_bounds__(64) void gdn_ckpt_kernel(GdnBwdParams p) {
     const int col0 = blockIdx.x * GB_CW, col = col0 + c;
     float S[RPT];
     const int64_t DD = (int64_t)D * D;
-    if (a.s0) {
+    const int64_t seg = blockIdx.z, sc0 = seg * p.segc, sc1 = sc0 + p.segc < p.nc ? sc0 + p.segc : p.nc;
+    if (seg > 0) {  // the segment's start state, written by the carry
+        const float* s = p.ckpt + (bh * p.nc + sc0) * DD + (int64_t)r0 * D + col;
+#pragma unroll
+        for (int m = 0; m < RPT; ++m) S[m] = s[(int64_t)m * D];
+    } else if (a.s0) {
         const float* s = a.s0 + bh * DD + (int64_t)r0 * D + col;
 #pragma unroll
         for (int m = 0; m < RPT; ++m) S[m] = s[(int64_t)m * D];
@@ -182,13 +201,15 @@ __global__ __launch_bounds__(64) void gdn_ckpt_kernel(GdnBwdParams p) {
 #pragma unroll
         for (int m = 0; m < RPT; ++m) S[m] = 0.f;
     }
-    for (int64_t sc = 0; sc < p.nc; ++sc) {
+    for (int64_t sc = sc0; sc < sc1; ++sc) {
         const int64_t t0 = sc * L;
         const int nv = (int)(a.T - t0 < L ? a.T - t0 : L);
         float* ck = p.ckpt + (bh * p.nc + sc) * DD + (int64_t)r0 * D + col;
+        if (sc > sc0 || seg == 0) {
 #pragma unroll
-        for (int m = 0; m < RPT; ++m) ck[(int64_t)m * D] = S[m];
-        if (sc + 1 == p.nc) break;  // the last sub-chunk's tokens are not needed here
+            for (int m = 0; m < RPT; ++m) ck[(int64_t)m * D] = S[m];
+        }
+        if (sc + 1 == sc1) break;  // the segment's last sub-chunk's tokens are not needed here
         __syncthreads();
         stage_rows<L, D>(sK, a.k, a.io_dt, a.k_sb, a.k_st, a.k_sh, b, t0, h, 0, nv);
         stage_rows<L, D>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
@@ -229,15 +250,18 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
     const int64_t DD = (int64_t)D * D;
     const int64_t BTH = a.B * a.T * a.H;
     float dS[RPT];
-    if (p.dsf) {
-        const float* s = p.dsf + bh * DD + (int64_t)r0 * D + col;
+    const int64_t seg = blockIdx.z, sc0 = seg * p.bsegc, sc1 = sc0 + p.bsegc < p.nc ? sc0 + p.bsegc : p.nc;
+    const int64_t last = (seg + 1) * p.bsegr < p.nseg ? (seg + 1) * p.bsegr - 1 : p.nseg - 1;  // its last segment
+    const float* dsi = p.nseg > 1 ? p.seg_de + (bh * p.nseg + last) * DD : (p.dsf ? p.dsf + bh * DD : nullptr);
+    if (dsi) {
+        const float* s = dsi + (int64_t)r0 * D + col;
 #pragma unroll
         for (int m = 0; m < RPT; ++m) dS[m] = s[(int64_t)m * D];
     } else {
 #pragma unroll
         for (int m = 0; m < RPT; ++m) dS[m] = 0.f;
     }
-    for (int64_t sc = p.nc - 1; sc >= 0; --sc) {
+    for (int64_t sc = sc1 - 1; sc >= sc0; --sc) {
         const int64_t t0 = sc * L;
         const int nv = (int)(a.T - t0 < L ? a.T - t0 : L);
         __syncthreads();  // the previous sub-chunk's reads of the staging arrays are done
@@ -346,10 +370,159 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
             }
         }
     }
-    if (p.ds0) {
+    if (p.ds0 && seg == 0) {
         float* s = p.ds0 + bh * DD + (int64_t)r0 * D + col;
 #pragma unroll
         for (int m = 0; m < RPT; ++m) s[(int64_t)m * D] = dS[m];
+    }
+}
+
+// Segment maps: grid (2 D / 8, B * H, NSEG).  Slices below D / 8 walk columns of the identity
+// with v = 0 (-> M_s), the others the value columns from zero (-> N_s).  Not for beta per value.
+template <int D, int SL, int BK>
+__global__ __launch_bounds__(64) void gdn_segmap_kernel(GdnBwdParams p) {
+    using Ly = GbLay<D, GB_CW, SL>;
+    constexpr int RPT = Ly::RPT, L = Ly::L;
+    static_assert(BK != BETA_VALUE, "beta per value column has a map per column");
+    const GdnParams& a = p.f;
+    __shared__ __attribute__((aligned(16))) float sK[L * D];
+    __shared__ __attribute__((aligned(16))) float sG[L * D];
+    __shared__ __attribute__((aligned(16))) float sV[L * GB_CW];
+    __shared__ __attribute__((aligned(16))) float sB[BK == BETA_KEY ? L * D : L];
+    const int lane = threadIdx.x, c = lane % GB_CW, rg = lane / GB_CW, r0 = rg * RPT;
+    const int64_t bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+    const bool ident = blockIdx.x < D / GB_CW;
+    const int col0 = (ident ? (int)blockIdx.x : (int)blockIdx.x - D / GB_CW) * GB_CW, col = col0 + c;
+    const int64_t DD = (int64_t)D * D;
+    const int64_t seg = blockIdx.z, sc0 = seg * p.segc, sc1 = sc0 + p.segc < p.nc ? sc0 + p.segc : p.nc;
+    float S[RPT];
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) S[m] = ident && r0 + m == col ? 1.f : 0.f;
+    for (int64_t sc = sc0; sc < sc1; ++sc) {
+        const int64_t t0 = sc * L;
+        const int nv = (int)(a.T - t0 < L ? a.T - t0 : L);
+        __syncthreads();
+        stage_rows<L, D>(sK, a.k, a.io_dt, a.k_sb, a.k_st, a.k_sh, b, t0, h, 0, nv);
+        stage_rows<L, D>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
+        if (!ident) stage_rows<L, GB_CW>(sV, a.v, a.io_dt, a.v_sb, a.v_st, a.v_sh, b, t0, h, col0, nv);
+        if constexpr (BK == BETA_HEAD) stage_head_beta<L>(sB, a, b, t0, h, nv);
+        if constexpr (BK == BETA_KEY) stage_rows<L, D>(sB, a.beta, a.beta_dt, a.b_sb, a.b_st, a.b_sh, b, t0, h, 0, nv);
+        __syncthreads();
+        for (int tt = 0; tt < nv; ++tt) {
+            float kq[RPT], gg[RPT], br[RPT];
+            lds_read<RPT>(sK + tt * D + r0, kq);
+            lds_read<RPT>(sG + tt * D + r0, gg);
+            if constexpr (BK == BETA_KEY) lds_read<RPT>(sB + tt * D + r0, br);
+            const float bc = BK == BETA_HEAD ? sB[tt] : 1.f;
+            gb_forward_token<RPT, GB_CW, BK>(S, kq, gg, br, ident ? 0.f : sV[tt * GB_CW + c], bc);
+        }
+    }
+    float* o = (ident ? p.seg_m : p.seg_n) + (bh * p.nseg + seg) * DD + (int64_t)r0 * D + col;
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) o[(int64_t)m * D] = S[m];
+}
+
+// D_loc[s] for segments s >= 1: grid (D / 8, B * H, NSEG - 1), the walk of D alone from zero.
+template <int D, int SL, int BK>
+__global__ __launch_bounds__(64) void gdn_dloc_kernel(GdnBwdParams p) {
+    using Ly = GbLay<D, GB_CW, SL>;
+    constexpr int RPT = Ly::RPT, L = Ly::L;
+    static_assert(BK != BETA_VALUE, "beta per value column has a map per column");
+    const GdnParams& a = p.f;
+    __shared__ __attribute__((aligned(16))) float sQ[L * D];
+    __shared__ __attribute__((aligned(16))) float sK[L * D];
+    __shared__ __attribute__((aligned(16))) float sG[L * D];
+    __shared__ __attribute__((aligned(16))) float sDO[L * GB_CW];
+    __shared__ __attribute__((aligned(16))) float sB[BK == BETA_KEY ? L * D : L];
+    const int lane = threadIdx.x, c = lane % GB_CW, rg = lane / GB_CW, r0 = rg * RPT;
+    const int64_t bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+    const int col0 = blockIdx.x * GB_CW, col = col0 + c;
+    const int64_t DD = (int64_t)D * D;
+    const int64_t seg = (int64_t)blockIdx.z + 1, sc0 = seg * p.segc, sc1 = sc0 + p.segc < p.nc ? sc0 + p.segc : p.nc;
+    float dS[RPT];
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) dS[m] = 0.f;
+    for (int64_t sc = sc1 - 1; sc >= sc0; --sc) {
+        const int64_t t0 = sc * L;
+        const int nv = (int)(a.T - t0 < L ? a.T - t0 : L);
+        __syncthreads();
+        stage_rows<L, D>(sQ, a.q, a.io_dt, a.q_sb, a.q_st, a.q_sh, b, t0, h, 0, nv);
+        stage_rows<L, D>(sK, a.k, a.io_dt, a.k_sb, a.k_st, a.k_sh, b, t0, h, 0, nv);
+        stage_rows<L, D>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
+        if (p.dout) stage_rows<L, GB_CW>(sDO, p.dout, p.do_dt, p.do_sb, p.do_st, p.do_sh, b, t0, h, col0, nv);
+        if constexpr (BK == BETA_HEAD) stage_head_beta<L>(sB, a, b, t0, h, nv);
+        if constexpr (BK == BETA_KEY) stage_rows<L, D>(sB, a.beta, a.beta_dt, a.b_sb, a.b_st, a.b_sh, b, t0, h, 0, nv);
+        __syncthreads();
+        for (int tt = nv - 1; tt >= 0; --tt) {
+            float qq[RPT], kq[RPT], gg[RPT], br[RPT];
+            lds_read<RPT>(sQ + tt * D + r0, qq);
+            lds_read<RPT>(sK + tt * D + r0, kq);
+            lds_read<RPT>(sG + tt * D + r0, gg);
+            if constexpr (BK == BETA_KEY) lds_read<RPT>(sB + tt * D + r0, br);
+            const float bc = BK == BETA_HEAD ? sB[tt] : 1.f;
+            const float doj = p.dout ? sDO[tt * GB_CW + c] : 0.f;
+            float cpart = 0.f;
+#pragma unroll
+            for (int m = 0; m < RPT; ++m) {
+                dS[m] = fmaf(qq[m], doj, dS[m]);
+                cpart = fmaf(dS[m], BK == BETA_KEY ? br[m] * kq[m] : kq[m], cpart);
+            }
+            const float cj = rg_sum<GB_CW>(cpart);
+            const float dpred = -(BK == BETA_HEAD ? bc * cj : cj);
+#pragma unroll
+            for (int m = 0; m < RPT; ++m) dS[m] = fmaf(fast_exp(fminf(gg[m], 0.f)), dS[m], kq[m] * dpred);
+        }
+    }
+    float* o = p.seg_dl + (bh * p.nseg + seg) * DD + (int64_t)r0 * D + col;
+#pragma unroll
+    for (int m = 0; m < RPT; ++m) o[(int64_t)m * D] = dS[m];
+}
+
+// Carry over segments, grid (D / 16, B * H), 256 threads; thread (i0, j) holds rows i0 + 16 m of
+// column cb + j.  Forward (REV false): X = S_start[0] (s0 or zero), X <- M_s X + N_s into the
+// checkpoint of segment s + 1.  REV: X = dS_final (or zero) into D_end[NSEG-1], X <- M_s^T X +
+// D_loc[s] into D_end[s-1].  M_s is staged in LDS each step, X through LDS.
+template <int D, bool REV>
+__global__ __launch_bounds__(256) void gdn_carry_kernel(GdnBwdParams p) {
+    constexpr int NR = D / 16;
+    __shared__ __attribute__((aligned(16))) float sM[D * D];
+    __shared__ __attribute__((aligned(16))) float sX[D * 16];
+    const int t = threadIdx.x, j = t & 15, i0 = t >> 4;
+    const int64_t bh = blockIdx.y, DD = (int64_t)D * D;
+    const int cb = blockIdx.x * 16;
+    auto el = [&](int m) { return (int64_t)(i0 + 16 * m) * D + cb + j; };
+    float x[NR];
+    const float* x0 = REV ? (p.dsf ? p.dsf + bh * DD : nullptr) : (p.f.s0 ? p.f.s0 + bh * DD : nullptr);
+#pragma unroll
+    for (int m = 0; m < NR; ++m) x[m] = x0 ? x0[el(m)] : 0.f;
+    if constexpr (REV) {
+#pragma unroll
+        for (int m = 0; m < NR; ++m) p.seg_de[(bh * p.nseg + p.nseg - 1) * DD + el(m)] = x[m];
+    }
+    for (int64_t n = 1; n < p.nseg; ++n) {
+        const int64_t s = REV ? p.nseg - n : n - 1;  // the segment whose map is applied
+        const float4* M4 = reinterpret_cast<const float4*>(p.seg_m + (bh * p.nseg + s) * DD);
+        const float* Y = (REV ? p.seg_dl : p.seg_n) + (bh * p.nseg + s) * DD;
+        __syncthreads();  // the previous step's reads of sM and sX are done
+#pragma unroll
+        for (int e = t; e < D * D / 4; e += 256) reinterpret_cast<float4*>(sM)[e] = M4[e];
+#pragma unroll
+        for (int m = 0; m < NR; ++m) sX[(i0 + 16 * m) * 16 + j] = x[m];
+        float y[NR];
+#pragma unroll
+        for (int m = 0; m < NR; ++m) y[m] = Y[el(m)];
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < NR; ++m) {
+            const int i = i0 + 16 * m;
+            float acc = y[m];
+#pragma unroll 16
+            for (int kk = 0; kk < D; ++kk) acc = fmaf(REV ? sM[kk * D + i] : sM[i * D + kk], sX[kk * 16 + j], acc);
+            x[m] = acc;
+        }
+        float* out = REV ? p.seg_de + (bh * p.nseg + s - 1) * DD : p.ckpt + (bh * p.nc + (s + 1) * p.segc) * DD;
+#pragma unroll
+        for (int m = 0; m < NR; ++m) out[el(m)] = x[m];
     }
 }
 
@@ -374,11 +547,29 @@ int gdn_bwd_col_slices(int D) { return D / GB_CW; }
 
 template <int D, int SL, int BK>
 static hipError_t launch_gdn_bwd_lk(const GdnBwdParams& p, hipStream_t stream) {
-    const dim3 grid(D / GB_CW, (unsigned)(p.f.B * p.f.H));
+    const unsigned bh = (unsigned)(p.f.B * p.f.H), ns = (unsigned)p.nseg;
+    const dim3 grid(D / GB_CW, bh, ns);
+    const dim3 bgrid(D / GB_CW, bh, (unsigned)((p.nc + p.bsegc - 1) / p.bsegc));
+    hipError_t e;
+    if constexpr (BK != BETA_VALUE) {
+        if (ns > 1) {
+            hipLaunchKernelGGL((gdn_segmap_kernel<D, SL, BK>), dim3(2 * D / GB_CW, bh, ns), dim3(64), 0, stream, p);
+            hipLaunchKernelGGL((gdn_carry_kernel<D, false>), dim3(D / 16, bh), dim3(256), 0, stream, p);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+    } else {
+        if (ns != 1) return hipErrorInvalidValue;
+    }
     hipLaunchKernelGGL((gdn_ckpt_kernel<D, SL, BK>), grid, dim3(64), 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((gdn_bwd_kernel<D, SL, BK>), grid, dim3(64), 0, stream, p);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if constexpr (BK != BETA_VALUE) {
+        if (ns > 1) {
+            hipLaunchKernelGGL((gdn_dloc_kernel<D, SL, BK>), dim3(D / GB_CW, bh, ns - 1), dim3(64), 0, stream, p);
+            hipLaunchKernelGGL((gdn_carry_kernel<D, true>), dim3(D / 16, bh), dim3(256), 0, stream, p);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
+    }
+    hipLaunchKernelGGL((gdn_bwd_kernel<D, SL, BK>), bgrid, dim3(64), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -386,6 +577,7 @@ template <int D, int BK>
 static hipError_t launch_gdn_bwd_dk(const GdnBwdParams& p, hipStream_t stream) {
     if (p.L == 2048 / D) return launch_gdn_bwd_lk<D, 2048 / D, BK>(p, stream);
     if (p.L == 1024 / D) return launch_gdn_bwd_lk<D, 1024 / D, BK>(p, stream);
+    if (p.L == 512 / D) return launch_gdn_bwd_lk<D, 512 / D, BK>(p, stream);
     return hipErrorInvalidValue;
 }
 

@@ -152,6 +152,15 @@ struct GdnBwdParams {
     float* ds0;              // [B, H, D, D] or null
     int64_t nc;              // sub-chunks per sequence
     int L;                   // tokens per sub-chunk (gdn_bwd_chunk_tokens)
+    // Segments of segc sub-chunks walked in parallel (nseg > 1; beta per value column keeps one):
+    // [B, H, NSEG, D, D] fp32 each
+    int64_t nseg, segc;
+    // gdn_bwd_kernel walks coarser segments of bsegr of those (bsegc = bsegr * segc sub-chunks)
+    int64_t bsegc, bsegr;
+    float* seg_m;            // forward map of segment s: S_end = M_s S_start + N_s
+    float* seg_n;            // N_s, the segment's end state from zero
+    float* seg_dl;           // gradient reaching the state before segment s, walked from zero
+    float* seg_de;           // gradient reaching the last state of segment s
 };
 
 // GLA input pre-processing (in place): q, k in qkv [B, T, 3, H, HD] (element strides sb, st, sp
