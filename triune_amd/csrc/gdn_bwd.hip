@@ -57,8 +57,11 @@ struct GbLay {
 };
 
 // Rows [t0, t0 + nv) of a token tensor (element strides sb, st, sh; W elements from col0) into LDS
-// as fp32 [L][W]; rows past nv are zero.
-template <int L, int W>
+// as fp32 [L][W]; rows past nv are zero.  DECAY (the gate): each g is stored as its decay factor
+// exp(g) where g <= 0 and as -1 where the clamp min(g, 0) holds it (decay 1, no gradient), so the
+// walks take |x| as the decay and x >= 0 as the clamp's pass flag, one exp per element and
+// sub-chunk instead of one per lane and token.
+template <int L, int W, bool DECAY = false>
 __device__ __forceinline__ void stage_rows(float* dst, const void* base, int dt, int64_t sb, int64_t st, int64_t sh,
                                            int64_t b, int64_t t0, int64_t h, int col0, int nv) {
     constexpr int CPR = W / 8;
@@ -70,6 +73,10 @@ __device__ __forceinline__ void stage_rows(float* dst, const void* base, int dt,
         float x[8];
         const int64_t off = b * sb + (t0 + tt) * st + h * sh + col0 + c8;
         load8_dt(reinterpret_cast<const char*>(base) + off * es, dt, tt < nv, x);
+        if constexpr (DECAY) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) x[i] = x[i] > 0.f ? -1.f : fast_exp(fminf(x[i], 0.f));
+        }
         float4* d4 = reinterpret_cast<float4*>(dst + tt * W + c8);
         d4[0] = make_float4(x[0], x[1], x[2], x[3]);
         d4[1] = make_float4(x[4], x[5], x[6], x[7]);
@@ -152,7 +159,8 @@ __device__ __forceinline__ void col_reduce_scatter(float (&x)[RPT], int c) {
     rs_step<RPT, N0 / 8, 0xB1, 0>(x, c);   // quad_perm [1, 0, 3, 2]: lane ^ 1
 }
 
-// One forward token on the lane's RPT rows of column c: returns u_j (before beta); S updated.
+// One forward token on the lane's RPT rows of column c (gg: the staged decay factors, see
+// stage_rows): returns u_j (before beta); S updated.
 template <int RPT, int CW, int BK>
 __device__ __forceinline__ float gb_forward_token(float (&S)[RPT], const float* kq, const float* gg,
                                                   const float* brow, float vj, float bc) {
@@ -164,7 +172,7 @@ __device__ __forceinline__ float gb_forward_token(float (&S)[RPT], const float* 
     const float uu = (BK == BETA_HEAD || BK == BETA_VALUE) ? bc * u : u;
 #pragma unroll
     for (int m = 0; m < RPT; ++m) {
-        const float d = fast_exp(fminf(gg[m], 0.f));
+        const float d = fabsf(gg[m]);
         const float w = BK == BETA_KEY ? brow[m] * kq[m] : kq[m];
         S[m] = fmaf(d, S[m], w * uu);
     }
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(64) void gdn_ckpt_kernel(GdnBwdParams p) {
         if (sc + 1 == sc1) break;  // the segment's last sub-chunk's tokens are not needed here
         __syncthreads();
         stage_rows<L, D>(sK, a.k, a.io_dt, a.k_sb, a.k_st, a.k_sh, b, t0, h, 0, nv);
-        stage_rows<L, D>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
+        stage_rows<L, D, true>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
         stage_rows<L, GB_CW>(sV, a.v, a.io_dt, a.v_sb, a.v_st, a.v_sh, b, t0, h, col0, nv);
         if constexpr (BK == BETA_HEAD) stage_head_beta<L>(sB, a, b, t0, h, nv);
         if constexpr (BK == BETA_KEY) stage_rows<L, D>(sB, a.beta, a.beta_dt, a.b_sb, a.b_st, a.b_sh, b, t0, h, 0, nv);
@@ -267,7 +275,7 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
         __syncthreads();  // the previous sub-chunk's reads of the staging arrays are done
         stage_rows<L, D>(sQ, a.q, a.io_dt, a.q_sb, a.q_st, a.q_sh, b, t0, h, 0, nv);
         stage_rows<L, D>(sK, a.k, a.io_dt, a.k_sb, a.k_st, a.k_sh, b, t0, h, 0, nv);
-        stage_rows<L, D>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
+        stage_rows<L, D, true>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
         stage_rows<L, GB_CW>(sV, a.v, a.io_dt, a.v_sb, a.v_st, a.v_sh, b, t0, h, col0, nv);
         if (p.dout) stage_rows<L, GB_CW>(sDO, p.dout, p.do_dt, p.do_sb, p.do_st, p.do_sh, b, t0, h, col0, nv);
         if constexpr (BK == BETA_HEAD) stage_head_beta<L>(sB, a, b, t0, h, nv);
@@ -316,7 +324,7 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
             float cpart = 0.f;
 #pragma unroll
             for (int m = 0; m < RPT; ++m) {
-                dec[m] = fast_exp(fminf(gg[m], 0.f));
+                dec[m] = fabsf(gg[m]);
                 w[m] = BK == BETA_KEY ? br[m] * kq[m] : kq[m];
                 const float st = fmaf(dec[m], P[m], w[m] * uu);  // S_t
                 xq[m] = st * doj;
@@ -365,7 +373,7 @@ __global__ __launch_bounds__(64) void gdn_bwd_kernel(GdnBwdParams p) {
                 const float gr = sG[tt * D + row];
                 pq[i] = xq[i];
                 pk[i] = xk[i];
-                pg[i] = gr <= 0.f ? xg[i] * fast_exp(gr) : 0.f;
+                pg[i] = gr >= 0.f ? xg[i] * gr : 0.f;  // gr: exp(g) where g <= 0, else -1
                 if constexpr (BK == BETA_KEY) p.part[((int64_t)3 * nsl + slice) * BTH * D + tok + i] = xb[i];
             }
         }
@@ -403,7 +411,7 @@ __global__ __launch_bounds__(64) void gdn_segmap_kernel(GdnBwdParams p) {
         const int nv = (int)(a.T - t0 < L ? a.T - t0 : L);
         __syncthreads();
         stage_rows<L, D>(sK, a.k, a.io_dt, a.k_sb, a.k_st, a.k_sh, b, t0, h, 0, nv);
-        stage_rows<L, D>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
+        stage_rows<L, D, true>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
         if (!ident) stage_rows<L, GB_CW>(sV, a.v, a.io_dt, a.v_sb, a.v_st, a.v_sh, b, t0, h, col0, nv);
         if constexpr (BK == BETA_HEAD) stage_head_beta<L>(sB, a, b, t0, h, nv);
         if constexpr (BK == BETA_KEY) stage_rows<L, D>(sB, a.beta, a.beta_dt, a.b_sb, a.b_st, a.b_sh, b, t0, h, 0, nv);
@@ -448,7 +456,7 @@ __global__ __launch_bounds__(64) void gdn_dloc_kernel(GdnBwdParams p) {
         __syncthreads();
         stage_rows<L, D>(sQ, a.q, a.io_dt, a.q_sb, a.q_st, a.q_sh, b, t0, h, 0, nv);
         stage_rows<L, D>(sK, a.k, a.io_dt, a.k_sb, a.k_st, a.k_sh, b, t0, h, 0, nv);
-        stage_rows<L, D>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
+        stage_rows<L, D, true>(sG, a.g, a.g_dt, a.g_sb, a.g_st, a.g_sh, b, t0, h, 0, nv);
         if (p.dout) stage_rows<L, GB_CW>(sDO, p.dout, p.do_dt, p.do_sb, p.do_st, p.do_sh, b, t0, h, col0, nv);
         if constexpr (BK == BETA_HEAD) stage_head_beta<L>(sB, a, b, t0, h, nv);
         if constexpr (BK == BETA_KEY) stage_rows<L, D>(sB, a.beta, a.beta_dt, a.b_sb, a.b_st, a.b_sh, b, t0, h, 0, nv);
@@ -470,7 +478,7 @@ __global__ __launch_bounds__(64) void gdn_dloc_kernel(GdnBwdParams p) {
             const float cj = rg_sum<GB_CW>(cpart);
             const float dpred = -(BK == BETA_HEAD ? bc * cj : cj);
 #pragma unroll
-            for (int m = 0; m < RPT; ++m) dS[m] = fmaf(fast_exp(fminf(gg[m], 0.f)), dS[m], kq[m] * dpred);
+            for (int m = 0; m < RPT; ++m) dS[m] = fmaf(fabsf(gg[m]), dS[m], kq[m] * dpred);
         }
     }
     float* o = p.seg_dl + (bh * p.nseg + seg) * DD + (int64_t)r0 * D + col;
