@@ -405,6 +405,34 @@ def bench_gdn_bwd(dev, reps=3):
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
 
+def bench_gdn_bwd128(dev, reps=3):
+    """Gated DeltaNet backward at the reference model's head dim (B=4, T=8192, H=12, D=128, bf16,
+    q, k = normalize(elu(x) + 1), logsigmoid gates per key dim, no beta, zero initial state): the
+    gradients of q, k, v and g for an upstream gradient of o."""
+    from triune_amd import _lib
+    from triune_amd.fast_gla import _gdn_bwd
+
+    B, T, H, D = 4, 8192, 12, 128
+    gen = torch.Generator(device=dev).manual_seed(13)
+    qk = torch.randn(B, T, 2, H, D, device=dev, generator=gen)
+    qk = torch.nn.functional.normalize(torch.nn.functional.elu(qk) + 1.0, dim=-1).bfloat16()
+    q, k = qk[:, :, 0].contiguous(), qk[:, :, 1].contiguous()
+    v = torch.randn(B, T, H, D, device=dev, generator=gen).bfloat16()
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, D, device=dev, generator=gen)).bfloat16()
+    do = torch.randn(B, T, H, D, device=dev, generator=gen).bfloat16()
+    fn = lambda: _gdn_bwd(q, k, v, g, None, None, _lib.BETA_NONE, do, None)  # noqa: E731
+    fn()
+    torch.cuda.synchronize()
+    ms = _events_time_ms(fn, reps, torch.cuda.current_stream())
+    alg = B * T * H * (9 * D * 2)  # q, k, v, g, do read; dq, dk, dv, dg written (bf16)
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"workload": "Gated DeltaNet backward at head dim 128 (B=4, H=12, T=8192, D=128, bf16, "
+                        "per-key-dim logsigmoid gate, no beta)",
+            "ms": round(ms, 3), "tok_s": round(B * T / (ms * 1e-3), 1), "alg_bytes": alg,
+            "roofline": {"bound": "latency (token-serial)", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
 def bench_gdn128(dev, reps=10):
     """Gated DeltaNet prefill as the reference model calls it at its default head dim
     (triune/model/attention.py:509-536, config.py GLA_HEAD_DIM = 128): q, k = normalize(elu(x) + 1),
@@ -658,7 +686,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "gdn_decode", "gdn_bwd", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
+        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "gdn_decode", "gdn_bwd", "gdn_bwd128", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -687,7 +715,7 @@ def main():
             res = bench_fused_decode(args.decode_steps, dev)
         else:
             res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "gdn_vbeta": bench_gdn_vbeta, "gdn_decode": bench_gdn_decode,
-                   "gdn_bwd": bench_gdn_bwd,
+                   "gdn_bwd": bench_gdn_bwd, "gdn_bwd128": bench_gdn_bwd128,
                    "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
                    "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
@@ -700,6 +728,7 @@ def main():
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev),
                                       "gdn_vbeta": bench_gdn_vbeta(dev), "gdn_decode": bench_gdn_decode(dev),
                                       "gdn_bwd": bench_gdn_bwd(dev),
+                                      "gdn_bwd128": bench_gdn_bwd128(dev),
                                       "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
