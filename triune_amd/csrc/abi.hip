@@ -772,6 +772,9 @@ static GdnBwdPlan plan_gdn_bwd(int64_t B, int64_t T, int64_t H, int D, int beta_
     p.nsl = gdn_bwd_col_slices(D);
     const int64_t waves = B * H * p.nsl, cus = device_cus();
     p.nseg = beta_kind != TRIUNE_BETA_VALUE && waves > 0 ? 6 * cus / waves : 1;
+    // two segments at 4-token sub-chunks (D = 128, 768 waves) ran no faster than one at 8 tokens
+    // and wrote twice the checkpoints: segment from three up
+    if (p.nseg < 3) p.nseg = 1;
     p.L = p.nseg >= 2 ? 512 / D : gdn_bwd_chunk_tokens(D, waves, cus);
     p.nc = T > 0 ? (T + p.L - 1) / p.L : 0;
     if (p.nseg > p.nc) p.nseg = p.nc;
