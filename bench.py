@@ -47,17 +47,25 @@ def _events_time_ms(fn, iters, stream):
     return start.elapsed_time(end) / iters
 
 
-def bench_prefill(steps, warmup, dev):
+def prefill_inputs(dev):
+    """Config-1 inputs in HBM: two input sets used in turn (the second is the first rolled by one
+    token), so 2 x 201 MB of q/k/v/g exceeds the 256 MB MALL and every pass reads its inputs from
+    HBM; the initial state; an output buffer per set."""
+    from triune_amd.workloads import config1
+
+    q, k, v, g, s0 = config1(T=16384, B=4, H=6, D=64)
+    sets = [[x.to(dev) for x in (q, k, v, g)], [x.roll(1, dims=1).to(dev) for x in (q, k, v, g)]]
+    outs = [torch.empty_like(v, device=dev) for _ in sets]
+    torch.cuda.synchronize()
+    return sets, s0.to(dev), outs
+
+
+def bench_prefill(steps, warmup, dev, inputs=None):
     from triune_amd import fast_chunk_gla
-    from triune_amd.workloads import config1, gla_algorithmic_bytes, gla_algorithmic_flops
+    from triune_amd.workloads import gla_algorithmic_bytes, gla_algorithmic_flops
 
     B, T, H, D = 4, 16384, 6, 64
-    q, k, v, g, s0 = config1(T=T, B=B, H=H, D=D)
-    # Two input sets used in turn (the second is the first rolled by one token): 2 x 201 MB of
-    # q/k/v/g exceeds the 256 MB MALL, so every pass reads its inputs from HBM.
-    sets = [[x.to(dev) for x in (q, k, v, g)], [x.roll(1, dims=1).to(dev) for x in (q, k, v, g)]]
-    s0 = s0.to(dev)
-    outs = [torch.empty_like(v, device=dev) for _ in sets]
+    sets, s0, outs = inputs if inputs is not None else prefill_inputs(dev)
     turn = [0]
 
     def fn():
@@ -650,6 +658,40 @@ def cpu_baseline(budget_s=12.0):
     }
 
 
+def cpu_baseline_decode(budget_s=5.0, steps=8):
+    """The reference's T == 1 op sequence on CPU (fast_gla.py:746-753: S <- e^g S + k v^T, o = q S),
+    restated in oracle/ref_port.py, on the config-2 shapes (B=256, H=6, D=64, fp32: the reference
+    computes in q.dtype, and its CPU path is run here in fp32), the state carried from step to step
+    as the reference's decode loop does; repeated for about budget_s seconds on all host cores."""
+    from oracle.ref_port import decode_step_cpu
+    from triune_amd.workloads import config2
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    B, H, D = 256, 6, 64
+    q, k, v, g, s0 = config2(steps=steps, B=B, H=H, D=D)
+    q, k, v, g = (x.float() for x in (q, k, v, g))
+    with torch.no_grad():
+        decode_step_cpu(q[0], k[0], v[0], g[0], s0)  # warm-up
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 3 or time.perf_counter() < t_end:
+            S = s0
+            t0 = time.perf_counter()
+            for t in range(steps):
+                _, S = decode_step_cpu(q[t], k[t], v[t], g[t], S)
+            times.append((time.perf_counter() - t0) / steps)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": B / med,
+        "unit": "tok/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"config-2 decode (B=256, H=6, D=64, fp32 math, state carried), {steps}-step loops, median "
+        f"of {len(times)} loops, {med * 1e3:.2f} ms per step; os.cpu_count()={os.cpu_count()}",
+    }
+
+
 def _traffic_from_profiles(key="output_kernel_bytes_per_launch"):
     """A figure of the config-1 prefill measured with rocprofv3 counters on this build
     (profiles/prefill_traffic.json, written from those runs): HBM bytes per output-kernel launch
@@ -720,10 +762,14 @@ def main():
                    "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
-    # Order: the CPU baseline first (the GPU idles meanwhile), then the secondary GPU legs, then
-    # the headline prefill, so no leg is timed right after the GPU sat idle for seconds.  The
-    # headline itself still does exactly `warmup` untimed passes before its `steps` timed ones.
+    # Order: the CPU baselines and the headline's input generation first (the GPU idles
+    # meanwhile), then the secondary GPU legs, then the headline prefill, so no leg is timed right
+    # after the GPU sat idle for seconds (clocks ramp down when idle: after an idle gap the first
+    # few hundred passes run up to 13 % slower).  The headline itself does exactly `warmup`
+    # untimed passes before its `steps` timed ones.
     cpu = None if args.no_cpu else cpu_baseline()
+    cpu_dec = None if args.no_cpu or args.no_decode else cpu_baseline_decode()
+    pre_in = prefill_inputs(dev)
     dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
     extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev),
                                       "gdn_vbeta": bench_gdn_vbeta(dev), "gdn_decode": bench_gdn_decode(dev),
@@ -734,7 +780,7 @@ def main():
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "bwd128": bench_bwd128(dev),
                                       "scan": bench_scan(dev)}
-    pre = bench_prefill(args.steps, args.warmup, dev)
+    pre = bench_prefill(args.steps, args.warmup, dev, pre_in)
     line = {
         "metric": METRIC,
         "value": round(pre["tok_s"], 1),
@@ -799,6 +845,7 @@ def main():
                 "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
                 "alg_bytes_per_step": dec["step_bytes"],
             },
+            "cpu_baseline": cpu_dec,
         }
     line.update(extra)
     print(json.dumps(line), flush=True)

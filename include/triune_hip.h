@@ -58,7 +58,7 @@
 extern "C" {
 #endif
 
-#define TRIUNE_HIP_ABI_VERSION 2
+#define TRIUNE_HIP_ABI_VERSION 3
 
 enum {
     TRIUNE_DT_F32 = 0,
@@ -75,6 +75,7 @@ enum {
     TRIUNE_ERR_WORKSPACE = -5,   /* workspace missing or smaller than required */
     TRIUNE_ERR_LAUNCH = -6,      /* the HIP runtime rejected a launch */
     TRIUNE_ERR_SCRATCH = -7,     /* larger than the allocation-free entry point's static scratch */
+    TRIUNE_ERR_MEMORY = -8,      /* a pointer is not device memory of the current device */
 };
 
 /* Prefill flags. */
@@ -119,7 +120,11 @@ int triune_hip_gla_decode_step(const void* q, const void* k, const void* v, cons
 /* The reference's own decode-step signatures, for callers that bind them by name (device
  * pointers instead of the reference's host pointers; both run triune_hip_gla_decode_step in
  * place and return nothing, as the reference's do; the status of the last such call on this
- * host thread is triune_hip_last_error()).
+ * host thread is triune_hip_last_error()).  Before launching, each asks the HIP runtime where
+ * every pointer lives (hipPointerGetAttributes): unless all are device memory of the current
+ * device, nothing is launched or written and the status is TRIUNE_ERR_MEMORY.  The reference's
+ * caller of triune_gla_recurrent_step_f32 (triune/ops/_c_bridge.py:259-294) passes host memory
+ * of CPU tensors; it gets that error here, never a kernel on host pointers. 
  *   launch_gla_decode_step: bf16 Q, K, V, Out [B, 1, H, HD] and fp32 G [B, 1, H, HD], fp32
  *     State [B, H, HD, HD] updated in place, all contiguous, on `stream` (a hipStream_t);
  *     HD in {32, 64, 128}.  Replaces: launch_gla_decode_step, csrc/kernels/gla.cu:97-114.

@@ -52,6 +52,7 @@ def test_error_strings_and_codes_match_header():
         "TRIUNE_ERR_WORKSPACE": -5,
         "TRIUNE_ERR_LAUNCH": -6,
         "TRIUNE_ERR_SCRATCH": -7,
+        "TRIUNE_ERR_MEMORY": -8,
     }
     lib = L.lib()
     for c in [0, *codes.values()]:
@@ -60,6 +61,33 @@ def test_error_strings_and_codes_match_header():
 
 
 _FAKE = ctypes.c_void_p(0x1000)  # 16-byte aligned, never dereferenced: validation fails first
+
+
+def test_reference_twins_refuse_host_memory():
+    """The reference's caller of triune_gla_recurrent_step_f32 (triune/ops/_c_bridge.py:259-294,
+    guard at :272) hands over host pointers of CPU fp32 tensors; launch_gla_decode_step's caller
+    (csrc/kernels/gla.cu:97-114) device pointers.  Given host memory, both twins ask the runtime
+    where the pointers live, launch nothing, leave every buffer as it was and report
+    TRIUNE_ERR_MEMORY (-8); the reference's own step on the same rows (the fp64 oracle, which is
+    pinned to it) is what such a caller computes on the CPU."""
+    lib = L.lib()
+    gen = torch.Generator().manual_seed(5)
+    bh, d = 6, 64
+    q, k, v = (torch.randn(bh, d, generator=gen) for _ in range(3))
+    g = torch.nn.functional.logsigmoid(torch.randn(bh, d, generator=gen)) / 16
+    state = 0.1 * torch.randn(bh, d, d, generator=gen)
+    out = torch.full((bh, d), 7.0)
+    before = [t.clone() for t in (q, k, v, g, state, out)]
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    lib.triune_gla_recurrent_step_f32(ptr(q), ptr(k), ptr(v), ptr(g), ptr(state), ptr(out), bh, d)
+    assert lib.triune_hip_last_error() == -8
+    for a, b in zip((q, k, v, g, state, out), before):
+        assert torch.equal(a, b)
+    qb, kb, vb, ob = (t.bfloat16() for t in (q, k, v, out))
+    lib.launch_gla_decode_step(ptr(qb), ptr(kb), ptr(vb), ptr(g), ptr(state), ptr(ob), 1, bh, d, None)
+    assert lib.triune_hip_last_error() == -8
+    assert torch.equal(state, before[4]) and torch.equal(ob, before[5].bfloat16())
+    assert b"device memory" in lib.triune_hip_error_string(-8)
 
 
 def test_output_kernel_event_hook_arms_and_disarms():
@@ -110,6 +138,8 @@ def test_decode_and_gdn_and_scan_validation_errors():
     assert lib.triune_hip_last_error() == -2
     lib.triune_gla_recurrent_step_f32(None, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 1, 64)
     assert lib.triune_hip_last_error() == -1
+    lib.triune_gla_recurrent_step_f32(_FAKE, _FAKE, _FAKE, _FAKE, _FAKE, _FAKE, 1, 48)
+    assert lib.triune_hip_last_error() == -2
     gdn = lib.triune_hip_gdn_prefill
     assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 1, _st(18), None, _FAKE, 1, None, 1, 8, 1, 64, 64, None) == -1
     assert gdn(_FAKE, _FAKE, _FAKE, _FAKE, 1, 1, None, 1, 9, _st(18), None, _FAKE, 1, None, 1, 8, 1, 64, 64, None) == -2

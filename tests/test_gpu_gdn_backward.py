@@ -72,7 +72,8 @@ def _oracle(q, k, v, g, beta, s0, do, ds, kind):
 @pytest.mark.parametrize("T", [1, 7, 16, 17, 33, 100])
 def test_gdn_bwd_fp32(dev, kind, D, T):
     """Every gradient (q, k, v, g, beta, initial state) through the C-ABI entry, fp32, sub-chunk
-    tails (32 tokens per checkpoint at D = 64, 16 at 128)."""
+    tails.  B * H = 6 leaves room for segments walked in parallel: 8 tokens per sub-chunk at D = 64
+    (4 at 128); beta per value column walks one segment of 32-token (16 at 128) sub-chunks."""
     B, H = 2, 3
     q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, kind, seed=T * 7 + D)
     args = [x.to(dev) if x is not None else None for x in (q, k, v, g, beta)]
@@ -212,20 +213,43 @@ def test_zero_tokens(dev):
     assert float((s0.grad - ds).abs().max()) == 0.0
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_more_waves_than_cus_short_sub_chunks(dev, D):
-    """B * H * D / 8 waves above the CU count (256 on MI355X) select the short sub-chunks (1024/D
-    tokens, three workgroups per CU); fp32 against the oracle with a tail past the last
-    checkpoint."""
-    B, T, H = 4, 45, 9 if D == 64 else 5
-    assert B * H * D // 8 > torch.cuda.get_device_properties(dev).multi_processor_count
-    q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, "head", seed=D + 1)
-    args = [x.to(dev) for x in (q, k, v, g, beta)]
-    got = _gdn_bwd(*args, s0.to(dev), _lib.BETA_HEAD, do.to(dev), ds.to(dev))
-    torch.cuda.synchronize()
-    ref = _oracle(q, k, v, g, beta, s0, do, ds, "head")
+def _check_fp32(got, ref):
     for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), got, ref):
+        if r is None:
+            assert x is None, name
+            continue
         assert _rel_err(x, r) <= 1e-5, (name, _rel_err(x, r))
+
+
+@pytest.mark.parametrize("kind", ["none", "head", "key"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_one_segment_short_sub_chunks(dev, kind, D):
+    """More than two waves per CU (B * H * D / 8 > 512 on MI355X's 256 CUs) keep each sequence one
+    segment, walked in sub-chunks of 1024 / D tokens (the plan of the model's D = 128 shape, B = 4,
+    H = 12); fp32 against the oracle with a ragged tail, for each beta kind that can segment."""
+    B, T, H = 4, 45, 17 if D == 64 else 9
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert B * H * D // 8 > 2 * cus
+    q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, kind, seed=D + 3)
+    args = [x.to(dev) if x is not None else None for x in (q, k, v, g, beta)]
+    got = _gdn_bwd(*args, s0.to(dev), KINDS[kind], do.to(dev), ds.to(dev))
+    torch.cuda.synchronize()
+    _check_fp32(got, _oracle(q, k, v, g, beta, s0, do, ds, kind))
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_value_beta_more_waves_than_cus(dev, D):
+    """beta per value column never segments; with more waves than CUs (257-512 on MI355X) it walks
+    sub-chunks of 1024 / D tokens instead of 2048 / D; fp32 against the oracle with a tail past
+    the last checkpoint."""
+    B, T, H = 4, 45, 9 if D == 64 else 5
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert cus < B * H * D // 8 <= 2 * cus
+    q, k, v, g, beta, s0, do, ds = _inputs(B, T, H, D, "value", seed=D + 1)
+    args = [x.to(dev) for x in (q, k, v, g, beta)]
+    got = _gdn_bwd(*args, s0.to(dev), _lib.BETA_VALUE, do.to(dev), ds.to(dev))
+    torch.cuda.synchronize()
+    _check_fp32(got, _oracle(q, k, v, g, beta, s0, do, ds, "value"))
 
 
 @pytest.mark.parametrize("kind", ["none", "head", "key"])

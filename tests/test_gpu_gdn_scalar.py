@@ -136,3 +136,12 @@ def test_scalar_and_per_dim_kernels_agree(dev, monkeypatch):
     monkeypatch.setattr(FG, "_scalar_gdn_enabled", False)
     o2, s2 = _run(q, k, v, gd, beta, None, dev, out_dtype=torch.float32)
     assert _err(o1, o2) <= 1e-4 and _err(s1, s2) <= 1e-4
+
+
+def test_gate_of_unaccepted_shape_is_a_clear_error(dev):
+    """A 4-D gate whose last dim is neither 1, the head dim, nor a stride-0 broadcast (here 32 wide
+    at D = 64) is refused with a ValueError naming the accepted shapes, before any launch."""
+    q, k, v, la, beta, s0 = (x.to(dev) for x in _case(1, 8, 2, 64, "head", seed=3))
+    g = la.unsqueeze(-1).repeat(1, 1, 1, 32)
+    with pytest.raises(ValueError, match=r"\[B, T, H\]"):
+        fast_chunk_gated_deltanet(q, k, v, g, beta=beta)

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libtriune_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 FLAG_TAIL_UNCLAMPED = 0x1

@@ -4,6 +4,7 @@
 #include "kernels.h"
 
 #include <atomic>
+#include <initializer_list>
 #include <map>
 #include <mutex>
 
@@ -218,6 +219,7 @@ const char* triune_hip_error_string(int code) {
         case TRIUNE_ERR_SCRATCH:
             return "problem exceeds the static scratch of the allocation-free entry point "
                    "(use the entry point that takes a workspace)";
+        case TRIUNE_ERR_MEMORY: return "a pointer is not device memory of the current device";
         default: return "unknown error";
     }
 }
@@ -258,8 +260,53 @@ static thread_local int g_last_error = TRIUNE_OK;
 
 int triune_hip_last_error(void) { return g_last_error; }
 
+// The twins' callers hand over pointers whose memory space the reference's own functions never had
+// to ask about: its C step (engine.cpp:419-475) works on host memory, reached from
+// triune/ops/_c_bridge.py:259-294 with CPU tensors only.  A GPU kernel given pageable host memory
+// takes a memory fault (this pool runs without XNACK), so each twin first asks the runtime where
+// every pointer lives and launches only when all of them are device memory of the current device.
+// A failed query (an unknown pointer, or no device) leaves an error in the runtime's last-error
+// slot; it is cleared here so that the caller's next HIP call does not report it.
+}  // extern "C"
+
+namespace {
+
+bool on_current_device(std::initializer_list<const void*> ptrs) {
+    const int dev = current_device();
+    if (dev < 0) {
+        (void)hipGetLastError();
+        return false;
+    }
+    for (const void* p : ptrs) {
+        if (!p) return false;
+        hipPointerAttribute_t at{};
+        if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+        if (at.type != hipMemoryTypeDevice || at.device != dev) return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
 void launch_gla_decode_step(const void* Q, const void* K, const void* V, const float* G, float* State, void* Out,
                             int B, int H, int HD, void* stream) {
+    if (!Q || !K || !V || !G || !State || !Out) {
+        g_last_error = TRIUNE_ERR_NULL;
+        return;
+    }
+    if (B < 0 || H <= 0 || (HD != 32 && HD != 64 && HD != 128)) {
+        g_last_error = TRIUNE_ERR_SHAPE;
+        return;
+    }
+    if (B > 0 && !on_current_device({Q, K, V, G, State, Out})) {
+        g_last_error = TRIUNE_ERR_MEMORY;
+        return;
+    }
     const int64_t row = HD, bat = (int64_t)H * HD;  // contiguous [B, 1, H, HD]
     const int64_t st[10] = {bat, row, bat, row, bat, row, bat, row, bat, row};
     g_last_error = triune_hip_gla_decode_step(Q, K, V, G, TRIUNE_DT_BF16, TRIUNE_DT_F32, st, State, State, nullptr,
@@ -268,6 +315,18 @@ void launch_gla_decode_step(const void* Q, const void* K, const void* V, const f
 
 void triune_gla_recurrent_step_f32(const float* q, const float* k, const float* v, const float* g, float* state,
                                    float* out, int batch_heads, int head_dim) {
+    if (!q || !k || !v || !g || !state || !out) {
+        g_last_error = TRIUNE_ERR_NULL;
+        return;
+    }
+    if (batch_heads < 0 || (head_dim != 32 && head_dim != 64 && head_dim != 128)) {
+        g_last_error = TRIUNE_ERR_SHAPE;
+        return;
+    }
+    if (batch_heads > 0 && !on_current_device({q, k, v, g, state, out})) {
+        g_last_error = TRIUNE_ERR_MEMORY;
+        return;
+    }
     const int64_t row = head_dim;  // contiguous [batch_heads, head_dim] rows: one head per row
     const int64_t st[10] = {row, row, row, row, row, row, row, row, row, row};
     g_last_error = triune_hip_gla_decode_step(q, k, v, g, TRIUNE_DT_F32, TRIUNE_DT_F32, st, state, state, nullptr,
@@ -759,8 +818,10 @@ int triune_hip_gdn_prefill(const void* q, const void* k, const void* v, const vo
 // Gated DeltaNet backward: checkpoints every L tokens, per-slice partial sums.  Where one wave per
 // (b, h, 8 value columns) leaves resident slots free (six one-wave gradient workgroups of about
 // 25 KB of LDS per CU at L = 512 / D), the tokens are cut into segments walked in parallel (not for
-// beta per value column): the gradient kernel's NB segments, each of up to four segments of the
-// lighter kernels (at most about 16 of those per sequence, so the carries stay short).
+// beta per value column): the gradient kernel's NB segments (at most 16), each of up to four
+// segments of the lighter kernels (4 from 3 gradient segments, 2 from 8, 1 from 16: at most 30
+// light segments per sequence, so the serial carries over the segment maps stay short).  With
+// more than two waves per CU (NB < 3) the sequence stays one segment.
 struct GdnBwdPlan {
     int64_t nc, nsl, nq, nseg, segc, bsegc, bsegr;
     int L;
@@ -772,6 +833,7 @@ static GdnBwdPlan plan_gdn_bwd(int64_t B, int64_t T, int64_t H, int D, int beta_
     p.nsl = gdn_bwd_col_slices(D);
     const int64_t waves = B * H * p.nsl, cus = device_cus();
     p.nseg = beta_kind != TRIUNE_BETA_VALUE && waves > 0 ? 6 * cus / waves : 1;
+    if (p.nseg > 16) p.nseg = 16;  // each carry step is a D x D map product, walked serially
     // two segments at 4-token sub-chunks (D = 128, 768 waves) ran no faster than one at 8 tokens
     // and wrote twice the checkpoints: segment from three up
     if (p.nseg < 3) p.nseg = 1;

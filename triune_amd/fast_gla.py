@@ -619,6 +619,9 @@ def _gdn(q, k, v, g, beta, initial_state, beta_kind, out_dtype=None):
     _check_io(q, k, v, g)
     if g.dim() == 3 or g.shape[-1] != q.shape[-1]:  # one gate per (token, head): the per-dim kernels take it broadcast
         sg = _scalar_gate(g)
+        if sg is None:
+            raise ValueError(f"Gated DeltaNet gate of shape {tuple(g.shape)}: expected [B, T, H], [B, T, H, 1], "
+                             "[B, T, H, D] broadcast over the head dim, or [B, T, H, Dk]")
         g = sg.unsqueeze(-1).expand(*sg.shape, q.shape[-1])
     _on_device(beta, initial_state)
     if _needs_grad(q, k, v, g, beta, initial_state):
