@@ -249,54 +249,168 @@ def bench_prep(dev, reps=10):
                          "unit": "GB/s", "frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
+def _graph_us_per_call(calls, restore=None, reps=5):
+    """GPU time per call of `calls` (zero-argument callables) run back to back: they are captured
+    in one HIP graph on a side stream (after a warm-up there), and the replay is timed with events;
+    `restore` (not timed) runs before each replay, e.g. to give in-place operations their raw inputs
+    back.  Median over `reps` replays."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        if restore:
+            restore()
+        for f in calls:
+            f()
+        if restore:
+            restore()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for f in calls:
+                f()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps + 2):
+        if restore:
+            restore()
+            torch.cuda.synchronize()
+        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        b.record()
+        graph.replay()
+        e.record()
+        e.synchronize()
+        times.append(b.elapsed_time(e))
+    times = sorted(times[2:])
+    return times[len(times) // 2] * 1e3 / len(calls)
+
+
 def bench_fused_prefill(dev, reps=20, T=16384):
     """VectorisedGLA's prefill from raw projections (qkv [4, T, 3, 6, 64] and gate logits
-    g [4, T, 6, 64] bf16, fp32 RoPE tables, fp32 S0; the bench line uses T = 1024, the tile
-    VectorisedGLA runs every prefill in, attention.py:458-499): fused_qkv_g_prep_chunk_gla against
-    the two-step pipeline the reference launches (in-place pre-processing, then the prefill)."""
+    g [4, T, 6, 64] bf16, fp32 RoPE tables, fp32 S0; T = 1024 is the tile VectorisedGLA runs every
+    prefill in, attention.py:458-499): fused_qkv_g_prep_chunk_gla as dispatched (one launch where
+    the call fits the single-launch prefill, as at T = 1024), the same entry with the single launch
+    switched off (pre-processing inside the segment-state kernel, then the carry scan and the
+    output kernel; past four chunk-heads per CU the prep pass and then the prefill), and the
+    two-step pipeline the reference launches (in-place pre-processing, then the three-launch
+    prefill).  "us": GPU time per call, calls back to back in a replayed HIP graph, each on its own
+    raw input set (restored before every replay, untimed); "eager_us": one Python call at a time
+    between events, host work included."""
+    import triune_amd.fast_gla as FG
     from triune_amd import fast_chunk_gla, fused_qkv_g_prep_chunk_gla, fused_qkv_g_prep_inplace
     from triune_amd.workloads import gla_algorithmic_bytes
 
     B, H, HD = 4, 6, 64
+    n_sets = 16 if T <= 2048 else 2
     gen = torch.Generator().manual_seed(15)
-    qkv = torch.randn(B, T, 3, H, HD, generator=gen).bfloat16().to(dev)
+    raw_qkv = torch.randn(B, T, 3, H, HD, generator=gen).bfloat16().to(dev)
     # raw gate logits N(3, 1): logsigmoid of them decays about 0.05 nats per token, the scale of
     # config 1's logsigmoid(N(0, 1)) / 16
-    g = (torch.randn(B, T, H, HD, generator=gen) + 3.0).bfloat16().to(dev)
+    raw_g = (torch.randn(B, T, H, HD, generator=gen) + 3.0).bfloat16().to(dev)
     s0 = (0.1 * torch.randn(B, H, HD, HD, generator=gen)).to(dev)
     inv = 1.0 / (10000.0 ** (torch.arange(0, HD, 2, dtype=torch.float32) / HD))
     emb = torch.cat([torch.outer(torch.arange(T, dtype=torch.float32), inv)] * 2, dim=-1)
     cos, sin = emb.cos().to(dev), emb.sin().to(dev)
-    out = torch.empty(B, T, H, HD, device=dev, dtype=torch.bfloat16)
-    # Both pipelines pre-process qkv and g in place, as the reference does: every call gets the raw
-    # inputs restored first (outside its timed region) and is timed by an event pair of its own.
-    raw_qkv, raw_g = qkv.clone(), g.clone()
-    fused = lambda: fused_qkv_g_prep_chunk_gla(qkv, g, cos, sin, initial_state=s0, out=out)  # noqa: E731
+    sets = [(raw_qkv.clone(), raw_g.clone(), torch.empty(B, T, H, HD, device=dev, dtype=torch.bfloat16))
+            for _ in range(n_sets)]
 
-    def two_step():
+    def restore():
+        for qkv, g, _ in sets:
+            qkv.copy_(raw_qkv)
+            g.copy_(raw_g)
+
+    def fused(i):
+        qkv, g, out = sets[i]
+        fused_qkv_g_prep_chunk_gla(qkv, g, cos, sin, initial_state=s0, out=out)
+
+    def two_step(i):
+        qkv, g, out = sets[i]
         fused_qkv_g_prep_inplace(qkv, g, cos, sin)
         fast_chunk_gla(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, initial_state=s0, out=out)
 
     stream = torch.cuda.current_stream()
-    res = {}
-    for name, fn in (("fused", fused), ("prep_then_prefill", two_step)):
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for i in range(10 + reps):
-            qkv.copy_(raw_qkv)
-            g.copy_(raw_g)
-            if i >= 10:
-                ev[i - 10][0].record(stream)
-            fn()
-            if i >= 10:
-                ev[i - 10][1].record(stream)
-        torch.cuda.synchronize()
-        res[name] = sorted(b.elapsed_time(e) for b, e in ev)[reps // 2]  # median
+    res, eager = {}, {}
+    onepass0 = FG.ONEPASS
+    try:
+        for name, fn, onepass in (("fused", fused, True), ("fused_three_launch", fused, False),
+                                  ("prep_then_prefill", two_step, False)):
+            FG.ONEPASS = onepass
+            res[name] = _graph_us_per_call([lambda i=i: fn(i) for i in range(n_sets)], restore)
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for i in range(10 + reps):
+                restore()
+                if i >= 10:
+                    ev[i - 10][0].record(stream)
+                fn(0)
+                if i >= 10:
+                    ev[i - 10][1].record(stream)
+            torch.cuda.synchronize()
+            eager[name] = sorted(b.elapsed_time(e) for b, e in ev)[reps // 2] * 1e3  # median
+    finally:
+        FG.ONEPASS = onepass0
     alg = gla_algorithmic_bytes(B * T * H, HD, HD, 2, 2, 2) + 2 * B * H * HD * HD * 4
-    gbs = alg / (res["fused"] * 1e-3) / 1e9
+    gbs = alg / (res["fused"] * 1e-6) / 1e9
+    from triune_amd._lib import lib as _l
+
+    one = bool(_l().triune_hip_gla_prefill_onepass_supported(B, T, H, HD, 1, 1, 1, 0))
     return {"workload": f"VectorisedGLA prefill from raw projections (B=4, T={T}, H=6, HD=64, bf16, "
-            "RoPE, gate logits N(3,1)): pre-processing inside the chunk kernels", "us": round(res["fused"] * 1e3, 2),
-            "tok_s": round(B * T / (res["fused"] * 1e-3), 1),
-            "prep_then_prefill_us": round(res["prep_then_prefill"] * 1e3, 2), "alg_bytes": alg,
+            "RoPE, gate logits N(3,1))",
+            "path": "single launch (pre-processing, chunk states and outputs)" if one else
+            "pre-processing pass, then the three-launch prefill",
+            "timing": f"GPU time per call: {n_sets} calls on their own input sets back to back in a replayed "
+            "HIP graph; eager_*: one Python call between events",
+            "us": round(res["fused"], 2), "tok_s": round(B * T / (res["fused"] * 1e-6), 1),
+            "fused_three_launch_us": round(res["fused_three_launch"], 2),
+            "prep_then_prefill_us": round(res["prep_then_prefill"], 2),
+            "eager_us": round(eager["fused"], 2), "eager_fused_three_launch_us": round(eager["fused_three_launch"], 2),
+            "eager_prep_then_prefill_us": round(eager["prep_then_prefill"], 2), "alg_bytes": alg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+
+
+def bench_tile_prefill(dev, reps=50, T=1024):
+    """fast_chunk_gla on VectorisedGLA's prefill tile of already pre-processed inputs (B=4, T=1024,
+    H=6, D=64, bf16, fp32 S0, bf16 outputs; the call attention.py:486-494 makes per tile): the
+    single-launch prefill against the three-launch one on the same inputs.  "us": GPU time per call
+    (16 calls on 8 rotating input sets back to back in a replayed HIP graph); "eager_us": one Python
+    call between events."""
+    import triune_amd.fast_gla as FG
+    from triune_amd import fast_chunk_gla
+    from triune_amd.workloads import gla_algorithmic_bytes, gla_inputs
+
+    B, H, D = 4, 6, 64
+    sets = []
+    for i in range(8):
+        q, k, v, g, s0 = (x.to(dev) for x in gla_inputs(B, T, H, D, seed=17 + i, dtype=torch.bfloat16,
+                                                         init_std=0.1))
+        sets.append((q, k, v, g, s0, torch.empty_like(v)))
+    calls = [lambda i=i: fast_chunk_gla(*sets[i % 8][:4], initial_state=sets[i % 8][4], out=sets[i % 8][5])
+             for i in range(16)]
+    stream = torch.cuda.current_stream()
+    res, eager = {}, {}
+    onepass0 = FG.ONEPASS
+    try:
+        for name, onepass in (("onepass", True), ("three_launch", False)):
+            FG.ONEPASS = onepass
+            res[name] = _graph_us_per_call(calls)
+            for _ in range(20):
+                calls[0]()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+            for b, e in ev:
+                b.record(stream)
+                calls[0]()
+                e.record(stream)
+            torch.cuda.synchronize()
+            eager[name] = sorted(b.elapsed_time(e) for b, e in ev)[reps // 2] * 1e3
+    finally:
+        FG.ONEPASS = onepass0
+    alg = gla_algorithmic_bytes(B * T * H, D, D, 2, 2, 2) + 2 * B * H * D * D * 4
+    gbs = alg / (res["onepass"] * 1e-6) / 1e9
+    return {"workload": f"GLA prefill tile (B=4, T={T}, H=6, D=64, bf16 I/O, fp32 S0), fast_chunk_gla",
+            "timing": "GPU time per call: 16 calls back to back in a replayed HIP graph; eager_*: one Python "
+            "call between events",
+            "us": round(res["onepass"], 2), "tok_s": round(B * T / (res["onepass"] * 1e-6), 1),
+            "three_launch_us": round(res["three_launch"], 2), "eager_us": round(eager["onepass"], 2),
+            "eager_three_launch_us": round(eager["three_launch"], 2), "alg_bytes": alg,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 
@@ -728,7 +842,7 @@ def main():
     )
     ap.add_argument(
         "--only",
-        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "gdn_decode", "gdn_bwd", "gdn_bwd128", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan"),
+        choices=("decode", "gdn", "gdn128", "gdn_vbeta", "gdn_decode", "gdn_bwd", "gdn_bwd128", "varlen", "prep", "fused_prefill", "fused_decode", "bwd", "bwd128", "scan", "tile_prefill"),
         default=None,
         help="profiling aid: run one secondary workload alone and print its own JSON line",
     )
@@ -759,7 +873,8 @@ def main():
             res = {"gdn": bench_gdn, "gdn128": bench_gdn128, "gdn_vbeta": bench_gdn_vbeta, "gdn_decode": bench_gdn_decode,
                    "gdn_bwd": bench_gdn_bwd, "gdn_bwd128": bench_gdn_bwd128,
                    "varlen": bench_varlen, "prep": bench_prep, "bwd": bench_bwd, "bwd128": bench_bwd128,
-                   "scan": bench_scan, "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
+                   "scan": bench_scan, "tile_prefill": bench_tile_prefill,
+                   "fused_prefill": lambda d: bench_fused_prefill(d, T=args.fused_prefill_t)}[args.only](dev)
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     # Order: the CPU baselines and the headline's input generation first (the GPU idles
@@ -777,6 +892,8 @@ def main():
                                       "gdn_bwd128": bench_gdn_bwd128(dev),
                                       "varlen": bench_varlen(dev), "prep": bench_prep(dev),
                                       "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
+                                      "fused_prefill_t16k": bench_fused_prefill(dev, T=16384),
+                                      "tile_prefill": bench_tile_prefill(dev),
                                       "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
                                       "bwd128": bench_bwd128(dev),
                                       "scan": bench_scan(dev)}

@@ -173,6 +173,38 @@ int triune_hip_gla_prefill_prep(const void* q, const void* k, const void* v, con
                                 int use_rope, const float* s0, void* o, int o_dtype, float* s_final, int64_t B,
                                 int64_t T, int64_t H, int D, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Single-launch GLA prefill for calls of few chunks (Dk = Dv = D = 64, bf16 or fp16 I/O): one
+ * workgroup per two consecutive 64-token chunks of each (sequence, head); each publishes the state
+ * map of its chunks and folds the earlier ones' into the state it enters with, so pre-processing
+ * (prep != 0), states and outputs take one launch instead of the three of
+ * triune_hip_gla_prefill(_prep).
+ * Arguments as triune_hip_gla_prefill (prep == 0: g_dtype is io_dtype or fp32, flags 0 or
+ * TRIUNE_FLAG_TAIL_UNCLAMPED) or triune_hip_gla_prefill_prep (prep != 0: q, k, g raw projections,
+ * rewritten in place with RoPE(normalize(elu(x) + 1)) / logsigmoid; g_dtype = io_dtype; flags 0;
+ * cos/sin fp32 [T, D] rows cs_stride apart when use_rope).
+ * triune_hip_gla_prefill_onepass_supported says whether a call fits: at most 64 chunks per sequence
+ * and every workgroup resident at once (one per CU: ceil(B * H / 8) x ceil(chunks / 2) at most
+ * CUs / 8); otherwise the entry returns TRIUNE_ERR_SHAPE and launches nothing.
+ * workspace: at least triune_hip_gla_prefill_onepass_workspace_size bytes (16 KB per chunk pair).
+ * ctrl: caller-owned device buffer of at least triune_hip_gla_prefill_onepass_ctrl_size bytes,
+ * 16-byte aligned, ZERO before its first use; each call leaves it ready for the next.  Calls that
+ * share a ctrl buffer must be ordered on one stream (concurrent calls need their own).  Word 2 of
+ * ctrl is an error mask the kernel sets if a wait for earlier chunks ever ran out (bit 0) or their
+ * workgroup ran on another XCD than the reader's (bit 1); neither happens when the hardware hands
+ * workgroups to XCDs round robin, as it does; outputs of a call that sets either are not valid.
+ * Replaces: VectorisedGLA's prefill tile, _fused_qkv_g_prep_inplace_kernel followed by
+ * _triton_chunk_gla_tc_fwd (triune/model/attention.py:14-79, 425-451, 458-499), and
+ * _triton_chunk_gla_tc_fwd / fast_chunk_gla on such calls (triune/kernels/fast_gla.py:318-380, 692-778). */
+int triune_hip_gla_prefill_onepass_supported(int64_t B, int64_t T, int64_t H, int D, int io_dtype, int g_dtype,
+                                             int prep, int flags);
+size_t triune_hip_gla_prefill_onepass_workspace_size(int64_t B, int64_t T, int64_t H, int D);
+size_t triune_hip_gla_prefill_onepass_ctrl_size(int64_t B, int64_t T, int64_t H, int D);
+int triune_hip_gla_prefill_onepass(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                   int g_dtype, const int64_t* strides, const float* cos, const float* sin,
+                                   int64_t cs_stride, int prep, int use_rope, const float* s0, void* o, int o_dtype,
+                                   float* s_final, int64_t B, int64_t T, int64_t H, int D, int flags, void* workspace,
+                                   size_t workspace_bytes, void* ctrl, size_t ctrl_bytes, void* stream);
+
 /* triune_hip_gla_prefill without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  The workspace is a static device array of

@@ -21,6 +21,16 @@ TOL16 = 2e-3  # bf16 / fp16 I/O, fp32 accumulation and outputs
 TOL32 = 1e-5  # fp32 I/O
 
 
+@pytest.fixture(autouse=True, params=["onepass", "three_launch"])
+def prefill_path(request, monkeypatch):
+    """Every case on both dense paths: calls of few chunks (head dim 64, 16-bit I/O) take the
+    single-launch prefill unless it is switched off."""
+    import triune_amd.fast_gla as FG
+
+    monkeypatch.setattr(FG, "ONEPASS", request.param == "onepass")
+    return request.param
+
+
 def _run(q, k, v, g, s0, dev, out_dtype=torch.float32, **kw):
     qd, kd, vd, gd = (x.to(dev) for x in (q, k, v, g))
     out = torch.empty(v.shape, device=dev, dtype=out_dtype)

@@ -187,6 +187,16 @@ def test_fused_decode_steps_equal_prep_then_decode(dev):
 # scan then runs on those rounded values.  Checked in two parts: the values left in qkv and g
 # against oracle.qkv_g_prep (one ULP of the I/O dtype), and the outputs and final states against
 # oracle.gla_fwd on the values the device left (2e-3 for fp32 outputs, one bf16 ULP + 2e-3 for
+
+@pytest.fixture(params=["onepass", "three_launch"])
+def prefill_path(request, monkeypatch):
+    """The fused pre-processing prefill on both paths: calls of few chunks at head dim 64 take the
+    single launch unless it is switched off."""
+    import triune_amd.fast_gla as FG
+
+    monkeypatch.setattr(FG, "ONEPASS", request.param == "onepass")
+    return request.param
+
 # bf16 outputs).
 def _fused_case(B, T, H, HD, seed, dtype=torch.bfloat16, gate_shift=0.0):
     gen = torch.Generator().manual_seed(seed)
@@ -216,7 +226,7 @@ def _check_prepped(qd, gd_pre, qkv, g, cos, sin):
 @pytest.mark.parametrize("HD", [32, 64, 128])
 @pytest.mark.parametrize("T", [200, 301])
 @pytest.mark.parametrize("rope", [True, False])
-def test_fused_prep_prefill_matches_oracle(dev, HD, T, rope):
+def test_fused_prep_prefill_matches_oracle(prefill_path, dev, HD, T, rope):
     """T = 200 runs the unchecked-row instances with a partial last chunk, T = 301 the checked ones;
     fp32 outputs in a separate buffer, so g keeps the pre-processed gate for the check."""
     from triune_amd import fused_qkv_g_prep_chunk_gla
@@ -238,7 +248,7 @@ def test_fused_prep_prefill_matches_oracle(dev, HD, T, rope):
 
 @pytest.mark.parametrize("HD", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_fused_prep_prefill_out_over_g(dev, HD, dtype):
+def test_fused_prep_prefill_out_over_g(prefill_path, dev, HD, dtype):
     """The reference's call shape (attention.py:443-451): outputs written over g in the I/O dtype."""
     from triune_amd import fused_qkv_g_prep_chunk_gla
 
@@ -260,7 +270,7 @@ def test_fused_prep_prefill_out_over_g(dev, HD, dtype):
     assert float(np.abs(s.cpu().numpy() - rs).max()) <= 2e-3
 
 
-def test_fused_prep_prefill_tokenwise_chunks_and_no_final(dev):
+def test_fused_prep_prefill_tokenwise_chunks_and_no_final(prefill_path, dev):
     """Very negative raw gates (logsigmoid(g) ~ g) push chunks past the factored decay range: the
     output kernel runs them token by token on the pre-processed values; outputs over g."""
     from triune_amd import fused_qkv_g_prep_chunk_gla
@@ -286,7 +296,7 @@ def test_fused_prep_prefill_tokenwise_chunks_and_no_final(dev):
     assert s3.numel() == 1
 
 
-def test_fused_prep_prefill_equals_prep_then_prefill(dev):
+def test_fused_prep_prefill_equals_prep_then_prefill(prefill_path, dev):
     """Against this library's two-step pipeline (the in-place prep kernel, then the prefill): the
     processed tensors agree to one ULP plus 1e-6 (the two kernels round the same fp32 values, formed
     in a different order), and so do the outputs up to what such one-ULP input differences move."""
@@ -310,7 +320,7 @@ def test_fused_prep_prefill_equals_prep_then_prefill(dev):
     assert float((sf - s2).abs().max()) <= 2.0**-7 * float(s2.abs().max())
 
 
-def test_fused_prep_prefill_large_call_takes_two_step_path(dev):
+def test_fused_prep_prefill_large_call_takes_two_step_path(prefill_path, dev):
     """B * H * chunks beyond four per compute unit: the entry runs the prep kernel and then the
     prefill (the faster arrangement there); same checks as the fused path."""
     from triune_amd import fused_qkv_g_prep_chunk_gla

@@ -60,6 +60,14 @@ def _bind(lib):
              _vp],
             _i,
         ),
+        "triune_hip_gla_prefill_onepass_supported": ([_i64, _i64, _i64, _i, _i, _i, _i, _i], _i),
+        "triune_hip_gla_prefill_onepass_workspace_size": ([_i64, _i64, _i64, _i], _sz),
+        "triune_hip_gla_prefill_onepass_ctrl_size": ([_i64, _i64, _i64, _i], _sz),
+        "triune_hip_gla_prefill_onepass": (
+            [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _i64, _i, _i, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i,
+             _vp, _sz, _vp, _sz, _vp],
+            _i,
+        ),
         "triune_hip_gla_prefill_noalloc_max_bytes": ([], _sz),
         "triune_hip_gla_prefill_noalloc": (
             [_vp, _vp, _vp, _vp, _i, _i, _i64p, _vp, _vp, _i, _vp, _i64, _i64, _i64, _i, _i, _i, _vp],
@@ -136,6 +144,10 @@ EXPORTS = (
     "triune_hip_gla_prefill_workspace_size",
     "triune_hip_gla_prefill",
     "triune_hip_gla_prefill_prep",
+    "triune_hip_gla_prefill_onepass_supported",
+    "triune_hip_gla_prefill_onepass_workspace_size",
+    "triune_hip_gla_prefill_onepass_ctrl_size",
+    "triune_hip_gla_prefill_onepass",
     "triune_hip_gla_prefill_noalloc_max_bytes",
     "triune_hip_gla_prefill_noalloc",
     "triune_hip_gla_prefill_varlen_workspace_size",
@@ -196,3 +208,19 @@ def strides(*pairs) -> ctypes.Array:
 
 def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+_CTRL: dict = {}
+
+
+def onepass_ctrl(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The control block of triune_hip_gla_prefill_onepass for calls on the current stream of
+    `device`: zero when first made, left ready for the next call by every call, one per (device,
+    stream) so that calls on different streams never share one.  Grown (as a new zeroed block)
+    when a call needs more flags than the block holds."""
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    blk = _CTRL.get(key)
+    if blk is None or blk.numel() < nbytes:
+        blk = torch.zeros(max(int(nbytes), 4096), device=device, dtype=torch.uint8)
+        _CTRL[key] = blk
+    return blk

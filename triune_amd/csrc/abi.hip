@@ -484,6 +484,128 @@ int triune_hip_gla_prefill_prep(const void* q, const void* k, const void* v, con
 
 namespace {
 
+// Single-launch prefill plan: one workgroup per two 64-token chunks; each XCD runs the chunk pairs
+// of ceil(B * H / 8) (sequence, head) pairs, which must all be resident at once on its CUs (a
+// workgroup waits for the earlier chunk pairs of its (sequence, head)).  The fold reads every
+// earlier pair's map, so pairs per sequence stay at most gla_onepass_max_pairs() (32).
+constexpr size_t kOnePassHdrBytes = 64;
+
+int64_t onepass_pairs(int64_t T) { return ((T + 63) / 64 + 1) / 2; }
+
+int onepass_slots_per_xcd() {
+    static std::atomic<int> cache[kMaxDevices];
+    const int dev = current_device();
+    if (dev >= 0) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    const int slots = device_cus() / 8 * gla_onepass_blocks_per_cu();
+    if (dev >= 0 && slots > 0) cache[dev].store(slots, std::memory_order_relaxed);
+    return slots;
+}
+
+bool onepass_fits(int64_t B, int64_t T, int64_t H, int D) {
+    if (B <= 0 || T <= 0 || H <= 0 || D != 64) return false;
+    const int64_t np = onepass_pairs(T), bh = B * H;
+    if (np > gla_onepass_max_pairs() || bh > 0x7fffffff / np) return false;
+    return (bh + 7) / 8 * np <= onepass_slots_per_xcd();
+}
+
+size_t onepass_ws_bytes(int64_t B, int64_t T, int64_t H, int D) {
+    const int64_t n = B * H * onepass_pairs(T);
+    return align_up((size_t)n * D * D * sizeof(float)) + align_up((size_t)n * D * sizeof(float));
+}
+
+size_t onepass_ctrl_bytes(int64_t B, int64_t T, int64_t H) {
+    return kOnePassHdrBytes + align_up((size_t)(B * H * onepass_pairs(T)) * sizeof(uint64_t));
+}
+
+}  // namespace
+
+extern "C" {
+
+int triune_hip_gla_prefill_onepass_supported(int64_t B, int64_t T, int64_t H, int D, int io_dtype, int g_dtype,
+                                             int prep, int flags) {
+    if (!gla_onepass_dtypes_ok(io_dtype, g_dtype, prep != 0)) return 0;
+    if ((flags & ~TRIUNE_FLAG_TAIL_UNCLAMPED) != 0 || (prep && flags != 0)) return 0;
+    return onepass_fits(B, T, H, D) ? 1 : 0;
+}
+
+size_t triune_hip_gla_prefill_onepass_workspace_size(int64_t B, int64_t T, int64_t H, int D) {
+    if (B <= 0 || T <= 0 || H <= 0 || D != 64) return 0;
+    return onepass_ws_bytes(B, T, H, D);
+}
+
+size_t triune_hip_gla_prefill_onepass_ctrl_size(int64_t B, int64_t T, int64_t H, int D) {
+    if (B <= 0 || T <= 0 || H <= 0 || D != 64) return 0;
+    return onepass_ctrl_bytes(B, T, H);
+}
+
+int triune_hip_gla_prefill_onepass(const void* q, const void* k, const void* v, const void* g, int io_dtype,
+                                   int g_dtype, const int64_t* strides, const float* cos, const float* sin,
+                                   int64_t cs_stride, int prep, int use_rope, const float* s0, void* o, int o_dtype,
+                                   float* s_final, int64_t B, int64_t T, int64_t H, int D, int flags, void* workspace,
+                                   size_t workspace_bytes, void* ctrl, size_t ctrl_bytes, void* stream) {
+    if (!q || !k || !v || !g || !o || !strides || (prep && use_rope && (!cos || !sin))) return TRIUNE_ERR_NULL;
+    if (!dtype_ok(io_dtype) || !dtype_ok(g_dtype) || !dtype_ok(o_dtype)) return TRIUNE_ERR_DTYPE;
+    if (!gla_onepass_dtypes_ok(io_dtype, g_dtype, prep != 0)) return TRIUNE_ERR_DTYPE;
+    if (B < 0 || T < 0 || H <= 0 || D != 64) return TRIUNE_ERR_SHAPE;
+    if ((flags & ~TRIUNE_FLAG_TAIL_UNCLAMPED) != 0 || (prep && flags != 0)) return TRIUNE_ERR_SHAPE;
+    if (!vec_ok(q, io_dtype, strides + 0, 3) || !vec_ok(k, io_dtype, strides + 3, 3) ||
+        !vec_ok(v, io_dtype, strides + 6, 3) || !vec_ok(g, g_dtype, strides + 9, 3) ||
+        !vec_ok(o, o_dtype, strides + 12, 3) || reinterpret_cast<uintptr_t>(s0) % 16 ||
+        reinterpret_cast<uintptr_t>(s_final) % 16 || !tok_strides_ok(strides, io_dtype, g_dtype, o_dtype, D, D))
+        return TRIUNE_ERR_LAYOUT;
+    if (prep && use_rope &&
+        (!vec_ok(cos, TRIUNE_DT_F32, &cs_stride, 1) || !vec_ok(sin, TRIUNE_DT_F32, &cs_stride, 1) || cs_stride < D ||
+         (64 * cs_stride + D) * 4 >= ((int64_t)1 << 31)))
+        return TRIUNE_ERR_LAYOUT;
+    if (B == 0 || T == 0) return TRIUNE_ERR_SHAPE;  // nothing for a chunk kernel: the caller's other paths
+    if (!onepass_fits(B, T, H, D)) return TRIUNE_ERR_SHAPE;
+    if (!workspace || workspace_bytes < onepass_ws_bytes(B, T, H, D)) return TRIUNE_ERR_WORKSPACE;
+    if (!ctrl || ctrl_bytes < onepass_ctrl_bytes(B, T, H)) return TRIUNE_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 || reinterpret_cast<uintptr_t>(ctrl) % 16)
+        return TRIUNE_ERR_LAYOUT;
+    const int64_t nch = (T + 63) / 64, npair = onepass_pairs(T), n = B * H * npair;
+    char* ws = reinterpret_cast<char*>(workspace);
+    PrefillParams a{};
+    fill_tok(a.q, q, strides + 0, B, T, H, D, io_dtype);
+    fill_tok(a.k, k, strides + 3, B, T, H, D, io_dtype);
+    fill_tok(a.v, v, strides + 6, B, T, H, D, io_dtype);
+    fill_tok(a.g, g, strides + 9, B, T, H, D, g_dtype);
+    a.o = o; a.o_sb = strides[12]; a.o_st = strides[13]; a.o_sh = strides[14];
+    a.g_dt = g_dtype; a.o_dt = o_dtype;
+    a.s0 = s0;
+    a.seq_final = s_final;
+    a.ws_state = reinterpret_cast<float*>(ws);
+    a.ws_gamma = reinterpret_cast<float*>(ws + align_up((size_t)n * D * D * sizeof(float)));
+    a.n_seqs = B; a.H = H; a.T = T; a.Dk = D; a.Dv = D;
+    a.P = 1; a.nseg_dense = (int)nch; a.varlen = 0; a.flags = flags & TRIUNE_FLAG_TAIL_UNCLAMPED;
+    a.use_rope = prep && use_rope ? 1 : 0;
+    if (a.use_rope) {  // [T, D] tables shared by every sequence and head (batch and head strides 0)
+        const int64_t cst[3] = {0, cs_stride, 0};
+        fill_tok(a.cs, cos, cst, 1, T, 1, D, TRIUNE_DT_F32);
+        fill_tok(a.sn, sin, cst, 1, T, 1, D, TRIUNE_DT_F32);
+    }
+    OnePassCtl c{};
+    c.hdr = reinterpret_cast<uint32_t*>(ctrl);
+    c.flags = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(ctrl) + kOnePassHdrBytes);
+    c.nch = nch;
+    c.npair = npair;
+    c.nh8 = (B * H + 7) / 8;
+    const OutputEvents ev = g_output_events;  // the measurement hook brackets the one kernel
+    hipStream_t st = (hipStream_t)stream;
+    if (ev.begin && hipEventRecord(ev.begin, st) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    const int rc = launch_status(launch_gla_onepass(a, c, io_dtype, prep != 0, st));
+    if (rc != TRIUNE_OK) return rc;
+    if (ev.end && hipEventRecord(ev.end, st) != hipSuccess) return TRIUNE_ERR_LAUNCH;
+    return TRIUNE_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
 // Allocation-free prefill: the workspace of triune_hip_gla_prefill lives in this file-scope
 // device array instead of a caller buffer.  Each GPU holds its own copy until the process ends;
 // host code must use the address hipGetSymbolAddress returns for the current device (the

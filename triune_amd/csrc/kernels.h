@@ -198,6 +198,19 @@ struct FusedDecodeParams {
     int64_t n_state_rows;
 };
 
+// Control block of the single-launch prefill (gla_onepass.hip): hdr[0] epoch, hdr[1] finished
+// workgroups, hdr[2] error bits (1: a wait for an earlier chunk pair ran out; 2: a pair's map was
+// written on another XCD than its reader's); flags[bh * npair + p] = the epoch + 1 of the call that
+// published chunk pair p of (sequence, head) bh (low 32 bits) and the XCD its workgroup ran on
+// (high 32 bits).
+struct OnePassCtl {
+    uint32_t* hdr;
+    uint64_t* flags;
+    int64_t nch;    // chunks per sequence
+    int64_t npair;  // chunk pairs per sequence: ceil(nch / 2), one workgroup each
+    int64_t nh8;    // (sequence, head) pairs per XCD: ceil(B * H / 8)
+};
+
 hipError_t launch_recurrent_scan(const ScanParams& a, hipStream_t stream);
 hipError_t launch_recurrent_scan_bwd(const ScanBwdParams& a, hipStream_t stream);
 bool gla_bwd_supported(int D, int io_dt);
@@ -236,5 +249,12 @@ bool prefill_dtype_supported(int Dk, int Dv, int io_dt);
 bool prefill_prep_supported(int D, int io_dt);
 hipError_t launch_gla_prep_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 int gla_seg_output_blocks_per_cu(int Dk, int Dv, bool ck);
+// Single-launch prefill (one workgroup per two 64-token chunks, Dk = Dv = 64, 16-bit I/O; prep: q,
+// k, g raw projections pre-processed in place).  Every workgroup of the grid must be resident at once.
+unsigned gla_onepass_grid(int64_t BH, int64_t npair);
+int gla_onepass_max_pairs();
+int gla_onepass_blocks_per_cu();
+bool gla_onepass_dtypes_ok(int io_dt, int g_dt, bool prep);
+hipError_t launch_gla_onepass(const PrefillParams& a, const OnePassCtl& c, int io_dt, bool prep, hipStream_t stream);
 
 }  // namespace triune

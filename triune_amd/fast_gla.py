@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from ._lib import TriuneHipError, check, dtype_code, lib, ptr, stream_of, strides
+from ._lib import TriuneHipError, check, dtype_code, lib, onepass_ctrl, ptr, stream_of, strides
 
 __all__ = [
     "fast_chunk_gla",
@@ -117,6 +117,12 @@ def _gate(g, q):
     return g if g.dtype in (q.dtype, torch.float32) else g.float()
 
 
+# Calls of few chunks (at most 64 per sequence, every chunk-head workgroup resident at once, head
+# dim 64, 16-bit I/O) run the single-launch prefill; False forces the three-launch path (tests
+# cover both).
+ONEPASS = True
+
+
 def _prefill(q, k, v, g, initial_state, out, flags, save_final=True, out_dtype=None):
     B, T, H, Dk0 = q.shape
     Dv0 = v.shape[-1]
@@ -154,14 +160,27 @@ def _prefill(q, k, v, g, initial_state, out, flags, save_final=True, out_dtype=N
     s0 = _state_in(initial_state, Dk, Dv)
     sf = torch.empty(B, H, Dk, Dv, device=q.device, dtype=torch.float32) if save_final else None
     L = lib()
-    wsb = L.triune_hip_gla_prefill_workspace_size(B, T, H, Dk, Dv, flags)
-    ws = torch.empty(max(int(wsb), 256), device=q.device, dtype=torch.uint8)
     st = strides(_tok3(qp), _tok3(kp), _tok3(vp), _tok3(gp), _tok3(o))
-    rc = L.triune_hip_gla_prefill(
-        ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, ptr(s0), ptr(o), dtype_code(o),
-        ptr(sf), B, T, H, Dk, Dv, flags, ptr(ws), ws.numel(), stream_of(q),
-    )
-    check(rc, "triune_hip_gla_prefill")
+    if ONEPASS and Dk == Dv == 64 and L.triune_hip_gla_prefill_onepass_supported(
+            B, T, H, 64, dtype_code(qp), dtype_code(gp), 0, flags):
+        # few chunks: states and outputs in one launch (triune_hip_gla_prefill_onepass)
+        ws = torch.empty(int(L.triune_hip_gla_prefill_onepass_workspace_size(B, T, H, 64)), device=q.device,
+                         dtype=torch.uint8)
+        ctrl = onepass_ctrl(q.device, int(L.triune_hip_gla_prefill_onepass_ctrl_size(B, T, H, 64)))
+        rc = L.triune_hip_gla_prefill_onepass(
+            ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, None, None, 0, 0, 0, ptr(s0),
+            ptr(o), dtype_code(o), ptr(sf), B, T, H, 64, flags, ptr(ws), ws.numel(), ptr(ctrl), ctrl.numel(),
+            stream_of(q),
+        )
+        check(rc, "triune_hip_gla_prefill_onepass")
+    else:
+        wsb = L.triune_hip_gla_prefill_workspace_size(B, T, H, Dk, Dv, flags)
+        ws = torch.empty(max(int(wsb), 256), device=q.device, dtype=torch.uint8)
+        rc = L.triune_hip_gla_prefill(
+            ptr(qp), ptr(kp), ptr(vp), ptr(gp), dtype_code(qp), dtype_code(gp), st, ptr(s0), ptr(o), dtype_code(o),
+            ptr(sf), B, T, H, Dk, Dv, flags, ptr(ws), ws.numel(), stream_of(q),
+        )
+        check(rc, "triune_hip_gla_prefill")
     if o is not out:
         res = o[..., :Dv0]
         if out is not None:

@@ -24,7 +24,7 @@ from __future__ import annotations
 
 import torch
 
-from ._lib import check, dtype_code, lib, ptr, stream_of, strides
+from ._lib import check, dtype_code, lib, onepass_ctrl, ptr, stream_of, strides
 
 __all__ = ["fused_qkv_g_prep_inplace", "fused_qkvg_decode_step", "fused_qkvg_decode_step_pool",
            "fused_qkv_g_prep_chunk_gla"]
@@ -184,7 +184,11 @@ def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin
     leaves them) and forms the segment states from those values; the output kernel then reads the
     processed tensors.
 
-    The fused form runs while the call is small enough for the chunk kernels to be latency-bound
+    Calls of at most 64 chunks per sequence whose chunk-head workgroups are all resident at once
+    (head dim 64; B = 4, H = 6, T = 1024 is 384 of them) run everything in one launch,
+    triune_hip_gla_prefill_onepass: each workgroup pre-processes its chunk, publishes the chunk's
+    local state, folds the earlier chunks' into the state it enters with and writes its outputs.
+    Otherwise the fused form runs while the call is small enough for the chunk kernels to be latency-bound
     (B * H * ceil(T / 64) at most 4 per compute unit, as at VectorisedGLA's 1024-token prefill tiles,
     attention.py:458-499: 35.0 against 36.1 us for the two-step pipeline at B = 4, H = 6, T = 1024
     on MI355X).  Past that the kernels are throughput-bound and the pre-processing work weighs more
@@ -209,7 +213,12 @@ def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin
         raise TypeError("qkv and g must share one 16-bit dtype (bfloat16 or float16)")
     from .fast_gla import _tok3, _triton_chunk_gla_tc_fwd, _vec_layout
 
-    if B * H * ((T + 63) // 64) > 4 * torch.cuda.get_device_properties(qkv.device).multi_processor_count:
+    from . import fast_gla as _fg
+
+    L = lib()
+    onepass = _fg.ONEPASS and HD == 64 and bool(
+        L.triune_hip_gla_prefill_onepass_supported(B, T, H, HD, dtype_code(qkv), dtype_code(qkv), 1, 0))
+    if not onepass and B * H * ((T + 63) // 64) > 4 * torch.cuda.get_device_properties(qkv.device).multi_processor_count:
         fused_qkv_g_prep_inplace(qkv, g, cos, sin, use_rope=use_rope)
         return _triton_chunk_gla_tc_fwd(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, initial_state=initial_state,
                                         out=g if out is None else out, save_final=save_final)
@@ -233,16 +242,26 @@ def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin
         cs_st = cos.stride(0)
     s0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
     sf = torch.empty(B, H, HD, HD, device=qkv.device, dtype=torch.float32) if save_final else None
-    L = lib()
-    wsb = L.triune_hip_gla_prefill_workspace_size(B, T, H, HD, HD, 0)
-    ws = torch.empty(max(int(wsb), 256), device=qkv.device, dtype=torch.uint8)
     st = strides(_tok3(q), _tok3(k), _tok3(v), _tok3(gp), _tok3(o))
-    rc = L.triune_hip_gla_prefill_prep(
-        ptr(q), ptr(k), ptr(v), ptr(gp), dtype_code(q), st, ptr(cos) if use_rope else None,
-        ptr(sin) if use_rope else None, cs_st, 1 if use_rope else 0, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
-        B, T, H, HD, ptr(ws), ws.numel(), stream_of(qkv),
-    )
-    check(rc, "triune_hip_gla_prefill_prep")
+    if onepass:  # pre-processing, states and outputs in one launch
+        ws = torch.empty(int(L.triune_hip_gla_prefill_onepass_workspace_size(B, T, H, HD)), device=qkv.device,
+                         dtype=torch.uint8)
+        ctrl = onepass_ctrl(qkv.device, int(L.triune_hip_gla_prefill_onepass_ctrl_size(B, T, H, HD)))
+        rc = L.triune_hip_gla_prefill_onepass(
+            ptr(q), ptr(k), ptr(v), ptr(gp), dtype_code(q), dtype_code(gp), st, ptr(cos) if use_rope else None,
+            ptr(sin) if use_rope else None, cs_st, 1, 1 if use_rope else 0, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
+            B, T, H, HD, 0, ptr(ws), ws.numel(), ptr(ctrl), ctrl.numel(), stream_of(qkv),
+        )
+        check(rc, "triune_hip_gla_prefill_onepass")
+    else:
+        wsb = L.triune_hip_gla_prefill_workspace_size(B, T, H, HD, HD, 0)
+        ws = torch.empty(max(int(wsb), 256), device=qkv.device, dtype=torch.uint8)
+        rc = L.triune_hip_gla_prefill_prep(
+            ptr(q), ptr(k), ptr(v), ptr(gp), dtype_code(q), st, ptr(cos) if use_rope else None,
+            ptr(sin) if use_rope else None, cs_st, 1 if use_rope else 0, ptr(s0), ptr(o), dtype_code(o), ptr(sf),
+            B, T, H, HD, ptr(ws), ws.numel(), stream_of(qkv),
+        )
+        check(rc, "triune_hip_gla_prefill_prep")
     for dst, src in zip(views, (q, k, v, gp)):  # the in-place results reach copied inputs too
         if src is not dst and not (src is gp and o.data_ptr() == gp.data_ptr()):
             dst.copy_(src)
