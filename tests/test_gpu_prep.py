@@ -338,3 +338,24 @@ def test_fused_prep_prefill_large_call_takes_two_step_path(prefill_path, dev):
     ro, rs = O.gla_fwd(qd[:, :, 0].cpu(), qd[:, :, 1].cpu(), qd[:, :, 2].cpu(), gd.cpu(), s0)
     assert float(np.abs(o.double().cpu().numpy() - ro).max()) <= 2e-3
     assert float(np.abs(s.double().cpu().numpy() - rs).max()) <= 2e-3
+
+
+@pytest.mark.parametrize("B,H", [(1, 3), (4, 6)])
+def test_fused_prep_prefill_config1_length(dev, B, H):
+    """The fused entry at config 1's length (T = 16384): B = 1, H = 3 (768 chunk-heads) runs the
+    pre-processing inside the segment-state kernel, B = 4, H = 6 (6144) the prep pass and then the
+    prefill; both against the oracle on the values the device left (2e-3 for fp32 outputs and
+    states, one ULP of the I/O dtype for the pre-processed tensors)."""
+    from triune_amd import fused_qkv_g_prep_chunk_gla
+
+    T, HD = 16384, 64
+    qkv, g, s0 = _fused_case(B, T, H, HD, seed=B * 100 + H, gate_shift=3.0)
+    cos, sin = _tables(T, HD)
+    qd, gd = qkv.to(dev), g.to(dev)
+    out = torch.empty(B, T, H, HD, device=dev, dtype=torch.float32)
+    o, s = fused_qkv_g_prep_chunk_gla(qd, gd, cos.to(dev), sin.to(dev), initial_state=s0.to(dev), out=out)
+    torch.cuda.synchronize()
+    _check_prepped(qd, gd, qkv, g, cos, sin)
+    ro, rs = O.gla_fwd(qd[:, :, 0].cpu(), qd[:, :, 1].cpu(), qd[:, :, 2].cpu(), gd.cpu(), s0)
+    assert float(np.abs(o.double().cpu().numpy() - ro).max()) <= 2e-3
+    assert float(np.abs(s.double().cpu().numpy() - rs).max()) <= 2e-3
