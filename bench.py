@@ -171,7 +171,7 @@ def bench_decode(steps_total, dev, n_bufs=12):
     }
 
 
-def bench_gdn_decode(dev, steps=64, n_bufs=12):
+def bench_gdn_decode(dev, steps=512, n_bufs=12):
     """Gated DeltaNet decode step (T == 1) at config 2's batch shape (B=256, H=6, D=64), beta per
     head, bf16 q/k/v/g/o, fp32 state, through the C-ABI entry the operator calls
     (triune_hip_gdn_prefill, which runs the decode kernel for T == 1).  `steps` steps in one HIP

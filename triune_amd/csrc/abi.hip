@@ -61,6 +61,11 @@ int device_cus() {
     return ncu;
 }
 
+// Grid cap of the fused decode step, in workgroups per CU: at the config-2 shape (B = 256,
+// H = 6, HD = 64: 1536 rows) 9.2 us per step at 5, 9.9 at 4, 9.7 at 4.5, 11.0 at 5.5 and
+// 10.6 at 6.  The plain and Gated DeltaNet decode steps measured best at 4.
+constexpr int kFusedDecodeBlocksPerCU = 5;
+
 // Resident (segment, head) workgroups the device holds at once: CUs x output-kernel occupancy
 // of the instance that runs (ck: checked row addressing, used unless every sequence length is a
 // multiple of 4).  Queried once per device and cached (host-side runtime queries only; nothing
@@ -1276,7 +1281,7 @@ int triune_hip_gla_fused_decode_step(const void* qkvg, int io_dtype, const int64
     a.has_init = state_in != nullptr; a.save_final = state_out != nullptr;
     a.state_in = state_in; a.state_out = state_out;
     a.o = o; a.o_dt = o_dtype; a.o_sb = o_strides[0]; a.o_sh = o_strides[1];
-    a.B = B; a.H = H; a.max_blocks = 4 * device_cus();
+    a.B = B; a.H = H; a.max_blocks = kFusedDecodeBlocksPerCU * device_cus();
     return launch_status(
         launch_gla_fused_decode(a, HD, io_dtype, use_rope ? cs_dtype : TRIUNE_DT_F32, state_dtype, (hipStream_t)stream));
 }
@@ -1307,7 +1312,7 @@ int triune_hip_gla_fused_decode_step_slots(const void* qkvg, int io_dtype, const
     a.state_in = state_pool; a.state_out = state_pool;
     a.slots = slots; a.n_state_rows = n_slots;
     a.o = o; a.o_dt = o_dtype; a.o_sb = o_strides[0]; a.o_sh = o_strides[1];
-    a.B = B; a.H = H; a.max_blocks = 4 * device_cus();
+    a.B = B; a.H = H; a.max_blocks = kFusedDecodeBlocksPerCU * device_cus();
     return launch_status(
         launch_gla_fused_decode(a, HD, io_dtype, use_rope ? cs_dtype : TRIUNE_DT_F32, state_dtype, (hipStream_t)stream));
 }

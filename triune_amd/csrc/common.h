@@ -184,6 +184,24 @@ __device__ __forceinline__ void store4_dt(void* p, int dt, float a, float b, flo
     }
 }
 
+// Store four floats as dtype dt at byte offset off of a buffer resource: a store whose offset
+// lies past the resource's records is dropped, so lanes (or whole waves) with nothing to store
+// still issue it and every wave keeps the same count of memory operations in flight.
+__device__ __forceinline__ void buffer_store4_dt(__amdgpu_buffer_rsrc_t r, int off, int dt, const f32x4& x) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+    if (dt == DT_F32) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, off, 0, 0);
+    } else if (dt == DT_BF16) {
+        const bf16x4 h = {(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, h), r, off, 0, 0);
+    } else {
+        const f16x4 h = {(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, h), r, off, 0, 0);
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Lane helpers (wave64).
 // ---------------------------------------------------------------------------------------

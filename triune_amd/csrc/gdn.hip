@@ -111,10 +111,12 @@ static hipError_t launch_gdn_t(const GdnParams& a, hipStream_t stream) {
 // once (s0 read, s_final written, nontemporal float4).  The thread layout is the GLA decode
 // step's (gla_decode.hip): a 256-thread block takes one state row (b, h) at a time, thread
 // (rg, cg) owning rows rg*RPT .. rg*RPT+RPT-1 and columns 4*cg .. 4*cg+3, and walks rows
-// blockIdx.x, + gridDim.x, ... with the next row's state loads issued before this row's state
-// is stored.  Two reductions over the row groups per row: the prediction S^T k (before the
-// update; every thread needs its four columns of it) and the readout S'^T q.  beta (BK != NONE)
-// is fp32.
+// blockIdx.x, + gridDim.x, ...  A row loads its q, k, g, v, beta at its top; the next row's
+// state loads are issued after the prediction's reduction and complete before this row's state
+// is stored (a wave's state reads and writes do not overlap: at the config-2 shape 9.3 us per
+// step, against 11.1-11.7 us with the next row's reads in flight during this row's stores).  Two
+// reductions over the row groups per row: the prediction S^T k (before the update; every thread
+// needs its four columns of it) and the readout S'^T q.  beta (BK != NONE) is fp32.
 // ---------------------------------------------------------------------------------------
 template <typename T>
 using DVec4 = T __attribute__((ext_vector_type(4)));
@@ -127,95 +129,128 @@ __global__ __launch_bounds__(DK * DV / (4 * RPT)) void gdn_decode_kernel(GdnPara
     const int cg = tid % CG, rg = tid / CG, r0 = rg * RPT, wave = tid / 64;
     const uint32_t H32 = (uint32_t)a.H;  // rows = B * H < 2^31
     __shared__ f32x4 redp[2][WAVES][CG], redo[2][WAVES][CG];
-    auto fetch = [&](f32x4 (&st)[RPT], uint32_t row) {
-        if (!a.s0) {
-#pragma unroll
-            for (int m = 0; m < RPT; ++m) st[m] = zero4();
-            return;
-        }
-        const float* sin = a.s0 + (int64_t)row * (DK * DV) + (int64_t)r0 * DV + 4 * cg;
-#pragma unroll
-        for (int m = 0; m < RPT; ++m) st[m] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sin + m * DV));
+    // A row's inputs in their storage types until used.
+    struct In {
+        f32x4 st[RPT];
+        DVec4<TIO> q[RPT / 4], k[RPT / 4], v;
+        DVec4<TG> g[RPT / 4];
+        f32x4 bk[BK == BETA_KEY ? RPT / 4 : 1];  // beta per key row (BETA_KEY) or value column (BETA_VALUE)
+        float bh;                                // beta per head
     };
-    uint32_t row = blockIdx.x;
-    f32x4 cur[RPT];
-    fetch(cur, row);
-    for (int buf = 0; row < rows; row += gridDim.x, buf ^= 1) {
+    // The state goes through a buffer resource over the row (no records without s0, or when
+    // `live` is false past the last row: the loads then read zeros and touch no memory), so every
+    // path issues the same loads.
+    const int32_t soff = (r0 * DV + 4 * cg) * 4;
+    auto fetch_small = [&](In& x, uint32_t row) {
         const int64_t b = row / H32, h = row % H32;
-        DVec4<TIO> q4[RPT / 4], k4[RPT / 4], v4;
-        DVec4<TG> g4[RPT / 4];
-        {
-            const DVec4<TIO>* qp = reinterpret_cast<const DVec4<TIO>*>(reinterpret_cast<const TIO*>(a.q) + b * a.q_sb + h * a.q_sh + r0);
-            const DVec4<TIO>* kp = reinterpret_cast<const DVec4<TIO>*>(reinterpret_cast<const TIO*>(a.k) + b * a.k_sb + h * a.k_sh + r0);
-            const DVec4<TG>* gp = reinterpret_cast<const DVec4<TG>*>(reinterpret_cast<const TG*>(a.g) + b * a.g_sb + h * a.g_sh + r0);
+        const TIO* q = reinterpret_cast<const TIO*>(a.q) + b * a.q_sb + h * a.q_sh + r0;
+        const TIO* k = reinterpret_cast<const TIO*>(a.k) + b * a.k_sb + h * a.k_sh + r0;
+        const TG* g = reinterpret_cast<const TG*>(a.g) + b * a.g_sb + h * a.g_sh + r0;
 #pragma unroll
-            for (int i = 0; i < RPT / 4; ++i) {
-                q4[i] = qp[i];
-                k4[i] = kp[i];
-                g4[i] = gp[i];
-            }
-            v4 = *reinterpret_cast<const DVec4<TIO>*>(reinterpret_cast<const TIO*>(a.v) + b * a.v_sb + h * a.v_sh + 4 * cg);
+        for (int i = 0; i < RPT / 4; ++i) {
+            x.q[i] = reinterpret_cast<const DVec4<TIO>*>(q)[i];
+            x.k[i] = reinterpret_cast<const DVec4<TIO>*>(k)[i];
+            x.g[i] = reinterpret_cast<const DVec4<TG>*>(g)[i];
         }
+        x.v = *reinterpret_cast<const DVec4<TIO>*>(reinterpret_cast<const TIO*>(a.v) + b * a.v_sb + h * a.v_sh + 4 * cg);
         const float* bp = reinterpret_cast<const float*>(a.beta) + b * a.b_sb + h * a.b_sh;
-        float bh = 1.f;
-        f32x4 bkr[RPT / 4], bvc = f32x4{1.f, 1.f, 1.f, 1.f};
-        if constexpr (BK == BETA_HEAD) bh = bp[0];
+        if constexpr (BK == BETA_HEAD) x.bh = bp[0];
         if constexpr (BK == BETA_KEY) {
 #pragma unroll
-            for (int i = 0; i < RPT / 4; ++i) bkr[i] = reinterpret_cast<const f32x4*>(bp + r0)[i];
+            for (int i = 0; i < RPT / 4; ++i) x.bk[i] = reinterpret_cast<const f32x4*>(bp + r0)[i];
         }
-        if constexpr (BK == BETA_VALUE) bvc = *reinterpret_cast<const f32x4*>(bp + 4 * cg);
+        if constexpr (BK == BETA_VALUE) x.bk[0] = *reinterpret_cast<const f32x4*>(bp + 4 * cg);
+    };
+    auto fetch_state = [&](In& x, uint32_t srow, bool live) {
+        const bool on = live && a.s0 != nullptr;
+        const auto r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.s0) + (on ? (int64_t)srow * (DK * DV) : 0),
+                                                         (short)0, on ? DK * DV * 4 : 0, 0x00020000);
+#pragma unroll
+        for (int m = 0; m < RPT; ++m)
+            x.st[m] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, soff + m * DV * 4, 0, 2));
+    };
+    auto step = [&](In& cur, In& nxt, uint32_t row, int buf) {
+        fetch_small(cur, row);
+        const uint32_t nrow = row + gridDim.x;
+        const bool more = nrow < rows;
+        const int64_t b = row / H32, h = row % H32;
         // prediction S^T k for this thread's four columns
         float p4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < RPT; ++m) {
-            const float km = (float)k4[m / 4][m % 4];
+            const float km = (float)cur.k[m / 4][m % 4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) p4[c] += km * cur[m][c];
+            for (int c = 0; c < 4; ++c) p4[c] += km * cur.st[m][c];
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) p4[c] = xor_group_sum<CG>(p4[c]);
         if ((tid % 64) < CG) redp[buf][wave][cg] = f32x4{p4[0], p4[1], p4[2], p4[3]};
-        __syncthreads();
+        // barriers order LDS only: the loads and stores in flight need not complete before them
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         f32x4 pred = redp[buf][0][cg];
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) pred += redp[buf][w][cg];
+        fetch_state(nxt, nrow, more);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        const f32x4 bvc = BK == BETA_VALUE ? cur.bk[0] : f32x4{1.f, 1.f, 1.f, 1.f};
         float y[4];  // the written values u (beta per value column: beta (.) u)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) y[c] = bvc[c] * ((float)v4[c] - pred[c]);
+        for (int c = 0; c < 4; ++c) y[c] = bvc[c] * ((float)cur.v[c] - pred[c]);
         f32x4 ns[RPT];
         float o4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < RPT; ++m) {
-            const float d = expf(fminf((float)g4[m / 4][m % 4], 0.f));
-            float wm = (float)k4[m / 4][m % 4];
-            if constexpr (BK == BETA_HEAD) wm *= bh;
-            if constexpr (BK == BETA_KEY) wm *= bkr[m / 4][m % 4];
-            const float qm = (float)q4[m / 4][m % 4];
+            const float d = expf(fminf((float)cur.g[m / 4][m % 4], 0.f));
+            float wm = (float)cur.k[m / 4][m % 4];
+            if constexpr (BK == BETA_HEAD) wm *= cur.bh;
+            if constexpr (BK == BETA_KEY) wm *= cur.bk[m / 4][m % 4];
+            const float qm = (float)cur.q[m / 4][m % 4];
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                ns[m][c] = d * cur[m][c] + wm * y[c];
+                ns[m][c] = d * cur.st[m][c] + wm * y[c];
                 o4[c] += qm * ns[m][c];
             }
         }
-        const uint32_t nrow = row + gridDim.x;
-        if (nrow < rows) fetch(cur, nrow);
-        if (a.s_final) {
-            float* sout = a.s_final + (int64_t)row * (DK * DV) + (int64_t)r0 * DV + 4 * cg;
+        {
+            // no records without s_final: the stores are issued all the same and dropped
+            const bool on = a.s_final != nullptr;
+            const auto r = __builtin_amdgcn_make_buffer_rsrc(a.s_final + (on ? (int64_t)row * (DK * DV) : 0), (short)0,
+                                                             on ? DK * DV * 4 : 0, 0x00020000);
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-            for (int m = 0; m < RPT; ++m) __builtin_nontemporal_store(ns[m], reinterpret_cast<f32x4*>(sout + m * DV));
+            for (int m = 0; m < RPT; ++m)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, ns[m]), r, soff + m * DV * 4, 0, 2);
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) o4[c] = xor_group_sum<CG>(o4[c]);
         if ((tid % 64) < CG) redo[buf][wave][cg] = f32x4{o4[0], o4[1], o4[2], o4[3]};
-        __syncthreads();
-        if (tid < CG) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        // the readout: threads tid < CG store columns 4*cg .. 4*cg+3; the others issue the same
+        // store past the row's records (dropped)
+        {
             f32x4 sum = redo[buf][0][cg];
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) sum += redo[buf][w][cg];
-            const int64_t off = b * a.o_sb + h * a.o_sh + 4 * cg;
-            store4_dt(reinterpret_cast<char*>(a.o) + off * dt_size(a.o_dt), a.o_dt, sum[0], sum[1], sum[2], sum[3]);
+            const int ob = dt_size(a.o_dt);
+            const auto rout = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(a.o) + (b * a.o_sb + h * a.o_sh) * ob,
+                                                                (short)0, DV * ob, 0x00020000);
+            buffer_store4_dt(rout, tid < CG ? 4 * cg * ob : DV * ob, a.o_dt, sum);
         }
+    };
+    // Two input sets used in turn, so no loaded state is ever copied between registers.
+    In A, B;
+    uint32_t row = blockIdx.x;
+    fetch_state(A, row, true);
+    while (row < rows) {
+        step(A, B, row, 0);
+        row += gridDim.x;
+        if (row >= rows) break;
+        step(B, A, row, 1);
+        row += gridDim.x;
     }
 }
 

@@ -124,10 +124,10 @@ __global__ __launch_bounds__(256) void gla_prep_kernel(PrepParams a) {
 // ---------------------------------------------------------------------------------------
 // Fused decode: qkvg [B, 4, H, HD] (q, k, v, g raw), cos/sin [HD] of the step's position,
 // state [B, H, HD, HD] in TS (fp32 or the I/O type), o [B, H, HD].  A block walks rows
-// blockIdx.x, + gridDim.x, ... and issues the next row's state loads before storing the current
-// row (as the plain decode kernel does).  State accesses are buffer loads/stores over one row
-// whose record count is 0 without an initial state (loads return 0) or without a state output
-// (stores are dropped), so every path issues the same memory operations.
+// blockIdx.x, + gridDim.x, ... and loads the next row's state while it pre-processes the current
+// row's inputs; the loads complete before the current row is stored.  State accesses are buffer
+// loads/stores over one row whose record count is 0 without an initial state (loads return 0) or
+// without a state output (stores are dropped), so every path issues the same memory operations.
 // ---------------------------------------------------------------------------------------
 template <int HD>
 struct FusedDecodeTiling {
@@ -153,20 +153,27 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
         return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, on ? HD * HD * SB : 0, 0x00020000);
     };
     // State row of (b, h): row itself, or through the pool's slots (-1: b's slot lies outside the
-    // pool, a padded batch row; its buffer resources then hold no records).
+    // pool, a padded batch row; its buffer resources then hold no records).  The slot index is
+    // the same for the whole block and read through the scalar cache (a vector load would need a
+    // wait on every load outstanding before the state address is known).
+    const int32_t nsr = (int32_t)(a.n_state_rows < INT32_MAX ? a.n_state_rows : INT32_MAX);
     auto state_row = [&](uint32_t row) -> int64_t {
         if (!a.slots) return (int64_t)row;
-        const int64_t sl = (int64_t)a.slots[row / H32];
-        return (sl >= 0 && sl < a.n_state_rows) ? sl * a.H + row % H32 : -1;
+        const auto* sp = (const __attribute__((address_space(4))) int32_t*)a.slots;
+        const int32_t sl = sp[row / H32];
+        return (sl >= 0 && sl < nsr) ? (int64_t)sl * a.H + row % H32 : -1;
     };
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     struct Raw {
         u32x4 w[RPT];  // 16-bit states use the first two words
+        int64_t srow;
     };
-    auto fetch = [&](Raw& x, uint32_t row) {
-        const int64_t sr = state_row(row);
-        const auto r = row_rsrc(a.state_in, sr, a.has_init != 0 && sr >= 0);
+    // `live` false: the loads are issued all the same but over a resource of no records (they read
+    // zeros and touch no memory), so every path issues the same loads and waits for the same ones.
+    auto fetch = [&](Raw& x, uint32_t row, bool live) {
+        x.srow = state_row(row);
+        const auto r = row_rsrc(a.state_in, x.srow, live && a.has_init != 0 && x.srow >= 0);
 #pragma unroll
         for (int m = 0; m < RPT; ++m) {
             if constexpr (SB == 4) {
@@ -199,46 +206,68 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
             for (int i = 0; i < 4; ++i) x[i] = (float)v[i];
         }
     };
-    __shared__ f32x4 red[2][WAVES][CG];
-    // One row: compute from `cur`, issue the next row's state loads into `nxt`, store, reduce.
-    auto step = [&](const Raw& cur, Raw& nxt, uint32_t row, int buf) {
+    auto ld4 = [](const auto* p, float* x) {
+        using T = std::remove_const_t<std::remove_pointer_t<decltype(p)>>;
+        const V4<T> v = *reinterpret_cast<const V4<T>*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = (float)v[i];
+    };
+    constexpr int PH = HD / 2;
+    const float rope = a.use_rope ? 1.f : 0.f;
+    // HD <= 64: lane d (mod HD) finishes element d of q and k (HD = 32: lanes 32..63 repeat 0..31,
+    // counted once in the norms).  The RoPE entries of element d are the same for every row (one
+    // position per step) and loaded once; buffer loads over a table of HD entries, or of none when
+    // RoPE is off (they then read zeros and never touch memory, as cos and sin may be null).
+    const int d = lane % HD;
+    float ce = 0.f, se = 0.f;
+    if constexpr (EPL == 1) {
+        if constexpr (sizeof(TCS) == 4) {
+            ce = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcos, d * 4, 0, 0));
+            se = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsin, d * 4, 0, 0));
+        } else {
+            ce = (float)__builtin_bit_cast(TCS, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rcos, d * 2, 0, 0));
+            se = (float)__builtin_bit_cast(TCS, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rsin, d * 2, 0, 0));
+        }
+    }
+    // The row's small inputs for HD <= 64, in their storage type until used: element d of q and k,
+    // this thread's key rows of g and its 4 value columns.
+    struct Small {
+        TIO q, k;
+        V4<TIO> g[RPT / 4], v;
+    };
+    auto row_base = [&](uint32_t row) {
         const int64_t b = row / H32, h = row % H32;
-        const TIO* base = reinterpret_cast<const TIO*>(a.qkvg) + b * a.x_sb + h * a.x_sh;
-        const TIO* qr = base;
-        const TIO* kr = base + a.x_sp;
-        const TIO* vr = base + 2 * a.x_sp;
-        const TIO* gr = base + 3 * a.x_sp;
-        float qv[RPT], kv[RPT], dv[RPT], gg[RPT], vv[4];
-        auto ld4 = [](const auto* p, float* x) {
-            using T = std::remove_const_t<std::remove_pointer_t<decltype(p)>>;
-            const V4<T> v = *reinterpret_cast<const V4<T>*>(p);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = (float)v[i];
-        };
-        constexpr int PH = HD / 2;
-        const float rope = a.use_rope ? 1.f : 0.f;
+        return reinterpret_cast<const TIO*>(a.qkvg) + b * a.x_sb + h * a.x_sh;
+    };
+    auto fetch_small = [&](Small& x, uint32_t row) {
         if constexpr (EPL == 1) {
-            // HD <= 64: lane d (mod HD) finishes element d of q and k once (ELU+1, norm, RoPE with
-            // the partner element d +- HD/2 from lane d ^ HD/2), then every thread gathers its key
-            // rows from those lanes.  All of the row's small loads are issued together: element d
-            // of q, k, cos, sin (buffer loads over a table of HD entries, or of none when RoPE is
-            // off: they then read zeros and never touch memory, as cos and sin may be null), this
-            // thread's key rows of g and its 4 value columns.
-            const int d = lane % HD;  // HD = 32: lanes 32..63 repeat 0..31 (counted once below)
-            const float qe = (float)qr[d], ke = (float)kr[d];
-            float ce, se;
-            if constexpr (sizeof(TCS) == 4) {
-                ce = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rcos, d * 4, 0, 0));
-                se = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsin, d * 4, 0, 0));
-            } else {
-                ce = (float)__builtin_bit_cast(TCS, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rcos, d * 2, 0, 0));
-                se = (float)__builtin_bit_cast(TCS, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rsin, d * 2, 0, 0));
-            }
+            const TIO* base = row_base(row);
+            x.q = base[d];
+            x.k = base[a.x_sp + d];
 #pragma unroll
-            for (int m = 0; m < RPT; m += 4) ld4(gr + r0 + m, gg + m);
-            ld4(vr + 4 * cg, vv);
+            for (int m = 0; m < RPT; m += 4) x.g[m / 4] = *reinterpret_cast<const V4<TIO>*>(base + 3 * a.x_sp + r0 + m);
+            x.v = *reinterpret_cast<const V4<TIO>*>(base + 2 * a.x_sp + 4 * cg);
+        }
+    };
+    __shared__ f32x4 red[2][WAVES][CG];
+    // One row, its state in `cur` (loaded during the previous row): load its small inputs and
+    // pre-process them, issue the next row's state loads into `nxt` (past the last row they read
+    // nothing), wait for every load and store of the wave, then update, store and reduce.  The
+    // wait keeps a wave's state reads and writes from overlapping: at the config-2 shape
+    // (B = 256, H = 6, HD = 64) 9.2 us per step, against 10.1-10.4 us with the next row's
+    // reads in flight during this row's stores (issued before or after them).
+    auto step = [&](const Raw& cur, Raw& nxt, uint32_t row, int buf) {
+        const uint32_t nrow = row + gridDim.x;
+        const bool more = nrow < rows;
+        Small sc;
+        fetch_small(sc, row);
+        const int64_t b = row / H32, h = row % H32;
+        float qv[RPT], kv[RPT], dv[RPT], vv[4];
+        if constexpr (EPL == 1) {
+            // ELU+1, norm and RoPE (partner element d +- HD/2 from lane d ^ HD/2) once per element;
+            // every thread then gathers its key rows from those lanes.
+            const float q1 = elu1((float)sc.q), k1 = elu1((float)sc.k);
             const bool first = lane < HD;
-            const float q1 = elu1(qe), k1 = elu1(ke);
             const float sq = wave_sum(first ? q1 * q1 : 0.f), sk = wave_sum(first ? k1 * k1 : 0.f);
             const float qn = q1 * inv_norm(sq), kn = k1 * inv_norm(sk);
             const float qo = __shfl_xor(qn, PH), ko = __shfl_xor(kn, PH);
@@ -248,20 +277,27 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
             for (int m = 0; m < RPT; ++m) {
                 qv[m] = lane_bcast(qr_d, r0 + m);
                 kv[m] = lane_bcast(kr_d, r0 + m);
-                dv[m] = sigmoid(gg[m]);
+                dv[m] = sigmoid((float)sc.g[m / 4][m % 4]);
             }
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) vv[c4] = (float)sc.v[c4];
         } else {
             // HD = 128 (two elements per lane): each thread forms its key rows and their RoPE
             // partner rows itself; the norm elements, rows, partners, cos/sin and value columns are
-            // loaded together.
-            float qa[EPL], ka[EPL];
+            // loaded together at the top of the row.
+            const TIO* base = row_base(row);
+            const TIO* qr = base;
+            const TIO* kr = base + a.x_sp;
+            const TIO* vr = base + 2 * a.x_sp;
+            const TIO* gr = base + 3 * a.x_sp;
+            float qa[EPL], ka[EPL], gg[RPT];
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
                 qa[e] = (float)qr[lane + 64 * e];
                 ka[e] = (float)kr[lane + 64 * e];
             }
             const int rp = r0 < PH ? r0 + PH : r0 - PH;  // partner rows rp .. rp+RPT-1
-            float qo[RPT], qp[RPT], ko[RPT], kp[RPT], cs[RPT], sn[RPT];
+            float qo[RPT], qp[RPT], ko[RPT], kp[RPT], cs[RPT], sn2[RPT];
 #pragma unroll
             for (int m = 0; m < RPT; m += 4) {
                 ld4(qr + r0 + m, qo + m);
@@ -270,7 +306,7 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
                 ld4(kr + rp + m, kp + m);
                 ld4(gr + r0 + m, gg + m);
                 ld_table4(rcos, (r0 + m) * (int)sizeof(TCS), cs + m);
-                ld_table4(rsin, (r0 + m) * (int)sizeof(TCS), sn + m);
+                ld_table4(rsin, (r0 + m) * (int)sizeof(TCS), sn2 + m);
             }
             ld4(vr + 4 * cg, vv);
             float sq = 0.f, sk = 0.f;
@@ -288,13 +324,15 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
             for (int m = 0; m < RPT; ++m) {
                 const float qn = elu1(qo[m]) * iq, kn = elu1(ko[m]) * ik;
                 const float qn2 = elu1(qp[m]) * iq, kn2 = elu1(kp[m]) * ik;
-                const float c = rope * cs[m] + (1.f - rope), sg = rope * sgn * sn[m];
+                const float c = rope * cs[m] + (1.f - rope), sg = rope * sgn * sn2[m];
                 qv[m] = qn * c + sg * qn2;
                 kv[m] = kn * c + sg * kn2;
                 dv[m] = sigmoid(gg[m]);
             }
         }
 
+        fetch(nxt, more ? nrow : row, more);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         f32x4 y[RPT];
         float o4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -306,7 +344,7 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
                 o4[c] += qv[m] * y[m][c];
             }
         }
-        const int64_t sr = state_row(row);
+        const int64_t sr = cur.srow;
         const auto ro = row_rsrc(a.state_out, sr, a.save_final != 0 && sr >= 0);
 #pragma unroll
         for (int m = 0; m < RPT; ++m) {
@@ -317,31 +355,30 @@ __global__ __launch_bounds__(FusedDecodeTiling<HD>::TPB) void gla_fused_decode_k
                 __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), ro, voff + m * HD * SB, 0, 2);
             }
         }
-        // the next row's state loads go out after this row's stores (a later wait for them then
-        // also covers these stores, which by then have long completed)
-        const uint32_t nrow = row + gridDim.x;
-        if (nrow < rows) fetch(nxt, nrow);
 #pragma unroll
         for (int c = 0; c < 4; ++c) o4[c] = xor_group_sum<CG>(o4[c]);
         if (lane < CG) red[buf][wave][cg] = f32x4{o4[0], o4[1], o4[2], o4[3]};
-        // barrier ordering LDS only: the state stores need not complete before it
+        // barrier ordering LDS only: the state loads and stores in flight need not complete before it
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        if (tid < CG) {
+        // the readout: threads tid < CG store columns 4*cg .. 4*cg+3; the others issue the same
+        // store past the row's records (dropped)
+        {
             f32x4 s = red[buf][0][cg];
 #pragma unroll
             for (int w = 1; w < WAVES; ++w) s += red[buf][w][cg];
             if (sr < 0) s = zero4();
-            store4_dt(reinterpret_cast<char*>(a.o) + (b * a.o_sb + h * a.o_sh + 4 * cg) * dt_size(a.o_dt), a.o_dt, s[0],
-                      s[1], s[2], s[3]);
+            const int ob = dt_size(a.o_dt);
+            const auto rout = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(a.o) + (b * a.o_sb + h * a.o_sh) * ob,
+                                                                (short)0, HD * ob, 0x00020000);
+            buffer_store4_dt(rout, tid < CG ? 4 * cg * ob : HD * ob, a.o_dt, s);
         }
     };
-    // Two register sets used in turn, so no loaded state is ever copied between registers (a copy
-    // would wait for the prefetch before the current row's stores).
+    // Two state register sets used in turn, so no loaded state is ever copied between registers.
     Raw A, B;
     uint32_t row = blockIdx.x;
-    fetch(A, row);
+    fetch(A, row, true);
     while (row < rows) {
         step(A, B, row, 0);
         row += gridDim.x;
