@@ -36,6 +36,11 @@ BF16_PEAK_TFLOPS = 2500.0
 METRIC = "GLA prefill tok/s @B4 H6 T16k D64 (MFMA %); decode tok/s @B256 (HBM GB/s %)"
 
 
+def _progress(msg):
+    """One progress line on stderr as each leg ends (the JSON line stays the only stdout line)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
 def _events_time_ms(fn, iters, stream):
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -73,17 +78,31 @@ def bench_prefill(steps, warmup, dev, inputs=None):
         turn[0] += 1
         fast_chunk_gla(*sets[i], initial_state=s0, out=outs[i])
 
+    # The timed passes are one replay of a HIP graph holding `steps` passes (the same calls, the
+    # two input sets in turn), captured before the warm-up: host-side launch jitter (a stalled
+    # Python loop left the GPU idle for a third of one 20-pass measurement) stays out of the timed
+    # region, and the replay follows the warm-up passes with no idle gap.
+    stream = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        fn()  # first call outside the capture (library load, workspace sizes)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(steps):
+            fn()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    L = lib()
-    # The timed passes: direct calls (host work plus three launches each), nothing else on the
-    # stream between the two events.  The warm-up must be long enough for the clocks to settle
-    # (a few hundred passes; 20 passes leave the pass about 8% slower).
     t0 = time.perf_counter()
-    ms = _events_time_ms(fn, steps, stream)
+    ms = _events_time_ms(graph.replay, 1, stream) / steps
+    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # the same passes as direct calls (host work plus three launches each), for reference
+    eager_ms = _events_time_ms(fn, steps, stream)
+    L = lib()
     # The roofline's kernel time, in a second loop of as many passes: one event pair per pass,
     # recorded by the library on this stream around the output kernel (the dominant of the
     # pass's three kernels).  The records add small bubbles, so this loop is not the timed one.
@@ -106,6 +125,7 @@ def bench_prefill(steps, warmup, dev, inputs=None):
     alg_flops = gla_algorithmic_flops(n_th, D, D)
     return {
         "ms": ms,
+        "eager_ms": eager_ms,
         "wall_s": wall,
         "tok_s": B * T / (ms * 1e-3),
         "alg_bytes": alg_bytes,
@@ -878,26 +898,34 @@ def main():
         print(json.dumps({"only": args.only, **res}), flush=True)
         return
     # Order: the CPU baselines and the headline's input generation first (the GPU idles
-    # meanwhile), then the secondary GPU legs, then the headline prefill, so no leg is timed right
-    # after the GPU sat idle for seconds (clocks ramp down when idle: after an idle gap the first
-    # few hundred passes run up to 13 % slower).  The headline itself does exactly `warmup`
-    # untimed passes before its `steps` timed ones.
-    cpu = None if args.no_cpu else cpu_baseline()
-    cpu_dec = None if args.no_cpu or args.no_decode else cpu_baseline_decode()
+    # meanwhile), then the secondary GPU legs, the last of them a replayed graph with no host gaps,
+    # then the headline prefill, so no leg is timed right after the GPU sat idle (clocks ramp down
+    # when idle: after a 2 s idle gap the first hundred passes run up to 25 % slower, and even
+    # right after other GPU work the first ten run about 6 % slower than the steady state).  The
+    # headline itself does exactly `warmup` untimed passes before its `steps` timed ones.
+    def leg(name, fn, *fa):
+        r = fn(*fa)
+        _progress(f"{name} done")
+        return r
+
+    cpu = None if args.no_cpu else leg("cpu baseline (prefill)", cpu_baseline)
+    cpu_dec = None if args.no_cpu or args.no_decode else leg("cpu baseline (decode)", cpu_baseline_decode)
     pre_in = prefill_inputs(dev)
-    dec = None if args.no_decode else bench_decode(args.decode_steps, dev)
-    extra = {} if args.no_extra else {"gdn": bench_gdn(dev), "gdn128": bench_gdn128(dev),
-                                      "gdn_vbeta": bench_gdn_vbeta(dev), "gdn_decode": bench_gdn_decode(dev),
-                                      "gdn_bwd": bench_gdn_bwd(dev),
-                                      "gdn_bwd128": bench_gdn_bwd128(dev),
-                                      "varlen": bench_varlen(dev), "prep": bench_prep(dev),
-                                      "fused_prefill": bench_fused_prefill(dev, T=args.fused_prefill_t),
-                                      "fused_prefill_t16k": bench_fused_prefill(dev, T=16384),
-                                      "tile_prefill": bench_tile_prefill(dev),
-                                      "fused_decode": bench_fused_decode(args.decode_steps, dev), "bwd": bench_bwd(dev),
-                                      "bwd128": bench_bwd128(dev),
-                                      "scan": bench_scan(dev)}
+    dec = None if args.no_decode else leg("decode", bench_decode, args.decode_steps, dev)
+    extra = {}
+    if not args.no_extra:
+        legs = (("gdn", bench_gdn, dev), ("gdn128", bench_gdn128, dev), ("gdn_vbeta", bench_gdn_vbeta, dev),
+                ("gdn_decode", bench_gdn_decode, dev), ("gdn_bwd", bench_gdn_bwd, dev),
+                ("gdn_bwd128", bench_gdn_bwd128, dev), ("varlen", bench_varlen, dev), ("prep", bench_prep, dev),
+                ("fused_prefill", lambda d: bench_fused_prefill(d, T=args.fused_prefill_t), dev),
+                ("fused_prefill_t16k", lambda d: bench_fused_prefill(d, T=16384), dev),
+                ("tile_prefill", bench_tile_prefill, dev), ("bwd", bench_bwd, dev),
+                ("bwd128", bench_bwd128, dev), ("scan", bench_scan, dev),
+                ("fused_decode", bench_fused_decode, args.decode_steps, dev))
+        for name, fn, *fa in legs:
+            extra[name] = leg(name, fn, *fa)
     pre = bench_prefill(args.steps, args.warmup, dev, pre_in)
+    _progress("headline prefill done")
     line = {
         "metric": METRIC,
         "value": round(pre["tok_s"], 1),
@@ -906,6 +934,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(pre["ms"], 4),
+        "timing": "one HIP-graph replay of the `steps` passes (events around it), after `warmup` direct calls; "
+        f"the same passes as direct calls: {pre['eager_ms']:.4f} ms/pass",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
