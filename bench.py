@@ -103,9 +103,10 @@ def bench_prefill(steps, warmup, dev, inputs=None):
     # the same passes as direct calls (host work plus three launches each), for reference
     eager_ms = _events_time_ms(fn, steps, stream)
     L = lib()
-    # The roofline's kernel time, in a second loop of as many passes: one event pair per pass,
-    # recorded by the library on this stream around the output kernel (the dominant of the
-    # pass's three kernels).  The records add small bubbles, so this loop is not the timed one.
+    # The roofline's kernel time, in a second loop of as many passes: one event pair per pass that
+    # the library attaches to the output kernel's dispatch (the dominant of the pass's three
+    # kernels).  HIP events include the dispatch latency, about 4 us per launch on MI355X, which
+    # rocprofv3's kernel trace leaves out of a kernel's duration.
     k3 = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for b, e in k3:  # torch creates an event on its first record
         b.record(stream)
@@ -959,7 +960,7 @@ def main():
             "unit": "GB/s",
             "frac": round(pre["k3_gbs"] / HBM_PEAK_GBS, 4),
             "traffic": _traffic_from_profiles(),
-            "kernel": "gla_seg_output_kernel<bf16,bf16,64,64> (HIP events around each launch)",
+            "kernel": "gla_seg_output_kernel<bf16,bf16,64,64> (HIP events on its dispatch, one pair per pass)",
             "kernel_us": round(pre["k3_ms"] * 1e3, 2),
             "alg_bytes_per_launch": pre["k3_bytes"],
             "pass": {

@@ -96,10 +96,11 @@ int triune_hip_abi_version(void);
 const char* triune_hip_error_string(int code);
 
 /* Measurement hook (no reference counterpart; for benchmarks and profilers): arm two hipEvent_t
- * (passed as void*) that the following GLA prefill calls (dense and varlen) of this host thread
- * record on their stream immediately before and after the output kernel (the dominant one of the
- * three), so its duration can be read with hipEventElapsedTime.  Both NULL disarms; exactly one
- * NULL returns TRIUNE_ERR_NULL.  Recording adds no device work. */
+ * (passed as void*) that the following GLA prefill calls (dense and varlen: the output kernel,
+ * the dominant one of the three; the single-launch entry: its one kernel) of this host thread
+ * attach to that kernel's dispatch (hipExtLaunchKernel), so its duration can be read with
+ * hipEventElapsedTime (including the dispatch latency, about 4 us on MI355X).  Both NULL
+ * disarms; exactly one NULL returns TRIUNE_ERR_NULL.  Arming adds no device work. */
 int triune_hip_set_output_kernel_events(void* begin, void* end);
 
 /* Batched recurrent decode step, for every row (b, h):

@@ -39,6 +39,8 @@
 // stored.
 #include "gla_prefill.h"
 
+#include <hip/hip_ext.h>
+
 namespace triune {
 
 namespace {
@@ -570,19 +572,24 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
     }
 }
 
+// ev0 / ev1: if not null, events stamped with the kernel's own start and end (hipExtLaunchKernel).
 template <typename TIn, typename TG, bool CK, bool PREP>
-static hipError_t launch_op(const PrefillParams& a, const OnePassCtl& c, unsigned grid, hipStream_t stream) {
-    if (a.o_dt == DT_BF16)
-        hipLaunchKernelGGL((gla_onepass_kernel<TIn, TG, CK, PREP, true>), dim3(grid), dim3(OP_THREADS), 0, stream, a, c);
-    else
-        hipLaunchKernelGGL((gla_onepass_kernel<TIn, TG, CK, PREP, false>), dim3(grid), dim3(OP_THREADS), 0, stream, a, c);
+static hipError_t launch_op(const PrefillParams& a, const OnePassCtl& c, unsigned grid, hipStream_t stream,
+                            hipEvent_t ev0, hipEvent_t ev1) {
+    auto go = [&](auto kern) {
+        if (ev0) hipExtLaunchKernelGGL(kern, dim3(grid), dim3(OP_THREADS), 0, stream, ev0, ev1, 0, a, c);
+        else hipLaunchKernelGGL(kern, dim3(grid), dim3(OP_THREADS), 0, stream, a, c);
+    };
+    if (a.o_dt == DT_BF16) go(gla_onepass_kernel<TIn, TG, CK, PREP, true>);
+    else go(gla_onepass_kernel<TIn, TG, CK, PREP, false>);
     return hipGetLastError();
 }
 
 template <typename TIn, typename TG, bool PREP>
-static hipError_t launch_op_ck(const PrefillParams& a, const OnePassCtl& c, unsigned grid, hipStream_t stream) {
-    return a.T % 4 == 0 ? launch_op<TIn, TG, false, PREP>(a, c, grid, stream)
-                        : launch_op<TIn, TG, true, PREP>(a, c, grid, stream);
+static hipError_t launch_op_ck(const PrefillParams& a, const OnePassCtl& c, unsigned grid, hipStream_t stream,
+                               hipEvent_t ev0, hipEvent_t ev1) {
+    return a.T % 4 == 0 ? launch_op<TIn, TG, false, PREP>(a, c, grid, stream, ev0, ev1)
+                        : launch_op<TIn, TG, true, PREP>(a, c, grid, stream, ev0, ev1);
 }
 
 // Grid: eight XCD lanes x ((sequence, head) pairs per XCD x chunk pairs).
@@ -602,18 +609,19 @@ bool gla_onepass_dtypes_ok(int io_dt, int g_dt, bool prep) {
     return g_dt == io_dt || (!prep && g_dt == DT_F32);
 }
 
-hipError_t launch_gla_onepass(const PrefillParams& a, const OnePassCtl& c, int io_dt, bool prep, hipStream_t stream) {
+hipError_t launch_gla_onepass(const PrefillParams& a, const OnePassCtl& c, int io_dt, bool prep, hipStream_t stream,
+                              hipEvent_t ev0, hipEvent_t ev1) {
     const unsigned grid = gla_onepass_grid(a.n_seqs * a.H, c.npair);
     const bool g32 = a.g_dt == DT_F32;
     if (io_dt == DT_BF16) {
-        if (prep) return launch_op_ck<__bf16, __bf16, true>(a, c, grid, stream);
-        return g32 ? launch_op_ck<__bf16, float, false>(a, c, grid, stream)
-                   : launch_op_ck<__bf16, __bf16, false>(a, c, grid, stream);
+        if (prep) return launch_op_ck<__bf16, __bf16, true>(a, c, grid, stream, ev0, ev1);
+        return g32 ? launch_op_ck<__bf16, float, false>(a, c, grid, stream, ev0, ev1)
+                   : launch_op_ck<__bf16, __bf16, false>(a, c, grid, stream, ev0, ev1);
     }
     if (io_dt == DT_F16) {
-        if (prep) return launch_op_ck<_Float16, _Float16, true>(a, c, grid, stream);
-        return g32 ? launch_op_ck<_Float16, float, false>(a, c, grid, stream)
-                   : launch_op_ck<_Float16, _Float16, false>(a, c, grid, stream);
+        if (prep) return launch_op_ck<_Float16, _Float16, true>(a, c, grid, stream, ev0, ev1);
+        return g32 ? launch_op_ck<_Float16, float, false>(a, c, grid, stream, ev0, ev1)
+                   : launch_op_ck<_Float16, _Float16, false>(a, c, grid, stream, ev0, ev1);
     }
     return hipErrorInvalidValue;
 }

@@ -2,6 +2,8 @@
 // raw q/k/g inputs, dense and varlen, and the varlen plan kernel.
 #include "gla_prefill.h"
 
+#include <hip/hip_ext.h>
+
 namespace triune {
 
 // K0 (varlen): segment offsets from cu_seqlens, one thread block.
@@ -46,17 +48,24 @@ bool prefill_dtype_supported(int Dk, int Dv, int io_dt) {
     return prefill_shape_supported(Dk, Dv) && !(io_dt == DT_F32 && Dk == 128 && Dv == 128);
 }
 
+// ev0 / ev1 (output kernel only): events stamped with the kernel's own start and end
+// (hipExtLaunchKernel), or null.
 template <typename TIn, typename TG, bool CK>
-static hipError_t launch_seg_ck(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
+static hipError_t launch_seg_ck(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream,
+                                hipEvent_t ev0, hipEvent_t ev1) {
     const dim3 grid((unsigned)n_work, (unsigned)a.H);
     const dim3 block((unsigned)(a.Dv * 4));
     constexpr bool OBF_ok = std::is_same<TIn, __bf16>::value;
     const bool obf = OBF_ok && a.o_dt == DT_BF16;
+    auto out = [&](auto kern) {
+        if (ev0 || ev1) hipExtLaunchKernelGGL(kern, grid, block, 0, stream, ev0, ev1, 0, a);
+        else hipLaunchKernelGGL(kern, grid, block, 0, stream, a);
+    };
 #define TRIUNE_SEG_CASE(DK_, DV_)                                                                       \
     if (a.Dk == DK_ && a.Dv == DV_) {                                                                   \
-        if (with_out && obf) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_, CK, OBF_ok>), grid, block, 0, stream, a); \
-        else if (with_out) hipLaunchKernelGGL((gla_seg_output_kernel<TIn, TG, DK_, DV_, CK, false>), grid, block, 0, stream, a); \
-        else hipLaunchKernelGGL((gla_seg_state_kernel<TIn, TG, DK_, DV_, CK>), grid, block, 0, stream, a);          \
+        if (with_out && obf) out(gla_seg_output_kernel<TIn, TG, DK_, DV_, CK, OBF_ok>);                  \
+        else if (with_out) out(gla_seg_output_kernel<TIn, TG, DK_, DV_, CK, false>);                     \
+        else hipLaunchKernelGGL((gla_seg_state_kernel<TIn, TG, DK_, DV_, CK>), grid, block, 0, stream, a); \
         return hipGetLastError();                                                                       \
     }
     TRIUNE_SEG_CASE(64, 64)
@@ -72,21 +81,23 @@ static hipError_t launch_seg_ck(const PrefillParams& a, int64_t n_work, bool wit
 // Unchecked row addressing only when every sequence is a whole number of four-row groups (dense
 // with T % 4 == 0): then no chunk reaches past a tensor's extent with part of a group.
 template <typename TIn, typename TG>
-static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream) {
-    if (!a.varlen && a.T % 4 == 0) return launch_seg_ck<TIn, TG, false>(a, n_work, with_out, stream);
-    return launch_seg_ck<TIn, TG, true>(a, n_work, with_out, stream);
+static hipError_t launch_seg_t(const PrefillParams& a, int64_t n_work, bool with_out, hipStream_t stream,
+                               hipEvent_t ev0, hipEvent_t ev1) {
+    if (!a.varlen && a.T % 4 == 0) return launch_seg_ck<TIn, TG, false>(a, n_work, with_out, stream, ev0, ev1);
+    return launch_seg_ck<TIn, TG, true>(a, n_work, with_out, stream, ev0, ev1);
 }
 
-static hipError_t launch_seg(const PrefillParams& a, int64_t n_work, int io_dt, bool with_out, hipStream_t stream) {
+static hipError_t launch_seg(const PrefillParams& a, int64_t n_work, int io_dt, bool with_out, hipStream_t stream,
+                             hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
     const bool g32 = a.g_dt == DT_F32;
     if (io_dt == DT_BF16) {
-        if (g32) return launch_seg_t<__bf16, float>(a, n_work, with_out, stream);
-        if (a.g_dt == DT_BF16) return launch_seg_t<__bf16, __bf16>(a, n_work, with_out, stream);
+        if (g32) return launch_seg_t<__bf16, float>(a, n_work, with_out, stream, ev0, ev1);
+        if (a.g_dt == DT_BF16) return launch_seg_t<__bf16, __bf16>(a, n_work, with_out, stream, ev0, ev1);
     } else if (io_dt == DT_F16) {
-        if (g32) return launch_seg_t<_Float16, float>(a, n_work, with_out, stream);
-        if (a.g_dt == DT_F16) return launch_seg_t<_Float16, _Float16>(a, n_work, with_out, stream);
+        if (g32) return launch_seg_t<_Float16, float>(a, n_work, with_out, stream, ev0, ev1);
+        if (a.g_dt == DT_F16) return launch_seg_t<_Float16, _Float16>(a, n_work, with_out, stream, ev0, ev1);
     } else if (io_dt == DT_F32 && g32) {
-        return launch_seg_t<float, float>(a, n_work, with_out, stream);
+        return launch_seg_t<float, float>(a, n_work, with_out, stream, ev0, ev1);
     }
     return hipErrorInvalidValue;
 }
@@ -116,8 +127,9 @@ hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_d
     return launch_seg(a, n_work, io_dt, false, stream);
 }
 
-hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream) {
-    return launch_seg(a, n_work, io_dt, true, stream);
+hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream, hipEvent_t ev0,
+                                 hipEvent_t ev1) {
+    return launch_seg(a, n_work, io_dt, true, stream, ev0, ev1);
 }
 
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream) {

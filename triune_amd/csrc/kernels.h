@@ -232,7 +232,9 @@ hipError_t launch_gdn_slice_sum(const float* src, int nsl, int64_t stride, int64
                                 hipStream_t stream);
 // Prefill: K1 segment states, K2 scan, K3 outputs (and, for varlen, K0 plan).
 hipError_t launch_gla_seg_state(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
-hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
+// ev0 / ev1: if not null, events stamped with the output kernel's own start and end.
+hipError_t launch_gla_seg_output(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream,
+                                 hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 hipError_t launch_gla_varlen_plan(const int32_t* cu, int64_t n_seqs, int P, int32_t* seg_off, hipStream_t stream);
 hipError_t launch_gdn_seg_mn(const PrefillParams& a, int64_t n_work, int io_dt, hipStream_t stream);
 hipError_t launch_gdn_seg_scan(const PrefillParams& a, float* s_final, int io_dt, hipStream_t stream);
@@ -255,6 +257,7 @@ unsigned gla_onepass_grid(int64_t BH, int64_t npair);
 int gla_onepass_max_pairs();
 int gla_onepass_blocks_per_cu();
 bool gla_onepass_dtypes_ok(int io_dt, int g_dt, bool prep);
-hipError_t launch_gla_onepass(const PrefillParams& a, const OnePassCtl& c, int io_dt, bool prep, hipStream_t stream);
+hipError_t launch_gla_onepass(const PrefillParams& a, const OnePassCtl& c, int io_dt, bool prep, hipStream_t stream,
+                              hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr);
 
 }  // namespace triune
