@@ -149,10 +149,12 @@ struct GdnStep {
     // K3 at D = 128: issued after the chunk's output stores, before its state update.
     static constexpr bool LATE_LOAD_OUT = OUT && D > 64;
 
+    // bv_in (BV): this chunk's beta in stage 3's layout (rows 16i + 4*g4 + k, column c0 + r16),
+    // loaded a chunk ahead by the caller; null: stage 3 loads it.
     template <typename Hook>
     __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
                                const GChunkIn<TIn, TG, PBK>& cur, const TokAddr& kb, f32x4 (&S)[NDB],
-                               f32x4 (&SN)[NDB], bool skip_m, char* smem, Hook&& after_inputs) {
+                               f32x4 (&SN)[NDB], bool skip_m, char* smem, const f32x4* bv_in, Hook&& after_inputs) {
         int lane = threadIdx.x & 63;
         // At D = 128 the planes span more than the 64 KB reach of an LDS instruction's offset, so
         // every operand read needs its own lane address; computed once per kernel they outlive
@@ -373,11 +375,16 @@ struct GdnStep {
             }
             f32x4 bv[4];  // BV: beta of rows 16i + 4*g4 + k, column c0 + r16 (rows past nv: the last row's)
             if constexpr (BV) {
+                if (bv_in) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                    for (int i = 0; i < 4; ++i) bv[i] = bv_in[i];
+                } else {
 #pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        bv[i][k] = tok_row<float>(a.kb, wk, tc + min(16 * i + 4 * g4 + k, nv - 1), h, c0)[r16];
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            bv[i][k] = tok_row<float>(a.kb, wk, tc + min(16 * i + 4 * g4 + k, nv - 1), h, c0)[r16];
+                }
             }
             Split8<NS> sf[NKS];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
 #pragma unroll
@@ -530,9 +537,34 @@ __device__ void gdn_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x
     auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
     GChunkIn<TIn, TG, St::PBK> A;
     gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(0), true);
-    for (int64_t c = 0; c < nch; ++c)
-        St::run(a, wk, h, tok(c), chunk_nv(c), A, kb, S, SN, skip_m, smem,
-                [&] { gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch); });
+    // BV outputs at D = 64: the chunk's beta in stage 3's layout, loaded with the chunk's other
+    // inputs (a chunk ahead) rather than inside stage 3, whose dependent chain is the walk's
+    // critical path (1.154 -> 1.113 ms at config 3's shape; at D = 128 the 16 extra registers
+    // spill: 1.96 -> 2.11 ms, so stage 3 loads it there)
+    constexpr bool BVP = OUT && BV && D == 64;
+    f32x4 bvn[BVP ? 4 : 1], bvc[BVP ? 4 : 1];
+    const int g4 = lane >> 4, r16 = lane & 15, c0 = wave * 16;
+    auto load_bv = [&](int64_t c) {
+        if constexpr (BVP) {
+            const int nvc = chunk_nv(c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    bvn[i][k] = tok_row<float>(a.kb, wk, tok(c) + min(16 * i + 4 * g4 + k, nvc - 1), h, c0)[r16];
+        }
+    };
+    load_bv(0);
+    for (int64_t c = 0; c < nch; ++c) {
+        if constexpr (BVP) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bvc[i] = bvn[i];
+        }
+        St::run(a, wk, h, tok(c), chunk_nv(c), A, kb, S, SN, skip_m, smem, BVP ? bvc : nullptr, [&] {
+            gchunk_load<OUT, CK>(A, ad, kb, key_beta, tok(c + 1), c + 1 < nch);
+            if (c + 1 < nch) load_bv(c + 1);
+        });
+    }
 }
 
 // Waves per SIMD the chunk kernels ask for: two at D = 64 where the LDS of two workgroups fits
@@ -565,9 +597,10 @@ __global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, false, D>())) void gdn_s
 // workgroups per CU where two fit in LDS (bf16 I/O); fp16 and fp32 I/O hold larger planes and run
 // one.  At D = 128 (16-bit I/O) one workgroup of eight waves per CU.
 // gdn_whole (beta per value column, BV): each value column then has its own segment map, so there
-// is one segment per sequence, walked from s0 (or zero), and the final state is written here.
+// is one segment per sequence, walked from s0 (or zero), and the final state is written here;
+// with B * H workgroups in all, each may take a whole SIMD's registers.
 template <typename TIn, typename TG, bool CK, int D, bool BV>
-__global__ __launch_bounds__(4 * D, (gdn_min_waves<TIn, true, D>())) void gdn_seg_out_kernel(PrefillParams a) {
+__global__ __launch_bounds__(4 * D, (BV ? 1 : gdn_min_waves<TIn, true, D>())) void gdn_seg_out_kernel(PrefillParams a) {
     using L = GLay<TIn, true, D>;
     constexpr int NDB = D / 16;
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
