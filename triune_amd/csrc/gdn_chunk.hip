@@ -149,32 +149,51 @@ struct GdnStep {
     // K3 at D = 128: issued after the chunk's output stores, before its state update.
     static constexpr bool LATE_LOAD_OUT = OUT && D > 64;
 
-    // bv_in (BV): this chunk's beta in stage 3's layout (rows 16i + 4*g4 + k, column c0 + r16),
-    // loaded a chunk ahead by the caller; null: stage 3 loads it.
-    template <typename Hook>
-    __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
-                               const GChunkIn<TIn, TG, PBK>& cur, const TokAddr& kb, f32x4 (&S)[NDB],
-                               f32x4 (&SN)[NDB], bool skip_m, char* smem, const f32x4* bv_in, Hook&& after_inputs) {
+    // Lane context of wave `wave` (0 .. NW - 1: its 16 value columns and stage-1 dims) in the chunk
+    // region at smem.
+    struct Ctx {
+        int lane, wave, r16, g4, tg, row, c0, dl0;
+        char *sQT, *sWT, *sBT, *sAT, *sLT, *sTI, *sVP;
+        float* sEM;
+        int* sFLAG;
+    };
+    __device__ static Ctx ctx(char* smem, int wave) {
         int lane = threadIdx.x & 63;
         // At D = 128 the planes span more than the 64 KB reach of an LDS instruction's offset, so
         // every operand read needs its own lane address; computed once per kernel they outlive
         // the register file and spill.  An opaque lane index per chunk keeps them in the step.
         if constexpr (D > 64) asm volatile("" : "+v"(lane));
-        const int wave = wave_id(), r16 = lane & 15, g4 = lane >> 4;
-        const int tg = lane >> 2, row = lane & 3;
-        const int c0 = wave * 16;
-        const int dl0 = wave * 16 + DL * row;
-        char* sQT = smem + L::OFF_QT;
-        char* sWT = smem + L::OFF_WT;
-        char* sBT = smem + L::OFF_BT;
-        char* sAT = smem + L::OFF_AT;
-        char* sLT = smem + L::OFF_LT;
-        char* sTI = smem + L::OFF_TI;
-        char* sVP = smem + L::OFF_VP + wave * NX * L::VPP;
-        float* sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
-        int* sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
+        Ctx c;
+        c.lane = lane;
+        c.wave = wave;
+        c.r16 = lane & 15;
+        c.g4 = lane >> 4;
+        c.tg = lane >> 2;
+        c.row = lane & 3;
+        c.c0 = wave * 16;
+        c.dl0 = wave * 16 + DL * c.row;
+        c.sQT = smem + L::OFF_QT;
+        c.sWT = smem + L::OFF_WT;
+        c.sBT = smem + L::OFF_BT;
+        c.sAT = smem + L::OFF_AT;
+        c.sLT = smem + L::OFF_LT;
+        c.sTI = smem + L::OFF_TI;
+        c.sVP = smem + L::OFF_VP + wave * NX * L::VPP;
+        c.sEM = reinterpret_cast<float*>(smem + L::OFF_FAC);
+        c.sFLAG = reinterpret_cast<int*>(smem + L::OFF_FLAG);
+        return c;
+    }
 
-        // ---------------- stage 1: factors and split operands -> LDS ------------------------
+    // Stage 1: factors and split operands of the chunk -> LDS, and this wave's span flag.
+    __device__ static void stage1(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+                                  const GChunkIn<TIn, TG, PBK>& cur, const TokAddr& kb, const Ctx& c) {
+        const int lane = c.lane, wave = c.wave, r16 = c.r16, g4 = c.g4, tg = c.tg, row = c.row, c0 = c.c0,
+                  dl0 = c.dl0;
+        char *sQT = c.sQT, *sWT = c.sWT, *sBT = c.sBT, *sAT = c.sAT, *sLT = c.sLT, *sTI = c.sTI, *sVP = c.sVP;
+        float* sEM = c.sEM;
+        int* sFLAG = c.sFLAG;
+        (void)lane; (void)wave; (void)r16; (void)g4; (void)tg; (void)row; (void)c0; (void)dl0;
+        (void)sQT; (void)sWT; (void)sBT; (void)sAT; (void)sLT; (void)sTI; (void)sVP; (void)sEM; (void)sFLAG;
         {
             float G[4][DL], Gc[4][DL], GC[DL], x[4][DL];
             chunk_float<CK>(cur.x.g, G, tg, nv);
@@ -257,19 +276,25 @@ struct GdnStep {
 #pragma unroll
             for (int j = 0; j < 4; ++j) lds_put_row<NX, 4>(sVP, L::VPP, (4 * tg + j) * L::VS + 4 * row, vx[j]);
         }
-        if constexpr (!LATE_LOAD && !LATE_LOAD_OUT) after_inputs();
-        __syncthreads();
+    }
+
+    // Whether every wave of the chunk region found its decay span in range (after stage 1's barrier).
+    __device__ static bool chunk_fast(const Ctx& c) {
         bool fast = true;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
-        if (!fast) {
-            if (!skip_m) gdn_tokenwise<TIn, TG, OUT, BV>(a, wk, h, c0, tc, nv, g4, r16, OUT, S);
-            if (!OUT) gdn_tokenwise<TIn, TG, false, BV>(a, wk, h, c0, tc, nv, g4, r16, true, SN);
-            if constexpr (LATE_LOAD || LATE_LOAD_OUT) after_inputs();
-            __syncthreads();
-            return;
-        }
+        for (int w = 0; w < NW; ++w) fast = fast && (c.sFLAG[w] == 0);
+        return fast;
+    }
 
+    // Stage 2: tiles -> LDS; diagonal-block inverses.
+    __device__ static void stage2(const Ctx& c) {
+        const int lane = c.lane, wave = c.wave, r16 = c.r16, g4 = c.g4, tg = c.tg, row = c.row, c0 = c.c0,
+                  dl0 = c.dl0;
+        char *sQT = c.sQT, *sWT = c.sWT, *sBT = c.sBT, *sAT = c.sAT, *sLT = c.sLT, *sTI = c.sTI, *sVP = c.sVP;
+        float* sEM = c.sEM;
+        int* sFLAG = c.sFLAG;
+        (void)lane; (void)wave; (void)r16; (void)g4; (void)tg; (void)row; (void)c0; (void)dl0;
+        (void)sQT; (void)sWT; (void)sBT; (void)sAT; (void)sLT; (void)sTI; (void)sVP; (void)sEM; (void)sFLAG;
         // ---------------- stage 2: tiles -> LDS; diagonal-block inverses -------------------
         // Tile list: the ten lower tiles of A^T = Wt Qt^T (OUT) and the six strictly lower
         // off-diagonal tiles of L^T = Wt Bt^T; tile (sb, tb) holds rows s of block sb, columns t
@@ -360,161 +385,192 @@ struct GdnStep {
                 lds_put_row<NS, 4>(sTI, L::DIAGP, (ib * 64 + lane) * 4, xv);
             }
         }
-        __syncthreads();
+    }
 
-        // ---------------- stage 3: residuals, UT solve, outputs, state ----------------------
-        // One pass per state: K3 runs it on S with V; K1 on S with V = 0 and on SN with V.
-        auto pass = [&](auto with_v, f32x4 (&St)[NDB]) {
-            constexpr bool WV = decltype(with_v)::value;
-            f32x4 Sp[NDB];
+    // Stage 3 on one state (K3 runs it on S with V; K1 on S with V = 0 and on SN with V): residuals,
+    // UT solve, outputs, state update.  mid() runs between the solve and the rest.
+    template <bool WV, typename LateHook, typename Mid>
+    __device__ static void pass(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+                                f32x4 (&St)[NDB], const Ctx& c, const f32x4* bv_in, LateHook&& after_inputs,
+                                Mid&& mid) {
+        const int lane = c.lane, wave = c.wave, r16 = c.r16, g4 = c.g4, tg = c.tg, row = c.row, c0 = c.c0,
+                  dl0 = c.dl0;
+        char *sQT = c.sQT, *sWT = c.sWT, *sBT = c.sBT, *sAT = c.sAT, *sLT = c.sLT, *sTI = c.sTI, *sVP = c.sVP;
+        float* sEM = c.sEM;
+        int* sFLAG = c.sFLAG;
+        (void)lane; (void)wave; (void)r16; (void)g4; (void)tg; (void)row; (void)c0; (void)dl0;
+        (void)sQT; (void)sWT; (void)sBT; (void)sAT; (void)sLT; (void)sTI; (void)sVP; (void)sEM; (void)sFLAG;
+        f32x4 Sp[NDB];
 #pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
+        for (int db = 0; db < NDB; ++db) {
+            const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) Sp[db][i] = St[db][i] * em[i];
+            for (int i = 0; i < 4; ++i) Sp[db][i] = St[db][i] * em[i];
+        }
+        f32x4 bv[4];  // BV: beta of rows 16i + 4*g4 + k, column c0 + r16 (rows past nv: the last row's)
+        if constexpr (BV) {
+            if (bv_in) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) bv[i] = bv_in[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        bv[i][k] = tok_row<float>(a.kb, wk, tc + min(16 * i + 4 * g4 + k, nv - 1), h, c0)[r16];
             }
-            f32x4 bv[4];  // BV: beta of rows 16i + 4*g4 + k, column c0 + r16 (rows past nv: the last row's)
-            if constexpr (BV) {
-                if (bv_in) {
+        }
+        Split8<NS> sf[NKS];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) bv[i] = bv_in[i];
-                } else {
+        for (int ks = 0; ks < NKS; ++ks) sf[ks] = split_k32<NS>(Sp[2 * ks], Sp[2 * ks + 1]);
+        // R_i = V_i - Bt_i S'  (D layout: rows t = 16i + 4*g4 + k, column c0 + r16)
+        f32x4 R[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            f32x4 p = zero4();
 #pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            bv[i][k] = tok_row<float>(a.kb, wk, tc + min(16 * i + 4 * g4 + k, nv - 1), h, c0)[r16];
+            for (int ks = 0; ks < NKS; ++ks) {
+                const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4);
+                p = mfma_split<NS, NS, NS>(bf, sf[ks], p);
+            }
+            f32x4 vv = zero4();
+            if constexpr (WV) {
+                const int off = (16 * i + 4 * g4 + (r16 >> 2)) * L::VS + 4 * (r16 & 3);
+#pragma unroll
+                for (int pl = 0; pl < NX; ++pl) {
+                    const bf16x4 t4 = lds_read_tr(reinterpret_cast<const __bf16*>(sVP + pl * L::VPP) + off);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) vv[k] += (float)t4[k];
                 }
             }
-            Split8<NS> sf[NKS];  // S' with K = key dims (A-operand of S'^T, B-operand of S')
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) sf[ks] = split_k32<NS>(Sp[2 * ks], Sp[2 * ks + 1]);
-            // R_i = V_i - Bt_i S'  (D layout: rows t = 16i + 4*g4 + k, column c0 + r16)
-            f32x4 R[4];
+            for (int k = 0; k < 4; ++k) R[i][k] = vv[k] - p[k];
+        }
+        // O^T from the carried state first (Qt S'), so that S' in split form is dead before
+        // the UT solve
+        f32x4 Ot[4];
+        if constexpr (OUT) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f32x4 p = zero4();
+            for (int tb = 0; tb < 4; ++tb) {
+                f32x4 o = zero4();
 #pragma unroll
                 for (int ks = 0; ks < NKS; ++ks) {
-                    const Split8<NS> bf = lds_frag<NS>(sBT, L::ROWP, L::RS, 16 * i + r16, 32 * ks, g4);
-                    p = mfma_split<NS, NS, NS>(bf, sf[ks], p);
+                    const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                    o = mfma_split<NS, NS, NS>(sf[ks], qf, o);
                 }
-                f32x4 vv = zero4();
-                if constexpr (WV) {
-                    const int off = (16 * i + 4 * g4 + (r16 >> 2)) * L::VS + 4 * (r16 & 3);
-#pragma unroll
-                    for (int pl = 0; pl < NX; ++pl) {
-                        const bf16x4 t4 = lds_read_tr(reinterpret_cast<const __bf16*>(sVP + pl * L::VPP) + off);
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) vv[k] += (float)t4[k];
-                    }
-                }
-#pragma unroll
-                for (int k = 0; k < 4; ++k) R[i][k] = vv[k] - p[k];
+                Ot[tb] = o;
             }
-            // O^T from the carried state first (Qt S'), so that S' in split form is dead before
-            // the UT solve
-            f32x4 Ot[4];
-            if constexpr (OUT) {
+        }
+        // U_i = T_ii (R_i - sum_{j<i} L_ij U_j)
+        f32x4 U[4];
+        Split8<NS> us[4];
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    f32x4 o = zero4();
-#pragma unroll
-                    for (int ks = 0; ks < NKS; ++ks) {
-                        const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
-                        o = mfma_split<NS, NS, NS>(sf[ks], qf, o);
+        for (int i = 0; i < 4; ++i) {
+            f32x4 X = R[i];
+            if (i >= 1) {
+                f32x4 p = zero4();
+                if (i >= 2) {  // blocks 0 and 1 together (K = 32)
+                    const Split8<NS> lf = tile_frag<NS>(sLT, L::LTP, lt_index(0, i), lt_index(1, i), true, lane);
+                    p = mfma_split<NS, NS, NS>(lf, split_k32<NS>(U[0], U[1]), p);
+                    if (i == 3) {
+                        const Split8<NS> lf2 = tile_frag<NS>(sLT, L::LTP, lt_index(2, 3), 0, false, lane);
+                        p = mfma_split<NS, NS, NS>(lf2, us[2], p);
                     }
-                    Ot[tb] = o;
-                }
-            }
-            // U_i = T_ii (R_i - sum_{j<i} L_ij U_j)
-            f32x4 U[4];
-            Split8<NS> us[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f32x4 X = R[i];
-                if (i >= 1) {
-                    f32x4 p = zero4();
-                    if (i >= 2) {  // blocks 0 and 1 together (K = 32)
-                        const Split8<NS> lf = tile_frag<NS>(sLT, L::LTP, lt_index(0, i), lt_index(1, i), true, lane);
-                        p = mfma_split<NS, NS, NS>(lf, split_k32<NS>(U[0], U[1]), p);
-                        if (i == 3) {
-                            const Split8<NS> lf2 = tile_frag<NS>(sLT, L::LTP, lt_index(2, 3), 0, false, lane);
-                            p = mfma_split<NS, NS, NS>(lf2, us[2], p);
-                        }
-                    } else {
-                        const Split8<NS> lf = tile_frag<NS>(sLT, L::LTP, lt_index(0, 1), 0, false, lane);
-                        p = mfma_split<NS, NS, NS>(lf, us[0], p);
-                    }
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) X[k] -= p[k];
-                }
-                if constexpr (BV) {
-                    U[i] = col_solve(X, bv[i], reinterpret_cast<const float*>(sTI) + i * 256, g4, r16);
                 } else {
-                    const Split8<NS> tf = tile_frag<NS>(sTI, L::DIAGP, i, 0, false, lane);
-                    U[i] = mfma_split<NS, NS, NS>(tf, split_k16<NS>(X), zero4());
+                    const Split8<NS> lf = tile_frag<NS>(sLT, L::LTP, lt_index(0, 1), 0, false, lane);
+                    p = mfma_split<NS, NS, NS>(lf, us[0], p);
                 }
-                us[i] = split_k16<NS>(U[i]);
-            }
-            // U with K = tokens 32*k2 + pi(g4, j): A-operand of U^T, B-operand of U
-            Split8<NS> uf[2];
 #pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) uf[k2] = split_k32<NS>(U[2 * k2], U[2 * k2 + 1]);
+                for (int k = 0; k < 4; ++k) X[k] -= p[k];
+            }
+            if constexpr (BV) {
+                U[i] = col_solve(X, bv[i], reinterpret_cast<const float*>(sTI) + i * 256, g4, r16);
+            } else {
+                const Split8<NS> tf = tile_frag<NS>(sTI, L::DIAGP, i, 0, false, lane);
+                U[i] = mfma_split<NS, NS, NS>(tf, split_k16<NS>(X), zero4());
+            }
+            us[i] = split_k16<NS>(U[i]);
+        }
+        mid();  // the two-role kernel's barrier between the solve and the rest
+        // U with K = tokens 32*k2 + pi(g4, j): A-operand of U^T, B-operand of U
+        Split8<NS> uf[2];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) uf[k2] = split_k32<NS>(U[2 * k2], U[2 * k2 + 1]);
 
-            if constexpr (OUT) {
+        if constexpr (OUT) {
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    f32x4 o = Ot[tb];
-#pragma unroll
-                    for (int k2 = 0; k2 < 2; ++k2) {
-                        if (2 * k2 > tb) continue;
-                        const bool has_hi = 2 * k2 + 1 <= tb;
-                        const Split8<NS> af = tile_frag<NS>(sAT, L::TILEP, tile_index(2 * k2, tb),
-                                                            has_hi ? tile_index(2 * k2 + 1, tb) : 0, has_hi, lane);
-                        o = mfma_split<NS, NS, NS>(uf[k2], af, o);
-                    }
-                    Ot[tb] = o;
-                }
-                // lane (g4, r16) holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3]; stage
-                // through this wave's V planes (read above) and store quad-coalesced rows
-                float* sO = reinterpret_cast<float*>(sVP);
-                const int es = dt_size(a.o_dt);
-                const int64_t ost = a.o_st * es;
-                char* obase = reinterpret_cast<char*>(a.o) +
-                              uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
-                const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);
-                const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
-                const OutRsrc orr = out_rsrc(obase, ost, es, nv, a.o_dt == DT_F32);
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) {
-                    *reinterpret_cast<f32x4*>(sO + r16 * L::OS + 4 * g4) = Ot[tb];
-                    const f32x4 xo = *reinterpret_cast<const f32x4*>(sO + tq * L::OS + 4 * q);
-                    out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, xo);
-                }
-            }
-            if constexpr (LATE_LOAD_OUT) after_inputs();
-            // S <- e^m (S' + Wt^T U)
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                f32x4 acc = Sp[db];
+            for (int tb = 0; tb < 4; ++tb) {
+                f32x4 o = Ot[tb];
 #pragma unroll
                 for (int k2 = 0; k2 < 2; ++k2) {
-                    const Split8<NS> wf = lds_frag_tr<NS>(sWT, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
-                    acc = mfma_split<NS, NS, NS>(wf, uf[k2], acc);
+                    if (2 * k2 > tb) continue;
+                    const bool has_hi = 2 * k2 + 1 <= tb;
+                    const Split8<NS> af = tile_frag<NS>(sAT, L::TILEP, tile_index(2 * k2, tb),
+                                                        has_hi ? tile_index(2 * k2 + 1, tb) : 0, has_hi, lane);
+                    o = mfma_split<NS, NS, NS>(uf[k2], af, o);
                 }
-                const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) St[db][i] = em[i] * acc[i];
+                Ot[tb] = o;
             }
-        };
+            // lane (g4, r16) holds O[token 16*tb + r16][columns c0 + 4*g4 + 0..3]; stage
+            // through this wave's V planes (read above) and store quad-coalesced rows
+            float* sO = reinterpret_cast<float*>(sVP);
+            const int es = dt_size(a.o_dt);
+            const int64_t ost = a.o_st * es;
+            char* obase = reinterpret_cast<char*>(a.o) +
+                          uniform_i64((wk.b * a.o_sb + (wk.row0 + tc) * a.o_st + h * a.o_sh + c0) * es);
+            const int q = lane & 3, tq = (lane >> 4) + 4 * ((lane >> 2) & 3);
+            const int32_t olane = (int32_t)(tq * ost) + 4 * q * es;
+            const OutRsrc orr = out_rsrc(obase, ost, es, nv, a.o_dt == DT_F32);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                *reinterpret_cast<f32x4*>(sO + r16 * L::OS + 4 * g4) = Ot[tb];
+                const f32x4 xo = *reinterpret_cast<const f32x4*>(sO + tq * L::OS + 4 * q);
+                out_store4(orr, (int32_t)(16 * tb * ost) + olane, a.o_dt, xo);
+            }
+        }
+        if constexpr (LATE_LOAD_OUT) after_inputs();
+        // S <- e^m (S' + Wt^T U)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            f32x4 acc = Sp[db];
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const Split8<NS> wf = lds_frag_tr<NS>(sWT, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
+                acc = mfma_split<NS, NS, NS>(wf, uf[k2], acc);
+            }
+            const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) St[db][i] = em[i] * acc[i];
+        }
+    }
+
+    // bv_in (BV): this chunk's beta in stage 3's layout (rows 16i + 4*g4 + k, column c0 + r16),
+    // loaded a chunk ahead by the caller; null: stage 3 loads it.
+    template <typename Hook>
+    __device__ static void run(const PrefillParams& a, const Work& wk, int64_t h, int64_t tc, int nv,
+                               const GChunkIn<TIn, TG, PBK>& cur, const TokAddr& kb, f32x4 (&S)[NDB],
+                               f32x4 (&SN)[NDB], bool skip_m, char* smem, const f32x4* bv_in, Hook&& after_inputs) {
+        const Ctx c = ctx(smem, wave_id());
+        stage1(a, wk, h, tc, nv, cur, kb, c);
+        if constexpr (!LATE_LOAD && !LATE_LOAD_OUT) after_inputs();
+        __syncthreads();
+        if (!chunk_fast(c)) {
+            if (!skip_m) gdn_tokenwise<TIn, TG, OUT, BV>(a, wk, h, c.c0, tc, nv, c.g4, c.r16, OUT, S);
+            if (!OUT) gdn_tokenwise<TIn, TG, false, BV>(a, wk, h, c.c0, tc, nv, c.g4, c.r16, true, SN);
+            if constexpr (LATE_LOAD || LATE_LOAD_OUT) after_inputs();
+            __syncthreads();
+            return;
+        }
+        stage2(c);
+        __syncthreads();
+        auto nomid = [] {};
         if constexpr (OUT) {
-            pass(std::true_type{}, S);
+            pass<true>(a, wk, h, tc, nv, S, c, bv_in, after_inputs, nomid);
         } else {
-            if (!skip_m) pass(std::false_type{}, S);
+            if (!skip_m) pass<false>(a, wk, h, tc, nv, S, c, bv_in, after_inputs, nomid);
             if constexpr (LATE_LOAD) after_inputs();
             __builtin_amdgcn_sched_barrier(0);  // one pass at a time: their temporaries never overlap
-            pass(std::true_type{}, SN);
+            pass<true>(a, wk, h, tc, nv, SN, c, bv_in, after_inputs, nomid);
         }
         __syncthreads();  // the next chunk rewrites LDS
     }
@@ -624,6 +680,108 @@ __global__ __launch_bounds__(4 * D, (BV ? 1 : gdn_min_waves<TIn, true, D>())) vo
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int i = 0; i < 4; ++i) a.seq_final[sb + (16 * db + 4 * g4 + i) * D + c] = S[db][i];
+    }
+}
+
+// Beta per value column at D = 64 with bf16 I/O: the whole-sequence walk of gdn_seg_out_kernel in
+// two roles over two chunk regions of LDS.  The walk's critical path is stage 3 (the residuals,
+// the column solves and the state update depend on the state), while stages 1 and 2 (factors,
+// split operands, tiles, diagonal blocks) depend only on the chunk's inputs.  Waves 0-3 run
+// stages 1 and 2 of chunk i + 1 in region (i + 1) & 1 while waves 4-7 run stage 3 of chunk i from
+// region i & 1; two workgroup barriers per chunk: after stage 1 of the front waves (the back
+// waves' barrier sits between their solve and the rest of stage 3), and at the end of the chunk.
+// Wave w of either role owns value columns 16w .. 16w + 15, so the back waves read the V rows the
+// front waves of the same index staged.
+template <typename TG, bool CK>
+__global__ __launch_bounds__(512, 1) void gdn_bv_pipe_kernel(PrefillParams a) {
+    using TIn = __bf16;
+    constexpr int D = 64;
+    using St = GdnStep<TIn, TG, true, CK, D, true>;
+    using L = GLay<TIn, true, D>;
+    constexpr int RB = (L::BYTES + 255) / 256 * 256;
+    static_assert(RB + L::BYTES <= 160 * 1024, "two chunk regions fit in LDS");
+    __shared__ __attribute__((aligned(256))) char smem[RB + L::BYTES];
+    const int64_t h = blockIdx.y;
+    Work wk;
+    if (!find_work(a, blockIdx.x, wk)) return;
+    const int wave8 = wave_id(), wave = wave8 & 3;
+    const bool front = wave8 < 4;
+    const int lane = threadIdx.x & 63, g4 = lane >> 4, r16 = lane & 15, tg = lane >> 2, row = lane & 3;
+    const int c0 = wave * 16;
+    const int64_t nch = (wk.t_end - wk.t_begin + CHUNK - 1) / CHUNK;
+    auto chunk_nv = [&](int64_t c) {
+        const int64_t r = wk.t_end - (wk.t_begin + c * CHUNK);
+        return (int)(r < CHUNK ? r : CHUNK);
+    };
+    auto tok = [&](int64_t c) { return wk.t_begin + c * CHUNK; };
+    auto region = [&](int64_t c) { return smem + (c & 1) * RB; };
+    auto nohook = [] {};
+
+    // front waves: the chunk inputs, a chunk ahead
+    const ChunkAddr ad = chunk_addr<true, TIn, TG>(a, wk, h, tg, c0 + 4 * row, c0 + 4 * row);
+    const TokAddr kb{};
+    GChunkIn<TIn, TG, St::PBK> A;
+    // back waves: the state (rows 16 db + 4 g4 + i, column c0 + r16) and beta a chunk ahead
+    f32x4 S[4], bvn[4], bvc[4];
+    const int64_t sb = (wk.seq * a.H + h) * (int64_t)D * D;
+    auto load_bv = [&](int64_t c) {
+        const int nvc = chunk_nv(c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                bvn[i][k] = tok_row<float>(a.kb, wk, tok(c) + min(16 * i + 4 * g4 + k, nvc - 1), h, c0)[r16];
+    };
+    if (front) {
+        gchunk_load<true, CK>(A, ad, kb, false, tok(0), nch > 0);
+    } else {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[db][i] = a.s0 ? a.s0[sb + (16 * db + 4 * g4 + i) * D + c0 + r16] : 0.f;
+        if (nch > 0) load_bv(0);
+    }
+    // chunk 0's stages 1 and 2
+    if (front && nch > 0) {
+        St::stage1(a, wk, h, tok(0), chunk_nv(0), A, kb, St::ctx(region(0), wave));
+        gchunk_load<true, CK>(A, ad, kb, false, tok(1), nch > 1);
+    }
+    __syncthreads();
+    if (front && nch > 0) {
+        const auto c = St::ctx(region(0), wave);
+        if (St::chunk_fast(c)) St::stage2(c);
+    }
+    __syncthreads();
+    for (int64_t i = 0; i < nch; ++i) {
+        if (front) {
+            if (i + 1 < nch) {
+                St::stage1(a, wk, h, tok(i + 1), chunk_nv(i + 1), A, kb, St::ctx(region(i + 1), wave));
+                gchunk_load<true, CK>(A, ad, kb, false, tok(i + 2), i + 2 < nch);
+            }
+            __syncthreads();
+            if (i + 1 < nch) {
+                const auto c = St::ctx(region(i + 1), wave);
+                if (St::chunk_fast(c)) St::stage2(c);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) bvc[k] = bvn[k];
+            if (i + 1 < nch) load_bv(i + 1);
+            const auto c = St::ctx(region(i), wave);
+            if (St::chunk_fast(c)) {
+                St::template pass<true>(a, wk, h, tok(i), chunk_nv(i), S, c, bvc, nohook, [] { __syncthreads(); });
+            } else {  // decay span out of the factored range: token by token from the state
+                gdn_tokenwise<TIn, TG, true, true>(a, wk, h, c0, tok(i), chunk_nv(i), g4, r16, true, S);
+                __syncthreads();
+            }
+        }
+        __syncthreads();  // the next chunk rewrites the region this one read
+    }
+    if (!front && a.seq_final) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a.seq_final[sb + (16 * db + 4 * g4 + i) * D + c0 + r16] = S[db][i];
     }
 }
 
@@ -739,6 +897,12 @@ static hipError_t launch_gdn_bv(const PrefillParams& a, int64_t n_work, int whic
     if (which == 0) {
         hipLaunchKernelGGL((gdn_seg_mn_kernel<TIn, TG, CK, D, BV>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D),
                            0, stream, a);
+    } else if constexpr (BV && D == 64 && std::is_same<TIn, __bf16>::value) {
+        if (a.gdn_whole)
+            hipLaunchKernelGGL((gdn_bv_pipe_kernel<TG, CK>), dim3((unsigned)n_work, (unsigned)a.H), dim3(512), 0, stream, a);
+        else
+            hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG, CK, D, BV>), dim3((unsigned)n_work, (unsigned)a.H),
+                               dim3(4 * D), 0, stream, a);
     } else {
         hipLaunchKernelGGL((gdn_seg_out_kernel<TIn, TG, CK, D, BV>), dim3((unsigned)n_work, (unsigned)a.H), dim3(4 * D),
                            0, stream, a);
