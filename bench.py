@@ -311,12 +311,15 @@ def bench_fused_prefill(dev, reps=20, T=16384):
     prefill in, attention.py:458-499): fused_qkv_g_prep_chunk_gla as dispatched (one launch where
     the call fits the single-launch prefill, as at T = 1024), the same entry with the single launch
     switched off (pre-processing inside the segment-state kernel, then the carry scan and the
-    output kernel; past four chunk-heads per CU the prep pass and then the prefill), and the
+    output kernel; past four chunk-heads per CU the prep pass and then the prefill), the
     two-step pipeline the reference launches (in-place pre-processing, then the three-launch
-    prefill).  "us": GPU time per call, calls back to back in a replayed HIP graph, each on its own
+    prefill) and, past four chunk-heads per CU, the entry with the pre-processing kept inside the
+    segment-state kernel ("fused_in_state_kernel").  A warm-up of 60 two-step calls precedes the
+    legs.  "us": GPU time per call, calls back to back in a replayed HIP graph, each on its own
     raw input set (restored before every replay, untimed); "eager_us": one Python call at a time
     between events, host work included."""
     import triune_amd.fast_gla as FG
+    import triune_amd.gla_prep as GP
     from triune_amd import fast_chunk_gla, fused_qkv_g_prep_chunk_gla, fused_qkv_g_prep_inplace
     from triune_amd.workloads import gla_algorithmic_bytes
 
@@ -349,12 +352,23 @@ def bench_fused_prefill(dev, reps=20, T=16384):
         fast_chunk_gla(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, initial_state=s0, out=out)
 
     stream = torch.cuda.current_stream()
+    # clocks up before the first timed leg (after an idle spell the first ~100 calls run slower)
+    for i in range(60):
+        if i % n_sets == 0:
+            restore()
+        two_step(i % n_sets)
+    torch.cuda.synchronize()
     res, eager = {}, {}
-    onepass0 = FG.ONEPASS
+    onepass0, fmax0 = FG.ONEPASS, GP.FUSED_MAX_CHUNK_HEADS_PER_CU
+    legs = [("fused", fused, True, fmax0), ("fused_three_launch", fused, False, fmax0),
+            ("prep_then_prefill", two_step, False, fmax0)]
+    if B * H * ((T + 63) // 64) > fmax0 * torch.cuda.get_device_properties(dev).multi_processor_count:
+        # past the threshold the entry runs the pre-processing pass first: time the other form too
+        legs.append(("fused_in_state_kernel", fused, False, 1 << 30))
     try:
-        for name, fn, onepass in (("fused", fused, True), ("fused_three_launch", fused, False),
-                                  ("prep_then_prefill", two_step, False)):
+        for name, fn, onepass, fmax in legs:
             FG.ONEPASS = onepass
+            GP.FUSED_MAX_CHUNK_HEADS_PER_CU = fmax
             res[name] = _graph_us_per_call([lambda i=i: fn(i) for i in range(n_sets)], restore)
             ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
             for i in range(10 + reps):
@@ -367,7 +381,7 @@ def bench_fused_prefill(dev, reps=20, T=16384):
             torch.cuda.synchronize()
             eager[name] = sorted(b.elapsed_time(e) for b, e in ev)[reps // 2] * 1e3  # median
     finally:
-        FG.ONEPASS = onepass0
+        FG.ONEPASS, GP.FUSED_MAX_CHUNK_HEADS_PER_CU = onepass0, fmax0
     alg = gla_algorithmic_bytes(B * T * H, HD, HD, 2, 2, 2) + 2 * B * H * HD * HD * 4
     gbs = alg / (res["fused"] * 1e-6) / 1e9
     from triune_amd._lib import lib as _l
@@ -383,7 +397,11 @@ def bench_fused_prefill(dev, reps=20, T=16384):
             "fused_three_launch_us": round(res["fused_three_launch"], 2),
             "prep_then_prefill_us": round(res["prep_then_prefill"], 2),
             "eager_us": round(eager["fused"], 2), "eager_fused_three_launch_us": round(eager["fused_three_launch"], 2),
-            "eager_prep_then_prefill_us": round(eager["prep_then_prefill"], 2), "alg_bytes": alg,
+            "eager_prep_then_prefill_us": round(eager["prep_then_prefill"], 2),
+            **({"fused_in_state_kernel_us": round(res["fused_in_state_kernel"], 2),
+                "eager_fused_in_state_kernel_us": round(eager["fused_in_state_kernel"], 2)}
+               if "fused_in_state_kernel" in res else {}),
+            "alg_bytes": alg,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)}}
 

@@ -9,14 +9,18 @@
 //   1. each chunk's rows are loaded once; with PREP, q, k, g are raw projections and stage 1 forms
 //      q, k <- RoPE(normalize(elu(x) + 1)), g <- logsigmoid(g) (attention.py:14-79), rounds them to
 //      the I/O dtype and writes them back in place, as the reference's prep kernel does;
-//   2. stages 1 and 2 of the chunk kernel (factored operands Qt, Kt in LDS, the causal A^T tiles)
-//      and the chunk's local end state L = e^m (Kt^T V);
+//   2. stage 1 of the chunk kernel (factored operands Qt, Kt in LDS) and the chunk's local end
+//      state L = e^m (Kt^T V);
 //   3. the pair's state map (e^{G_C}, L) -- the second chunk's applied to the first's -- is
 //      published to the workspace, followed by a flag;
-//   4. the state entering the pair is folded from s0 and the earlier pairs' published maps,
+//   4. what does not depend on the state entering the chunk, while the earlier pairs publish:
+//      stage 2 (the causal A^T tiles) and the outputs' in-chunk part O^T = V^T A^T;
+//   5. the state entering the pair is folded from s0 and the earlier pairs' published maps,
 //      S <- e^{G_C(j)} S + L_j for j = 0 .. p-1 (the affine scan the carry kernel runs); the second
 //      chunk applies the first chunk's map to it;
-//   5. each chunk's outputs O^T = (e^m S)^T Qt^T + V^T A^T; the last chunk stores the final state.
+//   6. each chunk's outputs O^T += (e^m S)^T Qt^T; the last chunk stores the final state.
+// Workgroup barriers that order only LDS traffic wait for LDS alone (lds_sync), so the in-place
+// write-back of step 1 stays in flight until the wait before the flag.
 // Chunks whose decay span exceeds the factored range (or that hold the unclamped 1-token tail)
 // stage their rows in LDS and walk the tokens one by one, for the local state and the outputs.
 //
@@ -344,12 +348,79 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
         }
         stage_rows(stg + 2 * 64 * 64 * sizeof(TIn), cur.v, tg, c0 + 4 * row);
     }
-    __syncthreads();
+    // LDS rows of every wave; LDS only, so the write-back stores (PREP) stay in flight until the
+    // wait before the flag
+    lds_sync();
 
     // ---- the chunk's local end state P (this wave's columns, D layout) -----------------------
     const OutCtx oc = out_ctx(a, wk, h);
     const int64_t t_unc = t_unclamped - tc;  // in-chunk index of the unclamped token (or out of range)
     f32x4 P[4];
+    if (fast) {
+        // L = e^m (Kt^T V)
+        Split8<NX> vf[2];
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            P[db] = zero4();
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const Split8<NS> kf = lds_frag_tr<NS>(sKT, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
+                P[db] = mfma_split<NS, NX, NS>(kf, vf[k2], P[db]);
+            }
+            const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) P[db][i] *= em[i];
+        }
+    } else {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) P[db] = zero4();
+        walk_staged<TIn, TG, false>(smem + L::OFF_QT, nv, t_unc, c0, g4, r16, P, oc, tc);
+    }
+
+    // ---- publish the pair's map (e^{G_C(B)} e^{G_C(A)}, e^{G_C(B)} L_A + L_B) -----------------
+    if (grp == 0) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(sX + (db * 256 + tid) * 4) = P[db];
+    }
+    lds_sync();
+    const float* sEG0 = reinterpret_cast<const float*>(lds + L::OFF_FAC) + DK;  // e^{G_C} of chunk A
+    const int64_t slot = bh * ctl.npair + p;
+    const __amdgpu_buffer_rsrc_t rL = __builtin_amdgcn_make_buffer_rsrc(
+        a.ws_state + bh * ctl.npair * (int64_t)(DK * DV), (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rE =
+        __builtin_amdgcn_make_buffer_rsrc(a.ws_gamma + bh * ctl.npair * DK, (short)0, 0x7fffffff, 0x00020000);
+    if (grp == 1 && !last_pair) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        const int lo = (int)(p * (DK * DV) * 4) + tid * 16;  // [4][256 threads][4] (see fold_states)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const f32x4 la = *reinterpret_cast<const f32x4*>(sX + (db * 256 + tid) * 4);
+            const f32x4 eb = *reinterpret_cast<const f32x4*>(sEG + 16 * db + 4 * g4);
+            f32x4 m;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) m[i] = fmaf(eb[i], la[i], P[db][i]);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, m), rL, lo + 4096 * db, 0, 0);
+        }
+        if (tid < DK)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sEG0[tid] * sEG[tid]), rE,
+                                                  (int)(p * DK * 4) + tid * 4, 0, 0);
+    }
+    // Stores complete (the map in this XCD's L2; PREP: the rows written back in stage 1, which
+    // also precede every output of this workgroup, as o may alias g) before the flag.
+    wait_vmem();
+    __syncthreads();
+    const uint32_t xcc = (uint32_t)__builtin_amdgcn_s_getreg(OP_HWREG_XCC_ID) & 0xfu;
+    if (!last_pair && threadIdx.x == 0)
+        __hip_atomic_store(ctl.flags + slot, (uint64_t)ep | ((uint64_t)xcc << 32), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- while earlier pairs publish: stage 2 and the outputs' in-chunk part ------------------
+    // Neither depends on the state entering the chunk: A^T tiles -> LDS, then O^T = V^T A^T.
+    f32x4 Ot[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) Ot[tb] = zero4();
     if (fast) {
         // stage 2: causal tiles of A^T -> LDS
         {
@@ -384,132 +455,18 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
                 lds_put_row<NS, 4>(sAT, L::ATP, (i * 64 + lane) * 4, xx);
             }
         }
-        // L = e^m (Kt^T V)
-        Split8<NX> vf[2];
-#pragma unroll
-        for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            P[db] = zero4();
-#pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                const Split8<NS> kf = lds_frag_tr<NS>(sKT, L::ROWP, L::RS, 32 * k2, 16 * db, g4, r16);
-                P[db] = mfma_split<NS, NX, NS>(kf, vf[k2], P[db]);
-            }
-            const f32x4 em = *reinterpret_cast<const f32x4*>(sEM + 16 * db + 4 * g4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) P[db][i] *= em[i];
-        }
-    } else {
-#pragma unroll
-        for (int db = 0; db < 4; ++db) P[db] = zero4();
-        walk_staged<TIn, TG, false>(smem + L::OFF_QT, nv, t_unc, c0, g4, r16, P, oc, tc);
     }
-
-    // ---- publish the pair's map (e^{G_C(B)} e^{G_C(A)}, e^{G_C(B)} L_A + L_B) -----------------
-    if (grp == 0) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db) *reinterpret_cast<f32x4*>(sX + (db * 256 + tid) * 4) = P[db];
-    }
-    __syncthreads();
-    const float* sEG0 = reinterpret_cast<const float*>(lds + L::OFF_FAC) + DK;  // e^{G_C} of chunk A
-    const int64_t slot = bh * ctl.npair + p;
-    const __amdgpu_buffer_rsrc_t rL = __builtin_amdgcn_make_buffer_rsrc(
-        a.ws_state + bh * ctl.npair * (int64_t)(DK * DV), (short)0, 0x7fffffff, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rE =
-        __builtin_amdgcn_make_buffer_rsrc(a.ws_gamma + bh * ctl.npair * DK, (short)0, 0x7fffffff, 0x00020000);
-    if (grp == 1 && !last_pair) {
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        const int lo = (int)(p * (DK * DV) * 4) + tid * 16;  // [4][256 threads][4] (see fold_states)
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const f32x4 la = *reinterpret_cast<const f32x4*>(sX + (db * 256 + tid) * 4);
-            const f32x4 eb = *reinterpret_cast<const f32x4*>(sEG + 16 * db + 4 * g4);
-            f32x4 m;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) m[i] = fmaf(eb[i], la[i], P[db][i]);
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, m), rL, lo + 4096 * db, 0, 0);
-        }
-        if (tid < DK)
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sEG0[tid] * sEG[tid]), rE,
-                                                  (int)(p * DK * 4) + tid * 4, 0, 0);
-    }
-    // Stores complete (the map in this XCD's L2; PREP: the rows written back in stage 1, which
-    // also precede every output of this workgroup, as o may alias g) before the flag.
-    wait_vmem();
-    __syncthreads();
-    const uint32_t xcc = (uint32_t)__builtin_amdgcn_s_getreg(OP_HWREG_XCC_ID) & 0xfu;
-    if (!last_pair && threadIdx.x == 0)
-        __hip_atomic_store(ctl.flags + slot, (uint64_t)ep | ((uint64_t)xcc << 32), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-
-    // ---- the state entering the chunk ------------------------------------------------------------
-    f32x4 S[4];
-    if (a.s0) {
-        const float* s0 = a.s0 + bh * (int64_t)(DK * DV);
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) S[db][i] = s0[state_off(db, i, g4, r16, wave, DV)];
-    } else {
-#pragma unroll
-        for (int db = 0; db < 4; ++db) S[db] = zero4();
-    }
-    if (p > 0) {
-        // lanes j < p watch the flag word of pair j of this (sequence, head): the epoch of the call
-        // that published it (low half) and the XCD its workgroup ran on (high half)
-        const uint64_t* fl = ctl.flags + bh * ctl.npair;
-        bool ok = false, same = true;
-        for (uint32_t n = 0; n < OP_SPIN_MAX; ++n) {
-            uint64_t f = 0;
-            if (lane < p) f = __hip_atomic_load(fl + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (__all(lane >= p || (uint32_t)f == ep)) {
-                ok = true;
-                same = __all(lane >= p || (uint32_t)(f >> 32) == xcc);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        if (lane == 0 && (!ok || !same))
-            __hip_atomic_fetch_or(ctl.hdr + 2, ok ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (same) fold_states<OP_SC0>(rL, rE, sEGj, (int)p, S, g4);
-        else fold_states<OP_SC1>(rL, rE, sEGj, (int)p, S, g4);
-    }
-    if (grp == 1) {  // through the pair's first chunk: S <- e^{G_C(A)} S + L_A
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const f32x4 la = *reinterpret_cast<const f32x4*>(sX + (db * 256 + tid) * 4);
-            const f32x4 ea = *reinterpret_cast<const f32x4*>(sEG0 + 16 * db + 4 * g4);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) S[db][i] = fmaf(ea[i], S[db][i], la[i]);
-        }
-    }
-
-    // ---- outputs ------------------------------------------------------------------------------
+    lds_sync();  // every wave's A^T tiles (both groups take it)
+    // lanes j < p watch the flag word of pair j of this (sequence, head): the epoch of the call
+    // that published it (low half) and the XCD its workgroup ran on (high half).  The first read
+    // is issued here and checked after the in-chunk outputs.
+    const uint64_t* fl = ctl.flags + bh * ctl.npair;
+    uint64_t fw = 0;
+    if (lane < p) fw = __hip_atomic_load(fl + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (fast) {
         Split8<NX> vf[2];
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) vf[k2] = lds_frag_tr<NX>(sVP, L::VPP, L::VS, 32 * k2, 0, g4, r16);
-        f32x4 Ot[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) Ot[tb] = zero4();
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {  // (e^m S)^T Qt^T
-            const f32x4 e0 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 4 * g4);
-            const f32x4 e1 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 16 + 4 * g4);
-            float xx[8];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xx[i] = S[2 * ks][i] * e0[i];
-                xx[4 + i] = S[2 * ks + 1][i] * e1[i];
-            }
-            const Split8<NS> sf = split8<NS>(xx);
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
-                Ot[tb] = mfma_split<NS, NS, NS>(sf, qf, Ot[tb]);
-            }
-        }
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {  // V^T A^T over key blocks <= tb
 #pragma unroll
@@ -529,6 +486,65 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
                                       : bf16x8{lo[0], lo[1], lo[2], lo[3], z, z, z, z};
                 }
                 Ot[tb] = mfma_split<NX, NS, NS>(vf[k2], af, Ot[tb]);
+            }
+        }
+    }
+
+    // ---- the state entering the chunk ------------------------------------------------------------
+    f32x4 S[4];
+    if (a.s0) {
+        const float* s0 = a.s0 + bh * (int64_t)(DK * DV);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[db][i] = s0[state_off(db, i, g4, r16, wave, DV)];
+    } else {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) S[db] = zero4();
+    }
+    if (p > 0) {
+        bool ok = false, same = true;
+        for (uint32_t n = 0; n < OP_SPIN_MAX; ++n) {
+            if (__all(lane >= p || (uint32_t)fw == ep)) {
+                ok = true;
+                same = __all(lane >= p || (uint32_t)(fw >> 32) == xcc);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            if (lane < p) fw = __hip_atomic_load(fl + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (lane == 0 && (!ok || !same))
+            __hip_atomic_fetch_or(ctl.hdr + 2, ok ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (same) fold_states<OP_SC0>(rL, rE, sEGj, (int)p, S, g4);
+        else fold_states<OP_SC1>(rL, rE, sEGj, (int)p, S, g4);
+    }
+    if (grp == 1) {  // through the pair's first chunk: S <- e^{G_C(A)} S + L_A
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const f32x4 la = *reinterpret_cast<const f32x4*>(sX + (db * 256 + tid) * 4);
+            const f32x4 ea = *reinterpret_cast<const f32x4*>(sEG0 + 16 * db + 4 * g4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) S[db][i] = fmaf(ea[i], S[db][i], la[i]);
+        }
+    }
+
+    // ---- outputs: O^T += (e^m S)^T Qt^T ------------------------------------------------------------
+    if (fast) {
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const f32x4 e0 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 4 * g4);
+            const f32x4 e1 = *reinterpret_cast<const f32x4*>(sEM + 32 * ks + 16 + 4 * g4);
+            float xx[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                xx[i] = S[2 * ks][i] * e0[i];
+                xx[4 + i] = S[2 * ks + 1][i] * e1[i];
+            }
+            const Split8<NS> sf = split8<NS>(xx);
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const Split8<NS> qf = lds_frag<NS>(sQT, L::ROWP, L::RS, 16 * tb + r16, 32 * ks, g4);
+                Ot[tb] = mfma_split<NS, NS, NS>(sf, qf, Ot[tb]);
             }
         }
         PendingOut pend;

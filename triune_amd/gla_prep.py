@@ -31,6 +31,11 @@ __all__ = ["fused_qkv_g_prep_inplace", "fused_qkvg_decode_step", "fused_qkvg_dec
 
 _HD = (32, 64, 128)
 
+# Past this many chunk-head workgroups per compute unit fused_qkv_g_prep_chunk_gla runs the
+# pre-processing pass and then the prefill instead of the pre-processing inside the segment-state
+# kernel (both give the same results; the bench times either form by changing it).
+FUSED_MAX_CHUNK_HEADS_PER_CU = 4
+
 
 def _cuda(*ts):
     for t in ts:
@@ -218,7 +223,8 @@ def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin
     L = lib()
     onepass = _fg.ONEPASS and HD == 64 and bool(
         L.triune_hip_gla_prefill_onepass_supported(B, T, H, HD, dtype_code(qkv), dtype_code(qkv), 1, 0))
-    if not onepass and B * H * ((T + 63) // 64) > 4 * torch.cuda.get_device_properties(qkv.device).multi_processor_count:
+    cus = torch.cuda.get_device_properties(qkv.device).multi_processor_count
+    if not onepass and B * H * ((T + 63) // 64) > FUSED_MAX_CHUNK_HEADS_PER_CU * cus:
         fused_qkv_g_prep_inplace(qkv, g, cos, sin, use_rope=use_rope)
         return _triton_chunk_gla_tc_fwd(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], g, initial_state=initial_state,
                                         out=g if out is None else out, save_final=save_final)
