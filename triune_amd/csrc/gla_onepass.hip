@@ -75,11 +75,15 @@ struct OpLay {
 };
 
 // The state entering pair p from s0's value in S and the published maps of pairs j < p:
-// S <- e^{G_C(j)} S + L_j in order.  The decay factors are staged in LDS (sEGj, p x 64 floats) by
-// the whole workgroup; each thread then loads its 16 values of up to eight L_j at a time.
-template <int CPOL>
-__device__ __forceinline__ void fold_states(__amdgpu_buffer_rsrc_t rL, __amdgpu_buffer_rsrc_t rE, float* sEGj,
-                                            int pj, f32x4 (&S)[4], int g4) {
+// S <- e^{G_C(j)} S + L_j in order, on the rows 32 HALF .. 32 HALF + 31 of the state (vectors
+// db = 2 HALF, 2 HALF + 1); each chunk group folds one half and the caller exchanges them, so a
+// workgroup reads every map once.  The decay factors are staged in LDS (sEGj, p x 64 floats) by
+// the whole workgroup; each thread then loads its 8 values of up to eight L_j at a time (slots
+// past the last map read through a resource without records, which moves no data).  maps: L_0 of
+// this (sequence, head).
+template <int CPOL, int HALF>
+__device__ __forceinline__ void fold_half(const float* maps, __amdgpu_buffer_rsrc_t rE, float* sEGj, int pj,
+                                          f32x4 (&S)[4], int g4) {
     auto ld4 = [](__amdgpu_buffer_rsrc_t r, int off) {
         return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL));
     };
@@ -88,26 +92,27 @@ __device__ __forceinline__ void fold_states(__amdgpu_buffer_rsrc_t rL, __amdgpu_
     __syncthreads();
     // L_j as [4][256 threads][4 floats]: the values of vector db of every thread of a group are
     // 4 KB in a row, so each 16-byte-per-lane load of a wave reads 1 KB of whole cache lines
-    const int lo = ((int)threadIdx.x & 255) * 16;
-    // eight maps per round, all loads in flight together (a short last round reloads map pj - 1
-    // for its unused slots and skips them)
+    const int lo = ((int)threadIdx.x & 255) * 16 + 4096 * 2 * HALF;
     for (int j = 0; j < pj; j += 8) {
         const int n = pj - j < 8 ? pj - j : 8;
-        f32x4 lj[8][4];
+        f32x4 lj[8][2];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int m = j + (u < n ? u : n - 1);
+            const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float*>(maps) + (int64_t)(j + u) * (OP_D * OP_D), (short)0, u < n ? OP_D * OP_D * 4 : 0,
+                0x00020000);
 #pragma unroll
-            for (int db = 0; db < 4; ++db) lj[u][db] = ld4(rL, m * (OP_D * OP_D * 4) + lo + 4096 * db);
+            for (int dh = 0; dh < 2; ++dh) lj[u][dh] = ld4(r, lo + 4096 * dh);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             if (u >= n) break;
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
+            for (int dh = 0; dh < 2; ++dh) {
+                const int db = 2 * HALF + dh;
                 const f32x4 e = *reinterpret_cast<const f32x4*>(sEGj + (j + u) * OP_D + 16 * db + 4 * g4);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) S[db][i] = fmaf(e[i], S[db][i], lj[u][db][i]);
+                for (int i = 0; i < 4; ++i) S[db][i] = fmaf(e[i], S[db][i], lj[u][dh][i]);
             }
         }
     }
@@ -502,8 +507,9 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
 #pragma unroll
         for (int db = 0; db < 4; ++db) S[db] = zero4();
     }
+    bool same = true;  // every awaited map in this XCD's L2
     if (p > 0) {
-        bool ok = false, same = true;
+        bool ok = false;
         for (uint32_t n = 0; n < OP_SPIN_MAX; ++n) {
             if (__all(lane >= p || (uint32_t)fw == ep)) {
                 ok = true;
@@ -515,16 +521,47 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
         }
         if (lane == 0 && (!ok || !same))
             __hip_atomic_fetch_or(ctl.hdr + 2, ok ? 2u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (same) fold_states<OP_SC0>(rL, rE, sEGj, (int)p, S, g4);
-        else fold_states<OP_SC1>(rL, rE, sEGj, (int)p, S, g4);
+    }
+    f32x4 la[4];  // group 1: L_A, taken from sX before the halves pass through it
+    if (grp == 1) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) la[db] = *reinterpret_cast<const f32x4*>(sX + (db * 256 + tid) * 4);
+    }
+    if (p > 0) {
+        const float* maps = a.ws_state + bh * ctl.npair * (int64_t)(DK * DV);
+        if (grp == 0) {
+            if (same) fold_half<OP_SC0, 0>(maps, rE, sEGj, (int)p, S, g4);
+            else fold_half<OP_SC1, 0>(maps, rE, sEGj, (int)p, S, g4);
+        } else {
+            if (same) fold_half<OP_SC0, 1>(maps, rE, sEGj, (int)p, S, g4);
+            else fold_half<OP_SC1, 1>(maps, rE, sEGj, (int)p, S, g4);
+        }
+        // the halves through sX (thread tid of either group holds the same state entries; the
+        // barrier inside the fold orders group 1's reads of L_A before these writes)
+        auto put = [&](int db) { *reinterpret_cast<f32x4*>(sX + (db * 256 + tid) * 4) = S[db]; };
+        auto get = [&](int db) { S[db] = *reinterpret_cast<const f32x4*>(sX + (db * 256 + tid) * 4); };
+        if (grp == 0) {
+            put(0);
+            put(1);
+        } else {
+            put(2);
+            put(3);
+        }
+        lds_sync();
+        if (grp == 0) {
+            get(2);
+            get(3);
+        } else {
+            get(0);
+            get(1);
+        }
     }
     if (grp == 1) {  // through the pair's first chunk: S <- e^{G_C(A)} S + L_A
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
-            const f32x4 la = *reinterpret_cast<const f32x4*>(sX + (db * 256 + tid) * 4);
             const f32x4 ea = *reinterpret_cast<const f32x4*>(sEG0 + 16 * db + 4 * g4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) S[db][i] = fmaf(ea[i], S[db][i], la[i]);
+            for (int i = 0; i < 4; ++i) S[db][i] = fmaf(ea[i], S[db][i], la[db][i]);
         }
     }
 
