@@ -156,11 +156,17 @@ __global__ __launch_bounds__(SCAN_TPB) void recurrent_scan_typed_kernel(ScanPara
 // The prefill's carry over segments: fp32 kv and s_all (the same buffer), fp32 log-decay, fp32
 // init / fin.  All U loads of a block of steps are issued before the dependent chain runs, so a
 // typical sequence (at most U segments) pays one memory latency; the chain itself is four
-// independent FMA lanes per step with exp on the hardware exp2.
+// independent FMA lanes per step with exp on the hardware exp2.  The steps go through buffer
+// instructions: per block of steps one resource based at the block's lowest step (the first, or
+// with a negative step stride, as the backward's reverse scan has, the last) at the workgroup's
+// first element (kv) or the decays, the lane's offset in the vector register and the step's
+// distance from the base in the scalar offset, so no step costs vector address arithmetic.
 template <int U>
 __global__ __launch_bounds__(SCAN_TPB) void seg_scan_f32_kernel(ScanParams a) {
     const int64_t DD = (int64_t)a.Dk * a.Dv;
-    const int64_t e = ((int64_t)blockIdx.x * SCAN_TPB + threadIdx.x) * 4;
+    const int64_t eb = (int64_t)blockIdx.x * SCAN_TPB * 4;  // the workgroup's first element
+    const int t = (int)threadIdx.x;
+    const int64_t e = eb + 4 * t;
     if (e >= DD) return;
     const int64_t h = blockIdx.y, o = blockIdx.z;
     const int row = (int)(e / a.Dv);
@@ -178,22 +184,34 @@ __global__ __launch_bounds__(SCAN_TPB) void seg_scan_f32_kernel(ScanParams a) {
     }
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (a.init && has_row) s = *reinterpret_cast<const float4*>(a.init + srow * a.i_so + h * a.i_sh + e);
-    float* kv = const_cast<float*>(reinterpret_cast<const float*>(a.kv)) + o * a.kv_so + h * a.kv_sh + e;
-    const float* dec = reinterpret_cast<const float*>(a.dec) + o * a.d_so + h * a.d_sh + row;
+    float* kv = const_cast<float*>(reinterpret_cast<const float*>(a.kv)) + o * a.kv_so + h * a.kv_sh + eb;
+    float* dec = const_cast<float*>(reinterpret_cast<const float*>(a.dec)) + o * a.d_so + h * a.d_sh;
+    const bool kneg = a.kv_sn < 0, dneg = a.d_sn < 0;
+    const int32_t kst = (int32_t)((kneg ? -a.kv_sn : a.kv_sn) * 4);  // bytes per step
+    const int32_t dst = (int32_t)((dneg ? -a.d_sn : a.d_sn) * 4);
+    const int32_t kvo = 16 * t, dvo = 4 * row;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     for (int64_t n = 0; n < N; n += U) {
+        const int32_t last = (int32_t)(N - n < U ? N - n : U) - 1;  // the block's last step
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            kv + (n0 + n + (kneg ? last : 0)) * a.kv_sn, (short)0, 0x7fffffff, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+            dec + (n0 + n + (dneg ? last : 0)) * a.d_sn, (short)0, 0x7fffffff, 0x00020000);
+        auto koff = [&](int32_t u) { return (kneg ? last - u : u) * kst; };
+        auto doff = [&](int32_t u) { return (dneg ? last - u : u) * dst; };
         float4 x[U];
         float d[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t i = n0 + (n + u < N ? n + u : N - 1);
-            x[u] = *reinterpret_cast<const float4*>(kv + i * a.kv_sn);
-            d[u] = dec[i * a.d_sn];
+            const int32_t uu = u < last ? u : last;  // a short block re-reads its last step
+            x[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, kvo, koff(uu), 0));
+            d[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, dvo, doff(uu), 0));
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            if (n + u < N) {
+            if (u <= last) {
                 const float dd = fast_exp(d[u]);
-                *reinterpret_cast<float4*>(kv + (n0 + n + u) * a.kv_sn) = s;  // exclusive prefix
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, s), rk, kvo, koff(u), 0);  // exclusive prefix
                 s.x = s.x * dd + x[u].x;
                 s.y = s.y * dd + x[u].y;
                 s.z = s.z * dd + x[u].z;
