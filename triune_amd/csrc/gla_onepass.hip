@@ -222,9 +222,6 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
     const int c0 = wave * 16;
     const int dl0 = stage1_dim0<DK, DPW, PREP>(wave, row);
 
-    // epoch of this call: flags of this call carry ep; the last workgroup to finish stores ep
-    const uint32_t ep =
-        (uint32_t)__builtin_amdgcn_readfirstlane((int)__hip_atomic_load(ctl.hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) + 1u;
 
     const ChunkAddr ad = chunk_addr<true, TIn, TG>(a, wk, h, tg, dl0, c0 + 4 * row);
     ChunkIn<TIn, TG, DL> cur;
@@ -293,6 +290,10 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
         }
     }
     __syncthreads();  // every wave's flags (and PREP: norm partials)
+    // Epoch of this call: flags of this call carry ep; the last workgroup to finish stores ep.
+    // Read once the chunk's loads are all out, and made uniform where the flag is stored, so its
+    // latency runs under the rest of stage 1.
+    const uint32_t ep_word = __hip_atomic_load(ctl.hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     bool fast = true;
 #pragma unroll
     for (int w = 0; w < NW; ++w) fast = fast && (sFLAG[w] == 0);
@@ -417,6 +418,7 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
     wait_vmem();
     __syncthreads();
     const uint32_t xcc = (uint32_t)__builtin_amdgcn_s_getreg(OP_HWREG_XCC_ID) & 0xfu;
+    const uint32_t ep = (uint32_t)__builtin_amdgcn_readfirstlane((int)ep_word) + 1u;
     if (!last_pair && threadIdx.x == 0)
         __hip_atomic_store(ctl.flags + slot, (uint64_t)ep | ((uint64_t)xcc << 32), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
