@@ -5,8 +5,9 @@ fp32 state (config 1), with the batched decode step at B=256 (config 2) reported
 
   step (prefill) = one fast_chunk_gla forward over the whole [4, 16384, 6, 64] batch, inputs
                    resident in HBM (two input sets used in turn, together larger than the 256 MB
-                   MALL), bf16 outputs and fp32 final states written to HBM (three kernels,
-                   called directly; a HIP-graph replay of the pass measured no faster).
+                   MALL), bf16 outputs and fp32 final states written to HBM (three kernels; the
+                   timed passes are one HIP-graph replay, the same passes as direct calls are
+                   reported beside it).
   step (decode)  = one decode step for 256 sequences (H=6, D=64) on one of 12 rotating fp32
                    state buffers (302 MB in total, larger than the 256 MB MALL) with one of 12
                    rotating q/k/v/g/o sets; the 512-step loop is captured in a HIP graph and
@@ -309,13 +310,12 @@ def bench_fused_prefill(dev, reps=20, T=16384):
     """VectorisedGLA's prefill from raw projections (qkv [4, T, 3, 6, 64] and gate logits
     g [4, T, 6, 64] bf16, fp32 RoPE tables, fp32 S0; T = 1024 is the tile VectorisedGLA runs every
     prefill in, attention.py:458-499): fused_qkv_g_prep_chunk_gla as dispatched (one launch where
-    the call fits the single-launch prefill, as at T = 1024), the same entry with the single launch
-    switched off (pre-processing inside the segment-state kernel, then the carry scan and the
-    output kernel; past four chunk-heads per CU the prep pass and then the prefill), the
-    two-step pipeline the reference launches (in-place pre-processing, then the three-launch
-    prefill) and, past four chunk-heads per CU, the entry with the pre-processing kept inside the
-    segment-state kernel ("fused_in_state_kernel").  A warm-up of 60 two-step calls precedes the
-    legs.  "us": GPU time per call, calls back to back in a replayed HIP graph, each on its own
+    the call fits the single-launch prefill, as at T = 1024; otherwise the prep pass and then the
+    prefill), the same entry with the single launch switched off, the two-step pipeline the
+    reference launches (in-place pre-processing, then the three-launch prefill) called directly,
+    and the entry with the pre-processing forced inside the segment-state kernel
+    ("fused_in_state_kernel", gla_prep.FUSED_MAX_CHUNK_HEADS_PER_CU raised).  A warm-up of 60
+    two-step calls precedes the legs.  "us": GPU time per call, calls back to back in a replayed HIP graph, each on its own
     raw input set (restored before every replay, untimed); "eager_us": one Python call at a time
     between events, host work included."""
     import triune_amd.fast_gla as FG
@@ -360,10 +360,13 @@ def bench_fused_prefill(dev, reps=20, T=16384):
     torch.cuda.synchronize()
     res, eager = {}, {}
     onepass0, fmax0 = FG.ONEPASS, GP.FUSED_MAX_CHUNK_HEADS_PER_CU
+    from triune_amd._lib import lib as _l
+
+    one = bool(_l().triune_hip_gla_prefill_onepass_supported(B, T, H, HD, 1, 1, 1, 0))
+    in_state = not one and B * H * ((T + 63) // 64) <= fmax0 * torch.cuda.get_device_properties(dev).multi_processor_count
     legs = [("fused", fused, True, fmax0), ("fused_three_launch", fused, False, fmax0),
             ("prep_then_prefill", two_step, False, fmax0)]
-    if B * H * ((T + 63) // 64) > fmax0 * torch.cuda.get_device_properties(dev).multi_processor_count:
-        # past the threshold the entry runs the pre-processing pass first: time the other form too
+    if not in_state:  # the entry does not take the pre-processing inside the segment-state kernel: time it too
         legs.append(("fused_in_state_kernel", fused, False, 1 << 30))
     try:
         for name, fn, onepass, fmax in legs:
@@ -384,13 +387,11 @@ def bench_fused_prefill(dev, reps=20, T=16384):
         FG.ONEPASS, GP.FUSED_MAX_CHUNK_HEADS_PER_CU = onepass0, fmax0
     alg = gla_algorithmic_bytes(B * T * H, HD, HD, 2, 2, 2) + 2 * B * H * HD * HD * 4
     gbs = alg / (res["fused"] * 1e-6) / 1e9
-    from triune_amd._lib import lib as _l
-
-    one = bool(_l().triune_hip_gla_prefill_onepass_supported(B, T, H, HD, 1, 1, 1, 0))
     return {"workload": f"VectorisedGLA prefill from raw projections (B=4, T={T}, H=6, HD=64, bf16, "
             "RoPE, gate logits N(3,1))",
             "path": "single launch (pre-processing, chunk states and outputs)" if one else
-            "pre-processing pass, then the three-launch prefill",
+            ("pre-processing inside the segment-state kernel, then the carry scan and the output kernel"
+             if in_state else "pre-processing pass, then the three-launch prefill"),
             "timing": f"GPU time per call: {n_sets} calls on their own input sets back to back in a replayed "
             "HIP graph; eager_*: one Python call between events",
             "us": round(res["fused"], 2), "tok_s": round(B * T / (res["fused"] * 1e-6), 1),

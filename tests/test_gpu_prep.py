@@ -188,13 +188,17 @@ def test_fused_decode_steps_equal_prep_then_decode(dev):
 # against oracle.qkv_g_prep (one ULP of the I/O dtype), and the outputs and final states against
 # oracle.gla_fwd on the values the device left (2e-3 for fp32 outputs, one bf16 ULP + 2e-3 for
 
-@pytest.fixture(params=["onepass", "three_launch"])
+@pytest.fixture(params=["onepass", "in_state", "two_step"])
 def prefill_path(request, monkeypatch):
-    """The fused pre-processing prefill on both paths: calls of few chunks at head dim 64 take the
-    single launch unless it is switched off."""
+    """The fused pre-processing prefill on its three paths: calls of few chunks at head dim 64 take
+    the single launch unless it is switched off; without it the entry runs the pre-processing
+    inside the segment-state kernel up to gla_prep.FUSED_MAX_CHUNK_HEADS_PER_CU chunk-heads per
+    compute unit (raised here to reach that kernel) and the prep pass then the prefill past it."""
     import triune_amd.fast_gla as FG
+    import triune_amd.gla_prep as GP
 
     monkeypatch.setattr(FG, "ONEPASS", request.param == "onepass")
+    monkeypatch.setattr(GP, "FUSED_MAX_CHUNK_HEADS_PER_CU", 1 << 30 if request.param == "in_state" else 0)
     return request.param
 
 # bf16 outputs).
@@ -320,9 +324,10 @@ def test_fused_prep_prefill_equals_prep_then_prefill(prefill_path, dev):
     assert float((sf - s2).abs().max()) <= 2.0**-7 * float(s2.abs().max())
 
 
-def test_fused_prep_prefill_large_call_takes_two_step_path(prefill_path, dev):
-    """B * H * chunks beyond four per compute unit: the entry runs the prep kernel and then the
-    prefill (the faster arrangement there); same checks as the fused path."""
+def test_fused_prep_prefill_large_call_takes_two_step_path(dev):
+    """B * H * chunks beyond four per compute unit, with the entry's default settings: the call does
+    not fit the single launch, so the entry runs the prep kernel and then the prefill (the faster
+    arrangement); same checks as the fused paths."""
     from triune_amd import fused_qkv_g_prep_chunk_gla
 
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
@@ -340,13 +345,18 @@ def test_fused_prep_prefill_large_call_takes_two_step_path(prefill_path, dev):
     assert float(np.abs(s.double().cpu().numpy() - rs).max()) <= 2e-3
 
 
-@pytest.mark.parametrize("B,H", [(1, 3), (4, 6)])
-def test_fused_prep_prefill_config1_length(dev, B, H):
-    """The fused entry at config 1's length (T = 16384): B = 1, H = 3 (768 chunk-heads) runs the
-    pre-processing inside the segment-state kernel, B = 4, H = 6 (6144) the prep pass and then the
-    prefill; both against the oracle on the values the device left (2e-3 for fp32 outputs and
-    states, one ULP of the I/O dtype for the pre-processed tensors)."""
+@pytest.mark.parametrize("B,H,in_state", [(1, 3, True), (4, 6, False)])
+def test_fused_prep_prefill_config1_length(dev, B, H, in_state, monkeypatch):
+    """The fused entry at config 1's length (T = 16384) with the pre-processing inside the
+    segment-state kernel (forced through gla_prep.FUSED_MAX_CHUNK_HEADS_PER_CU) and on the entry's
+    default path (the prep pass and then the prefill), against the oracle on the values the device
+    left (2e-3 for fp32 outputs and states, one ULP of the I/O dtype for the pre-processed
+    tensors)."""
+    import triune_amd.gla_prep as GP
     from triune_amd import fused_qkv_g_prep_chunk_gla
+
+    if in_state:
+        monkeypatch.setattr(GP, "FUSED_MAX_CHUNK_HEADS_PER_CU", 1 << 30)
 
     T, HD = 16384, 64
     qkv, g, s0 = _fused_case(B, T, H, HD, seed=B * 100 + H, gate_shift=3.0)

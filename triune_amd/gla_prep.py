@@ -31,10 +31,13 @@ __all__ = ["fused_qkv_g_prep_inplace", "fused_qkvg_decode_step", "fused_qkvg_dec
 
 _HD = (32, 64, 128)
 
-# Past this many chunk-head workgroups per compute unit fused_qkv_g_prep_chunk_gla runs the
-# pre-processing pass and then the prefill instead of the pre-processing inside the segment-state
-# kernel (both give the same results; the bench times either form by changing it).
-FUSED_MAX_CHUNK_HEADS_PER_CU = 4
+# Calls that the single launch does not take run the pre-processing inside the segment-state
+# kernel (triune_hip_gla_prefill_prep) only up to this many chunk-head workgroups per compute unit,
+# and the pre-processing pass and then the prefill past it.  Both give the same results; the pass
+# and the prefill measured faster at every size (B = 4, H = 6 on MI355X: T = 1024 with the single
+# launch off 29.1 against 31.0 us, T = 2048 44.4 against 46.7 us, T = 4096 65.8 against 69.9 us,
+# T = 16384 176 against 196 us), so 0: never.  Tests and the bench raise it to reach the other form.
+FUSED_MAX_CHUNK_HEADS_PER_CU = 0
 
 
 def _cuda(*ts):
@@ -190,16 +193,15 @@ def fused_qkv_g_prep_chunk_gla(qkv: torch.Tensor, g: torch.Tensor, cos=None, sin
     processed tensors.
 
     Calls of at most 64 chunks per sequence whose chunk-head workgroups are all resident at once
-    (head dim 64; B = 4, H = 6, T = 1024 is 384 of them) run everything in one launch,
-    triune_hip_gla_prefill_onepass: each workgroup pre-processes its chunk, publishes the chunk's
-    local state, folds the earlier chunks' into the state it enters with and writes its outputs.
-    Otherwise the fused form runs while the call is small enough for the chunk kernels to be latency-bound
-    (B * H * ceil(T / 64) at most 4 per compute unit, as at VectorisedGLA's 1024-token prefill tiles,
-    attention.py:458-499: 35.0 against 36.1 us for the two-step pipeline at B = 4, H = 6, T = 1024
-    on MI355X).  Past that the kernels are throughput-bound and the pre-processing work weighs more
-    inside the segment-state kernel than as a pass of its own (T = 4096: 71 against 65 us; T = 16384:
-    206 against 173 us), so larger calls run fused_qkv_g_prep_inplace and then the prefill, with the
-    same results.
+    (head dim 64; B = 4, H = 6, T = 1024 is 384 of them, VectorisedGLA's prefill tile,
+    attention.py:458-499) run everything in one launch, triune_hip_gla_prefill_onepass: each
+    workgroup pre-processes its chunk pair, publishes the pair's local state, folds the earlier
+    pairs' into the state it enters with and writes its outputs (19.8-20.4 us per call against
+    29-31 us for the pre-processing pass and then the prefill).  Other calls run
+    fused_qkv_g_prep_inplace and then the prefill, with the same results: the pre-processing inside
+    the segment-state kernel (triune_hip_gla_prefill_prep, used while B * H * ceil(T / 64) is at
+    most FUSED_MAX_CHUNK_HEADS_PER_CU per compute unit) measured slower at every size, its VALU work
+    weighing more inside the chunk kernel's dependent chain than as a bandwidth-bound pass.
 
     qkv: [B, T, 3, H, HD] raw projections (bf16 or fp16), g: [B, T, H, HD] raw gate (same dtype),
     cos/sin: [T, HD] (used when use_rope; converted to fp32 if needed), initial_state: [B, H, HD,
