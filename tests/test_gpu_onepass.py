@@ -1,8 +1,9 @@
 """GPU parity of the single-launch GLA prefill (triune_hip_gla_prefill_onepass) against the fp64
 oracle, and of its control-block protocol.
 
-One workgroup per 64-token chunk of each (sequence, head) publishes its chunk-local state and folds
-the earlier chunks' into the state it enters with (no carry-scan kernel).  The call shapes are the
+One workgroup per pair of 64-token chunks of each (sequence, head) publishes the pair's state map
+and folds the earlier pairs' into the state it enters with (no carry-scan kernel).  The call shapes
+are the
 prefill tiles the reference's VectorisedGLA runs (B = 4, T <= 1024, H = 6, head dim 64:
 triune/model/attention.py:425-451, 458-499) and ragged, token-wise and clamp-dispatch cases.
 Tolerances as for the three-launch path: fp32 outputs and states within 2e-3 of the oracle for
@@ -88,6 +89,26 @@ def test_ragged_lengths_against_three_launch_and_oracle(dev, T, with_init, monke
     assert _supported(2, T, 3)
     qd, kd, vd, gd = (x.to(dev) for x in (q, k, v, g))
     s0d = None if s0 is None else s0.to(dev)
+    ro, rs = O.gla_fwd(q, k, v, g, s0)
+    for onepass in (True, False):
+        monkeypatch.setattr(FG, "ONEPASS", onepass)
+        out = torch.empty(v.shape, device=dev, dtype=torch.float32)
+        o, s = fast_chunk_gla(qd, kd, vd, gd, initial_state=s0d, out=out)
+        torch.cuda.synchronize()
+        assert _err(o, ro) <= TOL16, (onepass, _err(o, ro))
+        assert _err(s, rs) <= TOL16, (onepass, _err(s, rs))
+    assert _ctrl(dev)[2] == 0
+
+
+@pytest.mark.parametrize("T", [1100, 2500, 4096])
+def test_many_pairs_fold_in_rounds(dev, T, monkeypatch):
+    """Up to 64 chunks per sequence (32 pairs): a workgroup folds the earlier pairs' maps eight at a
+    time, so T = 1100 (9 pairs) ends on one full round, T = 2500 (20 pairs) on a short third round and
+    T = 4096 on four rounds; each chunk group folds half the state rows and the halves meet in LDS.
+    Against the oracle, with the three-launch path on the same inputs held to the same bar."""
+    q, k, v, g, s0 = gla_inputs(1, T, 2, 64, seed=500 + T, dtype=torch.bfloat16, init_std=0.2)
+    assert _supported(1, T, 2)
+    qd, kd, vd, gd, s0d = (x.to(dev) for x in (q, k, v, g, s0))
     ro, rs = O.gla_fwd(q, k, v, g, s0)
     for onepass in (True, False):
         monkeypatch.setattr(FG, "ONEPASS", onepass)
