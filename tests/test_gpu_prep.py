@@ -250,6 +250,28 @@ def test_fused_prep_prefill_matches_oracle(prefill_path, dev, HD, T, rope):
     assert e_o <= 2e-3 and e_s <= 2e-3, (e_o, e_s)
 
 
+@pytest.mark.parametrize("T", [2500, 4096])
+def test_fused_prep_single_launch_many_pairs(dev, T):
+    """The single launch with the pre-processing over 20 and 32 chunk pairs per sequence (the fold
+    of the earlier pairs' maps in rounds of eight); the values left in place and the outputs and
+    final states against the oracle."""
+    from triune_amd import fused_qkv_g_prep_chunk_gla
+    from triune_amd._lib import lib
+
+    B, H, HD = 1, 2, 64
+    assert lib().triune_hip_gla_prefill_onepass_supported(B, T, H, HD, 1, 1, 1, 0)
+    qkv, g, s0 = _fused_case(B, T, H, HD, seed=T, gate_shift=3.0)
+    cos, sin = _tables(T, HD)
+    qd, gd = qkv.to(dev), g.to(dev)
+    out = torch.empty(B, T, H, HD, device=dev, dtype=torch.float32)
+    o, s = fused_qkv_g_prep_chunk_gla(qd, gd, cos.to(dev), sin.to(dev), initial_state=s0.to(dev), out=out)
+    torch.cuda.synchronize()
+    _check_prepped(qd, gd, qkv, g, cos, sin)
+    ro, rs = O.gla_fwd(qd[:, :, 0].cpu(), qd[:, :, 1].cpu(), qd[:, :, 2].cpu(), gd.cpu(), s0)
+    e_o, e_s = float(np.abs(o.double().cpu().numpy() - ro).max()), float(np.abs(s.double().cpu().numpy() - rs).max())
+    assert e_o <= 2e-3 and e_s <= 2e-3, (e_o, e_s)
+
+
 @pytest.mark.parametrize("HD", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_fused_prep_prefill_out_over_g(prefill_path, dev, HD, dtype):
