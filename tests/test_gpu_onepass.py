@@ -74,7 +74,7 @@ def test_reference_tile_matches_oracle(dev, out_dtype):
         assert float(excess.max()) <= 0, float(excess.max())
     assert _err(s, rs) <= TOL16, _err(s, rs)
     hdr = _ctrl(dev)
-    assert hdr[1] == 0 and hdr[2] == 0, hdr  # finished-workgroup count reset, no wait ran out
+    assert hdr[1] == 0 and hdr[2] == 0, hdr  # epoch-read count back to zero, no wait ran out
     if before is not None:
         assert hdr[0] == before[0] + 1, (before, hdr)
 

@@ -30,8 +30,9 @@
 // out records an error bit in the control block and the kernel still ends.
 //
 // Flags need no clearing between calls: the control block (caller-owned, zero before its first
-// use, reused stream-ordered) holds an epoch; a call publishes epoch + 1, and the workgroup that
-// finishes last advances the epoch, so flags left by earlier calls never match.
+// use, reused stream-ordered) holds an epoch; a call publishes epoch + 1, and once every
+// workgroup has read the epoch (a count) the last one counted advances it at its end, so flags
+// left by earlier calls never match.
 //
 // Where the published maps live.  Dispatch hands workgroup x to XCD x mod 8 (round robin; with
 // fewer XCDs per partition, a divisor of 8, the residue still fixes the XCD), and all pairs of a
@@ -422,6 +423,16 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
     if (!last_pair && threadIdx.x == 0)
         __hip_atomic_store(ctl.flags + slot, (uint64_t)ep | ((uint64_t)xcc << 32), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+    // Count this workgroup's epoch read (complete: its value is in ep).  The count wraps to zero
+    // at the number of workgroups (an increment that wraps at total - 1), and the workgroup that
+    // sees total - 1 counted last: every workgroup has read the epoch, so it may advance it; the
+    // next call reads it after this kernel has ended.  The count orders nothing but itself and its
+    // result is used only at the end, so the round trip runs under the rest of the pair (a
+    // wrapping increment, unlike an add, is not rewritten into a combined add whose result the
+    // wave must wait for at once).
+    const uint32_t total = (uint32_t)(BH * ctl.npair);
+    uint32_t counted = 0;
+    if (threadIdx.x == 0) counted = __builtin_amdgcn_atomic_inc32(ctl.hdr + 1, total - 1u, __ATOMIC_RELAXED, "agent");
 
     // ---- while earlier pairs publish: stage 2 and the outputs' in-chunk part ------------------
     // Neither depends on the state entering the chunk: A^T tiles -> LDS, then O^T = V^T A^T.
@@ -613,18 +624,9 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
             for (int i = 0; i < 4; ++i) sf[state_off(db, i, g4, r16, wave, DV)] = S[db][i];
     }
 
-    // ---- the last workgroup to finish advances the epoch (flags of this call become stale) ----
-    __syncthreads();  // every wave is past its flag reads
-    if (threadIdx.x == 0) {
-        const uint32_t total = (uint32_t)(BH * ctl.npair);
-        // the count orders nothing but itself: the epoch it advances is read by the next call,
-        // after this kernel has ended
-        const uint32_t d = __hip_atomic_fetch_add(ctl.hdr + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (d + 1 == total) {
-            __hip_atomic_store(ctl.hdr + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(ctl.hdr, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    // ---- the last workgroup to count advances the epoch (flags of this call become stale) -----
+    if (threadIdx.x == 0 && counted == total - 1u)
+        __hip_atomic_store(ctl.hdr, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ev0 / ev1: if not null, events stamped with the kernel's own start and end (hipExtLaunchKernel).
