@@ -291,7 +291,8 @@ __global__ __launch_bounds__(OP_THREADS, 1) void gla_onepass_kernel(PrefillParam
         }
     }
     __syncthreads();  // every wave's flags (and PREP: norm partials)
-    // Epoch of this call: flags of this call carry ep; the last workgroup to finish stores ep.
+    // Epoch of this call: flags of this call carry ep; the last workgroup to count its read of it
+    // stores ep at its end.
     // Read once the chunk's loads are all out, and made uniform where the flag is stored, so its
     // latency runs under the rest of stage 1.
     const uint32_t ep_word = __hip_atomic_load(ctl.hdr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
