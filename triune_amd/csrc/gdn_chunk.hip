@@ -551,9 +551,14 @@ struct GdnStep {
                                const GChunkIn<TIn, TG, PBK>& cur, const TokAddr& kb, f32x4 (&S)[NDB],
                                f32x4 (&SN)[NDB], bool skip_m, char* smem, const f32x4* bv_in, Hook&& after_inputs) {
         const Ctx c = ctx(smem, wave_id());
+        // Issue priority: stage 1 at the base level, stage 2 and the passes that carry the state one
+        // level up, so of the workgroups on a CU the one further along issues first (config 3 with
+        // per-key-dim gates 0.166 -> 0.159 ms, same-box A/B).
+        __builtin_amdgcn_s_setprio(0);
         stage1(a, wk, h, tc, nv, cur, kb, c);
         if constexpr (!LATE_LOAD && !LATE_LOAD_OUT) after_inputs();
         __syncthreads();
+        __builtin_amdgcn_s_setprio(1);
         if (!chunk_fast(c)) {
             if (!skip_m) gdn_tokenwise<TIn, TG, OUT, BV>(a, wk, h, c.c0, tc, nv, c.g4, c.r16, OUT, S);
             if (!OUT) gdn_tokenwise<TIn, TG, false, BV>(a, wk, h, c.c0, tc, nv, c.g4, c.r16, true, SN);
