@@ -347,7 +347,7 @@ struct OutStep {
         // Issue priority: stage 1 (throughput work: factors, splits, the previous chunk's stores) at
         // the base level, stages 2-3 (the MFMA chains that carry the state) one level up, so of the
         // two workgroups on a CU the one in stages 2-3 issues first and the other fills its gaps
-        // (config-1 pass 123.6 -> 118.1 us, output kernel 79.0 -> 74.5 us by events, same box).
+        // (config-1 pass 120.9 -> 118.2 us, output kernel 76.1 -> 72.3 us by events, same-box A/B).
         __builtin_amdgcn_s_setprio(0);
         // ---------------- stage 1 -------------------------------------------------------
         if constexpr (DMA) {

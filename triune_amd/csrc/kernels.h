@@ -199,10 +199,10 @@ struct FusedDecodeParams {
 };
 
 // Control block of the single-launch prefill (gla_onepass.hip): hdr[0] epoch, hdr[1] workgroups of
-// the running call that have read the epoch (back to zero when all have), hdr[2] error bits (1: a wait for an earlier chunk pair ran out; 2: a pair's map was
-// written on another XCD than its reader's); flags[bh * npair + p] = the epoch + 1 of the call that
-// published chunk pair p of (sequence, head) bh (low 32 bits) and the XCD its workgroup ran on
-// (high 32 bits).
+// the running call that have read the epoch (back to zero when all have), hdr[2] error bits (1: a
+// wait for an earlier chunk pair ran out; 2: a pair's map was written on another XCD than its
+// reader's); flags[bh * npair + p] = the epoch + 1 of the call that published chunk pair p of
+// (sequence, head) bh (low 32 bits) and the XCD its workgroup ran on (high 32 bits).
 struct OnePassCtl {
     uint32_t* hdr;
     uint64_t* flags;
