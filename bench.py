@@ -174,17 +174,23 @@ def bench_decode(steps_total, dev, n_bufs=12):
             i = t if cold else t % n_bufs
             gla_decode_step(q[i], k[i], v[i], g[i], states[t % n_bufs], inplace=True, out=outs[i])
 
-    def graphed(cold):
+    # A reference for the state traffic: torch's device copy moving the same bytes per step (one
+    # state read, one written) over the same rotating buffers (run after the decode loops).
+    def copy_loop(cold=False):
+        for t in range(steps_total):
+            states[(t - 1) % n_bufs].copy_(states[t % n_bufs])
+
+    def graphed(cold, body=loop):
         # warm up on a side stream, then capture the whole loop in one graph
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            loop(cold)
+            body(cold)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            loop(cold)
+            body(cold)
         graph.replay()
         torch.cuda.synchronize()
         return graph
@@ -194,13 +200,17 @@ def bench_decode(steps_total, dev, n_bufs=12):
     ms_loop = _events_time_ms(graphed(False).replay, reps, stream)
     ms_cold = _events_time_ms(graphed(True).replay, reps, stream)
     eager_ms = _events_time_ms(loop, 1, stream)
+    ms_copy = _events_time_ms(graphed(False, copy_loop).replay, reps, stream)
     step_us = ms_loop * 1e3 / steps_total
     state_bytes = B * H * D * D * 4
     step_bytes = 2 * state_bytes + B * H * D * 2 * 4 + B * H * D * 2  # state r+w; q,k,v,g read; o write
+    copy_us = ms_copy * 1e3 / steps_total
     return {
         "step_us": step_us,
         "eager_step_us": eager_ms * 1e3 / steps_total,
         "cold_step_us": ms_cold * 1e3 / steps_total,
+        "copy_step_us": copy_us,
+        "copy_gbs": 2 * state_bytes / (copy_us * 1e-6) / 1e9,
         "tok_s": B / (step_us * 1e-6),
         "step_bytes": step_bytes,
         "gbs": step_bytes / (step_us * 1e-6) / 1e9,
@@ -1032,6 +1042,8 @@ def main():
             "us_per_step": round(dec["step_us"], 3),
             "eager_us_per_step": round(dec["eager_step_us"], 3),
             "cold_inputs_us_per_step": round(dec["cold_step_us"], 3),
+            "torch_copy_same_state_bytes": {"us_per_step": round(dec["copy_step_us"], 3),
+                                            "achieved": round(dec["copy_gbs"], 1), "unit": "GB/s"},
             "roofline": {
                 "bound": "hbm",
                 "achieved": round(dec["gbs"], 1),
