@@ -213,3 +213,27 @@ def test_graph_replays_match_eager(dev):
         # eager work on the same buffers between replays
         _ = fast_chunk_gla(q, k, v, g, initial_state=s0, out=torch.empty_like(out))
         torch.cuda.synchronize()
+
+
+def test_alternating_call_sizes_share_the_control_block(dev):
+    """Calls of different grid sizes in turn on one stream's control block (the count of epoch
+    reads wraps at each call's own workgroup count): every call matches the oracle, advances the
+    epoch by one and leaves the count at zero and no error bits."""
+    cases = []
+    for (B, T, H) in ((4, 1024, 6), (1, 130, 2), (2, 640, 3), (1, 64, 1)):
+        q, k, v, g, s0 = gla_inputs(B, T, H, 64, seed=500 + T, dtype=torch.bfloat16, init_std=0.2)
+        cases.append(((q, k, v, g, s0), O.gla_fwd(q, k, v, g, s0)))
+    for rnd in range(3):
+        for (q, k, v, g, s0), (ro, rs) in cases:
+            assert _supported(q.shape[0], q.shape[1], q.shape[2])
+            key = (dev.index if dev.index is not None else 0, torch.cuda.current_stream(dev).cuda_stream)
+            before = _ctrl(dev) if key in L._CTRL else None
+            out = torch.empty(v.shape, device=dev, dtype=torch.float32)
+            o, s = fast_chunk_gla(q.to(dev), k.to(dev), v.to(dev), g.to(dev), initial_state=s0.to(dev), out=out)
+            torch.cuda.synchronize()
+            assert _err(o, ro) <= TOL16, (rnd, q.shape, _err(o, ro))
+            assert _err(s, rs) <= TOL16, (rnd, q.shape, _err(s, rs))
+            hdr = _ctrl(dev)
+            assert hdr[1] == 0 and hdr[2] == 0, (rnd, q.shape, hdr)
+            if before is not None:
+                assert hdr[0] == before[0] + 1, (rnd, q.shape, before, hdr)
