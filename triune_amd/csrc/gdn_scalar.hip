@@ -336,6 +336,9 @@ struct SgStep {
         float* sWS = reinterpret_cast<float*>(smem + L::OFF_WS + wave * L::WSB);
         float* sF = reinterpret_cast<float*>(smem + L::OFF_F);
 
+        // Issue priority: stage 1 at the base level, stages 2-3 (the solve and the state chain) one
+        // level up, so of the two workgroups on a CU the one further along issues first.
+        __builtin_amdgcn_s_setprio(0);
         // ---------------- stage 1: operands as loaded -> LDS; per-token factors ------------
         {
             const int col = c0 + 4 * row;
@@ -396,6 +399,7 @@ struct SgStep {
             return;
         }
 
+        __builtin_amdgcn_s_setprio(1);
         // ---------------- stage 2: everything of key block i = wave --------------------------
         {
             const int ib = wave;
@@ -690,11 +694,14 @@ __device__ void sg_walk(const PrefillParams& a, const Work& wk, int64_t h, f32x4
         });
 }
 
-// Workgroups per CU the launch bounds ask for: three where the LDS allows (16-bit I/O), else as many
-// as fit.
+// Workgroups per CU the launch bounds ask for: two where the LDS allows, else one.  The 16-bit
+// kernels' LDS would fit three, but at two the registers grow to 169-182 with no spill, the plan
+// takes 21 segments of 6-7 chunks per config-3 sequence instead of 32 of 4, and with the stage
+// priorities of SgStep::run the two workgroups of a CU interleave their phases: config 3 0.1258 ->
+// 0.1214 ms per pass, same-box A/B (at three per CU the priorities gained nothing).
 template <typename Lay>
 constexpr int sg_occupancy() {
-    return 3 * Lay::BYTES <= 160 * 1024 ? 3 : (2 * Lay::BYTES <= 160 * 1024 ? 2 : 1);
+    return 2 * Lay::BYTES <= 160 * 1024 ? 2 : 1;
 }
 
 // K1: the segment map driven from [I | 0] with V = 0 (-> M_p) and from 0 with the real V (-> N_p).
